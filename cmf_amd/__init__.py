@@ -1,0 +1,266 @@
+"""cmf_amd — MI355X (gfx950) backend for the cortiq decode hot path.
+
+Python mirror of the engine's GPU backend seam (crates/cortiq-engine/src/gpu.rs
+of infosave2007/cmf) over the C ABI of libcmfhip.so (include/cmf_hip.h).
+The seam functions keep the reference's names and meaning: they return True
+when the GPU did the work and False when it declined (the caller then runs its
+CPU path); genuine failures raise CmfError.  There is no CPU fallback inside
+this package: if libcmfhip.so is missing, importing the library raises.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcmfhip.so")
+
+DT_Q8ROW, DT_Q4T, DT_Q4TP = 3, 11, 15
+
+
+class CmfError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libcmfhip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise CmfError(f"{LIB_PATH} is missing: run `python -m cmf_amd.build` (hipcc, gfx950)")
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+class ModelConfig(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int), ("n_kv", C.c_int),
+                ("head_dim", C.c_int), ("inter", C.c_int), ("vocab", C.c_int), ("max_seq", C.c_int),
+                ("rope_theta", C.c_float), ("eps", C.c_double)]
+
+
+class Tensor(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("rows", C.c_int), ("cols", C.c_int),
+                ("q", C.c_void_p), ("row_scale", C.c_void_p), ("bytes", C.c_void_p)]
+
+
+class LayerDesc(C.Structure):
+    _fields_ = [("input_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p), ("wq", Tensor), ("wk", Tensor), ("wv", Tensor), ("wo", Tensor),
+                ("gate", Tensor), ("up", Tensor), ("down", Tensor)]
+
+
+class SamplerConfig(C.Structure):
+    """SamplerConfig (sampler.rs:88-121); defaults as Default::default()."""
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("repetition_penalty", C.c_float), ("min_p", C.c_float), ("presence_penalty", C.c_float)]
+
+    def __init__(self, temperature=0.7, top_p=0.9, top_k=40, repetition_penalty=1.1, min_p=0.05,
+                 presence_penalty=0.0):
+        super().__init__(temperature, top_p, top_k, repetition_penalty, min_p, presence_penalty)
+
+
+class GenStats(C.Structure):
+    _fields_ = [("generated", C.c_int), ("drafted", C.c_int), ("accepted", C.c_int), ("rounds", C.c_int),
+                ("device_ms", C.c_double)]
+
+
+# every symbol include/cmf_hip.h declares, with its ctypes signature
+_P, _I, _F, _S, _U64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint64
+SIGNATURES = {
+    "cmf_last_error": (C.c_char_p, []),
+    "cmf_init": (_I, [_I]),
+    "cmf_device_count": (_I, []),
+    "cmf_sync": (_I, []),
+    "cmf_weight_upload": (_I, [_P, _S, _I, _I, _I, C.POINTER(_P)]),
+    "cmf_weight_upload_q8": (_I, [_P, _P, _I, _I, C.POINTER(_P)]),
+    "cmf_weight_free": (_I, [_P]),
+    "cmf_weight_device_bytes": (_S, [_P]),
+    "cmf_q8_matvec_range": (_I, [_P, _I, _P, _I, _I, _P]),
+    "cmf_q8_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
+    "cmf_q4t_matvec": (_I, [_P, _P, _I, _I, _P]),
+    "cmf_q4t_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
+    "cmf_q4tp_matvec": (_I, [_P, _P, _I, _I, _P]),
+    "cmf_q4tp_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
+    "cmf_ffn": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "cmf_dev_alloc": (_P, [_S]),
+    "cmf_dev_free": (_I, [_P]),
+    "cmf_h2d": (_I, [_P, _P, _S]),
+    "cmf_d2h": (_I, [_P, _P, _S]),
+    "cmf_prep_bytes": (_S, [_P]),
+    "cmf_prep_dev": (_I, [_P, _P, _I, _I, _P, _P]),
+    "cmf_gemv_prepared": (_I, [_P, _P, _P, _I, _P, _I, _I]),
+    "cmf_time_gemv": (_I, [C.POINTER(_P), _I, _P, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
+    "cmf_model_create": (_I, [C.POINTER(ModelConfig), C.POINTER(_P)]),
+    "cmf_model_free": (_I, [_P]),
+    "cmf_model_set_layer": (_I, [_P, _I, C.POINTER(LayerDesc)]),
+    "cmf_model_set_head": (_I, [_P, C.POINTER(Tensor), _P]),
+    "cmf_model_set_mtp": (_I, [_P, _P, _P, C.POINTER(Tensor), C.POINTER(LayerDesc), _P]),
+    "cmf_prefill": (_I, [_P, _P, _I]),
+    "cmf_decode": (_I, [_P, _I, C.POINTER(SamplerConfig), _U64, _I, _I, _P, C.POINTER(GenStats)]),
+    "cmf_forward_batch": (_I, [_P, _P, _I, _I, _P, _P]),
+    "cmf_kv_truncate": (_I, [_P, _I]),
+    "cmf_state_get": (_I, [_P, C.POINTER(_I), _P]),
+    "cmf_kv_export": (_I, [_P, _I, _I, _P, _P]),
+    # host-only synthetic data generators (csrc/synth.cpp)
+    "cmf_synth_normal": (None, [_U64, C.c_int64, _F, _P]),
+    "cmf_synth_q8_uniform": (None, [_U64, _I, _I, _P, _P]),
+    "cmf_synth_q4t_uniform": (None, [_U64, _I, _I, _F, _P]),
+    "cmf_synth_q4tp_uniform": (None, [_U64, _I, _I, _F, _F, _P]),
+    "cmf_synth_q8_normal": (None, [_U64, _I, _I, _F, _P, _P]),
+    "cmf_synth_q4t_normal": (None, [_U64, _I, _I, _F, _P]),
+    "cmf_synth_ids": (None, [_U64, _I, _I, _P]),
+}
+
+
+def _declare(L):
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def check(rc):
+    """0 -> True (done), >0 -> False (declined), <0 -> CmfError."""
+    if rc < 0:
+        raise CmfError(lib().cmf_last_error().decode())
+    return rc == 0
+
+
+def init(device=0):
+    check(lib().cmf_init(device))
+
+
+def device_count():
+    return lib().cmf_device_count()
+
+
+# --------------------------------------------------------------------------
+# weights
+# --------------------------------------------------------------------------
+class Weight:
+    """A device-resident quantized tensor (the reference's resident weight,
+    keyed here by handle instead of (model, idx))."""
+
+    def __init__(self, dtype, rows, cols, payload=None, q=None, row_scale=None):
+        self.dtype, self.rows, self.cols = dtype, rows, cols
+        h = C.c_void_p()
+        if dtype == DT_Q8ROW and q is not None:
+            q = np.ascontiguousarray(q, dtype=np.int8)
+            rs = np.ascontiguousarray(row_scale, dtype=np.float32)
+            check(lib().cmf_weight_upload_q8(_ptr(q), _ptr(rs), rows, cols, C.byref(h)))
+        else:
+            payload = np.ascontiguousarray(payload, dtype=np.uint8)
+            check(lib().cmf_weight_upload(_ptr(payload), payload.nbytes, dtype, rows, cols, C.byref(h)))
+        self.h = h
+
+    @property
+    def device_bytes(self):
+        return lib().cmf_weight_device_bytes(self.h)
+
+    def free(self):
+        if self.h:
+            lib().cmf_weight_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _seam_out(rows, b=1):
+    return np.empty((b, rows), dtype=np.float32)
+
+
+def q8_matvec_range(w, row0, xs, rows, cols, out):
+    """gpu.rs:1104 — rows [row0, row0+rows) of q8 w times xs into out."""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_q8_matvec_range(w.h, row0, _ptr(xs), rows, cols, _ptr(out)))
+
+
+def q8_matmat(w, xs, b, rows, cols, out):
+    """gpu.rs:1155 — out[b*rows + r]."""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_q8_matmat(w.h, _ptr(xs), b, rows, cols, _ptr(out)))
+
+
+def q4t_matvec(w, xs, rows, cols, out):
+    """gpu.rs:2423"""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_q4t_matvec(w.h, _ptr(xs), rows, cols, _ptr(out)))
+
+
+def q4t_matmat(w, xs, b, rows, cols, out):
+    """gpu.rs:2439"""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_q4t_matmat(w.h, _ptr(xs), b, rows, cols, _ptr(out)))
+
+
+def q4tp_matvec(w, xs, rows, cols, out):
+    """gpu.rs:2400"""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_q4tp_matvec(w.h, _ptr(xs), rows, cols, _ptr(out)))
+
+
+def q4tp_matmat(w, xs, b, rows, cols, out):
+    """gpu.rs:2358"""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_q4tp_matmat(w.h, _ptr(xs), b, rows, cols, _ptr(out)))
+
+
+def ffn(w1, w3, w2, xs, b, hidden, inter, out):
+    """gpu.rs:1773/1794 q4t_ffn / q4tp_ffn: out = w2 (silu(w1 x) * w3 x)."""
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    return check(lib().cmf_ffn(w1.h, w3.h, w2.h, _ptr(xs), b, hidden, inter, _ptr(out)))
+
+
+def matmul(w, xs):
+    """Convenience: w * xs for xs [b][cols] (any b), returns [b][rows]."""
+    xs = np.ascontiguousarray(np.atleast_2d(xs), dtype=np.float32)
+    b = xs.shape[0]
+    out = np.empty((b, w.rows), dtype=np.float32)
+    fn = {DT_Q8ROW: q8_matmat, DT_Q4T: q4t_matmat, DT_Q4TP: q4tp_matmat}[w.dtype]
+    if not fn(w, xs, b, w.rows, w.cols, out):
+        raise CmfError("declined")
+    return out
+
+
+# --------------------------------------------------------------------------
+# device buffers (plumbing for device-resident benchmarks; no torch needed)
+# --------------------------------------------------------------------------
+class DevBuf:
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.p = lib().cmf_dev_alloc(self.nbytes)
+        if not self.p:
+            raise CmfError(lib().cmf_last_error().decode())
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(lib().cmf_h2d(self.p, _ptr(arr), arr.nbytes))
+
+    def download(self, shape, dtype=np.float32):
+        out = np.empty(shape, dtype=dtype)
+        check(lib().cmf_d2h(_ptr(out), self.p, out.nbytes))
+        return out
+
+    def free(self):
+        if self.p:
+            lib().cmf_dev_free(self.p)
+            self.p = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

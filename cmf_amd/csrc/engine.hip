@@ -1,0 +1,618 @@
+// The decode engine: a Qwen3-arch decoder with an MTP head resident on one
+// MI355X, the batched verify forward (the counterpart of the reference's
+// forward_batch_graph, gpu.rs:1466-1497) and the speculative decode loop
+// (graph_spec_step, pipeline.rs:3582-4213) run device-side: drafted tokens,
+// acceptance and the commit never leave HBM; the host reads back one small
+// state record per round.
+#include <math.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/cmf_hip.h"
+#include "common.h"
+#include "gemv.h"
+#include "layers.h"
+#include "runtime.h"
+#include "sample.h"
+
+namespace cmf {
+
+struct LayerDev {
+    float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    DevWeight qkv, wo, gu, down;
+    float *kc = nullptr, *vc = nullptr;
+};
+
+}  // namespace cmf
+
+using namespace cmf;
+
+struct cmf_model_s {
+    cmf_model_config c{};
+    std::vector<LayerDev> L;
+    bool has_head = false, has_mtp = false;
+    DevWeight lm;
+    float* final_norm = nullptr;
+    float *enorm = nullptr, *hnorm = nullptr, *mtp_norm = nullptr;
+    DevWeight eh;
+    LayerDev mtp;
+    float2* rope = nullptr;
+    // scratch
+    float *hv = nullptr, *hm = nullptr, *attn_out = nullptr, *ffn_out = nullptr, *qkv_out = nullptr,
+          *qrot = nullptr, *gu_out = nullptr, *logits = nullptr;
+    uint8_t* planes = nullptr;
+    size_t planes_cap = 0;
+    float* xs = nullptr;
+    float *pm = nullptr, *pl = nullptr, *po = nullptr;
+    int nch_cap = 0;
+    float* am_v = nullptr;
+    int* am_i = nullptr;
+    int* toks = nullptr;  // [2*MAXB] token staging
+    DState* st = nullptr;
+    int* out = nullptr;
+    int out_cap = 0;
+    float* h_tip = nullptr;
+    SampleBufs sb;
+    std::vector<void*> allocs;
+    int next_pos_host = 0;
+    bool prefilled = false;
+};
+
+namespace {
+
+int dalloc(cmf_model_s* m, void** p, size_t bytes) {
+    CMF_HIP(hipMalloc(p, bytes));
+    CMF_HIP(hipMemset(*p, 0, bytes));
+    m->allocs.push_back(*p);
+    return CMF_OK;
+}
+
+template <class T>
+int dalloc_t(cmf_model_s* m, T** p, size_t n) {
+    return dalloc(m, (void**)p, n * sizeof(T));
+}
+
+int upload_f32(cmf_model_s* m, float** d, const float* h, size_t n) {
+    if (!h) return fail("missing norm weights");
+    if (dalloc_t(m, d, n) != CMF_OK) return CMF_ERR;
+    CMF_HIP(hipMemcpy(*d, h, n * sizeof(float), hipMemcpyHostToDevice));
+    return CMF_OK;
+}
+
+int check_tensor(const cmf_tensor& t, int rows, int cols, const char* name) {
+    if (t.rows != rows || t.cols != cols)
+        return fail(std::string(name) + ": shape mismatch (got " + std::to_string(t.rows) + "x" +
+                    std::to_string(t.cols) + ", want " + std::to_string(rows) + "x" + std::to_string(cols) + ")");
+    if (t.dtype == DT_Q8ROW) {
+        if (!t.q || !t.row_scale) return fail(std::string(name) + ": q8 needs q and row_scale");
+    } else if (t.dtype == DT_Q4T || t.dtype == DT_Q4TP) {
+        if (!t.bytes) return fail(std::string(name) + ": q4 needs bytes");
+        if (cols % 32) return fail(std::string(name) + ": q4 needs cols % 32 == 0");
+    } else {
+        return fail(std::string(name) + ": unsupported dtype");
+    }
+    return CMF_OK;
+}
+
+// Concatenate tensors along rows into one device weight (one launch serves
+// q/k/v, or gate/up).
+int build_cat(DevWeight& w, const std::vector<const cmf_tensor*>& ts) {
+    const int dt = ts[0]->dtype, cols = ts[0]->cols;
+    for (auto* t : ts)
+        if (t->dtype != dt || t->cols != cols) return fail("fused tensors must share dtype and cols");
+    if (dt == DT_Q8ROW) {
+        std::vector<const int8_t*> rp;
+        std::vector<float> rs;
+        for (auto* t : ts)
+            for (int r = 0; r < t->rows; r++) {
+                rp.push_back(t->q + (size_t)r * cols);
+                rs.push_back(t->row_scale[r]);
+            }
+        return build_q8(w, (int)rp.size(), cols, rp.data(), rs.data());
+    }
+    Q4Src s;
+    for (auto* t : ts) fill_q4src(s, dt, t->rows, cols, t->bytes, 0);
+    return build_q4(w, s);
+}
+
+PrepDst prep_for(cmf_model_s* m, const DevWeight& w) {
+    PrepDst d;
+    d.kind = w.dtype == DT_Q8ROW ? 8 : 16;
+    d.nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
+    d.planes = m->planes;
+    d.xs = m->xs;
+    return d;
+}
+
+int upload_layer(cmf_model_s* m, LayerDev& l, const cmf_layer_desc* d, bool kv) {
+    const auto& c = m->c;
+    const int H = c.hidden, hd = c.head_dim, Q = c.n_heads * hd, KV = c.n_kv * hd, I = c.inter;
+    if (check_tensor(d->wq, Q, H, "wq") || check_tensor(d->wk, KV, H, "wk") ||
+        check_tensor(d->wv, KV, H, "wv") || check_tensor(d->wo, H, Q, "wo") ||
+        check_tensor(d->gate, I, H, "gate") || check_tensor(d->up, I, H, "up") ||
+        check_tensor(d->down, H, I, "down"))
+        return CMF_ERR;
+    if (upload_f32(m, &l.in_norm, d->input_norm, H) || upload_f32(m, &l.post_norm, d->post_norm, H) ||
+        upload_f32(m, &l.q_norm, d->q_norm, hd) || upload_f32(m, &l.k_norm, d->k_norm, hd))
+        return CMF_ERR;
+    free_weight(l.qkv);
+    free_weight(l.wo);
+    free_weight(l.gu);
+    free_weight(l.down);
+    if (build_cat(l.qkv, {&d->wq, &d->wk, &d->wv}) || build_cat(l.wo, {&d->wo}) ||
+        build_cat(l.gu, {&d->gate, &d->up}) || build_cat(l.down, {&d->down}))
+        return CMF_ERR;
+    if (kv && !l.kc) {
+        const size_t n = (size_t)c.n_kv * c.max_seq * hd;
+        if (dalloc_t(m, &l.kc, n) || dalloc_t(m, &l.vc, n)) return CMF_ERR;
+    }
+    return CMF_OK;
+}
+
+void free_layer(LayerDev& l) {
+    free_weight(l.qkv);
+    free_weight(l.wo);
+    free_weight(l.gu);
+    free_weight(l.down);
+}
+
+EmbedSrc embed_src(cmf_model_s* m) {
+    return EmbedSrc{(const int8_t*)m->lm.w, (const float*)m->lm.scale, m->lm.rows, m->lm.kchunks};
+}
+
+// One decoder block over nb rows of h at positions *pb + padd + i.  The
+// pending residual `pend` (the previous block's FFN output) is added by the
+// fused norm, as forward_layers adds it before the next rms_norm.
+void run_block(cmf_model_s* m, LayerDev& l, float* h, const float* pend, int nb, const int* pb,
+               int padd, int max_len, hipStream_t s) {
+    const auto& c = m->c;
+    const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
+    const int QKV = (nh + 2 * nkv) * hd, I = c.inter;
+    launch_add_rmsnorm_prep(h, H, pend, H, l.in_norm, H, c.eps, prep_for(m, l.qkv), nullptr, 0, nb, s);
+    launch_gemv(l.qkv, m->planes, m->xs, m->qkv_out, QKV, nb, 0, QKV, s);
+    launch_qk_rope_append(m->qkv_out, QKV, l.q_norm, l.k_norm, m->rope, nh, nkv, hd, c.eps, pb, padd,
+                          l.kc, l.vc, c.max_seq, m->qrot, nh * hd, nb, s);
+    launch_attention(m->qrot, nh * hd, l.kc, l.vc, c.max_seq, nb, nh, nkv, pb, padd, max_len, m->pm,
+                     m->pl, m->po, m->nch_cap, prep_for(m, l.wo), nullptr, s);
+    launch_gemv(l.wo, m->planes, m->xs, m->attn_out, H, nb, 0, H, s);
+    launch_add_rmsnorm_prep(h, H, m->attn_out, H, l.post_norm, H, c.eps, prep_for(m, l.gu), nullptr, 0,
+                            nb, s);
+    launch_gemv(l.gu, m->planes, m->xs, m->gu_out, 2 * I, nb, 0, 2 * I, s);
+    launch_silu_mul_prep(m->gu_out, 2 * I, I, prep_for(m, l.down), nullptr, nb, s);
+    launch_gemv(l.down, m->planes, m->xs, m->ffn_out, H, nb, 0, H, s);
+}
+
+// Trunk forward of nb rows already in m->hv; leaves the final hidden rows in
+// m->hv and the lm_head input prepared; logits when want_logits.
+void trunk_forward(cmf_model_s* m, int nb, const int* pb, int padd, int max_len, bool want_logits,
+                   hipStream_t s) {
+    const auto& c = m->c;
+    const int H = c.hidden;
+    for (int li = 0; li < c.n_layers; li++)
+        run_block(m, m->L[li], m->hv, li == 0 ? nullptr : m->ffn_out, nb, pb, padd, max_len, s);
+    launch_add_rmsnorm_prep(m->hv, H, m->ffn_out, H, m->final_norm, H, c.eps, prep_for(m, m->lm),
+                            nullptr, 0, nb, s);
+    if (want_logits) launch_gemv(m->lm, m->planes, m->xs, m->logits, c.vocab, nb, 0, c.vocab, s);
+}
+
+// MTP warm (mtp_warm, pipeline.rs:3532-3572): eh_proj on [enorm(embed(tok));
+// hnorm(h)], input norm, q/k/v, qk-norm + RoPE, KV append.  No attention.
+void mtp_warm(cmf_model_s* m, const int* toks, const float* hid, int nb, const int* pb, int padd,
+              hipStream_t s) {
+    const auto& c = m->c;
+    const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
+    const int QKV = (nh + 2 * nkv) * hd;
+    launch_mtp_cat_prep(toks, hid, H, embed_src(m), m->enorm, m->hnorm, H, c.eps, prep_for(m, m->eh), nb, s);
+    launch_gemv(m->eh, m->planes, m->xs, m->hm, H, nb, 0, H, s);
+    launch_add_rmsnorm_prep(m->hm, H, nullptr, H, m->mtp.in_norm, H, c.eps, prep_for(m, m->mtp.qkv),
+                            nullptr, 0, nb, s);
+    launch_gemv(m->mtp.qkv, m->planes, m->xs, m->qkv_out, QKV, nb, 0, QKV, s);
+    launch_qk_rope_append(m->qkv_out, QKV, m->mtp.q_norm, m->mtp.k_norm, m->rope, nh, nkv, hd, c.eps, pb,
+                          padd, m->mtp.kc, m->mtp.vc, c.max_seq, m->qrot, nh * hd, nb, s);
+}
+
+// One MTP draft step (mtp_step_hl, pipeline.rs:3051-3160) for a single row:
+// tok (device), hidden hin (device row) -> m->hm = block output hidden,
+// logits row 0.
+void mtp_step(cmf_model_s* m, const int* tok, const float* hin, const int* pb, int padd, int max_len,
+              hipStream_t s) {
+    const auto& c = m->c;
+    const int H = c.hidden;
+    launch_mtp_cat_prep(tok, hin, H, embed_src(m), m->enorm, m->hnorm, H, c.eps, prep_for(m, m->eh), 1, s);
+    launch_gemv(m->eh, m->planes, m->xs, m->hm, H, 1, 0, H, s);
+    run_block(m, m->mtp, m->hm, nullptr, 1, pb, padd, max_len, s);
+    launch_add_rmsnorm_prep(m->hm, H, m->ffn_out, H, m->mtp_norm, H, c.eps, prep_for(m, m->lm), nullptr, 0,
+                            1, s);
+    launch_gemv(m->lm, m->planes, m->xs, m->logits, c.vocab, 1, 0, c.vocab, s);
+}
+
+int alloc_scratch(cmf_model_s* m) {
+    const auto& c = m->c;
+    const int H = c.hidden, hd = c.head_dim, QKV = (c.n_heads + 2 * c.n_kv) * hd;
+    m->nch_cap = (c.max_seq + ATT_C - 1) / ATT_C;
+    if (dalloc_t(m, &m->hv, (size_t)MAXB * H) || dalloc_t(m, &m->hm, (size_t)MAXB * H) ||
+        dalloc_t(m, &m->attn_out, (size_t)MAXB * H) || dalloc_t(m, &m->ffn_out, (size_t)MAXB * H) ||
+        dalloc_t(m, &m->qkv_out, (size_t)MAXB * QKV) || dalloc_t(m, &m->qrot, (size_t)MAXB * c.n_heads * hd) ||
+        dalloc_t(m, &m->gu_out, (size_t)MAXB * 2 * c.inter) || dalloc_t(m, &m->xs, 64) ||
+        dalloc_t(m, &m->pm, (size_t)MAXB * c.n_heads * m->nch_cap) ||
+        dalloc_t(m, &m->pl, (size_t)MAXB * c.n_heads * m->nch_cap) ||
+        dalloc_t(m, &m->po, (size_t)MAXB * c.n_heads * m->nch_cap * hd) ||
+        dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H))
+        return CMF_ERR;
+    // planes large enough for every weight the model uses: q8 K <= max(H, nh*hd, 2H) ; q4 K <= max(H, I)
+    const int kmax = std::max(std::max(2 * H, c.n_heads * hd), c.inter);
+    m->planes_cap = (size_t)((kmax + 127) / 128) * 4 * 1024 * 3;
+    if (dalloc(m, (void**)&m->planes, m->planes_cap)) return CMF_ERR;
+    // rope table (cos, sin) per (position, freq) with the host libm, as
+    // rope_rotate (attention.rs:71-81) evaluates it
+    const int half = hd / 2;
+    std::vector<float> inv(half);
+    for (int i = 0; i < half; i++) inv[i] = 1.0f / powf(c.rope_theta, 2.0f * (float)i / (float)hd);
+    std::vector<float2> tab((size_t)c.max_seq * half);
+    for (int p = 0; p < c.max_seq; p++)
+        for (int i = 0; i < half; i++) {
+            const float ang = (float)p * inv[i];
+            tab[(size_t)p * half + i] = make_float2(cosf(ang), sinf(ang));
+        }
+    if (dalloc_t(m, &m->rope, tab.size())) return CMF_ERR;
+    CMF_HIP(hipMemcpy(m->rope, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+    return CMF_OK;
+}
+
+int ensure_logits(cmf_model_s* m) {
+    if (m->logits) return CMF_OK;
+    const int V = m->c.vocab;
+    if (dalloc_t(m, &m->logits, (size_t)(MAXB + 1) * V)) return CMF_ERR;
+    const int ns = (V + 4095) / 4096;
+    if (dalloc_t(m, &m->am_v, (size_t)(MAXB + 1) * ns) || dalloc_t(m, &m->am_i, (size_t)(MAXB + 1) * ns))
+        return CMF_ERR;
+    return sample_alloc(m->sb, V, [&](void** p, size_t b) { return dalloc(m, p, b); });
+}
+
+int ensure_out(cmf_model_s* m, int cap) {
+    if (m->out_cap >= cap) return CMF_OK;
+    if (dalloc_t(m, &m->out, cap)) return CMF_ERR;
+    m->out_cap = cap;
+    return CMF_OK;
+}
+
+__global__ void k_set_int(int* p, int v) { *p = v; }
+
+__global__ void k_copy_rows_i32(int* dst, const int* src, int n) {
+    const int i = threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+// verify batch tokens [t_next, d_0 .. d_{K-1}]
+__global__ void k_build_vtok(DState* st, int k) {
+    const int i = threadIdx.x;
+    if (i == 0) st->vtok[0] = st->t_next;
+    else if (i <= k) st->vtok[i] = st->drafts[i - 1];
+}
+
+// greedy acceptance (pipeline.rs:3989-3999): a = longest prefix with
+// argmax(row i) == d_i; emits [t_next, d_0..d_{a-1}]; next token argmax(row a)
+__global__ void k_accept_greedy(DState* st, int k, int* out) {
+    int a = 0;
+    while (a < k && st->argmax[a] == st->drafts[a]) a++;
+    const int n = st->n_out;
+    out[n] = st->t_next;
+    for (int j = 0; j < a; j++) out[n + 1 + j] = st->drafts[j];
+    st->n_out = n + 1 + a;
+    st->a = a;
+    st->t_new = st->argmax[a];
+    st->accepted += a;
+}
+
+// commit: h_tip = hidden row a, next_pos += a + 1, t_next = t_new
+__global__ void k_commit(DState* st, const float* hv, float* h_tip, int H) {
+    const int a = st->a;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) h_tip[i] = hv[(size_t)a * H + i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        st->next_pos += a + 1;
+        st->t_next = st->t_new;
+    }
+}
+
+// plain step commit: emit t_next, next token = row-0 pick
+__global__ void k_plain_commit(DState* st, const float* hv, float* h_tip, int H, int* out,
+                               int use_sample) {
+    for (int i = threadIdx.x; i < H; i += blockDim.x) h_tip[i] = hv[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        out[st->n_out] = st->t_next;
+        st->n_out += 1;
+        st->next_pos += 1;
+        st->t_next = use_sample ? st->t_new : st->argmax[0];
+    }
+}
+
+// emit t_next without advancing (the last token of a generation)
+__global__ void k_emit(DState* st, int* out) { out[st->n_out++] = st->t_next; }
+
+// after prefill: t_next = pick of the last hidden's logits
+__global__ void k_first_token(DState* st, int use_sample) {
+    st->t_next = use_sample ? st->t_new : st->argmax[0];
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!cfg || !out) return fail("model_create: null argument");
+    const auto& c = *cfg;
+    if (c.n_layers < 1 || c.hidden < 64 || c.n_heads < 1 || c.n_kv < 1 || c.n_heads % c.n_kv ||
+        c.vocab < 1 || c.max_seq < 8 || c.inter < 32)
+        return fail("model_create: bad config");
+    if (c.head_dim != 128) return fail("model_create: the attention kernels are built for head_dim 128");
+    if (c.hidden > 4096 || c.inter > 12288 || c.n_heads * c.head_dim > 4096)
+        return fail("model_create: hidden <= 4096, inter <= 12288, heads*head_dim <= 4096");
+    if (c.hidden % 32 || c.inter % 32) return fail("model_create: hidden and inter must be multiples of 32");
+    auto* m = new cmf_model_s();
+    m->c = c;
+    m->L.resize(c.n_layers);
+    if (alloc_scratch(m) != CMF_OK) {
+        cmf_model_free(m);
+        return CMF_ERR;
+    }
+    *out = m;
+    return CMF_OK;
+}
+
+int cmf_model_free(cmf_model m) {
+    if (!m) return CMF_OK;
+    (void)hipStreamSynchronize(stream());
+    for (auto& l : m->L) free_layer(l);
+    free_layer(m->mtp);
+    free_weight(m->lm);
+    free_weight(m->eh);
+    for (void* p : m->allocs) (void)hipFree(p);
+    delete m;
+    return CMF_OK;
+}
+
+int cmf_model_set_layer(cmf_model m, int li, const cmf_layer_desc* d) {
+    if (!m || !d || li < 0 || li >= m->c.n_layers) return fail("set_layer: bad arguments");
+    if (m->c.n_heads / m->c.n_kv * MAXB > 32 && m->c.n_heads / m->c.n_kv > 2)
+        return fail("set_layer: the attention kernel serves <= 32 queries per KV head");
+    return upload_layer(m, m->L[li], d, true);
+}
+
+int cmf_model_set_head(cmf_model m, const cmf_tensor* lm, const float* final_norm) {
+    if (!m || !lm) return fail("set_head: null argument");
+    if (lm->dtype != DT_Q8ROW) return fail("set_head: the tied lm_head/embedding must be q8");
+    if (check_tensor(*lm, m->c.vocab, m->c.hidden, "lm_head")) return CMF_ERR;
+    if (upload_f32(m, &m->final_norm, final_norm, m->c.hidden)) return CMF_ERR;
+    free_weight(m->lm);
+    if (build_cat(m->lm, {lm})) return CMF_ERR;
+    if (ensure_logits(m)) return CMF_ERR;
+    m->has_head = true;
+    return CMF_OK;
+}
+
+int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh,
+                      const cmf_layer_desc* layer, const float* norm) {
+    if (!m || !eh || !layer) return fail("set_mtp: null argument");
+    const int H = m->c.hidden;
+    if (check_tensor(*eh, H, 2 * H, "eh_proj")) return CMF_ERR;
+    if (upload_f32(m, &m->enorm, enorm, H) || upload_f32(m, &m->hnorm, hnorm, H) ||
+        upload_f32(m, &m->mtp_norm, norm, H))
+        return CMF_ERR;
+    free_weight(m->eh);
+    if (build_cat(m->eh, {eh})) return CMF_ERR;
+    if (upload_layer(m, m->mtp, layer, true)) return CMF_ERR;
+    m->has_mtp = true;
+    return CMF_OK;
+}
+
+static int ready(cmf_model m) {
+    if (!m) return fail("null model");
+    if (!m->has_head) return fail("model has no lm_head (cmf_model_set_head)");
+    for (auto& l : m->L)
+        if (!l.qkv.w) return fail("model has unset layers (cmf_model_set_layer)");
+    return CMF_OK;
+}
+
+int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
+    if (ready(m)) return CMF_ERR;
+    if (!ids || n < 1 || n + 1 > m->c.max_seq) return fail("prefill: 1 <= n < max_seq");
+    hipStream_t s = stream();
+    const int H = m->c.hidden;
+    int* pb = &m->st->next_pos;
+    for (int p0 = 0; p0 < n; p0 += MAXB) {
+        const int cnt = std::min(MAXB, n - p0);
+        CMF_HIP(hipMemcpyAsync(m->toks, ids + p0, cnt * sizeof(int), hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, p0);
+        launch_embed(m->toks, embed_src(m), H, m->hv, H, cnt, s);
+        trunk_forward(m, cnt, pb, 0, p0 + cnt, false, s);
+        if (m->has_mtp) {
+            const int pairs = (p0 + cnt < n) ? cnt : cnt - 1;
+            if (pairs > 0) {
+                CMF_HIP(hipMemcpyAsync(m->toks + MAXB, ids + p0 + 1, pairs * sizeof(int), hipMemcpyHostToDevice, s));
+                mtp_warm(m, m->toks + MAXB, m->hv, pairs, pb, 0, s);
+            }
+        }
+        if (p0 + cnt == n)
+            CMF_HIP(hipMemcpyAsync(m->h_tip, m->hv + (size_t)(cnt - 1) * H, H * sizeof(float),
+                                   hipMemcpyDeviceToDevice, s));
+        CMF_HIP(hipStreamSynchronize(s));  // host buffers of this chunk are reused
+    }
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, n);
+    CMF_HIP(hipMemsetAsync(&m->st->n_out, 0, sizeof(int), s));
+    CMF_HIP(hipStreamSynchronize(s));
+    CMF_HIP(hipGetLastError());
+    m->next_pos_host = n;
+    m->prefilled = true;
+    return CMF_OK;
+}
+
+// logits of the tip hidden -> next token (greedy argmax or device sampler)
+static void pick_from_tip(cmf_model m, bool sampling, const cmf_sampler_config* sc, hipStream_t s) {
+    const int H = m->c.hidden;
+    (void)hipMemcpyAsync(m->hm, m->h_tip, H * sizeof(float), hipMemcpyDeviceToDevice, s);
+    launch_add_rmsnorm_prep(m->hm, H, nullptr, H, m->final_norm, H, m->c.eps, prep_for(m, m->lm), nullptr, 0,
+                            1, s);
+    launch_gemv(m->lm, m->planes, m->xs, m->logits, m->c.vocab, 1, 0, m->c.vocab, s);
+    if (sampling) sample_rows(m->sb, m->logits, m->c.vocab, 1, *sc, m->st, SampleMode::Plain, 0, nullptr, s);
+    else launch_argmax(m->logits, m->c.vocab, m->c.vocab, 1, m->am_v, m->am_i, m->st->argmax, s);
+}
+
+int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
+               int k, int32_t* out, cmf_gen_stats* stats) {
+    if (ready(m)) return CMF_ERR;
+    if (!m->prefilled) return fail("decode: call cmf_prefill first");
+    if (!sc || !out || max_tokens < 1) return fail("decode: bad arguments");
+    if (spec && !m->has_mtp) return fail("decode: speculation needs the MTP head (cmf_model_set_mtp)");
+    if (spec && (k < 1 || k > 8)) return fail("decode: k must be 1..8 (CMF_GRAPH_SPEC_K range)");
+    if (sc->repetition_penalty != 1.0f || sc->presence_penalty != 0.0f) return CMF_DECLINED;
+    const bool sampling = sc->temperature >= 1e-6f;
+    if (sampling && (sc->top_k < 1 || sc->top_k > SPARSE_K_MAX)) return CMF_DECLINED;
+    if (m->next_pos_host + max_tokens + k + 2 > m->c.max_seq) return fail("decode: max_seq too small");
+    if (ensure_out(m, max_tokens + 16)) return CMF_ERR;
+    hipStream_t s = stream();
+    const int H = m->c.hidden, V = m->c.vocab;
+    int* pb = &m->st->next_pos;
+    hipEvent_t e0, e1;
+    CMF_HIP(hipEventCreate(&e0));
+    CMF_HIP(hipEventCreate(&e1));
+    DState init{};
+    init.next_pos = m->next_pos_host;
+    init.rng = seed;
+    CMF_HIP(hipMemcpyAsync(m->st, &init, sizeof(DState), hipMemcpyHostToDevice, s));
+    CMF_HIP(hipStreamSynchronize(s));
+    CMF_HIP(hipEventRecord(e0, s));
+    pick_from_tip(m, sampling, sc, s);
+    hipLaunchKernelGGL(k_first_token, dim3(1), dim3(1), 0, s, m->st, sampling ? 1 : 0);
+    int generated = 0, rounds = 0, np = m->next_pos_host;
+    DState hs{};
+    while (true) {
+        if (generated + 1 >= max_tokens) {  // emitting t_next reaches max_tokens
+            hipLaunchKernelGGL(k_emit, dim3(1), dim3(1), 0, s, m->st, m->out);
+            generated += 1;
+            break;
+        }
+        if (spec && generated + 2 < max_tokens) {
+            // ---- graph_spec_step: draft K from the MTP head ----
+            for (int j = 0; j < k; j++) {
+                const int* tok = j == 0 ? &m->st->t_next : &m->st->drafts[j - 1];
+                const float* hin = j == 0 ? m->h_tip : m->hm;
+                mtp_step(m, tok, hin, pb, j - 1, np + j, s);
+                if (sampling)
+                    sample_rows(m->sb, m->logits, V, 1, *sc, m->st, SampleMode::Draft, j, nullptr, s);
+                else
+                    launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, &m->st->drafts[j], s);
+            }
+            // ---- verify the K+1 rows in one batched forward ----
+            hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
+            launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, k + 1, s);
+            trunk_forward(m, k + 1, pb, 0, np + k + 1, true, s);
+            // ---- accept ----
+            if (sampling) {
+                sample_rows(m->sb, m->logits, V, k + 1, *sc, m->st, SampleMode::Accept, k, m->out, s);
+            } else {
+                launch_argmax(m->logits, V, V, k + 1, m->am_v, m->am_i, m->st->argmax, s);
+                hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(1), 0, s, m->st, k, m->out);
+            }
+            // ---- commit: MTP re-warm on the verified pairs, then advance ----
+            mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, s);
+            hipLaunchKernelGGL(k_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H);
+            CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
+            CMF_HIP(hipStreamSynchronize(s));
+            rounds++;
+            generated = hs.n_out;
+            np = hs.next_pos;
+        } else {
+            // ---- plain step: forward t_next ----
+            launch_embed(&m->st->t_next, embed_src(m), H, m->hv, H, 1, s);
+            trunk_forward(m, 1, pb, 0, np + 1, true, s);
+            if (sampling) sample_rows(m->sb, m->logits, V, 1, *sc, m->st, SampleMode::Plain, 0, nullptr, s);
+            else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, m->st->argmax, s);
+            hipLaunchKernelGGL(k_plain_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H, m->out,
+                               sampling ? 1 : 0);
+            generated += 1;
+            np += 1;
+        }
+    }
+    CMF_HIP(hipEventRecord(e1, s));
+    CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
+    CMF_HIP(hipStreamSynchronize(s));
+    CMF_HIP(hipGetLastError());
+    float ms = 0.f;
+    CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    std::vector<int> tok(hs.n_out);
+    CMF_HIP(hipMemcpy(tok.data(), m->out, hs.n_out * sizeof(int), hipMemcpyDeviceToHost));
+    for (int i = 0; i < hs.n_out; i++) out[i] = tok[i];
+    // the stream state continues from here
+    m->next_pos_host = hs.next_pos;
+    if (stats) {
+        stats->generated = hs.n_out;
+        stats->drafted = rounds * k;
+        stats->accepted = hs.accepted;
+        stats->rounds = rounds;
+        stats->device_ms = ms;
+    }
+    return CMF_OK;
+}
+
+int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden, float* logits) {
+    if (ready(m)) return CMF_ERR;
+    if (!tokens || b < 1 || b > MAXB || pos0 < 0 || pos0 + b > m->c.max_seq)
+        return fail("forward_batch: 1 <= b <= 16 and pos0 + b <= max_seq");
+    hipStream_t s = stream();
+    const int H = m->c.hidden;
+    int* pb = &m->st->next_pos;
+    CMF_HIP(hipMemcpyAsync(m->toks, tokens, b * sizeof(int), hipMemcpyHostToDevice, s));
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, pos0);
+    launch_embed(m->toks, embed_src(m), H, m->hv, H, b, s);
+    trunk_forward(m, b, pb, 0, pos0 + b, logits != nullptr, s);
+    if (hidden) CMF_HIP(hipMemcpyAsync(hidden, m->hv, (size_t)b * H * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (logits)
+        CMF_HIP(hipMemcpyAsync(logits, m->logits, (size_t)b * m->c.vocab * sizeof(float), hipMemcpyDeviceToHost, s));
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, pos0 + b);
+    CMF_HIP(hipStreamSynchronize(s));
+    CMF_HIP(hipGetLastError());
+    m->next_pos_host = pos0 + b;
+    return CMF_OK;
+}
+
+int cmf_kv_truncate(cmf_model m, int n) {
+    if (!m || n < 0) return fail("kv_truncate: bad arguments");
+    const int np = std::max(0, m->next_pos_host - n);
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, stream(), &m->st->next_pos, np);
+    CMF_HIP(hipStreamSynchronize(stream()));
+    m->next_pos_host = np;
+    return CMF_OK;
+}
+
+int cmf_state_get(cmf_model m, int* next_pos, float* hidden) {
+    if (!m) return fail("null model");
+    if (next_pos) *next_pos = m->next_pos_host;
+    if (hidden) CMF_HIP(hipMemcpy(hidden, m->h_tip, m->c.hidden * sizeof(float), hipMemcpyDeviceToHost));
+    return CMF_OK;
+}
+
+int cmf_kv_export(cmf_model m, int li, int n, float* k, float* v) {
+    if (!m || !k || !v || n < 0 || n > m->c.max_seq) return fail("kv_export: bad arguments");
+    LayerDev* l = li < 0 ? &m->mtp : (li < m->c.n_layers ? &m->L[li] : nullptr);
+    if (!l || !l->kc) return fail("kv_export: no such layer");
+    const int hd = m->c.head_dim;
+    for (int g = 0; g < m->c.n_kv; g++) {
+        CMF_HIP(hipMemcpy(k + (size_t)g * n * hd, l->kc + (size_t)g * m->c.max_seq * hd, (size_t)n * hd * 4,
+                          hipMemcpyDeviceToHost));
+        CMF_HIP(hipMemcpy(v + (size_t)g * n * hd, l->vc + (size_t)g * m->c.max_seq * hd, (size_t)n * hd * 4,
+                          hipMemcpyDeviceToHost));
+    }
+    return CMF_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// GEMV launchers and the activation-preparation helpers shared by the
+// standalone preparation kernel and the fused producers (norms, SwiGLU,
+// attention merge) of the model path.
+#pragma once
+
+#include "common.h"
+
+namespace cmf {
+
+size_t prep_bytes(const DevWeight& w);
+int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
+                hipStream_t st);
+// y[b*ldy + (r - row_lo)] for rows [row_lo, row_hi) and b < m.
+int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
+                int m, int row_lo, int row_hi, hipStream_t st, int ks_override = 0);
+
+// Writes batch row b of the q8 activation planes: three int8 planes with
+// x ~= sx * (q0 + q1/128 + q2/16384), sx = max|x|/127, lane order
+// [chunk of 64][lane 16*s + b][16 bytes of columns 64c + 16s ..].
+__device__ inline void prep8_row(const float* x, int K, float amax, int nk, int b,
+                                 uint8_t* planes, float* xs, int tid, int nthr) {
+    const float sx = amax > 0.f ? amax / 127.0f : 1.0f;
+    const float inv = 1.0f / sx;
+    if (tid == 0) xs[b] = sx;
+    uint8_t* p0 = planes;
+    uint8_t* p1 = planes + (size_t)nk * 1024;
+    uint8_t* p2 = planes + (size_t)nk * 2048;
+    for (int idx = tid; idx < nk * 4; idx += nthr) {
+        const int kc = idx >> 2, s = idx & 3, c0 = kc * 64 + 16 * s;
+        uint32_t w0[4], w1[4], w2[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            uint32_t a = 0, bb = 0, c = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int col = c0 + 4 * q + j;
+                const float v = col < K ? x[col] * inv : 0.f;
+                const float q0 = fminf(127.f, fmaxf(-127.f, rintf(v)));
+                const float r1 = (v - q0) * 128.0f;
+                const float q1 = fminf(127.f, fmaxf(-127.f, rintf(r1)));
+                const float r2 = (r1 - q1) * 128.0f;
+                const float q2 = fminf(127.f, fmaxf(-127.f, rintf(r2)));
+                a |= (uint32_t)(uint8_t)(int8_t)q0 << (8 * j);
+                bb |= (uint32_t)(uint8_t)(int8_t)q1 << (8 * j);
+                c |= (uint32_t)(uint8_t)(int8_t)q2 << (8 * j);
+            }
+            w0[q] = a;
+            w1[q] = bb;
+            w2[q] = c;
+        }
+        const size_t off = ((size_t)kc * 64 + 16 * s + b) * 16;
+        *(uint4*)(p0 + off) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+        *(uint4*)(p1 + off) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        *(uint4*)(p2 + off) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+    }
+}
+
+// Writes batch row b of the q4 activation planes: f16 hi/lo of x*2^e with
+// max|x*2^e| < 2^15, xs[b] = 2^-e, lane order [tile][16*s + b][8 halves of
+// columns 32t + 8s + {0,2,4,6,1,3,5,7}].
+__device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b,
+                                  uint8_t* planes, float* xs, int tid, int nthr) {
+    int ex = 0;
+    if (amax > 0.f) frexpf(amax, &ex);
+    const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+    if (tid == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+    uint8_t* ph = planes;
+    uint8_t* pl = planes + (size_t)ntiles * 1024;
+    const int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    for (int idx = tid; idx < ntiles * 4; idx += nthr) {
+        const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
+        uint16_t hv[8], lv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int col = c0 + ord[j];
+            const float v = col < K ? x[col] * scale : 0.f;
+            const _Float16 h = (_Float16)v;
+            const _Float16 l = (_Float16)(v - (float)h);
+            hv[j] = __builtin_bit_cast(uint16_t, h);
+            lv[j] = __builtin_bit_cast(uint16_t, l);
+        }
+        const size_t off = ((size_t)t * 64 + 16 * s + b) * 16;
+        *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
+                                         hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+        *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
+                                         lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
+    }
+}
+
+}  // namespace cmf

@@ -1,0 +1,440 @@
+// Decode-layer kernels around the GEMVs: fused residual-add + RMSNorm +
+// activation preparation, qk-norm + RoPE + KV append, split-K decode
+// attention over the appended KV (causal inside the verify block), merge +
+// preparation, SwiGLU + preparation, embedding gather and argmax.
+//
+// Semantics follow the reference CPU path:
+//   rms_norm_into / add_rmsnorm_fused_into   inference.rs:33-86
+//   rmsnorm_head (qk-norm), rope_rotate       attention.rs:606-624, 71-81
+//   finish_projection order (norm then RoPE)  attention.rs:818-890
+//   attend_group (scale 1/sqrt(hd), softmax)  kv_cache.rs:521-690
+//   silu(g) * u                               inference.rs:14-16
+//   argmax, ties to the highest index         sampler.rs:832-867
+#include "common.h"
+#include "gemv.h"
+#include "layers.h"
+
+namespace cmf {
+
+// --------------------------------------------------------------------------
+// block reductions (256 threads)
+// --------------------------------------------------------------------------
+__device__ inline double block_sum_d(double v, double* red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    const int nw = blockDim.x >> 6;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+__device__ inline float block_max_f(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+    const int nw = blockDim.x >> 6;
+    for (int i = 1; i < nw; i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+__device__ inline void prep_any(const float* vals, int K, float amax, const PrepDst& d, int b) {
+    if (d.kind == 8) prep8_row(vals, K, amax, d.nk, b, d.planes, d.xs, threadIdx.x, blockDim.x);
+    else prep16_row(vals, K, amax, d.nk, b, d.planes, d.xs, threadIdx.x, blockDim.x);
+}
+
+// h[b] (+= delta[b]); out = rms_norm(h[b]) * w, prepared for the next GEMV.
+// One workgroup per batch row; H <= 8192.
+__global__ __launch_bounds__(256) void k_add_rmsnorm_prep(float* __restrict__ h, int ldh,
+                                                          const float* __restrict__ delta, int ldd,
+                                                          const float* __restrict__ w, int H,
+                                                          double eps, PrepDst dst,
+                                                          float* __restrict__ out_f32, int ldo) {
+    const int b = blockIdx.x;
+    __shared__ float vals[8192];
+    __shared__ double redd[4];
+    __shared__ float redf[4];
+    float* hr = h + (size_t)b * ldh;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float v = hr[i];
+        if (delta) {
+            v = v + delta[(size_t)b * ldd + i];
+            hr[i] = v;
+        }
+        vals[i] = v;
+        ss += (double)v * (double)v;
+    }
+    ss = block_sum_d(ss, redd);
+    const float inv = 1.0f / (float)sqrt(ss / (double)H + eps);
+    float am = 0.f;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const float o = vals[i] * inv * w[i];
+        vals[i] = o;
+        am = fmaxf(am, fabsf(o));
+        if (out_f32) out_f32[(size_t)b * ldo + i] = o;
+    }
+    am = block_max_f(am, redf);
+    __syncthreads();
+    prep_any(vals, H, am, dst, b);
+}
+
+// MTP input: cat = [rms_norm(embed(tok), enorm) ; rms_norm(hid, hnorm)]
+// (embedding first, pipeline.rs:3085-3094), prepared for eh_proj.
+__global__ __launch_bounds__(256) void k_mtp_cat_prep(const int* __restrict__ toks,
+                                                      const float* __restrict__ hid, int ldh,
+                                                      EmbedSrc emb, const float* __restrict__ enorm,
+                                                      const float* __restrict__ hnorm, int H,
+                                                      double eps, PrepDst dst) {
+    const int b = blockIdx.x;
+    __shared__ float vals[8192];
+    __shared__ double redd[4];
+    __shared__ float redf[4];
+    const int tok = toks[b];
+    const bool ok = tok >= 0 && tok < emb.rows;
+    const float rs = ok ? emb.rs[tok] : 0.f;
+    const int rb = tok >> 4, r = tok & 15;
+    double s1 = 0.0, s2 = 0.0;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float e = 0.f;
+        if (ok) {
+            const int kc = i >> 6, s = (i >> 4) & 3, j = i & 15;
+            const int8_t q = emb.w[(((size_t)rb * emb.nkc + kc) * 64 + 16 * s + r) * 16 + j];
+            e = (float)q * rs;
+        }
+        const float hv = hid[(size_t)b * ldh + i];
+        vals[i] = e;
+        vals[H + i] = hv;
+        s1 += (double)e * (double)e;
+        s2 += (double)hv * (double)hv;
+    }
+    s1 = block_sum_d(s1, redd);
+    __syncthreads();
+    s2 = block_sum_d(s2, redd);
+    const float i1 = 1.0f / (float)sqrt(s1 / (double)H + eps);
+    const float i2 = 1.0f / (float)sqrt(s2 / (double)H + eps);
+    float am = 0.f;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const float a = vals[i] * i1 * enorm[i];
+        const float c = vals[H + i] * i2 * hnorm[i];
+        vals[i] = a;
+        vals[H + i] = c;
+        am = fmaxf(am, fmaxf(fabsf(a), fabsf(c)));
+    }
+    am = block_max_f(am, redf);
+    __syncthreads();
+    prep_any(vals, 2 * H, am, dst, b);
+}
+
+// Embedding rows from the (tied) q8 lm_head: out[b] = q8 row * row_scale
+// (pipeline.rs:5568-5575).  grid (nb), block 256.
+__global__ __launch_bounds__(256) void k_embed(const int* __restrict__ toks, EmbedSrc emb, int H,
+                                               float* __restrict__ out, int ldo) {
+    const int b = blockIdx.x;
+    const int tok = toks[b];
+    const bool ok = tok >= 0 && tok < emb.rows;
+    const float rs = ok ? emb.rs[tok] : 0.f;
+    const int rb = tok >> 4, r = tok & 15;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        float e = 0.f;
+        if (ok) {
+            const int kc = i >> 6, s = (i >> 4) & 3, j = i & 15;
+            e = (float)emb.w[(((size_t)rb * emb.nkc + kc) * 64 + 16 * s + r) * 16 + j] * rs;
+        }
+        out[(size_t)b * ldo + i] = e;
+    }
+}
+
+// qk-norm + RoPE for the Q and K heads of qkv rows, K/V rows appended at
+// position pos0 + b.  grid (nb, nh + 2*nkv), block hd (<= 256, even).
+__global__ __launch_bounds__(256) void k_qk_rope_append(
+    const float* __restrict__ qkv, int ldq, const float* __restrict__ qn,
+    const float* __restrict__ kn, const float2* __restrict__ rope, int nh, int nkv, int hd,
+    double eps, const int* __restrict__ pbase, int padd, float* __restrict__ kc,
+    float* __restrict__ vc, int max_seq, float* __restrict__ qout, int ldqo) {
+    const int b = blockIdx.x, j = blockIdx.y, t = threadIdx.x;
+    const int pos = *pbase + padd + b;
+    __shared__ float x[256];
+    __shared__ double redd[4];
+    const float v = qkv[(size_t)b * ldq + (size_t)j * hd + t];
+    if (j >= nh + nkv) {  // V head: stored as projected
+        const int g = j - nh - nkv;
+        vc[((size_t)g * max_seq + pos) * hd + t] = v;
+        return;
+    }
+    const float* wn = j < nh ? qn : kn;
+    const double ss = block_sum_d((double)v * (double)v, redd);
+    const float inv = (float)(1.0 / sqrt(ss / (double)hd + eps));
+    x[t] = v * inv * wn[t];
+    __syncthreads();
+    const int half = hd >> 1;
+    float o;
+    if (t < half) {
+        const float2 cs = rope[(size_t)pos * half + t];  // (cos, sin)
+        o = x[t] * cs.x - x[t + half] * cs.y;
+    } else {
+        const float2 cs = rope[(size_t)pos * half + (t - half)];
+        o = x[t - half] * cs.y + x[t] * cs.x;
+    }
+    if (j < nh) {
+        qout[(size_t)b * ldqo + (size_t)j * hd + t] = o;
+    } else {
+        const int g = j - nh;
+        kc[((size_t)g * max_seq + pos) * hd + t] = o;
+    }
+}
+
+// Split-K decode attention.  grid (nkv, nchunks), block 256.  Query rows
+// b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.  Each block
+// handles ATT_C positions of one KV head for all nb * hpk queries and
+// writes (max, sum, unnormalised output) partials.
+__global__ __launch_bounds__(256) void k_attn_partial(
+    const float* __restrict__ q, int ldq, const float* __restrict__ kc,
+    const float* __restrict__ vc, int max_seq, int nb, int nh, int nkv, const int* __restrict__ pbase,
+    int padd, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po, int nch) {
+    constexpr int C = ATT_C, HD = 128;
+    const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    const int hpk = nh / nkv, nq = nb * hpk;
+    const int pos0 = *pbase + padd;
+    const int stored = pos0 + nb;  // rows present after this step's append
+    const int p0 = c * C;
+    __shared__ float Kt[HD][C + 1];
+    __shared__ float V[C][HD];
+    __shared__ float Q[32][HD];
+    __shared__ float S[32][C];
+    if (p0 >= stored) {
+        for (int i = t; i < nq; i += 256) {
+            const int bi = i / hpk, hh = i % hpk, h = g * hpk + hh;
+            const size_t row = (size_t)bi * nh + h;
+            pm[row * nch + c] = -INFINITY;
+            pl[row * nch + c] = 0.f;
+        }
+        return;
+    }
+    for (int i = t; i < nq * HD; i += 256) {
+        const int qi = i / HD, d = i % HD;
+        const int bi = qi / hpk, hh = qi % hpk;
+        Q[qi][d] = q[(size_t)bi * ldq + (size_t)(g * hpk + hh) * HD + d];
+    }
+    const float* Kg = kc + (size_t)g * max_seq * HD;
+    const float* Vg = vc + (size_t)g * max_seq * HD;
+    for (int i = t; i < C * HD; i += 256) {
+        const int p = i / HD, d = i % HD;
+        const bool in = p0 + p < stored;
+        Kt[d][p] = in ? Kg[(size_t)(p0 + p) * HD + d] : 0.f;
+        V[p][d] = in ? Vg[(size_t)(p0 + p) * HD + d] : 0.f;
+    }
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)HD);
+    {
+        const int p = t % C;
+        for (int qi = t / C; qi < nq; qi += 256 / C) {
+            const int bi = qi / hpk;
+            float acc = 0.f;
+#pragma unroll 8
+            for (int d = 0; d < HD; d++) acc += Q[qi][d] * Kt[d][p];
+            S[qi][p] = (p0 + p <= pos0 + bi) ? acc * scale : -INFINITY;
+        }
+    }
+    __syncthreads();
+    for (int qi = t; qi < nq; qi += 256) {
+        float m = -INFINITY;
+        for (int p = 0; p < C; p++) m = fmaxf(m, S[qi][p]);
+        float l = 0.f;
+        for (int p = 0; p < C; p++) {
+            const float e = m == -INFINITY ? 0.f : expf(S[qi][p] - m);
+            S[qi][p] = e;
+            l += e;
+        }
+        const int bi = qi / hpk, hh = qi % hpk, h = g * hpk + hh;
+        const size_t row = (size_t)bi * nh + h;
+        pm[row * nch + c] = m;
+        pl[row * nch + c] = l;
+    }
+    __syncthreads();
+    {
+        const int d = t % HD;
+        for (int qi = t / HD; qi < nq; qi += 256 / HD) {
+            float acc = 0.f;
+#pragma unroll 8
+            for (int p = 0; p < C; p++) acc += S[qi][p] * V[p][d];
+            const int bi = qi / hpk, hh = qi % hpk, h = g * hpk + hh;
+            const size_t row = (size_t)bi * nh + h;
+            po[(row * nch + c) * HD + d] = acc;
+        }
+    }
+}
+
+// Merge the partials of one query row (all heads) and prepare the result
+// for the O projection.  grid (nb), block 256.
+__global__ __launch_bounds__(256) void k_attn_merge_prep(const float* __restrict__ pm,
+                                                         const float* __restrict__ pl,
+                                                         const float* __restrict__ po, int nh,
+                                                         int nch, const int* __restrict__ pbase,
+                                                         int padd, PrepDst dst,
+                                                         float* __restrict__ out_f32) {
+    constexpr int HD = 128;
+    const int b = blockIdx.x;
+    __shared__ float vals[32 * HD];
+    __shared__ float redf[4];
+    const int pos0 = *pbase + padd;
+    const int used = (pos0 + b + ATT_C) / ATT_C;  // chunks holding keys 0..pos0+b
+    float am = 0.f;
+    for (int i = threadIdx.x; i < nh * HD; i += blockDim.x) {
+        const int h = i / HD, d = i % HD;
+        const size_t row = (size_t)b * nh + h;
+        float M = -INFINITY;
+        for (int c = 0; c < used; c++) M = fmaxf(M, pm[row * nch + c]);
+        float L = 0.f, O = 0.f;
+        for (int c = 0; c < used; c++) {
+            const float m = pm[row * nch + c];
+            if (m == -INFINITY) continue;
+            const float f = expf(m - M);
+            L += pl[row * nch + c] * f;
+            O += po[(row * nch + c) * HD + d] * f;
+        }
+        const float o = L > 0.f ? O / L : 0.f;
+        vals[i] = o;
+        if (out_f32) out_f32[(size_t)b * nh * HD + i] = o;
+        am = fmaxf(am, fabsf(o));
+    }
+    am = block_max_f(am, redf);
+    __syncthreads();
+    prep_any(vals, nh * HD, am, dst, b);
+}
+
+// SwiGLU on the fused gate/up output gu[b] = [g (I) ; u (I)], prepared for
+// the down projection.  grid (nb), block 256; I <= 12288.
+__global__ __launch_bounds__(256) void k_silu_mul_prep(const float* __restrict__ gu, int ldg, int I,
+                                                       PrepDst dst, float* __restrict__ out_f32) {
+    const int b = blockIdx.x;
+    __shared__ float vals[12288];
+    __shared__ float redf[4];
+    float am = 0.f;
+    for (int i = threadIdx.x; i < I; i += blockDim.x) {
+        const float g = gu[(size_t)b * ldg + i], u = gu[(size_t)b * ldg + I + i];
+        const float v = (g / (1.0f + expf(-g))) * u;
+        vals[i] = v;
+        if (out_f32) out_f32[(size_t)b * I + i] = v;
+        am = fmaxf(am, fabsf(v));
+    }
+    am = block_max_f(am, redf);
+    __syncthreads();
+    prep_any(vals, I, am, dst, b);
+}
+
+// Argmax per row, ties to the highest index.  Pass 1: grid (nslices, nrows).
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int ld, int n,
+                                                     int slice, float* __restrict__ pv,
+                                                     int* __restrict__ pi) {
+    const int s = blockIdx.x, r = blockIdx.y;
+    const float* row = x + (size_t)r * ld;
+    const int lo = s * slice, hi = min(n, lo + slice);
+    float bv = -INFINITY;
+    int bi = lo;
+    for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
+        const float v = row[i];
+        if (v > bv || (v == bv && i > bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o) {
+            const float v2 = sv[threadIdx.x + o];
+            const int i2 = si[threadIdx.x + o];
+            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 > si[threadIdx.x])) {
+                sv[threadIdx.x] = v2;
+                si[threadIdx.x] = i2;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        pv[(size_t)r * gridDim.x + s] = sv[0];
+        pi[(size_t)r * gridDim.x + s] = si[0];
+    }
+}
+
+// Pass 2: one thread per row.
+__global__ void k_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi, int ns,
+                               int nrows, int* __restrict__ out) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= nrows) return;
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int s = 0; s < ns; s++) {
+        const float v = pv[(size_t)r * ns + s];
+        const int i = pi[(size_t)r * ns + s];
+        if (v > bv || (v == bv && i > bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    out[r] = bi;
+}
+
+// ---------------------------------------------------------------------------
+// host launchers
+// ---------------------------------------------------------------------------
+void launch_add_rmsnorm_prep(float* h, int ldh, const float* delta, int ldd, const float* w, int H,
+                             double eps, const PrepDst& d, float* out, int ldo, int nb,
+                             hipStream_t st) {
+    hipLaunchKernelGGL(k_add_rmsnorm_prep, dim3(nb), dim3(256), 0, st, h, ldh, delta, ldd, w, H, eps,
+                       d, out, ldo);
+}
+
+void launch_mtp_cat_prep(const int* toks, const float* hid, int ldh, const EmbedSrc& e,
+                         const float* enorm, const float* hnorm, int H, double eps, const PrepDst& d,
+                         int nb, hipStream_t st) {
+    hipLaunchKernelGGL(k_mtp_cat_prep, dim3(nb), dim3(256), 0, st, toks, hid, ldh, e, enorm, hnorm,
+                       H, eps, d);
+}
+
+void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
+                  hipStream_t st) {
+    hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
+}
+
+void launch_qk_rope_append(const float* qkv, int ldq, const float* qn, const float* kn,
+                           const float2* rope, int nh, int nkv, int hd, double eps, const int* pbase,
+                           int padd, float* kc, float* vc, int max_seq, float* qout, int ldqo, int nb,
+                           hipStream_t st) {
+    hipLaunchKernelGGL(k_qk_rope_append, dim3(nb, nh + 2 * nkv), dim3(hd), 0, st, qkv, ldq, qn, kn,
+                       rope, nh, nkv, hd, eps, pbase, padd, kc, vc, max_seq, qout, ldqo);
+}
+
+void launch_attention(const float* q, int ldq, const float* kc, const float* vc, int max_seq, int nb,
+                      int nh, int nkv, const int* pbase, int padd, int max_len, float* pm, float* pl,
+                      float* po, int nch_cap, const PrepDst& d, float* out_f32, hipStream_t st) {
+    const int nch = (max_len + ATT_C - 1) / ATT_C;
+    hipLaunchKernelGGL(k_attn_partial, dim3(nkv, nch), dim3(256), 0, st, q, ldq, kc, vc, max_seq, nb,
+                       nh, nkv, pbase, padd, pm, pl, po, nch_cap);
+    hipLaunchKernelGGL(k_attn_merge_prep, dim3(nb), dim3(256), 0, st, pm, pl, po, nh, nch_cap, pbase,
+                       padd, d, out_f32);
+}
+
+void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_silu_mul_prep, dim3(nb), dim3(256), 0, st, gu, ldg, I, d, out);
+}
+
+void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
+                   hipStream_t st) {
+    const int slice = 4096, ns = (n + slice - 1) / slice;
+    hipLaunchKernelGGL(k_argmax_part, dim3(ns, nrows), dim3(256), 0, st, x, ld, n, slice, pv, pi);
+    hipLaunchKernelGGL(k_argmax_final, dim3((nrows + 63) / 64), dim3(64), 0, st, pv, pi, ns, nrows,
+                       out);
+}
+
+}  // namespace cmf

@@ -1,0 +1,30 @@
+// Runtime internals shared by runtime.hip and engine.hip.
+#pragma once
+
+#include <vector>
+
+#include "common.h"
+
+namespace cmf {
+
+hipStream_t stream();
+int device();
+int ensure_init();
+
+// Sources of a q4t / q4tp tensor, one entry per device row (concatenation of
+// several tensors along rows is expressed by appending their rows).
+struct Q4Src {
+    int dtype = 0;
+    int rows = 0, cols = 0;
+    std::vector<const uint8_t*> rowbase;  // q4t: 18-byte tiles; q4tp: 16-byte nibble tiles
+    std::vector<const uint8_t*> codes;    // q4tp: the row's 5-bit code bytes
+    std::vector<const uint8_t*> params;   // q4tp: the row's (f16 lo, f16 step)
+    size_t code_stride = 0;
+};
+
+int build_q8(DevWeight& w, int rows, int cols, const int8_t* const* rowptr, const float* rs);
+int build_q4(DevWeight& w, const Q4Src& src);
+int fill_q4src(Q4Src& s, int dtype, int rows, int cols, const uint8_t* payload, int row_offset);
+void free_weight(DevWeight& w);
+
+}  // namespace cmf

@@ -1,0 +1,493 @@
+// Library runtime: errors, device/stream, weight residency (upload + repack
+// into the device layouts of common.h) and the matmul seam entry points.
+#include <math.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/cmf_hip.h"
+#include "common.h"
+#include "gemv.h"
+#include "layers.h"
+#include "runtime.h"
+
+namespace cmf {
+
+static thread_local std::string g_err;
+void set_error(const std::string& m) { g_err = m; }
+int fail(const std::string& m) {
+    g_err = m;
+    return CMF_ERR;
+}
+
+static std::mutex g_mu;
+static bool g_init = false;
+static int g_dev = 0;
+static hipStream_t g_stream = nullptr;
+
+hipStream_t stream() { return g_stream; }
+int device() { return g_dev; }
+
+int ensure_init() {
+    if (g_init) return CMF_OK;
+    return cmf_init(0);
+}
+
+static float f16_to_f32_host(uint16_t h) {
+    uint32_t sign = h >> 15, exp = (h >> 10) & 0x1F, mant = h & 0x3FF, bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            uint32_t e = 0, m = mant;
+            while (!(m & 0x400)) {
+                m <<= 1;
+                e++;
+            }
+            bits = (sign << 31) | ((113 - e) << 23) | ((m & 0x3FF) << 13);
+        }
+    } else if (exp == 0x1F) {
+        bits = (sign << 31) | (0xFFu << 23) | (mant << 13);
+    } else {
+        bits = (sign << 31) | ((exp + 112) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// Repack on the host, then one upload.
+// ---------------------------------------------------------------------------
+static int upload_blocks(DevWeight& w, const std::vector<uint8_t>& wb, const void* sc, size_t scb,
+                         const std::vector<float2>* rp) {
+    CMF_HIP(hipMalloc(&w.w, wb.size()));
+    CMF_HIP(hipMemcpy(w.w, wb.data(), wb.size(), hipMemcpyHostToDevice));
+    CMF_HIP(hipMalloc(&w.scale, scb));
+    CMF_HIP(hipMemcpy(w.scale, sc, scb, hipMemcpyHostToDevice));
+    w.bytes = wb.size() + scb;
+    if (rp) {
+        CMF_HIP(hipMalloc(&w.rowp, rp->size() * sizeof(float2)));
+        CMF_HIP(hipMemcpy(w.rowp, rp->data(), rp->size() * sizeof(float2), hipMemcpyHostToDevice));
+        w.bytes += rp->size() * sizeof(float2);
+    }
+    w.device = g_dev;
+    return CMF_OK;
+}
+
+// q8: rows of int8 (stride `cols`) + f32 row scales.  row_of(i) maps device
+// row i to a source row pointer (concatenation support).
+int build_q8(DevWeight& w, int rows, int cols, const int8_t* const* rowptr, const float* rs) {
+    w.dtype = DT_Q8ROW;
+    w.rows = rows;
+    w.cols = cols;
+    w.rows_pad = (rows + 15) / 16 * 16;
+    w.cols_pad = (cols + 63) / 64 * 64;
+    w.kchunks = w.cols_pad / 64;
+    const int nrb = w.rows_pad / 16;
+    std::vector<uint8_t> wb((size_t)nrb * w.kchunks * 1024, 0);
+    for (int rb = 0; rb < nrb; rb++)
+        for (int kc = 0; kc < w.kchunks; kc++)
+            for (int s = 0; s < 4; s++)
+                for (int r = 0; r < 16; r++) {
+                    const int row = rb * 16 + r;
+                    if (row >= rows) continue;
+                    uint8_t* dst = wb.data() + (((size_t)rb * w.kchunks + kc) * 64 + 16 * s + r) * 16;
+                    const int c0 = kc * 64 + 16 * s;
+                    const int n = std::max(0, std::min(16, cols - c0));
+                    if (n > 0) memcpy(dst, rowptr[row] + c0, n);
+                }
+    std::vector<float> scl(w.rows_pad, 0.f);
+    memcpy(scl.data(), rs, sizeof(float) * rows);
+    return upload_blocks(w, wb, scl.data(), scl.size() * sizeof(float), nullptr);
+}
+
+static int code_at(const uint8_t* codes, size_t stride, size_t g) {
+    size_t bit = g * 5, b = bit / 8, sh = bit % 8;
+    uint16_t lo = codes[b];
+    uint16_t hi = (sh > 3 && b + 1 < stride) ? codes[b + 1] : 0;
+    return (int)(((lo | (hi << 8)) >> sh) & 0x1F);
+}
+
+int build_q4(DevWeight& w, const Q4Src& src) {
+    const int rows = src.rows, cols = src.cols;
+    if (cols % 32) return fail("q4 tensors need cols % 32 == 0");
+    w.dtype = src.dtype;
+    w.rows = rows;
+    w.cols = cols;
+    w.rows_pad = (rows + 15) / 16 * 16;
+    w.cols_pad = (cols + 127) / 128 * 128;
+    w.kchunks = w.cols_pad / 128;  // groups of 4 tiles
+    const int gpr = cols / 32, nrb = w.rows_pad / 16, ntg = w.kchunks;
+    const bool tp = src.dtype == DT_Q4TP;
+    const int tstride = tp ? 16 : 18, toff = tp ? 0 : 2;
+    std::vector<uint8_t> wb((size_t)nrb * ntg * 1024, 0);
+    std::vector<uint8_t> scl((size_t)nrb * ntg * (tp ? 64 : 128), 0);
+    std::vector<float2> rp;
+    if (tp) rp.assign(w.rows_pad, make_float2(0.f, 0.f));
+    for (int row = 0; row < rows; row++) {
+        const int rb = row / 16, r = row % 16;
+        const uint8_t* base = src.rowbase[row];
+        for (int tg = 0; tg < ntg; tg++) {
+            uint32_t cw = 0;
+            for (int t = 0; t < 4; t++) {
+                const int tile = tg * 4 + t;
+                if (tile >= gpr) continue;
+                const uint8_t* tb = base + (size_t)tile * tstride;
+                for (int s = 0; s < 4; s++) {
+                    uint8_t* dst = wb.data() + (((size_t)rb * ntg + tg) * 64 + 16 * s + r) * 16 + 4 * t;
+                    memcpy(dst, tb + toff + 4 * s, 4);
+                }
+                if (!tp) {
+                    uint8_t* sd = scl.data() + (((size_t)rb * ntg + tg) * 16 + r) * 8 + 2 * t;
+                    sd[0] = tb[0];
+                    sd[1] = tb[1];
+                } else {
+                    cw |= (uint32_t)code_at(src.codes[row], src.code_stride, tile) << (5 * t);
+                }
+            }
+            if (tp) memcpy(scl.data() + (((size_t)rb * ntg + tg) * 16 + r) * 4, &cw, 4);
+        }
+        if (tp) {
+            // 2^lo and 2^step with the host libm, as q4tp_ladder (quant.rs:399-410)
+            const uint8_t* p = src.params[row];
+            const float lo = f16_to_f32_host((uint16_t)(p[0] | (p[1] << 8)));
+            const float st = f16_to_f32_host((uint16_t)(p[2] | (p[3] << 8)));
+            rp[row] = make_float2(exp2f(lo), exp2f(st));
+        }
+    }
+    return upload_blocks(w, wb, scl.data(), scl.size(), tp ? &rp : nullptr);
+}
+
+int fill_q4src(Q4Src& s, int dtype, int rows, int cols, const uint8_t* payload, int row_offset) {
+    // appends rows of one payload to s (concatenation support)
+    const size_t gpr = cols / 32;
+    s.dtype = dtype;
+    s.cols = cols;
+    if (dtype == DT_Q4T) {
+        for (int r = 0; r < rows; r++) s.rowbase.push_back(payload + (size_t)r * gpr * 18);
+    } else {
+        const size_t nib = (size_t)rows * gpr * 16, stride = (gpr * 5 + 7) / 8;
+        s.code_stride = stride;
+        for (int r = 0; r < rows; r++) {
+            s.rowbase.push_back(payload + (size_t)r * gpr * 16);
+            s.params.push_back(payload + nib + (size_t)r * 4);
+            s.codes.push_back(payload + nib + (size_t)rows * 4 + (size_t)r * stride);
+        }
+    }
+    s.rows += rows;
+    (void)row_offset;
+    return CMF_OK;
+}
+
+void free_weight(DevWeight& w) {
+    if (w.w) (void)hipFree(w.w);
+    if (w.scale) (void)hipFree(w.scale);
+    if (w.rowp) (void)hipFree(w.rowp);
+    w.w = nullptr;
+    w.scale = nullptr;
+    w.rowp = nullptr;
+}
+
+// Device scratch for the host-slice seam ops (grown on demand).
+struct SeamScratch {
+    uint8_t* planes = nullptr;
+    size_t planes_cap = 0;
+    float* xs = nullptr;
+    float* x = nullptr;
+    size_t x_cap = 0;
+    float* y = nullptr;
+    size_t y_cap = 0;
+};
+static SeamScratch g_ss;
+
+static int grow(void** p, size_t* cap, size_t need) {
+    if (*cap >= need) return CMF_OK;
+    if (*p) (void)hipFree(*p);
+    *p = nullptr;
+    CMF_HIP(hipMalloc(p, need));
+    *cap = need;
+    return CMF_OK;
+}
+
+// y (host) = w rows [row0, row0+rows) * x (host), x [b][cols].
+int seam_matmat(const DevWeight& w, int row0, const float* xs, int b, int rows, float* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (row0 < 0 || rows < 1 || row0 + rows > w.rows) return fail("row range outside the tensor");
+    if (grow((void**)&g_ss.planes, &g_ss.planes_cap, prep_bytes(w)) != CMF_OK) return CMF_ERR;
+    if (!g_ss.xs) CMF_HIP(hipMalloc(&g_ss.xs, 64 * sizeof(float)));
+    const size_t xb = (size_t)std::min(b, MAXB) * w.cols * sizeof(float);
+    const size_t yb = (size_t)std::min(b, MAXB) * rows * sizeof(float);
+    if (grow((void**)&g_ss.x, &g_ss.x_cap, xb) != CMF_OK) return CMF_ERR;
+    if (grow((void**)&g_ss.y, &g_ss.y_cap, yb) != CMF_OK) return CMF_ERR;
+    hipStream_t st = stream();
+    for (int b0 = 0; b0 < b; b0 += MAXB) {
+        const int m = std::min(MAXB, b - b0);
+        CMF_HIP(hipMemcpyAsync(g_ss.x, xs + (size_t)b0 * w.cols, (size_t)m * w.cols * sizeof(float),
+                               hipMemcpyHostToDevice, st));
+        launch_prep(w, g_ss.x, w.cols, m, g_ss.planes, g_ss.xs, st);
+        if (launch_gemv(w, g_ss.planes, g_ss.xs, g_ss.y, rows, m, row0, row0 + rows, st) != CMF_OK)
+            return CMF_ERR;
+        CMF_HIP(hipMemcpyAsync(out + (size_t)b0 * rows, g_ss.y, (size_t)m * rows * sizeof(float),
+                               hipMemcpyDeviceToHost, st));
+    }
+    CMF_HIP(hipStreamSynchronize(st));
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
+}  // namespace cmf
+
+using namespace cmf;
+
+struct cmf_weight_s {
+    DevWeight w;
+};
+
+extern "C" {
+
+const char* cmf_last_error(void) { return g_err.c_str(); }
+
+int cmf_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int cmf_init(int dev) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_init) return CMF_OK;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail("no HIP device visible");
+    if (dev < 0 || dev >= n) return fail("device index out of range");
+    CMF_HIP(hipSetDevice(dev));
+    hipDeviceProp_t p;
+    CMF_HIP(hipGetDeviceProperties(&p, dev));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(std::string("libcmfhip is built for gfx950, device is ") + p.gcnArchName);
+    CMF_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    g_dev = dev;
+    g_init = true;
+    return CMF_OK;
+}
+
+int cmf_sync(void) {
+    if (!g_init) return fail("cmf_init not called");
+    CMF_HIP(hipStreamSynchronize(g_stream));
+    return CMF_OK;
+}
+
+int cmf_weight_upload(const uint8_t* payload, size_t nbytes, int dtype, int rows, int cols,
+                      cmf_weight* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!payload || !out || rows < 1 || cols < 1) return fail("weight_upload: bad arguments");
+    auto* h = new cmf_weight_s();
+    int rc;
+    if (dtype == DT_Q8ROW) {
+        if (nbytes < (size_t)rows * cols + (size_t)rows * 2) {
+            delete h;
+            return fail("q8 payload too short");
+        }
+        std::vector<const int8_t*> rp(rows);
+        std::vector<float> rs(rows);
+        for (int r = 0; r < rows; r++) {
+            rp[r] = (const int8_t*)payload + (size_t)r * cols;
+            const uint8_t* s = payload + (size_t)rows * cols + 2 * (size_t)r;
+            rs[r] = f16_to_f32_host((uint16_t)(s[0] | (s[1] << 8)));
+        }
+        rc = build_q8(h->w, rows, cols, rp.data(), rs.data());
+    } else if (dtype == DT_Q4T || dtype == DT_Q4TP) {
+        if (cols % 32) {
+            delete h;
+            return fail("q4 tensors need cols % 32 == 0");
+        }
+        const size_t gpr = cols / 32;
+        const size_t need = dtype == DT_Q4T ? (size_t)rows * gpr * 18
+                                            : (size_t)rows * gpr * 16 + (size_t)rows * 4 +
+                                                  (size_t)rows * ((gpr * 5 + 7) / 8);
+        if (nbytes < need) {
+            delete h;
+            return fail("q4 payload too short");
+        }
+        Q4Src s;
+        s.rows = 0;
+        fill_q4src(s, dtype, rows, cols, payload, 0);
+        rc = build_q4(h->w, s);
+    } else {
+        delete h;
+        return CMF_DECLINED;
+    }
+    if (rc != CMF_OK) {
+        free_weight(h->w);
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return CMF_OK;
+}
+
+int cmf_weight_upload_q8(const int8_t* q, const float* rs, int rows, int cols, cmf_weight* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!q || !rs || !out || rows < 1 || cols < 1) return fail("weight_upload_q8: bad arguments");
+    auto* h = new cmf_weight_s();
+    std::vector<const int8_t*> rp(rows);
+    for (int r = 0; r < rows; r++) rp[r] = q + (size_t)r * cols;
+    int rc = build_q8(h->w, rows, cols, rp.data(), rs);
+    if (rc != CMF_OK) {
+        free_weight(h->w);
+        delete h;
+        return rc;
+    }
+    *out = h;
+    return CMF_OK;
+}
+
+int cmf_weight_free(cmf_weight w) {
+    if (!w) return CMF_OK;
+    free_weight(w->w);
+    delete w;
+    return CMF_OK;
+}
+
+size_t cmf_weight_device_bytes(cmf_weight w) { return w ? w->w.bytes : 0; }
+
+static int seam(cmf_weight w, int dt, int row0, const float* xs, int b, int rows, int cols,
+                float* out) {
+    if (!w || !xs || !out) return fail("null argument");
+    if (w->w.dtype != dt) return CMF_DECLINED;  // not this codec: caller's CPU path
+    if (cols != w->w.cols) return fail("cols mismatch");
+    return seam_matmat(w->w, row0, xs, b, rows, out);
+}
+
+int cmf_q8_matvec_range(cmf_weight w, int row0, const float* xs, int rows, int cols, float* out) {
+    return seam(w, DT_Q8ROW, row0, xs, 1, rows, cols, out);
+}
+int cmf_q8_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out) {
+    return seam(w, DT_Q8ROW, 0, xs, b, rows, cols, out);
+}
+int cmf_q4t_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out) {
+    return seam(w, DT_Q4T, 0, xs, 1, rows, cols, out);
+}
+int cmf_q4t_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out) {
+    return seam(w, DT_Q4T, 0, xs, b, rows, cols, out);
+}
+int cmf_q4tp_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out) {
+    return seam(w, DT_Q4TP, 0, xs, 1, rows, cols, out);
+}
+int cmf_q4tp_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out) {
+    return seam(w, DT_Q4TP, 0, xs, b, rows, cols, out);
+}
+
+int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b, int hidden,
+            int inter, float* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!w1 || !w3 || !w2 || !xs || !out) return fail("null argument");
+    if (w1->w.rows != inter || w3->w.rows != inter || w1->w.cols != hidden || w3->w.cols != hidden ||
+        w2->w.rows != hidden || w2->w.cols != inter)
+        return fail("ffn: shape mismatch");
+    if (w1->w.dtype != w3->w.dtype) return CMF_DECLINED;
+    hipStream_t st = stream();
+    // device buffers: x [m][hidden], g/u [m][2*inter], planes, out [m][hidden]
+    float *dx = nullptr, *dgu = nullptr, *dy = nullptr, *dxs = nullptr;
+    uint8_t* pl = nullptr;
+    const size_t pb = std::max(prep_bytes(w1->w), prep_bytes(w2->w));
+    CMF_HIP(hipMalloc(&dx, (size_t)MAXB * hidden * sizeof(float)));
+    CMF_HIP(hipMalloc(&dgu, (size_t)MAXB * 2 * inter * sizeof(float)));
+    CMF_HIP(hipMalloc(&dy, (size_t)MAXB * hidden * sizeof(float)));
+    CMF_HIP(hipMalloc(&dxs, 64 * sizeof(float)));
+    CMF_HIP(hipMalloc(&pl, pb));
+    int rc = CMF_OK;
+    for (int b0 = 0; b0 < b && rc == CMF_OK; b0 += MAXB) {
+        const int m = std::min(MAXB, b - b0);
+        CMF_HIP(hipMemcpyAsync(dx, xs + (size_t)b0 * hidden, (size_t)m * hidden * 4, hipMemcpyHostToDevice, st));
+        launch_prep(w1->w, dx, hidden, m, pl, dxs, st);
+        rc = launch_gemv(w1->w, pl, dxs, dgu, 2 * inter, m, 0, inter, st);
+        if (rc == CMF_OK) rc = launch_gemv(w3->w, pl, dxs, dgu + inter, 2 * inter, m, 0, inter, st);
+        if (rc != CMF_OK) break;
+        PrepDst d{w2->w.dtype == DT_Q8ROW ? 8 : 16,
+                  w2->w.dtype == DT_Q8ROW ? w2->w.kchunks : w2->w.kchunks * 4, pl, dxs};
+        launch_silu_mul_prep(dgu, 2 * inter, inter, d, nullptr, m, st);
+        rc = launch_gemv(w2->w, pl, dxs, dy, hidden, m, 0, hidden, st);
+        if (rc != CMF_OK) break;
+        CMF_HIP(hipMemcpyAsync(out + (size_t)b0 * hidden, dy, (size_t)m * hidden * 4, hipMemcpyDeviceToHost, st));
+    }
+    CMF_HIP(hipStreamSynchronize(st));
+    (void)hipFree(dx);
+    (void)hipFree(dgu);
+    (void)hipFree(dy);
+    (void)hipFree(dxs);
+    (void)hipFree(pl);
+    if (rc == CMF_OK) CMF_HIP(hipGetLastError());
+    return rc;
+}
+
+void* cmf_dev_alloc(size_t bytes) {
+    if (ensure_init() != CMF_OK) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+        set_error("hipMalloc failed");
+        return nullptr;
+    }
+    return p;
+}
+int cmf_dev_free(void* p) {
+    if (p) CMF_HIP(hipFree(p));
+    return CMF_OK;
+}
+int cmf_h2d(void* d, const void* s, size_t n) {
+    CMF_HIP(hipMemcpy(d, s, n, hipMemcpyHostToDevice));
+    return CMF_OK;
+}
+int cmf_d2h(void* d, const void* s, size_t n) {
+    CMF_HIP(hipMemcpy(d, s, n, hipMemcpyDeviceToHost));
+    return CMF_OK;
+}
+
+size_t cmf_prep_bytes(cmf_weight w) { return w ? prep_bytes(w->w) : 0; }
+
+int cmf_prep_dev(cmf_weight w, const float* d_x, int ldx, int b, void* d_planes, float* d_xs) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!w || b < 1 || b > MAXB) return fail("prep_dev: bad arguments");
+    launch_prep(w->w, d_x, ldx, b, (uint8_t*)d_planes, d_xs, stream());
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
+int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int b, float* d_y,
+                      int ldy, int ks) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!w) return fail("null weight");
+    int rc = launch_gemv(w->w, (const uint8_t*)d_planes, d_xs, d_y, ldy, b, 0, w->w.rows, stream(), ks);
+    if (rc != CMF_OK) return rc;
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
+int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const float* d_xs, int b,
+                  float* d_y, int ldy, int ks, int warmup, int iters, float* avg_ms) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!ws || nw < 1 || iters < 1) return fail("time_gemv: bad arguments");
+    hipStream_t st = stream();
+    for (int i = 0; i < warmup; i++)
+        if (launch_gemv(ws[i % nw]->w, (const uint8_t*)d_planes, d_xs, d_y, ldy, b, 0, ws[i % nw]->w.rows, st, ks) != CMF_OK)
+            return CMF_ERR;
+    hipEvent_t e0, e1;
+    CMF_HIP(hipEventCreate(&e0));
+    CMF_HIP(hipEventCreate(&e1));
+    CMF_HIP(hipEventRecord(e0, st));
+    for (int i = 0; i < iters; i++)
+        launch_gemv(ws[i % nw]->w, (const uint8_t*)d_planes, d_xs, d_y, ldy, b, 0, ws[i % nw]->w.rows, st, ks);
+    CMF_HIP(hipEventRecord(e1, st));
+    CMF_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_ms = ms / iters;
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
+}  // extern "C"

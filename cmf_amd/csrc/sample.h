@@ -1,0 +1,59 @@
+// Device-side decode state and the sparse sampling chain + speculative
+// acceptance (sampler.rs:440-514, 661-711) run on the GPU.
+#pragma once
+
+#include <functional>
+
+#include "../../include/cmf_hip.h"
+#include "common.h"
+
+namespace cmf {
+
+constexpr int SPARSE_K_MAX = 64;  // largest top_k the device sampler serves
+constexpr int SLICE = 4096;       // logits per selection block
+
+// Decode state kept in HBM; kernels read positions from it so a round needs
+// no host values.
+struct DState {
+    int next_pos;        // next trunk position (trunk KV holds [0, next_pos))
+    int a;               // accepted drafts of the last round
+    int t_next;          // token to emit next
+    int t_new;           // token picked by the last accept / plain pick
+    int n_out;           // tokens emitted
+    int accepted;        // total accepted drafts
+    int forced;          // correction token of the last round, -1 if none
+    int pad;
+    unsigned long long rng;  // SplitMix64 state (sampler.rs:54-84)
+    int drafts[16];
+    int vtok[17];
+    int argmax[17];
+};
+
+enum class SampleMode { Draft, Plain, Accept };
+
+struct SampleBufs {
+    int V = 0, nslices = 0;
+    int* cid = nullptr;     // [rows][nslices][K_MAX]
+    float* cv = nullptr;
+    float* smax = nullptr;  // [rows][nslices]
+    float* ssum = nullptr;
+    int* rid = nullptr;     // [rows][K_MAX] merged, value desc / id asc
+    float* rv = nullptr;
+    float* lmax = nullptr;  // [rows]
+    float* sum = nullptr;   // [rows]
+    int* qid = nullptr;     // draft distributions [8][K_MAX]
+    float* qp = nullptr;
+    int* qn = nullptr;      // [8]
+};
+
+int sample_alloc(SampleBufs& b, int V, const std::function<int(void**, size_t)>& alloc);
+
+// Selection + the sparse chain for `rows` logit rows (ld = V), then:
+//   Draft : q_j from row 0, draw -> st->drafts[j]
+//   Plain : p from row 0, draw -> st->t_new
+//   Accept: rows 0..k against q_0..q_{k-1}; emits [t_next, accepted drafts]
+//           into out, sets a, forced, t_new (correction or draw from row a)
+void sample_rows(SampleBufs& b, const float* logits, int V, int rows, const cmf_sampler_config& sc,
+                 DState* st, SampleMode mode, int j_or_k, int* out, hipStream_t s);
+
+}  // namespace cmf

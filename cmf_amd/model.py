@@ -1,0 +1,109 @@
+"""The device-resident decode engine (libcmfhip cmf_model_*).
+
+Mirrors the reference pipeline's decode entry points (pipeline.rs):
+prefill (prompt positions + MTP warm), the speculative decode loop
+(graph_spec_step rounds) or plain decode, and the batched verify forward
+(forward_batch_graph)."""
+import ctypes as C
+
+import numpy as np
+
+from . import (CmfError, GenStats, LayerDesc, ModelConfig, SamplerConfig, Tensor, _ptr, check, lib)
+
+
+def _tensor(t, keep):
+    q = rs = b = None
+    if t["q"] is not None:
+        q = np.ascontiguousarray(t["q"], dtype=np.int8)
+        rs = np.ascontiguousarray(t["row_scale"], dtype=np.float32)
+        keep += [q, rs]
+    if t["bytes"] is not None:
+        b = np.ascontiguousarray(t["bytes"], dtype=np.uint8)
+        keep.append(b)
+    return Tensor(t["dtype"], t["rows"], t["cols"], _ptr(q), _ptr(rs), _ptr(b))
+
+
+def _f32(a, keep):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    keep.append(a)
+    return _ptr(a)
+
+
+def _layer(l, keep):
+    return LayerDesc(_f32(l["input_norm"], keep), _f32(l["post_norm"], keep), _f32(l["q_norm"], keep),
+                     _f32(l["k_norm"], keep), _tensor(l["wq"], keep), _tensor(l["wk"], keep),
+                     _tensor(l["wv"], keep), _tensor(l["wo"], keep), _tensor(l["gate"], keep),
+                     _tensor(l["up"], keep), _tensor(l["down"], keep))
+
+
+class Model:
+    def __init__(self, sm):
+        c = sm["cfg"]
+        self.cfg = c
+        mc = ModelConfig(c["n_layers"], c["hidden"], c["n_heads"], c["n_kv"], c["head_dim"], c["inter"],
+                         c["vocab"], c["max_seq"], c["rope_theta"], c["eps"])
+        h = C.c_void_p()
+        check(lib().cmf_model_create(C.byref(mc), C.byref(h)))
+        self.h = h
+        for li, l in enumerate(sm["layers"]):
+            keep = []
+            check(lib().cmf_model_set_layer(self.h, li, C.byref(_layer(l, keep))))
+        keep = []
+        check(lib().cmf_model_set_head(self.h, C.byref(_tensor(sm["lm_head"], keep)),
+                                       _f32(sm["final_norm"], keep)))
+        self.has_mtp = "mtp" in sm
+        if self.has_mtp:
+            mt, keep = sm["mtp"], []
+            check(lib().cmf_model_set_mtp(self.h, _f32(mt["enorm"], keep), _f32(mt["hnorm"], keep),
+                                          C.byref(_tensor(mt["eh_proj"], keep)),
+                                          C.byref(_layer(mt["layer"], keep)), _f32(mt["norm"], keep)))
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(lib().cmf_prefill(self.h, _ptr(ids), len(ids)))
+
+    def decode(self, max_tokens, sampler=None, seed=0, spec=True, k=4):
+        """Returns (tokens, stats).  sampler=None is greedy."""
+        sc = sampler if sampler is not None else SamplerConfig(temperature=0.0, repetition_penalty=1.0)
+        out = np.zeros(max_tokens + k + 2, dtype=np.int32)
+        st = GenStats()
+        ok = check(lib().cmf_decode(self.h, max_tokens, C.byref(sc), seed, 1 if spec else 0, k, _ptr(out),
+                                    C.byref(st)))
+        if not ok:
+            raise CmfError("decode declined (penalised sampler config or top_k beyond the device sampler)")
+        return out[: st.generated].copy(), st
+
+    def forward_batch(self, tokens, pos0, want_logits=True):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        b = len(tokens)
+        hid = np.empty((b, self.cfg["hidden"]), dtype=np.float32)
+        lg = np.empty((b, self.cfg["vocab"]), dtype=np.float32) if want_logits else None
+        check(lib().cmf_forward_batch(self.h, _ptr(tokens), b, pos0, _ptr(hid), _ptr(lg)))
+        return hid, lg
+
+    def kv_truncate(self, n):
+        check(lib().cmf_kv_truncate(self.h, n))
+
+    def state(self):
+        np_ = C.c_int()
+        hid = np.empty(self.cfg["hidden"], dtype=np.float32)
+        check(lib().cmf_state_get(self.h, C.byref(np_), _ptr(hid)))
+        return np_.value, hid
+
+    def kv_export(self, li, n):
+        c = self.cfg
+        k = np.empty((c["n_kv"], n, c["head_dim"]), dtype=np.float32)
+        v = np.empty_like(k)
+        check(lib().cmf_kv_export(self.h, li, n, _ptr(k), _ptr(v)))
+        return k, v
+
+    def free(self):
+        if getattr(self, "h", None):
+            lib().cmf_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -1,0 +1,167 @@
+/*
+ * libcmfhip — MI355X (gfx950) backend for the cortiq decode hot path.
+ *
+ * A C ABI shaped like the engine's GPU backend seam
+ * (infosave2007/cmf crates/cortiq-engine/src/gpu.rs): plain pointers and
+ * sizes, no framework types.  Return convention of every op (gpu.rs:1-12,
+ * where `false` means "declined, the caller runs the CPU path"):
+ *     0  done                     (CMF_OK)
+ *    >0  declined, nothing written (the caller runs its CPU path)
+ *    <0  error; cmf_last_error() says why (thread-local, like
+ *        cortiq_last_error in crates/cortiq-ffi/include/cortiq.h:6-24)
+ * Calls on one handle are serialised by the caller (cortiq.h:3-5); every
+ * handle runs on one HIP stream.
+ */
+#ifndef CMF_HIP_H
+#define CMF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* TensorDtype ids, cortiq-core/src/types.rs:10-90 */
+#define CMF_DT_Q8ROW 3
+#define CMF_DT_Q4T 11
+#define CMF_DT_Q4TP 15
+
+/* ---- library -------------------------------------------------------- */
+/* Thread-local message of the last failing call (cortiq.h:6-24). */
+const char* cmf_last_error(void);
+/* Select the device and create the library stream.  Replaces the backend
+ * selection of gpu.rs:866-936.  Idempotent. */
+int cmf_init(int device);
+int cmf_device_count(void);
+/* Wait for all work on the library stream. */
+int cmf_sync(void);
+
+/* ---- weights (residency: gpu.rs:507 weight_is_resident) -------------- */
+typedef struct cmf_weight_s* cmf_weight;
+
+/* Upload a tensor payload in the reference byte layout (quant.rs):
+ *   CMF_DT_Q8ROW: [int8 rows*cols][f16 scale rows]      (quant.rs:4-5)
+ *   CMF_DT_Q4T  : rows*cols/32 tiles of [f16 scale][16 B nibbles] (:322)
+ *   CMF_DT_Q4TP : [nibbles][row params f16 lo,step][5-bit codes]  (:346-431)
+ * The library repacks it once into its device layout. */
+int cmf_weight_upload(const uint8_t* payload, size_t nbytes, int dtype, int rows, int cols,
+                      cmf_weight* out);
+/* q8 in the engine's in-memory form: int8 rows + f32 row_scale
+ * (QTensor::from_model q8 arm, qtensor.rs:196-231). */
+int cmf_weight_upload_q8(const int8_t* q, const float* row_scale, int rows, int cols,
+                         cmf_weight* out);
+int cmf_weight_free(cmf_weight w);
+size_t cmf_weight_device_bytes(cmf_weight w);
+
+/* ---- seam ops on host slices (gpu.rs) -------------------------------- */
+/* gpu.rs:1104 q8_matvec_range: rows [row0, row0+rows) of w times x. */
+int cmf_q8_matvec_range(cmf_weight w, int row0, const float* xs, int rows, int cols, float* out);
+/* gpu.rs:1155 q8_matmat: out[b*rows + r], b <= 16 per launch (larger b is
+ * split into launches of 16). */
+int cmf_q8_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out);
+/* gpu.rs:2423 / 2439 */
+int cmf_q4t_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out);
+int cmf_q4t_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out);
+/* gpu.rs:2400 / 2358 */
+int cmf_q4tp_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out);
+int cmf_q4tp_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out);
+/* gpu.rs:1773 / 1794 q4t_ffn / q4tp_ffn: out = w2 * (silu(w1 x) * (w3 x)),
+ * xs [b][hidden], out [b][hidden]. */
+int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b, int hidden,
+            int inter, float* out);
+
+/* ---- device-resident variants (inputs already in HBM) ----------------- */
+void* cmf_dev_alloc(size_t bytes);
+int cmf_dev_free(void* p);
+int cmf_h2d(void* dst, const void* src, size_t bytes);
+int cmf_d2h(void* dst, const void* src, size_t bytes);
+/* Bytes of the prepared-activation buffer a GEMV on w needs (b <= 16). */
+size_t cmf_prep_bytes(cmf_weight w);
+/* Prepare x[b][ldx] (device f32) for w: planes (cmf_prep_bytes) + xs[16]. */
+int cmf_prep_dev(cmf_weight w, const float* d_x, int ldx, int b, void* d_planes, float* d_xs);
+/* y[b][ldy] = w * x from prepared activations; all pointers on the device.
+ * ks = waves per workgroup splitting K (0 = heuristic). */
+int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int b, float* d_y,
+                      int ldy, int ks);
+/* Average device time (ms) of `iters` back-to-back launches of the GEMV
+ * on ws[i % nw] (rotating copies defeat the 256 MB last-level cache),
+ * measured with HIP events on the library stream. */
+int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const float* d_xs, int b,
+                  float* d_y, int ldy, int ks, int warmup, int iters, float* avg_ms);
+
+/* ---- model: Qwen3-arch decoder + MTP head (pipeline.rs) --------------- */
+typedef struct cmf_model_s* cmf_model;
+
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv, head_dim, inter, vocab, max_seq;
+    float rope_theta;
+    double eps;
+} cmf_model_config;
+
+/* A quantized tensor as the engine holds it (QTensor): q8 as int8 rows +
+ * f32 row_scale, q4t / q4tp as their quant.rs payloads. */
+typedef struct {
+    int dtype, rows, cols;
+    const int8_t* q;
+    const float* row_scale;
+    const uint8_t* bytes;
+} cmf_tensor;
+
+/* One decoder block (LayerWeights, AttnKind::Full + dense SwiGLU FFN). */
+typedef struct {
+    const float *input_norm, *post_norm, *q_norm, *k_norm;
+    cmf_tensor wq, wk, wv, wo, gate, up, down;
+} cmf_layer_desc;
+
+int cmf_model_create(const cmf_model_config* cfg, cmf_model* out);
+int cmf_model_free(cmf_model m);
+int cmf_model_set_layer(cmf_model m, int li, const cmf_layer_desc* d);
+/* lm_head (q8) doubles as the tied embedding table; final_norm [hidden]. */
+int cmf_model_set_head(cmf_model m, const cmf_tensor* lm_head, const float* final_norm);
+/* MtpModule (pipeline.rs:600-612). */
+int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh_proj,
+                      const cmf_layer_desc* layer, const float* norm);
+
+/* SamplerConfig (sampler.rs:88-121).  Penalised configs are declined by the
+ * device sampler (speculation is gated off under penalties,
+ * pipeline.rs:2035-2037). */
+typedef struct {
+    float temperature, top_p;
+    uint32_t top_k;
+    float repetition_penalty, min_p, presence_penalty;
+} cmf_sampler_config;
+
+typedef struct {
+    int generated, drafted, accepted, rounds;
+    double device_ms;
+} cmf_gen_stats;
+
+/* Prefill ids at positions 0..n-1 (trunk KV + MTP warm on the (h_p,
+ * id_{p+1}) pairs, pipeline.rs:2275-2318) and reset the decode state. */
+int cmf_prefill(cmf_model m, const int32_t* ids, int n);
+/* Decode after cmf_prefill: samples the first token from the prefill's last
+ * hidden, then runs graph_spec_step rounds (spec=1, k drafts,
+ * pipeline.rs:3582-4213) or plain tokens (spec=0) until at least max_tokens
+ * are produced.  out: capacity max_tokens + k + 1.  Returns via stats. */
+int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
+               int k, int32_t* out, cmf_gen_stats* st);
+/* forward_batch_graph counterpart (gpu.rs:1466-1497): run b tokens at
+ * positions pos0.. through the trunk (appending KV), write final hidden rows
+ * [b][hidden] and logits [b][vocab] (either may be NULL). */
+int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden,
+                      float* logits);
+/* KV rollback (kv_cache.rs:883 truncate_last / gpu.rs:1514 graph_kv_reset):
+ * the decode position moves back by n. */
+int cmf_kv_truncate(cmf_model m, int n);
+/* Decode state after cmf_prefill / cmf_decode: next position, the tip
+ * hidden [hidden] (trunk output at next_pos-1). */
+int cmf_state_get(cmf_model m, int* next_pos, float* hidden);
+/* Copy KV rows [0, n) of layer li (li == -1: the MTP block) into
+ * k/v [n_kv][n][head_dim]. */
+int cmf_kv_export(cmf_model m, int li, int n, float* k, float* v);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,241 @@
+"""ctypes bindings of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg as the checker / CPU baseline, never by the
+product package cmf_amd.  The C sources restate the reference CPU path of
+infosave2007/cmf and cite it file:line (see oracle.h).
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+DT_Q8ROW, DT_Q4T, DT_Q4TP = 3, 11, 15
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+class QT(C.Structure):
+    _fields_ = [("dtype", C.c_int), ("rows", C.c_int), ("cols", C.c_int), ("q", C.c_void_p),
+                ("row_scale", C.c_void_p), ("bytes", C.c_void_p)]
+
+
+class Cfg(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("hidden", C.c_int), ("n_heads", C.c_int), ("n_kv", C.c_int),
+                ("head_dim", C.c_int), ("inter", C.c_int), ("vocab", C.c_int), ("max_seq", C.c_int),
+                ("rope_theta", C.c_float), ("eps", C.c_double)]
+
+
+class Layer(C.Structure):
+    _fields_ = [("input_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p), ("wq", QT), ("wk", QT), ("wv", QT), ("wo", QT), ("gate", QT),
+                ("up", QT), ("down", QT)]
+
+
+class Model(C.Structure):
+    _fields_ = [("cfg", Cfg), ("layers", C.c_void_p), ("lm_head", QT), ("final_norm", C.c_void_p),
+                ("has_mtp", C.c_int), ("enorm", C.c_void_p), ("hnorm", C.c_void_p), ("mtp_norm", C.c_void_p),
+                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int)]
+
+
+class KV(C.Structure):
+    _fields_ = [("k", C.c_void_p), ("v", C.c_void_p), ("len", C.c_int)]
+
+
+class State(C.Structure):
+    _fields_ = [("trunk", C.c_void_p), ("mtp", KV), ("inv_freq", C.c_void_p)]
+
+
+class SamplerCfg(C.Structure):
+    _fields_ = [("temperature", C.c_float), ("top_p", C.c_float), ("top_k", C.c_uint32),
+                ("repetition_penalty", C.c_float), ("min_p", C.c_float), ("presence_penalty", C.c_float)]
+
+
+class GenCfg(C.Structure):
+    _fields_ = [("spec", C.c_int), ("k", C.c_int), ("sc", SamplerCfg), ("seed", C.c_uint64)]
+
+
+class GenStats(C.Structure):
+    _fields_ = [("drafted", C.c_int), ("accepted", C.c_int), ("rounds", C.c_int)]
+
+
+_lib = None
+P = C.c_void_p
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            build()
+        L = C.CDLL(LIB)
+        sig = {
+            "or_f16_to_f32": (C.c_float, [C.c_uint16]),
+            "or_f32_to_f16": (C.c_uint16, [C.c_float]),
+            "or_dequant_q8_row": (None, [P, C.c_int, C.c_int, P]),
+            "or_dequant_q4t": (None, [P, C.c_size_t, P]),
+            "or_q4tp_code": (C.c_int, [P, C.c_size_t, C.c_size_t]),
+            "or_q4tp_put_code": (None, [P, C.c_size_t, C.c_int]),
+            "or_q4tp_ladder": (None, [P, C.c_size_t, P]),
+            "or_dequant_q4tp": (None, [P, C.c_int, C.c_int, P]),
+            "or_matvec": (None, [C.POINTER(QT), P, P, C.c_int]),
+            "or_matmat": (None, [C.POINTER(QT), P, C.c_int, P, C.c_int]),
+            "or_matvec_a8w8": (None, [C.POINTER(QT), P, P, C.c_int]),
+            "or_split_act": (C.c_int, [P, C.c_int, P, P, P, P, P]),
+            "or_rng_next_u64": (C.c_uint64, [P]),
+            "or_rng_next_f32": (C.c_float, [P]),
+            "or_argmax": (C.c_uint32, [P, C.c_int]),
+            "or_sparse_distribution": (C.c_int, [P, C.c_int, C.POINTER(SamplerCfg), P, C.c_int, P, P]),
+            "or_draw_sparse": (C.c_uint32, [P, P, C.c_int, P]),
+            "or_spec_accept_sparse": (C.c_int64, [P, P, C.c_int, P, P, C.c_int, C.c_uint32, P]),
+            "or_spec_accept_dense": (C.c_int64, [P, P, C.c_int, C.c_uint32, P]),
+            "or_categorical": (C.c_uint32, [P, C.c_int, C.c_float]),
+            "or_sample": (C.c_uint32, [P, C.c_int, C.POINTER(SamplerCfg), P, C.c_int, P]),
+            "or_rms_norm": (None, [P, P, C.c_int, C.c_double, P]),
+            "or_rope_inv_freq": (None, [C.c_int, C.c_float, P]),
+            "or_embed": (None, [C.POINTER(Model), C.c_uint32, P]),
+            "or_forward": (None, [C.POINTER(Model), C.POINTER(State), P, C.c_int]),
+            "or_logits": (None, [C.POINTER(Model), P, P]),
+            "or_mtp_step": (None, [C.POINTER(Model), C.POINTER(State), P, C.c_uint32, C.c_int, P, P]),
+            "or_generate": (C.c_int, [C.POINTER(Model), C.POINTER(State), P, C.c_int, C.c_int,
+                                      C.POINTER(GenCfg), P, C.POINTER(GenStats)]),
+            "or_decode": (C.c_int, [C.POINTER(Model), C.POINTER(State), P, C.c_int, P, C.c_int, C.c_int,
+                                    C.POINTER(GenCfg), P, P, C.POINTER(GenStats)]),
+            "or_moe_route": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, P, P]),
+            "or_moe_ffn": (None, [P, C.c_int, C.c_int, P, P, C.c_int, P, C.c_int]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype, f.argtypes = r, a
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def qt(t, keep):
+    q = rs = b = None
+    if t.get("q") is not None:
+        q = np.ascontiguousarray(t["q"], dtype=np.int8)
+        rs = np.ascontiguousarray(t["row_scale"], dtype=np.float32)
+        keep += [q, rs]
+    if t.get("bytes") is not None:
+        b = np.ascontiguousarray(t["bytes"], dtype=np.uint8)
+        keep.append(b)
+    return QT(t["dtype"], t["rows"], t["cols"], _p(q), _p(rs), _p(b))
+
+
+def matmat(t, xs, threads=8, a8w8=False):
+    """Exact-contract (or a8w8 for b == 1) reference matmul: [b][rows]."""
+    keep = []
+    w = qt(t, keep)
+    xs = np.ascontiguousarray(np.atleast_2d(xs), dtype=np.float32)
+    b = xs.shape[0]
+    out = np.empty((b, t["rows"]), dtype=np.float32)
+    if a8w8:
+        for i in range(b):
+            lib().or_matvec_a8w8(C.byref(w), _p(xs[i]), _p(out[i]), threads)
+    else:
+        lib().or_matmat(C.byref(w), _p(xs), b, _p(out), threads)
+    return out
+
+
+def _f32(a, keep):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    keep.append(a)
+    return _p(a)
+
+
+def _layer(l, keep):
+    return Layer(_f32(l["input_norm"], keep), _f32(l["post_norm"], keep), _f32(l["q_norm"], keep),
+                 _f32(l["k_norm"], keep), qt(l["wq"], keep), qt(l["wk"], keep), qt(l["wv"], keep),
+                 qt(l["wo"], keep), qt(l["gate"], keep), qt(l["up"], keep), qt(l["down"], keep))
+
+
+class OracleModel:
+    """The CPU reference model over the same synthetic arrays the GPU uses."""
+
+    def __init__(self, sm, threads=8):
+        c = sm["cfg"]
+        self.c = c
+        self.keep = []
+        layers = (Layer * c["n_layers"])(*[_layer(l, self.keep) for l in sm["layers"]])
+        self.keep.append(layers)
+        m = Model()
+        m.cfg = Cfg(c["n_layers"], c["hidden"], c["n_heads"], c["n_kv"], c["head_dim"], c["inter"], c["vocab"],
+                    c["max_seq"], c["rope_theta"], c["eps"])
+        m.layers = C.cast(layers, C.c_void_p)
+        m.lm_head = qt(sm["lm_head"], self.keep)
+        m.final_norm = _f32(sm["final_norm"], self.keep)
+        m.threads = threads
+        if "mtp" in sm:
+            mt = sm["mtp"]
+            m.has_mtp = 1
+            m.enorm = _f32(mt["enorm"], self.keep)
+            m.hnorm = _f32(mt["hnorm"], self.keep)
+            m.mtp_norm = _f32(mt["norm"], self.keep)
+            m.eh_proj = qt(mt["eh_proj"], self.keep)
+            m.mtp = _layer(mt["layer"], self.keep)
+        self.m = m
+        self.reset()
+
+    def reset(self, kv_len=0, mtp_len=0):
+        c = self.c
+        shape = (c["n_kv"], c["max_seq"], c["head_dim"])
+        self.kk = [np.zeros(shape, np.float32) for _ in range(c["n_layers"] + 1)]
+        self.vv = [np.zeros(shape, np.float32) for _ in range(c["n_layers"] + 1)]
+        self.kvs = (KV * c["n_layers"])(*[KV(_p(self.kk[i]), _p(self.vv[i]), kv_len) for i in range(c["n_layers"])])
+        self.inv = np.empty(c["head_dim"] // 2, np.float32)
+        lib().or_rope_inv_freq(c["head_dim"], c["rope_theta"], _p(self.inv))
+        self.st = State(C.cast(self.kvs, C.c_void_p), KV(_p(self.kk[-1]), _p(self.vv[-1]), mtp_len), _p(self.inv))
+
+    def import_kv(self, li, k, v):
+        """Load rows [0, n) of layer li (-1: MTP) from [n_kv][n][hd] arrays."""
+        i = li if li >= 0 else self.c["n_layers"]
+        n = k.shape[1]
+        self.kk[i][:, :n] = k
+        self.vv[i][:, :n] = v
+        if li >= 0:
+            self.kvs[li].len = n
+        else:
+            self.st.mtp.len = n
+
+    def generate(self, prompt, max_tokens, spec=True, k=4, sampler=None, seed=0):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        sc = sampler or SamplerCfg(0.0, 0.9, 40, 1.0, 0.05, 0.0)
+        g = GenCfg(1 if spec else 0, k, sc, seed)
+        out = np.zeros(max_tokens + k + 2, np.uint32)
+        st = GenStats()
+        n = lib().or_generate(C.byref(self.m), C.byref(self.st), _p(prompt), len(prompt), max_tokens, C.byref(g),
+                              _p(out), C.byref(st))
+        return out[:n].astype(np.int32), st
+
+    def decode(self, hidden, next_pos, ids, max_tokens, spec=True, k=4, sampler=None, seed=0):
+        hidden = np.ascontiguousarray(hidden, dtype=np.float32).copy()
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        sc = sampler or SamplerCfg(0.0, 0.9, 40, 1.0, 0.05, 0.0)
+        g = GenCfg(1 if spec else 0, k, sc, seed)
+        out = np.zeros(max_tokens + k + 2, np.uint32)
+        st = GenStats()
+        rs = C.c_uint64(seed)
+        n = lib().or_decode(C.byref(self.m), C.byref(self.st), _p(hidden), next_pos, _p(ids), len(ids), max_tokens,
+                            C.byref(g), C.byref(rs), _p(out), C.byref(st))
+        return out[:n].astype(np.int32), st
+
+    def forward(self, tok, pos):
+        h = np.empty(self.c["hidden"], np.float32)
+        lib().or_embed(C.byref(self.m), tok, _p(h))
+        lib().or_forward(C.byref(self.m), C.byref(self.st), _p(h), pos)
+        return h
+
+    def logits(self, h):
+        out = np.empty(self.c["vocab"], np.float32)
+        lib().or_logits(C.byref(self.m), _p(np.ascontiguousarray(h, np.float32)), _p(out))
+        return out
