@@ -101,6 +101,9 @@ SIGNATURES = {
     "cmf_model_set_mtp": (_I, [_P, _P, _P, C.POINTER(Tensor), C.POINTER(LayerDesc), _P]),
     "cmf_prefill": (_I, [_P, _P, _I]),
     "cmf_decode": (_I, [_P, _I, C.POINTER(SamplerConfig), _U64, _I, _I, _P, C.POINTER(GenStats)]),
+    "cmf_decode_begin": (_I, [_P, C.POINTER(SamplerConfig), _U64]),
+    "cmf_decode_rounds": (_I, [_P, _I, _I, _I, C.POINTER(GenStats)]),
+    "cmf_decode_tokens": (_I, [_P, _P, _I]),
     "cmf_forward_batch": (_I, [_P, _P, _I, _I, _P, _P]),
     "cmf_kv_truncate": (_I, [_P, _I]),
     "cmf_state_get": (_I, [_P, C.POINTER(_I), _P]),

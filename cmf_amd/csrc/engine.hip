@@ -58,6 +58,10 @@ struct cmf_model_s {
     std::vector<void*> allocs;
     int next_pos_host = 0;
     bool prefilled = false;
+    bool decoding = false;
+    int rounds = 0;
+    int emitted_host = 0;
+    cmf_sampler_config sc{};
 };
 
 namespace {
@@ -465,79 +469,106 @@ static void pick_from_tip(cmf_model m, bool sampling, const cmf_sampler_config* 
     else launch_argmax(m->logits, m->c.vocab, m->c.vocab, 1, m->am_v, m->am_i, m->st->argmax, s);
 }
 
-int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
-               int k, int32_t* out, cmf_gen_stats* stats) {
-    if (ready(m)) return CMF_ERR;
-    if (!m->prefilled) return fail("decode: call cmf_prefill first");
-    if (!sc || !out || max_tokens < 1) return fail("decode: bad arguments");
-    if (spec && !m->has_mtp) return fail("decode: speculation needs the MTP head (cmf_model_set_mtp)");
-    if (spec && (k < 1 || k > 8)) return fail("decode: k must be 1..8 (CMF_GRAPH_SPEC_K range)");
-    if (sc->repetition_penalty != 1.0f || sc->presence_penalty != 0.0f) return CMF_DECLINED;
-    const bool sampling = sc->temperature >= 1e-6f;
-    if (sampling && (sc->top_k < 1 || sc->top_k > SPARSE_K_MAX)) return CMF_DECLINED;
-    if (m->next_pos_host + max_tokens + k + 2 > m->c.max_seq) return fail("decode: max_seq too small");
-    if (ensure_out(m, max_tokens + 16)) return CMF_ERR;
-    hipStream_t s = stream();
+// One speculative round (graph_spec_step, pipeline.rs:3582-4213) on the
+// device state: K chained MTP drafts, the K+1-row verify, acceptance, the
+// MTP re-warm of the verified pairs and the commit.  np = next_pos (host
+// mirror, sizes the attention grids).
+static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_config& sc, int np,
+                       hipStream_t s) {
     const int H = m->c.hidden, V = m->c.vocab;
     int* pb = &m->st->next_pos;
-    hipEvent_t e0, e1;
-    CMF_HIP(hipEventCreate(&e0));
-    CMF_HIP(hipEventCreate(&e1));
+    for (int j = 0; j < k; j++) {
+        const int* tok = j == 0 ? &m->st->t_next : &m->st->drafts[j - 1];
+        const float* hin = j == 0 ? m->h_tip : m->hm;
+        mtp_step(m, tok, hin, pb, j - 1, np + j, s);
+        if (sampling) sample_rows(m->sb, m->logits, V, 1, sc, m->st, SampleMode::Draft, j, nullptr, s);
+        else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, &m->st->drafts[j], s);
+    }
+    hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
+    launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, k + 1, s);
+    trunk_forward(m, k + 1, pb, 0, np + k + 1, true, s);
+    if (sampling) {
+        sample_rows(m->sb, m->logits, V, k + 1, sc, m->st, SampleMode::Accept, k, m->out, s);
+    } else {
+        launch_argmax(m->logits, V, V, k + 1, m->am_v, m->am_i, m->st->argmax, s);
+        hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(1), 0, s, m->st, k, m->out);
+    }
+    mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, s);
+    hipLaunchKernelGGL(k_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H);
+}
+
+// One plain decode step: forward t_next at next_pos, emit it, pick the next.
+static void plain_step(cmf_model m, bool sampling, const cmf_sampler_config& sc, int np, hipStream_t s) {
+    const int H = m->c.hidden, V = m->c.vocab;
+    int* pb = &m->st->next_pos;
+    launch_embed(&m->st->t_next, embed_src(m), H, m->hv, H, 1, s);
+    trunk_forward(m, 1, pb, 0, np + 1, true, s);
+    if (sampling) sample_rows(m->sb, m->logits, V, 1, sc, m->st, SampleMode::Plain, 0, nullptr, s);
+    else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, m->st->argmax, s);
+    hipLaunchKernelGGL(k_plain_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H, m->out,
+                       sampling ? 1 : 0);
+}
+
+static int check_sampler(cmf_model m, const cmf_sampler_config* sc) {
+    if (!sc) return fail("null sampler config");
+    if (sc->repetition_penalty != 1.0f || sc->presence_penalty != 0.0f) return CMF_DECLINED;
+    if (sc->temperature >= 1e-6f) {
+        if (sc->top_k < 1 || (int)sc->top_k > SPARSE_K_MAX) return CMF_DECLINED;
+        if (m->sb.nslices * (int)sc->top_k > SLICE) return CMF_DECLINED;
+    }
+    return CMF_OK;
+}
+
+int cmf_decode_begin(cmf_model m, const cmf_sampler_config* sc, uint64_t seed) {
+    if (ready(m)) return CMF_ERR;
+    if (!m->prefilled) return fail("decode: call cmf_prefill first");
+    int rc = check_sampler(m, sc);
+    if (rc != CMF_OK) return rc;
+    if (ensure_out(m, m->c.max_seq + 32)) return CMF_ERR;
+    hipStream_t s = stream();
     DState init{};
     init.next_pos = m->next_pos_host;
     init.rng = seed;
+    init.forced = -1;
     CMF_HIP(hipMemcpyAsync(m->st, &init, sizeof(DState), hipMemcpyHostToDevice, s));
     CMF_HIP(hipStreamSynchronize(s));
-    CMF_HIP(hipEventRecord(e0, s));
+    m->sc = *sc;
+    const bool sampling = sc->temperature >= 1e-6f;
     pick_from_tip(m, sampling, sc, s);
     hipLaunchKernelGGL(k_first_token, dim3(1), dim3(1), 0, s, m->st, sampling ? 1 : 0);
-    int generated = 0, rounds = 0, np = m->next_pos_host;
+    CMF_HIP(hipStreamSynchronize(s));
+    CMF_HIP(hipGetLastError());
+    m->decoding = true;
+    m->rounds = 0;
+    m->emitted_host = 0;
+    return CMF_OK;
+}
+
+int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats) {
+    if (ready(m)) return CMF_ERR;
+    if (!m->decoding) return fail("decode_rounds: call cmf_decode_begin first");
+    if (spec && !m->has_mtp) return fail("decode: speculation needs the MTP head (cmf_model_set_mtp)");
+    if (spec && (k < 1 || k > 8)) return fail("decode: k must be 1..8 (CMF_GRAPH_SPEC_K range)");
+    if (n < 0) return fail("decode_rounds: n < 0");
+    const int per = spec ? k + 1 : 1;
+    if (m->next_pos_host + (n + 1) * per + 2 > m->c.max_seq) return fail("decode: max_seq too small");
+    if (m->emitted_host + (n + 1) * per + 2 > m->out_cap) return fail("decode: output buffer full");
+    hipStream_t s = stream();
+    const bool sampling = m->sc.temperature >= 1e-6f;
+    hipEvent_t e0, e1;
+    CMF_HIP(hipEventCreate(&e0));
+    CMF_HIP(hipEventCreate(&e1));
+    CMF_HIP(hipEventRecord(e0, s));
     DState hs{};
-    while (true) {
-        if (generated + 1 >= max_tokens) {  // emitting t_next reaches max_tokens
-            hipLaunchKernelGGL(k_emit, dim3(1), dim3(1), 0, s, m->st, m->out);
-            generated += 1;
-            break;
-        }
-        if (spec && generated + 2 < max_tokens) {
-            // ---- graph_spec_step: draft K from the MTP head ----
-            for (int j = 0; j < k; j++) {
-                const int* tok = j == 0 ? &m->st->t_next : &m->st->drafts[j - 1];
-                const float* hin = j == 0 ? m->h_tip : m->hm;
-                mtp_step(m, tok, hin, pb, j - 1, np + j, s);
-                if (sampling)
-                    sample_rows(m->sb, m->logits, V, 1, *sc, m->st, SampleMode::Draft, j, nullptr, s);
-                else
-                    launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, &m->st->drafts[j], s);
-            }
-            // ---- verify the K+1 rows in one batched forward ----
-            hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
-            launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, k + 1, s);
-            trunk_forward(m, k + 1, pb, 0, np + k + 1, true, s);
-            // ---- accept ----
-            if (sampling) {
-                sample_rows(m->sb, m->logits, V, k + 1, *sc, m->st, SampleMode::Accept, k, m->out, s);
-            } else {
-                launch_argmax(m->logits, V, V, k + 1, m->am_v, m->am_i, m->st->argmax, s);
-                hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(1), 0, s, m->st, k, m->out);
-            }
-            // ---- commit: MTP re-warm on the verified pairs, then advance ----
-            mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, s);
-            hipLaunchKernelGGL(k_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H);
+    int np = m->next_pos_host;
+    for (int r = 0; r < n; r++) {
+        if (spec) {
+            spec_round(m, k, sampling, m->sc, np, s);
             CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
             CMF_HIP(hipStreamSynchronize(s));
-            rounds++;
-            generated = hs.n_out;
             np = hs.next_pos;
         } else {
-            // ---- plain step: forward t_next ----
-            launch_embed(&m->st->t_next, embed_src(m), H, m->hv, H, 1, s);
-            trunk_forward(m, 1, pb, 0, np + 1, true, s);
-            if (sampling) sample_rows(m->sb, m->logits, V, 1, *sc, m->st, SampleMode::Plain, 0, nullptr, s);
-            else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, m->st->argmax, s);
-            hipLaunchKernelGGL(k_plain_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H, m->out,
-                               sampling ? 1 : 0);
-            generated += 1;
+            plain_step(m, sampling, m->sc, np, s);
             np += 1;
         }
     }
@@ -549,18 +580,62 @@ int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64
     CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    std::vector<int> tok(hs.n_out);
-    CMF_HIP(hipMemcpy(tok.data(), m->out, hs.n_out * sizeof(int), hipMemcpyDeviceToHost));
-    for (int i = 0; i < hs.n_out; i++) out[i] = tok[i];
-    // the stream state continues from here
     m->next_pos_host = hs.next_pos;
+    m->emitted_host = hs.n_out;
+    m->rounds += spec ? n : 0;
     if (stats) {
         stats->generated = hs.n_out;
-        stats->drafted = rounds * k;
+        stats->drafted = m->rounds * k;
         stats->accepted = hs.accepted;
-        stats->rounds = rounds;
+        stats->rounds = m->rounds;
         stats->device_ms = ms;
     }
+    return CMF_OK;
+}
+
+int cmf_decode_tokens(cmf_model m, int32_t* out, int cap) {
+    if (!m || !out) return fail("decode_tokens: null argument");
+    const int n = std::min(cap, m->emitted_host);
+    if (n > 0) CMF_HIP(hipMemcpy(out, m->out, n * sizeof(int), hipMemcpyDeviceToHost));
+    return n;
+}
+
+// The reference decode loop (pipeline.rs:2546-2980) over the device rounds:
+// emit t_next; a speculative round while generated + 1 < max_tokens, else a
+// plain step; the last token is emitted without a forward.
+int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
+               int k, int32_t* out, cmf_gen_stats* stats) {
+    if (!out || max_tokens < 1) return fail("decode: bad arguments");
+    int rc = cmf_decode_begin(m, sc, seed);
+    if (rc != CMF_OK) return rc;
+    hipStream_t s = stream();
+    double ms = 0.0;
+    cmf_gen_stats st{};
+    int generated = 0;
+    while (true) {
+        if (generated + 1 >= max_tokens) {
+            hipLaunchKernelGGL(k_emit, dim3(1), dim3(1), 0, s, m->st, m->out);
+            CMF_HIP(hipStreamSynchronize(s));
+            m->emitted_host += 1;
+            generated += 1;
+            break;
+        }
+        const bool sp = spec && generated + 2 < max_tokens;
+        rc = cmf_decode_rounds(m, 1, sp ? 1 : 0, k, &st);
+        if (rc != CMF_OK) return rc;
+        ms += st.device_ms;
+        generated = m->emitted_host;
+    }
+    const int n = cmf_decode_tokens(m, out, m->emitted_host);
+    if (n < 0) return CMF_ERR;
+    if (stats) {
+        stats->generated = n;
+        stats->drafted = m->rounds * k;
+        stats->accepted = st.accepted;
+        stats->rounds = m->rounds;
+        stats->device_ms = ms;
+    }
+    m->decoding = false;
     return CMF_OK;
 }
 

@@ -73,6 +73,23 @@ class Model:
             raise CmfError("decode declined (penalised sampler config or top_k beyond the device sampler)")
         return out[: st.generated].copy(), st
 
+    def decode_begin(self, sampler=None, seed=0):
+        sc = sampler if sampler is not None else SamplerConfig(temperature=0.0, repetition_penalty=1.0)
+        if not check(lib().cmf_decode_begin(self.h, C.byref(sc), seed)):
+            raise CmfError("decode declined (penalised sampler config or top_k beyond the device sampler)")
+
+    def decode_rounds(self, n, spec=True, k=4):
+        st = GenStats()
+        check(lib().cmf_decode_rounds(self.h, n, 1 if spec else 0, k, C.byref(st)))
+        return st
+
+    def tokens(self):
+        out = np.zeros(self.cfg["max_seq"] + 32, dtype=np.int32)
+        n = lib().cmf_decode_tokens(self.h, _ptr(out), len(out))
+        if n < 0:
+            check(n)
+        return out[:n].copy()
+
     def forward_batch(self, tokens, pos0, want_logits=True):
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         b = len(tokens)

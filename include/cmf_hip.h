@@ -146,6 +146,14 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n);
  * are produced.  out: capacity max_tokens + k + 1.  Returns via stats. */
 int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
                int k, int32_t* out, cmf_gen_stats* st);
+/* The same loop in pieces, for callers that pace it themselves:
+ * begin (reset the emitted stream, sample the first token from the tip),
+ * exactly n speculative rounds (spec=1) or plain steps (spec=0) with no
+ * end-of-generation gating, and a copy of the emitted tokens (returns the
+ * count).  device_ms in stats is the device time of that call. */
+int cmf_decode_begin(cmf_model m, const cmf_sampler_config* sc, uint64_t seed);
+int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* st);
+int cmf_decode_tokens(cmf_model m, int32_t* out, int cap);
 /* forward_batch_graph counterpart (gpu.rs:1466-1497): run b tokens at
  * positions pos0.. through the trunk (appending KV), write final hidden rows
  * [b][hidden] and logits [b][vocab] (either may be NULL). */
