@@ -41,7 +41,7 @@ struct cmf_model_s {
     float2* rope = nullptr;
     // scratch
     float *hv = nullptr, *hm = nullptr, *attn_out = nullptr, *ffn_out = nullptr, *qkv_out = nullptr,
-          *qrot = nullptr, *gu_out = nullptr, *logits = nullptr;
+          *qrot = nullptr, *ao = nullptr, *xrows = nullptr, *hm2 = nullptr, *gu_out = nullptr, *logits = nullptr;
     uint8_t* planes = nullptr;
     size_t planes_cap = 0;
     float* xs = nullptr;
@@ -166,39 +166,90 @@ EmbedSrc embed_src(cmf_model_s* m) {
     return EmbedSrc{(const int8_t*)m->lm.w, (const float*)m->lm.scale, m->lm.rows, m->lm.kchunks};
 }
 
-// One decoder block over nb rows of h at positions *pb + padd + i.  The
-// pending residual `pend` (the previous block's FFN output) is added by the
-// fused norm, as forward_layers adds it before the next rms_norm.
-void run_block(cmf_model_s* m, LayerDev& l, float* h, const float* pend, int nb, const int* pb,
-               int padd, int max_len, hipStream_t s) {
+XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
+    XSrc r{};
+    r.mode = XS_NORM;
+    r.x = x;
+    r.ldx = ldx;
+    r.w = w;
+    r.eps = eps;
+    return r;
+}
+
+// W x with the operand produced in-kernel (LDS-staged).  Batches whose
+// operand does not fit the LDS staging are split into sub-batches that do
+// (each re-reads the weights); there is no global-memory operand path in
+// the model.
+int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int nb, bool resid,
+           hipStream_t s) {
+    (void)m;
+    int step = nb;
+    while (step > 1 && !fits_lds(w, step)) step--;
+    if (!fits_lds(w, step)) return fail("gemv: one operand row exceeds the LDS staging");
+    for (int b0 = 0; b0 < nb; b0 += step) {
+        const int mb = std::min(step, nb - b0);
+        XSrc sb = src;
+        sb.x = src.x ? src.x + (size_t)b0 * src.ldx : nullptr;
+        if (sb.toks) sb.toks = src.toks + b0;
+        const int rc = gemv(w, sb, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s);
+        if (rc != CMF_OK) return rc;
+    }
+    return CMF_OK;
+}
+
+// One decoder block over nb rows of the residual h at positions *pb + padd
+// + i (forward_layers_span, pipeline.rs:7981-8700):
+//   h += Wo attn(qk-norm/RoPE(Wqkv rms_norm(h)))
+//   h += Wdown (silu(Wg rms_norm(h)) * Wu rms_norm(h))
+// The norms and SwiGLU are evaluated inside the GEMVs that consume them and
+// the residual adds are their epilogues.
+void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int padd, int max_len,
+               hipStream_t s) {
     const auto& c = m->c;
     const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
     const int QKV = (nh + 2 * nkv) * hd, I = c.inter;
-    launch_add_rmsnorm_prep(h, H, pend, H, l.in_norm, H, c.eps, prep_for(m, l.qkv), nullptr, 0, nb, s);
-    launch_gemv(l.qkv, m->planes, m->xs, m->qkv_out, QKV, nb, 0, QKV, s);
+    gemv_f(m, l.qkv, src_norm(h, H, l.in_norm, c.eps), m->qkv_out, QKV, nb, false, s);
     launch_qk_rope_append(m->qkv_out, QKV, l.q_norm, l.k_norm, m->rope, nh, nkv, hd, c.eps, pb, padd,
                           l.kc, l.vc, c.max_seq, m->qrot, nh * hd, nb, s);
     launch_attention(m->qrot, nh * hd, l.kc, l.vc, c.max_seq, nb, nh, nkv, pb, padd, max_len, m->pm,
-                     m->pl, m->po, m->nch_cap, prep_for(m, l.wo), nullptr, s);
-    launch_gemv(l.wo, m->planes, m->xs, m->attn_out, H, nb, 0, H, s);
-    launch_add_rmsnorm_prep(h, H, m->attn_out, H, l.post_norm, H, c.eps, prep_for(m, l.gu), nullptr, 0,
-                            nb, s);
-    launch_gemv(l.gu, m->planes, m->xs, m->gu_out, 2 * I, nb, 0, 2 * I, s);
-    launch_silu_mul_prep(m->gu_out, 2 * I, I, prep_for(m, l.down), nullptr, nb, s);
-    launch_gemv(l.down, m->planes, m->xs, m->ffn_out, H, nb, 0, H, s);
+                     m->pl, m->po, m->nch_cap, m->ao, s);
+    XSrc ra{};
+    ra.mode = XS_ROWS;
+    ra.x = m->ao;
+    ra.ldx = nh * hd;
+    gemv_f(m, l.wo, ra, h, H, nb, true, s);
+    gemv_f(m, l.gu, src_norm(h, H, l.post_norm, c.eps), m->gu_out, 2 * I, nb, false, s);
+    XSrc sg{};
+    sg.mode = XS_SILU;
+    sg.x = m->gu_out;
+    sg.ldx = 2 * I;
+    sg.K = I;
+    gemv_f(m, l.down, sg, h, H, nb, true, s);
 }
 
-// Trunk forward of nb rows already in m->hv; leaves the final hidden rows in
-// m->hv and the lm_head input prepared; logits when want_logits.
+// Trunk forward of nb rows in m->hv (embeddings in, final hidden rows out,
+// pre-norm as forward_layers returns them); logits when want_logits.
 void trunk_forward(cmf_model_s* m, int nb, const int* pb, int padd, int max_len, bool want_logits,
                    hipStream_t s) {
     const auto& c = m->c;
-    const int H = c.hidden;
-    for (int li = 0; li < c.n_layers; li++)
-        run_block(m, m->L[li], m->hv, li == 0 ? nullptr : m->ffn_out, nb, pb, padd, max_len, s);
-    launch_add_rmsnorm_prep(m->hv, H, m->ffn_out, H, m->final_norm, H, c.eps, prep_for(m, m->lm),
-                            nullptr, 0, nb, s);
-    if (want_logits) launch_gemv(m->lm, m->planes, m->xs, m->logits, c.vocab, nb, 0, c.vocab, s);
+    for (int li = 0; li < c.n_layers; li++) run_block(m, m->L[li], m->hv, nb, pb, padd, max_len, s);
+    if (want_logits)
+        gemv_f(m, m->lm, src_norm(m->hv, c.hidden, m->final_norm, c.eps), m->logits, c.vocab, nb, false, s);
+}
+
+XSrc src_cat(cmf_model_s* m, const int* toks, const float* hid) {
+    XSrc r{};
+    r.mode = XS_CAT;
+    r.x = hid;
+    r.ldx = m->c.hidden;
+    r.w = m->enorm;
+    r.w2 = m->hnorm;
+    r.toks = toks;
+    r.emb = embed_src(m);
+    r.H = m->c.hidden;
+    r.K = 2 * m->c.hidden;
+    r.eps = m->c.eps;
+    return r;
 }
 
 // MTP warm (mtp_warm, pipeline.rs:3532-3572): eh_proj on [enorm(embed(tok));
@@ -208,28 +259,22 @@ void mtp_warm(cmf_model_s* m, const int* toks, const float* hid, int nb, const i
     const auto& c = m->c;
     const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
     const int QKV = (nh + 2 * nkv) * hd;
-    launch_mtp_cat_prep(toks, hid, H, embed_src(m), m->enorm, m->hnorm, H, c.eps, prep_for(m, m->eh), nb, s);
-    launch_gemv(m->eh, m->planes, m->xs, m->hm, H, nb, 0, H, s);
-    launch_add_rmsnorm_prep(m->hm, H, nullptr, H, m->mtp.in_norm, H, c.eps, prep_for(m, m->mtp.qkv),
-                            nullptr, 0, nb, s);
-    launch_gemv(m->mtp.qkv, m->planes, m->xs, m->qkv_out, QKV, nb, 0, QKV, s);
+    gemv_f(m, m->eh, src_cat(m, toks, hid), m->hm, H, nb, false, s);
+    gemv_f(m, m->mtp.qkv, src_norm(m->hm, H, m->mtp.in_norm, c.eps), m->qkv_out, QKV, nb, false, s);
     launch_qk_rope_append(m->qkv_out, QKV, m->mtp.q_norm, m->mtp.k_norm, m->rope, nh, nkv, hd, c.eps, pb,
                           padd, m->mtp.kc, m->mtp.vc, c.max_seq, m->qrot, nh * hd, nb, s);
 }
 
 // One MTP draft step (mtp_step_hl, pipeline.rs:3051-3160) for a single row:
-// tok (device), hidden hin (device row) -> m->hm = block output hidden,
-// logits row 0.
-void mtp_step(cmf_model_s* m, const int* tok, const float* hin, const int* pb, int padd, int max_len,
-              hipStream_t s) {
+// tok (device), hidden hin (device row) -> hout = the block's output hidden
+// (hout != hin), logits row 0.
+void mtp_step(cmf_model_s* m, const int* tok, const float* hin, float* hout, const int* pb, int padd,
+              int max_len, hipStream_t s) {
     const auto& c = m->c;
     const int H = c.hidden;
-    launch_mtp_cat_prep(tok, hin, H, embed_src(m), m->enorm, m->hnorm, H, c.eps, prep_for(m, m->eh), 1, s);
-    launch_gemv(m->eh, m->planes, m->xs, m->hm, H, 1, 0, H, s);
-    run_block(m, m->mtp, m->hm, nullptr, 1, pb, padd, max_len, s);
-    launch_add_rmsnorm_prep(m->hm, H, m->ffn_out, H, m->mtp_norm, H, c.eps, prep_for(m, m->lm), nullptr, 0,
-                            1, s);
-    launch_gemv(m->lm, m->planes, m->xs, m->logits, c.vocab, 1, 0, c.vocab, s);
+    gemv_f(m, m->eh, src_cat(m, tok, hin), hout, H, 1, false, s);
+    run_block(m, m->mtp, hout, 1, pb, padd, max_len, s);
+    gemv_f(m, m->lm, src_norm(hout, H, m->mtp_norm, c.eps), m->logits, c.vocab, 1, false, s);
 }
 
 int alloc_scratch(cmf_model_s* m) {
@@ -238,7 +283,9 @@ int alloc_scratch(cmf_model_s* m) {
     m->nch_cap = (c.max_seq + ATT_C - 1) / ATT_C;
     if (dalloc_t(m, &m->hv, (size_t)MAXB * H) || dalloc_t(m, &m->hm, (size_t)MAXB * H) ||
         dalloc_t(m, &m->attn_out, (size_t)MAXB * H) || dalloc_t(m, &m->ffn_out, (size_t)MAXB * H) ||
-        dalloc_t(m, &m->qkv_out, (size_t)MAXB * QKV) || dalloc_t(m, &m->qrot, (size_t)MAXB * c.n_heads * hd) ||
+        dalloc_t(m, &m->qkv_out, (size_t)MAXB * QKV) || dalloc_t(m, &m->qrot, (size_t)MAXB * c.n_heads * hd) || dalloc_t(m, &m->ao, (size_t)MAXB * c.n_heads * hd) ||
+        dalloc_t(m, &m->xrows, (size_t)MAXB * std::max(std::max(2 * H, c.inter), c.n_heads * hd)) ||
+        dalloc_t(m, &m->hm2, (size_t)MAXB * H) ||
         dalloc_t(m, &m->gu_out, (size_t)MAXB * 2 * c.inter) || dalloc_t(m, &m->xs, 64) ||
         dalloc_t(m, &m->pm, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->pl, (size_t)MAXB * c.n_heads * m->nch_cap) ||
@@ -283,6 +330,9 @@ int ensure_out(cmf_model_s* m, int cap) {
 }
 
 __global__ void k_set_int(int* p, int v) { *p = v; }
+
+// prompt positions per prefill step (the verify batch class of kernels)
+constexpr int PREFILL_CHUNK = 4;
 
 __global__ void k_copy_rows_i32(int* dst, const int* src, int n) {
     const int i = threadIdx.x;
@@ -357,6 +407,8 @@ int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
         c.vocab < 1 || c.max_seq < 8 || c.inter < 32)
         return fail("model_create: bad config");
     if (c.head_dim != 128) return fail("model_create: the attention kernels are built for head_dim 128");
+    if ((c.n_heads / c.n_kv) & (c.n_heads / c.n_kv - 1))
+        return fail("model_create: query heads per KV head must be a power of two");
     if (c.hidden > 4096 || c.inter > 12288 || c.n_heads * c.head_dim > 4096)
         return fail("model_create: hidden <= 4096, inter <= 12288, heads*head_dim <= 4096");
     if (c.hidden % 32 || c.inter % 32) return fail("model_create: hidden and inter must be multiples of 32");
@@ -431,8 +483,8 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
     hipStream_t s = stream();
     const int H = m->c.hidden;
     int* pb = &m->st->next_pos;
-    for (int p0 = 0; p0 < n; p0 += MAXB) {
-        const int cnt = std::min(MAXB, n - p0);
+    for (int p0 = 0; p0 < n; p0 += PREFILL_CHUNK) {
+        const int cnt = std::min(PREFILL_CHUNK, n - p0);
         CMF_HIP(hipMemcpyAsync(m->toks, ids + p0, cnt * sizeof(int), hipMemcpyHostToDevice, s));
         hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, p0);
         launch_embed(m->toks, embed_src(m), H, m->hv, H, cnt, s);
@@ -461,10 +513,7 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
 // logits of the tip hidden -> next token (greedy argmax or device sampler)
 static void pick_from_tip(cmf_model m, bool sampling, const cmf_sampler_config* sc, hipStream_t s) {
     const int H = m->c.hidden;
-    (void)hipMemcpyAsync(m->hm, m->h_tip, H * sizeof(float), hipMemcpyDeviceToDevice, s);
-    launch_add_rmsnorm_prep(m->hm, H, nullptr, H, m->final_norm, H, m->c.eps, prep_for(m, m->lm), nullptr, 0,
-                            1, s);
-    launch_gemv(m->lm, m->planes, m->xs, m->logits, m->c.vocab, 1, 0, m->c.vocab, s);
+    gemv_f(m, m->lm, src_norm(m->h_tip, H, m->final_norm, m->c.eps), m->logits, m->c.vocab, 1, false, s);
     if (sampling) sample_rows(m->sb, m->logits, m->c.vocab, 1, *sc, m->st, SampleMode::Plain, 0, nullptr, s);
     else launch_argmax(m->logits, m->c.vocab, m->c.vocab, 1, m->am_v, m->am_i, m->st->argmax, s);
 }
@@ -479,8 +528,9 @@ static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_conf
     int* pb = &m->st->next_pos;
     for (int j = 0; j < k; j++) {
         const int* tok = j == 0 ? &m->st->t_next : &m->st->drafts[j - 1];
-        const float* hin = j == 0 ? m->h_tip : m->hm;
-        mtp_step(m, tok, hin, pb, j - 1, np + j, s);
+        float* bufs[2] = {m->hm, m->hm2};
+        const float* hin = j == 0 ? m->h_tip : bufs[(j - 1) & 1];
+        mtp_step(m, tok, hin, bufs[j & 1], pb, j - 1, np + j, s);
         if (sampling) sample_rows(m->sb, m->logits, V, 1, sc, m->st, SampleMode::Draft, j, nullptr, s);
         else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, &m->st->drafts[j], s);
     }

@@ -7,6 +7,54 @@
 
 namespace cmf {
 
+// The tied q8 embedding table in its device layout.
+struct EmbedSrc {
+    const int8_t* w;
+    const float* rs;
+    int rows;
+    int nkc;
+};
+
+// Producer of a GEMV's activation operand, evaluated by every workgroup into
+// LDS (or, for XS_GLOBAL, prepared planes read from global memory):
+//   XS_NORM : x = rms_norm(x_row) * w                  (inference.rs:33-50)
+//   XS_SILU : x = silu(g) * u, g/u at [0, K) / [K, 2K)  (inference.rs:14-16)
+//   XS_ROWS : x = x_row
+//   XS_CAT  : x = [rms_norm(embed(tok), w) ; rms_norm(x_row, w2)]  (H each,
+//             the MTP input, pipeline.rs:3085-3094)
+enum { XS_GLOBAL = 0, XS_NORM = 2, XS_SILU = 3, XS_ROWS = 4, XS_CAT = 5 };
+struct XSrc {
+    int mode;
+    const float* x;
+    int ldx;
+    const float* w;
+    const float* w2;
+    const int* toks;
+    EmbedSrc emb;
+    int K;   // logical length of the operand (0: the weight's cols)
+    int H;   // XS_CAT: length of each half
+    double eps;
+    const uint8_t* planes;  // XS_GLOBAL
+    const float* xs;
+};
+
+struct GemvArgs {
+    const void* w;
+    const void* scale;
+    const float2* rowp;
+    float* y;
+    int ldy, m, nk, rb0, nrb, row_lo, row_hi, resid, lds;
+    XSrc src;
+};
+
+// y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m.
+int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
+         bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0);
+// Whether an m-row operand for w fits the LDS staging.
+bool fits_lds(const DevWeight& w, int m);
+// Evaluate an XSrc into f32 rows (for operands too large for LDS).
+int launch_xsrc_rows(const XSrc& s, int m, float* out, int ldo, hipStream_t st);
+
 size_t prep_bytes(const DevWeight& w);
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
                 hipStream_t st);

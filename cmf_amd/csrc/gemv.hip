@@ -1,21 +1,28 @@
 // Dequant GEMV / skinny GEMM kernels for gfx950 (MI355X).
 //
 // y[b][r] = sum_k W[r][k] * x[b][k] for b < M <= 16 and the three weight
-// codecs of the engine (q8 per-row, q4_tiled, q4tp).  One workgroup owns one
-// block of 16 weight rows; its KS waves split the K range and reduce in LDS
-// in a fixed order (deterministic).  Every wave streams 1 KiB of packed
-// weights per step with one 128-bit load per lane and feeds them to the
-// matrix cores with the activations as the MFMA A operand (16 batch rows,
-// zero-padded) and the weights as the B operand (16 weight rows):
-//
-//   q8   : v_mfma_i32_16x16x64_i8 on the raw int8 weights; x is carried as
-//          three int8 planes, x ~= sx*(q0 + q1/128 + q2/16384) (|error| <=
-//          2^-22 max|x|), each accumulated exactly in int32 over all of K.
-//   q4*  : v_mfma_f32_16x16x32_f16, one tile (32 columns = one scale) per
-//          MFMA; nibbles become exact f16 (n - 8) in registers and x is
-//          carried as f16 hi + lo of x*2^e (22-bit significand).  Each
-//          tile's f32 product is scaled by its tile scale and accumulated in
-//          f32, as q4t_row_exact does (qtensor.rs:4418-4432).
+// codecs of the engine (q8 per-row, q4_tiled, q4tp).  Work split:
+//   - a workgroup of KS waves owns one block of 16 weight rows at a time and
+//     walks row blocks with a grid stride (persistent); its waves split K
+//     and reduce in LDS in a fixed order (deterministic);
+//   - every wave streams 1 KiB of packed weights per step with one 128-bit
+//     load per lane, a whole K share in flight before the first MFMA;
+//   - the activations are the MFMA A operand (16 batch rows, zero-padded),
+//     the weights the B operand (16 weight rows):
+//       q8  : v_mfma_i32_16x16x64_i8 on the raw int8 weights; x is carried
+//             as three int8 planes, x ~= sx*(q0 + q1/128 + q2/16384)
+//             (|error| <= 2^-22 max|x|), each summed exactly in int32;
+//       q4* : v_mfma_f32_16x16x32_f16, one tile (32 columns, one scale) per
+//             MFMA; nibbles become exact f16 (n - 8) in registers and x is
+//             carried as f16 hi + lo of x*2^e (22-bit significand).  Each
+//             tile's product is scaled by its tile scale and accumulated in
+//             f32, as q4t_row_exact does (qtensor.rs:4418-4432).
+//   - the activation operand is built once per workgroup into LDS from its
+//     producer (RMSNorm of the residual rows, SwiGLU of the gate/up rows,
+//     plain rows, the MTP [enorm(embed); hnorm(h)] concat, or a prepared
+//     buffer), so the producer needs no kernel of its own; when it does not
+//     fit in LDS the prepared planes are read from global memory (L2).
+//   - optional residual epilogue: y is added into the output (h += W x).
 #include "common.h"
 #include "gemv.h"
 
@@ -25,6 +32,9 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef int int4v __attribute__((ext_vector_type(4)));
+
+constexpr int PF = 8;            // weight steps in flight per wave
+constexpr int LDSX_MAX = 128 * 1024;  // largest LDS-staged activation operand (+ scratch)
 
 // Four nibble bytes (8 weights: elements 8s..8s+7 of a tile) to exact f16
 // (n - 8) in the in-slot order {0,2,4,6,1,3,5,7}.
@@ -49,141 +59,428 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-template <int FMT, int NV, int KS>
-__global__ __launch_bounds__(64 * KS) void k_gemv_q4(
-    const uint4* __restrict__ W, const void* __restrict__ S, const float2* __restrict__ RP,
-    const uint4* __restrict__ XH, const uint4* __restrict__ XL, const float* __restrict__ XS,
-    float* __restrict__ Y, int ldy, int ntg, int M, int row_lo, int row_hi) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rb = blockIdx.x;
-    const int r = lane & 15, s = lane >> 4;
-    __shared__ float lad[FMT == DT_Q4TP ? 16 * 33 : 1];
-    __shared__ float4v part[KS][64];
-    if constexpr (FMT == DT_Q4TP) {
-        if (threadIdx.x < 16) {
-            const float2 p = RP[rb * 16 + threadIdx.x];
-            float t = p.x;
-            lad[threadIdx.x * 33] = t;
-            for (int c = 1; c < 32; c++) {
-                t = t * p.y;
-                lad[threadIdx.x * 33 + c] = t;
-            }
+// ---------------------------------------------------------------------------
+// Activation staging (once per workgroup)
+// ---------------------------------------------------------------------------
+__device__ inline double wg_sum_d(double v, double* red) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int i = 0; i < nw; i++) t += red[i];
+    return t;
+}
+
+__device__ inline float wg_max_f(float v, float* red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (l == 0) red[w] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int i = 1; i < nw; i++) t = fmaxf(t, red[i]);
+    return t;
+}
+
+__device__ __forceinline__ float embed_val(const EmbedSrc& e, int tok, int k) {
+    if (tok < 0 || tok >= e.rows) return 0.f;
+    const int rb = tok >> 4, r = tok & 15, kc = k >> 6, s = (k >> 4) & 3, j = k & 15;
+    return (float)e.w[(((size_t)rb * e.nkc + kc) * 64 + 16 * s + r) * 16 + j] * e.rs[tok];
+}
+
+// logical input element k of batch row b (inv1/inv2: the row's RMSNorm factors)
+__device__ __forceinline__ float xin(const XSrc& s, int b, int k, int tok, float inv1, float inv2) {
+    if (k >= s.K) return 0.f;
+    switch (s.mode) {
+        case XS_NORM: return s.x[(size_t)b * s.ldx + k] * inv1 * s.w[k];
+        case XS_SILU: {
+            const float g = s.x[(size_t)b * s.ldx + k], u = s.x[(size_t)b * s.ldx + s.K + k];
+            return (g / (1.0f + expf(-g))) * u;
         }
-        __syncthreads();
-    }
-    const bool xload = r < M;
-    const int tg0 = (ntg * wave) / KS, tg1 = (ntg * (wave + 1)) / KS;
-    const size_t wbase = (size_t)rb * ntg;
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-    const float4v zero = {0.f, 0.f, 0.f, 0.f};
-    for (int tg = tg0; tg < tg1; ++tg) {
-        const uint4 w = W[(wbase + tg) * 64 + lane];
-        float sc[4];
-        if constexpr (FMT == DT_Q4T) {
-            const uint2 sv = ((const uint2*)S)[(wbase + tg) * 16 + r];
-            sc[0] = f16_bits_to_f32(sv.x & 0xFFFFu);
-            sc[1] = f16_bits_to_f32(sv.x >> 16);
-            sc[2] = f16_bits_to_f32(sv.y & 0xFFFFu);
-            sc[3] = f16_bits_to_f32(sv.y >> 16);
-        } else {
-            const uint32_t cw = ((const uint32_t*)S)[(wbase + tg) * 16 + r];
-            sc[0] = lad[r * 33 + (cw & 31)];
-            sc[1] = lad[r * 33 + ((cw >> 5) & 31)];
-            sc[2] = lad[r * 33 + ((cw >> 10) & 31)];
-            sc[3] = lad[r * 33 + ((cw >> 15) & 31)];
-        }
-        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int tile = tg * 4 + t;
-            half8 xh = {}, xl = {};
-            if (xload) {
-                xh = __builtin_bit_cast(half8, XH[(size_t)tile * 64 + lane]);
-                xl = __builtin_bit_cast(half8, XL[(size_t)tile * 64 + lane]);
-            }
-            const half8 b = dq_nib_word(wv[t]);
-            float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, b, zero, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, b, d, 0, 0, 0);
-#pragma unroll
-            for (int v = 0; v < NV; v++) acc[v] += d[v] * sc[t];
-        }
-    }
-    if constexpr (KS > 1) {
-        part[wave][lane] = acc;
-        __syncthreads();
-        if (wave != 0) return;
-        for (int q = 1; q < KS; q++) {
-            const float4v o = part[q][lane];
-#pragma unroll
-            for (int v = 0; v < NV; v++) acc[v] += o[v];
-        }
-    }
-    const int row = rb * 16 + r;
-    if (row < row_lo || row >= row_hi) return;
-#pragma unroll
-    for (int v = 0; v < NV; v++) {
-        const int b = 4 * s + v;
-        if (b < M) Y[(size_t)b * ldy + (row - row_lo)] = acc[v] * XS[b];
-    }
-    if constexpr (NV == 4) {
-        (void)0;
+        case XS_CAT:
+            return k < s.H ? embed_val(s.emb, tok, k) * inv1 * s.w[k]
+                           : s.x[(size_t)b * s.ldx + (k - s.H)] * inv2 * s.w2[k - s.H];
+        default: return s.x[(size_t)b * s.ldx + k];
     }
 }
 
-template <int KS>
-__global__ __launch_bounds__(64 * KS) void k_gemv_q8(
-    const int4v* __restrict__ W, const float* __restrict__ RS, const int4v* __restrict__ X0,
-    const int4v* __restrict__ X1, const int4v* __restrict__ X2, const float* __restrict__ XS,
-    float* __restrict__ Y, int ldy, int nkc, int M, int row_lo, int row_hi) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rb = blockIdx.x;
-    const int r = lane & 15, s = lane >> 4;
-    __shared__ int4v part[KS > 1 ? KS : 1][3][64];
-    const bool xload = r < M;
-    const int k0 = (nkc * wave) / KS, k1 = (nkc * (wave + 1)) / KS;
-    const size_t wbase = (size_t)rb * nkc;
-    int4v a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0};
-    for (int kc = k0; kc < k1; ++kc) {
-        const int4v w = W[(wbase + kc) * 64 + lane];
-        int4v x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0}, x2 = {0, 0, 0, 0};
-        if (xload) {
-            x0 = X0[(size_t)kc * 64 + lane];
-            x1 = X1[(size_t)kc * 64 + lane];
-            x2 = X2[(size_t)kc * 64 + lane];
+// raw input element k of batch row b (before the RMSNorm factor / weight)
+__device__ __forceinline__ float xraw(const XSrc& s, int b, int k, int tok) {
+    switch (s.mode) {
+        case XS_SILU: {
+            const float g = s.x[(size_t)b * s.ldx + k], u = s.x[(size_t)b * s.ldx + s.K + k];
+            return (g / (1.0f + expf(-g))) * u;
         }
-        a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, w, a0, 0, 0, 0);
-        a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, w, a1, 0, 0, 0);
-        a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x2, w, a2, 0, 0, 0);
+        case XS_CAT: return k < s.H ? embed_val(s.emb, tok, k) : s.x[(size_t)b * s.ldx + (k - s.H)];
+        default: return s.x[(size_t)b * s.ldx + k];
     }
-    if constexpr (KS > 1) {
-        part[wave][0][lane] = a0;
-        part[wave][1][lane] = a1;
-        part[wave][2][lane] = a2;
-        __syncthreads();
-        if (wave != 0) return;
-        for (int q = 1; q < KS; q++) {
-            a0 += part[q][0][lane];
-            a1 += part[q][1][lane];
-            a2 += part[q][2][lane];
-        }
-    }
-    const int row = rb * 16 + r;
-    if (row < row_lo || row >= row_hi) return;
-    const float rs = RS[row];
+}
+
+__device__ __forceinline__ float xfin(const XSrc& s, int k, float raw, float inv1, float inv2) {
+    if (s.mode == XS_NORM) return raw * inv1 * s.w[k];
+    if (s.mode == XS_CAT) return k < s.H ? raw * inv1 * s.w[k] : raw * inv2 * s.w2[k - s.H];
+    return raw;
+}
+
+// Builds the operand of batch row b in LDS with one wave (wave-level
+// reductions; the raw row goes through an f32 LDS scratch `xf` [K]):
+//   q4: hi plane then lo plane, [tile*4 + s][b] x 16 B; lxs[b] = 2^-e
+//   q8: planes q0,q1,q2, [chunk*4 + s][b] x 16 B;      lxs[b] = sx
+__device__ __forceinline__ void stage_row(const XSrc& s, int b, int M, int fmt, int nk, uint8_t* lx,
+                                          float* lxs, float* xf) {
+    const int lane = threadIdx.x & 63;
+    const int K = s.K;
+    const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;  // nk: q8 chunks / q4 tiles
+    const int tok = s.mode == XS_CAT ? s.toks[b] : 0;
+    const bool nrm = s.mode == XS_NORM || s.mode == XS_CAT;
+    double s1 = 0.0, s2 = 0.0;
+    // pass 1: raw values (8 loads in flight per lane), sums of squares
+    for (int kb = 0; kb < kpad; kb += 512) {
+        float t[8];
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const int b = 4 * s + v;
-        if (b < M) {
-            const float t = (float)a0[v] + (float)a1[v] * 0.0078125f + (float)a2[v] * 6.103515625e-05f;
-            Y[(size_t)b * ldy + (row - row_lo)] = (t * XS[b]) * rs;
+        for (int u = 0; u < 8; u++) {
+            const int k = kb + 64 * u + lane;
+            t[u] = k < K ? xraw(s, b, k, tok) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int k = kb + 64 * u + lane;
+            if (k < kpad) xf[k] = t[u];
+            if (nrm) {
+                const double d = (double)t[u] * (double)t[u];
+                if (s.mode == XS_CAT && k >= s.H) s2 += d;
+                else s1 += d;
+            }
+        }
+    }
+    float inv1 = 1.f, inv2 = 1.f;
+    if (nrm) {
+        for (int o = 32; o > 0; o >>= 1) {
+            s1 += __shfl_xor(s1, o);
+            s2 += __shfl_xor(s2, o);
+        }
+        const int n1 = s.mode == XS_CAT ? s.H : K;
+        inv1 = 1.0f / (float)sqrt(s1 / (double)n1 + s.eps);
+        if (s.mode == XS_CAT) inv2 = 1.0f / (float)sqrt(s2 / (double)s.H + s.eps);
+    }
+    // pass 2: final values in place, max |x|
+    float am = 0.f;
+    if (s.mode == XS_NORM || s.mode == XS_CAT) {
+        for (int kb = 0; kb < K; kb += 512) {
+            float wv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int k = kb + 64 * u + lane;
+                wv[u] = k < K ? (s.mode == XS_CAT ? (k < s.H ? s.w[k] : s.w2[k - s.H]) : s.w[k]) : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int k = kb + 64 * u + lane;
+                if (k < K) {
+                    const float iv = (s.mode == XS_CAT && k >= s.H) ? inv2 : inv1;
+                    const float x = xf[k] * iv * wv[u];
+                    xf[k] = x;
+                    am = fmaxf(am, fabsf(x));
+                }
+            }
+        }
+    } else {
+        for (int k = lane; k < K; k += 64) am = fmaxf(am, fabsf(xf[k]));
+    }
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    __builtin_amdgcn_wave_barrier();
+    // pass 3: operand planes, one 16-byte item per lane step
+    const size_t pl = (size_t)nk * 4 * M * 16;
+    if (fmt == DT_Q8ROW) {
+        const float sx = am > 0.f ? am / 127.0f : 1.0f, inv = 1.0f / sx;
+        if (lane == 0) lxs[b] = sx;
+        for (int item = lane; item < nk * 4; item += 64) {
+            uint32_t w0[4], w1[4], w2[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                uint32_t a = 0, bb = 0, cc = 0;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float x = xf[item * 16 + 4 * c + j] * inv;
+                    const float q0 = fminf(127.f, fmaxf(-127.f, rintf(x)));
+                    const float r1 = (x - q0) * 128.0f;
+                    const float q1 = fminf(127.f, fmaxf(-127.f, rintf(r1)));
+                    const float q2 = fminf(127.f, fmaxf(-127.f, rintf((r1 - q1) * 128.0f)));
+                    a |= (uint32_t)(uint8_t)(int8_t)q0 << (8 * j);
+                    bb |= (uint32_t)(uint8_t)(int8_t)q1 << (8 * j);
+                    cc |= (uint32_t)(uint8_t)(int8_t)q2 << (8 * j);
+                }
+                w0[c] = a;
+                w1[c] = bb;
+                w2[c] = cc;
+            }
+            const size_t off = ((size_t)item * M + b) * 16;
+            *(uint4*)(lx + off) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+            *(uint4*)(lx + pl + off) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+            *(uint4*)(lx + 2 * pl + off) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+        }
+    } else {
+        int ex = 0;
+        if (am > 0.f) frexpf(am, &ex);
+        const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        if (lane == 0) lxs[b] = am > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+        for (int item = lane; item < nk * 4; item += 64) {
+            const float* xv = xf + item * 8;
+            uint32_t hv[4], lv[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                // in-slot order {0,2,4,6,1,3,5,7}
+                const int ja = j < 2 ? 4 * j : 4 * (j - 2) + 1, jb = ja + 2;
+                const float x0 = xv[ja] * sc, x1 = xv[jb] * sc;
+                const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
+                const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
+                hv[j] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
+                lv[j] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
+            }
+            const size_t off = ((size_t)item * M + b) * 16;
+            *(uint4*)(lx + off) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+            *(uint4*)(lx + pl + off) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+        }
+    }
+}
+
+// Operand staging of a whole workgroup: waves take batch rows round-robin;
+// XS_GLOBAL planes are copied into the LDS layout when they fit.
+__device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, uint8_t* lx, float* lxs) {
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (s.mode == XS_GLOBAL) {
+        // global [item/4][16*s + b] x 16 B  ->  LDS [item][b] x 16 B
+        const int npl = fmt == DT_Q8ROW ? 3 : 2;
+        const size_t gpl = (size_t)nk * 64, lpl = (size_t)nk * 4 * M;
+        const uint4* g = (const uint4*)s.planes;
+        uint4* l = (uint4*)lx;
+        const int n = nk * 4 * M;
+        for (int i = threadIdx.x; i < n * npl; i += blockDim.x) {
+            const int p = i / n, e = i % n, item = e / M, b = e % M;
+            l[p * lpl + e] = g[p * gpl + (size_t)(item >> 2) * 64 + 16 * (item & 3) + b];
+        }
+        if (threadIdx.x < 16) lxs[threadIdx.x] = s.xs[threadIdx.x];
+    } else {
+        const size_t pbytes = (size_t)nk * 4 * M * 16 * (fmt == DT_Q8ROW ? 3 : 2);
+        float* xf = (float*)(lx + pbytes);
+        const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;
+        for (int b = wave; b < M; b += nw) stage_row(s, b, M, fmt, nk, lx, lxs, xf + (size_t)(b % nw) * kpad);
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// q4t / q4tp
+// ---------------------------------------------------------------------------
+template <int FMT, int NV, int KS>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, s = lane >> 4;
+    const int M = a.m, ntg = a.nk;  // nk = groups of 4 tiles
+    __shared__ float lad[FMT == DT_Q4TP ? 16 * 33 : 1];
+    __shared__ float4v part[KS][64];
+    __shared__ float lxs[16];
+    const bool in_lds = a.lds != 0;
+    if (in_lds) stage_x(a.src, M, FMT, ntg * 4, smem, lxs);
+    else if (threadIdx.x < 16) lxs[threadIdx.x] = a.src.xs[threadIdx.x];
+    __syncthreads();
+    const uint4* XH = (const uint4*)a.src.planes;
+    const uint4* XL = XH + (size_t)ntg * 4 * 64;
+    const uint4* LH = (const uint4*)smem;
+    const uint4* LL = LH + (size_t)ntg * 4 * 4 * M;
+    const bool xload = r < M;
+    const int tg0 = (ntg * wave) / KS, tg1 = (ntg * (wave + 1)) / KS;
+    const float4v zero = {0.f, 0.f, 0.f, 0.f};
+    for (int rb = blockIdx.x; rb < a.nrb; rb += gridDim.x) {
+        const size_t wbase = (size_t)(a.rb0 + rb) * ntg;
+        if constexpr (FMT == DT_Q4TP) {
+            __syncthreads();
+            if (threadIdx.x < 16) {
+                const float2 p = a.rowp[(a.rb0 + rb) * 16 + threadIdx.x];
+                float tv = p.x;
+                lad[threadIdx.x * 33] = tv;
+                for (int c = 1; c < 32; c++) {
+                    tv = tv * p.y;
+                    lad[threadIdx.x * 33 + c] = tv;
+                }
+            }
+            __syncthreads();
+        }
+        float4v acc = {0.f, 0.f, 0.f, 0.f};
+        for (int it0 = tg0; it0 < tg1; it0 += PF) {
+            uint4 wv[PF];
+            uint32_t sv[PF][2];
+#pragma unroll
+            for (int u = 0; u < PF; u++) {
+                if (it0 + u < tg1) {
+                    wv[u] = ((const uint4*)a.w)[(wbase + it0 + u) * 64 + lane];
+                    if constexpr (FMT == DT_Q4T) {
+                        const uint2 v = ((const uint2*)a.scale)[(wbase + it0 + u) * 16 + r];
+                        sv[u][0] = v.x;
+                        sv[u][1] = v.y;
+                    } else {
+                        sv[u][0] = ((const uint32_t*)a.scale)[(wbase + it0 + u) * 16 + r];
+                        sv[u][1] = 0;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < PF; u++) {
+                if (it0 + u >= tg1) break;
+                const int tg = it0 + u;
+                float sc[4];
+                if constexpr (FMT == DT_Q4T) {
+                    sc[0] = f16_bits_to_f32(sv[u][0] & 0xFFFFu);
+                    sc[1] = f16_bits_to_f32(sv[u][0] >> 16);
+                    sc[2] = f16_bits_to_f32(sv[u][1] & 0xFFFFu);
+                    sc[3] = f16_bits_to_f32(sv[u][1] >> 16);
+                } else {
+                    const uint32_t cw = sv[u][0];
+                    sc[0] = lad[r * 33 + (cw & 31)];
+                    sc[1] = lad[r * 33 + ((cw >> 5) & 31)];
+                    sc[2] = lad[r * 33 + ((cw >> 10) & 31)];
+                    sc[3] = lad[r * 33 + ((cw >> 15) & 31)];
+                }
+                const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const int tile = tg * 4 + t;
+                    half8 xh = {}, xl = {};
+                    if (xload) {
+                        if (in_lds) {
+                            xh = __builtin_bit_cast(half8, LH[(size_t)(tile * 4 + s) * M + r]);
+                            xl = __builtin_bit_cast(half8, LL[(size_t)(tile * 4 + s) * M + r]);
+                        } else {
+                            xh = __builtin_bit_cast(half8, XH[(size_t)tile * 64 + lane]);
+                            xl = __builtin_bit_cast(half8, XL[(size_t)tile * 64 + lane]);
+                        }
+                    }
+                    const half8 bq = dq_nib_word(ww[t]);
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq, zero, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq, d, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < NV; v++) acc[v] += d[v] * sc[t];
+                }
+            }
+        }
+        if constexpr (KS > 1) {
+            part[wave][lane] = acc;
+            __syncthreads();
+            if (wave == 0) {
+                for (int q = 1; q < KS; q++) {
+                    const float4v o = part[q][lane];
+#pragma unroll
+                    for (int v = 0; v < NV; v++) acc[v] += o[v];
+                }
+            }
+            __syncthreads();
+        }
+        if (wave == 0) {
+            const int row = (a.rb0 + rb) * 16 + r;
+            if (row >= a.row_lo && row < a.row_hi) {
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const int b = 4 * s + v;
+                    if (b < M) {
+                        float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
+                        const float val = acc[v] * lxs[b];
+                        *yp = a.resid ? *yp + val : val;
+                    }
+                }
+            }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// Activation preparation from f32 x[M][ldx] (standalone GEMV calls).  One
-// workgroup per batch row; the fused producers of the model path write the
-// same layouts through the device helpers in prep.h.
+// q8
+// ---------------------------------------------------------------------------
+template <int KS>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, s = lane >> 4;
+    const int M = a.m, nkc = a.nk;
+    __shared__ int4v part[KS > 1 ? KS : 1][3][64];
+    __shared__ float lxs[16];
+    const bool in_lds = a.lds != 0;
+    if (in_lds) stage_x(a.src, M, DT_Q8ROW, nkc, smem, lxs);
+    else if (threadIdx.x < 16) lxs[threadIdx.x] = a.src.xs[threadIdx.x];
+    __syncthreads();
+    const int4v* X0 = (const int4v*)a.src.planes;
+    const size_t gpl = (size_t)nkc * 64, lpl = (size_t)nkc * 4 * M;
+    const int4v* L0 = (const int4v*)smem;
+    const bool xload = r < M;
+    const int k0 = (nkc * wave) / KS, k1 = (nkc * (wave + 1)) / KS;
+    for (int rb = blockIdx.x; rb < a.nrb; rb += gridDim.x) {
+        const size_t wbase = (size_t)(a.rb0 + rb) * nkc;
+        int4v a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0};
+        for (int it0 = k0; it0 < k1; it0 += PF) {
+            int4v wv[PF];
+#pragma unroll
+            for (int u = 0; u < PF; u++)
+                if (it0 + u < k1) wv[u] = ((const int4v*)a.w)[(wbase + it0 + u) * 64 + lane];
+#pragma unroll
+            for (int u = 0; u < PF; u++) {
+                if (it0 + u >= k1) break;
+                const int kc = it0 + u;
+                int4v x0 = {0, 0, 0, 0}, x1 = {0, 0, 0, 0}, x2 = {0, 0, 0, 0};
+                if (xload) {
+                    if (in_lds) {
+                        const size_t o = (size_t)(kc * 4 + s) * M + r;
+                        x0 = L0[o];
+                        x1 = L0[lpl + o];
+                        x2 = L0[2 * lpl + o];
+                    } else {
+                        x0 = X0[(size_t)kc * 64 + lane];
+                        x1 = X0[gpl + (size_t)kc * 64 + lane];
+                        x2 = X0[2 * gpl + (size_t)kc * 64 + lane];
+                    }
+                }
+                a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, wv[u], a0, 0, 0, 0);
+                a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, wv[u], a1, 0, 0, 0);
+                a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x2, wv[u], a2, 0, 0, 0);
+            }
+        }
+        if constexpr (KS > 1) {
+            part[wave][0][lane] = a0;
+            part[wave][1][lane] = a1;
+            part[wave][2][lane] = a2;
+            __syncthreads();
+            if (wave == 0) {
+                for (int q = 1; q < KS; q++) {
+                    a0 += part[q][0][lane];
+                    a1 += part[q][1][lane];
+                    a2 += part[q][2][lane];
+                }
+            }
+            __syncthreads();
+        }
+        if (wave == 0) {
+            const int row = (a.rb0 + rb) * 16 + r;
+            if (row >= a.row_lo && row < a.row_hi) {
+                const float rs = ((const float*)a.scale)[row];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int b = 4 * s + v;
+                    if (b < M) {
+                        const float tt = (float)a0[v] + (float)a1[v] * 0.0078125f + (float)a2[v] * 6.103515625e-05f;
+                        float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
+                        const float val = (tt * lxs[b]) * rs;
+                        *yp = a.resid ? *yp + val : val;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Activation preparation into global planes (standalone GEMV calls and the
+// operands too large for LDS).  One workgroup per batch row.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ X, int ldx, int K, int kind,
                                               int nk, uint8_t* __restrict__ planes,
@@ -204,15 +501,39 @@ __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ X, int l
     else prep16_row(x, K, amax, nk, b, planes, xs, threadIdx.x, 256);
 }
 
+// Producer-only kernel for operands too large for LDS: evaluates the XSrc
+// into f32 rows (one workgroup per batch row), then k_prep prepares them.
+__global__ __launch_bounds__(256) void k_xsrc_rows(XSrc s, float* __restrict__ out, int ldo) {
+    const int b = blockIdx.x, t = threadIdx.x;
+    __shared__ double redd[4];
+    float inv1 = 1.f, inv2 = 1.f;
+    int tok = 0;
+    if (s.mode == XS_CAT) tok = s.toks[b];
+    if (s.mode == XS_NORM || s.mode == XS_CAT) {
+        const int n1 = s.mode == XS_CAT ? s.H : s.K;
+        double a = 0.0;
+        for (int k = t; k < n1; k += 256) {
+            const float v = s.mode == XS_CAT ? embed_val(s.emb, tok, k) : s.x[(size_t)b * s.ldx + k];
+            a += (double)v * (double)v;
+        }
+        a = wg_sum_d(a, redd);
+        inv1 = 1.0f / (float)sqrt(a / (double)n1 + s.eps);
+        if (s.mode == XS_CAT) {
+            double c = 0.0;
+            for (int k = t; k < s.H; k += 256) {
+                const float v = s.x[(size_t)b * s.ldx + k];
+                c += (double)v * (double)v;
+            }
+            c = wg_sum_d(c, redd);
+            inv2 = 1.0f / (float)sqrt(c / (double)s.H + s.eps);
+        }
+    }
+    for (int k = t; k < s.K; k += 256) out[(size_t)b * ldo + k] = xin(s, b, k, tok, inv1, inv2);
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------
-static int pick_ks(int nrb, int nk) {
-    int ks = 1;
-    while (ks < 8 && nrb * ks < 3072 && nk / (ks * 2) >= 2) ks *= 2;
-    return ks;
-}
-
 size_t prep_bytes(const DevWeight& w) {
     // q8: 3 planes of nk*1 KiB ; q4: 2 planes of ntiles*1 KiB
     return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 1024 * 3 : (size_t)w.kchunks * 4 * 1024 * 2;
@@ -226,19 +547,38 @@ int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* pla
     return CMF_OK;
 }
 
+static size_t lds_bytes(const DevWeight& w, int m) {
+    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 128 * 4 * m;
+}
+// plus the f32 row scratch of the in-kernel producers (one row per wave)
+static size_t lds_scratch(const DevWeight& w, int rows) {
+    return (size_t)(w.dtype == DT_Q8ROW ? w.kchunks * 64 : w.kchunks * 128) * 4 * rows;
+}
+
+template <int FMT, int NV, int KS>
+static void set_lds_q4() {
+    static bool done = false;
+    if (!done) {
+        (void)hipFuncSetAttribute((const void*)k_gemv_q4<FMT, NV, KS>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, LDSX_MAX);
+        done = true;
+    }
+}
+template <int KS>
+static void set_lds_q8() {
+    static bool done = false;
+    if (!done) {
+        (void)hipFuncSetAttribute((const void*)k_gemv_q8<KS>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  LDSX_MAX);
+        done = true;
+    }
+}
+
 template <int FMT, int NV>
-static void launch_q4_nv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y,
-                         int ldy, int m, int rb0, int nrb, int row_lo, int row_hi, int ks,
-                         hipStream_t st) {
-    const uint4* W = (const uint4*)w.w + (size_t)rb0 * w.kchunks * 64;
-    const uint8_t* S = (const uint8_t*)w.scale + (size_t)rb0 * w.kchunks * (FMT == DT_Q4T ? 128 : 64);
-    const float2* RP = w.rowp ? w.rowp + (size_t)rb0 * 16 : nullptr;
-    const uint4* XH = (const uint4*)planes;
-    const uint4* XL = (const uint4*)(planes + (size_t)w.kchunks * 4 * 1024);
-    const int lo = row_lo - rb0 * 16, hi = row_hi - rb0 * 16;
-#define CMF_Q4(KS)                                                                       \
-    hipLaunchKernelGGL((k_gemv_q4<FMT, NV, KS>), dim3(nrb), dim3(64 * KS), 0, st, W, S, RP, \
-                       XH, XL, xs, y, ldy, w.kchunks, m, lo, hi)
+static void launch_q4_nv(const GemvArgs& a, int ks, int grid, size_t lds, hipStream_t st) {
+#define CMF_Q4(KS)                                                                             \
+    set_lds_q4<FMT, NV, KS>();                                                                 \
+    hipLaunchKernelGGL((k_gemv_q4<FMT, NV, KS>), dim3(grid), dim3(64 * KS), lds, st, a)
     switch (ks) {
         case 1: CMF_Q4(1); break;
         case 2: CMF_Q4(2); break;
@@ -248,22 +588,51 @@ static void launch_q4_nv(const DevWeight& w, const uint8_t* planes, const float*
 #undef CMF_Q4
 }
 
-int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
-                int m, int row_lo, int row_hi, hipStream_t st, int ks_override) {
+// K split (waves per workgroup) and persistent grid for nrb row blocks of nk
+// K steps: enough waves to fill 256 CUs, at least two steps per wave, and
+// few enough workgroups that the per-workgroup staging stays cheap.
+static void pick_shape(int nrb, int nk, int* ks, int* grid) {
+    int k = 1;
+    while (k < 8 && (long)nrb * k < 4096 && nk / (k * 2) >= 2) k *= 2;
+    *ks = k;
+    const int maxg = std::max(256, 2048 / k);
+    *grid = std::min(nrb, maxg);
+}
+
+int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
+         bool resid, hipStream_t st, int ks_override, int grid_override) {
     if (m < 1 || m > MAXB) return fail("gemv: batch must be 1..16");
     if (row_lo < 0 || row_hi > w.rows || row_lo >= row_hi) return fail("gemv: bad row range");
-    const int rb0 = row_lo / 16, rb1 = (row_hi + 15) / 16, nrb = rb1 - rb0;
-    const int ks = ks_override > 0 ? ks_override : pick_ks(nrb, w.kchunks);
+    GemvArgs a;
+    a.w = w.w;
+    a.scale = w.scale;
+    a.rowp = w.rowp;
+    a.y = y;
+    a.ldy = ldy;
+    a.m = m;
+    a.nk = w.kchunks;
+    a.rb0 = row_lo / 16;
+    a.nrb = (row_hi + 15) / 16 - a.rb0;
+    a.row_lo = row_lo;
+    a.row_hi = row_hi;
+    a.resid = resid ? 1 : 0;
+    a.src = src;
+    if (a.src.K == 0) a.src.K = w.cols;
+    int ks, grid;
+    pick_shape(a.nrb, w.kchunks, &ks, &grid);
+    if (ks_override > 0) ks = ks_override;
+    size_t lds = lds_bytes(w, m);
+    if (src.mode != XS_GLOBAL) lds += lds_scratch(w, std::min(m, ks));
+    if (lds > LDSX_MAX) {
+        if (src.mode != XS_GLOBAL) return fail("gemv: activation operand exceeds LDS; prepare it globally");
+        lds = 0;  // planes read from global memory per step
+    }
+    a.lds = lds ? 1 : 0;
+    if (grid_override > 0) grid = std::min(grid_override, a.nrb);
     if (w.dtype == DT_Q8ROW) {
-        const int4v* W = (const int4v*)w.w + (size_t)rb0 * w.kchunks * 64;
-        const float* RS = (const float*)w.scale + (size_t)rb0 * 16;
-        const int4v* X0 = (const int4v*)planes;
-        const int4v* X1 = X0 + (size_t)w.kchunks * 64;
-        const int4v* X2 = X1 + (size_t)w.kchunks * 64;
-        const int lo = row_lo - rb0 * 16, hi = row_hi - rb0 * 16;
-#define CMF_Q8(KS)                                                                                 \
-    hipLaunchKernelGGL((k_gemv_q8<KS>), dim3(nrb), dim3(64 * KS), 0, st, W, RS, X0, X1, X2, xs, y, \
-                       ldy, w.kchunks, m, lo, hi)
+#define CMF_Q8(KS) \
+    set_lds_q8<KS>(); \
+    hipLaunchKernelGGL((k_gemv_q8<KS>), dim3(grid), dim3(64 * KS), lds, st, a)
         switch (ks) {
             case 1: CMF_Q8(1); break;
             case 2: CMF_Q8(2); break;
@@ -274,12 +643,12 @@ int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, floa
         return CMF_OK;
     }
     const int nv = m >= 4 ? 4 : m;
-#define CMF_Q4F(FMT)                                                                                 \
-    switch (nv) {                                                                                    \
-        case 1: launch_q4_nv<FMT, 1>(w, planes, xs, y, ldy, m, rb0, nrb, row_lo, row_hi, ks, st); break; \
-        case 2: launch_q4_nv<FMT, 2>(w, planes, xs, y, ldy, m, rb0, nrb, row_lo, row_hi, ks, st); break; \
-        case 3: launch_q4_nv<FMT, 3>(w, planes, xs, y, ldy, m, rb0, nrb, row_lo, row_hi, ks, st); break; \
-        default: launch_q4_nv<FMT, 4>(w, planes, xs, y, ldy, m, rb0, nrb, row_lo, row_hi, ks, st); break; \
+#define CMF_Q4F(FMT)                                                        \
+    switch (nv) {                                                           \
+        case 1: launch_q4_nv<FMT, 1>(a, ks, grid, lds, st); break;          \
+        case 2: launch_q4_nv<FMT, 2>(a, ks, grid, lds, st); break;          \
+        case 3: launch_q4_nv<FMT, 3>(a, ks, grid, lds, st); break;          \
+        default: launch_q4_nv<FMT, 4>(a, ks, grid, lds, st); break;         \
     }
     if (w.dtype == DT_Q4T) {
         CMF_Q4F(DT_Q4T)
@@ -288,6 +657,22 @@ int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, floa
     }
 #undef CMF_Q4F
     return CMF_OK;
+}
+
+bool fits_lds(const DevWeight& w, int m) { return lds_bytes(w, m) + lds_scratch(w, std::min(m, 16)) <= LDSX_MAX; }
+
+int launch_xsrc_rows(const XSrc& s, int m, float* out, int ldo, hipStream_t st) {
+    hipLaunchKernelGGL(k_xsrc_rows, dim3(m), dim3(256), 0, st, s, out, ldo);
+    return CMF_OK;
+}
+
+int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
+                int m, int row_lo, int row_hi, hipStream_t st, int ks_override) {
+    XSrc s{};
+    s.mode = XS_GLOBAL;
+    s.planes = planes;
+    s.xs = xs;
+    return gemv(w, s, y, ldy, m, row_lo, row_hi, false, st, ks_override, 0);
 }
 
 }  // namespace cmf

@@ -2,10 +2,11 @@
 #pragma once
 
 #include "common.h"
+#include "gemv.h"
 
 namespace cmf {
 
-constexpr int ATT_C = 32;  // key positions per attention block
+constexpr int ATT_C = 64;  // key positions per attention wave
 
 // Where a producer writes its prepared activations (see gemv.h).
 struct PrepDst {
@@ -15,13 +16,6 @@ struct PrepDst {
     float* xs;
 };
 
-// The tied q8 embedding table in its device layout.
-struct EmbedSrc {
-    const int8_t* w;
-    const float* rs;
-    int rows;
-    int nkc;
-};
 
 void launch_add_rmsnorm_prep(float* h, int ldh, const float* delta, int ldd, const float* w, int H,
                              double eps, const PrepDst& d, float* out, int ldo, int nb,
@@ -37,7 +31,7 @@ void launch_qk_rope_append(const float* qkv, int ldq, const float* qn, const flo
                            hipStream_t st);
 void launch_attention(const float* q, int ldq, const float* kc, const float* vc, int max_seq, int nb,
                       int nh, int nkv, const int* pbase, int padd, int max_len, float* pm, float* pl,
-                      float* po, int nch_cap, const PrepDst& d, float* out_f32, hipStream_t st);
+                      float* po, int nch_cap, float* out_f32, hipStream_t st);
 void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,
                           hipStream_t st);
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,

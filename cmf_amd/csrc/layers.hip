@@ -189,123 +189,192 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(
     }
 }
 
-// Split-K decode attention.  grid (nkv, nchunks), block 256.  Query rows
-// b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.  Each block
-// handles ATT_C positions of one KV head for all nb * hpk queries and
-// writes (max, sum, unnormalised output) partials.
-__global__ __launch_bounds__(256) void k_attn_partial(
-    const float* __restrict__ q, int ldq, const float* __restrict__ kc,
-    const float* __restrict__ vc, int max_seq, int nb, int nh, int nkv, const int* __restrict__ pbase,
-    int padd, float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po, int nch) {
-    constexpr int C = ATT_C, HD = 128;
-    const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+// Split-K decode attention.  grid (nkv, nchunks), one wave per block.  Query
+// rows b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.  A wave
+// takes ATT_C = 64 key positions of one KV head for all nq = nb * hpk
+// queries, G queries at a time: lanes are positions for the scores (each
+// lane streams its own K row), the chunk softmax reduces across the wave,
+// and for the value pass lanes are head dims (coalesced V rows) with the
+// chunk weights broadcast by readlane.  Partials: running max, sum of exp,
+// unnormalised output.
+template <int G>
+__global__ __launch_bounds__(64) void k_attn_partial(
+    const float* __restrict__ q, int ldq, const float* __restrict__ kc, const float* __restrict__ vc,
+    int max_seq, int nb, int nh, int nkv, const int* __restrict__ pbase, int padd,
+    float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po, int nch) {
+    constexpr int HD = 128;
+    const int g = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
     const int hpk = nh / nkv, nq = nb * hpk;
     const int pos0 = *pbase + padd;
-    const int stored = pos0 + nb;  // rows present after this step's append
-    const int p0 = c * C;
-    __shared__ float Kt[HD][C + 1];
-    __shared__ float V[C][HD];
+    const int stored = pos0 + nb;
+    const int p0 = c * ATT_C;
     __shared__ float Q[32][HD];
-    __shared__ float S[32][C];
     if (p0 >= stored) {
-        for (int i = t; i < nq; i += 256) {
-            const int bi = i / hpk, hh = i % hpk, h = g * hpk + hh;
+        if (lane < nq) {
+            const int bi = lane / hpk, h = g * hpk + lane % hpk;
             const size_t row = (size_t)bi * nh + h;
             pm[row * nch + c] = -INFINITY;
             pl[row * nch + c] = 0.f;
         }
         return;
     }
-    for (int i = t; i < nq * HD; i += 256) {
-        const int qi = i / HD, d = i % HD;
-        const int bi = qi / hpk, hh = qi % hpk;
-        Q[qi][d] = q[(size_t)bi * ldq + (size_t)(g * hpk + hh) * HD + d];
-    }
-    const float* Kg = kc + (size_t)g * max_seq * HD;
-    const float* Vg = vc + (size_t)g * max_seq * HD;
-    for (int i = t; i < C * HD; i += 256) {
-        const int p = i / HD, d = i % HD;
-        const bool in = p0 + p < stored;
-        Kt[d][p] = in ? Kg[(size_t)(p0 + p) * HD + d] : 0.f;
-        V[p][d] = in ? Vg[(size_t)(p0 + p) * HD + d] : 0.f;
+    const int ng = (nq + G - 1) / G;
+    {
+        // the nq query rows of this KV head: for batch row bi the hpk heads
+        // g*hpk.. are contiguous (hpk * HD floats); hpk is a power of two
+        const int lg = 31 - __clz(hpk * (HD / 4));  // log2 of float4s per batch row
+        const float4* qs = (const float4*)q;
+        float4 qv[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int e = lane + 64 * u, bi = e >> lg, rem = e & ((1 << lg) - 1);
+            qv[u] = e < nq * (HD / 4) ? qs[((size_t)bi * ldq + (size_t)g * hpk * HD) / 4 + rem]
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int e = lane + 64 * u;
+            if (e < ng * G * (HD / 4)) ((float4*)Q)[e] = qv[u];
+        }
     }
     __syncthreads();
+    const int p = p0 + lane;
+    const bool valid = p < stored;
+    const float4* K = (const float4*)(kc + ((size_t)g * max_seq + (valid ? p : 0)) * HD);
+    const int np = min(ATT_C, stored - p0);
+    const float2* V = (const float2*)(vc + ((size_t)g * max_seq + p0) * HD) + lane;
     const float scale = 1.0f / sqrtf((float)HD);
-    {
-        const int p = t % C;
-        for (int qi = t / C; qi < nq; qi += 256 / C) {
-            const int bi = qi / hpk;
-            float acc = 0.f;
-#pragma unroll 8
-            for (int d = 0; d < HD; d++) acc += Q[qi][d] * Kt[d][p];
-            S[qi][p] = (p0 + p <= pos0 + bi) ? acc * scale : -INFINITY;
+    for (int grp = 0; grp < ng; grp++) {
+        const int q0 = grp * G;
+        float acc[G];
+#pragma unroll
+        for (int i = 0; i < G; i++) acc[i] = 0.f;
+#pragma unroll 1
+        for (int half = 0; half < 2; half++) {
+            float4 kv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) kv[j] = K[half * 16 + j];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                // opaque offset: keeps the G query reads of step j at step j
+                // (hoisting all of them would need 16*G*4 registers)
+                int d = (half * 16 + j) * 4;
+                CMF_OPAQUE(d);
+#pragma unroll
+                for (int i = 0; i < G; i++) {
+                    const float4 qq = *(const float4*)&Q[q0 + i][d];
+                    acc[i] += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+                }
+            }
         }
-    }
-    __syncthreads();
-    for (int qi = t; qi < nq; qi += 256) {
-        float m = -INFINITY;
-        for (int p = 0; p < C; p++) m = fmaxf(m, S[qi][p]);
-        float l = 0.f;
-        for (int p = 0; p < C; p++) {
-            const float e = m == -INFINITY ? 0.f : expf(S[qi][p] - m);
-            S[qi][p] = e;
-            l += e;
+        float w[G];
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+            const int qi = q0 + i, bi = qi / hpk;
+            const bool see = valid && p <= pos0 + bi && qi < nq;
+            const float sv = see ? acc[i] * scale : -INFINITY;
+            float m = sv;
+            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+            const float e = m == -INFINITY ? 0.f : expf(sv - m);
+            float l = e;
+            for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
+            w[i] = e;
+            if (lane == 0 && qi < nq) {
+                const size_t row = (size_t)bi * nh + g * hpk + qi % hpk;
+                pm[row * nch + c] = m;
+                pl[row * nch + c] = l;
+            }
         }
-        const int bi = qi / hpk, hh = qi % hpk, h = g * hpk + hh;
-        const size_t row = (size_t)bi * nh + h;
-        pm[row * nch + c] = m;
-        pl[row * nch + c] = l;
-    }
-    __syncthreads();
-    {
-        const int d = t % HD;
-        for (int qi = t / HD; qi < nq; qi += 256 / HD) {
-            float acc = 0.f;
-#pragma unroll 8
-            for (int p = 0; p < C; p++) acc += S[qi][p] * V[p][d];
-            const int bi = qi / hpk, hh = qi % hpk, h = g * hpk + hh;
-            const size_t row = (size_t)bi * nh + h;
-            po[(row * nch + c) * HD + d] = acc;
+        // value pass: lane owns dims 2*lane, 2*lane+1; 16 V rows in flight
+        float2 o[G];
+#pragma unroll
+        for (int i = 0; i < G; i++) o[i] = make_float2(0.f, 0.f);
+#pragma unroll 1
+        for (int pb = 0; pb < np; pb += 16) {
+            float2 vv[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                vv[j] = pb + j < np ? V[(size_t)(pb + j) * (HD / 2)] : make_float2(0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+#pragma unroll
+                for (int i = 0; i < G; i++) {
+                    const float ww = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), pb + j));
+                    o[i].x += ww * vv[j].x;
+                    o[i].y += ww * vv[j].y;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+            const int qi = q0 + i;
+            if (qi < nq) {
+                const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
+                ((float2*)(po + (row * nch + c) * HD))[lane] = o[i];
+            }
         }
     }
 }
 
-// Merge the partials of one query row (all heads) and prepare the result
-// for the O projection.  grid (nb), block 256.
-__global__ __launch_bounds__(256) void k_attn_merge_prep(const float* __restrict__ pm,
-                                                         const float* __restrict__ pl,
-                                                         const float* __restrict__ po, int nh,
-                                                         int nch, const int* __restrict__ pbase,
-                                                         int padd, PrepDst dst,
-                                                         float* __restrict__ out_f32) {
+// Merge the chunk partials of one (row, head): one wave, lanes = chunks for
+// the weights, lanes = dims for the output.  grid (nb * nh).
+__global__ __launch_bounds__(64) void k_attn_merge(const float* __restrict__ pm,
+                                                   const float* __restrict__ pl,
+                                                   const float* __restrict__ po, int nh, int nch,
+                                                   const int* __restrict__ pbase, int padd,
+                                                   float* __restrict__ out) {
     constexpr int HD = 128;
-    const int b = blockIdx.x;
-    __shared__ float vals[32 * HD];
-    __shared__ float redf[4];
+    const int rh = blockIdx.x, lane = threadIdx.x;
+    const int b = rh / nh;
+    const size_t row = (size_t)rh;  // == b * nh + h
     const int pos0 = *pbase + padd;
-    const int used = (pos0 + b + ATT_C) / ATT_C;  // chunks holding keys 0..pos0+b
-    float am = 0.f;
-    for (int i = threadIdx.x; i < nh * HD; i += blockDim.x) {
-        const int h = i / HD, d = i % HD;
-        const size_t row = (size_t)b * nh + h;
-        float M = -INFINITY;
-        for (int c = 0; c < used; c++) M = fmaxf(M, pm[row * nch + c]);
-        float L = 0.f, O = 0.f;
-        for (int c = 0; c < used; c++) {
-            const float m = pm[row * nch + c];
-            if (m == -INFINITY) continue;
-            const float f = expf(m - M);
-            L += pl[row * nch + c] * f;
-            O += po[(row * nch + c) * HD + d] * f;
+    const int used = (pos0 + b + ATT_C) / ATT_C;
+    float M = -INFINITY;
+    for (int c = lane; c < used; c += 64) M = fmaxf(M, pm[row * nch + c]);
+    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float L = 0.f;
+    float2 O = make_float2(0.f, 0.f);
+    for (int c0 = 0; c0 < used; c0 += 64) {
+        const int c = c0 + lane;
+        const float m = c < used ? pm[row * nch + c] : -INFINITY;
+        const float wgt = m == -INFINITY ? 0.f : expf(m - M);
+        float lw = c < used ? pl[row * nch + c] * wgt : 0.f;
+        for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o);
+        L += lw;
+        const int n = min(64, used - c0);
+        for (int jb = 0; jb < n; jb += 8) {
+            float2 vv[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                vv[j] = jb + j < n ? ((const float2*)(po + (row * nch + c0 + jb + j) * HD))[lane]
+                                   : make_float2(0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), jb + j));
+                O.x += wj * vv[j].x;
+                O.y += wj * vv[j].y;
+            }
         }
-        const float o = L > 0.f ? O / L : 0.f;
-        vals[i] = o;
-        if (out_f32) out_f32[(size_t)b * nh * HD + i] = o;
-        am = fmaxf(am, fabsf(o));
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    ((float2*)(out + (size_t)b * nh * HD + (size_t)(rh % nh) * HD))[lane] = make_float2(O.x * inv, O.y * inv);
+}
+
+// Preparation of f32 rows for the next GEMV (one workgroup per row).
+__global__ __launch_bounds__(256) void k_rows_prep(const float* __restrict__ x, int ldx, int K,
+                                                   PrepDst dst) {
+    const int b = blockIdx.x;
+    __shared__ float vals[8192];
+    __shared__ float redf[4];
+    float am = 0.f;
+    for (int i = threadIdx.x; i < K; i += blockDim.x) {
+        const float v = x[(size_t)b * ldx + i];
+        vals[i] = v;
+        am = fmaxf(am, fabsf(v));
     }
     am = block_max_f(am, redf);
     __syncthreads();
-    prep_any(vals, nh * HD, am, dst, b);
+    prep_any(vals, K, am, dst, b);
 }
 
 // SwiGLU on the fused gate/up output gu[b] = [g (I) ; u (I)], prepared for
@@ -337,10 +406,18 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x
     const int lo = s * slice, hi = min(n, lo + slice);
     float bv = -INFINITY;
     int bi = lo;
-    for (int i = lo + threadIdx.x; i < hi; i += blockDim.x) {
-        const float v = row[i];
-        if (v > bv || (v == bv && i > bi)) {
-            bv = v;
+    constexpr int PER = 16;  // slice / 256, loads in flight together
+    float vals[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = lo + threadIdx.x + j * 256;
+        vals[j] = i < hi ? row[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int i = lo + threadIdx.x + j * 256;
+        if (i < hi && (vals[j] > bv || (vals[j] == bv && i > bi))) {
+            bv = vals[j];
             bi = i;
         }
     }
@@ -416,12 +493,18 @@ void launch_qk_rope_append(const float* qkv, int ldq, const float* qn, const flo
 
 void launch_attention(const float* q, int ldq, const float* kc, const float* vc, int max_seq, int nb,
                       int nh, int nkv, const int* pbase, int padd, int max_len, float* pm, float* pl,
-                      float* po, int nch_cap, const PrepDst& d, float* out_f32, hipStream_t st) {
+                      float* po, int nch_cap, float* out_f32, hipStream_t st) {
     const int nch = (max_len + ATT_C - 1) / ATT_C;
-    hipLaunchKernelGGL(k_attn_partial, dim3(nkv, nch), dim3(256), 0, st, q, ldq, kc, vc, max_seq, nb,
-                       nh, nkv, pbase, padd, pm, pl, po, nch_cap);
-    hipLaunchKernelGGL(k_attn_merge_prep, dim3(nb), dim3(256), 0, st, pm, pl, po, nh, nch_cap, pbase,
-                       padd, d, out_f32);
+    const int nq = nb * (nh / nkv);
+#define CMF_ATT(G)                                                                                  \
+    hipLaunchKernelGGL((k_attn_partial<G>), dim3(nkv, nch), dim3(64), 0, st, q, ldq, kc, vc, max_seq, \
+                       nb, nh, nkv, pbase, padd, pm, pl, po, nch_cap)
+    if (nq <= 2) CMF_ATT(2);
+    else if (nq <= 4) CMF_ATT(4);
+    else CMF_ATT(8);
+#undef CMF_ATT
+    hipLaunchKernelGGL(k_attn_merge, dim3(nb * nh), dim3(64), 0, st, pm, pl, po, nh, nch_cap, pbase, padd,
+                       out_f32);
 }
 
 void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,

@@ -151,10 +151,22 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
     const int lo = sl * SLICE, n = min(SLICE, V - lo);
     const float* src = logits + (size_t)row * V + lo;
     float mx = -INFINITY;
-    for (int i = t; i < n; i += 256) {
-        vals[i] = src[i];
-        ids[i] = lo + i;
-        mx = fmaxf(mx, vals[i]);
+    {
+        float tmp[SLICE / 256];  // all loads in flight together
+#pragma unroll
+        for (int u = 0; u < SLICE / 256; u++) {
+            const int i = t + 256 * u;
+            tmp[u] = i < n ? src[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < SLICE / 256; u++) {
+            const int i = t + 256 * u;
+            if (i < n) {
+                vals[i] = tmp[u];
+                ids[i] = lo + i;
+                mx = fmaxf(mx, tmp[u]);
+            }
+        }
     }
     red[t] = mx;
     __syncthreads();
@@ -201,16 +213,26 @@ __global__ __launch_bounds__(256) void k_topk_merge(int V, SampCfg c, int nslice
     __shared__ int cnt[4];
     __shared__ float ov[SPARSE_K_MAX];
     __shared__ int oi[SPARSE_K_MAX];
-    int n = 0;
     const int k = min(c.k, V);
-    for (int s = 0; s < nslices; s++) {
-        const size_t base = ((size_t)row * nslices + s) * SPARSE_K_MAX;
-        for (int i = t; i < k; i += 256) {
-            const int id = cid[base + i];
-            vals[n + i] = id >= 0 ? cv[base + i] : -INFINITY;
-            ids[n + i] = id >= 0 ? id : 0x7FFFFFFF;
+    const int n = nslices * k;  // <= SLICE (checked by the host)
+    {
+        int ti_[SLICE / 256];
+        float tv_[SLICE / 256];
+#pragma unroll
+        for (int u = 0; u < SLICE / 256; u++) {
+            const int e = t + 256 * u, sl = e / k, i = e - sl * k;
+            const size_t at = ((size_t)row * nslices + sl) * SPARSE_K_MAX + i;
+            ti_[u] = e < n ? cid[at] : -1;
+            tv_[u] = e < n ? cv[at] : -INFINITY;
         }
-        n += k;
+#pragma unroll
+        for (int u = 0; u < SLICE / 256; u++) {
+            const int e = t + 256 * u;
+            if (e < n) {
+                vals[e] = ti_[u] >= 0 ? tv_[u] : -INFINITY;
+                ids[e] = ti_[u] >= 0 ? ti_[u] : 0x7FFFFFFF;
+            }
+        }
     }
     __syncthreads();
     select_topk(vals, ids, n, k, ov, oi, hist, tv, ti, cnt);
@@ -308,10 +330,11 @@ __global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restri
                                 const float* __restrict__ sum, int* __restrict__ qid,
                                 float* __restrict__ qp, int* __restrict__ qn, DState* st,
                                 int* __restrict__ out) {
+    // the O(k) chain runs in one thread; its working lists live in LDS
+    __shared__ int pid[SPARSE_K_MAX], rsid[SPARSE_K_MAX];
+    __shared__ float pp[SPARSE_K_MAX], rsp[SPARSE_K_MAX];
     if (threadIdx.x != 0) return;
     unsigned long long rng = st->rng;
-    int pid[SPARSE_K_MAX], rsid[SPARSE_K_MAX];
-    float pp[SPARSE_K_MAX], rsp[SPARSE_K_MAX];
     if (mode == 0 || mode == 1) {  // Draft / Plain: distribution of row 0, one draw
         int n = sparse_dist(rid, rv, lmax[0], sum[0], c, pid, pp);
         if (n == 0) {
