@@ -66,10 +66,4 @@ struct XPrep {
 
 constexpr int MAXB = 16;  // largest batch a GEMV launch serves
 
-// Makes a wave-uniform value opaque to the optimizer, so loads indexed by it
-// stay where the code places them instead of being hoisted together.
-#ifndef CMF_OPAQUE
-#define CMF_OPAQUE(x) asm volatile("" : "+s"(x))
-#endif
-
 }  // namespace cmf

@@ -5,7 +5,10 @@
 // acceptance and the commit never leave HBM; the host reads back one small
 // state record per round.
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <algorithm>
 
 #include <string>
 #include <vector>
@@ -58,6 +61,11 @@ struct cmf_model_s {
     std::vector<void*> allocs;
     int next_pos_host = 0;
     bool prefilled = false;
+    hipGraphExec_t round_graph = nullptr;
+    int graph_k = 0;
+    int graph_len = 0;  // attention length bound the captured round was built for
+    int graph_sampling = -1;
+    bool use_graph = true;
     bool decoding = false;
     int rounds = 0;
     int emitted_host = 0;
@@ -322,8 +330,15 @@ int ensure_logits(cmf_model_s* m) {
     return sample_alloc(m->sb, V, [&](void** p, size_t b) { return dalloc(m, p, b); });
 }
 
+// Forget the captured decode round (its nodes hold the buffer addresses).
+void drop_graph(cmf_model_s* m) {
+    if (m->round_graph) (void)hipGraphExecDestroy(m->round_graph);
+    m->round_graph = nullptr;
+}
+
 int ensure_out(cmf_model_s* m, int cap) {
     if (m->out_cap >= cap) return CMF_OK;
+    drop_graph(m);
     if (dalloc_t(m, &m->out, cap)) return CMF_ERR;
     m->out_cap = cap;
     return CMF_OK;
@@ -414,6 +429,8 @@ int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
     if (c.hidden % 32 || c.inter % 32) return fail("model_create: hidden and inter must be multiples of 32");
     auto* m = new cmf_model_s();
     m->c = c;
+    const char* g = getenv("CMF_DECODE_GRAPH");  // "0": launch every round eagerly
+    m->use_graph = !(g && g[0] == '0');
     m->L.resize(c.n_layers);
     if (alloc_scratch(m) != CMF_OK) {
         cmf_model_free(m);
@@ -426,6 +443,7 @@ int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
 int cmf_model_free(cmf_model m) {
     if (!m) return CMF_OK;
     (void)hipStreamSynchronize(stream());
+    if (m->round_graph) (void)hipGraphExecDestroy(m->round_graph);
     for (auto& l : m->L) free_layer(l);
     free_layer(m->mtp);
     free_weight(m->lm);
@@ -436,6 +454,7 @@ int cmf_model_free(cmf_model m) {
 }
 
 int cmf_model_set_layer(cmf_model m, int li, const cmf_layer_desc* d) {
+    if (m) drop_graph(m);
     if (!m || !d || li < 0 || li >= m->c.n_layers) return fail("set_layer: bad arguments");
     if (m->c.n_heads / m->c.n_kv * MAXB > 32 && m->c.n_heads / m->c.n_kv > 2)
         return fail("set_layer: the attention kernel serves <= 32 queries per KV head");
@@ -443,6 +462,7 @@ int cmf_model_set_layer(cmf_model m, int li, const cmf_layer_desc* d) {
 }
 
 int cmf_model_set_head(cmf_model m, const cmf_tensor* lm, const float* final_norm) {
+    if (m) drop_graph(m);
     if (!m || !lm) return fail("set_head: null argument");
     if (lm->dtype != DT_Q8ROW) return fail("set_head: the tied lm_head/embedding must be q8");
     if (check_tensor(*lm, m->c.vocab, m->c.hidden, "lm_head")) return CMF_ERR;
@@ -456,6 +476,7 @@ int cmf_model_set_head(cmf_model m, const cmf_tensor* lm, const float* final_nor
 
 int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh,
                       const cmf_layer_desc* layer, const float* norm) {
+    if (m) drop_graph(m);
     if (!m || !eh || !layer) return fail("set_mtp: null argument");
     const int H = m->c.hidden;
     if (check_tensor(*eh, H, 2 * H, "eh_proj")) return CMF_ERR;
@@ -523,20 +544,20 @@ static void pick_from_tip(cmf_model m, bool sampling, const cmf_sampler_config* 
 // MTP re-warm of the verified pairs and the commit.  np = next_pos (host
 // mirror, sizes the attention grids).
 static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_config& sc, int np,
-                       hipStream_t s) {
+                       hipStream_t s, int graph_len = 0) {
     const int H = m->c.hidden, V = m->c.vocab;
     int* pb = &m->st->next_pos;
     for (int j = 0; j < k; j++) {
         const int* tok = j == 0 ? &m->st->t_next : &m->st->drafts[j - 1];
         float* bufs[2] = {m->hm, m->hm2};
         const float* hin = j == 0 ? m->h_tip : bufs[(j - 1) & 1];
-        mtp_step(m, tok, hin, bufs[j & 1], pb, j - 1, np + j, s);
+        mtp_step(m, tok, hin, bufs[j & 1], pb, j - 1, graph_len ? graph_len : np + j, s);
         if (sampling) sample_rows(m->sb, m->logits, V, 1, sc, m->st, SampleMode::Draft, j, nullptr, s);
         else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, &m->st->drafts[j], s);
     }
     hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
     launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, k + 1, s);
-    trunk_forward(m, k + 1, pb, 0, np + k + 1, true, s);
+    trunk_forward(m, k + 1, pb, 0, graph_len ? graph_len : np + k + 1, true, s);
     if (sampling) {
         sample_rows(m->sb, m->logits, V, k + 1, sc, m->st, SampleMode::Accept, k, m->out, s);
     } else {
@@ -611,7 +632,35 @@ int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats)
     CMF_HIP(hipEventRecord(e0, s));
     DState hs{};
     int np = m->next_pos_host;
-    for (int r = 0; r < n; r++) {
+    int r0 = 0;
+    if (spec && m->use_graph && n > 1) {
+        // The captured round reads every position-dependent value from the
+        // device state; only the attention grid is sized on the host, by a
+        // bound on the positions these n rounds can reach (512-position steps).
+        const int need = std::min(m->c.max_seq, ((np + (n + 1) * (k + 1) + 511) / 512) * 512);
+        if (!m->round_graph || m->graph_k != k || m->graph_sampling != (int)sampling || m->graph_len < need) {
+            // one eager round first: it sets the kernels' launch attributes
+            spec_round(m, k, sampling, m->sc, np, s);
+            r0 = 1;
+            if (m->round_graph) {
+                (void)hipGraphExecDestroy(m->round_graph);
+                m->round_graph = nullptr;
+            }
+            hipGraph_t g;
+            CMF_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            spec_round(m, k, sampling, m->sc, np, s, need);
+            CMF_HIP(hipStreamEndCapture(s, &g));
+            const hipError_t ie = hipGraphInstantiate(&m->round_graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            CMF_HIP(ie);
+            m->graph_k = k;
+            m->graph_sampling = (int)sampling;
+            m->graph_len = need;
+        }
+        for (int r = r0; r < n; r++) CMF_HIP(hipGraphLaunch(m->round_graph, s));
+        r0 = n;
+    }
+    for (int r = r0; r < n; r++) {
         if (spec) {
             spec_round(m, k, sampling, m->sc, np, s);
             CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));

@@ -52,8 +52,6 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
          bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0);
 // Whether an m-row operand for w fits the LDS staging.
 bool fits_lds(const DevWeight& w, int m);
-// Evaluate an XSrc into f32 rows (for operands too large for LDS).
-int launch_xsrc_rows(const XSrc& s, int m, float* out, int ldo, hipStream_t st);
 
 size_t prep_bytes(const DevWeight& w);
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,

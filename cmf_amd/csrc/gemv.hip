@@ -62,148 +62,191 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // ---------------------------------------------------------------------------
 // Activation staging (once per workgroup)
 // ---------------------------------------------------------------------------
-__device__ inline double wg_sum_d(double v, double* red) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (l == 0) red[w] = v;
-    __syncthreads();
-    double t = 0.0;
-    for (int i = 0; i < nw; i++) t += red[i];
-    return t;
+constexpr int SEGJ = 8;            // float4 per lane per staging unit
+constexpr int SEG4 = 64 * SEGJ;    // float4 per staging unit (2048 elements)
+constexpr int SEGMAX = 8;          // staging units per row (operands up to 16384 elements)
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
+__device__ __forceinline__ float amax4(float m, float4v v) {
+    return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
+__device__ __forceinline__ double sq4(float4v v) {
+    return (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
+           (double)v.w * (double)v.w;
 }
 
-__device__ inline float wg_max_f(float v, float* red) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (l == 0) red[w] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int i = 1; i < nw; i++) t = fmaxf(t, red[i]);
-    return t;
-}
-
-__device__ __forceinline__ float embed_val(const EmbedSrc& e, int tok, int k) {
-    if (tok < 0 || tok >= e.rows) return 0.f;
-    const int rb = tok >> 4, r = tok & 15, kc = k >> 6, s = (k >> 4) & 3, j = k & 15;
-    return (float)e.w[(((size_t)rb * e.nkc + kc) * 64 + 16 * s + r) * 16 + j] * e.rs[tok];
-}
-
-// logical input element k of batch row b (inv1/inv2: the row's RMSNorm factors)
-__device__ __forceinline__ float xin(const XSrc& s, int b, int k, int tok, float inv1, float inv2) {
-    if (k >= s.K) return 0.f;
-    switch (s.mode) {
-        case XS_NORM: return s.x[(size_t)b * s.ldx + k] * inv1 * s.w[k];
-        case XS_SILU: {
-            const float g = s.x[(size_t)b * s.ldx + k], u = s.x[(size_t)b * s.ldx + s.K + k];
-            return (g / (1.0f + expf(-g))) * u;
-        }
-        case XS_CAT:
-            return k < s.H ? embed_val(s.emb, tok, k) * inv1 * s.w[k]
-                           : s.x[(size_t)b * s.ldx + (k - s.H)] * inv2 * s.w2[k - s.H];
-        default: return s.x[(size_t)b * s.ldx + k];
-    }
-}
-
-// raw input element k of batch row b (before the RMSNorm factor / weight)
-__device__ __forceinline__ float xraw(const XSrc& s, int b, int k, int tok) {
-    switch (s.mode) {
-        case XS_SILU: {
-            const float g = s.x[(size_t)b * s.ldx + k], u = s.x[(size_t)b * s.ldx + s.K + k];
-            return (g / (1.0f + expf(-g))) * u;
-        }
-        case XS_CAT: return k < s.H ? embed_val(s.emb, tok, k) : s.x[(size_t)b * s.ldx + (k - s.H)];
-        default: return s.x[(size_t)b * s.ldx + k];
-    }
-}
-
-__device__ __forceinline__ float xfin(const XSrc& s, int k, float raw, float inv1, float inv2) {
-    if (s.mode == XS_NORM) return raw * inv1 * s.w[k];
-    if (s.mode == XS_CAT) return k < s.H ? raw * inv1 * s.w[k] : raw * inv2 * s.w2[k - s.H];
-    return raw;
-}
-
-// Builds the operand of batch row b in LDS with one wave (wave-level
-// reductions; the raw row goes through an f32 LDS scratch `xf` [K]):
-//   q4: hi plane then lo plane, [tile*4 + s][b] x 16 B; lxs[b] = 2^-e
-//   q8: planes q0,q1,q2, [chunk*4 + s][b] x 16 B;      lxs[b] = sx
-__device__ __forceinline__ void stage_row(const XSrc& s, int b, int M, int fmt, int nk, uint8_t* lx,
-                                          float* lxs, float* xf) {
+// Phase 1 of one staging unit u (row b = u / S): lane element groups
+// k4 = base + 64*j + lane (4 elements each) are all requested at once (row 0
+// also requests the norm weights), the raw values stored to the scratch rows,
+// and the unit's sums of squares (norm producers) or max|x| reduced to LDS.
+template <int MODE>
+__device__ __forceinline__ void unit_phase1(const XSrc& s, int u, int S, int K4, int kp4, int H4, float4v* xf4,
+                                            float4v* wl4, double* red1, double* red2, float* mred) {
     const int lane = threadIdx.x & 63;
-    const int K = s.K;
-    const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;  // nk: q8 chunks / q4 tiles
-    const int tok = s.mode == XS_CAT ? s.toks[b] : 0;
-    const bool nrm = s.mode == XS_NORM || s.mode == XS_CAT;
-    double s1 = 0.0, s2 = 0.0;
-    // pass 1: raw values (8 loads in flight per lane), sums of squares
-    for (int kb = 0; kb < kpad; kb += 512) {
-        float t[8];
+    const int b = u / S, base = (u % S) * SEG4;
+    constexpr bool nrm = MODE == XS_NORM || MODE == XS_CAT;
+    const bool ldw = nrm && b == 0;
+    float4v v[SEGJ], wv[SEGJ];
+    const float4v z4 = float4v{0.f, 0.f, 0.f, 0.f};
+    const float* row = s.x + (size_t)b * s.ldx;
+    if constexpr (MODE == XS_SILU) {
+        float4v g[SEGJ], u[SEGJ];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int k = kb + 64 * u + lane;
-            t[u] = k < K ? xraw(s, b, k, tok) : 0.f;
+        for (int j = 0; j < SEGJ; j++) {
+            const int k4 = base + 64 * j + lane;
+            g[j] = k4 < K4 ? ((const float4v*)row)[k4] : z4;
+            u[j] = k4 < K4 ? ((const float4v*)(row + s.K))[k4] : z4;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int k = kb + 64 * u + lane;
-            if (k < kpad) xf[k] = t[u];
-            if (nrm) {
-                const double d = (double)t[u] * (double)t[u];
-                if (s.mode == XS_CAT && k >= s.H) s2 += d;
-                else s1 += d;
-            }
+        for (int j = 0; j < SEGJ; j++)
+            v[j] = float4v{silu_mul(g[j].x, u[j].x), silu_mul(g[j].y, u[j].y), silu_mul(g[j].z, u[j].z),
+                               silu_mul(g[j].w, u[j].w)};
+    } else if constexpr (MODE == XS_CAT) {
+        const int tok = s.toks[b];
+        const EmbedSrc& e = s.emb;
+        const bool tv = tok >= 0 && tok < e.rows;
+        const int rb = tok >> 4, r = tok & 15;
+        const float rs = tv ? e.rs[tok] : 0.f;
+#pragma unroll
+        for (int j = 0; j < SEGJ; j++) {
+            const int k4 = base + 64 * j + lane;
+            // four consecutive int8 of the token's row in the q8 device layout
+            const int k = 4 * k4, kc = k >> 6, sl = (k >> 4) & 3, jj = k & 15;
+            uint32_t q = 0u;
+            float4v xr = z4;
+            if (k4 < K4 && k4 < H4 && tv)
+                q = *(const uint32_t*)(e.w + (((size_t)rb * e.nkc + kc) * 64 + 16 * sl + r) * 16 + jj);
+            if (k4 < K4 && k4 >= H4) xr = ((const float4v*)row)[k4 - H4];
+            v[j] = k4 < H4 ? float4v{(float)(int8_t)(q & 0xFF), (float)(int8_t)((q >> 8) & 0xFF),
+                                         (float)(int8_t)((q >> 16) & 0xFF), (float)(int8_t)(q >> 24)}
+                           : xr;
+            wv[j] = ldw && k4 < K4 ? (k4 < H4 ? ((const float4v*)s.w)[k4] : ((const float4v*)s.w2)[k4 - H4]) : z4;
+        }
+#pragma unroll
+        for (int j = 0; j < SEGJ; j++) {
+            const int k4 = base + 64 * j + lane;
+            if (k4 < H4) v[j] = float4v{v[j].x * rs, v[j].y * rs, v[j].z * rs, v[j].w * rs};
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < SEGJ; j++) {
+            const int k4 = base + 64 * j + lane;
+            v[j] = k4 < K4 ? ((const float4v*)row)[k4] : z4;
+            if constexpr (MODE == XS_NORM) wv[j] = ldw && k4 < K4 ? ((const float4v*)s.w)[k4] : z4;
         }
     }
-    float inv1 = 1.f, inv2 = 1.f;
-    if (nrm) {
+    double s1 = 0.0, s2 = 0.0;
+    float am = 0.f;
+#pragma unroll
+    for (int j = 0; j < SEGJ; j++) {
+        const int k4 = base + 64 * j + lane;
+        if (k4 < kp4) {
+            xf4[(size_t)b * kp4 + k4] = v[j];
+            if (ldw) wl4[k4] = wv[j];
+        }
+        if constexpr (nrm) {
+            if (k4 < H4) s1 += sq4(v[j]);
+            else s2 += sq4(v[j]);
+        } else {
+            am = amax4(am, v[j]);
+        }
+    }
+    if constexpr (nrm) {
         for (int o = 32; o > 0; o >>= 1) {
             s1 += __shfl_xor(s1, o);
             s2 += __shfl_xor(s2, o);
         }
-        const int n1 = s.mode == XS_CAT ? s.H : K;
-        inv1 = 1.0f / (float)sqrt(s1 / (double)n1 + s.eps);
-        if (s.mode == XS_CAT) inv2 = 1.0f / (float)sqrt(s2 / (double)s.H + s.eps);
-    }
-    // pass 2: final values in place, max |x|
-    float am = 0.f;
-    if (s.mode == XS_NORM || s.mode == XS_CAT) {
-        for (int kb = 0; kb < K; kb += 512) {
-            float wv[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int k = kb + 64 * u + lane;
-                wv[u] = k < K ? (s.mode == XS_CAT ? (k < s.H ? s.w[k] : s.w2[k - s.H]) : s.w[k]) : 0.f;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; u++) {
-                const int k = kb + 64 * u + lane;
-                if (k < K) {
-                    const float iv = (s.mode == XS_CAT && k >= s.H) ? inv2 : inv1;
-                    const float x = xf[k] * iv * wv[u];
-                    xf[k] = x;
-                    am = fmaxf(am, fabsf(x));
-                }
-            }
+        if (lane == 0) {
+            red1[u] = s1;
+            red2[u] = s2;
         }
     } else {
-        for (int k = lane; k < K; k += 64) am = fmaxf(am, fabsf(xf[k]));
+        for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+        if (lane == 0) mred[u] = am;
     }
-    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-    __builtin_amdgcn_wave_barrier();
-    // pass 3: operand planes, one 16-byte item per lane step
-    const size_t pl = (size_t)nk * 4 * M * 16;
-    if (fmt == DT_Q8ROW) {
-        const float sx = am > 0.f ? am / 127.0f : 1.0f, inv = 1.0f / sx;
-        if (lane == 0) lxs[b] = sx;
-        for (int item = lane; item < nk * 4; item += 64) {
+}
+
+// Builds the operand of all M batch rows in LDS with the whole workgroup.
+// Rows are cut into units of 2048 elements; the waves take units round-robin.
+//   phase 1: every input element (and the norm weights) is requested at
+//            once, raw values go to the f32 scratch xf [M][kpad], per-unit
+//            sums of squares (f64) or max|x| to LDS;
+//   phase 2 (RMSNorm producers): inv = 1/sqrt(mean + eps) from the unit sums
+//            in a fixed order, x = (raw * inv) * w in place, per-unit max|x|;
+//   phase 3: operand planes, one 16-byte item per thread step:
+//     q4: hi plane then lo plane, [tile*4 + s][b] x 16 B; lxs[b] = 2^-e
+//     q8: planes q0,q1,q2, [chunk*4 + s][b] x 16 B;      lxs[b] = sx
+__device__ __forceinline__ void stage_fused(const XSrc& s, int M, int fmt, int nk, uint8_t* lx, float* lxs,
+                                            float* xf) {
+    __shared__ double red1[MAXB * SEGMAX], red2[MAXB * SEGMAX];
+    __shared__ float mred[MAXB * SEGMAX];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;  // nk: q8 chunks / q4 tiles
+    const int K4 = s.K >> 2, kp4 = kpad >> 2;
+    const int S = (kp4 + SEG4 - 1) / SEG4, units = M * S;
+    const bool nrm = s.mode == XS_NORM || s.mode == XS_CAT;
+    const int H4 = s.mode == XS_CAT ? s.H >> 2 : 0x7fffffff;
+    float4v* xf4 = (float4v*)xf;
+    float4v* wl4 = xf4 + (size_t)M * kp4;  // norm weight of every element
+    const float4v z4 = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int u = wave; u < units; u += nw) {
+        switch (s.mode) {
+            case XS_SILU: unit_phase1<XS_SILU>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
+            case XS_CAT: unit_phase1<XS_CAT>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
+            case XS_NORM: unit_phase1<XS_NORM>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
+            default: unit_phase1<XS_ROWS>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
+        }
+    }
+    __syncthreads();
+    if (nrm) {
+        const int n1 = s.mode == XS_CAT ? s.H : s.K;
+        for (int u = wave; u < units; u += nw) {
+            const int b = u / S, sg = u % S;
+            double t1 = 0.0, t2 = 0.0;
+            for (int q = 0; q < S; q++) {
+                t1 += red1[b * S + q];
+                t2 += red2[b * S + q];
+            }
+            const float inv1 = 1.0f / (float)sqrt(t1 / (double)n1 + s.eps);
+            const float inv2 = s.mode == XS_CAT ? 1.0f / (float)sqrt(t2 / (double)s.H + s.eps) : 1.f;
+            float am = 0.f;
+#pragma unroll
+            for (int j = 0; j < SEGJ; j++) {
+                const int k4 = sg * SEG4 + 64 * j + lane;
+                if (k4 < K4) {
+                    const float iv = k4 < H4 ? inv1 : inv2;
+                    const float4v x = xf4[(size_t)b * kp4 + k4], w = wl4[k4];
+                    const float4v y = float4v{x.x * iv * w.x, x.y * iv * w.y, x.z * iv * w.z, x.w * iv * w.w};
+                    xf4[(size_t)b * kp4 + k4] = y;
+                    am = amax4(am, y);
+                }
+            }
+            for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+            if (lane == 0) mred[u] = am;
+        }
+        __syncthreads();
+    }
+    const int nitems = nk * 4;
+    const size_t pl = (size_t)nitems * M * 16;
+    for (int i = threadIdx.x; i < M * nitems; i += blockDim.x) {
+        const int b = i / nitems, item = i - b * nitems;
+        float am = 0.f;
+        for (int q = 0; q < S; q++) am = fmaxf(am, mred[b * S + q]);
+        const float* xr = xf + (size_t)b * kpad;
+        const size_t off = ((size_t)item * M + b) * 16;
+        if (fmt == DT_Q8ROW) {
+            const float sx = am > 0.f ? am / 127.0f : 1.0f, inv = 1.0f / sx;
+            if (item == 0) lxs[b] = sx;
             uint32_t w0[4], w1[4], w2[4];
 #pragma unroll
             for (int c = 0; c < 4; c++) {
+                const float4v xv = *(const float4v*)(xr + item * 16 + 4 * c);
+                const float xs4[4] = {xv.x, xv.y, xv.z, xv.w};
                 uint32_t a = 0, bb = 0, cc = 0;
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const float x = xf[item * 16 + 4 * c + j] * inv;
+                    const float x = xs4[j] * inv;
                     const float q0 = fminf(127.f, fmaxf(-127.f, rintf(x)));
                     const float r1 = (x - q0) * 128.0f;
                     const float q1 = fminf(127.f, fmaxf(-127.f, rintf(r1)));
@@ -216,40 +259,35 @@ __device__ __forceinline__ void stage_row(const XSrc& s, int b, int M, int fmt, 
                 w1[c] = bb;
                 w2[c] = cc;
             }
-            const size_t off = ((size_t)item * M + b) * 16;
             *(uint4*)(lx + off) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
             *(uint4*)(lx + pl + off) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
             *(uint4*)(lx + 2 * pl + off) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
-        }
-    } else {
-        int ex = 0;
-        if (am > 0.f) frexpf(am, &ex);
-        const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-        if (lane == 0) lxs[b] = am > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
-        for (int item = lane; item < nk * 4; item += 64) {
-            const float* xv = xf + item * 8;
+        } else {
+            int ex = 0;
+            if (am > 0.f) frexpf(am, &ex);
+            const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+            if (item == 0) lxs[b] = am > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+            const float4v xa = *(const float4v*)(xr + item * 8), xb = *(const float4v*)(xr + item * 8 + 4);
+            // in-slot order {0,2,4,6,1,3,5,7}
+            const float xo[8] = {xa.x, xa.z, xb.x, xb.z, xa.y, xa.w, xb.y, xb.w};
             uint32_t hv[4], lv[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                // in-slot order {0,2,4,6,1,3,5,7}
-                const int ja = j < 2 ? 4 * j : 4 * (j - 2) + 1, jb = ja + 2;
-                const float x0 = xv[ja] * sc, x1 = xv[jb] * sc;
+                const float x0 = xo[2 * j] * sc, x1 = xo[2 * j + 1] * sc;
                 const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
                 const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
                 hv[j] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
                 lv[j] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
             }
-            const size_t off = ((size_t)item * M + b) * 16;
             *(uint4*)(lx + off) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
             *(uint4*)(lx + pl + off) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
         }
     }
 }
 
-// Operand staging of a whole workgroup: waves take batch rows round-robin;
-// XS_GLOBAL planes are copied into the LDS layout when they fit.
+// Operand staging of a whole workgroup; XS_GLOBAL planes are copied into the
+// LDS layout.
 __device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, uint8_t* lx, float* lxs) {
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     if (s.mode == XS_GLOBAL) {
         // global [item/4][16*s + b] x 16 B  ->  LDS [item][b] x 16 B
         const int npl = fmt == DT_Q8ROW ? 3 : 2;
@@ -264,9 +302,7 @@ __device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, u
         if (threadIdx.x < 16) lxs[threadIdx.x] = s.xs[threadIdx.x];
     } else {
         const size_t pbytes = (size_t)nk * 4 * M * 16 * (fmt == DT_Q8ROW ? 3 : 2);
-        float* xf = (float*)(lx + pbytes);
-        const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;
-        for (int b = wave; b < M; b += nw) stage_row(s, b, M, fmt, nk, lx, lxs, xf + (size_t)(b % nw) * kpad);
+        stage_fused(s, M, fmt, nk, lx, lxs, (float*)(lx + pbytes));
     }
     __syncthreads();
 }
@@ -283,6 +319,28 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     __shared__ float lad[FMT == DT_Q4TP ? 16 * 33 : 1];
     __shared__ float4v part[KS][64];
     __shared__ float lxs[16];
+    const int tg0 = (ntg * wave) / KS, tg1 = (ntg * (wave + 1)) / KS;
+    // the first weight steps are requested before the operand staging so
+    // the HBM latency overlaps it
+    uint4 wv[PF];
+    uint32_t sv[PF][2];
+    auto load_w = [&](size_t wbase, int it0) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            if (it0 + u < tg1) {
+                wv[u] = ((const uint4*)a.w)[(wbase + it0 + u) * 64 + lane];
+                if constexpr (FMT == DT_Q4T) {
+                    const uint2 v = ((const uint2*)a.scale)[(wbase + it0 + u) * 16 + r];
+                    sv[u][0] = v.x;
+                    sv[u][1] = v.y;
+                } else {
+                    sv[u][0] = ((const uint32_t*)a.scale)[(wbase + it0 + u) * 16 + r];
+                    sv[u][1] = 0;
+                }
+            }
+        }
+    };
+    if ((int)blockIdx.x < a.nrb) load_w((size_t)(a.rb0 + blockIdx.x) * ntg, tg0);
     const bool in_lds = a.lds != 0;
     if (in_lds) stage_x(a.src, M, FMT, ntg * 4, smem, lxs);
     else if (threadIdx.x < 16) lxs[threadIdx.x] = a.src.xs[threadIdx.x];
@@ -292,8 +350,8 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     const uint4* LH = (const uint4*)smem;
     const uint4* LL = LH + (size_t)ntg * 4 * 4 * M;
     const bool xload = r < M;
-    const int tg0 = (ntg * wave) / KS, tg1 = (ntg * (wave + 1)) / KS;
     const float4v zero = {0.f, 0.f, 0.f, 0.f};
+    bool have = true;
     for (int rb = blockIdx.x; rb < a.nrb; rb += gridDim.x) {
         const size_t wbase = (size_t)(a.rb0 + rb) * ntg;
         if constexpr (FMT == DT_Q4TP) {
@@ -311,22 +369,8 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
         }
         float4v acc = {0.f, 0.f, 0.f, 0.f};
         for (int it0 = tg0; it0 < tg1; it0 += PF) {
-            uint4 wv[PF];
-            uint32_t sv[PF][2];
-#pragma unroll
-            for (int u = 0; u < PF; u++) {
-                if (it0 + u < tg1) {
-                    wv[u] = ((const uint4*)a.w)[(wbase + it0 + u) * 64 + lane];
-                    if constexpr (FMT == DT_Q4T) {
-                        const uint2 v = ((const uint2*)a.scale)[(wbase + it0 + u) * 16 + r];
-                        sv[u][0] = v.x;
-                        sv[u][1] = v.y;
-                    } else {
-                        sv[u][0] = ((const uint32_t*)a.scale)[(wbase + it0 + u) * 16 + r];
-                        sv[u][1] = 0;
-                    }
-                }
-            }
+            if (!have) load_w(wbase, it0);
+            have = false;
 #pragma unroll
             for (int u = 0; u < PF; u++) {
                 if (it0 + u >= tg1) break;
@@ -406,6 +450,14 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
     const int M = a.m, nkc = a.nk;
     __shared__ int4v part[KS > 1 ? KS : 1][3][64];
     __shared__ float lxs[16];
+    const int k0 = (nkc * wave) / KS, k1 = (nkc * (wave + 1)) / KS;
+    int4v wv[PF];
+    auto load_w = [&](size_t wbase, int it0) {
+#pragma unroll
+        for (int u = 0; u < PF; u++)
+            if (it0 + u < k1) wv[u] = ((const int4v*)a.w)[(wbase + it0 + u) * 64 + lane];
+    };
+    if ((int)blockIdx.x < a.nrb) load_w((size_t)(a.rb0 + blockIdx.x) * nkc, k0);
     const bool in_lds = a.lds != 0;
     if (in_lds) stage_x(a.src, M, DT_Q8ROW, nkc, smem, lxs);
     else if (threadIdx.x < 16) lxs[threadIdx.x] = a.src.xs[threadIdx.x];
@@ -414,15 +466,13 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
     const size_t gpl = (size_t)nkc * 64, lpl = (size_t)nkc * 4 * M;
     const int4v* L0 = (const int4v*)smem;
     const bool xload = r < M;
-    const int k0 = (nkc * wave) / KS, k1 = (nkc * (wave + 1)) / KS;
+    bool have = true;
     for (int rb = blockIdx.x; rb < a.nrb; rb += gridDim.x) {
         const size_t wbase = (size_t)(a.rb0 + rb) * nkc;
         int4v a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0};
         for (int it0 = k0; it0 < k1; it0 += PF) {
-            int4v wv[PF];
-#pragma unroll
-            for (int u = 0; u < PF; u++)
-                if (it0 + u < k1) wv[u] = ((const int4v*)a.w)[(wbase + it0 + u) * 64 + lane];
+            if (!have) load_w(wbase, it0);
+            have = false;
 #pragma unroll
             for (int u = 0; u < PF; u++) {
                 if (it0 + u >= k1) break;
@@ -501,36 +551,6 @@ __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ X, int l
     else prep16_row(x, K, amax, nk, b, planes, xs, threadIdx.x, 256);
 }
 
-// Producer-only kernel for operands too large for LDS: evaluates the XSrc
-// into f32 rows (one workgroup per batch row), then k_prep prepares them.
-__global__ __launch_bounds__(256) void k_xsrc_rows(XSrc s, float* __restrict__ out, int ldo) {
-    const int b = blockIdx.x, t = threadIdx.x;
-    __shared__ double redd[4];
-    float inv1 = 1.f, inv2 = 1.f;
-    int tok = 0;
-    if (s.mode == XS_CAT) tok = s.toks[b];
-    if (s.mode == XS_NORM || s.mode == XS_CAT) {
-        const int n1 = s.mode == XS_CAT ? s.H : s.K;
-        double a = 0.0;
-        for (int k = t; k < n1; k += 256) {
-            const float v = s.mode == XS_CAT ? embed_val(s.emb, tok, k) : s.x[(size_t)b * s.ldx + k];
-            a += (double)v * (double)v;
-        }
-        a = wg_sum_d(a, redd);
-        inv1 = 1.0f / (float)sqrt(a / (double)n1 + s.eps);
-        if (s.mode == XS_CAT) {
-            double c = 0.0;
-            for (int k = t; k < s.H; k += 256) {
-                const float v = s.x[(size_t)b * s.ldx + k];
-                c += (double)v * (double)v;
-            }
-            c = wg_sum_d(c, redd);
-            inv2 = 1.0f / (float)sqrt(c / (double)s.H + s.eps);
-        }
-    }
-    for (int k = t; k < s.K; k += 256) out[(size_t)b * ldo + k] = xin(s, b, k, tok, inv1, inv2);
-}
-
 // ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------
@@ -550,9 +570,10 @@ int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* pla
 static size_t lds_bytes(const DevWeight& w, int m) {
     return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 128 * 4 * m;
 }
-// plus the f32 row scratch of the in-kernel producers (one row per wave)
-static size_t lds_scratch(const DevWeight& w, int rows) {
-    return (size_t)(w.dtype == DT_Q8ROW ? w.kchunks * 64 : w.kchunks * 128) * 4 * rows;
+// plus the f32 scratch of the in-kernel producers: the m raw rows and the
+// norm weights
+static size_t lds_scratch(const DevWeight& w, int m) {
+    return (size_t)(w.dtype == DT_Q8ROW ? w.kchunks * 64 : w.kchunks * 128) * 4 * (m + 1);
 }
 
 template <int FMT, int NV, int KS>
@@ -622,7 +643,13 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
     pick_shape(a.nrb, w.kchunks, &ks, &grid);
     if (ks_override > 0) ks = ks_override;
     size_t lds = lds_bytes(w, m);
-    if (src.mode != XS_GLOBAL) lds += lds_scratch(w, std::min(m, ks));
+    if (src.mode != XS_GLOBAL) {
+        const int kpad = w.dtype == DT_Q8ROW ? w.kchunks * 64 : w.kchunks * 128;
+        if (a.src.K % 4 || (src.mode != XS_CAT && src.ldx % 4) || (src.mode == XS_CAT && (src.H % 4 || src.ldx % 4)) ||
+            ((uintptr_t)src.x & 15) || kpad > 4 * SEG4 * SEGMAX)
+            return fail("gemv: fused operand needs K, H, ldx multiples of 4, a 16-byte aligned row base and K <= 16384");
+        lds += lds_scratch(w, m);
+    }
     if (lds > LDSX_MAX) {
         if (src.mode != XS_GLOBAL) return fail("gemv: activation operand exceeds LDS; prepare it globally");
         lds = 0;  // planes read from global memory per step
@@ -659,12 +686,7 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
     return CMF_OK;
 }
 
-bool fits_lds(const DevWeight& w, int m) { return lds_bytes(w, m) + lds_scratch(w, std::min(m, 16)) <= LDSX_MAX; }
-
-int launch_xsrc_rows(const XSrc& s, int m, float* out, int ldo, hipStream_t st) {
-    hipLaunchKernelGGL(k_xsrc_rows, dim3(m), dim3(256), 0, st, s, out, ldo);
-    return CMF_OK;
-}
+bool fits_lds(const DevWeight& w, int m) { return lds_bytes(w, m) + lds_scratch(w, m) <= LDSX_MAX; }
 
 int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
                 int m, int row_lo, int row_hi, hipStream_t st, int ks_override) {

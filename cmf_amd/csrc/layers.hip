@@ -189,128 +189,125 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(
     }
 }
 
-// Split-K decode attention.  grid (nkv, nchunks), one wave per block.  Query
-// rows b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.  A wave
-// takes ATT_C = 64 key positions of one KV head for all nq = nb * hpk
-// queries, G queries at a time: lanes are positions for the scores (each
-// lane streams its own K row), the chunk softmax reduces across the wave,
-// and for the value pass lanes are head dims (coalesced V rows) with the
-// chunk weights broadcast by readlane.  Partials: running max, sum of exp,
-// unnormalised output.
-template <int G>
-__global__ __launch_bounds__(64) void k_attn_partial(
+// Split-K decode attention.  grid (nkv, nchunks), 256 threads per block.
+// Query rows b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.
+// A block takes ATT_C = 64 key positions of one KV head for all nq = nb*hpk
+// (<= 32) queries.  Every thread issues its K and V loads at once (one
+// memory round trip), V goes to LDS, and:
+//   scores : lane = (position p = lane % 16 of the wave's 16, dim quarter
+//            lane / 16); partial dots over 32 dims, reduced across quarters;
+//   softmax: one thread per query over the 64 positions;
+//   values : thread = (dim, query parity), weights and V rows from LDS.
+// Partials: running max, sum of exp, unnormalised output per (row, head).
+__global__ __launch_bounds__(256) void k_attn_partial(
     const float* __restrict__ q, int ldq, const float* __restrict__ kc, const float* __restrict__ vc,
     int max_seq, int nb, int nh, int nkv, const int* __restrict__ pbase, int padd,
     float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po, int nch) {
-    constexpr int HD = 128;
-    const int g = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    constexpr int HD = 128, C = ATT_C;
+    const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
     const int hpk = nh / nkv, nq = nb * hpk;
     const int pos0 = *pbase + padd;
     const int stored = pos0 + nb;
-    const int p0 = c * ATT_C;
+    const int p0 = c * C;
     __shared__ float Q[32][HD];
-    if (p0 >= stored) {
-        if (lane < nq) {
-            const int bi = lane / hpk, h = g * hpk + lane % hpk;
-            const size_t row = (size_t)bi * nh + h;
-            pm[row * nch + c] = -INFINITY;
-            pl[row * nch + c] = 0.f;
-        }
-        return;
+    __shared__ float V[C][HD + 4];
+    __shared__ float S[32][C + 1];
+    if (p0 >= stored) return;  // the merge reads only chunks holding keys
+    const int np = min(C, stored - p0);
+    // ---- all loads first: K slice, V slice, Q ----
+    const int pk = wave * 16 + (lane & 15), dq = lane >> 4;  // score-phase position / dim quarter
+    const bool kvalid = pk < np;
+    const float4* Kp = (const float4*)(kc + ((size_t)g * max_seq + p0 + (kvalid ? pk : 0)) * HD + 32 * dq);
+    float4 kv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) kv[j] = Kp[j];
+    // V: 64 rows x 32 float4; thread t loads float4 column t % 32 of rows t/32 + 8u
+    const float4* Vg = (const float4*)(vc + ((size_t)g * max_seq + p0) * HD);
+    float4 vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int r = (t >> 5) + 8 * u;
+        vv[u] = r < np ? Vg[(size_t)r * (HD / 4) + (t & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const int ng = (nq + G - 1) / G;
-    {
-        // the nq query rows of this KV head: for batch row bi the hpk heads
-        // g*hpk.. are contiguous (hpk * HD floats); hpk is a power of two
-        const int lg = 31 - __clz(hpk * (HD / 4));  // log2 of float4s per batch row
-        const float4* qs = (const float4*)q;
-        float4 qv[16];
+    // Q rows: batch row bi holds heads g*hpk.. contiguously (hpk * HD floats)
+    const int lg = 31 - __clz(hpk * (HD / 4));
+    float4 qv[4];
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int e = lane + 64 * u, bi = e >> lg, rem = e & ((1 << lg) - 1);
-            qv[u] = e < nq * (HD / 4) ? qs[((size_t)bi * ldq + (size_t)g * hpk * HD) / 4 + rem]
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int u = 0; u < 4; u++) {
+        const int e = t + 256 * u, bi = e >> lg, rem = e & ((1 << lg) - 1);
+        qv[u] = e < nq * (HD / 4) ? ((const float4*)q)[((size_t)bi * ldq + (size_t)g * hpk * HD) / 4 + rem]
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; u++) ((float4*)Q)[t + 256 * u] = qv[u];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int r = (t >> 5) + 8 * u;
+        *(float4*)&V[r][4 * (t & 31)] = vv[u];
+    }
+    __syncthreads();
+    // ---- scores ----
+    const float scale = 1.0f / sqrtf((float)HD);
+    for (int q0 = 0; q0 < nq; q0 += 8) {
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float a = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 qq = *(const float4*)&Q[q0 + i][32 * dq + 4 * j];
+                a += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+            }
+            a += __shfl_xor(a, 16);
+            a += __shfl_xor(a, 32);
+            acc[i] = a;
         }
+        if (dq == 0) {
 #pragma unroll
-        for (int u = 0; u < 16; u++) {
-            const int e = lane + 64 * u;
-            if (e < ng * G * (HD / 4)) ((float4*)Q)[e] = qv[u];
+            for (int i = 0; i < 8; i++) {
+                const int qi = q0 + i;
+                if (qi < nq) {
+                    const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
+                    S[qi][pk] = see ? acc[i] * scale : -INFINITY;
+                }
+            }
         }
     }
     __syncthreads();
-    const int p = p0 + lane;
-    const bool valid = p < stored;
-    const float4* K = (const float4*)(kc + ((size_t)g * max_seq + (valid ? p : 0)) * HD);
-    const int np = min(ATT_C, stored - p0);
-    const float2* V = (const float2*)(vc + ((size_t)g * max_seq + p0) * HD) + lane;
-    const float scale = 1.0f / sqrtf((float)HD);
-    for (int grp = 0; grp < ng; grp++) {
-        const int q0 = grp * G;
-        float acc[G];
+    // ---- chunk softmax: one thread per query ----
+    if (t < nq) {
+        float m = -INFINITY;
+        for (int p = 0; p < C; p++) m = fmaxf(m, p < np ? S[t][p] : -INFINITY);
+        float l = 0.f;
+        for (int p = 0; p < C; p++) {
+            const float e = (p < np && m != -INFINITY) ? expf(S[t][p] - m) : 0.f;
+            S[t][p] = e;
+            l += e;
+        }
+        const size_t row = (size_t)(t / hpk) * nh + g * hpk + t % hpk;
+        pm[row * nch + c] = m;
+        pl[row * nch + c] = l;
+    }
+    __syncthreads();
+    // ---- values: thread = (dim d, query parity) ----
+    {
+        const int d = t & 127, par = t >> 7;
+        for (int qi0 = par; qi0 < nq; qi0 += 8) {
+            float o[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int p = 0; p < np; p++) {
+                const float vd = V[p][d];
 #pragma unroll
-        for (int i = 0; i < G; i++) acc[i] = 0.f;
-#pragma unroll 1
-        for (int half = 0; half < 2; half++) {
-            float4 kv[16];
+                for (int i = 0; i < 4; i++)
+                    if (qi0 + 2 * i < nq) o[i] += S[qi0 + 2 * i][p] * vd;
+            }
 #pragma unroll
-            for (int j = 0; j < 16; j++) kv[j] = K[half * 16 + j];
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                // opaque offset: keeps the G query reads of step j at step j
-                // (hoisting all of them would need 16*G*4 registers)
-                int d = (half * 16 + j) * 4;
-                CMF_OPAQUE(d);
-#pragma unroll
-                for (int i = 0; i < G; i++) {
-                    const float4 qq = *(const float4*)&Q[q0 + i][d];
-                    acc[i] += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+            for (int i = 0; i < 4; i++) {
+                const int qi = qi0 + 2 * i;
+                if (qi < nq) {
+                    const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
+                    po[(row * nch + c) * HD + d] = o[i];
                 }
-            }
-        }
-        float w[G];
-#pragma unroll
-        for (int i = 0; i < G; i++) {
-            const int qi = q0 + i, bi = qi / hpk;
-            const bool see = valid && p <= pos0 + bi && qi < nq;
-            const float sv = see ? acc[i] * scale : -INFINITY;
-            float m = sv;
-            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-            const float e = m == -INFINITY ? 0.f : expf(sv - m);
-            float l = e;
-            for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-            w[i] = e;
-            if (lane == 0 && qi < nq) {
-                const size_t row = (size_t)bi * nh + g * hpk + qi % hpk;
-                pm[row * nch + c] = m;
-                pl[row * nch + c] = l;
-            }
-        }
-        // value pass: lane owns dims 2*lane, 2*lane+1; 16 V rows in flight
-        float2 o[G];
-#pragma unroll
-        for (int i = 0; i < G; i++) o[i] = make_float2(0.f, 0.f);
-#pragma unroll 1
-        for (int pb = 0; pb < np; pb += 16) {
-            float2 vv[16];
-#pragma unroll
-            for (int j = 0; j < 16; j++)
-                vv[j] = pb + j < np ? V[(size_t)(pb + j) * (HD / 2)] : make_float2(0.f, 0.f);
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-#pragma unroll
-                for (int i = 0; i < G; i++) {
-                    const float ww = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[i]), pb + j));
-                    o[i].x += ww * vv[j].x;
-                    o[i].y += ww * vv[j].y;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < G; i++) {
-            const int qi = q0 + i;
-            if (qi < nq) {
-                const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
-                ((float2*)(po + (row * nch + c) * HD))[lane] = o[i];
             }
         }
     }
@@ -495,14 +492,8 @@ void launch_attention(const float* q, int ldq, const float* kc, const float* vc,
                       int nh, int nkv, const int* pbase, int padd, int max_len, float* pm, float* pl,
                       float* po, int nch_cap, float* out_f32, hipStream_t st) {
     const int nch = (max_len + ATT_C - 1) / ATT_C;
-    const int nq = nb * (nh / nkv);
-#define CMF_ATT(G)                                                                                  \
-    hipLaunchKernelGGL((k_attn_partial<G>), dim3(nkv, nch), dim3(64), 0, st, q, ldq, kc, vc, max_seq, \
-                       nb, nh, nkv, pbase, padd, pm, pl, po, nch_cap)
-    if (nq <= 2) CMF_ATT(2);
-    else if (nq <= 4) CMF_ATT(4);
-    else CMF_ATT(8);
-#undef CMF_ATT
+    hipLaunchKernelGGL(k_attn_partial, dim3(nkv, nch), dim3(256), 0, st, q, ldq, kc, vc, max_seq, nb, nh, nkv,
+                       pbase, padd, pm, pl, po, nch_cap);
     hipLaunchKernelGGL(k_attn_merge, dim3(nb * nh), dim3(64), 0, st, pm, pl, po, nh, nch_cap, pbase, padd,
                        out_f32);
 }

@@ -97,3 +97,34 @@ def test_sampling_spec_tokens_equal_oracle(small):
     print("cpu", ot.tolist(), ost.accepted, flush=True)
     n = min(len(gt), len(ot))
     assert gt[:n].tolist() == ot[:n].tolist()
+
+
+@pytest.mark.parametrize("sampling", [False, True])
+def test_captured_rounds_equal_eager_and_oracle(small, sampling, monkeypatch):
+    """decode_rounds(n > 1) replays one captured round n - 1 times; two such
+    calls in a row (the second replaying the graph kept from the first, with a
+    host state read in between) give the eagerly launched tokens and the
+    oracle's"""
+    sm, g = small
+    import cmf_amd
+    from cmf_amd import synth
+    from cmf_amd.model import Model
+    prompt = synth.ids(23, 18, SMALL["vocab"])
+    sg = cmf_amd.SamplerConfig(temperature=0.8, repetition_penalty=1.0) if sampling else None
+    so = orc.SamplerCfg(0.8, 0.9, 40, 1.0, 0.05, 0.0) if sampling else None
+    monkeypatch.setenv("CMF_DECODE_GRAPH", "0")
+    eager = Model(sm)
+    runs = []
+    for m in (g, eager):
+        m.prefill(prompt)
+        m.decode_begin(sampler=sg, seed=77)
+        m.decode_rounds(5, spec=True, k=3)
+        st = m.state()
+        m.decode_rounds(4, spec=True, k=3)
+        runs.append(m.tokens())
+        print("graph" if m is g else "eager", runs[-1].tolist(), "pos", st[0], flush=True)
+    eager.free()
+    assert runs[0].tolist() == runs[1].tolist()
+    o = orc.OracleModel(sm)
+    ot, _ = o.generate(prompt, len(runs[0]) + 8, spec=True, k=3, sampler=so, seed=77)
+    assert runs[0].tolist() == ot[:len(runs[0])].tolist()
