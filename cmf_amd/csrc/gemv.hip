@@ -181,7 +181,7 @@ __device__ __forceinline__ void stage_fused(const XSrc& s, int M, int fmt, int n
                                             float* xf) {
     __shared__ double red1[MAXB * SEGMAX], red2[MAXB * SEGMAX];
     __shared__ float mred[MAXB * SEGMAX];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
     const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;  // nk: q8 chunks / q4 tiles
     const int K4 = s.K >> 2, kp4 = kpad >> 2;
     const int S = (kp4 + SEG4 - 1) / SEG4, units = M * S;
@@ -313,7 +313,7 @@ __device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, u
 template <int FMT, int NV, int KS>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4;
     const int M = a.m, ntg = a.nk;  // nk = groups of 4 tiles
     __shared__ float lad[FMT == DT_Q4TP ? 16 * 33 : 1];
@@ -445,7 +445,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
 template <int KS>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4;
     const int M = a.m, nkc = a.nk;
     __shared__ int4v part[KS > 1 ? KS : 1][3][64];

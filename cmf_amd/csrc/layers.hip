@@ -189,6 +189,69 @@ __global__ __launch_bounds__(256) void k_qk_rope_append(
     }
 }
 
+// Chunk softmax and value pass of the NQ queries qi = w + 4i owned by one
+// wave: lane = key position for the softmax (max, exp, sum by wave
+// reductions; the weights overwrite the scores), lane = dim pair for the
+// values, o[qi][d] = sum_p e[qi][p] * V[p][d] in position order.
+template <int NQ>
+__device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[128 + 4], int w, int lane, int hpk,
+                                            int nh, int g, int c, int nch, float* pm, float* pl, float* po) {
+    constexpr int C = ATT_C, HD = 128;
+    float m[NQ], l[NQ], e[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) m[i] = S[w + 4 * i][lane];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+        for (int i = 0; i < NQ; i++) m[i] = fmaxf(m[i], __shfl_xor(m[i], off));
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        e[i] = m[i] == -INFINITY ? 0.f : expf(S[w + 4 * i][lane] - m[i]);
+        l[i] = e[i];
+        S[w + 4 * i][lane] = e[i];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+        for (int i = 0; i < NQ; i++) l[i] += __shfl_xor(l[i], off);
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const int qi = w + 4 * i;
+            const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
+            pm[row * nch + c] = m[i];
+            pl[row * nch + c] = l[i];
+        }
+    }
+    float2 o[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) o[i] = make_float2(0.f, 0.f);
+#pragma unroll 2
+    for (int p0 = 0; p0 < C; p0 += 4) {
+        float2 vd[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) vd[j] = *(const float2*)&V[p0 + j][2 * lane];
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            const float4 ew = *(const float4*)&S[w + 4 * i][p0];
+            o[i].x += ew.x * vd[0].x;
+            o[i].y += ew.x * vd[0].y;
+            o[i].x += ew.y * vd[1].x;
+            o[i].y += ew.y * vd[1].y;
+            o[i].x += ew.z * vd[2].x;
+            o[i].y += ew.z * vd[2].y;
+            o[i].x += ew.w * vd[3].x;
+            o[i].y += ew.w * vd[3].y;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int qi = w + 4 * i;
+        const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
+        ((float2*)(po + (row * nch + c) * HD))[lane] = o[i];
+    }
+}
+
 // Split-K decode attention.  grid (nkv, nchunks), 256 threads per block.
 // Query rows b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.
 // A block takes ATT_C = 64 key positions of one KV head for all nq = nb*hpk
@@ -212,7 +275,7 @@ __global__ __launch_bounds__(256) void k_attn_partial(
     const int p0 = c * C;
     __shared__ float Q[32][HD];
     __shared__ float V[C][HD + 4];
-    __shared__ float S[32][C + 1];
+    __shared__ __align__(16) float S[32][C];
     if (p0 >= stored) return;  // the merge reads only chunks holding keys
     const int np = min(C, stored - p0);
     // ---- all loads first: K slice, V slice, Q ----
@@ -275,41 +338,19 @@ __global__ __launch_bounds__(256) void k_attn_partial(
         }
     }
     __syncthreads();
-    // ---- chunk softmax: one thread per query ----
-    if (t < nq) {
-        float m = -INFINITY;
-        for (int p = 0; p < C; p++) m = fmaxf(m, p < np ? S[t][p] : -INFINITY);
-        float l = 0.f;
-        for (int p = 0; p < C; p++) {
-            const float e = (p < np && m != -INFINITY) ? expf(S[t][p] - m) : 0.f;
-            S[t][p] = e;
-            l += e;
-        }
-        const size_t row = (size_t)(t / hpk) * nh + g * hpk + t % hpk;
-        pm[row * nch + c] = m;
-        pl[row * nch + c] = l;
-    }
-    __syncthreads();
-    // ---- values: thread = (dim d, query parity) ----
-    {
-        const int d = t & 127, par = t >> 7;
-        for (int qi0 = par; qi0 < nq; qi0 += 8) {
-            float o[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int p = 0; p < np; p++) {
-                const float vd = V[p][d];
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    if (qi0 + 2 * i < nq) o[i] += S[qi0 + 2 * i][p] * vd;
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int qi = qi0 + 2 * i;
-                if (qi < nq) {
-                    const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
-                    po[(row * nch + c) * HD + d] = o[i];
-                }
-            }
-        }
+    // ---- softmax and values: wave w owns queries w, w+4, .. ----
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const int nqw = (nq - wv + 3) >> 2;
+    switch (nqw) {
+        case 0: break;
+        case 1: attn_values<1>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        case 2: attn_values<2>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        case 3: attn_values<3>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        case 4: attn_values<4>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        case 5: attn_values<5>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        case 6: attn_values<6>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        case 7: attn_values<7>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        default: attn_values<8>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
     }
 }
 
