@@ -217,10 +217,14 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
     const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
     const int QKV = (nh + 2 * nkv) * hd, I = c.inter;
     gemv_f(m, l.qkv, src_norm(h, H, l.in_norm, c.eps), m->qkv_out, QKV, nb, false, s);
-    launch_qk_rope_append(m->qkv_out, QKV, l.q_norm, l.k_norm, m->rope, nh, nkv, hd, c.eps, pb, padd,
-                          l.kc, l.vc, c.max_seq, m->qrot, nh * hd, nb, s);
-    launch_attention(m->qrot, nh * hd, l.kc, l.vc, c.max_seq, nb, nh, nkv, pb, padd, max_len, m->pm,
-                     m->pl, m->po, m->nch_cap, m->ao, s);
+    // the attention kernel holds at most 32 query heads per kv head
+    const int rows_per = std::max(1, 32 / (nh / nkv));
+    for (int b0 = 0; b0 < nb; b0 += rows_per) {
+        AttnArgs at{m->qkv_out + (size_t)b0 * QKV, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq,
+                    std::min(rows_per, nb - b0), nh, nkv, c.eps, pb, padd + b0, m->pm, m->pl, m->po, m->nch_cap,
+                    m->ao + (size_t)b0 * nh * hd, 1};
+        launch_attention(at, max_len, s);
+    }
     XSrc ra{};
     ra.mode = XS_ROWS;
     ra.x = m->ao;
@@ -262,15 +266,16 @@ XSrc src_cat(cmf_model_s* m, const int* toks, const float* hid) {
 
 // MTP warm (mtp_warm, pipeline.rs:3532-3572): eh_proj on [enorm(embed(tok));
 // hnorm(h)], input norm, q/k/v, qk-norm + RoPE, KV append.  No attention.
-void mtp_warm(cmf_model_s* m, const int* toks, const float* hid, int nb, const int* pb, int padd,
+void mtp_warm(cmf_model_s* m, const int* toks, const float* hid, int nb, const int* pb, int padd, int max_len,
               hipStream_t s) {
     const auto& c = m->c;
     const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
     const int QKV = (nh + 2 * nkv) * hd;
     gemv_f(m, m->eh, src_cat(m, toks, hid), m->hm, H, nb, false, s);
     gemv_f(m, m->mtp.qkv, src_norm(m->hm, H, m->mtp.in_norm, c.eps), m->qkv_out, QKV, nb, false, s);
-    launch_qk_rope_append(m->qkv_out, QKV, m->mtp.q_norm, m->mtp.k_norm, m->rope, nh, nkv, hd, c.eps, pb,
-                          padd, m->mtp.kc, m->mtp.vc, c.max_seq, m->qrot, nh * hd, nb, s);
+    AttnArgs at{m->qkv_out, QKV, m->mtp.q_norm, m->mtp.k_norm, m->rope, m->mtp.kc, m->mtp.vc, c.max_seq, nb, nh,
+                nkv, c.eps, pb, padd, nullptr, nullptr, nullptr, 0, nullptr, 0};
+    launch_attention(at, max_len, s);
 }
 
 // One MTP draft step (mtp_step_hl, pipeline.rs:3051-3160) for a single row:
@@ -424,6 +429,7 @@ int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
     if (c.head_dim != 128) return fail("model_create: the attention kernels are built for head_dim 128");
     if ((c.n_heads / c.n_kv) & (c.n_heads / c.n_kv - 1))
         return fail("model_create: query heads per KV head must be a power of two");
+    if (c.n_heads / c.n_kv > 32) return fail("model_create: at most 32 query heads per KV head");
     if (c.hidden > 4096 || c.inter > 12288 || c.n_heads * c.head_dim > 4096)
         return fail("model_create: hidden <= 4096, inter <= 12288, heads*head_dim <= 4096");
     if (c.hidden % 32 || c.inter % 32) return fail("model_create: hidden and inter must be multiples of 32");
@@ -514,7 +520,7 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
             const int pairs = (p0 + cnt < n) ? cnt : cnt - 1;
             if (pairs > 0) {
                 CMF_HIP(hipMemcpyAsync(m->toks + MAXB, ids + p0 + 1, pairs * sizeof(int), hipMemcpyHostToDevice, s));
-                mtp_warm(m, m->toks + MAXB, m->hv, pairs, pb, 0, s);
+                mtp_warm(m, m->toks + MAXB, m->hv, pairs, pb, 0, p0 + pairs, s);
             }
         }
         if (p0 + cnt == n)
@@ -564,7 +570,7 @@ static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_conf
         launch_argmax(m->logits, V, V, k + 1, m->am_v, m->am_i, m->st->argmax, s);
         hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(1), 0, s, m->st, k, m->out);
     }
-    mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, s);
+    mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, graph_len ? graph_len : np + k + 1, s);
     hipLaunchKernelGGL(k_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H);
 }
 

@@ -6,7 +6,7 @@
 
 namespace cmf {
 
-constexpr int ATT_C = 64;  // key positions per attention wave
+constexpr int ATT_C = 64;  // key positions per attention workgroup
 
 // Where a producer writes its prepared activations (see gemv.h).
 struct PrepDst {
@@ -25,13 +25,28 @@ void launch_mtp_cat_prep(const int* toks, const float* hid, int ldh, const Embed
                          int nb, hipStream_t st);
 void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
                   hipStream_t st);
-void launch_qk_rope_append(const float* qkv, int ldq, const float* qn, const float* kn,
-                           const float2* rope, int nh, int nkv, int hd, double eps, const int* pbase,
-                           int padd, float* kc, float* vc, int max_seq, float* qout, int ldqo, int nb,
-                           hipStream_t st);
-void launch_attention(const float* q, int ldq, const float* kc, const float* vc, int max_seq, int nb,
-                      int nh, int nkv, const int* pbase, int padd, int max_len, float* pm, float* pl,
-                      float* po, int nch_cap, float* out_f32, hipStream_t st);
+// One layer's decode attention (head_dim 128): q/k-norm + RoPE, KV append,
+// chunked causal attention over the cache and the merge into out
+// [nb][nh * 128].  pm/pl [MAXB * nh][nch], po [MAXB * nh][nch][128] hold the
+// chunk partials.
+struct AttnArgs {
+    const float* qkv;   // [nb][ldq] projected q | k | v heads
+    int ldq;
+    const float* qn;    // q-norm / k-norm weights [128]
+    const float* kn;
+    const float2* rope; // (cos, sin) [max_seq][64]
+    float* kc;          // [nkv][max_seq][128]
+    float* vc;
+    int max_seq, nb, nh, nkv;
+    double eps;
+    const int* pbase;   // rows sit at positions *pbase + padd + b
+    int padd;
+    float *pm, *pl, *po;
+    int nch;            // chunk capacity of the partial buffers
+    float* out;
+    int attend;         // 0: only append the rows' K/V (no queries, no output)
+};
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st);
 void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,
                           hipStream_t st);
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,

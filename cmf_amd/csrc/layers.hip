@@ -150,43 +150,17 @@ __global__ __launch_bounds__(256) void k_embed(const int* __restrict__ toks, Emb
     }
 }
 
-// qk-norm + RoPE for the Q and K heads of qkv rows, K/V rows appended at
-// position pos0 + b.  grid (nb, nh + 2*nkv), block hd (<= 256, even).
-__global__ __launch_bounds__(256) void k_qk_rope_append(
-    const float* __restrict__ qkv, int ldq, const float* __restrict__ qn,
-    const float* __restrict__ kn, const float2* __restrict__ rope, int nh, int nkv, int hd,
-    double eps, const int* __restrict__ pbase, int padd, float* __restrict__ kc,
-    float* __restrict__ vc, int max_seq, float* __restrict__ qout, int ldqo) {
-    const int b = blockIdx.x, j = blockIdx.y, t = threadIdx.x;
-    const int pos = *pbase + padd + b;
-    __shared__ float x[256];
-    __shared__ double redd[4];
-    const float v = qkv[(size_t)b * ldq + (size_t)j * hd + t];
-    if (j >= nh + nkv) {  // V head: stored as projected
-        const int g = j - nh - nkv;
-        vc[((size_t)g * max_seq + pos) * hd + t] = v;
-        return;
-    }
-    const float* wn = j < nh ? qn : kn;
-    const double ss = block_sum_d((double)v * (double)v, redd);
-    const float inv = (float)(1.0 / sqrt(ss / (double)hd + eps));
-    x[t] = v * inv * wn[t];
-    __syncthreads();
-    const int half = hd >> 1;
-    float o;
-    if (t < half) {
-        const float2 cs = rope[(size_t)pos * half + t];  // (cos, sin)
-        o = x[t] * cs.x - x[t + half] * cs.y;
-    } else {
-        const float2 cs = rope[(size_t)pos * half + (t - half)];
-        o = x[t - half] * cs.y + x[t] * cs.x;
-    }
-    if (j < nh) {
-        qout[(size_t)b * ldqo + (size_t)j * hd + t] = o;
-    } else {
-        const int g = j - nh;
-        kc[((size_t)g * max_seq + pos) * hd + t] = o;
-    }
+// qk-norm + RoPE of one head row x (lane holds dims lane and lane + 64, the
+// rotation pair): x * inv * w with inv = 1/sqrt(mean(x^2) + eps) (f64 sum),
+// then (a, b) -> (a cos - b sin, a sin + b cos) at position pos.
+__device__ __forceinline__ float2 head_norm_rope(float x0, float x1, const float* w, const float2* rope, int pos,
+                                                 double eps, int lane) {
+    double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float inv = (float)(1.0 / sqrt(ss / 128.0 + eps));
+    const float a = x0 * inv * w[lane], b = x1 * inv * w[lane + 64];
+    const float2 cs = rope[(size_t)pos * 64 + lane];  // (cos, sin)
+    return make_float2(a * cs.x - b * cs.y, a * cs.y + b * cs.x);
 }
 
 // Chunk softmax and value pass of the NQ queries qi = w + 4i owned by one
@@ -252,121 +226,42 @@ __device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[
     }
 }
 
-// Split-K decode attention.  grid (nkv, nchunks), 256 threads per block.
-// Query rows b = 0..nb-1 sit at positions pos0 + b and see keys 0..pos0+b.
-// A block takes ATT_C = 64 key positions of one KV head for all nq = nb*hpk
-// (<= 32) queries.  Every thread issues its K and V loads at once (one
-// memory round trip), V goes to LDS, and:
-//   scores : lane = (position p = lane % 16 of the wave's 16, dim quarter
-//            lane / 16); partial dots over 32 dims, reduced across quarters;
-//   softmax: one thread per query over the 64 positions;
-//   values : thread = (dim, query parity), weights and V rows from LDS.
-// Partials: running max, sum of exp, unnormalised output per (row, head).
-__global__ __launch_bounds__(256) void k_attn_partial(
-    const float* __restrict__ q, int ldq, const float* __restrict__ kc, const float* __restrict__ vc,
-    int max_seq, int nb, int nh, int nkv, const int* __restrict__ pbase, int padd,
-    float* __restrict__ pm, float* __restrict__ pl, float* __restrict__ po, int nch) {
+// K (k-norm + RoPE) and V rows of the new positions pos0 + b that fall in the
+// chunk at p0, one wave per row: appended to the cache and, when Kn is given,
+// kept in LDS (Kn[b], V[pos - p0]) for the chunk's own attention.
+__device__ __forceinline__ void append_rows(const AttnArgs& a, int g, int p0, int pos0, int wave, int lane,
+                                            float (*Kn)[128], float (*V)[128 + 4]) {
     constexpr int HD = 128, C = ATT_C;
-    const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    const int hpk = nh / nkv, nq = nb * hpk;
-    const int pos0 = *pbase + padd;
-    const int stored = pos0 + nb;
-    const int p0 = c * C;
-    __shared__ float Q[32][HD];
-    __shared__ float V[C][HD + 4];
-    __shared__ __align__(16) float S[32][C];
-    if (p0 >= stored) return;  // the merge reads only chunks holding keys
-    const int np = min(C, stored - p0);
-    // ---- all loads first: K slice, V slice, Q ----
-    const int pk = wave * 16 + (lane & 15), dq = lane >> 4;  // score-phase position / dim quarter
-    const bool kvalid = pk < np;
-    const float4* Kp = (const float4*)(kc + ((size_t)g * max_seq + p0 + (kvalid ? pk : 0)) * HD + 32 * dq);
-    float4 kv[8];
-#pragma unroll
-    for (int j = 0; j < 8; j++) kv[j] = Kp[j];
-    // V: 64 rows x 32 float4; thread t loads float4 column t % 32 of rows t/32 + 8u
-    const float4* Vg = (const float4*)(vc + ((size_t)g * max_seq + p0) * HD);
-    float4 vv[8];
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int r = (t >> 5) + 8 * u;
-        vv[u] = r < np ? Vg[(size_t)r * (HD / 4) + (t & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    // Q rows: batch row bi holds heads g*hpk.. contiguously (hpk * HD floats)
-    const int lg = 31 - __clz(hpk * (HD / 4));
-    float4 qv[4];
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int e = t + 256 * u, bi = e >> lg, rem = e & ((1 << lg) - 1);
-        qv[u] = e < nq * (HD / 4) ? ((const float4*)q)[((size_t)bi * ldq + (size_t)g * hpk * HD) / 4 + rem]
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-#pragma unroll
-    for (int u = 0; u < 4; u++) ((float4*)Q)[t + 256 * u] = qv[u];
-#pragma unroll
-    for (int u = 0; u < 8; u++) {
-        const int r = (t >> 5) + 8 * u;
-        *(float4*)&V[r][4 * (t & 31)] = vv[u];
-    }
-    __syncthreads();
-    // ---- scores ----
-    const float scale = 1.0f / sqrtf((float)HD);
-    for (int q0 = 0; q0 < nq; q0 += 8) {
-        float acc[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float a = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float4 qq = *(const float4*)&Q[q0 + i][32 * dq + 4 * j];
-                a += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
-            }
-            a += __shfl_xor(a, 16);
-            a += __shfl_xor(a, 32);
-            acc[i] = a;
+    const int b_lo = max(0, p0 - pos0), b_hi = min(a.nb, p0 + C - pos0);
+    const int nw = blockDim.x >> 6;
+    for (int b = b_lo + wave; b < b_hi; b += nw) {
+        const int pos = pos0 + b;
+        const float* xk = a.qkv + (size_t)b * a.ldq + (size_t)(a.nh + g) * HD;
+        const float* xv = a.qkv + (size_t)b * a.ldq + (size_t)(a.nh + a.nkv + g) * HD;
+        const float2 k = head_norm_rope(xk[lane], xk[lane + 64], a.kn, a.rope, pos, a.eps, lane);
+        const float v0 = xv[lane], v1 = xv[lane + 64];
+        if (Kn) {
+            Kn[b][lane] = k.x;
+            Kn[b][lane + 64] = k.y;
+            V[pos - p0][lane] = v0;
+            V[pos - p0][lane + 64] = v1;
         }
-        if (dq == 0) {
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int qi = q0 + i;
-                if (qi < nq) {
-                    const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
-                    S[qi][pk] = see ? acc[i] * scale : -INFINITY;
-                }
-            }
-        }
-    }
-    __syncthreads();
-    // ---- softmax and values: wave w owns queries w, w+4, .. ----
-    const int wv = __builtin_amdgcn_readfirstlane(wave);
-    const int nqw = (nq - wv + 3) >> 2;
-    switch (nqw) {
-        case 0: break;
-        case 1: attn_values<1>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        case 2: attn_values<2>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        case 3: attn_values<3>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        case 4: attn_values<4>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        case 5: attn_values<5>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        case 6: attn_values<6>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        case 7: attn_values<7>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
-        default: attn_values<8>(S, V, wv, lane, hpk, nh, g, c, nch, pm, pl, po); break;
+        float* kd = a.kc + ((size_t)g * a.max_seq + pos) * HD;
+        float* vd = a.vc + ((size_t)g * a.max_seq + pos) * HD;
+        kd[lane] = k.x;
+        kd[lane + 64] = k.y;
+        vd[lane] = v0;
+        vd[lane + 64] = v1;
     }
 }
 
-// Merge the chunk partials of one (row, head): one wave, lanes = chunks for
-// the weights, lanes = dims for the output.  grid (nb * nh).
-__global__ __launch_bounds__(64) void k_attn_merge(const float* __restrict__ pm,
-                                                   const float* __restrict__ pl,
-                                                   const float* __restrict__ po, int nh, int nch,
-                                                   const int* __restrict__ pbase, int padd,
-                                                   float* __restrict__ out) {
+// Merge of the chunk partials of one (batch row b, head h) by one wave:
+// lanes = chunks for the weights exp(m_c - M), lanes = dim pairs for the
+// output sum_c w_c o_c / sum_c w_c l_c.
+__device__ __forceinline__ void attn_merge_row(const float* pm, const float* pl, const float* po, int nch,
+                                               size_t row, int used, float* out) {
     constexpr int HD = 128;
-    const int rh = blockIdx.x, lane = threadIdx.x;
-    const int b = rh / nh;
-    const size_t row = (size_t)rh;  // == b * nh + h
-    const int pos0 = *pbase + padd;
-    const int used = (pos0 + b + ATT_C) / ATT_C;
+    const int lane = threadIdx.x & 63;
     float M = -INFINITY;
     for (int c = lane; c < used; c += 64) M = fmaxf(M, pm[row * nch + c]);
     for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
@@ -395,7 +290,120 @@ __global__ __launch_bounds__(64) void k_attn_merge(const float* __restrict__ pm,
         }
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
-    ((float2*)(out + (size_t)b * nh * HD + (size_t)(rh % nh) * HD))[lane] = make_float2(O.x * inv, O.y * inv);
+    ((float2*)out)[lane] = make_float2(O.x * inv, O.y * inv);
+}
+
+// Merge of the chunk partials, one wave per (row, head): grid nb * nh.
+__global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
+    const int rh = blockIdx.x, b = rh / a.nh;
+    const int used = (*a.pbase + a.padd + b + ATT_C) / ATT_C;
+    attn_merge_row(a.pm, a.pl, a.po, a.nch, (size_t)rh, used, a.out + (size_t)rh * 128);
+}
+
+// Decode attention of one layer for the nb rows at positions pos0 .. pos0+nb-1
+// (pos0 = *pbase + padd), one workgroup per (kv head g, 64-position chunk c):
+//   - q-norm + RoPE of the hpk query heads of g for every row (Q in LDS);
+//   - the chunk's cached K (registers) and V (LDS); the chunk that holds new
+//     positions computes their k-norm + RoPE K and V rows itself, appends
+//     them to the cache and uses them (finish_projection + append);
+//   - scores with the causal limit pos0 + b, chunk softmax and values
+//     (partials m, l, o per row/head/chunk);
+__global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
+    constexpr int HD = 128, C = ATT_C;
+    const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int nh = a.nh, hpk = nh / a.nkv, nq = a.nb * hpk;
+    const int pos0 = *a.pbase + a.padd;
+    const int stored = pos0 + a.nb;
+    const int p0 = c * C;
+    __shared__ __align__(16) float Q[32][HD];
+    __shared__ __align__(16) float V[C][HD + 4];
+    __shared__ __align__(16) float S[32][C];
+    __shared__ __align__(16) float Kn[MAXB][HD];
+    if (!a.attend) {  // KV append only (MTP warm-up)
+        if (p0 < stored) append_rows(a, g, p0, pos0, wave, lane, nullptr, nullptr);
+        return;
+    }
+    if (p0 < stored) {
+        const int np = min(C, stored - p0);
+        const int nold = min(np, max(0, pos0 - p0));  // cached positions of this chunk
+        // cached K: lane = (position pk, dim quarter dq)
+        const int pk = wave * 16 + (lane & 15), dq = lane >> 4;
+        const bool kvalid = pk < np;
+        const float4* Kp = (const float4*)(a.kc + ((size_t)g * a.max_seq + p0 + (pk < nold ? pk : 0)) * HD + 32 * dq);
+        float4 kv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[j] = Kp[j];
+        // cached V: thread t loads float4 column t % 32 of rows t/32 + 8u
+        const float4* Vg = (const float4*)(a.vc + ((size_t)g * a.max_seq + p0) * HD);
+        float4 vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int r = (t >> 5) + 8 * u;
+            vv[u] = r < nold ? Vg[(size_t)r * (HD / 4) + (t & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        // queries: wave per (row, head), rows of qkv hold [q heads | k heads | v heads]
+        for (int qi = wave; qi < nq; qi += 4) {
+            const int b = qi / hpk, h = g * hpk + qi % hpk;
+            const float* x = a.qkv + (size_t)b * a.ldq + (size_t)h * HD;
+            const float2 o = head_norm_rope(x[lane], x[lane + 64], a.qn, a.rope, pos0 + b, a.eps, lane);
+            Q[qi][lane] = o.x;
+            Q[qi][lane + 64] = o.y;
+        }
+        // new rows that fall in this chunk: K and V computed here and appended
+        append_rows(a, g, p0, pos0, wave, lane, Kn, V);
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int r = (t >> 5) + 8 * u;
+            if (r < nold || r >= np) *(float4*)&V[r][4 * (t & 31)] = vv[u];
+        }
+        __syncthreads();
+        if (kvalid && pk >= nold) {
+            const int b = p0 + pk - pos0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) kv[j] = *(const float4*)&Kn[b][32 * dq + 4 * j];
+        }
+        // scores: lanes (pk, dq) reduce their quarter dots over the 4 quarters
+        const float scale = 1.0f / sqrtf((float)HD);
+        for (int q0 = 0; q0 < nq; q0 += 8) {
+            float acc[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float s = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float4 qq = *(const float4*)&Q[q0 + i][32 * dq + 4 * j];
+                    s += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+                }
+                s += __shfl_xor(s, 16);
+                s += __shfl_xor(s, 32);
+                acc[i] = s;
+            }
+            if (dq == 0) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int qi = q0 + i;
+                    if (qi < nq) {
+                        const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
+                        S[qi][pk] = see ? acc[i] * scale : -INFINITY;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const int nqw = (nq - wave + 3) >> 2;
+        switch (nqw) {
+            case 0: break;
+            case 1: attn_values<1>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            case 2: attn_values<2>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            case 3: attn_values<3>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            case 4: attn_values<4>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            case 5: attn_values<5>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            case 6: attn_values<6>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            case 7: attn_values<7>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+            default: attn_values<8>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+        }
+    }
 }
 
 // Preparation of f32 rows for the next GEMV (one workgroup per row).
@@ -521,22 +529,10 @@ void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo
     hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
 }
 
-void launch_qk_rope_append(const float* qkv, int ldq, const float* qn, const float* kn,
-                           const float2* rope, int nh, int nkv, int hd, double eps, const int* pbase,
-                           int padd, float* kc, float* vc, int max_seq, float* qout, int ldqo, int nb,
-                           hipStream_t st) {
-    hipLaunchKernelGGL(k_qk_rope_append, dim3(nb, nh + 2 * nkv), dim3(hd), 0, st, qkv, ldq, qn, kn,
-                       rope, nh, nkv, hd, eps, pbase, padd, kc, vc, max_seq, qout, ldqo);
-}
-
-void launch_attention(const float* q, int ldq, const float* kc, const float* vc, int max_seq, int nb,
-                      int nh, int nkv, const int* pbase, int padd, int max_len, float* pm, float* pl,
-                      float* po, int nch_cap, float* out_f32, hipStream_t st) {
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st) {
     const int nch = (max_len + ATT_C - 1) / ATT_C;
-    hipLaunchKernelGGL(k_attn_partial, dim3(nkv, nch), dim3(256), 0, st, q, ldq, kc, vc, max_seq, nb, nh, nkv,
-                       pbase, padd, pm, pl, po, nch_cap);
-    hipLaunchKernelGGL(k_attn_merge, dim3(nb * nh), dim3(64), 0, st, pm, pl, po, nh, nch_cap, pbase, padd,
-                       out_f32);
+    hipLaunchKernelGGL(k_attention, dim3(a.nkv, nch), dim3(256), 0, st, a);
+    if (a.attend) hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
 }
 
 void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,
