@@ -45,9 +45,6 @@ struct cmf_model_s {
     // scratch
     float *hv = nullptr, *hm = nullptr, *attn_out = nullptr, *ffn_out = nullptr, *qkv_out = nullptr,
           *qrot = nullptr, *ao = nullptr, *xrows = nullptr, *hm2 = nullptr, *gu_out = nullptr, *logits = nullptr;
-    uint8_t* planes = nullptr;
-    size_t planes_cap = 0;
-    float* xs = nullptr;
     float *pm = nullptr, *pl = nullptr, *po = nullptr;
     int nch_cap = 0;
     float* am_v = nullptr;
@@ -127,15 +124,6 @@ int build_cat(DevWeight& w, const std::vector<const cmf_tensor*>& ts) {
     Q4Src s;
     for (auto* t : ts) fill_q4src(s, dt, t->rows, cols, t->bytes, 0);
     return build_q4(w, s);
-}
-
-PrepDst prep_for(cmf_model_s* m, const DevWeight& w) {
-    PrepDst d;
-    d.kind = w.dtype == DT_Q8ROW ? 8 : 16;
-    d.nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
-    d.planes = m->planes;
-    d.xs = m->xs;
-    return d;
 }
 
 int upload_layer(cmf_model_s* m, LayerDev& l, const cmf_layer_desc* d, bool kv) {
@@ -299,16 +287,12 @@ int alloc_scratch(cmf_model_s* m) {
         dalloc_t(m, &m->qkv_out, (size_t)MAXB * QKV) || dalloc_t(m, &m->qrot, (size_t)MAXB * c.n_heads * hd) || dalloc_t(m, &m->ao, (size_t)MAXB * c.n_heads * hd) ||
         dalloc_t(m, &m->xrows, (size_t)MAXB * std::max(std::max(2 * H, c.inter), c.n_heads * hd)) ||
         dalloc_t(m, &m->hm2, (size_t)MAXB * H) ||
-        dalloc_t(m, &m->gu_out, (size_t)MAXB * 2 * c.inter) || dalloc_t(m, &m->xs, 64) ||
+        dalloc_t(m, &m->gu_out, (size_t)MAXB * 2 * c.inter) ||
         dalloc_t(m, &m->pm, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->pl, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->po, (size_t)MAXB * c.n_heads * m->nch_cap * hd) ||
         dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H))
         return CMF_ERR;
-    // planes large enough for every weight the model uses: q8 K <= max(H, nh*hd, 2H) ; q4 K <= max(H, I)
-    const int kmax = std::max(std::max(2 * H, c.n_heads * hd), c.inter);
-    m->planes_cap = (size_t)((kmax + 127) / 128) * 4 * 1024 * 3;
-    if (dalloc(m, (void**)&m->planes, m->planes_cap)) return CMF_ERR;
     // rope table (cos, sin) per (position, freq) with the host libm, as
     // rope_rotate (attention.rs:71-81) evaluates it
     const int half = hd / 2;

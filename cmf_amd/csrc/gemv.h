@@ -47,6 +47,14 @@ struct GemvArgs {
     XSrc src;
 };
 
+// Kernel instance for m batch rows, operand source xm (0: prepared planes
+// staged in LDS, 1: fused producer staged in LDS, 2: prepared planes read in
+// place) and ks waves per workgroup (nullptr: none).
+typedef void (*GemvKernel)(GemvArgs);
+GemvKernel q4t_kernel(int m, int xm, int ks);
+GemvKernel q4tp_kernel(int m, int xm, int ks);
+GemvKernel q8_kernel(int m, int xm, int ks);
+
 // y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m.
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
          bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0);
@@ -60,17 +68,17 @@ int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* pla
 int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
                 int m, int row_lo, int row_hi, hipStream_t st, int ks_override = 0);
 
-// Writes batch row b of the q8 activation planes: three int8 planes with
-// x ~= sx * (q0 + q1/128 + q2/16384), sx = max|x|/127, lane order
-// [chunk of 64][lane 16*s + b][16 bytes of columns 64c + 16s ..].
-__device__ inline void prep8_row(const float* x, int K, float amax, int nk, int b,
+// Writes batch row b (of M) of the q8 activation planes: three int8 planes
+// with x ~= sx * (q0 + q1/128 + q2/16384), sx = max|x|/127, each plane
+// [item = 4*chunk + s][b] x 16 bytes of columns 64*chunk + 16*s ...
+__device__ inline void prep8_row(const float* x, int K, float amax, int nk, int b, int M,
                                  uint8_t* planes, float* xs, int tid, int nthr) {
     const float sx = amax > 0.f ? amax / 127.0f : 1.0f;
     const float inv = 1.0f / sx;
     if (tid == 0) xs[b] = sx;
     uint8_t* p0 = planes;
-    uint8_t* p1 = planes + (size_t)nk * 1024;
-    uint8_t* p2 = planes + (size_t)nk * 2048;
+    uint8_t* p1 = planes + (size_t)nk * 64 * M;
+    uint8_t* p2 = planes + (size_t)nk * 128 * M;
     for (int idx = tid; idx < nk * 4; idx += nthr) {
         const int kc = idx >> 2, s = idx & 3, c0 = kc * 64 + 16 * s;
         uint32_t w0[4], w1[4], w2[4];
@@ -94,24 +102,24 @@ __device__ inline void prep8_row(const float* x, int K, float amax, int nk, int 
             w1[q] = bb;
             w2[q] = c;
         }
-        const size_t off = ((size_t)kc * 64 + 16 * s + b) * 16;
+        const size_t off = ((size_t)idx * M + b) * 16;
         *(uint4*)(p0 + off) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
         *(uint4*)(p1 + off) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
         *(uint4*)(p2 + off) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
     }
 }
 
-// Writes batch row b of the q4 activation planes: f16 hi/lo of x*2^e with
-// max|x*2^e| < 2^15, xs[b] = 2^-e, lane order [tile][16*s + b][8 halves of
-// columns 32t + 8s + {0,2,4,6,1,3,5,7}].
-__device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b,
+// Writes batch row b (of M) of the q4 activation planes: f16 hi/lo of x*2^e
+// with max|x*2^e| < 2^15, xs[b] = 2^-e, each plane [item = 4*tile + s][b] x
+// 8 halves of columns 32*tile + 8*s + {0,2,4,6,1,3,5,7}.
+__device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b, int M,
                                   uint8_t* planes, float* xs, int tid, int nthr) {
     int ex = 0;
     if (amax > 0.f) frexpf(amax, &ex);
     const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
     if (tid == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
     uint8_t* ph = planes;
-    uint8_t* pl = planes + (size_t)ntiles * 1024;
+    uint8_t* pl = planes + (size_t)ntiles * 64 * M;
     const int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
     for (int idx = tid; idx < ntiles * 4; idx += nthr) {
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
@@ -125,7 +133,7 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
         }
-        const size_t off = ((size_t)t * 64 + 16 * s + b) * 16;
+        const size_t off = ((size_t)idx * M + b) * 16;
         *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),

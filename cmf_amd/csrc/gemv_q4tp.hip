@@ -1,0 +1,6 @@
+// q4tp GEMV kernel instances (k_gemv_q4, gemv_kern.h).
+#include "gemv_kern.h"
+
+namespace cmf {
+GemvKernel q4tp_kernel(int m, int xm, int ks) { return q4_pick<DT_Q4TP>(m, xm, ks); }
+}  // namespace cmf

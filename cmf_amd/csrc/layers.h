@@ -8,7 +8,8 @@ namespace cmf {
 
 constexpr int ATT_C = 64;  // key positions per attention workgroup
 
-// Where a producer writes its prepared activations (see gemv.h).
+// Where a producer writes its prepared activations (layout: prep8_row /
+// prep16_row); the batch size is the producer's grid size.
 struct PrepDst {
     int kind;         // 8 (q8 weights) or 16 (q4t / q4tp weights)
     int nk;           // q8: chunks of 64 columns; q4: tiles of 32 columns
@@ -17,12 +18,6 @@ struct PrepDst {
 };
 
 
-void launch_add_rmsnorm_prep(float* h, int ldh, const float* delta, int ldd, const float* w, int H,
-                             double eps, const PrepDst& d, float* out, int ldo, int nb,
-                             hipStream_t st);
-void launch_mtp_cat_prep(const int* toks, const float* hid, int ldh, const EmbedSrc& e,
-                         const float* enorm, const float* hnorm, int H, double eps, const PrepDst& d,
-                         int nb, hipStream_t st);
 void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
                   hipStream_t st);
 // One layer's decode attention (head_dim 128): q/k-norm + RoPE, KV append,

@@ -1,7 +1,7 @@
-// Decode-layer kernels around the GEMVs: fused residual-add + RMSNorm +
-// activation preparation, qk-norm + RoPE + KV append, split-K decode
-// attention over the appended KV (causal inside the verify block), merge +
-// preparation, SwiGLU + preparation, embedding gather and argmax.
+// Decode-layer kernels around the GEMVs: qk-norm + RoPE + KV append, split-K
+// decode attention over the appended KV (causal inside the verify block),
+// merge, SwiGLU + operand preparation (standalone FFN seam op), embedding
+// gather and argmax.
 //
 // Semantics follow the reference CPU path:
 //   rms_norm_into / add_rmsnorm_fused_into   inference.rs:33-86
@@ -44,91 +44,8 @@ __device__ inline float block_max_f(float v, float* red) {
 }
 
 __device__ inline void prep_any(const float* vals, int K, float amax, const PrepDst& d, int b) {
-    if (d.kind == 8) prep8_row(vals, K, amax, d.nk, b, d.planes, d.xs, threadIdx.x, blockDim.x);
-    else prep16_row(vals, K, amax, d.nk, b, d.planes, d.xs, threadIdx.x, blockDim.x);
-}
-
-// h[b] (+= delta[b]); out = rms_norm(h[b]) * w, prepared for the next GEMV.
-// One workgroup per batch row; H <= 8192.
-__global__ __launch_bounds__(256) void k_add_rmsnorm_prep(float* __restrict__ h, int ldh,
-                                                          const float* __restrict__ delta, int ldd,
-                                                          const float* __restrict__ w, int H,
-                                                          double eps, PrepDst dst,
-                                                          float* __restrict__ out_f32, int ldo) {
-    const int b = blockIdx.x;
-    __shared__ float vals[8192];
-    __shared__ double redd[4];
-    __shared__ float redf[4];
-    float* hr = h + (size_t)b * ldh;
-    double ss = 0.0;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        float v = hr[i];
-        if (delta) {
-            v = v + delta[(size_t)b * ldd + i];
-            hr[i] = v;
-        }
-        vals[i] = v;
-        ss += (double)v * (double)v;
-    }
-    ss = block_sum_d(ss, redd);
-    const float inv = 1.0f / (float)sqrt(ss / (double)H + eps);
-    float am = 0.f;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        const float o = vals[i] * inv * w[i];
-        vals[i] = o;
-        am = fmaxf(am, fabsf(o));
-        if (out_f32) out_f32[(size_t)b * ldo + i] = o;
-    }
-    am = block_max_f(am, redf);
-    __syncthreads();
-    prep_any(vals, H, am, dst, b);
-}
-
-// MTP input: cat = [rms_norm(embed(tok), enorm) ; rms_norm(hid, hnorm)]
-// (embedding first, pipeline.rs:3085-3094), prepared for eh_proj.
-__global__ __launch_bounds__(256) void k_mtp_cat_prep(const int* __restrict__ toks,
-                                                      const float* __restrict__ hid, int ldh,
-                                                      EmbedSrc emb, const float* __restrict__ enorm,
-                                                      const float* __restrict__ hnorm, int H,
-                                                      double eps, PrepDst dst) {
-    const int b = blockIdx.x;
-    __shared__ float vals[8192];
-    __shared__ double redd[4];
-    __shared__ float redf[4];
-    const int tok = toks[b];
-    const bool ok = tok >= 0 && tok < emb.rows;
-    const float rs = ok ? emb.rs[tok] : 0.f;
-    const int rb = tok >> 4, r = tok & 15;
-    double s1 = 0.0, s2 = 0.0;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        float e = 0.f;
-        if (ok) {
-            const int kc = i >> 6, s = (i >> 4) & 3, j = i & 15;
-            const int8_t q = emb.w[(((size_t)rb * emb.nkc + kc) * 64 + 16 * s + r) * 16 + j];
-            e = (float)q * rs;
-        }
-        const float hv = hid[(size_t)b * ldh + i];
-        vals[i] = e;
-        vals[H + i] = hv;
-        s1 += (double)e * (double)e;
-        s2 += (double)hv * (double)hv;
-    }
-    s1 = block_sum_d(s1, redd);
-    __syncthreads();
-    s2 = block_sum_d(s2, redd);
-    const float i1 = 1.0f / (float)sqrt(s1 / (double)H + eps);
-    const float i2 = 1.0f / (float)sqrt(s2 / (double)H + eps);
-    float am = 0.f;
-    for (int i = threadIdx.x; i < H; i += blockDim.x) {
-        const float a = vals[i] * i1 * enorm[i];
-        const float c = vals[H + i] * i2 * hnorm[i];
-        vals[i] = a;
-        vals[H + i] = c;
-        am = fmaxf(am, fmaxf(fabsf(a), fabsf(c)));
-    }
-    am = block_max_f(am, redf);
-    __syncthreads();
-    prep_any(vals, 2 * H, am, dst, b);
+    if (d.kind == 8) prep8_row(vals, K, amax, d.nk, b, gridDim.x, d.planes, d.xs, threadIdx.x, blockDim.x);
+    else prep16_row(vals, K, amax, d.nk, b, gridDim.x, d.planes, d.xs, threadIdx.x, blockDim.x);
 }
 
 // Embedding rows from the (tied) q8 lm_head: out[b] = q8 row * row_scale
@@ -406,23 +323,6 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     }
 }
 
-// Preparation of f32 rows for the next GEMV (one workgroup per row).
-__global__ __launch_bounds__(256) void k_rows_prep(const float* __restrict__ x, int ldx, int K,
-                                                   PrepDst dst) {
-    const int b = blockIdx.x;
-    __shared__ float vals[8192];
-    __shared__ float redf[4];
-    float am = 0.f;
-    for (int i = threadIdx.x; i < K; i += blockDim.x) {
-        const float v = x[(size_t)b * ldx + i];
-        vals[i] = v;
-        am = fmaxf(am, fabsf(v));
-    }
-    am = block_max_f(am, redf);
-    __syncthreads();
-    prep_any(vals, K, am, dst, b);
-}
-
 // SwiGLU on the fused gate/up output gu[b] = [g (I) ; u (I)], prepared for
 // the down projection.  grid (nb), block 256; I <= 12288.
 __global__ __launch_bounds__(256) void k_silu_mul_prep(const float* __restrict__ gu, int ldg, int I,
@@ -510,20 +410,6 @@ __global__ void k_argmax_final(const float* __restrict__ pv, const int* __restri
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-void launch_add_rmsnorm_prep(float* h, int ldh, const float* delta, int ldd, const float* w, int H,
-                             double eps, const PrepDst& d, float* out, int ldo, int nb,
-                             hipStream_t st) {
-    hipLaunchKernelGGL(k_add_rmsnorm_prep, dim3(nb), dim3(256), 0, st, h, ldh, delta, ldd, w, H, eps,
-                       d, out, ldo);
-}
-
-void launch_mtp_cat_prep(const int* toks, const float* hid, int ldh, const EmbedSrc& e,
-                         const float* enorm, const float* hnorm, int H, double eps, const PrepDst& d,
-                         int nb, hipStream_t st) {
-    hipLaunchKernelGGL(k_mtp_cat_prep, dim3(nb), dim3(256), 0, st, toks, hid, ldh, e, enorm, hnorm,
-                       H, eps, d);
-}
-
 void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
                   hipStream_t st) {
     hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
