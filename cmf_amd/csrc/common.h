@@ -52,18 +52,6 @@ struct DevWeight {
     int device = 0;
 };
 
-// Prepared activations for the q8 kernel: three int8 planes (x ~= sx * (q0 +
-// q1/128 + q2/16384)) in the MFMA A-operand lane order, [kchunk][64][16 B].
-// For the q4 kernels: f16 hi/lo planes of x * 2^e in the A-operand lane order
-// [tile][64][8 halves] with the in-slot order {0,2,4,6,1,3,5,7}.
-struct XPrep {
-    int kind = 0;      // 8 or 16
-    int m = 0;         // batch rows (<= 16)
-    int kchunks = 0;   // q8 chunks of 64 / q4 tiles of 32
-    uint8_t* planes = nullptr;
-    float* scale = nullptr;  // [16]: q8 sx ; q4 2^-e
-};
-
 constexpr int MAXB = 16;  // largest batch a GEMV launch serves
 
 }  // namespace cmf

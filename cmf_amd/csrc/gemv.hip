@@ -134,7 +134,8 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
             return fail("gemv: fused operand needs K, H, ldx multiples of 4, a 16-byte aligned row base and K <= 16384");
         lds += lds_scratch(w, m);
     }
-    if (lds > LDSX_MAX) {
+    static const int xg_rows = env_int("CMF_GEMV_XGLOBAL_M", 99);
+    if (lds > LDSX_MAX || (!fu && m >= xg_rows)) {
         if (fu) return fail("gemv: activation operand exceeds LDS; prepare it globally");
         lds = 0;  // planes read in place from global memory
     }

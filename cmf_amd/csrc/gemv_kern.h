@@ -303,6 +303,27 @@ __device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, u
     __syncthreads();
 }
 
+// Prepared planes go to LDS by direct global->LDS loads (no registers),
+// issued before the weight stream: the loads of a wave complete in order, so
+// the operand is in LDS once at most the weight loads issued after it are
+// outstanding (vmcnt).  Wave w copies 1 KiB chunks w, w + nw, ... (indices
+// clamped to the last item, so the copy never reads past the planes).
+__device__ __forceinline__ void x_dma(const XSrc& s, int n, uint8_t* lx) {
+    const uint4* g = (const uint4*)s.planes;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    for (int c = wave; c * 64 < n; c += nw)
+        __builtin_amdgcn_global_load_lds((const void*)(g + min(c * 64 + lane, n - 1)),
+                                         (__attribute__((address_space(3))) void*)(lx + c * 1024), 16, 0, 0);
+}
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
+// expcnt 6:4 left at 7, lgkmcnt 11:8)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+
 // ---------------------------------------------------------------------------
 // q4t / q4tp
 // ---------------------------------------------------------------------------
@@ -334,26 +355,30 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     const int P = (ntg + KS * SP - 1) / (KS * SP);  // K parts per row block
     int rb = blockIdx.x, kp = 0;
     if (rb >= a.nrb) return;  // uniform over the workgroup
-    auto load = [&](uint4* wv, uint2* sv, int rbl, int kpl) {
+    // weights + tile scales of a unit (q4tp: and the row ladder parameters
+    // of its row block), all unconditional (steps past the row clamped to
+    // its last one): a load under a branch makes the compiler wait for it
+    // at once.  NL = loads per call.
+    constexpr int NL = 2 * SP + (TP ? 1 : 0);
+    auto load = [&](uint4* wv, uint2* sv, float2& pv, int rbl, int kpl) {
         const size_t wbase = (size_t)(a.rb0 + rbl) * ntg;
         const int t0 = kpl * KS * SP + wave * SP;
 #pragma unroll
         for (int u = 0; u < SP; u++) {
-            if (t0 + u < ntg) {
-                wv[u] = ((const uint4*)a.w)[(wbase + t0 + u) * 64 + lane];
-                if constexpr (TP) sv[u] = make_uint2(((const uint32_t*)a.scale)[(wbase + t0 + u) * 16 + r], 0u);
-                else sv[u] = ((const uint2*)a.scale)[(wbase + t0 + u) * 16 + r];
-            }
+            const size_t t = wbase + min(t0 + u, ntg - 1);
+            wv[u] = ((const uint4*)a.w)[t * 64 + lane];
+            if constexpr (TP) sv[u] = make_uint2(((const uint32_t*)a.scale)[t * 16 + r], 0u);
+            else sv[u] = ((const uint2*)a.scale)[t * 16 + r];
         }
+        if constexpr (TP) pv = a.rowp[(a.rb0 + rbl) * 16 + r];
     };
-    // the 32-rung ladder of each row of row block rbl: t[c] = t[c-1] * ratio
+    // the 32-rung ladder of each row of a row block: t[c] = t[c-1] * ratio
     // (quant.rs:399-410), by 16 threads of the second wave (the first one
     // reduces meanwhile)
-    auto ladder = [&](int buf, int rbl) {
+    auto ladder = [&](int buf, float2 p) {
         if constexpr (TP) {
             const int lt = (int)threadIdx.x - (KS > 1 ? 64 : 0);
             if (lt >= 0 && lt < 16) {
-                const float2 p = a.rowp[(a.rb0 + rbl) * 16 + lt];
                 float tv = p.x;
                 lad[buf][lt * 33] = tv;
                 for (int c = 1; c < 32; c++) {
@@ -365,10 +390,24 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     };
     uint4 wA[SP], wB[SP];
     uint2 sA[SP], sB[SP];
-    load(wA, sA, rb, 0);
-    ladder(0, rb);
-    if constexpr (XM != XM_GLOBAL) stage_x<XM == XM_FUSED>(a.src, M, FMT, ntg * 4, smem, lxs);
-    else if (threadIdx.x < 16) lxs[threadIdx.x] = a.src.xs[threadIdx.x];
+    float2 pA{}, pB{};
+    float xsv = 0.f;
+    if constexpr (XM == XM_PREP) {
+        x_dma(a.src, ntg * 16 * M * 2, smem);  // hi + lo planes
+        xsv = a.src.xs[threadIdx.x & 15];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load(wA, sA, pA, rb, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XM == XM_PREP) {
+        wait_vmcnt<NL>();  // operand planes and xs are in
+        if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
+    } else if constexpr (XM == XM_FUSED) {
+        stage_x<true>(a.src, M, FMT, ntg * 4, smem, lxs);
+    } else if (threadIdx.x < 16) {
+        lxs[threadIdx.x] = a.src.xs[threadIdx.x];
+    }
+    ladder(0, pA);
     __syncthreads();
     // operand planes [item][b] x 16 B, hi then lo: in LDS, or read in place
     const uint4* LH = XM != XM_GLOBAL ? (const uint4*)smem : (const uint4*)a.src.planes;
@@ -383,7 +422,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     int buf = 0;
 
     // one work unit: rb/kp current, rn/kn the next one (rn >= nrb: none)
-    auto process = [&](const uint4* wv, const uint2* sv, int rn) {
+    auto process = [&](const uint4* wv, const uint2* sv, const float2& pn, int rn) {
         const int t0 = kp * KS * SP + wave * SP;
 #pragma unroll
         for (int u = 0; u < SP; u++) {
@@ -453,7 +492,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
             }
         }
         acc = zero;
-        if (rn < a.nrb) ladder(buf ^ 1, rn);
+        if (rn < a.nrb) ladder(buf ^ 1, pn);
         buf ^= 1;
         if constexpr (KS > 1 || TP) __syncthreads();
     };
@@ -464,8 +503,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
             kn = 0;
             rn += gridDim.x;
         }
-        if (rn < a.nrb) load(wB, sB, rn, kn);
-        process(wA, sA, rn);
+        __builtin_amdgcn_sched_barrier(0);  // next unit's loads go out before this unit's compute
+        if (rn < a.nrb) load(wB, sB, pB, rn, kn);
+        __builtin_amdgcn_sched_barrier(0);
+        process(wA, sA, pB, rn);
         if (rn >= a.nrb) break;
         rb = rn;
         kp = kn;
@@ -474,8 +515,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
             kn = 0;
             rn += gridDim.x;
         }
-        if (rn < a.nrb) load(wA, sA, rn, kn);
-        process(wB, sB, rn);
+        __builtin_amdgcn_sched_barrier(0);
+        if (rn < a.nrb) load(wA, sA, pA, rn, kn);
+        __builtin_amdgcn_sched_barrier(0);
+        process(wB, sB, pA, rn);
         if (rn >= a.nrb) break;
         rb = rn;
         kp = kn;
@@ -504,14 +547,27 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
     auto load = [&](int4v* wv, int rbl, int kpl) {
         const size_t wbase = (size_t)(a.rb0 + rbl) * nkc;
         const int c0 = kpl * KS * SP + wave * SP;
+        // unconditional loads (steps past the row clamped to its last one)
 #pragma unroll
-        for (int u = 0; u < SP; u++)
-            if (c0 + u < nkc) wv[u] = ((const int4v*)a.w)[(wbase + c0 + u) * 64 + lane];
+        for (int u = 0; u < SP; u++) wv[u] = ((const int4v*)a.w)[(wbase + min(c0 + u, nkc - 1)) * 64 + lane];
     };
     int4v wA[SP], wB[SP];
+    float xsv = 0.f;
+    if constexpr (XM == XM_PREP) {
+        x_dma(a.src, nkc * 4 * M * 3, smem);  // three planes
+        xsv = a.src.xs[threadIdx.x & 15];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     load(wA, rb, 0);
-    if constexpr (XM != XM_GLOBAL) stage_x<XM == XM_FUSED>(a.src, M, DT_Q8ROW, nkc, smem, lxs);
-    else if (threadIdx.x < 16) lxs[threadIdx.x] = a.src.xs[threadIdx.x];
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (XM == XM_PREP) {
+        wait_vmcnt<SP>();  // operand planes and xs are in
+        if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
+    } else if constexpr (XM == XM_FUSED) {
+        stage_x<true>(a.src, M, DT_Q8ROW, nkc, smem, lxs);
+    } else if (threadIdx.x < 16) {
+        lxs[threadIdx.x] = a.src.xs[threadIdx.x];
+    }
     __syncthreads();
     // operand planes [item][b] x 16 B, q0 q1 q2: in LDS, or read in place
     const int lpl = nkc * 4 * M;
@@ -612,7 +668,9 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
             kn = 0;
             rn += gridDim.x;
         }
+        __builtin_amdgcn_sched_barrier(0);  // next unit's loads go out before this unit's compute
         if (rn < a.nrb) load(wB, rn, kn);
+        __builtin_amdgcn_sched_barrier(0);
         process(wA);
         if (rn >= a.nrb) break;
         rb = rn;
@@ -622,7 +680,9 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
             kn = 0;
             rn += gridDim.x;
         }
+        __builtin_amdgcn_sched_barrier(0);
         if (rn < a.nrb) load(wA, rn, kn);
+        __builtin_amdgcn_sched_barrier(0);
         process(wB);
         if (rn >= a.nrb) break;
         rb = rn;
