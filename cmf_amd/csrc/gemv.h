@@ -109,9 +109,26 @@ __device__ inline void prep8_row(const float* x, int K, float amax, int nk, int 
     }
 }
 
-// Writes batch row b (of M) of the q4 activation planes: f16 hi/lo of x*2^e
-// with max|x*2^e| < 2^15, xs[b] = 2^-e, each plane [item = 4*tile + s][b] x
-// 8 halves of columns 32*tile + 8*s + {0,2,4,6,1,3,5,7}.
+// Bias of one tile for the denormal-nibble MFMA: the kernels multiply
+// x by n * 2^-24 (n = 0..15, an f16 denormal) and start the accumulator at
+// -8 * 2^-24 * sum(x) of the tile, so that D = 2^-24 * sum((n - 8) * x).
+// x here is the tile's 32 operand values as the MFMA sees them (f16 hi + lo).
+__device__ inline float q4_tile_bias(const float* x, int K, int col0, float scale) {
+    float sum = 0.f;
+    for (int j = 0; j < 32; j++) {
+        const float v = col0 + j < K ? x[col0 + j] * scale : 0.f;
+        const _Float16 h = (_Float16)v;
+        const _Float16 l = (_Float16)(v - (float)h);
+        sum += (float)h + (float)l;
+    }
+    return sum * -4.76837158203125e-07f;  // -8 * 2^-24
+}
+
+// Writes batch row b (of M) of the q4 activation operand: f16 hi/lo of
+// x*2^e with max|x*2^e| < 2^15, xs[b] = 2^-e, planes [item = 4*tile + s][b]
+// x 8 halves of columns 32*tile + 8*s + {0,4,2,6,1,5,3,7} (hi plane, then lo
+// plane), then the tile biases [tile][16] f32 (q4_tile_bias at [tile][b],
+// zero for rows >= M; the workgroup of row 0 writes those zeros).
 __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b, int M,
                                   uint8_t* planes, float* xs, int tid, int nthr) {
     int ex = 0;
@@ -120,7 +137,8 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
     if (tid == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
     uint8_t* ph = planes;
     uint8_t* pl = planes + (size_t)ntiles * 64 * M;
-    const int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    float* bias = (float*)(planes + (size_t)ntiles * 128 * M);
+    const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
     for (int idx = tid; idx < ntiles * 4; idx += nthr) {
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
         uint16_t hv[8], lv[8];
@@ -138,6 +156,11 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
                                          lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
+    }
+    for (int t = tid; t < ntiles; t += nthr) {
+        bias[t * 16 + b] = q4_tile_bias(x, K, t * 32, scale);
+        if (b == 0)
+            for (int r = M; r < 16; r++) bias[t * 16 + r] = 0.f;
     }
 }
 

@@ -34,7 +34,8 @@ __global__ __launch_bounds__(256) void k_prep(const float* __restrict__ X, int l
 // ---------------------------------------------------------------------------
 size_t prep_bytes(const DevWeight& w) {
     // at most 16 batch rows: q8 3 planes of nk*64*16 B ; q4 2 planes of ntiles*64*16 B
-    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 1024 * 3 : (size_t)w.kchunks * 4 * 1024 * 2;
+    // (+ q4 tile biases [tile][16] f32)
+    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 1024 * 3 : (size_t)w.kchunks * 4 * (1024 * 2 + 64);
 }
 
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
@@ -46,7 +47,8 @@ int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* pla
 }
 
 static size_t lds_bytes(const DevWeight& w, int m) {
-    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 128 * 4 * m;
+    // q4: hi + lo planes and the tile biases [tile][16] f32
+    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 4 * (128 * m + 64);
 }
 // plus the f32 scratch of the in-kernel producers: the m raw rows and the
 // norm weights
@@ -134,8 +136,7 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
             return fail("gemv: fused operand needs K, H, ldx multiples of 4, a 16-byte aligned row base and K <= 16384");
         lds += lds_scratch(w, m);
     }
-    static const int xg_rows = env_int("CMF_GEMV_XGLOBAL_M", 99);
-    if (lds > LDSX_MAX || (!fu && m >= xg_rows)) {
+    if (lds > LDSX_MAX) {
         if (fu) return fail("gemv: activation operand exceeds LDS; prepare it globally");
         lds = 0;  // planes read in place from global memory
     }
@@ -148,8 +149,7 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
     const int threads = 64 * ks;
     const int occ = resident_per_cu(k, threads, lds);
     if (occ < 1) return fail("gemv: kernel does not fit a CU (LDS or registers)");
-    static const int wgpcu = env_int("CMF_GEMV_WGPCU", 0);
-    int grid = std::min(a.nrb, (wgpcu > 0 ? std::min(occ, wgpcu) : occ) * num_cus());
+    int grid = std::min(a.nrb, occ * num_cus());
     if (grid_override > 0) grid = std::min(grid_override, a.nrb);
     void* args[] = {&a};
     CMF_HIP(hipLaunchKernel((const void*)k, dim3(grid), dim3(threads), args, lds, st));

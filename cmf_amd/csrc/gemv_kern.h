@@ -2,21 +2,25 @@
 //
 // y[b][r] = sum_k W[r][k] * x[b][k] for b < M <= 16 and the three weight
 // codecs of the engine (q8 per-row, q4_tiled, q4tp).  Work split:
-//   - a workgroup of KS waves owns one block of 16 weight rows at a time and
-//     walks row blocks with a grid stride (persistent); its waves split K
-//     and reduce in LDS in a fixed order (deterministic);
+//   - a workgroup of KS waves owns one block of 16 weight rows at a time
+//     (the grid is sized to what the CUs hold at once, so one block per
+//     workgroup unless the matrix is taller); its waves split K and reduce
+//     in LDS in a fixed order (deterministic);
 //   - every wave streams 1 KiB of packed weights per step with one 128-bit
-//     load per lane, a whole K share in flight before the first MFMA;
+//     load per lane, its whole K share (SP steps) requested at once;
 //   - the activations are the MFMA A operand (16 batch rows, zero-padded),
 //     the weights the B operand (16 weight rows):
 //       q8  : v_mfma_i32_16x16x64_i8 on the raw int8 weights; x is carried
 //             as three int8 planes, x ~= sx*(q0 + q1/128 + q2/16384)
 //             (|error| <= 2^-22 max|x|), each summed exactly in int32;
 //       q4* : v_mfma_f32_16x16x32_f16, one tile (32 columns, one scale) per
-//             MFMA; nibbles become exact f16 (n - 8) in registers and x is
-//             carried as f16 hi + lo of x*2^e (22-bit significand).  Each
-//             tile's product is scaled by its tile scale and accumulated in
-//             f32, as q4t_row_exact does (qtensor.rs:4418-4432).
+//             MFMA; nibbles become the exact f16 denormals n * 2^-24 in
+//             registers (one mask per pair), the format's -8 offset enters
+//             as the accumulator input -8 * 2^-24 * sum(x) of the tile, and
+//             x is carried as f16 hi + lo of x*2^e (22-bit significand).
+//             Each tile's product is scaled by its tile scale and
+//             accumulated in f32, as q4t_row_exact does
+//             (qtensor.rs:4418-4432).
 //   - the activation operand is built once per workgroup into LDS from its
 //     producer (RMSNorm of the residual rows, SwiGLU of the gate/up rows,
 //     plain rows, the MTP [enorm(embed); hnorm(h)] concat, or a prepared
@@ -37,23 +41,17 @@ typedef int int4v __attribute__((ext_vector_type(4)));
 
 constexpr int LDSX_MAX = 128 * 1024;  // largest LDS-staged activation operand (+ scratch)
 
-// Four nibble bytes (8 weights: elements 8s..8s+7 of a tile) to exact f16
-// (n - 8) in the in-slot order {0,2,4,6,1,3,5,7}: v_perm_b32 places each
-// nibble byte under the exponent byte 0x64 (f16 1024 + n), one packed f16
-// subtract of 1032 per pair.
+// Four nibble bytes (8 weights: elements 8s..8s+7 of a tile) to the f16
+// denormals n * 2^-24 (exact, the raw nibble under a zero exponent) in the
+// in-slot order {0,4,2,6,1,5,3,7}: one mask (and shift) per pair.  The -8
+// offset of the format enters through the MFMA accumulator (q4_tile_bias).
 __device__ __forceinline__ half8 dq_nib_word(uint32_t w) {
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    constexpr uint32_t E = 0x64646464u;
-    const uint32_t p0 = __builtin_amdgcn_perm(E, lo, 0x04010400u);  // elements 0, 2
-    const uint32_t p1 = __builtin_amdgcn_perm(E, lo, 0x04030402u);  // 4, 6
-    const uint32_t p2 = __builtin_amdgcn_perm(E, hi, 0x04010400u);  // 1, 3
-    const uint32_t p3 = __builtin_amdgcn_perm(E, hi, 0x04030402u);  // 5, 7
-    const half2v off = {(_Float16)1032.0f, (_Float16)1032.0f};
-    const half2v a = __builtin_bit_cast(half2v, p0) - off;
-    const half2v b = __builtin_bit_cast(half2v, p1) - off;
-    const half2v c = __builtin_bit_cast(half2v, p2) - off;
-    const half2v d = __builtin_bit_cast(half2v, p3) - off;
-    return half8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+    constexpr uint32_t K = 0x000F000Fu;
+    const uint32_t p0 = w & K;          // elements 0, 4
+    const uint32_t p1 = (w >> 8) & K;   // 2, 6
+    const uint32_t p2 = (w >> 4) & K;   // 1, 5
+    const uint32_t p3 = (w >> 12) & K;  // 3, 7
+    return __builtin_bit_cast(half8, make_uint4(p0, p1, p2, p3));
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
@@ -176,7 +174,8 @@ __device__ __forceinline__ void unit_phase1(const XSrc& s, int u, int S, int K4,
 //   phase 2 (RMSNorm producers): inv = 1/sqrt(mean + eps) from the unit sums
 //            in a fixed order, x = (raw * inv) * w in place, per-unit max|x|;
 //   phase 3: operand planes, one 16-byte item per thread step:
-//     q4: hi plane then lo plane, [tile*4 + s][b] x 16 B; lxs[b] = 2^-e
+//     q4: hi plane then lo plane, [tile*4 + s][b] x 16 B; lxs[b] = 2^-e;
+//         then the tile biases [tile][16] f32 (q4_tile_bias)
 //     q8: planes q0,q1,q2, [chunk*4 + s][b] x 16 B;      lxs[b] = sx
 __device__ __forceinline__ void stage_fused(const XSrc& s, int M, int fmt, int nk, uint8_t* lx, float* lxs,
                                             float* xf) {
@@ -269,8 +268,8 @@ __device__ __forceinline__ void stage_fused(const XSrc& s, int M, int fmt, int n
             const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
             if (item == 0) lxs[b] = am > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
             const float4v xa = *(const float4v*)(xr + item * 8), xb = *(const float4v*)(xr + item * 8 + 4);
-            // in-slot order {0,2,4,6,1,3,5,7}
-            const float xo[8] = {xa.x, xa.z, xb.x, xb.z, xa.y, xa.w, xb.y, xb.w};
+            // in-slot order {0,4,2,6,1,5,3,7}
+            const float xo[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};
             uint32_t hv[4], lv[4];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -282,6 +281,23 @@ __device__ __forceinline__ void stage_fused(const XSrc& s, int M, int fmt, int n
             }
             *(uint4*)(lx + off) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
             *(uint4*)(lx + pl + off) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+        }
+    }
+    if (fmt != DT_Q8ROW) {
+        // tile biases [tile][16] after the planes (q4_tile_bias; zero rows >= M)
+        float* bias = (float*)(lx + 2 * pl);
+        for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
+            const int t = i >> 4, b = i & 15;
+            float v = 0.f;
+            if (b < M) {
+                float am = 0.f;
+                for (int q = 0; q < S; q++) am = fmaxf(am, mred[b * S + q]);
+                int ex = 0;
+                if (am > 0.f) frexpf(am, &ex);
+                const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+                v = q4_tile_bias(xf + (size_t)b * kpad, kpad, t * 32, sc);
+            }
+            bias[i] = v;
         }
     }
 }
@@ -297,7 +313,8 @@ __device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, u
         for (int i = threadIdx.x; i < n; i += blockDim.x) l[i] = g[i];
         if (threadIdx.x < 16) lxs[threadIdx.x] = s.xs[threadIdx.x];
     } else {
-        const size_t pbytes = (size_t)nk * 4 * M * 16 * (fmt == DT_Q8ROW ? 3 : 2);
+        // planes (+ q4 tile biases), then the f32 scratch
+        const size_t pbytes = fmt == DT_Q8ROW ? (size_t)nk * 4 * M * 16 * 3 : (size_t)nk * (128 * M + 64);
         stage_fused(s, M, fmt, nk, lx, lxs, (float*)(lx + pbytes));
     }
     __syncthreads();
@@ -327,13 +344,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 // ---------------------------------------------------------------------------
 // q4t / q4tp
 // ---------------------------------------------------------------------------
-// Persistent: workgroup g walks the work units (row block rb, K part kp) of
-// row blocks g, g + grid, ...; a K part is KS*SP steps of 1 KiB (one step =
-// 16 rows x 128 columns), SP consecutive steps per wave.  The weights (and
-// tile scales) of the next unit are requested before the current one is
-// computed (two register buffers), so every wave keeps SP KiB in flight
-// while it computes.  After the last K part the KS partial sums are reduced
-// in LDS in wave order (deterministic).
+// Workgroup g walks the work units (row block rb, K part kp) of row blocks
+// g, g + grid, ...; a K part is KS*SP steps of 1 KiB (one step = 16 rows x
+// 128 columns), SP consecutive steps per wave, all requested at once.  After
+// the last K part the KS partial sums are reduced in LDS in wave order
+// (deterministic).  (A variant that requested the next unit's weights before
+// computing the current one held twice the registers, lost occupancy and was
+// no faster on MI355X.)
 // HL (m <= 8): A rows 0..7 carry the f16 hi plane of batch row r and rows
 // 8..15 the lo plane of batch row r - 8, one MFMA per tile; the two halves
 // are added at the end.  XM: where the activation operand comes from
@@ -388,12 +405,12 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
             }
         }
     };
-    uint4 wA[SP], wB[SP];
-    uint2 sA[SP], sB[SP];
-    float2 pA{}, pB{};
+    uint4 wA[SP];
+    uint2 sA[SP];
+    float2 pA{};
     float xsv = 0.f;
     if constexpr (XM == XM_PREP) {
-        x_dma(a.src, ntg * 16 * M * 2, smem);  // hi + lo planes
+        x_dma(a.src, ntg * (32 * M + 16), smem);  // hi + lo planes + tile biases
         xsv = a.src.xs[threadIdx.x & 15];
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -412,6 +429,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     // operand planes [item][b] x 16 B, hi then lo: in LDS, or read in place
     const uint4* LH = XM != XM_GLOBAL ? (const uint4*)smem : (const uint4*)a.src.planes;
     const uint4* LL = LH + ntg * 4 * 4 * M;
+    const float4v* LB = (const float4v*)(LL + ntg * 4 * 4 * M);  // tile biases [tile][16]
     // lanes whose A row is past the batch read batch row 0: their D rows are
     // never stored, and every lane loads unconditionally
     const uint4* LX = HL ? (r < 8 ? LH : LL) : LH;
@@ -446,14 +464,15 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
                 for (int t = 0; t < 4; t++) {
                     const int item = (tg * 4 + t) * M4 + xoff;
                     const half8 bq = dq_nib_word(ww[t]);
+                    const float4v cb = LB[(tg * 4 + t) * 4 + s];  // rows 4s..4s+3
                     float4v d;
                     if constexpr (HL) {
                         const half8 xa = __builtin_bit_cast(half8, LX[item]);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bq, zero, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bq, cb, 0, 0, 0);
                     } else {
                         const half8 xh = __builtin_bit_cast(half8, LH[item]);
                         const half8 xl = __builtin_bit_cast(half8, LL[item]);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq, zero, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq, cb, 0, 0, 0);
                         d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq, d, 0, 0, 0);
                     }
 #pragma unroll
@@ -485,7 +504,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
                     const int b = 4 * s + v;
                     if (b < M) {
                         float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
-                        const float val = acc[v] * lxs[b];
+                        const float val = acc[v] * lxs[b] * 16777216.0f;  // 2^24: denormal nibbles
                         *yp = a.resid ? *yp + val : val;
                     }
                 }
@@ -503,25 +522,14 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
             kn = 0;
             rn += gridDim.x;
         }
-        __builtin_amdgcn_sched_barrier(0);  // next unit's loads go out before this unit's compute
-        if (rn < a.nrb) load(wB, sB, pB, rn, kn);
-        __builtin_amdgcn_sched_barrier(0);
-        process(wA, sA, pB, rn);
+        float2 pn{};
+        if constexpr (TP)
+            if (rn < a.nrb) pn = a.rowp[(a.rb0 + rn) * 16 + r];
+        process(wA, sA, pn, rn);
         if (rn >= a.nrb) break;
         rb = rn;
         kp = kn;
-        kn = kp + 1;
-        if (kn == P) {
-            kn = 0;
-            rn += gridDim.x;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (rn < a.nrb) load(wA, sA, pA, rn, kn);
-        __builtin_amdgcn_sched_barrier(0);
-        process(wB, sB, pA, rn);
-        if (rn >= a.nrb) break;
-        rb = rn;
-        kp = kn;
+        load(wA, sA, pA, rb, kp);
     }
 }
 
@@ -551,7 +559,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
 #pragma unroll
         for (int u = 0; u < SP; u++) wv[u] = ((const int4v*)a.w)[(wbase + min(c0 + u, nkc - 1)) * 64 + lane];
     };
-    int4v wA[SP], wB[SP];
+    int4v wA[SP];
     float xsv = 0.f;
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, nkc * 4 * M * 3, smem);  // three planes
@@ -668,25 +676,11 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
             kn = 0;
             rn += gridDim.x;
         }
-        __builtin_amdgcn_sched_barrier(0);  // next unit's loads go out before this unit's compute
-        if (rn < a.nrb) load(wB, rn, kn);
-        __builtin_amdgcn_sched_barrier(0);
         process(wA);
         if (rn >= a.nrb) break;
         rb = rn;
         kp = kn;
-        kn = kp + 1;
-        if (kn == P) {
-            kn = 0;
-            rn += gridDim.x;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        if (rn < a.nrb) load(wA, rn, kn);
-        __builtin_amdgcn_sched_barrier(0);
-        process(wB);
-        if (rn >= a.nrb) break;
-        rb = rn;
-        kp = kn;
+        load(wA, rb, kp);
     }
 }
 
