@@ -28,6 +28,22 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
+COPY_BYTES = 64 << 20  # counter-calibration copy (read + write of this many bytes)
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4t_gemv_12288x4096_m1_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline GEMV from the committed rocprofv3
+    counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), or
+    None when no summary is present."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        return None
+    return None
 METRIC = "spec-verify decode tok/s + q4t GEMV HBM GB/s (% of peak), 1 MI355X"
 
 
@@ -71,6 +87,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV sweep")
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV sweep (profiling runs)")
+    ap.add_argument("--profile-gemv", action="store_true",
+                    help="only the HBM-counter workload: 20 plain copies of 64 MiB (counter calibration), then "
+                         "50 launches of the roofline GEMV (q4t 12288x4096 M=1)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the decode hot path has no "
@@ -80,6 +99,15 @@ def main():
     import cmf_amd as cmf
     from cmf_amd import synth
     cmf.init(0)
+    if args.profile_gemv:
+        import ctypes as C
+        ms = C.c_float()
+        cmf.check(cmf.lib().cmf_time_copy(COPY_BYTES, 4, 20, C.byref(ms)))
+        t2 = synth.q4t_uniform(31 + 12288, 12288, 4096)
+        g = time_gemv(cmf, t2, 1, copies=10, iters=50, warmup=10)
+        print(json.dumps({"copy_bytes": COPY_BYTES, "copy_us": round(ms.value * 1e3, 2),
+                          "gemv": "q4t 12288x4096 M=1", "gemv_us": round(g * 1e3, 3)}))
+        return
     t_setup = time.perf_counter()
     out = {"metric": METRIC, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
@@ -104,7 +132,7 @@ def main():
                 kernels.append(e)
                 if shape == (12288, 4096) and m == 1:
                     roof = {"bound": "hbm", "achieved": round(e["GB/s"], 1), "peak": PEAK_HBM, "unit": "GB/s",
-                            "frac": round(e["frac"], 4), "traffic": None,
+                            "frac": round(e["frac"], 4), "traffic": measured_traffic(),
                             "kernel": "k_gemv_q4<q4t> gate/up 12288x4096 M=1",
                             "bytes_per_launch": b, "avg_launch_us": round(ms * 1e3, 3)}
             t3 = synth.q4tp_uniform(41 + shape[0], shape[0], shape[1])
@@ -117,6 +145,10 @@ def main():
                 e[kk] = round(e[kk], 4 if kk == "frac" else 2)
         out["roofline"] = roof
         out["kernels"] = kernels
+        import ctypes as C
+        ms = C.c_float()
+        cmf.check(cmf.lib().cmf_time_copy(COPY_BYTES, 4, 20, C.byref(ms)))
+        out["device_copy_GB/s"] = round(2 * COPY_BYTES / ms.value / 1e6, 1)  # read + write, 64 MiB
     if args.gemv_only:
         print(json.dumps(out))
         return

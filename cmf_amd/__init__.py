@@ -94,6 +94,7 @@ SIGNATURES = {
     "cmf_prep_dev": (_I, [_P, _P, _I, _I, _P, _P]),
     "cmf_gemv_prepared": (_I, [_P, _P, _P, _I, _P, _I, _I]),
     "cmf_time_gemv": (_I, [C.POINTER(_P), _I, _P, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
+    "cmf_time_copy": (_I, [_S, _I, _I, C.POINTER(_F)]),
     "cmf_model_create": (_I, [C.POINTER(ModelConfig), C.POINTER(_P)]),
     "cmf_model_free": (_I, [_P]),
     "cmf_model_set_layer": (_I, [_P, _I, C.POINTER(LayerDesc)]),

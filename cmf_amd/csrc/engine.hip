@@ -54,6 +54,8 @@ struct cmf_model_s {
     int* out = nullptr;
     int out_cap = 0;
     float* h_tip = nullptr;
+    uint8_t* planes = nullptr;  // prepared GEMV operand (largest prep_bytes of the model)
+    float* xs = nullptr;        // its per-row scales [16]
     SampleBufs sb;
     std::vector<void*> allocs;
     int next_pos_host = 0;
@@ -172,22 +174,24 @@ XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
     return r;
 }
 
-// W x with the operand produced in-kernel (LDS-staged).  Batches whose
-// operand does not fit the LDS staging are split into sub-batches that do
-// (each re-reads the weights); there is no global-memory operand path in
-// the model.
+// W x with the operand of src: a one-workgroup-per-row producer writes the
+// prepared planes (norm / SwiGLU / concat evaluated once, not per GEMV
+// workgroup), the GEMV copies them to LDS (or reads them in place when they
+// do not fit).
 int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int nb, bool resid,
            hipStream_t s) {
-    (void)m;
-    int step = nb;
-    while (step > 1 && !fits_lds(w, step)) step--;
-    if (!fits_lds(w, step)) return fail("gemv: one operand row exceeds the LDS staging");
-    for (int b0 = 0; b0 < nb; b0 += step) {
-        const int mb = std::min(step, nb - b0);
+    for (int b0 = 0; b0 < nb; b0 += MAXB) {
+        const int mb = std::min(MAXB, nb - b0);
         XSrc sb = src;
         sb.x = src.x ? src.x + (size_t)b0 * src.ldx : nullptr;
         if (sb.toks) sb.toks = src.toks + b0;
-        const int rc = gemv(w, sb, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s);
+        int rc = launch_prep_src(w, sb, mb, m->planes, m->xs, s);
+        if (rc != CMF_OK) return rc;
+        XSrc g{};
+        g.mode = XS_GLOBAL;
+        g.planes = m->planes;
+        g.xs = m->xs;
+        rc = gemv(w, g, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s);
         if (rc != CMF_OK) return rc;
     }
     return CMF_OK;
@@ -291,8 +295,16 @@ int alloc_scratch(cmf_model_s* m) {
         dalloc_t(m, &m->pm, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->pl, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->po, (size_t)MAXB * c.n_heads * m->nch_cap * hd) ||
-        dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H))
+        dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H) ||
+        dalloc_t(m, &m->xs, 16))
         return CMF_ERR;
+    {
+        // prepared operand of the widest GEMV: q8 K <= max(2H, nh*hd), q4 K <= max(H, I)
+        const size_t k8 = ((size_t)std::max(2 * H, c.n_heads * hd) + 63) / 64;
+        const size_t k4 = ((size_t)std::max(H, c.inter) + 127) / 128;
+        const size_t pb = std::max(k8 * 1024 * 3, k4 * 4 * (1024 * 2 + 64));
+        if (dalloc(m, (void**)&m->planes, pb)) return CMF_ERR;
+    }
     // rope table (cos, sin) per (position, freq) with the host libm, as
     // rope_rotate (attention.rs:71-81) evaluates it
     const int half = hd / 2;

@@ -15,8 +15,8 @@ struct EmbedSrc {
     int nkc;
 };
 
-// Producer of a GEMV's activation operand, evaluated by every workgroup into
-// LDS (or, for XS_GLOBAL, prepared planes read from global memory):
+// Producer of a GEMV's activation operand (launch_prep_src evaluates it into
+// prepared planes; the GEMV itself takes XS_GLOBAL = prepared planes):
 //   XS_NORM : x = rms_norm(x_row) * w                  (inference.rs:33-50)
 //   XS_SILU : x = silu(g) * u, g/u at [0, K) / [K, 2K)  (inference.rs:14-16)
 //   XS_ROWS : x = x_row
@@ -58,10 +58,11 @@ GemvKernel q8_kernel(int m, int xm, int ks);
 // y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m.
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
          bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0);
-// Whether an m-row operand for w fits the LDS staging.
-bool fits_lds(const DevWeight& w, int m);
 
 size_t prep_bytes(const DevWeight& w);
+// Prepared planes (prep_bytes, the layout of prep8_row / prep16_row) and
+// xs[16] of the operand producer src for m batch rows of w.
+int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes, float* xs, hipStream_t st);
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
                 hipStream_t st);
 // y[b*ldy + (r - row_lo)] for rows [row_lo, row_hi) and b < m.
@@ -109,26 +110,16 @@ __device__ inline void prep8_row(const float* x, int K, float amax, int nk, int 
     }
 }
 
-// Bias of one tile for the denormal-nibble MFMA: the kernels multiply
-// x by n * 2^-24 (n = 0..15, an f16 denormal) and start the accumulator at
-// -8 * 2^-24 * sum(x) of the tile, so that D = 2^-24 * sum((n - 8) * x).
-// x here is the tile's 32 operand values as the MFMA sees them (f16 hi + lo).
-__device__ inline float q4_tile_bias(const float* x, int K, int col0, float scale) {
-    float sum = 0.f;
-    for (int j = 0; j < 32; j++) {
-        const float v = col0 + j < K ? x[col0 + j] * scale : 0.f;
-        const _Float16 h = (_Float16)v;
-        const _Float16 l = (_Float16)(v - (float)h);
-        sum += (float)h + (float)l;
-    }
-    return sum * -4.76837158203125e-07f;  // -8 * 2^-24
-}
-
 // Writes batch row b (of M) of the q4 activation operand: f16 hi/lo of
 // x*2^e with max|x*2^e| < 2^15, xs[b] = 2^-e, planes [item = 4*tile + s][b]
 // x 8 halves of columns 32*tile + 8*s + {0,4,2,6,1,5,3,7} (hi plane, then lo
-// plane), then the tile biases [tile][16] f32 (q4_tile_bias at [tile][b],
-// zero for rows >= M; the workgroup of row 0 writes those zeros).
+// plane), then the tile biases [tile][16] f32: -8 * 2^-24 * sum(hi + lo) of
+// the tile at [tile][b], zero for rows >= M (the workgroup of row 0 writes
+// those zeros).  The q4 kernels multiply x by the nibbles as f16 denormals
+// n * 2^-24 and start each tile's accumulator at this bias, so that
+// D = 2^-24 * sum((n - 8) * x).  nthr must
+// be a multiple of 64: the four items of a tile sit in lanes 4t..4t+3 of one
+// wave, which add their partial sums for the bias.
 __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b, int M,
                                   uint8_t* planes, float* xs, int tid, int nthr) {
     int ex = 0;
@@ -139,28 +130,35 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
     uint8_t* pl = planes + (size_t)ntiles * 64 * M;
     float* bias = (float*)(planes + (size_t)ntiles * 128 * M);
     const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
-    for (int idx = tid; idx < ntiles * 4; idx += nthr) {
+    for (int i0 = 0; i0 < ntiles * 4; i0 += nthr) {  // uniform trip count (shuffles below)
+        const int idx = i0 + tid;
+        const bool on = idx < ntiles * 4;
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
         uint16_t hv[8], lv[8];
+        float part = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int col = c0 + ord[j];
-            const float v = col < K ? x[col] * scale : 0.f;
+            const float v = on && col < K ? x[col] * scale : 0.f;
             const _Float16 h = (_Float16)v;
             const _Float16 l = (_Float16)(v - (float)h);
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
+            part += (float)h + (float)l;
         }
+        part += __shfl_xor(part, 1);
+        part += __shfl_xor(part, 2);
+        if (!on) continue;
         const size_t off = ((size_t)idx * M + b) * 16;
         *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
                                          lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
-    }
-    for (int t = tid; t < ntiles; t += nthr) {
-        bias[t * 16 + b] = q4_tile_bias(x, K, t * 32, scale);
-        if (b == 0)
-            for (int r = M; r < 16; r++) bias[t * 16 + r] = 0.f;
+        if (s == 0) {
+            bias[t * 16 + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
+            if (b == 0)
+                for (int r = M; r < 16; r++) bias[t * 16 + r] = 0.f;
+        }
     }
 }
 

@@ -7,31 +7,109 @@
 namespace cmf {
 
 // ---------------------------------------------------------------------------
-// Activation preparation into global planes (standalone GEMV calls and the
-// operands too large for LDS).  One workgroup per batch row.
+// Operand producers into prepared planes, one workgroup per batch row: the
+// producer (XSrc) is evaluated into LDS in f32, reduced (f64 sums of squares
+// for the RMSNorm producers, max|x|) and written as the planes of a weight
+// of format fmt (prep8_row / prep16_row), which the GEMV then copies to LDS.
+//   XS_ROWS: x          XS_NORM: rms_norm(x) * w (inference.rs:33-50)
+//   XS_SILU: silu(g) * u with g/u at [0, K) / [K, 2K) of the row (inference.rs:14-16)
+//   XS_CAT : [rms_norm(embed(tok)) * w ; rms_norm(x) * w2], H each (pipeline.rs:3085-3094)
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_prep(const float* __restrict__ X, int ldx, int K, int kind,
-                                              int nk, uint8_t* __restrict__ planes,
-                                              float* __restrict__ xs) {
-    const int b = blockIdx.x;
-    const float* x = X + (size_t)b * ldx;
-    __shared__ float red[256];
-    float m = 0.f;
-    for (int i = threadIdx.x; i < K; i += 256) m = fmaxf(m, fabsf(x[i]));
-    red[threadIdx.x] = m;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + o]);
-        __syncthreads();
+__global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk, uint8_t* __restrict__ planes,
+                                                  float* __restrict__ xs) {
+    extern __shared__ float vals[];  // K
+    __shared__ double red1[8], red2[8];
+    __shared__ float redm[8];
+    const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    const int nw = nt >> 6;
+    const bool nrm = s.mode == XS_NORM || s.mode == XS_CAT;
+    const int H = s.mode == XS_CAT ? s.H : K;
+    const float* row = s.x + (size_t)b * s.ldx;
+    int tok = 0, rb = 0, r = 0;
+    float rs = 0.f;
+    bool tv = false;
+    if (s.mode == XS_CAT) {
+        tok = s.toks[b];
+        tv = tok >= 0 && tok < s.emb.rows;
+        rb = tok >> 4;
+        r = tok & 15;
+        rs = tv ? s.emb.rs[tok] : 0.f;
     }
-    const float amax = red[0];
-    if (kind == 8) prep8_row(x, K, amax, nk, b, gridDim.x, planes, xs, threadIdx.x, 256);
-    else prep16_row(x, K, amax, nk, b, gridDim.x, planes, xs, threadIdx.x, 256);
+    double s1 = 0.0, s2 = 0.0;
+    for (int i = tid; i < K; i += nt) {
+        float v;
+        if (s.mode == XS_SILU) {
+            const float g = row[i], u = row[s.K + i];
+            v = (g / (1.0f + expf(-g))) * u;
+        } else if (s.mode == XS_CAT) {
+            if (i < H) {
+                // int8 of the token's row in the q8 device layout, times its row scale
+                const int kc = i >> 6, sl = (i >> 4) & 3, jj = i & 15;
+                const int8_t q = tv ? s.emb.w[(((size_t)rb * s.emb.nkc + kc) * 64 + 16 * sl + r) * 16 + jj] : 0;
+                v = (float)q * rs;
+            } else {
+                v = row[i - H];
+            }
+        } else {
+            v = row[i];
+        }
+        vals[i] = v;
+        if (nrm) {
+            if (i < H) s1 += (double)v * (double)v;
+            else s2 += (double)v * (double)v;
+        }
+    }
+    if (nrm) {
+        for (int o = 32; o > 0; o >>= 1) {
+            s1 += __shfl_xor(s1, o);
+            s2 += __shfl_xor(s2, o);
+        }
+        if (lane == 0) {
+            red1[wave] = s1;
+            red2[wave] = s2;
+        }
+    }
+    __syncthreads();
+    float am = 0.f;
+    if (nrm) {
+        double t1 = 0.0, t2 = 0.0;
+        for (int q = 0; q < nw; q++) {
+            t1 += red1[q];
+            t2 += red2[q];
+        }
+        const float inv1 = 1.0f / (float)sqrt(t1 / (double)H + s.eps);
+        const float inv2 = s.mode == XS_CAT ? 1.0f / (float)sqrt(t2 / (double)(K - H) + s.eps) : 1.f;
+        for (int i = tid; i < K; i += nt) {
+            const float y = i < H ? vals[i] * inv1 * s.w[i] : vals[i] * inv2 * s.w2[i - H];
+            vals[i] = y;
+            am = fmaxf(am, fabsf(y));
+        }
+    } else {
+        for (int i = tid; i < K; i += nt) am = fmaxf(am, fabsf(vals[i]));
+    }
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    if (lane == 0) redm[wave] = am;
+    __syncthreads();
+    am = 0.f;
+    for (int q = 0; q < nw; q++) am = fmaxf(am, redm[q]);
+    if (fmt == DT_Q8ROW) prep8_row(vals, K, am, nk, b, gridDim.x, planes, xs, tid, nt);
+    else prep16_row(vals, K, am, nk, b, gridDim.x, planes, xs, tid, nt);
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------
+int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes, float* xs, hipStream_t st) {
+    const int K = src.K ? src.K : w.cols;
+    if (m < 1 || m > MAXB) return fail("prep: batch must be 1..16");
+    if (K < 1 || K > w.cols || K > 16384) return fail("prep: operand length must be 1..min(cols, 16384)");
+    if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
+    const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
+    hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
+                       xs);
+    return CMF_OK;
+}
+
 size_t prep_bytes(const DevWeight& w) {
     // at most 16 batch rows: q8 3 planes of nk*64*16 B ; q4 2 planes of ntiles*64*16 B
     // (+ q4 tile biases [tile][16] f32)
@@ -40,22 +118,17 @@ size_t prep_bytes(const DevWeight& w) {
 
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
                 hipStream_t st) {
-    const int kind = w.dtype == DT_Q8ROW ? 8 : 16;
-    const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
-    hipLaunchKernelGGL(k_prep, dim3(m), dim3(256), 0, st, x, ldx, w.cols, kind, nk, planes, xs);
-    return CMF_OK;
+    XSrc r{};
+    r.mode = XS_ROWS;
+    r.x = x;
+    r.ldx = ldx;
+    return launch_prep_src(w, r, m, planes, xs, st);
 }
 
 static size_t lds_bytes(const DevWeight& w, int m) {
     // q4: hi + lo planes and the tile biases [tile][16] f32
     return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 4 * (128 * m + 64);
 }
-// plus the f32 scratch of the in-kernel producers: the m raw rows and the
-// norm weights
-static size_t lds_scratch(const DevWeight& w, int m) {
-    return (size_t)(w.dtype == DT_Q8ROW ? w.kchunks * 64 : w.kchunks * 128) * 4 * (m + 1);
-}
-
 static int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     return v && *v ? atoi(v) : dflt;
@@ -127,21 +200,11 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
     // 4 tiles (128 columns)
     int ks = ks_override > 0 ? ks_override : pick_ks(w.kchunks);
     if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);  // no 16-wave instance (registers)
-    const bool fu = src.mode != XS_GLOBAL;
+    if (src.mode != XS_GLOBAL) return fail("gemv: the operand must be prepared (launch_prep_src)");
     size_t lds = lds_bytes(w, m);
-    if (fu) {
-        const int kpad = w.dtype == DT_Q8ROW ? w.kchunks * 64 : w.kchunks * 128;
-        if (a.src.K % 4 || (src.mode != XS_CAT && src.ldx % 4) || (src.mode == XS_CAT && (src.H % 4 || src.ldx % 4)) ||
-            ((uintptr_t)src.x & 15) || kpad > 4 * SEG4 * SEGMAX)
-            return fail("gemv: fused operand needs K, H, ldx multiples of 4, a 16-byte aligned row base and K <= 16384");
-        lds += lds_scratch(w, m);
-    }
-    if (lds > LDSX_MAX) {
-        if (fu) return fail("gemv: activation operand exceeds LDS; prepare it globally");
-        lds = 0;  // planes read in place from global memory
-    }
+    if (lds > LDSX_MAX) lds = 0;  // planes read in place from global memory
     a.lds = lds ? 1 : 0;
-    const int xm = fu ? XM_FUSED : lds ? XM_PREP : XM_GLOBAL;
+    const int xm = lds ? XM_PREP : XM_GLOBAL;
     GemvKernel k = w.dtype == DT_Q8ROW ? q8_kernel(m, xm, ks)
                    : w.dtype == DT_Q4T ? q4t_kernel(m, xm, ks)
                                        : q4tp_kernel(m, xm, ks);
@@ -156,7 +219,6 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
     return CMF_OK;
 }
 
-bool fits_lds(const DevWeight& w, int m) { return lds_bytes(w, m) + lds_scratch(w, m) <= LDSX_MAX; }
 
 int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
                 int m, int row_lo, int row_hi, hipStream_t st, int ks_override) {

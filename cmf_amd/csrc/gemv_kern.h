@@ -16,16 +16,16 @@
 //       q4* : v_mfma_f32_16x16x32_f16, one tile (32 columns, one scale) per
 //             MFMA; nibbles become the exact f16 denormals n * 2^-24 in
 //             registers (one mask per pair), the format's -8 offset enters
-//             as the accumulator input -8 * 2^-24 * sum(x) of the tile, and
+//             as the accumulator input -8 * 2^-24 * sum(x) of the tile (prep16_row), and
 //             x is carried as f16 hi + lo of x*2^e (22-bit significand).
 //             Each tile's product is scaled by its tile scale and
 //             accumulated in f32, as q4t_row_exact does
 //             (qtensor.rs:4418-4432).
-//   - the activation operand is built once per workgroup into LDS from its
-//     producer (RMSNorm of the residual rows, SwiGLU of the gate/up rows,
-//     plain rows, the MTP [enorm(embed); hnorm(h)] concat, or a prepared
-//     buffer), so the producer needs no kernel of its own; when it does not
-//     fit in LDS the prepared planes are read from global memory (L2).
+//   - the activation operand arrives prepared (planes written by a producer
+//     kernel: RMSNorm of the residual rows, SwiGLU of the gate/up rows, the
+//     MTP [enorm(embed); hnorm(h)] concat or plain rows) and is copied to
+//     LDS by direct global->LDS loads; when it does not fit in LDS the
+//     planes are read from global memory (L2) in place.
 //   - optional residual epilogue: y is added into the output (h += W x).
 #pragma once
 
@@ -44,7 +44,8 @@ constexpr int LDSX_MAX = 128 * 1024;  // largest LDS-staged activation operand (
 // Four nibble bytes (8 weights: elements 8s..8s+7 of a tile) to the f16
 // denormals n * 2^-24 (exact, the raw nibble under a zero exponent) in the
 // in-slot order {0,4,2,6,1,5,3,7}: one mask (and shift) per pair.  The -8
-// offset of the format enters through the MFMA accumulator (q4_tile_bias).
+// offset of the format enters through the MFMA accumulator (the tile biases
+// written by prep16_row).
 __device__ __forceinline__ half8 dq_nib_word(uint32_t w) {
     constexpr uint32_t K = 0x000F000Fu;
     const uint32_t p0 = w & K;          // elements 0, 4
@@ -56,268 +57,6 @@ __device__ __forceinline__ half8 dq_nib_word(uint32_t w) {
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-
-// ---------------------------------------------------------------------------
-// Activation staging (once per workgroup)
-// ---------------------------------------------------------------------------
-constexpr int SEGJ = 8;            // float4 per lane per staging unit
-constexpr int SEG4 = 64 * SEGJ;    // float4 per staging unit (2048 elements)
-constexpr int SEGMAX = 8;          // staging units per row (operands up to 16384 elements)
-
-__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
-
-__device__ __forceinline__ float amax4(float m, float4v v) {
-    return fmaxf(fmaxf(m, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
-}
-__device__ __forceinline__ double sq4(float4v v) {
-    return (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
-           (double)v.w * (double)v.w;
-}
-
-// Phase 1 of one staging unit u (row b = u / S): lane element groups
-// k4 = base + 64*j + lane (4 elements each) are all requested at once (row 0
-// also requests the norm weights), the raw values stored to the scratch rows,
-// and the unit's sums of squares (norm producers) or max|x| reduced to LDS.
-template <int MODE>
-__device__ __forceinline__ void unit_phase1(const XSrc& s, int u, int S, int K4, int kp4, int H4, float4v* xf4,
-                                            float4v* wl4, double* red1, double* red2, float* mred) {
-    const int lane = threadIdx.x & 63;
-    const int b = u / S, base = (u % S) * SEG4;
-    constexpr bool nrm = MODE == XS_NORM || MODE == XS_CAT;
-    const bool ldw = nrm && b == 0;
-    float4v v[SEGJ], wv[SEGJ];
-    const float4v z4 = float4v{0.f, 0.f, 0.f, 0.f};
-    const float* row = s.x + (size_t)b * s.ldx;
-    if constexpr (MODE == XS_SILU) {
-        float4v g[SEGJ], u[SEGJ];
-#pragma unroll
-        for (int j = 0; j < SEGJ; j++) {
-            const int k4 = base + 64 * j + lane;
-            g[j] = k4 < K4 ? ((const float4v*)row)[k4] : z4;
-            u[j] = k4 < K4 ? ((const float4v*)(row + s.K))[k4] : z4;
-        }
-#pragma unroll
-        for (int j = 0; j < SEGJ; j++)
-            v[j] = float4v{silu_mul(g[j].x, u[j].x), silu_mul(g[j].y, u[j].y), silu_mul(g[j].z, u[j].z),
-                               silu_mul(g[j].w, u[j].w)};
-    } else if constexpr (MODE == XS_CAT) {
-        const int tok = s.toks[b];
-        const EmbedSrc& e = s.emb;
-        const bool tv = tok >= 0 && tok < e.rows;
-        const int rb = tok >> 4, r = tok & 15;
-        const float rs = tv ? e.rs[tok] : 0.f;
-#pragma unroll
-        for (int j = 0; j < SEGJ; j++) {
-            const int k4 = base + 64 * j + lane;
-            // four consecutive int8 of the token's row in the q8 device layout
-            const int k = 4 * k4, kc = k >> 6, sl = (k >> 4) & 3, jj = k & 15;
-            uint32_t q = 0u;
-            float4v xr = z4;
-            if (k4 < K4 && k4 < H4 && tv)
-                q = *(const uint32_t*)(e.w + (((size_t)rb * e.nkc + kc) * 64 + 16 * sl + r) * 16 + jj);
-            if (k4 < K4 && k4 >= H4) xr = ((const float4v*)row)[k4 - H4];
-            v[j] = k4 < H4 ? float4v{(float)(int8_t)(q & 0xFF), (float)(int8_t)((q >> 8) & 0xFF),
-                                         (float)(int8_t)((q >> 16) & 0xFF), (float)(int8_t)(q >> 24)}
-                           : xr;
-            wv[j] = ldw && k4 < K4 ? (k4 < H4 ? ((const float4v*)s.w)[k4] : ((const float4v*)s.w2)[k4 - H4]) : z4;
-        }
-#pragma unroll
-        for (int j = 0; j < SEGJ; j++) {
-            const int k4 = base + 64 * j + lane;
-            if (k4 < H4) v[j] = float4v{v[j].x * rs, v[j].y * rs, v[j].z * rs, v[j].w * rs};
-        }
-    } else {
-#pragma unroll
-        for (int j = 0; j < SEGJ; j++) {
-            const int k4 = base + 64 * j + lane;
-            v[j] = k4 < K4 ? ((const float4v*)row)[k4] : z4;
-            if constexpr (MODE == XS_NORM) wv[j] = ldw && k4 < K4 ? ((const float4v*)s.w)[k4] : z4;
-        }
-    }
-    double s1 = 0.0, s2 = 0.0;
-    float am = 0.f;
-#pragma unroll
-    for (int j = 0; j < SEGJ; j++) {
-        const int k4 = base + 64 * j + lane;
-        if (k4 < kp4) {
-            xf4[(size_t)b * kp4 + k4] = v[j];
-            if (ldw) wl4[k4] = wv[j];
-        }
-        if constexpr (nrm) {
-            if (k4 < H4) s1 += sq4(v[j]);
-            else s2 += sq4(v[j]);
-        } else {
-            am = amax4(am, v[j]);
-        }
-    }
-    if constexpr (nrm) {
-        for (int o = 32; o > 0; o >>= 1) {
-            s1 += __shfl_xor(s1, o);
-            s2 += __shfl_xor(s2, o);
-        }
-        if (lane == 0) {
-            red1[u] = s1;
-            red2[u] = s2;
-        }
-    } else {
-        for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-        if (lane == 0) mred[u] = am;
-    }
-}
-
-// Builds the operand of all M batch rows in LDS with the whole workgroup.
-// Rows are cut into units of 2048 elements; the waves take units round-robin.
-//   phase 1: every input element (and the norm weights) is requested at
-//            once, raw values go to the f32 scratch xf [M][kpad], per-unit
-//            sums of squares (f64) or max|x| to LDS;
-//   phase 2 (RMSNorm producers): inv = 1/sqrt(mean + eps) from the unit sums
-//            in a fixed order, x = (raw * inv) * w in place, per-unit max|x|;
-//   phase 3: operand planes, one 16-byte item per thread step:
-//     q4: hi plane then lo plane, [tile*4 + s][b] x 16 B; lxs[b] = 2^-e;
-//         then the tile biases [tile][16] f32 (q4_tile_bias)
-//     q8: planes q0,q1,q2, [chunk*4 + s][b] x 16 B;      lxs[b] = sx
-__device__ __forceinline__ void stage_fused(const XSrc& s, int M, int fmt, int nk, uint8_t* lx, float* lxs,
-                                            float* xf) {
-    __shared__ double red1[MAXB * SEGMAX], red2[MAXB * SEGMAX];
-    __shared__ float mred[MAXB * SEGMAX];
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
-    const int kpad = fmt == DT_Q8ROW ? nk * 64 : nk * 32;  // nk: q8 chunks / q4 tiles
-    const int K4 = s.K >> 2, kp4 = kpad >> 2;
-    const int S = (kp4 + SEG4 - 1) / SEG4, units = M * S;
-    const bool nrm = s.mode == XS_NORM || s.mode == XS_CAT;
-    const int H4 = s.mode == XS_CAT ? s.H >> 2 : 0x7fffffff;
-    float4v* xf4 = (float4v*)xf;
-    float4v* wl4 = xf4 + (size_t)M * kp4;  // norm weight of every element
-    const float4v z4 = float4v{0.f, 0.f, 0.f, 0.f};
-    for (int u = wave; u < units; u += nw) {
-        switch (s.mode) {
-            case XS_SILU: unit_phase1<XS_SILU>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
-            case XS_CAT: unit_phase1<XS_CAT>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
-            case XS_NORM: unit_phase1<XS_NORM>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
-            default: unit_phase1<XS_ROWS>(s, u, S, K4, kp4, H4, xf4, wl4, red1, red2, mred); break;
-        }
-    }
-    __syncthreads();
-    if (nrm) {
-        const int n1 = s.mode == XS_CAT ? s.H : s.K;
-        for (int u = wave; u < units; u += nw) {
-            const int b = u / S, sg = u % S;
-            double t1 = 0.0, t2 = 0.0;
-            for (int q = 0; q < S; q++) {
-                t1 += red1[b * S + q];
-                t2 += red2[b * S + q];
-            }
-            const float inv1 = 1.0f / (float)sqrt(t1 / (double)n1 + s.eps);
-            const float inv2 = s.mode == XS_CAT ? 1.0f / (float)sqrt(t2 / (double)s.H + s.eps) : 1.f;
-            float am = 0.f;
-#pragma unroll
-            for (int j = 0; j < SEGJ; j++) {
-                const int k4 = sg * SEG4 + 64 * j + lane;
-                if (k4 < K4) {
-                    const float iv = k4 < H4 ? inv1 : inv2;
-                    const float4v x = xf4[(size_t)b * kp4 + k4], w = wl4[k4];
-                    const float4v y = float4v{x.x * iv * w.x, x.y * iv * w.y, x.z * iv * w.z, x.w * iv * w.w};
-                    xf4[(size_t)b * kp4 + k4] = y;
-                    am = amax4(am, y);
-                }
-            }
-            for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-            if (lane == 0) mred[u] = am;
-        }
-        __syncthreads();
-    }
-    const int nitems = nk * 4;
-    const size_t pl = (size_t)nitems * M * 16;
-    for (int i = threadIdx.x; i < M * nitems; i += blockDim.x) {
-        const int b = i / nitems, item = i - b * nitems;
-        float am = 0.f;
-        for (int q = 0; q < S; q++) am = fmaxf(am, mred[b * S + q]);
-        const float* xr = xf + (size_t)b * kpad;
-        const size_t off = ((size_t)item * M + b) * 16;
-        if (fmt == DT_Q8ROW) {
-            const float sx = am > 0.f ? am / 127.0f : 1.0f, inv = 1.0f / sx;
-            if (item == 0) lxs[b] = sx;
-            uint32_t w0[4], w1[4], w2[4];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const float4v xv = *(const float4v*)(xr + item * 16 + 4 * c);
-                const float xs4[4] = {xv.x, xv.y, xv.z, xv.w};
-                uint32_t a = 0, bb = 0, cc = 0;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float x = xs4[j] * inv;
-                    const float q0 = fminf(127.f, fmaxf(-127.f, rintf(x)));
-                    const float r1 = (x - q0) * 128.0f;
-                    const float q1 = fminf(127.f, fmaxf(-127.f, rintf(r1)));
-                    const float q2 = fminf(127.f, fmaxf(-127.f, rintf((r1 - q1) * 128.0f)));
-                    a |= (uint32_t)(uint8_t)(int8_t)q0 << (8 * j);
-                    bb |= (uint32_t)(uint8_t)(int8_t)q1 << (8 * j);
-                    cc |= (uint32_t)(uint8_t)(int8_t)q2 << (8 * j);
-                }
-                w0[c] = a;
-                w1[c] = bb;
-                w2[c] = cc;
-            }
-            *(uint4*)(lx + off) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
-            *(uint4*)(lx + pl + off) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-            *(uint4*)(lx + 2 * pl + off) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
-        } else {
-            int ex = 0;
-            if (am > 0.f) frexpf(am, &ex);
-            const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-            if (item == 0) lxs[b] = am > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
-            const float4v xa = *(const float4v*)(xr + item * 8), xb = *(const float4v*)(xr + item * 8 + 4);
-            // in-slot order {0,4,2,6,1,5,3,7}
-            const float xo[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};
-            uint32_t hv[4], lv[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float x0 = xo[2 * j] * sc, x1 = xo[2 * j + 1] * sc;
-                const _Float16 h0 = (_Float16)x0, h1 = (_Float16)x1;
-                const _Float16 l0 = (_Float16)(x0 - (float)h0), l1 = (_Float16)(x1 - (float)h1);
-                hv[j] = __builtin_bit_cast(uint16_t, h0) | ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-                lv[j] = __builtin_bit_cast(uint16_t, l0) | ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-            }
-            *(uint4*)(lx + off) = make_uint4(hv[0], hv[1], hv[2], hv[3]);
-            *(uint4*)(lx + pl + off) = make_uint4(lv[0], lv[1], lv[2], lv[3]);
-        }
-    }
-    if (fmt != DT_Q8ROW) {
-        // tile biases [tile][16] after the planes (q4_tile_bias; zero rows >= M)
-        float* bias = (float*)(lx + 2 * pl);
-        for (int i = threadIdx.x; i < nk * 16; i += blockDim.x) {
-            const int t = i >> 4, b = i & 15;
-            float v = 0.f;
-            if (b < M) {
-                float am = 0.f;
-                for (int q = 0; q < S; q++) am = fmaxf(am, mred[b * S + q]);
-                int ex = 0;
-                if (am > 0.f) frexpf(am, &ex);
-                const float sc = am > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-                v = q4_tile_bias(xf + (size_t)b * kpad, kpad, t * 32, sc);
-            }
-            bias[i] = v;
-        }
-    }
-}
-
-// Operand staging of a whole workgroup; XS_GLOBAL planes have the LDS
-// layout already and are copied as they are.
-template <bool FU>
-__device__ __forceinline__ void stage_x(const XSrc& s, int M, int fmt, int nk, uint8_t* lx, float* lxs) {
-    if constexpr (!FU) {
-        const int n = nk * 4 * M * (fmt == DT_Q8ROW ? 3 : 2);  // 16-byte items
-        const uint4* g = (const uint4*)s.planes;
-        uint4* l = (uint4*)lx;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) l[i] = g[i];
-        if (threadIdx.x < 16) lxs[threadIdx.x] = s.xs[threadIdx.x];
-    } else {
-        // planes (+ q4 tile biases), then the f32 scratch
-        const size_t pbytes = fmt == DT_Q8ROW ? (size_t)nk * 4 * M * 16 * 3 : (size_t)nk * (128 * M + 64);
-        stage_fused(s, M, fmt, nk, lx, lxs, (float*)(lx + pbytes));
-    }
-    __syncthreads();
 }
 
 // Prepared planes go to LDS by direct global->LDS loads (no registers),
@@ -353,11 +92,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 // no faster on MI355X.)
 // HL (m <= 8): A rows 0..7 carry the f16 hi plane of batch row r and rows
 // 8..15 the lo plane of batch row r - 8, one MFMA per tile; the two halves
-// are added at the end.  XM: where the activation operand comes from
-// (XM_PREP prepared planes copied to LDS, XM_FUSED a fused producer staged
-// into LDS by stage_fused, XM_GLOBAL prepared planes read in place).
+// are added at the end.  XM: where the prepared activation operand is read
+// (XM_PREP: copied to LDS first, XM_GLOBAL: in place, for operands larger
+// than the LDS budget).
 constexpr int SP = 4;  // weight steps per wave and work unit
-enum { XM_PREP = 0, XM_FUSED = 1, XM_GLOBAL = 2 };
+enum { XM_PREP = 0, XM_GLOBAL = 2 };
 
 template <int FMT, int NV, int KS, bool HL, int XM>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
@@ -419,8 +158,6 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
     if constexpr (XM == XM_PREP) {
         wait_vmcnt<NL>();  // operand planes and xs are in
         if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
-    } else if constexpr (XM == XM_FUSED) {
-        stage_x<true>(a.src, M, FMT, ntg * 4, smem, lxs);
     } else if (threadIdx.x < 16) {
         lxs[threadIdx.x] = a.src.xs[threadIdx.x];
     }
@@ -571,8 +308,6 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
     if constexpr (XM == XM_PREP) {
         wait_vmcnt<SP>();  // operand planes and xs are in
         if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
-    } else if constexpr (XM == XM_FUSED) {
-        stage_x<true>(a.src, M, DT_Q8ROW, nkc, smem, lxs);
     } else if (threadIdx.x < 16) {
         lxs[threadIdx.x] = a.src.xs[threadIdx.x];
     }
@@ -705,7 +440,6 @@ template <int FMT, int NV, bool HL>
 GemvKernel q4_by_xm(int xm, int ks) {
     switch (xm) {
         case XM_PREP: return q4_by_ks<FMT, NV, HL, XM_PREP>(ks);
-        case XM_FUSED: return q4_by_ks<FMT, NV, HL, XM_FUSED>(ks);
         case XM_GLOBAL: return q4_by_ks<FMT, NV, HL, XM_GLOBAL>(ks);
     }
     return nullptr;
@@ -731,7 +465,6 @@ template <bool PK>
 GemvKernel q8_by_xm(int xm, int ks) {
     switch (xm) {
         case XM_PREP: return q8_by_ks<PK, XM_PREP>(ks);
-        case XM_FUSED: return q8_by_ks<PK, XM_FUSED>(ks);
         case XM_GLOBAL: return q8_by_ks<PK, XM_GLOBAL>(ks);
     }
     return nullptr;

@@ -8,16 +8,6 @@ namespace cmf {
 
 constexpr int ATT_C = 64;  // key positions per attention workgroup
 
-// Where a producer writes its prepared activations (layout: prep8_row /
-// prep16_row); the batch size is the producer's grid size.
-struct PrepDst {
-    int kind;         // 8 (q8 weights) or 16 (q4t / q4tp weights)
-    int nk;           // q8: chunks of 64 columns; q4: tiles of 32 columns
-    uint8_t* planes;
-    float* xs;
-};
-
-
 void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
                   hipStream_t st);
 // One layer's decode attention (head_dim 128): q/k-norm + RoPE, KV append,
@@ -42,8 +32,6 @@ struct AttnArgs {
     int attend;         // 0: only append the rows' K/V (no queries, no output)
 };
 void launch_attention(const AttnArgs& a, int max_len, hipStream_t st);
-void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,
-                          hipStream_t st);
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
                    hipStream_t st);
 

@@ -1,7 +1,6 @@
 // Decode-layer kernels around the GEMVs: qk-norm + RoPE + KV append, split-K
 // decode attention over the appended KV (causal inside the verify block),
-// merge, SwiGLU + operand preparation (standalone FFN seam op), embedding
-// gather and argmax.
+// merge, embedding gather and argmax.
 //
 // Semantics follow the reference CPU path:
 //   rms_norm_into / add_rmsnorm_fused_into   inference.rs:33-86
@@ -43,10 +42,6 @@ __device__ inline float block_max_f(float v, float* red) {
     return t;
 }
 
-__device__ inline void prep_any(const float* vals, int K, float amax, const PrepDst& d, int b) {
-    if (d.kind == 8) prep8_row(vals, K, amax, d.nk, b, gridDim.x, d.planes, d.xs, threadIdx.x, blockDim.x);
-    else prep16_row(vals, K, amax, d.nk, b, gridDim.x, d.planes, d.xs, threadIdx.x, blockDim.x);
-}
 
 // Embedding rows from the (tied) q8 lm_head: out[b] = q8 row * row_scale
 // (pipeline.rs:5568-5575).  grid (nb), block 256.
@@ -323,26 +318,6 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     }
 }
 
-// SwiGLU on the fused gate/up output gu[b] = [g (I) ; u (I)], prepared for
-// the down projection.  grid (nb), block 256; I <= 12288.
-__global__ __launch_bounds__(256) void k_silu_mul_prep(const float* __restrict__ gu, int ldg, int I,
-                                                       PrepDst dst, float* __restrict__ out_f32) {
-    const int b = blockIdx.x;
-    __shared__ float vals[12288];
-    __shared__ float redf[4];
-    float am = 0.f;
-    for (int i = threadIdx.x; i < I; i += blockDim.x) {
-        const float g = gu[(size_t)b * ldg + i], u = gu[(size_t)b * ldg + I + i];
-        const float v = (g / (1.0f + expf(-g))) * u;
-        vals[i] = v;
-        if (out_f32) out_f32[(size_t)b * I + i] = v;
-        am = fmaxf(am, fabsf(v));
-    }
-    am = block_max_f(am, redf);
-    __syncthreads();
-    prep_any(vals, I, am, dst, b);
-}
-
 // Argmax per row, ties to the highest index.  Pass 1: grid (nslices, nrows).
 __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, int ld, int n,
                                                      int slice, float* __restrict__ pv,
@@ -421,10 +396,6 @@ void launch_attention(const AttnArgs& a, int max_len, hipStream_t st) {
     if (a.attend) hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
 }
 
-void launch_silu_mul_prep(const float* gu, int ldg, int I, const PrepDst& d, float* out, int nb,
-                          hipStream_t st) {
-    hipLaunchKernelGGL(k_silu_mul_prep, dim3(nb), dim3(256), 0, st, gu, ldg, I, d, out);
-}
 
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
                    hipStream_t st) {

@@ -406,9 +406,13 @@ int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b,
         rc = launch_gemv(w1->w, pl, dxs, dgu, 2 * inter, m, 0, inter, st);
         if (rc == CMF_OK) rc = launch_gemv(w3->w, pl, dxs, dgu + inter, 2 * inter, m, 0, inter, st);
         if (rc != CMF_OK) break;
-        PrepDst d{w2->w.dtype == DT_Q8ROW ? 8 : 16,
-                  w2->w.dtype == DT_Q8ROW ? w2->w.kchunks : w2->w.kchunks * 4, pl, dxs};
-        launch_silu_mul_prep(dgu, 2 * inter, inter, d, nullptr, m, st);
+        XSrc sg{};
+        sg.mode = XS_SILU;
+        sg.x = dgu;
+        sg.ldx = 2 * inter;
+        sg.K = inter;
+        rc = launch_prep_src(w2->w, sg, m, pl, dxs, st);
+        if (rc != CMF_OK) break;
         rc = launch_gemv(w2->w, pl, dxs, dy, hidden, m, 0, hidden, st);
         if (rc != CMF_OK) break;
         CMF_HIP(hipMemcpyAsync(out + (size_t)b0 * hidden, dy, (size_t)m * hidden * 4, hipMemcpyDeviceToHost, st));
@@ -478,9 +482,51 @@ __global__ void k_spin(unsigned long long ticks, int max_iter) {
         __builtin_amdgcn_s_sleep(2);
     }
 }
+// Plain copy, 16 bytes per lane per step (the calibration kernel of the
+// HBM traffic counters).
+__global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
 }  // namespace cmf
 
 extern "C" {
+
+int cmf_time_copy(size_t bytes, int nbuf, int iters, float* avg_ms) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (bytes < 16 || bytes % 16 || nbuf < 1 || nbuf > 64 || iters < 1 || !avg_ms)
+        return fail("time_copy: bytes must be a positive multiple of 16, 1 <= nbuf <= 64, iters >= 1");
+    hipStream_t st = stream();
+    std::vector<void*> src(nbuf, nullptr);
+    void* dst = nullptr;
+    int rc = CMF_OK;
+    for (auto& p : src)
+        if (hipMalloc(&p, bytes) != hipSuccess || hipMemsetAsync(p, 1, bytes, st) != hipSuccess) rc = fail("time_copy: allocation failed");
+    if (rc == CMF_OK && hipMalloc(&dst, bytes) != hipSuccess) rc = fail("time_copy: allocation failed");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (rc == CMF_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)) rc = fail("time_copy: event");
+    if (rc == CMF_OK) {
+        const size_t n = bytes / 16;
+        const int grid = (int)std::min<size_t>((n + 255) / 256, 8192);
+        for (int i = 0; i < std::min(iters, 4); i++)
+            hipLaunchKernelGGL(k_copy16, dim3(grid), dim3(256), 0, st, (const uint4*)src[i % nbuf], (uint4*)dst, n);
+        (void)hipEventRecord(e0, st);
+        for (int i = 0; i < iters; i++)
+            hipLaunchKernelGGL(k_copy16, dim3(grid), dim3(256), 0, st, (const uint4*)src[i % nbuf], (uint4*)dst, n);
+        (void)hipEventRecord(e1, st);
+        float ms = 0.f;
+        if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) rc = fail("time_copy: timing");
+        *avg_ms = ms / iters;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(st);
+    for (auto p : src)
+        if (p) (void)hipFree(p);
+    if (dst) (void)hipFree(dst);
+    if (rc == CMF_OK) CMF_HIP(hipGetLastError());
+    return rc;
+}
 
 int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const float* d_xs, int b,
                   float* d_y, int ldy, int ks, int warmup, int iters, float* avg_ms) {

@@ -89,6 +89,12 @@ int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int
  * measured with HIP events on the library stream. */
 int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const float* d_xs, int b,
                   float* d_y, int ldy, int ks, int warmup, int iters, float* avg_ms);
+/* Average device time (ms) of `iters` launches of a plain device copy of
+ * `bytes` (16-byte vector loads and stores, a fresh source buffer each
+ * launch from `nbuf` rotating ones).  No counterpart in the reference: a
+ * measurement helper, the known-size kernel against which HBM traffic
+ * counters (FETCH_SIZE / WRITE_SIZE) are calibrated. */
+int cmf_time_copy(size_t bytes, int nbuf, int iters, float* avg_ms);
 
 /* ---- model: Qwen3-arch decoder + MTP head (pipeline.rs) --------------- */
 typedef struct cmf_model_s* cmf_model;
