@@ -38,6 +38,13 @@ struct XSrc {
     const float* xs;
 };
 
+// One weight of a group (an MoE expert): its device blocks.
+struct GemvDesc {
+    const void* w;
+    const void* scale;
+    const float2* rowp;
+};
+
 struct GemvArgs {
     const void* w;
     const void* scale;
@@ -45,6 +52,13 @@ struct GemvArgs {
     float* y;
     int ldy, m, nk, rb0, nrb, row_lo, row_hi, resid, lds;
     XSrc src;
+    // grouped launch (grid.y = job): jobs = [njobs, weight index of job 0,
+    // ...] on the device; job j multiplies desc[jobs[1 + j]] with the
+    // operand at planes + j * planes_stride (xs + 16 j; planes_stride 0: one
+    // operand, one xs for all jobs) into y + j * y_stride.
+    const int* jobs;
+    const GemvDesc* desc;
+    size_t planes_stride, y_stride;
 };
 
 // Kernel instance for m batch rows, operand source xm (0: prepared planes
@@ -58,11 +72,23 @@ GemvKernel q8_kernel(int m, int xm, int ks);
 // y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m.
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
          bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0);
+// Grouped GEMV: up to max_jobs jobs (the device list `jobs`, see GemvArgs),
+// every weight of the group shaped and typed like `proto`; job j reads the
+// prepared operand planes + j * planes_stride (xs + 16 j; stride 0: one
+// operand for all jobs) and writes y + j * y_stride ([m][ldy] each).
+int gemv_grouped(const DevWeight& proto, const GemvDesc* desc, const int* jobs, int max_jobs,
+                 const uint8_t* planes, size_t planes_stride, const float* xs, float* y, size_t y_stride,
+                 int ldy, int m, hipStream_t st);
 
 size_t prep_bytes(const DevWeight& w);
 // Prepared planes (prep_bytes, the layout of prep8_row / prep16_row) and
 // xs[16] of the operand producer src for m batch rows of w.
 int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes, float* xs, hipStream_t st);
+// The same for up to max_jobs jobs of a device job list (GemvArgs::jobs):
+// job j reads rows at src.x + j * x_stride and writes planes + j *
+// planes_stride, xs + 16 j.
+int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const int* jobs, int max_jobs,
+                            size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st);
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
                 hipStream_t st);
 // y[b*ldy + (r - row_lo)] for rows [row_lo, row_hi) and b < m.

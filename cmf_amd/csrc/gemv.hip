@@ -16,8 +16,16 @@ namespace cmf {
 //   XS_CAT : [rms_norm(embed(tok)) * w ; rms_norm(x) * w2], H each (pipeline.rs:3085-3094)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk, uint8_t* __restrict__ planes,
-                                                  float* __restrict__ xs) {
+                                                  float* __restrict__ xs, const int* __restrict__ jobs,
+                                                  size_t x_stride, size_t planes_stride) {
     extern __shared__ float vals[];  // K
+    if (jobs) {  // grouped: blockIdx.y = job
+        const int j = blockIdx.y;
+        if (j >= jobs[0]) return;
+        s.x += j * x_stride;
+        planes += j * planes_stride;
+        xs += 16 * j;
+    }
     __shared__ double red1[8], red2[8];
     __shared__ float redm[8];
     const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
@@ -106,7 +114,20 @@ int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes,
     if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
-                       xs);
+                       xs, (const int*)nullptr, (size_t)0, (size_t)0);
+    return CMF_OK;
+}
+
+int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const int* jobs, int max_jobs,
+                            size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st) {
+    const int K = src.K ? src.K : w.cols;
+    if (m < 1 || m > MAXB) return fail("prep: batch must be 1..16");
+    if (K < 1 || K > w.cols || K > 16384) return fail("prep: operand length must be 1..min(cols, 16384)");
+    if (src.mode == XS_CAT) return fail("prep: no grouped concat producer");
+    if (max_jobs < 1 || max_jobs > 65535 || !jobs) return fail("prep: bad job list");
+    const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
+    hipLaunchKernelGGL(k_prep_src, dim3(m, max_jobs), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk,
+                       planes, xs, jobs, x_stride, planes_stride);
     return CMF_OK;
 }
 
@@ -177,10 +198,38 @@ static int pick_ks(int nk) {
     return k;
 }
 
-int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
-         bool resid, hipStream_t st, int ks_override, int grid_override) {
-    if (m < 1 || m > MAXB) return fail("gemv: batch must be 1..16");
-    if (row_lo < 0 || row_hi > w.rows || row_lo >= row_hi) return fail("gemv: bad row range");
+// Kernel choice and launch of a filled GemvArgs (grid.y = gridy jobs).
+static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int grid_override, int gridy,
+                       hipStream_t st) {
+    const int m = a.m;
+    if (a.src.K == 0) a.src.K = w.cols;
+    // K steps of 1 KiB per row block: q8 chunks of 64 columns, q4 groups of
+    // 4 tiles (128 columns)
+    int ks = ks_override > 0 ? ks_override : pick_ks(w.kchunks);
+    if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);  // no 16-wave instance (registers)
+    if (a.src.mode != XS_GLOBAL) return fail("gemv: the operand must be prepared (launch_prep_src)");
+    size_t lds = lds_bytes(w, m);
+    if (lds > LDSX_MAX) lds = 0;  // planes read in place from global memory
+    a.lds = lds ? 1 : 0;
+    const int xm = lds ? XM_PREP : XM_GLOBAL;
+    GemvKernel k = w.dtype == DT_Q8ROW ? q8_kernel(m, xm, ks)
+                   : w.dtype == DT_Q4T ? q4t_kernel(m, xm, ks)
+                                       : q4tp_kernel(m, xm, ks);
+    if (!k) return fail("gemv: no kernel instance for this shape");
+    const int threads = 64 * ks;
+    const int occ = resident_per_cu(k, threads, lds);
+    if (occ < 1) return fail("gemv: kernel does not fit a CU (LDS or registers)");
+    // one workgroup per row block while the CUs hold them all at once;
+    // grouped launches always give every job its full set
+    int grid = gridy > 1 ? a.nrb : std::min(a.nrb, occ * num_cus());
+    if (grid_override > 0) grid = std::min(grid_override, a.nrb);
+    void* args[] = {&a};
+    CMF_HIP(hipLaunchKernel((const void*)k, dim3(grid, gridy), dim3(threads), args, lds, st));
+    return CMF_OK;
+}
+
+static GemvArgs base_args(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
+                          bool resid) {
     GemvArgs a;
     a.w = w.w;
     a.scale = w.scale;
@@ -194,29 +243,37 @@ int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_
     a.row_lo = row_lo;
     a.row_hi = row_hi;
     a.resid = resid ? 1 : 0;
+    a.lds = 0;
     a.src = src;
-    if (a.src.K == 0) a.src.K = w.cols;
-    // K steps of 1 KiB per row block: q8 chunks of 64 columns, q4 groups of
-    // 4 tiles (128 columns)
-    int ks = ks_override > 0 ? ks_override : pick_ks(w.kchunks);
-    if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);  // no 16-wave instance (registers)
-    if (src.mode != XS_GLOBAL) return fail("gemv: the operand must be prepared (launch_prep_src)");
-    size_t lds = lds_bytes(w, m);
-    if (lds > LDSX_MAX) lds = 0;  // planes read in place from global memory
-    a.lds = lds ? 1 : 0;
-    const int xm = lds ? XM_PREP : XM_GLOBAL;
-    GemvKernel k = w.dtype == DT_Q8ROW ? q8_kernel(m, xm, ks)
-                   : w.dtype == DT_Q4T ? q4t_kernel(m, xm, ks)
-                                       : q4tp_kernel(m, xm, ks);
-    if (!k) return fail("gemv: no kernel instance for this shape");
-    const int threads = 64 * ks;
-    const int occ = resident_per_cu(k, threads, lds);
-    if (occ < 1) return fail("gemv: kernel does not fit a CU (LDS or registers)");
-    int grid = std::min(a.nrb, occ * num_cus());
-    if (grid_override > 0) grid = std::min(grid_override, a.nrb);
-    void* args[] = {&a};
-    CMF_HIP(hipLaunchKernel((const void*)k, dim3(grid), dim3(threads), args, lds, st));
-    return CMF_OK;
+    a.jobs = nullptr;
+    a.desc = nullptr;
+    a.planes_stride = a.y_stride = 0;
+    return a;
+}
+
+int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
+         bool resid, hipStream_t st, int ks_override, int grid_override) {
+    if (m < 1 || m > MAXB) return fail("gemv: batch must be 1..16");
+    if (row_lo < 0 || row_hi > w.rows || row_lo >= row_hi) return fail("gemv: bad row range");
+    GemvArgs a = base_args(w, src, y, ldy, m, row_lo, row_hi, resid);
+    return launch_args(w, a, ks_override, grid_override, 1, st);
+}
+
+int gemv_grouped(const DevWeight& proto, const GemvDesc* desc, const int* jobs, int max_jobs,
+                 const uint8_t* planes, size_t planes_stride, const float* xs, float* y, size_t y_stride,
+                 int ldy, int m, hipStream_t st) {
+    if (m < 1 || m > MAXB) return fail("gemv: batch must be 1..16");
+    if (!desc || !jobs || max_jobs < 1 || max_jobs > 65535) return fail("gemv: bad job list");
+    XSrc src{};
+    src.mode = XS_GLOBAL;
+    src.planes = planes;
+    src.xs = xs;
+    GemvArgs a = base_args(proto, src, y, ldy, m, 0, proto.rows, false);
+    a.jobs = jobs;
+    a.desc = desc;
+    a.planes_stride = planes_stride;
+    a.y_stride = y_stride;
+    return launch_args(proto, a, 0, 0, max_jobs, st);
 }
 
 

@@ -99,7 +99,19 @@ constexpr int SP = 4;  // weight steps per wave and work unit
 enum { XM_PREP = 0, XM_GLOBAL = 2 };
 
 template <int FMT, int NV, int KS, bool HL, int XM>
-__global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
+    GemvArgs a = args;
+    if (a.jobs) {  // grouped launch: this workgroup serves job blockIdx.y
+        const int j = blockIdx.y;
+        if (j >= a.jobs[0]) return;  // uniform over the workgroup
+        const GemvDesc d = a.desc[a.jobs[1 + j]];
+        a.w = d.w;
+        a.scale = d.scale;
+        a.rowp = d.rowp;
+        a.src.planes += j * a.planes_stride;
+        if (a.planes_stride) a.src.xs += 16 * j;  // stride 0: one operand for all jobs
+        a.y += j * a.y_stride;
+    }
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4;
@@ -278,7 +290,19 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs a) {
 // one MFMA, A row p*m + b holding plane p of batch row b; otherwise one MFMA
 // per plane.
 template <int KS, bool PK, int XM>
-__global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs a) {
+__global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
+    GemvArgs a = args;
+    if (a.jobs) {  // grouped launch: this workgroup serves job blockIdx.y
+        const int j = blockIdx.y;
+        if (j >= a.jobs[0]) return;  // uniform over the workgroup
+        const GemvDesc d = a.desc[a.jobs[1 + j]];
+        a.w = d.w;
+        a.scale = d.scale;
+        a.rowp = d.rowp;
+        a.src.planes += j * a.planes_stride;
+        if (a.planes_stride) a.src.xs += 16 * j;  // stride 0: one operand for all jobs
+        a.y += j * a.y_stride;
+    }
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4;

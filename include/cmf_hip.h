@@ -129,6 +129,32 @@ int cmf_model_set_head(cmf_model m, const cmf_tensor* lm_head, const float* fina
 int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh_proj,
                       const cmf_layer_desc* layer, const float* norm);
 
+/* ---- MoE FFN (moe_ffn / moe_block) ------------------------------------ */
+typedef struct cmf_moe_s* cmf_moe;
+
+/* A routed-expert FFN layer (MoeFfn, pipeline.rs:10868-11045): n_experts
+ * SwiGLU experts gate/up [inter x hidden], down [hidden x inter], softmax
+ * router, top_k experts per token, norm_topk_prob and routed_scaling as
+ * moe_route (pipeline.rs:10780-10841).  No shared expert, expert bias, mask
+ * or tau trimming (the Qwen3-MoE configuration). */
+int cmf_moe_create(int n_experts, int hidden, int inter, int top_k, int norm_topk, float routed_scaling,
+                   cmf_moe* out);
+int cmf_moe_free(cmf_moe m);
+/* Upload expert e (quant.rs layouts; q8, q4t or q4tp; every expert with the
+ * same codecs).  >0 (declined) for a codec without a device kernel. */
+int cmf_moe_set_expert(cmf_moe m, int e, const cmf_tensor* gate, const cmf_tensor* up, const cmf_tensor* down);
+/* moe_ffn for a verify batch of b <= 16 tokens: route router_logits [b][ne],
+ * run every (token, expert) pair grouped by expert, out [b][hidden] =
+ * sum over the token's experts, in routing order, of w * expert(x).  Host
+ * pointers; idx_out / w_out [b][top_k] (nullable) receive the routing. */
+int cmf_moe_ffn(cmf_moe m, const float* x, const float* router_logits, int b, float* out, int32_t* idx_out,
+                float* w_out);
+/* The same on device pointers (inputs resident in HBM). */
+int cmf_moe_ffn_dev(cmf_moe m, const float* d_x, const float* d_logits, int b, float* d_out);
+/* moe_block (gpu.rs:2482): one token x [hidden], the caller's routing
+ * (experts[njobs], weights[njobs], njobs <= top_k) -> out [hidden]. */
+int cmf_moe_block(cmf_moe m, const float* x, const int32_t* experts, const float* weights, int njobs, float* out);
+
 /* SamplerConfig (sampler.rs:88-121).  Penalised configs are declined by the
  * device sampler (speculation is gated off under penalties,
  * pipeline.rs:2035-2037). */

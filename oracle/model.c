@@ -428,11 +428,13 @@ int or_moe_route(const float* lg, int ne, int top_k, int norm_topk, float routed
     return k;
 }
 
-void or_moe_ffn(const or_qt* ex, int ne, int top_k, const float* rl, const float* x, int hidden,
-                float* out, int threads) {
+/* moe_ffn_cpu's serial expert loop (pipeline.rs:11017-11030): out starts at
+ * 0, each routed expert in routing order adds w * dense_ffn(expert, x). */
+void or_moe_ffn(const or_qt* ex, int ne, int top_k, int norm_topk, float routed_scaling, const float* rl,
+                const float* x, int hidden, float* out, int threads) {
     int idx[256];
     float w[256];
-    int k = or_moe_route(rl, ne, top_k, 1, 1.0f, idx, w);
+    int k = or_moe_route(rl, ne, top_k, norm_topk, routed_scaling, idx, w);
     int I = ex[0].rows;
     float* g = (float*)malloc(sizeof(float) * (size_t)I);
     float* u = (float*)malloc(sizeof(float) * (size_t)I);

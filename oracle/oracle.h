@@ -191,8 +191,8 @@ int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const
  * 10868-11045). experts: 3*ne tensors (gate, up, down per expert). */
 int or_moe_route(const float* logits, int ne, int top_k, int norm_topk, float routed_scaling,
                  int* idx, float* w);
-void or_moe_ffn(const or_qt* experts, int ne, int top_k, const float* router_logits,
-                const float* x, int hidden, float* out, int threads);
+void or_moe_ffn(const or_qt* experts, int ne, int top_k, int norm_topk, float routed_scaling,
+                const float* router_logits, const float* x, int hidden, float* out, int threads);
 
 #ifdef __cplusplus
 }

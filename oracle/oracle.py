@@ -107,7 +107,7 @@ def lib():
             "or_decode": (C.c_int, [C.POINTER(Model), C.POINTER(State), P, C.c_int, P, C.c_int, C.c_int,
                                     C.POINTER(GenCfg), P, P, C.POINTER(GenStats)]),
             "or_moe_route": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, P, P]),
-            "or_moe_ffn": (None, [P, C.c_int, C.c_int, P, P, C.c_int, P, C.c_int]),
+            "or_moe_ffn": (None, [P, C.c_int, C.c_int, C.c_int, C.c_float, P, P, C.c_int, P, C.c_int]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -239,3 +239,24 @@ class OracleModel:
         out = np.empty(self.c["vocab"], np.float32)
         lib().or_logits(C.byref(self.m), _p(np.ascontiguousarray(h, np.float32)), _p(out))
         return out
+
+
+def moe_route(logits, top_k, norm_topk=True, routed_scaling=1.0):
+    """moe_route (pipeline.rs:10780-10841): (idx [k], w [k]) for one token."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    idx = np.empty(max(top_k, 1), np.int32)
+    w = np.empty(max(top_k, 1), np.float32)
+    k = lib().or_moe_route(_p(lg), len(lg), top_k, 1 if norm_topk else 0, routed_scaling, _p(idx), _p(w))
+    return idx[:k], w[:k]
+
+
+def moe_ffn(experts, top_k, router_logits, x, norm_topk=True, routed_scaling=1.0, threads=8):
+    """moe_ffn_cpu for one token: experts = [{"gate", "up", "down"}, ...]."""
+    keep = []
+    arr = (QT * (3 * len(experts)))(*[qt(ex[n], keep) for ex in experts for n in ("gate", "up", "down")])
+    lg = np.ascontiguousarray(router_logits, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(experts[0]["down"]["rows"], np.float32)
+    lib().or_moe_ffn(C.cast(arr, C.c_void_p), len(experts), top_k, 1 if norm_topk else 0, routed_scaling, _p(lg), _p(x), len(x),
+                     _p(out), threads)
+    return out
