@@ -77,6 +77,41 @@ def time_gemv(cmf, t, m, copies, iters=200, warmup=20, seed=7):
     return ms.value
 
 
+def moe_layer(cmf, synth, b=5, ne=128, hidden=2048, inter=768, top_k=8):
+    """the MoE FFN of an M=5 verify batch (router logits
+    N(0,1), 128 q4t experts, top-8) and the 4096x2048 q8 attention projection
+    at M=5, inputs resident in HBM.  Bytes: every distinct routed expert's
+    gate/up/down weights once + activations; the projection's weights."""
+    import ctypes as C
+    from cmf_amd.moe import MoE
+    ex = [{"gate": synth.q4t_uniform(900 + 3 * e, inter, hidden), "up": synth.q4t_uniform(901 + 3 * e, inter, hidden),
+           "down": synth.q4t_uniform(902 + 3 * e, hidden, inter)} for e in range(ne)]
+    moe = MoE(ne, hidden, inter, top_k, ex)
+    x = synth.normal(5001, b * hidden).reshape(b, hidden)
+    lg = synth.normal(5002, b * ne).reshape(b, ne)
+    _, idx, _ = moe.ffn(x, lg)
+    distinct = len(set(idx.ravel().tolist()))
+    dx, dl, do = cmf.DevBuf(x.nbytes), cmf.DevBuf(lg.nbytes), cmf.DevBuf(x.nbytes)
+    dx.upload(x)
+    dl.upload(lg)
+    ms = C.c_float()
+    cmf.check(cmf.lib().cmf_time_moe(moe.h, dx.p, dl.p, b, do.p, 10, 200, C.byref(ms)))
+    per_expert = 3 * inter * (hidden // 32) * 18
+    moe_bytes = distinct * per_expert + b * (hidden + ne) * 4 + b * hidden * 4
+    t8 = synth.q8_uniform(5003, 4096, 2048)
+    pms = time_gemv(cmf, t8, b, copies=16)
+    pbytes = 4096 * 2048 + 4096 * 4 + b * (2048 + 4096) * 4
+    moe.free()
+    for d in (dx, dl, do):
+        d.free()
+    return {"workload": f"M={b} verify tokens, {ne} q4t experts (hidden {hidden}, FFN {inter}), top-{top_k}, "
+                        "router logits N(0,1); + q8 4096x2048 projection",
+            "distinct_experts": distinct, "moe_us": round(ms.value * 1e3, 2),
+            "moe_GB/s": round(moe_bytes / ms.value / 1e6, 1), "moe_bytes": moe_bytes,
+            "proj_us": round(pms * 1e3, 2), "proj_GB/s": round(pbytes / pms / 1e6, 1),
+            "layer_us": round((ms.value + pms) * 1e3, 2)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -86,6 +121,8 @@ def main():
     ap.add_argument("--ctx", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemv", action="store_true", help="skip the GEMV sweep")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE verify layer (config 5)")
+    ap.add_argument("--moe-only", action="store_true", help="only the MoE verify layer (profiling runs)")
     ap.add_argument("--gemv-only", action="store_true", help="only the GEMV sweep (profiling runs)")
     ap.add_argument("--profile-gemv", action="store_true",
                     help="only the HBM-counter workload: 20 plain copies of 64 MiB (counter calibration), then "
@@ -150,6 +187,13 @@ def main():
         cmf.check(cmf.lib().cmf_time_copy(COPY_BYTES, 4, 20, C.byref(ms)))
         out["device_copy_GB/s"] = round(2 * COPY_BYTES / ms.value / 1e6, 1)  # read + write, 64 MiB
     if args.gemv_only:
+        print(json.dumps(out))
+        return
+
+    # ---------------- MoE verify layer ----------------
+    if not args.no_moe:
+        out["moe"] = moe_layer(cmf, synth)
+    if args.moe_only:
         print(json.dumps(out))
         return
 

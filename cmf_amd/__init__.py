@@ -101,6 +101,7 @@ SIGNATURES = {
     "cmf_moe_ffn": (_I, [_P, _P, _P, _I, _P, _P, _P]),
     "cmf_moe_ffn_dev": (_I, [_P, _P, _P, _I, _P]),
     "cmf_moe_block": (_I, [_P, _P, _P, _P, _I, _P]),
+    "cmf_time_moe": (_I, [_P, _P, _P, _I, _P, _I, _I, C.POINTER(_F)]),
     "cmf_model_create": (_I, [C.POINTER(ModelConfig), C.POINTER(_P)]),
     "cmf_model_free": (_I, [_P]),
     "cmf_model_set_layer": (_I, [_P, _I, C.POINTER(LayerDesc)]),

@@ -81,42 +81,68 @@ __global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ log
 }
 
 // jobs = [njobs, expert of job 0, ...] (experts in increasing order);
-// slot[t * k + i] = job of token t's rank-i expert.  One workgroup.
+// slot[t * k + i] = job of token t's rank-i expert.  One workgroup of 256:
+// per-wave ballots and popcounts number the used experts.
 __global__ __launch_bounds__(256) void k_moe_jobs(const int* __restrict__ idx, int b, int k, int ne,
                                                   int* __restrict__ jobs, int* __restrict__ slot) {
     __shared__ int job_of[MOE_MAX_EXPERTS];
-    const int tid = threadIdx.x;
-    for (int e = tid; e < ne; e += blockDim.x) {
-        int used = 0;
-        for (int i = 0; i < b * k; i++) used |= idx[i] == e;
-        job_of[e] = used;
+    __shared__ int used[MOE_MAX_EXPERTS];
+    __shared__ int wave_base[MOE_MAX_EXPERTS / 64 + 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    for (int e = tid; e < ne; e += blockDim.x) used[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < b * k; i += blockDim.x) used[idx[i]] = 1;  // benign same-value races
+    __syncthreads();
+    // expert e sits in chunk e / 64, lane e % 64; chunk c is counted by wave c % 4
+    const int nch = (ne + 63) / 64;
+    for (int c = tid >> 6; c < nch; c += blockDim.x >> 6) {
+        const int e = c * 64 + lane;
+        const bool u = e < ne && used[e];
+        const unsigned long long bal = __ballot(u);
+        if (lane == 0) wave_base[c] = __popcll(bal);
+        if (e < ne) job_of[e] = u ? (int)__popcll(bal & ((1ull << lane) - 1ull)) : -1;
     }
     __syncthreads();
     if (tid == 0) {
         int n = 0;
-        for (int e = 0; e < ne; e++) {
-            if (job_of[e]) {
-                jobs[1 + n] = e;
-                job_of[e] = n++;
-            } else {
-                job_of[e] = -1;
-            }
+        for (int c = 0; c < nch; c++) {
+            const int cnt = wave_base[c];
+            wave_base[c] = n;
+            n += cnt;
         }
         jobs[0] = n;
+    }
+    __syncthreads();
+    for (int e = tid; e < ne; e += blockDim.x) {
+        if (job_of[e] >= 0) {
+            job_of[e] += wave_base[e >> 6];
+            jobs[1 + job_of[e]] = e;
+        }
     }
     __syncthreads();
     for (int i = tid; i < b * k; i += blockDim.x) slot[i] = job_of[idx[i]];
 }
 
+// out[t][h] = sum over ranks i (in order, from 0) of w[t][i] * yd[job][t][h];
+// grid (hidden / 256, b): the k job rows of a thread are requested together.
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ yd, size_t y_stride, int ldy,
                                                      const int* __restrict__ slot, const float* __restrict__ w,
                                                      int k, int hidden, float* __restrict__ out) {
-    const int t = blockIdx.x;
-    for (int h = threadIdx.x; h < hidden; h += blockDim.x) {
-        float acc = 0.0f;
-        for (int i = 0; i < k; i++) acc += w[t * k + i] * yd[slot[t * k + i] * y_stride + (size_t)t * ldy + h];
-        out[(size_t)t * hidden + h] = acc;
+    __shared__ int js[MOE_MAX_TOPK];
+    __shared__ float ws[MOE_MAX_TOPK];
+    const int t = blockIdx.y, h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (threadIdx.x < k) {
+        js[threadIdx.x] = slot[t * k + threadIdx.x];
+        ws[threadIdx.x] = w[t * k + threadIdx.x];
     }
+    __syncthreads();
+    if (h >= hidden) return;
+    float v[MOE_MAX_TOPK];
+#pragma unroll 8
+    for (int i = 0; i < k; i++) v[i] = yd[js[i] * y_stride + (size_t)t * ldy + h];
+    float acc = 0.0f;
+    for (int i = 0; i < k; i++) acc += ws[i] * v[i];
+    out[(size_t)t * hidden + h] = acc;
 }
 
 }  // namespace cmf
@@ -187,7 +213,8 @@ static int moe_experts(cmf_moe m, const float* d_x, int b, int k, float* d_out, 
     if (rc == CMF_OK)
         rc = gemv_grouped(m->down[0], m->d_down, m->jobs, mj, m->ph, m->ph_stride, m->xsh, m->yd, yd_stride, H, b, s);
     if (rc != CMF_OK) return rc;
-    hipLaunchKernelGGL(k_moe_combine, dim3(b), dim3(256), 0, s, m->yd, yd_stride, H, m->slot, m->w, k, H, d_out);
+    hipLaunchKernelGGL(k_moe_combine, dim3((H + 255) / 256, b), dim3(256), 0, s, m->yd, yd_stride, H, m->slot, m->w,
+                       k, H, d_out);
     return CMF_OK;
 }
 
@@ -340,6 +367,28 @@ int cmf_moe_ffn(cmf_moe m, const float* x, const float* router_logits, int b, fl
     if (w_out) CMF_HIP(hipMemcpyAsync(w_out, m->w, sizeof(float) * b * m->top_k, hipMemcpyDeviceToHost, s));
     CMF_HIP(hipStreamSynchronize(s));
     return CMF_OK;
+}
+
+int cmf_time_moe(cmf_moe m, const float* d_x, const float* d_logits, int b, float* d_out, int warmup, int iters,
+                 float* avg_ms) {
+    if (!avg_ms || iters < 1 || warmup < 0) return fail("time_moe: bad arguments");
+    for (int i = 0; i < warmup; i++)
+        if (cmf_moe_ffn_dev(m, d_x, d_logits, b, d_out) != CMF_OK) return CMF_ERR;
+    hipStream_t s = stream();
+    hipEvent_t e0, e1;
+    CMF_HIP(hipEventCreate(&e0));
+    CMF_HIP(hipEventCreate(&e1));
+    CMF_HIP(hipEventRecord(e0, s));
+    int rc = CMF_OK;
+    for (int i = 0; i < iters && rc == CMF_OK; i++) rc = cmf_moe_ffn_dev(m, d_x, d_logits, b, d_out);
+    CMF_HIP(hipEventRecord(e1, s));
+    CMF_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_ms = ms / iters;
+    return rc;
 }
 
 int cmf_moe_block(cmf_moe m, const float* x, const int32_t* experts, const float* weights, int njobs, float* out) {

@@ -151,6 +151,11 @@ int cmf_moe_ffn(cmf_moe m, const float* x, const float* router_logits, int b, fl
                 float* w_out);
 /* The same on device pointers (inputs resident in HBM). */
 int cmf_moe_ffn_dev(cmf_moe m, const float* d_x, const float* d_logits, int b, float* d_out);
+/* Average device time (ms, HIP events on the library stream) of `iters`
+ * cmf_moe_ffn_dev calls after `warmup` ones.  No counterpart in the
+ * reference: a measurement helper. */
+int cmf_time_moe(cmf_moe m, const float* d_x, const float* d_logits, int b, float* d_out, int warmup, int iters,
+                 float* avg_ms);
 /* moe_block (gpu.rs:2482): one token x [hidden], the caller's routing
  * (experts[njobs], weights[njobs], njobs <= top_k) -> out [hidden]. */
 int cmf_moe_block(cmf_moe m, const float* x, const int32_t* experts, const float* weights, int njobs, float* out);
