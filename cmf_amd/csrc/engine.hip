@@ -128,6 +128,43 @@ int build_cat(DevWeight& w, const std::vector<const cmf_tensor*>& ts) {
     return build_q4(w, s);
 }
 
+// gate and up as one weight whose row blocks hold 8 gate rows then the 8
+// matching up rows, so that the GEMV's SwiGLU epilogue sees g and u of the
+// same index in one row block.
+int build_swiglu(DevWeight& w, const cmf_tensor* g, const cmf_tensor* u) {
+    const int dt = g->dtype, cols = g->cols, I = g->rows;
+    if (u->dtype != dt || u->cols != cols || u->rows != I) return fail("gate/up must share dtype and shape");
+    if (I % 8) return fail("gate/up rows must be a multiple of 8");
+    if (dt == DT_Q8ROW) {
+        std::vector<const int8_t*> rp;
+        std::vector<float> rs;
+        for (int r0 = 0; r0 < I; r0 += 8)
+            for (const cmf_tensor* t : {g, u})
+                for (int r = r0; r < r0 + 8; r++) {
+                    rp.push_back(t->q + (size_t)r * cols);
+                    rs.push_back(t->row_scale[r]);
+                }
+        return build_q8(w, 2 * I, cols, rp.data(), rs.data());
+    }
+    Q4Src sg, su, s;
+    fill_q4src(sg, dt, I, cols, g->bytes, 0);
+    fill_q4src(su, dt, I, cols, u->bytes, 0);
+    s.dtype = dt;
+    s.cols = cols;
+    s.code_stride = sg.code_stride;
+    for (int r0 = 0; r0 < I; r0 += 8)
+        for (const Q4Src* t : {&sg, &su})
+            for (int r = r0; r < r0 + 8; r++) {
+                s.rowbase.push_back(t->rowbase[r]);
+                if (dt == DT_Q4TP) {
+                    s.codes.push_back(t->codes[r]);
+                    s.params.push_back(t->params[r]);
+                }
+            }
+    s.rows = 2 * I;
+    return build_q4(w, s);
+}
+
 int upload_layer(cmf_model_s* m, LayerDev& l, const cmf_layer_desc* d, bool kv) {
     const auto& c = m->c;
     const int H = c.hidden, hd = c.head_dim, Q = c.n_heads * hd, KV = c.n_kv * hd, I = c.inter;
@@ -144,7 +181,7 @@ int upload_layer(cmf_model_s* m, LayerDev& l, const cmf_layer_desc* d, bool kv) 
     free_weight(l.gu);
     free_weight(l.down);
     if (build_cat(l.qkv, {&d->wq, &d->wk, &d->wv}) || build_cat(l.wo, {&d->wo}) ||
-        build_cat(l.gu, {&d->gate, &d->up}) || build_cat(l.down, {&d->down}))
+        build_swiglu(l.gu, &d->gate, &d->up) || build_cat(l.down, {&d->down}))
         return CMF_ERR;
     if (kv && !l.kc) {
         const size_t n = (size_t)c.n_kv * c.max_seq * hd;
@@ -175,11 +212,11 @@ XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
 }
 
 // W x with the operand of src: a one-workgroup-per-row producer writes the
-// prepared planes (norm / SwiGLU / concat evaluated once, not per GEMV
+// prepared planes (norm / concat / rows evaluated once, not per GEMV
 // workgroup), the GEMV copies them to LDS (or reads them in place when they
 // do not fit).
 int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int nb, bool resid,
-           hipStream_t s) {
+           hipStream_t s, int epi = EPI_NONE) {
     for (int b0 = 0; b0 < nb; b0 += MAXB) {
         const int mb = std::min(MAXB, nb - b0);
         XSrc sb = src;
@@ -191,7 +228,7 @@ int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int 
         g.mode = XS_GLOBAL;
         g.planes = m->planes;
         g.xs = m->xs;
-        rc = gemv(w, g, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s);
+        rc = gemv(w, g, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s, 0, 0, epi);
         if (rc != CMF_OK) return rc;
     }
     return CMF_OK;
@@ -201,8 +238,8 @@ int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int 
 // + i (forward_layers_span, pipeline.rs:7981-8700):
 //   h += Wo attn(qk-norm/RoPE(Wqkv rms_norm(h)))
 //   h += Wdown (silu(Wg rms_norm(h)) * Wu rms_norm(h))
-// The norms and SwiGLU are evaluated inside the GEMVs that consume them and
-// the residual adds are their epilogues.
+// The norms are evaluated by the GEMVs that consume them, SwiGLU is the
+// gate|up GEMV's epilogue and the residual adds are epilogues too.
 void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int padd, int max_len,
                hipStream_t s) {
     const auto& c = m->c;
@@ -211,24 +248,35 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
     gemv_f(m, l.qkv, src_norm(h, H, l.in_norm, c.eps), m->qkv_out, QKV, nb, false, s);
     // the attention kernel holds at most 32 query heads per kv head
     const int rows_per = std::max(1, 32 / (nh / nkv));
+    // one attention launch: its merge also writes wo's prepared operand
+    const bool merge_prep = nb <= rows_per && nb <= MAXB && nh <= 64;
     for (int b0 = 0; b0 < nb; b0 += rows_per) {
         AttnArgs at{m->qkv_out + (size_t)b0 * QKV, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq,
                     std::min(rows_per, nb - b0), nh, nkv, c.eps, pb, padd + b0, m->pm, m->pl, m->po, m->nch_cap,
                     m->ao + (size_t)b0 * nh * hd, 1};
-        launch_attention(at, max_len, s);
+        if (merge_prep) launch_attention(at, max_len, s, &l.wo, m->planes, m->xs);
+        else launch_attention(at, max_len, s);
     }
-    XSrc ra{};
-    ra.mode = XS_ROWS;
-    ra.x = m->ao;
-    ra.ldx = nh * hd;
-    gemv_f(m, l.wo, ra, h, H, nb, true, s);
-    gemv_f(m, l.gu, src_norm(h, H, l.post_norm, c.eps), m->gu_out, 2 * I, nb, false, s);
-    XSrc sg{};
-    sg.mode = XS_SILU;
-    sg.x = m->gu_out;
-    sg.ldx = 2 * I;
-    sg.K = I;
-    gemv_f(m, l.down, sg, h, H, nb, true, s);
+    if (merge_prep) {
+        XSrc g{};
+        g.mode = XS_GLOBAL;
+        g.planes = m->planes;
+        g.xs = m->xs;
+        gemv(l.wo, g, h, H, nb, 0, l.wo.rows, true, s);
+    } else {
+        XSrc ra{};
+        ra.mode = XS_ROWS;
+        ra.x = m->ao;
+        ra.ldx = nh * hd;
+        gemv_f(m, l.wo, ra, h, H, nb, true, s);
+    }
+    // gate|up with the SwiGLU epilogue: gu_out [nb][I] = silu(g) * u
+    gemv_f(m, l.gu, src_norm(h, H, l.post_norm, c.eps), m->gu_out, I, nb, false, s, EPI_SWIGLU);
+    XSrc sd{};
+    sd.mode = XS_ROWS;
+    sd.x = m->gu_out;
+    sd.ldx = I;
+    gemv_f(m, l.down, sd, h, H, nb, true, s);
 }
 
 // Trunk forward of nb rows in m->hv (embeddings in, final hidden rows out,

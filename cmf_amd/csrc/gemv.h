@@ -51,6 +51,7 @@ struct GemvArgs {
     const float2* rowp;
     float* y;
     int ldy, m, nk, rb0, nrb, row_lo, row_hi, resid, lds;
+    int epi;  // EPI_SWIGLU: rows interleaved 8 gate / 8 up per block, y = silu(g) * u [m][rows / 2]
     XSrc src;
     // grouped launch (grid.y = job): jobs = [njobs, weight index of job 0,
     // ...] on the device; job j multiplies desc[jobs[1 + j]] with the
@@ -69,9 +70,12 @@ GemvKernel q4t_kernel(int m, int xm, int ks);
 GemvKernel q4tp_kernel(int m, int xm, int ks);
 GemvKernel q8_kernel(int m, int xm, int ks);
 
-// y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m.
+enum { EPI_NONE = 0, EPI_SWIGLU = 1 };
+
+// y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m, from a
+// prepared operand (XS_GLOBAL; launch_prep_src writes it).
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
-         bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0);
+         bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0, int epi = EPI_NONE);
 // Grouped GEMV: up to max_jobs jobs (the device list `jobs`, see GemvArgs),
 // every weight of the group shaped and typed like `proto`; job j reads the
 // prepared operand planes + j * planes_stride (xs + 16 j; stride 0: one

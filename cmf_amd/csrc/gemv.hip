@@ -229,7 +229,7 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
 }
 
 static GemvArgs base_args(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
-                          bool resid) {
+                          bool resid, int epi = EPI_NONE) {
     GemvArgs a;
     a.w = w.w;
     a.scale = w.scale;
@@ -248,14 +248,17 @@ static GemvArgs base_args(const DevWeight& w, const XSrc& src, float* y, int ldy
     a.jobs = nullptr;
     a.desc = nullptr;
     a.planes_stride = a.y_stride = 0;
+    a.epi = epi;
     return a;
 }
 
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
-         bool resid, hipStream_t st, int ks_override, int grid_override) {
+         bool resid, hipStream_t st, int ks_override, int grid_override, int epi) {
     if (m < 1 || m > MAXB) return fail("gemv: batch must be 1..16");
     if (row_lo < 0 || row_hi > w.rows || row_lo >= row_hi) return fail("gemv: bad row range");
-    GemvArgs a = base_args(w, src, y, ldy, m, row_lo, row_hi, resid);
+    if (epi == EPI_SWIGLU && (row_lo != 0 || row_hi != w.rows || w.rows % 16 || resid))
+        return fail("gemv: the SwiGLU epilogue needs the whole interleaved gate/up weight, no residual");
+    GemvArgs a = base_args(w, src, y, ldy, m, row_lo, row_hi, resid, epi);
     return launch_args(w, a, ks_override, grid_override, 1, st);
 }
 

@@ -94,7 +94,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // 8..15 the lo plane of batch row r - 8, one MFMA per tile; the two halves
 // are added at the end.  XM: where the prepared activation operand is read
 // (XM_PREP: copied to LDS first, XM_GLOBAL: in place, for operands larger
-// than the LDS budget).
+// than the LDS budget).  (Producing the operand in every workgroup from the
+// raw rows instead of one producer launch per GEMV was measured 1.3-2x
+// slower per GEMV on MI355X: the per-workgroup staging sits on the critical
+// path of these latency-bound launches.)
 constexpr int SP = 4;  // weight steps per wave and work unit
 enum { XM_PREP = 0, XM_GLOBAL = 2 };
 
@@ -247,7 +250,18 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
                 for (int v = 0; v < NV; v++) acc[v] += __shfl_xor(acc[v], 32);
             }
             const int row = (a.rb0 + rb) * 16 + r;
-            if (row >= a.row_lo && row < a.row_hi && (!HL || s < 2)) {
+            if (a.epi == EPI_SWIGLU) {
+                // rows r < 8 gate, r + 8 the matching up row (lane ^ 8):
+                // y[b][8 rb + r] = silu(g) * u (inference.rs:14-16)
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const int b = 4 * s + v;
+                    const float val = acc[v] * lxs[b & 15] * 16777216.0f;
+                    const float u = __shfl_xor(val, 8);
+                    if (r < 8 && b < M && (!HL || s < 2))
+                        a.y[(size_t)b * a.ldy + (a.rb0 + rb) * 8 + r] = (val / (1.0f + expf(-val))) * u;
+                }
+            } else if (row >= a.row_lo && row < a.row_hi && (!HL || s < 2)) {
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
                     const int b = 4 * s + v;
@@ -412,7 +426,19 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
                 __builtin_amdgcn_wave_barrier();
             }
             const int row = (a.rb0 + rb) * 16 + r;
-            if (row >= a.row_lo && row < a.row_hi) {
+            if (a.epi == EPI_SWIGLU) {
+                // rows r < 8 gate, r + 8 the matching up row (lane ^ 8)
+                const float rs = ((const float*)a.scale)[row];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int b = 4 * s + v;
+                    const float tt = f0[v] + f1[v] * 0.0078125f + f2[v] * 6.103515625e-05f;
+                    const float val = (tt * lxs[b & 15]) * rs;
+                    const float u = __shfl_xor(val, 8);
+                    if (r < 8 && b < M)
+                        a.y[(size_t)b * a.ldy + (a.rb0 + rb) * 8 + r] = (val / (1.0f + expf(-val))) * u;
+                }
+            } else if (row >= a.row_lo && row < a.row_hi) {
                 const float rs = ((const float*)a.scale)[row];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {

@@ -212,6 +212,31 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     attn_merge_row(a.pm, a.pl, a.po, a.nch, (size_t)rh, used, a.out + (size_t)rh * 128);
 }
 
+// Merge + the next GEMV's prepared operand: one workgroup per row b, one
+// wave per head (looping past 16 heads); the merged row [nh * 128] stays in
+// LDS, its max|x| is reduced and the row is written as the operand planes
+// of a weight of format fmt (prep8_row / prep16_row layout, nb rows).
+__global__ __launch_bounds__(1024) void k_attn_merge_prep(AttnArgs a, int fmt, int nk, uint8_t* __restrict__ planes,
+                                                         float* __restrict__ xs) {
+    extern __shared__ float rowv[];  // nh * 128
+    __shared__ float redm[16];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+    const int used = (*a.pbase + a.padd + b + ATT_C) / ATT_C;
+    for (int h = wave; h < a.nh; h += nw)
+        attn_merge_row(a.pm, a.pl, a.po, a.nch, (size_t)b * a.nh + h, used, rowv + h * 128);
+    __syncthreads();
+    const int K = a.nh * 128;
+    float am = 0.f;
+    for (int i = tid; i < K; i += blockDim.x) am = fmaxf(am, fabsf(rowv[i]));
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    if (lane == 0) redm[wave] = am;
+    __syncthreads();
+    am = 0.f;
+    for (int q = 0; q < nw; q++) am = fmaxf(am, redm[q]);
+    if (fmt == DT_Q8ROW) prep8_row(rowv, K, am, nk, b, gridDim.x, planes, xs, tid, blockDim.x);
+    else prep16_row(rowv, K, am, nk, b, gridDim.x, planes, xs, tid, blockDim.x);
+}
+
 // Decode attention of one layer for the nb rows at positions pos0 .. pos0+nb-1
 // (pos0 = *pbase + padd), one workgroup per (kv head g, 64-position chunk c):
 //   - q-norm + RoPE of the hpk query heads of g for every row (Q in LDS);
@@ -390,10 +415,19 @@ void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo
     hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
 }
 
-void launch_attention(const AttnArgs& a, int max_len, hipStream_t st) {
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, const DevWeight* next, uint8_t* planes,
+                      float* xs) {
     const int nch = (max_len + ATT_C - 1) / ATT_C;
     hipLaunchKernelGGL(k_attention, dim3(a.nkv, nch), dim3(256), 0, st, a);
-    if (a.attend) hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
+    if (!a.attend) return;
+    if (next) {
+        const int nk = next->dtype == DT_Q8ROW ? next->kchunks : next->kchunks * 4;
+        const int threads = 64 * std::min(16, a.nh);
+        hipLaunchKernelGGL(k_attn_merge_prep, dim3(a.nb), dim3(threads), (size_t)a.nh * 128 * sizeof(float), st, a,
+                           next->dtype, nk, planes, xs);
+    } else {
+        hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
+    }
 }
 
 
