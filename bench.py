@@ -28,6 +28,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8000.0  # GB/s, MI355X HBM3E
+PEAK_F16 = 2500.0  # TFLOP/s, MI355X dense f16 MFMA
 COPY_BYTES = 64 << 20  # counter-calibration copy (read + write of this many bytes)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4t_gemv_12288x4096_m1_traffic.txt")
 
@@ -75,6 +76,30 @@ def time_gemv(cmf, t, m, copies, iters=200, warmup=20, seed=7):
     for w in ws:
         w.free()
     return ms.value
+
+
+def gemm_sweep(cmf, synth):
+    """Large-batch q4t GEMM (prefill / matmat b > 16) on the config-2 gate/up
+    shape: MFMA rate counting both f16 halves of the operand (2 MFMAs per
+    weight tile), against the 2.5 PFLOP/s dense f16 peak."""
+    import ctypes as C
+    t = synth.q4t_uniform(77, 12288, 4096)
+    w = cmf.Weight(t["dtype"], 12288, 4096, payload=t["bytes"])
+    res = []
+    for m in (64, 256, 2048):
+        x = synth.normal(78, m * 4096).reshape(m, 4096)
+        dx, dy = cmf.DevBuf(x.nbytes), cmf.DevBuf(m * 12288 * 4)
+        dx.upload(x)
+        ms = C.c_float()
+        cmf.check(cmf.lib().cmf_time_gemm(w.h, dx.p, m, dy.p, 3, 20, C.byref(ms)))
+        mfma_flops = 2 * 2.0 * m * 12288 * 4096  # hi + lo halves
+        res.append({"m": m, "us": round(ms.value * 1e3, 1),
+                    "TFLOP/s": round(2.0 * m * 12288 * 4096 / ms.value / 1e9, 1),
+                    "mfma_util": round(mfma_flops / ms.value / 1e9 / PEAK_F16, 4)})
+        dx.free()
+        dy.free()
+    w.free()
+    return res
 
 
 def moe_layer(cmf, synth, b=5, ne=128, hidden=2048, inter=768, top_k=8):
@@ -186,6 +211,7 @@ def main():
         ms = C.c_float()
         cmf.check(cmf.lib().cmf_time_copy(COPY_BYTES, 4, 20, C.byref(ms)))
         out["device_copy_GB/s"] = round(2 * COPY_BYTES / ms.value / 1e6, 1)  # read + write, 64 MiB
+        out["gemm"] = gemm_sweep(cmf, synth)
     if args.gemv_only:
         print(json.dumps(out))
         return

@@ -1,0 +1,247 @@
+// Dequant GEMM for large batches (q4t_matmat / q4tp_matmat with b > 16,
+// qtensor.rs:5830-5960 / 5422-5680, and the prefill's dense contractions):
+// Y[b][n] = sum_k X[b][k] W[n][k] for b < M (any M), W in the q4t / q4tp
+// device layout of the GEMV kernels.
+//
+// Tiling (MFMA f32 16x16x32 f16): a workgroup of 4 waves owns 64 batch rows
+// x 64 GRB weight rows (wave w holds GRB row blocks in registers), and walks
+// K in steps of 128 columns (4 tiles):
+//   - the operand step (hi / lo f16 planes of 64 rows x 4 tiles and their
+//     tile biases, 33 KiB) is loaded into registers one step ahead and
+//     written to the other half of a double-buffered LDS tile after the
+//     current step's MFMAs (one barrier per step);
+//   - the weights of the next step (4 row blocks x 1 KiB + scales per wave)
+//     are requested before the current step is computed;
+//   - per tile and row block: the nibbles become f16 denormals n * 2^-24
+//     (one mask per pair), the MFMA accumulator starts at the tile bias
+//     -8 * 2^-24 * sum(x) (so D = 2^-24 * sum((n - 8) x) exactly), the hi and
+//     lo planes take one MFMA each, and the tile scale multiplies D in f32
+//     as q4t_row_exact does (qtensor.rs:4418-4432).
+#include "gemv_kern.h"
+#include "runtime.h"
+
+namespace cmf {
+
+struct GemmArgs {
+    const void* w;        // [rb][group of 4 tiles][lane][16 B]
+    const void* scale;    // q4t f16 [rb][group][16][4]; q4tp u32 codes
+    const float2* rowp;   // q4tp (2^lo, 2^step) per row
+    const uint8_t* planes;  // hi [item][Mp], lo [item][Mp] (16 B), bias [tile][Mp] f32
+    const float* xs;      // [Mp] 2^-e per batch row
+    float* y;
+    int ldy, M, Mp, N, ntg, nrb;
+};
+
+constexpr int GB = 64;             // batch rows per workgroup
+constexpr int GCH = 33;            // 1 KiB operand chunks per K step (16 hi + 16 lo items, 1 bias)
+constexpr int GJ = (GCH + 3) / 4;  // chunks per wave (clamped)
+
+// GRB: row blocks per wave (4 for large batches; 1 gives small batches 4x
+// the workgroups).
+template <int FMT, int GRB>
+__global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
+    constexpr bool TP = FMT == DT_Q4TP;
+    __shared__ __align__(16) uint4 At[2][GCH * 64];
+    __shared__ float lad[TP ? 4 : 1][TP ? GRB * 16 * 33 : 1];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4;
+    const int by = blockIdx.y, rbw = (blockIdx.x * 4 + wave) * GRB;  // first row block of this wave
+    const int ntg = a.ntg, Mp = a.Mp;
+    const size_t items = (size_t)ntg * 16;  // operand items (4 per tile)
+    const uint4* PH = (const uint4*)a.planes;
+    const uint4* PL = PH + items * Mp;
+    const float* PB = (const float*)(PL + items * Mp);
+
+    // operand chunk c of step g for this lane: 16 hi items, 16 lo items, the
+    // biases.  One unconditional load per chunk, the source picked by selects
+    // (a load under a branch makes the compiler wait for it at once); chunk
+    // j of this wave is held in its own register quad (RA).
+    auto src_a = [&](int j, int g) __attribute__((always_inline)) -> const uint4* {
+        const int c = min(wave + 4 * j, GCH - 1);
+        const uint4* ph = PH + (size_t)(16 * g + c) * Mp + GB * by + lane;
+        const uint4* pl = PL + (size_t)(16 * g + c - 16) * Mp + GB * by + lane;
+        const uint4* pb = (const uint4*)(PB + (size_t)(4 * g + (lane >> 4)) * Mp + GB * by + 4 * (lane & 15));
+        return c < 16 ? ph : c < 32 ? pl : pb;
+    };
+    // the clamped chunk (the biases) is written by every wave with the same data
+    auto dst_a = [&](int j, int buf) __attribute__((always_inline)) -> uint4* {
+        return &At[buf][min(wave + 4 * j, GCH - 1) * 64 + lane];
+    };
+#define GEMM_RA(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
+#define GEMM_LD(J) ra##J = *src_a(J, g_);
+#define GEMM_ST(J) *dst_a(J, buf_) = ra##J;
+    // weights of step g for the wave's row blocks (clamped to the last block)
+    auto load_w = [&](uint4* wv, uint2* sv, int g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < GRB; q++) {
+            const size_t t = (size_t)min(rbw + q, a.nrb - 1) * ntg + g;
+            wv[q] = ((const uint4*)a.w)[t * 64 + lane];
+            if constexpr (TP) sv[q] = make_uint2(((const uint32_t*)a.scale)[t * 16 + r], 0u);
+            else sv[q] = ((const uint2*)a.scale)[t * 16 + r];
+        }
+    };
+    if constexpr (TP) {  // 32-rung ladders of the wave's rows (quant.rs:399-410)
+#pragma unroll
+        for (int q = 0; q < GRB; q++) {
+            if (s == 0) {
+                const float2 p = a.rowp[min(rbw + q, a.nrb - 1) * 16 + r];
+                float tv = p.x;
+                lad[wave][(q * 16 + r) * 33] = tv;
+                for (int c = 1; c < 32; c++) {
+                    tv = tv * p.y;
+                    lad[wave][(q * 16 + r) * 33 + c] = tv;
+                }
+            }
+        }
+    }
+    float4v acc[GRB][4];
+#pragma unroll
+    for (int q = 0; q < GRB; q++)
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++) acc[q][mb] = float4v{0.f, 0.f, 0.f, 0.f};
+
+    static_assert(GJ == 9, "GEMM_RA lists nine chunks");
+    uint4 ra0, ra1, ra2, ra3, ra4, ra5, ra6, ra7, ra8, wA[GRB], wB[GRB];
+    uint2 sA[GRB], sB[GRB];
+    {
+        const int g_ = 0, buf_ = 0;
+        GEMM_RA(GEMM_LD)
+        load_w(wA, sA, 0);
+        GEMM_RA(GEMM_ST)
+    }
+    __syncthreads();
+
+    auto compute = [&](int buf, const uint4* wv, const uint2* sv) __attribute__((always_inline)) {
+        const uint4* A = At[buf];
+        const float4v* Bias = (const float4v*)(A + 32 * 64);  // [tile][64 rows] f32
+#pragma unroll 1
+        for (int t = 0; t < 4; t++) {
+            half8 bq[GRB];
+            float sc[GRB];
+#pragma unroll
+            for (int q = 0; q < GRB; q++) {
+                const uint32_t wd = t == 0 ? wv[q].x : t == 1 ? wv[q].y : t == 2 ? wv[q].z : wv[q].w;
+                bq[q] = dq_nib_word(wd);
+                if constexpr (TP) {
+                    sc[q] = lad[wave][(q * 16 + r) * 33 + ((sv[q].x >> (5 * t)) & 31)];
+                } else {
+                    const uint32_t h = t < 2 ? sv[q].x : sv[q].y;
+                    sc[q] = f16_bits_to_f32((t & 1) ? h >> 16 : h & 0xFFFFu);
+                }
+            }
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                const half8 xh = __builtin_bit_cast(half8, A[(4 * t + s) * 64 + 16 * mb + r]);
+                const half8 xl = __builtin_bit_cast(half8, A[(16 + 4 * t + s) * 64 + 16 * mb + r]);
+                const float4v cb = Bias[t * 16 + 4 * mb + s];  // rows 16 mb + 4 s .. + 3
+#pragma unroll
+                for (int q = 0; q < GRB; q++) {
+                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq[q], cb, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq[q], d, 0, 0, 0);
+                    acc[q][mb] += d * sc[q];
+                }
+            }
+        }
+    };
+
+    for (int g = 0; g < ntg; g += 2) {
+        // the next step's operand and weights go out before this step's MFMAs
+        // (past the last step the loads repeat it and are not stored)
+        {
+            const int g_ = min(g + 1, ntg - 1), buf_ = 1;
+            GEMM_RA(GEMM_LD)
+            load_w(wB, sB, g_);
+            compute(0, wA, sA);
+            if (g + 1 < ntg) { GEMM_RA(GEMM_ST) }
+        }
+        __syncthreads();
+        if (g + 1 >= ntg) break;
+        {
+            const int g_ = min(g + 2, ntg - 1), buf_ = 0;
+            GEMM_RA(GEMM_LD)
+            load_w(wA, sA, g_);
+            compute(1, wB, sB);
+            if (g + 2 < ntg) { GEMM_RA(GEMM_ST) }
+        }
+        __syncthreads();
+    }
+#undef GEMM_RA
+#undef GEMM_LD
+#undef GEMM_ST
+#pragma unroll
+    for (int q = 0; q < GRB; q++) {
+        const int n = (rbw + q) * 16 + r;
+        if (rbw + q >= a.nrb || n >= a.N) continue;
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int b = GB * by + 16 * mb + 4 * s + v;
+                if (b < a.M) a.y[(size_t)b * a.ldy + n] = acc[q][mb][v] * a.xs[b] * 16777216.0f;
+            }
+    }
+}
+
+// Operand planes of the GEMM (grown on demand).
+static uint8_t* g_gemm_planes = nullptr;
+static size_t g_gemm_cap = 0;
+static float* g_gemm_xs = nullptr;
+static size_t g_gemm_xs_cap = 0;
+
+size_t gemm_planes_bytes(const DevWeight& w, int mp) {
+    // hi + lo: 2 * items * Mp * 16 B; biases: tiles * Mp * 4 B
+    return (size_t)w.kchunks * 16 * mp * 32 + (size_t)w.kchunks * 4 * mp * 4;
+}
+
+int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st) {
+    if (w.dtype != DT_Q4T && w.dtype != DT_Q4TP) return fail("gemm: q4t / q4tp weights only");
+    if (m < 1 || m > 65535 * GB) return fail("gemm: bad batch");
+    const int mp = (m + GB - 1) / GB * GB;
+    const size_t pb = gemm_planes_bytes(w, mp);
+    if (g_gemm_cap < pb) {
+        (void)hipStreamSynchronize(st);
+        if (g_gemm_planes) (void)hipFree(g_gemm_planes);
+        g_gemm_planes = nullptr;
+        g_gemm_cap = 0;
+        CMF_HIP(hipMalloc(&g_gemm_planes, pb));
+        g_gemm_cap = pb;
+    }
+    if (g_gemm_xs_cap < (size_t)mp) {
+        (void)hipStreamSynchronize(st);
+        if (g_gemm_xs) (void)hipFree(g_gemm_xs);
+        g_gemm_xs = nullptr;
+        g_gemm_xs_cap = 0;
+        CMF_HIP(hipMalloc(&g_gemm_xs, (size_t)mp * sizeof(float)));
+        g_gemm_xs_cap = mp;
+    }
+    int rc = launch_prep_rows_gemm(w, x, ldx, m, mp, g_gemm_planes, g_gemm_xs, st);
+    if (rc != CMF_OK) return rc;
+    GemmArgs a;
+    a.w = w.w;
+    a.scale = w.scale;
+    a.rowp = w.rowp;
+    a.planes = g_gemm_planes;
+    a.xs = g_gemm_xs;
+    a.y = y;
+    a.ldy = ldy;
+    a.M = m;
+    a.Mp = mp;
+    a.N = w.rows;
+    a.ntg = w.kchunks;
+    a.nrb = w.rows_pad / 16;
+    // four row blocks per wave once that still leaves ~4 workgroups per CU
+    const bool big = (long)((a.nrb + 15) / 16) * (mp / GB) >= 1024;
+    const int rbwg = big ? 16 : 4;
+    const dim3 grid((a.nrb + rbwg - 1) / rbwg, mp / GB);
+    if (w.dtype == DT_Q4T) {
+        if (big) hipLaunchKernelGGL((k_gemm_q4<DT_Q4T, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_q4<DT_Q4T, 1>), grid, dim3(256), 0, st, a);
+    } else {
+        if (big) hipLaunchKernelGGL((k_gemm_q4<DT_Q4TP, 4>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_q4<DT_Q4TP, 1>), grid, dim3(256), 0, st, a);
+    }
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
+}  // namespace cmf

@@ -88,6 +88,13 @@ size_t prep_bytes(const DevWeight& w);
 // Prepared planes (prep_bytes, the layout of prep8_row / prep16_row) and
 // xs[16] of the operand producer src for m batch rows of w.
 int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes, float* xs, hipStream_t st);
+// Prepared GEMM operand of m rows (q4 weights): planes with row stride
+// mstride (a multiple of 64) and tile biases [tile][mstride].
+int launch_prep_rows_gemm(const DevWeight& w, const float* x, int ldx, int m, int mstride, uint8_t* planes,
+                          float* xs, hipStream_t st);
+// y[b][n] (ldy) = W x[b] for b < m (x device rows, ldx), any m, q4t / q4tp
+// weights: the large-batch MFMA GEMM (gemm.hip).
+int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st);
 // The same for up to max_jobs jobs of a device job list (GemvArgs::jobs):
 // job j reads rows at src.x + j * x_stride and writes planes + j *
 // planes_stride, xs + 16 j.
@@ -143,15 +150,16 @@ __device__ inline void prep8_row(const float* x, int K, float amax, int nk, int 
 // Writes batch row b (of M) of the q4 activation operand: f16 hi/lo of
 // x*2^e with max|x*2^e| < 2^15, xs[b] = 2^-e, planes [item = 4*tile + s][b]
 // x 8 halves of columns 32*tile + 8*s + {0,4,2,6,1,5,3,7} (hi plane, then lo
-// plane), then the tile biases [tile][16] f32: -8 * 2^-24 * sum(hi + lo) of
-// the tile at [tile][b], zero for rows >= M (the workgroup of row 0 writes
-// those zeros).  The q4 kernels multiply x by the nibbles as f16 denormals
+// plane), then the tile biases [tile][bstride] f32: -8 * 2^-24 * sum(hi + lo)
+// of the tile at [tile][b], zero for rows in [M, bstride) (the workgroup of
+// row 0 writes those zeros).  M is the planes' row stride (the batch of a
+// GEMV; the padded row count of a GEMM, with bstride = M).  The q4 kernels multiply x by the nibbles as f16 denormals
 // n * 2^-24 and start each tile's accumulator at this bias, so that
 // D = 2^-24 * sum((n - 8) * x).  nthr must
 // be a multiple of 64: the four items of a tile sit in lanes 4t..4t+3 of one
 // wave, which add their partial sums for the bias.
 __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b, int M,
-                                  uint8_t* planes, float* xs, int tid, int nthr) {
+                                  uint8_t* planes, float* xs, int tid, int nthr, int bstride = 16) {
     int ex = 0;
     if (amax > 0.f) frexpf(amax, &ex);
     const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
@@ -185,9 +193,9 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
                                          lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
         if (s == 0) {
-            bias[t * 16 + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
+            bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
             if (b == 0)
-                for (int r = M; r < 16; r++) bias[t * 16 + r] = 0.f;
+                for (int r = M; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
         }
     }
 }

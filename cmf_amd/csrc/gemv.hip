@@ -17,7 +17,7 @@ namespace cmf {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk, uint8_t* __restrict__ planes,
                                                   float* __restrict__ xs, const int* __restrict__ jobs,
-                                                  size_t x_stride, size_t planes_stride) {
+                                                  size_t x_stride, size_t planes_stride, int mstride) {
     extern __shared__ float vals[];  // K
     if (jobs) {  // grouped: blockIdx.y = job
         const int j = blockIdx.y;
@@ -100,8 +100,11 @@ __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk
     __syncthreads();
     am = 0.f;
     for (int q = 0; q < nw; q++) am = fmaxf(am, redm[q]);
-    if (fmt == DT_Q8ROW) prep8_row(vals, K, am, nk, b, gridDim.x, planes, xs, tid, nt);
-    else prep16_row(vals, K, am, nk, b, gridDim.x, planes, xs, tid, nt);
+    // row stride of the planes: the batch (GEMV operands) or a padded row
+    // count (GEMM operands, whose tile biases share that stride)
+    const int ms = mstride ? mstride : gridDim.x;
+    if (fmt == DT_Q8ROW) prep8_row(vals, K, am, nk, b, ms, planes, xs, tid, nt);
+    else prep16_row(vals, K, am, nk, b, ms, planes, xs, tid, nt, mstride ? mstride : 16);
 }
 
 // ---------------------------------------------------------------------------
@@ -114,7 +117,21 @@ int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes,
     if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
-                       xs, (const int*)nullptr, (size_t)0, (size_t)0);
+                       xs, (const int*)nullptr, (size_t)0, (size_t)0, 0);
+    return CMF_OK;
+}
+
+int launch_prep_rows_gemm(const DevWeight& w, const float* x, int ldx, int m, int mstride, uint8_t* planes,
+                          float* xs, hipStream_t st) {
+    const int K = w.cols;
+    if (m < 1 || m > mstride || mstride % 64) return fail("prep: GEMM rows must be 1..mstride, mstride % 64 == 0");
+    if (w.dtype == DT_Q8ROW) return fail("prep: GEMM operands are q4 only");
+    XSrc r{};
+    r.mode = XS_ROWS;
+    r.x = x;
+    r.ldx = ldx;
+    hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, r, K, w.dtype, w.kchunks * 4,
+                       planes, xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride);
     return CMF_OK;
 }
 
@@ -127,7 +144,7 @@ int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const in
     if (max_jobs < 1 || max_jobs > 65535 || !jobs) return fail("prep: bad job list");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m, max_jobs), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk,
-                       planes, xs, jobs, x_stride, planes_stride);
+                       planes, xs, jobs, x_stride, planes_stride, 0);
     return CMF_OK;
 }
 

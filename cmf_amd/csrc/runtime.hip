@@ -223,6 +223,18 @@ int seam_matmat(const DevWeight& w, int row0, const float* xs, int b, int rows, 
     if (grow((void**)&g_ss.x, &g_ss.x_cap, xb) != CMF_OK) return CMF_ERR;
     if (grow((void**)&g_ss.y, &g_ss.y_cap, yb) != CMF_OK) return CMF_ERR;
     hipStream_t st = stream();
+    if (b > MAXB && w.dtype != DT_Q8ROW && row0 == 0 && rows == w.rows) {
+        // large batch: one MFMA GEMM pass over the weights
+        const size_t xb_all = (size_t)b * w.cols * sizeof(float), yb_all = (size_t)b * rows * sizeof(float);
+        if (grow((void**)&g_ss.x, &g_ss.x_cap, xb_all) != CMF_OK) return CMF_ERR;
+        if (grow((void**)&g_ss.y, &g_ss.y_cap, yb_all) != CMF_OK) return CMF_ERR;
+        CMF_HIP(hipMemcpyAsync(g_ss.x, xs, xb_all, hipMemcpyHostToDevice, st));
+        if (gemm_q4(w, g_ss.x, w.cols, b, g_ss.y, rows, st) != CMF_OK) return CMF_ERR;
+        CMF_HIP(hipMemcpyAsync(out, g_ss.y, yb_all, hipMemcpyDeviceToHost, st));
+        CMF_HIP(hipStreamSynchronize(st));
+        CMF_HIP(hipGetLastError());
+        return CMF_OK;
+    }
     for (int b0 = 0; b0 < b; b0 += MAXB) {
         const int m = std::min(MAXB, b - b0);
         CMF_HIP(hipMemcpyAsync(g_ss.x, xs + (size_t)b0 * w.cols, (size_t)m * w.cols * sizeof(float),
@@ -525,6 +537,28 @@ int cmf_time_copy(size_t bytes, int nbuf, int iters, float* avg_ms) {
         if (p) (void)hipFree(p);
     if (dst) (void)hipFree(dst);
     if (rc == CMF_OK) CMF_HIP(hipGetLastError());
+    return rc;
+}
+
+int cmf_time_gemm(cmf_weight w, const float* d_x, int m, float* d_y, int warmup, int iters, float* avg_ms) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!w || !d_x || !d_y || m < 1 || iters < 1 || warmup < 0 || !avg_ms) return fail("time_gemm: bad arguments");
+    hipStream_t st = stream();
+    for (int i = 0; i < warmup; i++)
+        if (gemm_q4(w->w, d_x, w->w.cols, m, d_y, w->w.rows, st) != CMF_OK) return CMF_ERR;
+    hipEvent_t e0, e1;
+    CMF_HIP(hipEventCreate(&e0));
+    CMF_HIP(hipEventCreate(&e1));
+    CMF_HIP(hipEventRecord(e0, st));
+    int rc = CMF_OK;
+    for (int i = 0; i < iters && rc == CMF_OK; i++) rc = gemm_q4(w->w, d_x, w->w.cols, m, d_y, w->w.rows, st);
+    CMF_HIP(hipEventRecord(e1, st));
+    CMF_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_ms = ms / iters;
     return rc;
 }
 

@@ -89,6 +89,10 @@ int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int
  * measured with HIP events on the library stream. */
 int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const float* d_xs, int b,
                   float* d_y, int ldy, int ks, int warmup, int iters, float* avg_ms);
+/* Average device time (ms) of `iters` large-batch GEMMs y[m][rows] = w x
+ * (q4t / q4tp; operand preparation included), x [m][cols] and y on the
+ * device.  No counterpart in the reference: a measurement helper. */
+int cmf_time_gemm(cmf_weight w, const float* d_x, int m, float* d_y, int warmup, int iters, float* avg_ms);
 /* Average device time (ms) of `iters` launches of a plain device copy of
  * `bytes` (16-byte vector loads and stores, a fresh source buffer each
  * launch from `nbuf` rotating ones).  No counterpart in the reference: a

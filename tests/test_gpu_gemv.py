@@ -75,9 +75,25 @@ def test_ragged_shapes(gpu):
 
 
 def test_large_batch_split(gpu):
-    """b > 16 is served as launches of 16"""
+    """q8 with b > 16 is served as GEMV launches of 16"""
     from cmf_amd import synth
-    _check(gpu, synth.q4t_uniform(71, 256, 512), _x(72, 37, 512))
+    _check(gpu, synth.q8_normal(71, 256, 512), _x(72, 37, 512))
+
+
+@pytest.mark.parametrize("b", [17, 64, 130])
+@pytest.mark.parametrize("fmt", ["q4t", "q4tp"])
+def test_gemm_large_batch(gpu, fmt, b):
+    """q4 with b > 16: the MFMA GEMM (ragged batch tiles and row blocks)"""
+    from cmf_amd import synth
+    mk = synth.q4t_uniform if fmt == "q4t" else synth.q4tp_uniform
+    _check(gpu, mk(73 + b, 272, 640), _x(74 + b, b, 640))
+
+
+@pytest.mark.parametrize("shape", [(12288, 4096), (4096, 12288)])
+def test_gemm_config2_prefill(gpu, shape):
+    """config 2 shapes at a prefill-sized batch (256 rows)"""
+    from cmf_amd import synth
+    _check(gpu, synth.q4t_uniform(75, *shape), _x(76, 256, shape[1]))
 
 
 def test_q8_matvec_range(gpu):
