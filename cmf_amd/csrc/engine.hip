@@ -211,10 +211,12 @@ XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
     return r;
 }
 
-// W x with the operand of src: a one-workgroup-per-row producer writes the
-// prepared planes (norm / concat / rows evaluated once, not per GEMV
-// workgroup), the GEMV copies them to LDS (or reads them in place when they
-// do not fit).
+// W x with the operand of src: norm and plain rows are evaluated by every
+// GEMV workgroup from raw rows loaded ahead of its weights (no producer
+// launch); other producers (concat, larger operands) run as a
+// one-workgroup-per-row kernel that writes the prepared planes, which the
+// GEMV copies to LDS (or reads in place when they do not fit).
+// CMF_GEMV_FUSED=n fuses batches of at most n rows (default 2, 0: never).
 int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int nb, bool resid,
            hipStream_t s, int epi = EPI_NONE) {
     for (int b0 = 0; b0 < nb; b0 += MAXB) {
@@ -222,6 +224,16 @@ int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int 
         XSrc sb = src;
         sb.x = src.x ? src.x + (size_t)b0 * src.ldx : nullptr;
         if (sb.toks) sb.toks = src.toks + b0;
+        // fused for m <= 2 (plain decode, MTP drafts): measured on MI355X the
+        // per-workgroup producer costs more than the producer launch for the
+        // m = 5 verify batch (2.62 vs 2.39 ms per K = 4 round) and less for
+        // m = 1 (1.40 vs 1.58 ms per plain round)
+        static const int fuse_max = getenv("CMF_GEMV_FUSED") ? atoi(getenv("CMF_GEMV_FUSED")) : 2;
+        if (mb <= fuse_max && fused_lds_bytes(w, sb, mb) > 0) {
+            const int rc = gemv(w, sb, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s, 0, 0, epi);
+            if (rc != CMF_OK) return rc;
+            continue;
+        }
         int rc = launch_prep_src(w, sb, mb, m->planes, m->xs, s);
         if (rc != CMF_OK) return rc;
         XSrc g{};

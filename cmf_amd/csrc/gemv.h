@@ -66,14 +66,18 @@ struct GemvArgs {
 // staged in LDS, 1: fused producer staged in LDS, 2: prepared planes read in
 // place) and ks waves per workgroup (nullptr: none).
 typedef void (*GemvKernel)(GemvArgs);
-GemvKernel q4t_kernel(int m, int xm, int ks);
-GemvKernel q4tp_kernel(int m, int xm, int ks);
+GemvKernel q4t_kernel(int m, int xm, int ks, int rb);
+GemvKernel q4tp_kernel(int m, int xm, int ks, int rb);
 GemvKernel q8_kernel(int m, int xm, int ks);
 
 enum { EPI_NONE = 0, EPI_SWIGLU = 1 };
 
 // y[b*ldy + (r - row_lo)] (+)= W x for rows [row_lo, row_hi), b < m, from a
-// prepared operand (XS_GLOBAL; launch_prep_src writes it).
+// prepared operand (XS_GLOBAL; launch_prep_src writes it) or from XS_NORM /
+// XS_ROWS rows that every workgroup prepares itself (fused_lds_bytes > 0).
+// LDS bytes of a GEMV whose workgroups evaluate src (XS_NORM / XS_ROWS)
+// themselves, 0 when src must be prepared by launch_prep_src first.
+size_t fused_lds_bytes(const DevWeight& w, const XSrc& src, int m);
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
          bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0, int epi = EPI_NONE);
 // Grouped GEMV: up to max_jobs jobs (the device list `jobs`, see GemvArgs),
@@ -106,6 +110,21 @@ int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* pla
 int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
                 int m, int row_lo, int row_hi, hipStream_t st, int ks_override = 0);
 
+// x ~= q0 + q1/128 + q2/16384 (each int8, |error| <= 2^-22 * 127), the
+// three bytes or-ed into byte j of a, b, c.  v = x / (amax / 127) lies
+// within 127 * (1 + 2^-22) of zero, so rint(v) is in [-127, 127] and the
+// remainders (v - q0) * 128 and (r1 - q1) * 128 in [-64, 64]: no clamps.
+__device__ __forceinline__ void q8_split(float v, int j, uint32_t& a, uint32_t& b, uint32_t& c) {
+    const float q0 = rintf(v);
+    const float r1 = (v - q0) * 128.0f;
+    const float q1 = rintf(r1);
+    const float r2 = (r1 - q1) * 128.0f;
+    const float q2 = rintf(r2);
+    a |= (uint32_t)(uint8_t)(int8_t)q0 << (8 * j);
+    b |= (uint32_t)(uint8_t)(int8_t)q1 << (8 * j);
+    c |= (uint32_t)(uint8_t)(int8_t)q2 << (8 * j);
+}
+
 // Writes batch row b (of M) of the q8 activation planes: three int8 planes
 // with x ~= sx * (q0 + q1/128 + q2/16384), sx = max|x|/127, each plane
 // [item = 4*chunk + s][b] x 16 bytes of columns 64*chunk + 16*s ...
@@ -126,15 +145,7 @@ __device__ inline void prep8_row(const float* x, int K, float amax, int nk, int 
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int col = c0 + 4 * q + j;
-                const float v = col < K ? x[col] * inv : 0.f;
-                const float q0 = fminf(127.f, fmaxf(-127.f, rintf(v)));
-                const float r1 = (v - q0) * 128.0f;
-                const float q1 = fminf(127.f, fmaxf(-127.f, rintf(r1)));
-                const float r2 = (r1 - q1) * 128.0f;
-                const float q2 = fminf(127.f, fmaxf(-127.f, rintf(r2)));
-                a |= (uint32_t)(uint8_t)(int8_t)q0 << (8 * j);
-                bb |= (uint32_t)(uint8_t)(int8_t)q1 << (8 * j);
-                c |= (uint32_t)(uint8_t)(int8_t)q2 << (8 * j);
+                q8_split(col < K ? x[col] * inv : 0.f, j, a, bb, c);
             }
             w0[q] = a;
             w1[q] = bb;
@@ -196,6 +207,81 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
             bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
             if (b == 0)
                 for (int r = M; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
+        }
+    }
+}
+
+// The planes of rows b < m at raw + b*K (prep8_row / prep16_row layout, M =
+// m) by the whole workgroup at once, the work of all rows spread over its
+// threads (q8: 4 columns per unit; q4: one item of 8 columns); amv[b] =
+// max|x| of row b.
+__device__ inline void prep8_rows(const float* raw, int K, const float* amv, int nk, int m,
+                                  uint8_t* planes, float* xs, int tid, int nthr) {
+    const int units = nk * 16;
+    uint8_t* p0 = planes;
+    uint8_t* p1 = planes + (size_t)nk * 64 * m;
+    uint8_t* p2 = planes + (size_t)nk * 128 * m;
+    for (int j = tid; j < m * units; j += nthr) {
+        const int b = j / units, u = j - b * units;
+        const float amax = amv[b];
+        const float sx = amax > 0.f ? amax / 127.0f : 1.0f;
+        const float inv = 1.0f / sx;
+        if (u == 0) xs[b] = sx;
+        const int idx = u >> 2, q4 = u & 3;
+        const int c0 = (idx >> 2) * 64 + 16 * (idx & 3) + 4 * q4;
+        const float* x = raw + (size_t)b * K;
+        uint32_t a = 0, bb = 0, c = 0;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) q8_split(c0 + jj < K ? x[c0 + jj] * inv : 0.f, jj, a, bb, c);
+        const size_t off = ((size_t)idx * m + b) * 16 + 4 * q4;
+        *(uint32_t*)(p0 + off) = a;
+        *(uint32_t*)(p1 + off) = bb;
+        *(uint32_t*)(p2 + off) = c;
+    }
+}
+__device__ inline void prep16_rows(const float* raw, int K, const float* amv, int ntiles, int m,
+                                   uint8_t* planes, float* xs, int tid, int nthr) {
+    constexpr int bstride = 16;
+    uint8_t* ph = planes;
+    uint8_t* pl = planes + (size_t)ntiles * 64 * m;
+    float* bias = (float*)(planes + (size_t)ntiles * 128 * m);
+    const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+    const int per = ntiles * 4;  // items per row (a multiple of 4: tiles never straddle rows)
+    for (int i0 = 0; i0 < m * per; i0 += nthr) {  // uniform trip count (shuffles below)
+        const int jx = i0 + tid;
+        const bool on = jx < m * per;
+        const int b = on ? jx / per : 0, idx = jx - b * per;
+        const float amax = amv[b];
+        int ex = 0;
+        if (amax > 0.f) frexpf(amax, &ex);
+        const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        if (on && idx == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+        const float* x = raw + (size_t)b * K;
+        const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
+        uint16_t hv[8], lv[8];
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int col = c0 + ord[j];
+            const float v = on && col < K ? x[col] * scale : 0.f;
+            const _Float16 h = (_Float16)v;
+            const _Float16 l = (_Float16)(v - (float)h);
+            hv[j] = __builtin_bit_cast(uint16_t, h);
+            lv[j] = __builtin_bit_cast(uint16_t, l);
+            part += (float)h + (float)l;
+        }
+        part += __shfl_xor(part, 1);
+        part += __shfl_xor(part, 2);
+        if (!on) continue;
+        const size_t off = ((size_t)idx * m + b) * 16;
+        *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
+                                         hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
+        *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
+                                         lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
+        if (s == 0) {
+            bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
+            if (b == 0)
+                for (int r = m; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
         }
     }
 }

@@ -167,6 +167,21 @@ static size_t lds_bytes(const DevWeight& w, int m) {
     // q4: hi + lo planes and the tile biases [tile][16] f32
     return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 4 * (128 * m + 64);
 }
+// LDS of a GEMV that evaluates the producer of src itself (XM_FUSED): the
+// planes (1 KiB aligned), then the raw rows and the norm weight; 0 when that
+// path does not apply (other producers, the f16 operand of m > 8 rows,
+// unaligned rows, more than the LDS budget).
+size_t fused_lds_bytes(const DevWeight& w, const XSrc& src, int m) {
+    if (src.mode != XS_NORM && src.mode != XS_ROWS) return 0;
+    if (w.dtype != DT_Q8ROW && m > 8) return 0;
+    const int K = src.K ? src.K : w.cols;
+    if (K != w.cols || K % 4 || src.ldx % 4 || (uintptr_t)src.x % 16) return 0;
+    if (src.mode == XS_NORM && (!src.w || (uintptr_t)src.w % 16)) return 0;
+    const size_t planes = (lds_bytes(w, m) + 1023) & ~(size_t)1023;
+    const size_t raw = ((size_t)(m + (src.mode == XS_NORM ? 1 : 0)) * K * 4 + 1023) & ~(size_t)1023;
+    return planes + raw <= (size_t)LDSX_MAX ? planes + raw : 0;
+}
+
 static int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     return v && *v ? atoi(v) : dflt;
@@ -224,21 +239,49 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
     // 4 tiles (128 columns)
     int ks = ks_override > 0 ? ks_override : pick_ks(w.kchunks);
     if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);  // no 16-wave instance (registers)
-    if (a.src.mode != XS_GLOBAL) return fail("gemv: the operand must be prepared (launch_prep_src)");
-    size_t lds = lds_bytes(w, m);
-    if (lds > LDSX_MAX) lds = 0;  // planes read in place from global memory
+    size_t lds = 0;
+    int xm = XM_GLOBAL;
+    if (a.src.mode == XS_GLOBAL) {
+        lds = lds_bytes(w, m);
+        if (lds > LDSX_MAX) lds = 0;  // planes read in place from global memory
+        xm = lds ? XM_PREP : XM_GLOBAL;
+    } else {
+        lds = fused_lds_bytes(w, a.src, m);
+        if (!lds || gridy > 1) return fail("gemv: this operand must be prepared (launch_prep_src)");
+        xm = XM_FUSED;
+    }
     a.lds = lds ? 1 : 0;
-    const int xm = lds ? XM_PREP : XM_GLOBAL;
-    GemvKernel k = w.dtype == DT_Q8ROW ? q8_kernel(m, xm, ks)
-                   : w.dtype == DT_Q4T ? q4t_kernel(m, xm, ks)
-                                       : q4tp_kernel(m, xm, ks);
-    if (!k) return fail("gemv: no kernel instance for this shape");
     const int threads = 64 * ks;
-    const int occ = resident_per_cu(k, threads, lds);
+    auto pick = [&](int rb) -> GemvKernel {
+        return w.dtype == DT_Q8ROW ? (rb == 1 ? q8_kernel(m, xm, ks) : nullptr)
+               : w.dtype == DT_Q4T ? q4t_kernel(m, xm, ks, rb)
+                                   : q4tp_kernel(m, xm, ks, rb);
+    };
+    // row blocks per workgroup (q4, LDS-staged operand): the smallest RB
+    // whose grid the CUs hold at once, so that no workgroup walks its row
+    // blocks one after another (CMF_GEMV_RB forces one)
+    static const int rb_env = env_int("CMF_GEMV_RB", 0);
+    int rb = 1;
+    GemvKernel k = pick(1);
+    if (!k) return fail("gemv: no kernel instance for this shape");
+    int occ = resident_per_cu(k, threads, lds);
     if (occ < 1) return fail("gemv: kernel does not fit a CU (LDS or registers)");
-    // one workgroup per row block while the CUs hold them all at once;
+    if (gridy == 1 && grid_override <= 0 && pick(2)) {
+        for (int c = 2; c <= 3; c++) {
+            const bool want = rb_env > 0 ? c == rb_env : (a.nrb + rb - 1) / rb > occ * num_cus();
+            if (!want) continue;
+            GemvKernel kc = pick(c);
+            const int oc = kc ? resident_per_cu(kc, threads, lds) : 0;
+            if (oc < 1) break;
+            k = kc;
+            occ = oc;
+            rb = c;
+        }
+    }
+    // one workgroup per RB row blocks while the CUs hold them all at once;
     // grouped launches always give every job its full set
-    int grid = gridy > 1 ? a.nrb : std::min(a.nrb, occ * num_cus());
+    const int units = (a.nrb + rb - 1) / rb;
+    int grid = gridy > 1 ? units : std::min(units, occ * num_cus());
     if (grid_override > 0) grid = std::min(grid_override, a.nrb);
     void* args[] = {&a};
     CMF_HIP(hipLaunchKernel((const void*)k, dim3(grid, gridy), dim3(threads), args, lds, st));

@@ -39,6 +39,15 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef int int4v __attribute__((ext_vector_type(4)));
 
+// Weight words are read exactly once per launch: nontemporal loads keep the
+// stream from displacing the operand planes and partials in L2 (measured on
+// a plain 28 MB read: 5.8 -> 5.6 us; 108 MB: 19.0 -> 17.6 us).
+__device__ __forceinline__ int4v ld_stream(const int4v* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+    const int4v v = __builtin_nontemporal_load((const int4v*)p);
+    return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
+}
+
 constexpr int LDSX_MAX = 128 * 1024;  // largest LDS-staged activation operand (+ scratch)
 
 // Four nibble bytes (8 weights: elements 8s..8s+7 of a tile) to the f16
@@ -72,6 +81,108 @@ __device__ __forceinline__ void x_dma(const XSrc& s, int n, uint8_t* lx) {
         __builtin_amdgcn_global_load_lds((const void*)(g + min(c * 64 + lane, n - 1)),
                                          (__attribute__((address_space(3))) void*)(lx + c * 1024), 16, 0, 0);
 }
+// Fused operand (XM_FUSED): the raw rows b < m of the operand (K floats at
+// x + b*ldx) and, for XS_NORM, the norm weight (K floats) go to LDS by
+// direct loads, issued before the weight stream like x_dma; stage_fused then
+// evaluates the producer in every workgroup while its weights are in flight.
+// raw[] sits after the planes at a 1 KiB boundary and its allocation is
+// rounded up to 1 KiB, so the clamped tail of the last wave load stays in it.
+__device__ __forceinline__ void x_dma_rows(const XSrc& s, int m, int K, float* raw) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    const int c16 = K >> 2;  // 16-byte chunks per row
+    const int n = (m + (s.mode == XS_NORM ? 1 : 0)) * c16;
+    for (int c = wave * 64; c < n; c += nw * 64) {
+        const int idx = min(c + lane, n - 1);
+        const int b = idx / c16, j = idx - b * c16;
+        const float* g = b < m ? s.x + (size_t)b * s.ldx + 4 * j : s.w + 4 * j;
+        __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)(raw + 4 * c), 16,
+                                         0, 0);
+    }
+}
+
+// Wave-wide reductions by DPP row operations (no LDS permutes): pairs and
+// quads, row_shr 4 and 8 (the row's total in lanes 12..15), row_bcast 15 and
+// 31 (rows 0+1 in lane 31, the wave's total in lane 63), read from lane 63.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double dpp_step_add(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = dpp_u32<CTRL, ROWS>((uint32_t)u), hi = dpp_u32<CTRL, ROWS>((uint32_t)(u >> 32));
+    return v + __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);  // invalid source lanes read 0.0
+}
+__device__ __forceinline__ double wave_sum(double v) {
+    v = dpp_step_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
+    v = dpp_step_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
+    v = dpp_step_add<0x114, 0xf>(v);  // row_shr 4
+    v = dpp_step_add<0x118, 0xf>(v);  // row_shr 8
+    v = dpp_step_add<0x142, 0xa>(v);  // row_bcast 15 into rows 1, 3
+    v = dpp_step_add<0x143, 0xc>(v);  // row_bcast 31 into rows 2, 3
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_step_max(float v) {  // v >= 0: invalid lanes read 0
+    return fmaxf(v, __builtin_bit_cast(float, dpp_u32<CTRL, ROWS>(__builtin_bit_cast(uint32_t, v))));
+}
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = dpp_step_max<0xb1, 0xf>(v);
+    v = dpp_step_max<0x4e, 0xf>(v);
+    v = dpp_step_max<0x114, 0xf>(v);
+    v = dpp_step_max<0x118, 0xf>(v);
+    v = dpp_step_max<0x142, 0xa>(v);
+    v = dpp_step_max<0x143, 0xc>(v);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// The producer of k_prep_src (XS_NORM: rms_norm(x) * w, inference.rs:33-50;
+// XS_ROWS: the rows) for the m rows in raw[] (in place), then their planes
+// (prep8_rows / prep16_rows) into planes and xs, all in LDS.  One wave per
+// row (rows wave, wave + nw, ...): sum of squares in f64 and the row's
+// max|y| reduce inside the wave, so the rows proceed in parallel with no
+// workgroup barrier between them.  Ends with a barrier; the caller has made
+// raw[] visible (barrier after the loads).
+__device__ __forceinline__ void stage_fused(int mode, double eps, int m, int K, int fmt, int nk, float* raw,
+                                            uint8_t* planes, float* xs) {
+    __shared__ float amv[MAXB];
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nt >> 6;
+    const bool nrm = mode == XS_NORM;
+    const float* wn = raw + (size_t)m * K;
+    for (int b = wave; b < m; b += nw) {
+        float* xr = raw + (size_t)b * K;
+        float inv = 1.f;
+        if (nrm) {
+            double acc = 0.0;
+            for (int i = lane; i < K; i += 64) acc += (double)xr[i] * (double)xr[i];
+            inv = 1.0f / (float)sqrt(wave_sum(acc) / (double)K + eps);
+        }
+        float am = 0.f;
+        for (int i = lane; i < K; i += 64) {
+            const float y = nrm ? xr[i] * inv * wn[i] : xr[i];
+            xr[i] = y;
+            am = fmaxf(am, fabsf(y));
+        }
+        am = wave_max_nonneg(am);
+        if (lane == 0) amv[b] = am;
+    }
+    __syncthreads();
+    if (fmt == DT_Q8ROW) prep8_rows(raw, K, amv, nk, m, planes, xs, tid, nt);
+    else prep16_rows(raw, K, amv, nk, m, planes, xs, tid, nt);
+    __syncthreads();
+}
+// bytes of the prepared planes a GEMV workgroup holds in LDS (1 KiB aligned:
+// the raw rows of XM_FUSED follow)
+__device__ __forceinline__ int planes_lds_bytes(int fmt, int nk, int m) {
+    const int b = fmt == DT_Q8ROW ? nk * 192 * m : nk * 16 * (32 * m + 16);
+    return (b + 1023) & ~1023;
+}
+
 // s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
 // expcnt 6:4 left at 7, lgkmcnt 11:8)
 template <int N>
@@ -99,9 +210,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // slower per GEMV on MI355X: the per-workgroup staging sits on the critical
 // path of these latency-bound launches.)
 constexpr int SP = 4;  // weight steps per wave and work unit
-enum { XM_PREP = 0, XM_GLOBAL = 2 };
+enum { XM_PREP = 0, XM_FUSED = 1, XM_GLOBAL = 2 };
 
-template <int FMT, int NV, int KS, bool HL, int XM>
+template <int FMT, int NV, int KS, bool HL, int XM, int RB>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     GemvArgs a = args;
     if (a.jobs) {  // grouped launch: this workgroup serves job blockIdx.y
@@ -120,52 +231,65 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     const int r = lane & 15, s = lane >> 4;
     const int M = a.m, ntg = a.nk;  // nk = groups of 4 tiles
     constexpr bool TP = FMT == DT_Q4TP;
-    __shared__ float lad[TP ? 2 : 1][TP ? 16 * 33 : 1];  // ladders of the current / next row block
-    __shared__ float4v part[KS][64];
+    constexpr int LD = 16 * 33;  // one row block's ladders
+    __shared__ float lad[TP ? 2 : 1][TP ? RB * LD : 1];  // ladders of the current / next row blocks
+    __shared__ float4v part[KS][RB][64];
     __shared__ float lxs[16];
     const int P = (ntg + KS * SP - 1) / (KS * SP);  // K parts per row block
-    int rb = blockIdx.x, kp = 0;
-    if (rb >= a.nrb) return;  // uniform over the workgroup
+    const int rstep = gridDim.x * RB;
+    int rb = blockIdx.x * RB, kp = 0;  // first of the RB row blocks of the unit
+    if (rb >= a.nrb) return;           // uniform over the workgroup
     // weights + tile scales of a unit (q4tp: and the row ladder parameters
-    // of its row block), all unconditional (steps past the row clamped to
-    // its last one): a load under a branch makes the compiler wait for it
-    // at once.  NL = loads per call.
-    constexpr int NL = 2 * SP + (TP ? 1 : 0);
-    auto load = [&](uint4* wv, uint2* sv, float2& pv, int rbl, int kpl) {
-        const size_t wbase = (size_t)(a.rb0 + rbl) * ntg;
+    // of its row blocks), all unconditional (steps past the row clamped to
+    // its last one, row blocks past the matrix to its last one): a load
+    // under a branch makes the compiler wait for it at once.  NL = loads per
+    // call.
+    constexpr int NL = RB * (2 * SP + (TP ? 1 : 0));
+    auto load = [&](uint4* wv, uint2* sv, float2* pv, int rbl, int kpl) {
         const int t0 = kpl * KS * SP + wave * SP;
 #pragma unroll
-        for (int u = 0; u < SP; u++) {
-            const size_t t = wbase + min(t0 + u, ntg - 1);
-            wv[u] = ((const uint4*)a.w)[t * 64 + lane];
-            if constexpr (TP) sv[u] = make_uint2(((const uint32_t*)a.scale)[t * 16 + r], 0u);
-            else sv[u] = ((const uint2*)a.scale)[t * 16 + r];
+        for (int q = 0; q < RB; q++) {
+            const size_t wbase = (size_t)(a.rb0 + min(rbl + q, a.nrb - 1)) * ntg;
+#pragma unroll
+            for (int u = 0; u < SP; u++) {
+                const size_t t = wbase + min(t0 + u, ntg - 1);
+                wv[q * SP + u] = ld_stream((const uint4*)a.w + t * 64 + lane);
+                if constexpr (TP) sv[q * SP + u] = make_uint2(((const uint32_t*)a.scale)[t * 16 + r], 0u);
+                else sv[q * SP + u] = ((const uint2*)a.scale)[t * 16 + r];
+            }
+            if constexpr (TP) pv[q] = a.rowp[(a.rb0 + min(rbl + q, a.nrb - 1)) * 16 + r];
         }
-        if constexpr (TP) pv = a.rowp[(a.rb0 + rbl) * 16 + r];
     };
-    // the 32-rung ladder of each row of a row block: t[c] = t[c-1] * ratio
-    // (quant.rs:399-410), by 16 threads of the second wave (the first one
-    // reduces meanwhile)
-    auto ladder = [&](int buf, float2 p) {
+    // the 32-rung ladder of each row of the RB row blocks: t[c] = t[c-1] *
+    // ratio (quant.rs:399-410), by 16 threads per row block starting at the
+    // second wave (the first one reduces meanwhile)
+    auto ladder = [&](int buf, const float2* p) {
         if constexpr (TP) {
             const int lt = (int)threadIdx.x - (KS > 1 ? 64 : 0);
-            if (lt >= 0 && lt < 16) {
-                float tv = p.x;
-                lad[buf][lt * 33] = tv;
-                for (int c = 1; c < 32; c++) {
-                    tv = tv * p.y;
-                    lad[buf][lt * 33 + c] = tv;
+#pragma unroll
+            for (int q = 0; q < RB; q++) {
+                if (lt >= 16 * q && lt < 16 * q + 16) {
+                    float tv = p[q].x;
+                    float* lq = &lad[buf][q * LD + (lt - 16 * q) * 33];
+                    lq[0] = tv;
+                    for (int c = 1; c < 32; c++) {
+                        tv = tv * p[q].y;
+                        lq[c] = tv;
+                    }
                 }
             }
         }
     };
-    uint4 wA[SP];
-    uint2 sA[SP];
-    float2 pA{};
+    uint4 wA[RB * SP];
+    uint2 sA[RB * SP];
+    float2 pA[RB] = {};
     float xsv = 0.f;
+    float* raw = (float*)(smem + planes_lds_bytes(FMT, ntg, M));
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, ntg * (32 * M + 16), smem);  // hi + lo planes + tile biases
         xsv = a.src.xs[threadIdx.x & 15];
+    } else if constexpr (XM == XM_FUSED) {
+        x_dma_rows(a.src, M, a.src.K, raw);
     }
     __builtin_amdgcn_sched_barrier(0);
     load(wA, sA, pA, rb, 0);
@@ -173,6 +297,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     if constexpr (XM == XM_PREP) {
         wait_vmcnt<NL>();  // operand planes and xs are in
         if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
+    } else if constexpr (XM == XM_FUSED) {
+        wait_vmcnt<NL>();  // raw rows are in
+        __syncthreads();
+        stage_fused(a.src.mode, a.src.eps, M, a.src.K, FMT, ntg * 4, raw, smem, lxs);
     } else if (threadIdx.x < 16) {
         lxs[threadIdx.x] = a.src.xs[threadIdx.x];
     }
@@ -188,92 +316,117 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     const int xb = HL ? ((r & 7) < M ? (r & 7) : 0) : (r < M ? r : 0);
     const int xoff = s * M + xb, M4 = 4 * M;
     const float4v zero = {0.f, 0.f, 0.f, 0.f};
-    float4v acc = zero;
+    float4v acc[RB];
+#pragma unroll
+    for (int q = 0; q < RB; q++) acc[q] = zero;
     int buf = 0;
 
-    // one work unit: rb/kp current, rn/kn the next one (rn >= nrb: none)
-    auto process = [&](const uint4* wv, const uint2* sv, const float2& pn, int rn) {
+    // one work unit: rb/kp current, rn the next unit's first row block
+    // (rn >= nrb: none); one operand read serves the RB row blocks
+    auto process = [&](const uint4* wv, const uint2* sv, const float2* pn, int rn) {
         const int t0 = kp * KS * SP + wave * SP;
 #pragma unroll
         for (int u = 0; u < SP; u++) {
             if (t0 + u < ntg) {
                 const int tg = t0 + u;
-                float sc[4];
-                if constexpr (!TP) {
-                    sc[0] = f16_bits_to_f32(sv[u].x & 0xFFFFu);
-                    sc[1] = f16_bits_to_f32(sv[u].x >> 16);
-                    sc[2] = f16_bits_to_f32(sv[u].y & 0xFFFFu);
-                    sc[3] = f16_bits_to_f32(sv[u].y >> 16);
-                } else {
-                    const uint32_t cw = sv[u].x;
-                    sc[0] = lad[buf][r * 33 + (cw & 31)];
-                    sc[1] = lad[buf][r * 33 + ((cw >> 5) & 31)];
-                    sc[2] = lad[buf][r * 33 + ((cw >> 10) & 31)];
-                    sc[3] = lad[buf][r * 33 + ((cw >> 15) & 31)];
+                float sc[RB][4];
+#pragma unroll
+                for (int q = 0; q < RB; q++) {
+                    const uint2 sq = sv[q * SP + u];
+                    if constexpr (!TP) {
+                        sc[q][0] = f16_bits_to_f32(sq.x & 0xFFFFu);
+                        sc[q][1] = f16_bits_to_f32(sq.x >> 16);
+                        sc[q][2] = f16_bits_to_f32(sq.y & 0xFFFFu);
+                        sc[q][3] = f16_bits_to_f32(sq.y >> 16);
+                    } else {
+                        const uint32_t cw = sq.x;
+                        const float* lq = &lad[buf][q * LD + r * 33];
+                        sc[q][0] = lq[cw & 31];
+                        sc[q][1] = lq[(cw >> 5) & 31];
+                        sc[q][2] = lq[(cw >> 10) & 31];
+                        sc[q][3] = lq[(cw >> 15) & 31];
+                    }
                 }
-                const uint32_t ww[4] = {wv[u].x, wv[u].y, wv[u].z, wv[u].w};
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     const int item = (tg * 4 + t) * M4 + xoff;
-                    const half8 bq = dq_nib_word(ww[t]);
                     const float4v cb = LB[(tg * 4 + t) * 4 + s];  // rows 4s..4s+3
-                    float4v d;
+                    half8 xa, xh, xl;
                     if constexpr (HL) {
-                        const half8 xa = __builtin_bit_cast(half8, LX[item]);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bq, cb, 0, 0, 0);
+                        xa = __builtin_bit_cast(half8, LX[item]);
                     } else {
-                        const half8 xh = __builtin_bit_cast(half8, LH[item]);
-                        const half8 xl = __builtin_bit_cast(half8, LL[item]);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq, cb, 0, 0, 0);
-                        d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq, d, 0, 0, 0);
+                        xh = __builtin_bit_cast(half8, LH[item]);
+                        xl = __builtin_bit_cast(half8, LL[item]);
                     }
 #pragma unroll
-                    for (int v = 0; v < NV; v++) acc[v] += d[v] * sc[t];
+                    for (int q = 0; q < RB; q++) {
+                        const uint32_t wq = t == 0 ? wv[q * SP + u].x
+                                            : t == 1 ? wv[q * SP + u].y
+                                            : t == 2 ? wv[q * SP + u].z
+                                                     : wv[q * SP + u].w;
+                        const half8 bq = dq_nib_word(wq);
+                        float4v d;
+                        if constexpr (HL) {
+                            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bq, cb, 0, 0, 0);
+                        } else {
+                            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq, cb, 0, 0, 0);
+                            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq, d, 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int v = 0; v < NV; v++) acc[q][v] += d[v] * sc[q][t];
+                    }
                 }
             }
         }
-        if (kp < P - 1) return;  // the row block continues in the next unit
+        if (kp < P - 1) return;  // the row blocks continue in the next unit
         if constexpr (KS > 1) {
-            part[wave][lane] = acc;
+#pragma unroll
+            for (int q = 0; q < RB; q++) part[wave][q][lane] = acc[q];
             __syncthreads();
         }
         if (wave == 0) {
 #pragma unroll
-            for (int q = 1; q < KS; q++) {
-                const float4v o = part[q][lane];
+            for (int q = 0; q < RB; q++) {
+                float4v o4 = acc[q];
 #pragma unroll
-                for (int v = 0; v < NV; v++) acc[v] += o[v];
-            }
-            if constexpr (HL) {
-                // hi rows (lanes s = 0, 1) + lo rows (lanes s = 2, 3)
+                for (int w = 1; w < KS; w++) {
+                    const float4v o = part[w][q][lane];
 #pragma unroll
-                for (int v = 0; v < NV; v++) acc[v] += __shfl_xor(acc[v], 32);
-            }
-            const int row = (a.rb0 + rb) * 16 + r;
-            if (a.epi == EPI_SWIGLU) {
-                // rows r < 8 gate, r + 8 the matching up row (lane ^ 8):
-                // y[b][8 rb + r] = silu(g) * u (inference.rs:14-16)
-#pragma unroll
-                for (int v = 0; v < NV; v++) {
-                    const int b = 4 * s + v;
-                    const float val = acc[v] * lxs[b & 15] * 16777216.0f;
-                    const float u = __shfl_xor(val, 8);
-                    if (r < 8 && b < M && (!HL || s < 2))
-                        a.y[(size_t)b * a.ldy + (a.rb0 + rb) * 8 + r] = (val / (1.0f + expf(-val))) * u;
+                    for (int v = 0; v < NV; v++) o4[v] += o[v];
                 }
-            } else if (row >= a.row_lo && row < a.row_hi && (!HL || s < 2)) {
+                if constexpr (HL) {
+                    // hi rows (lanes s = 0, 1) + lo rows (lanes s = 2, 3)
 #pragma unroll
-                for (int v = 0; v < NV; v++) {
-                    const int b = 4 * s + v;
-                    if (b < M) {
-                        float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
-                        const float val = acc[v] * lxs[b] * 16777216.0f;  // 2^24: denormal nibbles
-                        *yp = a.resid ? *yp + val : val;
+                    for (int v = 0; v < NV; v++) o4[v] += __shfl_xor(o4[v], 32);
+                }
+                const int rbq = rb + q;
+                const int row = (a.rb0 + rbq) * 16 + r;
+                if (a.epi == EPI_SWIGLU) {
+                    // rows r < 8 gate, r + 8 the matching up row (lane ^ 8):
+                    // y[b][8 rb + r] = silu(g) * u (inference.rs:14-16)
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        const int b = 4 * s + v;
+                        const float val = o4[v] * lxs[b & 15] * 16777216.0f;
+                        const float u = __shfl_xor(val, 8);
+                        if (rbq < a.nrb && r < 8 && b < M && (!HL || s < 2))
+                            a.y[(size_t)b * a.ldy + (a.rb0 + rbq) * 8 + r] = (val / (1.0f + expf(-val))) * u;
+                    }
+                } else if (rbq < a.nrb && row >= a.row_lo && row < a.row_hi && (!HL || s < 2)) {
+#pragma unroll
+                    for (int v = 0; v < NV; v++) {
+                        const int b = 4 * s + v;
+                        if (b < M) {
+                            float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
+                            const float val = o4[v] * lxs[b] * 16777216.0f;  // 2^24: denormal nibbles
+                            *yp = a.resid ? *yp + val : val;
+                        }
                     }
                 }
             }
         }
-        acc = zero;
+#pragma unroll
+        for (int q = 0; q < RB; q++) acc[q] = zero;
         if (rn < a.nrb) ladder(buf ^ 1, pn);
         buf ^= 1;
         if constexpr (KS > 1 || TP) __syncthreads();
@@ -283,11 +436,14 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
         int rn = rb, kn = kp + 1;
         if (kn == P) {
             kn = 0;
-            rn += gridDim.x;
+            rn += rstep;
         }
-        float2 pn{};
+        float2 pn[RB] = {};
         if constexpr (TP)
-            if (rn < a.nrb) pn = a.rowp[(a.rb0 + rn) * 16 + r];
+            if (rn < a.nrb) {
+#pragma unroll
+                for (int q = 0; q < RB; q++) pn[q] = a.rowp[(a.rb0 + min(rn + q, a.nrb - 1)) * 16 + r];
+            }
         process(wA, sA, pn, rn);
         if (rn >= a.nrb) break;
         rb = rn;
@@ -332,13 +488,16 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
         const int c0 = kpl * KS * SP + wave * SP;
         // unconditional loads (steps past the row clamped to its last one)
 #pragma unroll
-        for (int u = 0; u < SP; u++) wv[u] = ((const int4v*)a.w)[(wbase + min(c0 + u, nkc - 1)) * 64 + lane];
+        for (int u = 0; u < SP; u++) wv[u] = ld_stream((const int4v*)a.w + (wbase + min(c0 + u, nkc - 1)) * 64 + lane);
     };
     int4v wA[SP];
     float xsv = 0.f;
+    float* raw = (float*)(smem + planes_lds_bytes(DT_Q8ROW, nkc, M));
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, nkc * 4 * M * 3, smem);  // three planes
         xsv = a.src.xs[threadIdx.x & 15];
+    } else if constexpr (XM == XM_FUSED) {
+        x_dma_rows(a.src, M, a.src.K, raw);
     }
     __builtin_amdgcn_sched_barrier(0);
     load(wA, rb, 0);
@@ -346,6 +505,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     if constexpr (XM == XM_PREP) {
         wait_vmcnt<SP>();  // operand planes and xs are in
         if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
+    } else if constexpr (XM == XM_FUSED) {
+        wait_vmcnt<SP>();  // raw rows are in
+        __syncthreads();
+        stage_fused(a.src.mode, a.src.eps, M, a.src.K, DT_Q8ROW, nkc, raw, smem, lxs);
     } else if (threadIdx.x < 16) {
         lxs[threadIdx.x] = a.src.xs[threadIdx.x];
     }
@@ -472,33 +635,45 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
 // ---------------------------------------------------------------------------
 // Kernel instance tables (one translation unit per weight codec).
 // ---------------------------------------------------------------------------
-template <int FMT, int NV, bool HL, int XM>
+template <int FMT, int NV, bool HL, int XM, int RB>
 GemvKernel q4_by_ks(int ks) {
     switch (ks) {
-        case 1: return k_gemv_q4<FMT, NV, 1, HL, XM>;
-        case 2: return k_gemv_q4<FMT, NV, 2, HL, XM>;
-        case 4: return k_gemv_q4<FMT, NV, 4, HL, XM>;
-        case 8: return k_gemv_q4<FMT, NV, 8, HL, XM>;
+        case 1:  // (RB > 1 spills at one wave)
+            if constexpr (RB == 1) return k_gemv_q4<FMT, NV, 1, HL, XM, RB>;
+            return nullptr;
+        case 2: return k_gemv_q4<FMT, NV, 2, HL, XM, RB>;
+        case 4: return k_gemv_q4<FMT, NV, 4, HL, XM, RB>;
+        case 8: return k_gemv_q4<FMT, NV, 8, HL, XM, RB>;
     }
-    // two MFMAs per tile need more than the 128 registers a 16-wave
-    // workgroup leaves each wave
-    if constexpr (HL)
-        if (ks == 16) return k_gemv_q4<FMT, NV, 16, HL, XM>;
+    // two MFMAs per tile (or three row blocks) need more than the 128
+    // registers a 16-wave workgroup leaves each wave
+    if constexpr (HL && RB < 3)
+        if (ks == 16) return k_gemv_q4<FMT, NV, 16, HL, XM, RB>;
     return nullptr;
 }
+// RB > 1 only for the LDS-staged one-MFMA-per-tile kernels (m <= 8)
 template <int FMT, int NV, bool HL>
-GemvKernel q4_by_xm(int xm, int ks) {
-    switch (xm) {
-        case XM_PREP: return q4_by_ks<FMT, NV, HL, XM_PREP>(ks);
-        case XM_GLOBAL: return q4_by_ks<FMT, NV, HL, XM_GLOBAL>(ks);
+GemvKernel q4_by_xm(int xm, int ks, int rb) {
+    if (xm == XM_GLOBAL) return rb == 1 ? q4_by_ks<FMT, NV, HL, XM_GLOBAL, 1>(ks) : nullptr;
+    if constexpr (HL)
+        if (xm == XM_FUSED) return rb == 1 ? q4_by_ks<FMT, NV, HL, XM_FUSED, 1>(ks) : nullptr;
+    if (xm != XM_PREP) return nullptr;
+    if constexpr (HL) {
+        switch (rb) {
+            case 1: return q4_by_ks<FMT, NV, HL, XM_PREP, 1>(ks);
+            case 2: return q4_by_ks<FMT, NV, HL, XM_PREP, 2>(ks);
+            case 3: return q4_by_ks<FMT, NV, HL, XM_PREP, 3>(ks);
+        }
+        return nullptr;
+    } else {
+        return rb == 1 ? q4_by_ks<FMT, NV, HL, XM_PREP, 1>(ks) : nullptr;
     }
-    return nullptr;
 }
 template <int FMT>
-GemvKernel q4_pick(int m, int xm, int ks) {
-    if (m == 1) return q4_by_xm<FMT, 1, true>(xm, ks);
-    if (m <= 8) return q4_by_xm<FMT, 4, true>(xm, ks);
-    return q4_by_xm<FMT, 4, false>(xm, ks);
+GemvKernel q4_pick(int m, int xm, int ks, int rb) {
+    if (m == 1) return q4_by_xm<FMT, 1, true>(xm, ks, rb);
+    if (m <= 8) return q4_by_xm<FMT, 4, true>(xm, ks, rb);
+    return q4_by_xm<FMT, 4, false>(xm, ks, rb);
 }
 template <bool PK, int XM>
 GemvKernel q8_by_ks(int ks) {
@@ -515,6 +690,7 @@ template <bool PK>
 GemvKernel q8_by_xm(int xm, int ks) {
     switch (xm) {
         case XM_PREP: return q8_by_ks<PK, XM_PREP>(ks);
+        case XM_FUSED: return q8_by_ks<PK, XM_FUSED>(ks);
         case XM_GLOBAL: return q8_by_ks<PK, XM_GLOBAL>(ks);
     }
     return nullptr;

@@ -2,5 +2,5 @@
 #include "gemv_kern.h"
 
 namespace cmf {
-GemvKernel q4t_kernel(int m, int xm, int ks) { return q4_pick<DT_Q4T>(m, xm, ks); }
+GemvKernel q4t_kernel(int m, int xm, int ks, int rb) { return q4_pick<DT_Q4T>(m, xm, ks, rb); }
 }  // namespace cmf
