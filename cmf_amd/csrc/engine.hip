@@ -216,7 +216,16 @@ XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
 // launch); other producers (concat, larger operands) run as a
 // one-workgroup-per-row kernel that writes the prepared planes, which the
 // GEMV copies to LDS (or reads in place when they do not fit).
-// CMF_GEMV_FUSED=n fuses batches of at most n rows (default 2, 0: never).
+// Whether a batch of mb rows of src is prepared inside the GEMV workgroups:
+// for m <= 2 (plain decode, MTP drafts); measured on MI355X the
+// per-workgroup producer costs more than the producer launch for the m = 5
+// verify batch (2.62 vs 2.39 ms per K = 4 round) and less for m = 1 (1.40 vs
+// 1.58 ms per plain round).  CMF_GEMV_FUSED=n moves the limit (0: never).
+static bool fuse_ok(const DevWeight& w, const XSrc& src, int mb) {
+    static const int fuse_max = getenv("CMF_GEMV_FUSED") ? atoi(getenv("CMF_GEMV_FUSED")) : 2;
+    return mb <= fuse_max && fused_lds_bytes(w, src, mb) > 0;
+}
+
 int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int nb, bool resid,
            hipStream_t s, int epi = EPI_NONE) {
     for (int b0 = 0; b0 < nb; b0 += MAXB) {
@@ -224,12 +233,7 @@ int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int 
         XSrc sb = src;
         sb.x = src.x ? src.x + (size_t)b0 * src.ldx : nullptr;
         if (sb.toks) sb.toks = src.toks + b0;
-        // fused for m <= 2 (plain decode, MTP drafts): measured on MI355X the
-        // per-workgroup producer costs more than the producer launch for the
-        // m = 5 verify batch (2.62 vs 2.39 ms per K = 4 round) and less for
-        // m = 1 (1.40 vs 1.58 ms per plain round)
-        static const int fuse_max = getenv("CMF_GEMV_FUSED") ? atoi(getenv("CMF_GEMV_FUSED")) : 2;
-        if (mb <= fuse_max && fused_lds_bytes(w, sb, mb) > 0) {
+        if (fuse_ok(w, sb, mb)) {
             const int rc = gemv(w, sb, y + (size_t)b0 * ldy, ldy, mb, 0, w.rows, resid, s, 0, 0, epi);
             if (rc != CMF_OK) return rc;
             continue;
@@ -258,30 +262,24 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
     const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv;
     const int QKV = (nh + 2 * nkv) * hd, I = c.inter;
     gemv_f(m, l.qkv, src_norm(h, H, l.in_norm, c.eps), m->qkv_out, QKV, nb, false, s);
-    // the attention kernel holds at most 32 query heads per kv head
-    const int rows_per = std::max(1, 32 / (nh / nkv));
-    // one attention launch: its merge also writes wo's prepared operand
-    const bool merge_prep = nb <= rows_per && nb <= MAXB && nh <= 64;
+    // the attention kernel holds at most 32 query heads per kv head and
+    // MAXB new rows
+    const int rows_per = std::min(MAXB, std::max(1, 32 / (nh / nkv)));
     for (int b0 = 0; b0 < nb; b0 += rows_per) {
         AttnArgs at{m->qkv_out + (size_t)b0 * QKV, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq,
                     std::min(rows_per, nb - b0), nh, nkv, c.eps, pb, padd + b0, m->pm, m->pl, m->po, m->nch_cap,
                     m->ao + (size_t)b0 * nh * hd, 1};
-        if (merge_prep) launch_attention(at, max_len, s, &l.wo, m->planes, m->xs);
-        else launch_attention(at, max_len, s);
+        launch_attention(at, max_len, s);
     }
-    if (merge_prep) {
-        XSrc g{};
-        g.mode = XS_GLOBAL;
-        g.planes = m->planes;
-        g.xs = m->xs;
-        gemv(l.wo, g, h, H, nb, 0, l.wo.rows, true, s);
-    } else {
-        XSrc ra{};
-        ra.mode = XS_ROWS;
-        ra.x = m->ao;
-        ra.ldx = nh * hd;
-        gemv_f(m, l.wo, ra, h, H, nb, true, s);
-    }
+    // the merged rows (ao) are the wo operand: prepared inside the wo GEMV
+    // for small batches, by a producer launch otherwise (measured on MI355X
+    // both beat a merge that also writes the prepared operand: its one
+    // workgroup per row serialises the 16 heads' merges)
+    XSrc ra{};
+    ra.mode = XS_ROWS;
+    ra.x = m->ao;
+    ra.ldx = nh * hd;
+    gemv_f(m, l.wo, ra, h, H, nb, true, s);
     // gate|up with the SwiGLU epilogue: gu_out [nb][I] = silu(g) * u
     gemv_f(m, l.gu, src_norm(h, H, l.post_norm, c.eps), m->gu_out, I, nb, false, s, EPI_SWIGLU);
     XSrc sd{};

@@ -31,6 +31,7 @@
 
 #include "common.h"
 #include "gemv.h"
+#include "wave.h"
 
 namespace cmf {
 
@@ -101,45 +102,6 @@ __device__ __forceinline__ void x_dma_rows(const XSrc& s, int m, int K, float* r
     }
 }
 
-// Wave-wide reductions by DPP row operations (no LDS permutes): pairs and
-// quads, row_shr 4 and 8 (the row's total in lanes 12..15), row_bcast 15 and
-// 31 (rows 0+1 in lane 31, the wave's total in lane 63), read from lane 63.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROWS, 0xf, false);
-}
-template <int CTRL, int ROWS>
-__device__ __forceinline__ double dpp_step_add(double v) {
-    const uint64_t u = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = dpp_u32<CTRL, ROWS>((uint32_t)u), hi = dpp_u32<CTRL, ROWS>((uint32_t)(u >> 32));
-    return v + __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);  // invalid source lanes read 0.0
-}
-__device__ __forceinline__ double wave_sum(double v) {
-    v = dpp_step_add<0xb1, 0xf>(v);   // quad_perm [1,0,3,2]
-    v = dpp_step_add<0x4e, 0xf>(v);   // quad_perm [2,3,0,1]
-    v = dpp_step_add<0x114, 0xf>(v);  // row_shr 4
-    v = dpp_step_add<0x118, 0xf>(v);  // row_shr 8
-    v = dpp_step_add<0x142, 0xa>(v);  // row_bcast 15 into rows 1, 3
-    v = dpp_step_add<0x143, 0xc>(v);  // row_bcast 31 into rows 2, 3
-    const uint64_t u = __builtin_bit_cast(uint64_t, v);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp_step_max(float v) {  // v >= 0: invalid lanes read 0
-    return fmaxf(v, __builtin_bit_cast(float, dpp_u32<CTRL, ROWS>(__builtin_bit_cast(uint32_t, v))));
-}
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-    v = dpp_step_max<0xb1, 0xf>(v);
-    v = dpp_step_max<0x4e, 0xf>(v);
-    v = dpp_step_max<0x114, 0xf>(v);
-    v = dpp_step_max<0x118, 0xf>(v);
-    v = dpp_step_max<0x142, 0xa>(v);
-    v = dpp_step_max<0x143, 0xc>(v);
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
 // The producer of k_prep_src (XS_NORM: rms_norm(x) * w, inference.rs:33-50;
 // XS_ROWS: the rows) for the m rows in raw[] (in place), then their planes
 // (prep8_rows / prep16_rows) into planes and xs, all in LDS.  One wave per
@@ -168,7 +130,7 @@ __device__ __forceinline__ void stage_fused(int mode, double eps, int m, int K, 
             xr[i] = y;
             am = fmaxf(am, fabsf(y));
         }
-        am = wave_max_nonneg(am);
+        am = wave_max(am);
         if (lane == 0) amv[b] = am;
     }
     __syncthreads();

@@ -31,10 +31,8 @@ struct AttnArgs {
     float* out;
     int attend;         // 0: only append the rows' K/V (no queries, no output)
 };
-// With `next`, the merge also writes the prepared operand of that weight
-// (the wo projection) for the a.nb rows: planes / xs as launch_prep_src.
-void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, const DevWeight* next = nullptr,
-                      uint8_t* planes = nullptr, float* xs = nullptr);
+// k_attention (chunk partials) then k_attn_merge (rows of a.out).
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st);
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
                    hipStream_t st);
 

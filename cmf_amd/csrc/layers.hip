@@ -12,6 +12,7 @@
 #include "common.h"
 #include "gemv.h"
 #include "layers.h"
+#include "wave.h"
 
 namespace cmf {
 
@@ -64,32 +65,30 @@ __global__ __launch_bounds__(256) void k_embed(const int* __restrict__ toks, Emb
 
 // qk-norm + RoPE of one head row x (lane holds dims lane and lane + 64, the
 // rotation pair): x * inv * w with inv = 1/sqrt(mean(x^2) + eps) (f64 sum),
-// then (a, b) -> (a cos - b sin, a sin + b cos) at position pos.
-__device__ __forceinline__ float2 head_norm_rope(float x0, float x1, const float* w, const float2* rope, int pos,
-                                                 double eps, int lane) {
-    double ss = (double)x0 * (double)x0 + (double)x1 * (double)x1;
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+// then (a, b) -> (a cos - b sin, a sin + b cos); w0/w1 = w[lane], w[lane +
+// 64], cs = the (cos, sin) of the position at lane.
+__device__ __forceinline__ float2 norm_rope(float x0, float x1, float w0, float w1, float2 cs, double eps) {
+    const double ss = wave_sum((double)x0 * (double)x0 + (double)x1 * (double)x1);
     const float inv = (float)(1.0 / sqrt(ss / 128.0 + eps));
-    const float a = x0 * inv * w[lane], b = x1 * inv * w[lane + 64];
-    const float2 cs = rope[(size_t)pos * 64 + lane];  // (cos, sin)
+    const float a = x0 * inv * w0, b = x1 * inv * w1;
     return make_float2(a * cs.x - b * cs.y, a * cs.y + b * cs.x);
 }
+__device__ __forceinline__ float2 head_norm_rope(float x0, float x1, const float* w, const float2* rope, int pos,
+                                                 double eps, int lane) {
+    return norm_rope(x0, x1, w[lane], w[lane + 64], rope[(size_t)pos * 64 + lane], eps);
+}
 
-// Chunk softmax and value pass of the NQ queries qi = w + 4i owned by one
-// wave: lane = key position for the softmax (max, exp, sum by wave
+// Chunk softmax and value pass of the n <= NQ queries qi = w + 4i owned by
+// one wave: lane = key position for the softmax (max, exp, sum by wave
 // reductions; the weights overwrite the scores), lane = dim pair for the
 // values, o[qi][d] = sum_p e[qi][p] * V[p][d] in position order.
 template <int NQ>
 __device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[128 + 4], int w, int lane, int hpk,
-                                            int nh, int g, int c, int nch, float* pm, float* pl, float* po) {
+                                            int nh, int g, int c, int nch, int n, float* pm, float* pl, float* po) {
     constexpr int C = ATT_C, HD = 128;
     float m[NQ], l[NQ], e[NQ];
 #pragma unroll
-    for (int i = 0; i < NQ; i++) m[i] = S[w + 4 * i][lane];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-        for (int i = 0; i < NQ; i++) m[i] = fmaxf(m[i], __shfl_xor(m[i], off));
+    for (int i = 0; i < NQ; i++) m[i] = wave_max(S[w + 4 * i][lane]);
 #pragma unroll
     for (int i = 0; i < NQ; i++) {
         e[i] = m[i] == -INFINITY ? 0.f : expf(S[w + 4 * i][lane] - m[i]);
@@ -97,16 +96,16 @@ __device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[
         S[w + 4 * i][lane] = e[i];
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-        for (int i = 0; i < NQ; i++) l[i] += __shfl_xor(l[i], off);
+    for (int i = 0; i < NQ; i++) l[i] = wave_sum(l[i]);
     if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             const int qi = w + 4 * i;
             const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
-            pm[row * nch + c] = m[i];
-            pl[row * nch + c] = l[i];
+            if (i < n) {
+                pm[row * nch + c] = m[i];
+                pl[row * nch + c] = l[i];
+            }
         }
     }
     float2 o[NQ];
@@ -134,7 +133,7 @@ __device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[
     for (int i = 0; i < NQ; i++) {
         const int qi = w + 4 * i;
         const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
-        ((float2*)(po + (row * nch + c) * HD))[lane] = o[i];
+        if (i < n) ((float2*)(po + (row * nch + c) * HD))[lane] = o[i];
     }
 }
 
@@ -168,36 +167,45 @@ __device__ __forceinline__ void append_rows(const AttnArgs& a, int g, int p0, in
 }
 
 // Merge of the chunk partials of one (batch row b, head h) by one wave:
-// lanes = chunks for the weights exp(m_c - M), lanes = dim pairs for the
-// output sum_c w_c o_c / sum_c w_c l_c.
+// out = sum_c w_c o_c / sum_c w_c l_c with w_c = exp(m_c - M), M = max_c m_c.
+// The chunk maxima, sums and the first CB chunks' outputs (lane = dim pair)
+// are requested together, so a merge over <= CB chunks costs one memory
+// round trip (chunk indices clamped; chunks past `used` weigh 0).
+template <int CB>
 __device__ __forceinline__ void attn_merge_row(const float* pm, const float* pl, const float* po, int nch,
                                                size_t row, int used, float* out) {
     constexpr int HD = 128;
+    static_assert(64 % CB == 0, "chunk batch");
     const int lane = threadIdx.x & 63;
-    float M = -INFINITY;
-    for (int c = lane; c < used; c += 64) M = fmaxf(M, pm[row * nch + c]);
-    for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float* pmr = pm + row * nch;
+    const float* plr = pl + row * nch;
+    const float2* por = (const float2*)(po + row * nch * HD);
+    float2 ov[CB];
+#pragma unroll
+    for (int j = 0; j < CB; j++) ov[j] = por[(size_t)min(j, used - 1) * (HD / 2) + lane];
+    const float m_first = pmr[min(lane, used - 1)], l_first = plr[min(lane, used - 1)];
+    float M = lane < used ? m_first : -INFINITY;
+    for (int c = lane + 64; c < used; c += 64) M = fmaxf(M, pmr[c]);
+    M = wave_max(M);
     float L = 0.f;
     float2 O = make_float2(0.f, 0.f);
-    for (int c0 = 0; c0 < used; c0 += 64) {
-        const int c = c0 + lane;
-        const float m = c < used ? pm[row * nch + c] : -INFINITY;
-        const float wgt = m == -INFINITY ? 0.f : expf(m - M);
-        float lw = c < used ? pl[row * nch + c] * wgt : 0.f;
-        for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o);
-        L += lw;
-        const int n = min(64, used - c0);
-        for (int jb = 0; jb < n; jb += 8) {
-            float2 vv[8];
+    for (int c1 = 0; c1 < used; c1 += 64) {
+        const int c = c1 + lane;
+        const float mc = c1 == 0 ? (lane < used ? m_first : -INFINITY) : (c < used ? pmr[c] : -INFINITY);
+        const float lc = c1 == 0 ? l_first : (c < used ? plr[c] : 0.f);
+        const float wgt = mc == -INFINITY ? 0.f : expf(mc - M);
+        L += wave_sum(c < used ? lc * wgt : 0.f);
+        const int c_end = min(used, c1 + 64);
+        for (int c0 = c1; c0 < c_end; c0 += CB) {
+            if (c0 > 0) {
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                vv[j] = jb + j < n ? ((const float2*)(po + (row * nch + c0 + jb + j) * HD))[lane]
-                                   : make_float2(0.f, 0.f);
+                for (int j = 0; j < CB; j++) ov[j] = por[(size_t)min(c0 + j, used - 1) * (HD / 2) + lane];
+            }
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), jb + j));
-                O.x += wj * vv[j].x;
-                O.y += wj * vv[j].y;
+            for (int j = 0; j < CB; j++) {
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wgt), c0 - c1 + j));
+                O.x += wj * ov[j].x;
+                O.y += wj * ov[j].y;
             }
         }
     }
@@ -209,138 +217,158 @@ __device__ __forceinline__ void attn_merge_row(const float* pm, const float* pl,
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     const int rh = blockIdx.x, b = rh / a.nh;
     const int used = (*a.pbase + a.padd + b + ATT_C) / ATT_C;
-    attn_merge_row(a.pm, a.pl, a.po, a.nch, (size_t)rh, used, a.out + (size_t)rh * 128);
-}
-
-// Merge + the next GEMV's prepared operand: one workgroup per row b, one
-// wave per head (looping past 16 heads); the merged row [nh * 128] stays in
-// LDS, its max|x| is reduced and the row is written as the operand planes
-// of a weight of format fmt (prep8_row / prep16_row layout, nb rows).
-__global__ __launch_bounds__(1024) void k_attn_merge_prep(AttnArgs a, int fmt, int nk, uint8_t* __restrict__ planes,
-                                                         float* __restrict__ xs) {
-    extern __shared__ float rowv[];  // nh * 128
-    __shared__ float redm[16];
-    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
-    const int used = (*a.pbase + a.padd + b + ATT_C) / ATT_C;
-    for (int h = wave; h < a.nh; h += nw)
-        attn_merge_row(a.pm, a.pl, a.po, a.nch, (size_t)b * a.nh + h, used, rowv + h * 128);
-    __syncthreads();
-    const int K = a.nh * 128;
-    float am = 0.f;
-    for (int i = tid; i < K; i += blockDim.x) am = fmaxf(am, fabsf(rowv[i]));
-    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-    if (lane == 0) redm[wave] = am;
-    __syncthreads();
-    am = 0.f;
-    for (int q = 0; q < nw; q++) am = fmaxf(am, redm[q]);
-    if (fmt == DT_Q8ROW) prep8_row(rowv, K, am, nk, b, gridDim.x, planes, xs, tid, blockDim.x);
-    else prep16_row(rowv, K, am, nk, b, gridDim.x, planes, xs, tid, blockDim.x);
+    attn_merge_row<32>(a.pm, a.pl, a.po, a.nch, (size_t)rh, used, a.out + (size_t)rh * 128);
 }
 
 // Decode attention of one layer for the nb rows at positions pos0 .. pos0+nb-1
-// (pos0 = *pbase + padd), one workgroup per (kv head g, 64-position chunk c):
-//   - q-norm + RoPE of the hpk query heads of g for every row (Q in LDS);
-//   - the chunk's cached K (registers) and V (LDS); the chunk that holds new
-//     positions computes their k-norm + RoPE K and V rows itself, appends
-//     them to the cache and uses them (finish_projection + append);
-//   - scores with the causal limit pos0 + b, chunk softmax and values
-//     (partials m, l, o per row/head/chunk);
+// (pos0 = *pbase + padd), one workgroup per (kv head g, 64-position chunk c),
+// NQW = queries per wave (the hpk * nb queries of g, query qi on wave qi % 4):
+//   - loads in the order they are needed, so that the short ones do not
+//     wait behind the KV stream (a wave's loads complete in order): the
+//     query rows, the new K/V rows that fall in the chunk, then the chunk's
+//     cached K (registers) and V;
+//   - q-norm + RoPE of the queries (Q in LDS) and, in the chunk that holds
+//     new positions, k-norm + RoPE of their K rows, appended to the cache
+//     and used from LDS with their V rows (finish_projection + append);
+//   - scores with the causal limit pos0 + b (lanes = position x dim
+//     quarter, the quarters summed by quad DPP), chunk softmax and values
+//     (partials m, l, o per row/head/chunk).
+template <int NQW>
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
-    constexpr int HD = 128, C = ATT_C;
+    constexpr int HD = 128, C = ATT_C, NR = MAXB / 4;  // NR: new rows per wave
     const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int nh = a.nh, hpk = nh / a.nkv, nq = a.nb * hpk;
     const int pos0 = *a.pbase + a.padd;
     const int stored = pos0 + a.nb;
     const int p0 = c * C;
-    __shared__ __align__(16) float Q[32][HD];
+    __shared__ __align__(16) float Q[4 * NQW][HD];
     __shared__ __align__(16) float V[C][HD + 4];
-    __shared__ __align__(16) float S[32][C];
+    __shared__ __align__(16) float S[4 * NQW][C];
     __shared__ __align__(16) float Kn[MAXB][HD];
     if (!a.attend) {  // KV append only (MTP warm-up)
         if (p0 < stored) append_rows(a, g, p0, pos0, wave, lane, nullptr, nullptr);
         return;
     }
-    if (p0 < stored) {
-        const int np = min(C, stored - p0);
-        const int nold = min(np, max(0, pos0 - p0));  // cached positions of this chunk
-        // cached K: lane = (position pk, dim quarter dq)
-        const int pk = wave * 16 + (lane & 15), dq = lane >> 4;
-        const bool kvalid = pk < np;
-        const float4* Kp = (const float4*)(a.kc + ((size_t)g * a.max_seq + p0 + (pk < nold ? pk : 0)) * HD + 32 * dq);
-        float4 kv[8];
+    if (p0 >= stored) return;
+    const int np = min(C, stored - p0);
+    const int nold = min(np, max(0, pos0 - p0));  // cached positions of this chunk
+    // 1. query rows (indices clamped: every lane loads, extra rows unused)
+    float qx0[NQW], qx1[NQW];
+    float2 qcs[NQW];
 #pragma unroll
-        for (int j = 0; j < 8; j++) kv[j] = Kp[j];
-        // cached V: thread t loads float4 column t % 32 of rows t/32 + 8u
-        const float4* Vg = (const float4*)(a.vc + ((size_t)g * a.max_seq + p0) * HD);
-        float4 vv[8];
+    for (int i = 0; i < NQW; i++) {
+        const int qi = min(wave + 4 * i, nq - 1), b = qi / hpk, h = g * hpk + qi % hpk;
+        const float* x = a.qkv + (size_t)b * a.ldq + (size_t)h * HD;
+        qx0[i] = x[lane];
+        qx1[i] = x[lane + 64];
+        qcs[i] = a.rope[(size_t)(pos0 + b) * 64 + lane];
+    }
+    const float qw0 = a.qn[lane], qw1 = a.qn[lane + 64];
+    // 2. new rows b of this chunk (pos0 + b in [p0, p0 + C)): wave w takes
+    // b_lo + w + 4j
+    const int b_lo = max(0, p0 - pos0), b_hi = min(a.nb, p0 + C - pos0);
+    float kx0[NR], kx1[NR], vx0[NR], vx1[NR];
+    float2 kcs[NR];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int r = (t >> 5) + 8 * u;
-            vv[u] = r < nold ? Vg[(size_t)r * (HD / 4) + (t & 31)] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        // queries: wave per (row, head), rows of qkv hold [q heads | k heads | v heads]
-        for (int qi = wave; qi < nq; qi += 4) {
-            const int b = qi / hpk, h = g * hpk + qi % hpk;
-            const float* x = a.qkv + (size_t)b * a.ldq + (size_t)h * HD;
-            const float2 o = head_norm_rope(x[lane], x[lane + 64], a.qn, a.rope, pos0 + b, a.eps, lane);
+    for (int j = 0; j < NR; j++) {
+        const int b = min(b_lo + wave + 4 * j, a.nb - 1);
+        const float* xk = a.qkv + (size_t)b * a.ldq + (size_t)(nh + g) * HD;
+        const float* xv = a.qkv + (size_t)b * a.ldq + (size_t)(nh + a.nkv + g) * HD;
+        kx0[j] = xk[lane];
+        kx1[j] = xk[lane + 64];
+        vx0[j] = xv[lane];
+        vx1[j] = xv[lane + 64];
+        kcs[j] = a.rope[(size_t)(pos0 + b) * 64 + lane];
+    }
+    const float kw0 = a.kn[lane], kw1 = a.kn[lane + 64];
+    // 3. cached K: lane = (position pk = 16 wave + lane / 4, dim quarter dq =
+    // lane % 4), float4 j at dims 16 j + 4 dq (four lanes cover 64 B)
+    const int pk = wave * 16 + (lane >> 2), dq = lane & 3;
+    const bool kvalid = pk < np;
+    const float4* Kp = (const float4*)(a.kc + ((size_t)g * a.max_seq + p0 + (pk < nold ? pk : 0)) * HD) + dq;
+    float4 kv[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) kv[j] = Kp[4 * j];
+    // cached V: thread t loads float4 column t % 32 of rows t/32 + 8u
+    const float4* Vg = (const float4*)(a.vc + ((size_t)g * a.max_seq + p0) * HD);
+    float4 vv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int r = (t >> 5) + 8 * u;
+        vv[u] = Vg[(size_t)(r < nold ? r : 0) * (HD / 4) + (t & 31)];
+    }
+    // queries: q-norm + RoPE
+#pragma unroll
+    for (int i = 0; i < NQW; i++) {
+        const int qi = wave + 4 * i;
+        const float2 o = norm_rope(qx0[i], qx1[i], qw0, qw1, qcs[i], a.eps);
+        if (qi < nq) {
             Q[qi][lane] = o.x;
             Q[qi][lane + 64] = o.y;
         }
-        // new rows that fall in this chunk: K and V computed here and appended
-        append_rows(a, g, p0, pos0, wave, lane, Kn, V);
+    }
+    // new rows: k-norm + RoPE, appended to the cache, kept in LDS
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int r = (t >> 5) + 8 * u;
-            if (r < nold || r >= np) *(float4*)&V[r][4 * (t & 31)] = vv[u];
-        }
-        __syncthreads();
-        if (kvalid && pk >= nold) {
-            const int b = p0 + pk - pos0;
-#pragma unroll
-            for (int j = 0; j < 8; j++) kv[j] = *(const float4*)&Kn[b][32 * dq + 4 * j];
-        }
-        // scores: lanes (pk, dq) reduce their quarter dots over the 4 quarters
-        const float scale = 1.0f / sqrtf((float)HD);
-        for (int q0 = 0; q0 < nq; q0 += 8) {
-            float acc[8];
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                float s = 0.f;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float4 qq = *(const float4*)&Q[q0 + i][32 * dq + 4 * j];
-                    s += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
-                }
-                s += __shfl_xor(s, 16);
-                s += __shfl_xor(s, 32);
-                acc[i] = s;
-            }
-            if (dq == 0) {
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int qi = q0 + i;
-                    if (qi < nq) {
-                        const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
-                        S[qi][pk] = see ? acc[i] * scale : -INFINITY;
-                    }
-                }
-            }
-        }
-        __syncthreads();
-        const int nqw = (nq - wave + 3) >> 2;
-        switch (nqw) {
-            case 0: break;
-            case 1: attn_values<1>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            case 2: attn_values<2>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            case 3: attn_values<3>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            case 4: attn_values<4>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            case 5: attn_values<5>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            case 6: attn_values<6>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            case 7: attn_values<7>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
-            default: attn_values<8>(S, V, wave, lane, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po); break;
+    for (int j = 0; j < NR; j++) {
+        const int b = b_lo + wave + 4 * j;
+        if (b < b_hi) {
+            const int pos = pos0 + b;
+            const float2 k = norm_rope(kx0[j], kx1[j], kw0, kw1, kcs[j], a.eps);
+            Kn[b][lane] = k.x;
+            Kn[b][lane + 64] = k.y;
+            V[pos - p0][lane] = vx0[j];
+            V[pos - p0][lane + 64] = vx1[j];
+            float* kd = a.kc + ((size_t)g * a.max_seq + pos) * HD;
+            float* vd = a.vc + ((size_t)g * a.max_seq + pos) * HD;
+            kd[lane] = k.x;
+            kd[lane + 64] = k.y;
+            vd[lane] = vx0[j];
+            vd[lane + 64] = vx1[j];
         }
     }
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        const int r = (t >> 5) + 8 * u;
+        if (r < nold || r >= np) *(float4*)&V[r][4 * (t & 31)] = r < nold ? vv[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();
+    if (kvalid && pk >= nold) {
+        const int b = p0 + pk - pos0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) kv[j] = *(const float4*)&Kn[b][16 * j + 4 * dq];
+    }
+    // scores: lanes (pk, dq) dot their dims with every query, quad sums
+    const float scale = 1.0f / sqrtf((float)HD);
+    constexpr int QB = 4 * NQW < 8 ? 4 * NQW : 8;
+    for (int q0 = 0; q0 < nq; q0 += QB) {
+        float acc[QB];
+#pragma unroll
+        for (int i = 0; i < QB; i++) {
+            float sv = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 qq = *(const float4*)&Q[min(q0 + i, 4 * NQW - 1)][16 * j + 4 * dq];
+                sv += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+            }
+            sv += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sv), 0xb1, 0xf, 0xf, false));
+            sv += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sv), 0x4e, 0xf, 0xf, false));
+            acc[i] = sv;
+        }
+        if (dq == 0) {
+#pragma unroll
+            for (int i = 0; i < QB; i++) {
+                const int qi = q0 + i;
+                if (qi < nq) {
+                    const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
+                    S[qi][pk] = see ? acc[i] * scale : -INFINITY;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    const int nqw = (nq - wave + 3) >> 2;  // queries of this wave
+    if (nqw > 0) attn_values<NQW>(S, V, wave, lane, hpk, nh, g, c, a.nch, nqw, a.pm, a.pl, a.po);
 }
 
 // Argmax per row, ties to the highest index.  Pass 1: grid (nslices, nrows).
@@ -415,21 +443,25 @@ void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo
     hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
 }
 
-void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, const DevWeight* next, uint8_t* planes,
-                      float* xs) {
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st) {
     const int nch = (max_len + ATT_C - 1) / ATT_C;
-    hipLaunchKernelGGL(k_attention, dim3(a.nkv, nch), dim3(256), 0, st, a);
-    if (!a.attend) return;
-    if (next) {
-        const int nk = next->dtype == DT_Q8ROW ? next->kchunks : next->kchunks * 4;
-        const int threads = 64 * std::min(16, a.nh);
-        hipLaunchKernelGGL(k_attn_merge_prep, dim3(a.nb), dim3(threads), (size_t)a.nh * 128 * sizeof(float), st, a,
-                           next->dtype, nk, planes, xs);
-    } else {
-        hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
+    const int nqw = (a.nb * (a.nh / a.nkv) + 3) / 4;  // queries per wave
+    void (*k)(AttnArgs) = nullptr;
+    switch (nqw) {
+        case 0:
+        case 1: k = k_attention<1>; break;
+        case 2: k = k_attention<2>; break;
+        case 3: k = k_attention<3>; break;
+        case 4: k = k_attention<4>; break;
+        case 5: k = k_attention<5>; break;
+        case 6: k = k_attention<6>; break;
+        case 7: k = k_attention<7>; break;
+        default: k = k_attention<8>; break;
     }
+    hipLaunchKernelGGL(k, dim3(a.nkv, nch), dim3(256), 0, st, a);
+    if (!a.attend) return;
+    hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
 }
-
 
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
                    hipStream_t st) {
