@@ -216,14 +216,13 @@ XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
 // launch); other producers (concat, larger operands) run as a
 // one-workgroup-per-row kernel that writes the prepared planes, which the
 // GEMV copies to LDS (or reads in place when they do not fit).
-// Whether a batch of mb rows of src is prepared inside the GEMV workgroups:
-// for m <= 2 (plain decode, MTP drafts); measured on MI355X the
-// per-workgroup producer costs more than the producer launch for the m = 5
-// verify batch (2.62 vs 2.39 ms per K = 4 round) and less for m = 1 (1.40 vs
-// 1.58 ms per plain round).  CMF_GEMV_FUSED=n moves the limit (0: never).
+// Whether a batch of mb rows of src is prepared inside the GEMV workgroups
+// (gemv_fuse_pays; CMF_GEMV_FUSED=n instead fuses every batch of at most n
+// rows, 0: never).
 static bool fuse_ok(const DevWeight& w, const XSrc& src, int mb) {
-    static const int fuse_max = getenv("CMF_GEMV_FUSED") ? atoi(getenv("CMF_GEMV_FUSED")) : 2;
-    return mb <= fuse_max && fused_lds_bytes(w, src, mb) > 0;
+    static const int fuse_env = getenv("CMF_GEMV_FUSED") ? atoi(getenv("CMF_GEMV_FUSED")) : -1;
+    if (fused_lds_bytes(w, src, mb) == 0) return false;
+    return fuse_env >= 0 ? mb <= fuse_env : gemv_fuse_pays(w, mb);
 }
 
 int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int nb, bool resid,

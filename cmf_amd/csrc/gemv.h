@@ -78,6 +78,8 @@ enum { EPI_NONE = 0, EPI_SWIGLU = 1 };
 // LDS bytes of a GEMV whose workgroups evaluate src (XS_NORM / XS_ROWS)
 // themselves, 0 when src must be prepared by launch_prep_src first.
 size_t fused_lds_bytes(const DevWeight& w, const XSrc& src, int m);
+// Whether that path is the faster one for m rows of w.
+bool gemv_fuse_pays(const DevWeight& w, int m);
 int gemv(const DevWeight& w, const XSrc& src, float* y, int ldy, int m, int row_lo, int row_hi,
          bool resid, hipStream_t st, int ks_override = 0, int grid_override = 0, int epi = EPI_NONE);
 // Grouped GEMV: up to max_jobs jobs (the device list `jobs`, see GemvArgs),
@@ -229,10 +231,13 @@ __device__ inline void prep8_rows(const float* raw, int K, const float* amv, int
         if (u == 0) xs[b] = sx;
         const int idx = u >> 2, q4 = u & 3;
         const int c0 = (idx >> 2) * 64 + 16 * (idx & 3) + 4 * q4;
-        const float* x = raw + (size_t)b * K;
+        // K % 4 == 0: a unit is all inside or all past the row
+        const float4 xv = c0 < K ? *(const float4*)(raw + (size_t)b * K + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
         uint32_t a = 0, bb = 0, c = 0;
-#pragma unroll
-        for (int jj = 0; jj < 4; jj++) q8_split(c0 + jj < K ? x[c0 + jj] * inv : 0.f, jj, a, bb, c);
+        q8_split(xv.x * inv, 0, a, bb, c);
+        q8_split(xv.y * inv, 1, a, bb, c);
+        q8_split(xv.z * inv, 2, a, bb, c);
+        q8_split(xv.w * inv, 3, a, bb, c);
         const size_t off = ((size_t)idx * m + b) * 16 + 4 * q4;
         *(uint32_t*)(p0 + off) = a;
         *(uint32_t*)(p1 + off) = bb;
@@ -245,7 +250,6 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
     uint8_t* ph = planes;
     uint8_t* pl = planes + (size_t)ntiles * 64 * m;
     float* bias = (float*)(planes + (size_t)ntiles * 128 * m);
-    const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
     const int per = ntiles * 4;  // items per row (a multiple of 4: tiles never straddle rows)
     for (int i0 = 0; i0 < m * per; i0 += nthr) {  // uniform trip count (shuffles below)
         const int jx = i0 + tid;
@@ -256,22 +260,27 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
         if (amax > 0.f) frexpf(amax, &ex);
         const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
         if (on && idx == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
-        const float* x = raw + (size_t)b * K;
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
+        // K % 4 == 0: each half of the item is all inside or all past the row
+        const float* x = raw + (size_t)b * K + c0;
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 xa = on && c0 < K ? *(const float4*)x : z4;
+        const float4 xb = on && c0 + 4 < K ? *(const float4*)(x + 4) : z4;
+        const float xv[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};  // columns {0,4,2,6,1,5,3,7}
         uint16_t hv[8], lv[8];
         float part = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const int col = c0 + ord[j];
-            const float v = on && col < K ? x[col] * scale : 0.f;
+            const float v = xv[j] * scale;
             const _Float16 h = (_Float16)v;
             const _Float16 l = (_Float16)(v - (float)h);
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
             part += (float)h + (float)l;
         }
-        part += __shfl_xor(part, 1);
-        part += __shfl_xor(part, 2);
+        // the four items of a tile are lanes 4t'..4t'+3 of one quad
+        part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0xb1, 0xf, 0xf, false));
+        part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0x4e, 0xf, 0xf, false));
         if (!on) continue;
         const size_t off = ((size_t)idx * m + b) * 16;
         *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),

@@ -230,6 +230,16 @@ static int pick_ks(int nk) {
     return k;
 }
 
+// Whether evaluating the producer inside the GEMV workgroups beats a
+// producer launch: measured on MI355X (decode-layer shapes, m = 1, 2, 5) it
+// does while every wave of a workgroup stages at most two operand rows
+// (the staging is spread over the workgroup's 64 * KS threads).
+bool gemv_fuse_pays(const DevWeight& w, int m) {
+    int ks = pick_ks(w.kchunks);
+    if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);
+    return m <= 2 * ks;
+}
+
 // Kernel choice and launch of a filled GemvArgs (grid.y = gridy jobs).
 static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int grid_override, int gridy,
                        hipStream_t st) {

@@ -116,19 +116,33 @@ __device__ __forceinline__ void stage_fused(int mode, double eps, int m, int K, 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nt >> 6;
     const bool nrm = mode == XS_NORM;
     const float* wn = raw + (size_t)m * K;
+    // float4 LDS reads, four in flight per lane (K % 4 == 0, rows 16 B
+    // aligned): each pass costs about one LDS round trip per 1024 columns
+    const int K4 = K >> 2;
     for (int b = wave; b < m; b += nw) {
-        float* xr = raw + (size_t)b * K;
+        float4* xr = (float4*)(raw + (size_t)b * K);
+        const float4* w4 = (const float4*)wn;
         float inv = 1.f;
         if (nrm) {
             double acc = 0.0;
-            for (int i = lane; i < K; i += 64) acc += (double)xr[i] * (double)xr[i];
+#pragma unroll 4
+            for (int i = lane; i < K4; i += 64) {
+                const float4 v = xr[i];
+                acc += (double)v.x * (double)v.x + (double)v.y * (double)v.y + (double)v.z * (double)v.z +
+                       (double)v.w * (double)v.w;
+            }
             inv = 1.0f / (float)sqrt(wave_sum(acc) / (double)K + eps);
         }
         float am = 0.f;
-        for (int i = lane; i < K; i += 64) {
-            const float y = nrm ? xr[i] * inv * wn[i] : xr[i];
-            xr[i] = y;
-            am = fmaxf(am, fabsf(y));
+#pragma unroll 4
+        for (int i = lane; i < K4; i += 64) {
+            float4 v = xr[i];
+            if (nrm) {
+                const float4 ww = w4[i];
+                v = make_float4(v.x * inv * ww.x, v.y * inv * ww.y, v.z * inv * ww.z, v.w * inv * ww.w);
+                xr[i] = v;
+            }
+            am = fmaxf(am, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
         }
         am = wave_max(am);
         if (lane == 0) amv[b] = am;

@@ -591,4 +591,59 @@ int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const floa
     return CMF_OK;
 }
 
+int cmf_time_gemv_rows(const cmf_weight* ws, int nw, const float* d_x, int ldx, const float* d_norm_w, int b,
+                       float* d_y, int ldy, int fused, int warmup, int iters, float* avg_ms) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!ws || nw < 1 || iters < 1 || b < 1 || b > MAXB || !d_x || !avg_ms) return fail("time_gemv_rows: bad arguments");
+    hipStream_t st = stream();
+    XSrc src{};
+    src.mode = d_norm_w ? XS_NORM : XS_ROWS;
+    src.x = d_x;
+    src.ldx = ldx;
+    src.w = d_norm_w;
+    src.eps = 1e-6;
+    uint8_t* planes = nullptr;
+    float* xs = nullptr;
+    size_t pb = 0;
+    for (int i = 0; i < nw; i++) pb = std::max(pb, prep_bytes(ws[i]->w));
+    if (!fused) {
+        CMF_HIP(hipMalloc(&planes, pb));
+        CMF_HIP(hipMalloc(&xs, 16 * sizeof(float)));
+    }
+    auto one = [&](int i) -> int {
+        const DevWeight& w = ws[i % nw]->w;
+        if (fused) return gemv(w, src, d_y, ldy, b, 0, w.rows, false, st);
+        if (launch_prep_src(w, src, b, planes, xs, st) != CMF_OK) return CMF_ERR;
+        XSrc g{};
+        g.mode = XS_GLOBAL;
+        g.planes = planes;
+        g.xs = xs;
+        return gemv(w, g, d_y, ldy, b, 0, w.rows, false, st);
+    };
+    int rc = CMF_OK;
+    for (int i = 0; i < warmup && rc == CMF_OK; i++) rc = one(i);
+    float ms = 0.f;
+    if (rc == CMF_OK) {
+        int rate_khz = 100000;
+        (void)hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, g_dev);
+        hipEvent_t e0, e1;
+        CMF_HIP(hipEventCreate(&e0));
+        CMF_HIP(hipEventCreate(&e1));
+        hipLaunchKernelGGL(k_spin, dim3(1), dim3(64), 0, st, (unsigned long long)rate_khz * 5, 1 << 22);
+        CMF_HIP(hipEventRecord(e0, st));
+        for (int i = 0; i < iters && rc == CMF_OK; i++) rc = one(i);
+        CMF_HIP(hipEventRecord(e1, st));
+        CMF_HIP(hipEventSynchronize(e1));
+        CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+        (void)hipEventDestroy(e0);
+        (void)hipEventDestroy(e1);
+    }
+    if (planes) (void)hipFree(planes);
+    if (xs) (void)hipFree(xs);
+    if (rc != CMF_OK) return rc;
+    *avg_ms = ms / iters;
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
 }  // extern "C"

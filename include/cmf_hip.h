@@ -89,6 +89,15 @@ int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int
  * measured with HIP events on the library stream. */
 int cmf_time_gemv(const cmf_weight* ws, int nw, const void* d_planes, const float* d_xs, int b,
                   float* d_y, int ldy, int ks, int warmup, int iters, float* avg_ms);
+/* Average device time (ms) of `iters` back-to-back GEMVs y[b] = ws[i % nw]
+ * x'[b] whose operand x' is produced from device rows d_x [b][ldx] (the
+ * layer input): rms_norm(x) * d_norm_w when d_norm_w is not NULL (eps
+ * 1e-6), else the rows themselves.  fused = 1: every GEMV workgroup
+ * evaluates the producer itself (fails when that path does not apply);
+ * fused = 0: a producer launch before each GEMV.  No counterpart in the
+ * reference: a measurement helper for the decode layer's operand paths. */
+int cmf_time_gemv_rows(const cmf_weight* ws, int nw, const float* d_x, int ldx, const float* d_norm_w, int b,
+                       float* d_y, int ldy, int fused, int warmup, int iters, float* avg_ms);
 /* Average device time (ms) of `iters` large-batch GEMMs y[m][rows] = w x
  * (q4t / q4tp; operand preparation included), x [m][cols] and y on the
  * device.  No counterpart in the reference: a measurement helper. */
