@@ -95,6 +95,7 @@ SIGNATURES = {
     "cmf_gemv_prepared": (_I, [_P, _P, _P, _I, _P, _I, _I]),
     "cmf_time_gemv": (_I, [C.POINTER(_P), _I, _P, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_copy": (_I, [_S, _I, _I, C.POINTER(_F)]),
+    "cmf_time_attention": (_I, [_P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_gemv_rows": (_I, [C.POINTER(_P), _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_gemm": (_I, [_P, _P, _I, _P, _I, _I, C.POINTER(_F)]),
     "cmf_moe_create": (_I, [_I, _I, _I, _I, _I, _F, C.POINTER(_P)]),

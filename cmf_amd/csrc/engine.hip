@@ -848,4 +848,49 @@ int cmf_kv_export(cmf_model m, int li, int n, float* k, float* v) {
     return CMF_OK;
 }
 
+int cmf_time_attention(cmf_model m, int nb, int pos0, int merge, int iters, float* avg_ms) {
+    if (ready(m)) return CMF_ERR;
+    const auto& c = m->c;
+    if (nb < 1 || nb > MAXB || pos0 < 0 || pos0 + nb > c.max_seq || iters < 1 || !avg_ms)
+        return fail("time_attention: 1 <= nb <= 16, pos0 + nb <= max_seq");
+    if (c.n_heads / c.n_kv * nb > 32) return fail("time_attention: at most 32 queries per kv head");
+    hipStream_t s = stream();
+    const int hd = c.head_dim, QKV = (c.n_heads + 2 * c.n_kv) * hd;
+    int* pb = m->toks;  // position base (scratch)
+    hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, pos0);
+    auto one = [&](int i) {
+        LayerDev& l = m->L[i % c.n_layers];
+        AttnArgs at{m->qkv_out, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq, nb, c.n_heads, c.n_kv,
+                    c.eps, pb, 0, m->pm, m->pl, m->po, m->nch_cap, m->ao, 1};
+        launch_attention(at, pos0 + nb, s, merge != 0);
+    };
+    for (int i = 0; i < 2 * c.n_layers; i++) one(i);
+    int rate_khz = 100000;
+    (void)hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, 0);
+    hipEvent_t e0, e1;
+    CMF_HIP(hipEventCreate(&e0));
+    CMF_HIP(hipEventCreate(&e1));
+    // captured into a graph, as the decode rounds run
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    CMF_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < iters; i++) one(i);
+    CMF_HIP(hipStreamEndCapture(s, &g));
+    CMF_HIP(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    CMF_HIP(hipGraphLaunch(ge, s));
+    CMF_HIP(hipEventRecord(e0, s));
+    CMF_HIP(hipGraphLaunch(ge, s));
+    CMF_HIP(hipEventRecord(e1, s));
+    CMF_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipGraphExecDestroy(ge);
+    (void)hipGraphDestroy(g);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *avg_ms = ms / iters;
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
 }  // extern "C"

@@ -31,8 +31,8 @@ struct AttnArgs {
     float* out;
     int attend;         // 0: only append the rows' K/V (no queries, no output)
 };
-// k_attention (chunk partials) then k_attn_merge (rows of a.out).
-void launch_attention(const AttnArgs& a, int max_len, hipStream_t st);
+// k_attention (chunk partials) then, with merge, k_attn_merge (rows of a.out).
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge = true);
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
                    hipStream_t st);
 

@@ -16,6 +16,8 @@
 
 namespace cmf {
 
+typedef float float4v __attribute__((ext_vector_type(4)));
+
 // --------------------------------------------------------------------------
 // block reductions (256 threads)
 // --------------------------------------------------------------------------
@@ -242,7 +244,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const int pos0 = *a.pbase + a.padd;
     const int stored = pos0 + a.nb;
     const int p0 = c * C;
-    __shared__ __align__(16) float Q[4 * NQW][HD];
+    constexpr int QR = 4 * NQW < 16 ? 16 : 4 * NQW;  // Q rows: whole MFMA query blocks
+    __shared__ __align__(16) float Q[QR][HD];
     __shared__ __align__(16) float V[C][HD + 4];
     __shared__ __align__(16) float S[4 * NQW][C];
     __shared__ __align__(16) float Kn[MAXB][HD];
@@ -282,9 +285,13 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
         kcs[j] = a.rope[(size_t)(pos0 + b) * 64 + lane];
     }
     const float kw0 = a.kn[lane], kw1 = a.kn[lane + 64];
-    // 3. cached K: lane = (position pk = 16 wave + lane / 4, dim quarter dq =
-    // lane % 4), float4 j at dims 16 j + 4 dq (four lanes cover 64 B)
-    const int pk = wave * 16 + (lane >> 2), dq = lane & 3;
+    // 3. cached K: lane = (position pk, dim group dq), float4 j at dims 16 j
+    // + 4 dq.  MF (several queries per wave): pk = 16 wave + lane % 16, dq =
+    // lane / 16, the B operand of the score MFMAs (k step 4 j + c <-> dim
+    // 16 j + 4 dq + c); otherwise pk = 16 wave + lane / 4, dq = lane % 4 and
+    // the four dim groups of a position are one quad (VALU dots, quad sums).
+    constexpr bool MF = NQW > 1;
+    const int pk = wave * 16 + (MF ? (lane & 15) : (lane >> 2)), dq = MF ? lane >> 4 : lane & 3;
     const bool kvalid = pk < np;
     const float4* Kp = (const float4*)(a.kc + ((size_t)g * a.max_seq + p0 + (pk < nold ? pk : 0)) * HD) + dq;
     float4 kv[8];
@@ -298,6 +305,8 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
         const int r = (t >> 5) + 8 * u;
         vv[u] = Vg[(size_t)(r < nold ? r : 0) * (HD / 4) + (t & 31)];
     }
+    // every load is issued before any of them is waited for
+    __builtin_amdgcn_sched_barrier(0);
     // queries: q-norm + RoPE
 #pragma unroll
     for (int i = 0; i < NQW; i++) {
@@ -338,31 +347,55 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < 8; j++) kv[j] = *(const float4*)&Kn[b][16 * j + 4 * dq];
     }
-    // scores: lanes (pk, dq) dot their dims with every query, quad sums
+    // scores (MF) by fp32 MFMA (16x16x4): A = 16 queries (lane % 16) x the dims
+    // of group lane / 16, B = K (positions of this wave x the same dims),
+    // 32 k steps cover the 128 dims; D row 4 (lane / 16) + e = query, column
+    // lane % 16 = position.  Query rows past nq are never stored.
     const float scale = 1.0f / sqrtf((float)HD);
-    constexpr int QB = 4 * NQW < 8 ? 4 * NQW : 8;
-    for (int q0 = 0; q0 < nq; q0 += QB) {
-        float acc[QB];
+    if constexpr (!MF) {
+        // at most 4 queries: VALU dots of the lane's 32 dims, quad DPP sums
+        float acc[4];
 #pragma unroll
-        for (int i = 0; i < QB; i++) {
+        for (int i = 0; i < 4; i++) {
             float sv = 0.f;
+            if (i < nq) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float4 qq = *(const float4*)&Q[min(q0 + i, 4 * NQW - 1)][16 * j + 4 * dq];
-                sv += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+                for (int j = 0; j < 8; j++) {
+                    const float4 qq = *(const float4*)&Q[i][16 * j + 4 * dq];
+                    sv += kv[j].x * qq.x + kv[j].y * qq.y + kv[j].z * qq.z + kv[j].w * qq.w;
+                }
+                sv += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sv), 0xb1, 0xf, 0xf, false));
+                sv += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sv), 0x4e, 0xf, 0xf, false));
             }
-            sv += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sv), 0xb1, 0xf, 0xf, false));
-            sv += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sv), 0x4e, 0xf, 0xf, false));
             acc[i] = sv;
         }
         if (dq == 0) {
 #pragma unroll
-            for (int i = 0; i < QB; i++) {
-                const int qi = q0 + i;
-                if (qi < nq) {
-                    const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
-                    S[qi][pk] = see ? acc[i] * scale : -INFINITY;
+            for (int i = 0; i < 4; i++) {
+                if (i < nq) {
+                    const bool see = kvalid && p0 + pk <= pos0 + i / hpk;
+                    S[i][pk] = see ? acc[i] * scale : -INFINITY;
                 }
+            }
+        }
+    }
+    for (int qb = 0; MF && qb < nq; qb += 16) {
+        const float* qrow = Q[min(qb + (lane & 15), QR - 1)];
+        float4v d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float4 qa = *(const float4*)&qrow[16 * j + 4 * dq];
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.x, kv[j].x, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.y, kv[j].y, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.z, kv[j].z, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa.w, kv[j].w, d, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int qi = qb + 4 * dq + e;
+            if (qi < nq) {
+                const bool see = kvalid && p0 + pk <= pos0 + qi / hpk;
+                S[qi][pk] = see ? d[e] * scale : -INFINITY;
             }
         }
     }
@@ -443,7 +476,7 @@ void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo
     hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
 }
 
-void launch_attention(const AttnArgs& a, int max_len, hipStream_t st) {
+void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge) {
     const int nch = (max_len + ATT_C - 1) / ATT_C;
     const int nqw = (a.nb * (a.nh / a.nkv) + 3) / 4;  // queries per wave
     void (*k)(AttnArgs) = nullptr;
@@ -459,7 +492,7 @@ void launch_attention(const AttnArgs& a, int max_len, hipStream_t st) {
         default: k = k_attention<8>; break;
     }
     hipLaunchKernelGGL(k, dim3(a.nkv, nch), dim3(256), 0, st, a);
-    if (!a.attend) return;
+    if (!a.attend || !merge) return;
     hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
 }
 

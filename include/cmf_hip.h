@@ -219,6 +219,14 @@ int cmf_state_get(cmf_model m, int* next_pos, float* hidden);
  * k/v [n_kv][n][head_dim]. */
 int cmf_kv_export(cmf_model m, int li, int n, float* k, float* v);
 
+/* Average device time (ms) of the decode attention of nb rows at positions
+ * pos0 .. pos0+nb-1 (qk-norm, RoPE, KV append, causal attention over the
+ * cache; merge = 0 leaves out the merge of the chunk partials), rotating
+ * over the layers of model m, `iters` launches captured in a HIP graph.
+ * Writes the KV rows at those positions.  No counterpart in the reference:
+ * a measurement helper. */
+int cmf_time_attention(cmf_model m, int nb, int pos0, int merge, int iters, float* avg_ms);
+
 #ifdef __cplusplus
 }
 #endif
