@@ -233,10 +233,14 @@ static int pick_ks(int nk) {
 // Whether evaluating the producer inside the GEMV workgroups beats a
 // producer launch: measured on MI355X (decode-layer shapes, m = 1, 2, 5) it
 // does while every wave of a workgroup stages at most two operand rows
-// (the staging is spread over the workgroup's 64 * KS threads).
+// (the staging is spread over the workgroup's 64 * KS threads), except on
+// matrices much taller than one wave of workgroups for m > 2 (the lm_head:
+// there the raw rows' LDS halves the occupancy that hides the weight
+// stream's latency, 40.7 vs 32.2 us at m = 5).
 bool gemv_fuse_pays(const DevWeight& w, int m) {
     int ks = pick_ks(w.kchunks);
     if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);
+    if (m > 2 && w.rows_pad / 16 > 8 * num_cus()) return false;
     return m <= 2 * ks;
 }
 

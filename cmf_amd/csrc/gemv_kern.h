@@ -43,6 +43,11 @@ typedef int int4v __attribute__((ext_vector_type(4)));
 // Weight words are read exactly once per launch: nontemporal loads keep the
 // stream from displacing the operand planes and partials in L2 (measured on
 // a plain 28 MB read: 5.8 -> 5.6 us; 108 MB: 19.0 -> 17.6 us).
+// These are flat loads (generic pointer), which also count against
+// lgkmcnt: a wave's first LDS read of the operand then waits for its whole
+// batch of weight steps.  Measured on MI355X that is faster than computing
+// step by step as global loads arrive (q4t 12288x4096 m=1: 8.05 vs 8.30 us,
+// 4096x12288: 9.04 vs 9.94 us, decode round 1.07 vs 1.09 ms).
 __device__ __forceinline__ int4v ld_stream(const int4v* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
     const int4v v = __builtin_nontemporal_load((const int4v*)p);
@@ -159,12 +164,26 @@ __device__ __forceinline__ int planes_lds_bytes(int fmt, int nk, int m) {
     return (b + 1023) & ~1023;
 }
 
-// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14,
-// expcnt 6:4 left at 7, lgkmcnt 11:8)
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4
+// and lgkmcnt 11:8 left at their maxima, i.e. not waited for)
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The epilogue's global reads for row block rb, issued at the start of the
+// kernel: the q8 row scale (rowscale != nullptr) and, for a residual GEMV,
+// y[b][row] of the lane's batch rows b = 4s + v (indices clamped, so every
+// lane loads; values for rows or batch rows out of range are never used).
+__device__ __forceinline__ void prefetch_epilogue(const GemvArgs& a, int rb, int r, int s, int M,
+                                                  const float* rowscale, float& rs, float (&yv)[4]) {
+    const int row = max(a.row_lo, min((a.rb0 + rb) * 16 + r, a.row_hi - 1));
+    rs = rowscale ? rowscale[row] : 0.f;
+    if (a.resid) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) yv[v] = a.y[(size_t)min(4 * s + v, M - 1) * a.ldy + (row - a.row_lo)];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -261,6 +280,12 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     float2 pA[RB] = {};
     float xsv = 0.f;
     float* raw = (float*)(smem + planes_lds_bytes(FMT, ntg, M));
+    // the first row blocks' residual rows, requested first (the epilogue
+    // then waits for no memory round trip)
+    const int rb_first = rb;
+    float rs_unused, y_first[RB][4];
+#pragma unroll
+    for (int q = 0; q < RB; q++) prefetch_epilogue(a, rb + q, r, s, M, nullptr, rs_unused, y_first[q]);
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, ntg * (32 * M + 16), smem);  // hi + lo planes + tile biases
         xsv = a.src.xs[threadIdx.x & 15];
@@ -395,7 +420,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
                         if (b < M) {
                             float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
                             const float val = o4[v] * lxs[b] * 16777216.0f;  // 2^24: denormal nibbles
-                            *yp = a.resid ? *yp + val : val;
+                            *yp = a.resid ? (rb == rb_first ? y_first[q][v] : *yp) + val : val;
                         }
                     }
                 }
@@ -469,6 +494,11 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     int4v wA[SP];
     float xsv = 0.f;
     float* raw = (float*)(smem + planes_lds_bytes(DT_Q8ROW, nkc, M));
+    // the first row block's row scale and residual rows, requested first so
+    // that the epilogue does not wait for a memory round trip
+    const int rb_first = rb;
+    float rs_first, y_first[4];
+    prefetch_epilogue(a, rb, r, s, M, (const float*)a.scale, rs_first, y_first);
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, nkc * 4 * M * 3, smem);  // three planes
         xsv = a.src.xs[threadIdx.x & 15];
@@ -565,9 +595,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
                 __builtin_amdgcn_wave_barrier();
             }
             const int row = (a.rb0 + rb) * 16 + r;
+            const bool first = rb == rb_first;
             if (a.epi == EPI_SWIGLU) {
                 // rows r < 8 gate, r + 8 the matching up row (lane ^ 8)
-                const float rs = ((const float*)a.scale)[row];
+                const float rs = first ? rs_first : ((const float*)a.scale)[row];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int b = 4 * s + v;
@@ -578,7 +609,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
                         a.y[(size_t)b * a.ldy + (a.rb0 + rb) * 8 + r] = (val / (1.0f + expf(-val))) * u;
                 }
             } else if (row >= a.row_lo && row < a.row_hi) {
-                const float rs = ((const float*)a.scale)[row];
+                const float rs = first ? rs_first : ((const float*)a.scale)[row];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int b = 4 * s + v;
@@ -586,7 +617,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
                         const float tt = f0[v] + f1[v] * 0.0078125f + f2[v] * 6.103515625e-05f;
                         float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
                         const float val = (tt * lxs[b]) * rs;
-                        *yp = a.resid ? *yp + val : val;
+                        *yp = a.resid ? (first ? y_first[v] : *yp) + val : val;
                     }
                 }
             }
