@@ -43,14 +43,28 @@ typedef int int4v __attribute__((ext_vector_type(4)));
 // Weight words are read exactly once per launch: nontemporal loads keep the
 // stream from displacing the operand planes and partials in L2 (measured on
 // a plain 28 MB read: 5.8 -> 5.6 us; 108 MB: 19.0 -> 17.6 us).
-// These are flat loads (generic pointer), which also count against
-// lgkmcnt: a wave's first LDS read of the operand then waits for its whole
-// batch of weight steps.  Measured on MI355X that is faster than computing
-// step by step as global loads arrive (q4t 12288x4096 m=1: 8.05 vs 8.30 us,
-// 4096x12288: 9.04 vs 9.94 us, decode round 1.07 vs 1.09 ms).
-__device__ __forceinline__ int4v ld_stream(const int4v* p) { return __builtin_nontemporal_load(p); }
+// Every load issued while the operand's direct-to-LDS copy is in flight
+// goes through a global-address-space pointer: a generic (flat) load may
+// alias LDS, so the compiler waits for the whole copy (vmcnt(0)) before
+// issuing it, which put a full memory round trip in front of the weight
+// stream.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gptr(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+// (scalar and ext_vector types only: the HIP vector classes cannot be copied
+// out of another address space)
+template <class T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return *gptr(p);
+}
+__device__ __forceinline__ float2 ldg_f2(const float2* p) {
+    const uint64_t u = ldg((const uint64_t*)p);
+    return make_float2(__uint_as_float((uint32_t)u), __uint_as_float((uint32_t)(u >> 32)));
+}
+__device__ __forceinline__ int4v ld_stream(const int4v* p) { return __builtin_nontemporal_load(gptr(p)); }
 __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
-    const int4v v = __builtin_nontemporal_load((const int4v*)p);
+    const int4v v = __builtin_nontemporal_load(gptr((const int4v*)p));
     return make_uint4((uint32_t)v.x, (uint32_t)v.y, (uint32_t)v.z, (uint32_t)v.w);
 }
 
@@ -179,10 +193,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 __device__ __forceinline__ void prefetch_epilogue(const GemvArgs& a, int rb, int r, int s, int M,
                                                   const float* rowscale, float& rs, float (&yv)[4]) {
     const int row = max(a.row_lo, min((a.rb0 + rb) * 16 + r, a.row_hi - 1));
-    rs = rowscale ? rowscale[row] : 0.f;
+    rs = rowscale ? ldg(rowscale + row) : 0.f;
     if (a.resid) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) yv[v] = a.y[(size_t)min(4 * s + v, M - 1) * a.ldy + (row - a.row_lo)];
+        for (int v = 0; v < 4; v++) yv[v] = ldg(a.y + (size_t)min(4 * s + v, M - 1) * a.ldy + (row - a.row_lo));
     }
 }
 
@@ -249,10 +263,13 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
             for (int u = 0; u < SP; u++) {
                 const size_t t = wbase + min(t0 + u, ntg - 1);
                 wv[q * SP + u] = ld_stream((const uint4*)a.w + t * 64 + lane);
-                if constexpr (TP) sv[q * SP + u] = make_uint2(((const uint32_t*)a.scale)[t * 16 + r], 0u);
-                else sv[q * SP + u] = ((const uint2*)a.scale)[t * 16 + r];
+                if constexpr (TP) sv[q * SP + u] = make_uint2(ldg((const uint32_t*)a.scale + t * 16 + r), 0u);
+                else {
+                    const uint64_t sw = ldg((const uint64_t*)a.scale + t * 16 + r);  // (scalar type: see gptr)
+                    sv[q * SP + u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
+                }
             }
-            if constexpr (TP) pv[q] = a.rowp[(a.rb0 + min(rbl + q, a.nrb - 1)) * 16 + r];
+            if constexpr (TP) pv[q] = ldg_f2(a.rowp + (a.rb0 + min(rbl + q, a.nrb - 1)) * 16 + r);
         }
     };
     // the 32-rung ladder of each row of the RB row blocks: t[c] = t[c-1] *
@@ -288,9 +305,13 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     for (int q = 0; q < RB; q++) prefetch_epilogue(a, rb + q, r, s, M, nullptr, rs_unused, y_first[q]);
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, ntg * (32 * M + 16), smem);  // hi + lo planes + tile biases
-        xsv = a.src.xs[threadIdx.x & 15];
+        xsv = ldg(a.src.xs + (threadIdx.x & 15));
     } else if constexpr (XM == XM_FUSED) {
         x_dma_rows(a.src, M, a.src.K, raw);
+        // the raw rows arrive before the weight stream is requested: measured
+        // on MI355X, staging overlapped with the stream then starts earlier
+        // than with both in flight together (down 1024x3072 m=1: 5.7 vs 6.4 us)
+        wait_vmcnt<0>();
     }
     __builtin_amdgcn_sched_barrier(0);
     load(wA, sA, pA, rb, 0);
@@ -443,7 +464,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
         if constexpr (TP)
             if (rn < a.nrb) {
 #pragma unroll
-                for (int q = 0; q < RB; q++) pn[q] = a.rowp[(a.rb0 + min(rn + q, a.nrb - 1)) * 16 + r];
+                for (int q = 0; q < RB; q++) pn[q] = ldg_f2(a.rowp + (a.rb0 + min(rn + q, a.nrb - 1)) * 16 + r);
             }
         process(wA, sA, pn, rn);
         if (rn >= a.nrb) break;
@@ -501,9 +522,13 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     prefetch_epilogue(a, rb, r, s, M, (const float*)a.scale, rs_first, y_first);
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, nkc * 4 * M * 3, smem);  // three planes
-        xsv = a.src.xs[threadIdx.x & 15];
+        xsv = ldg(a.src.xs + (threadIdx.x & 15));
     } else if constexpr (XM == XM_FUSED) {
         x_dma_rows(a.src, M, a.src.K, raw);
+        // the raw rows arrive before the weight stream is requested: measured
+        // on MI355X, staging overlapped with the stream then starts earlier
+        // than with both in flight together (down 1024x3072 m=1: 5.7 vs 6.4 us)
+        wait_vmcnt<0>();
     }
     __builtin_amdgcn_sched_barrier(0);
     load(wA, rb, 0);
