@@ -230,10 +230,12 @@ static int pick_ks(int nk) {
     return k;
 }
 
+constexpr int FUSED_MIN_KS = 8;  // waves of a workgroup that stages m > 2 rows
+
 // Whether evaluating the producer inside the GEMV workgroups beats a
 // producer launch: measured on MI355X (decode-layer shapes, m = 1, 2, 5) it
 // does while every wave of a workgroup stages at most two operand rows
-// (the staging is spread over the workgroup's 64 * KS threads), except on
+// (the staging is spread over the workgroup's threads), except on
 // matrices much taller than one wave of workgroups for m > 2 (the lm_head:
 // there the raw rows' LDS halves the occupancy that hides the weight
 // stream's latency, 40.7 vs 32.2 us at m = 5).
@@ -241,7 +243,7 @@ bool gemv_fuse_pays(const DevWeight& w, int m) {
     int ks = pick_ks(w.kchunks);
     if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);
     if (m > 2 && w.rows_pad / 16 > 8 * num_cus()) return false;
-    return m <= 2 * ks;
+    return m <= 8 && m <= 2 * std::max(ks, FUSED_MIN_KS);  // (measured up to the m = 5 verify batch)
 }
 
 // Kernel choice and launch of a filled GemvArgs (grid.y = gridy jobs).
@@ -253,6 +255,11 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
     // 4 tiles (128 columns)
     int ks = ks_override > 0 ? ks_override : pick_ks(w.kchunks);
     if (w.dtype != DT_Q8ROW && m > 8) ks = std::min(ks, 8);  // no 16-wave instance (registers)
+    // a workgroup that stages m > 2 rows itself gets at least 8 waves (those
+    // past the row's K steps only help with the staging, which is VALU
+    // bound; measured on MI355X 8 beats 4 and 16: K=4 round 1.80 ms vs 1.86
+    // and 1.88)
+    if (a.src.mode != XS_GLOBAL && m > 2 && ks_override <= 0) ks = std::max(ks, FUSED_MIN_KS);
     size_t lds = 0;
     int xm = XM_GLOBAL;
     if (a.src.mode == XS_GLOBAL) {
