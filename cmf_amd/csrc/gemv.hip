@@ -299,6 +299,19 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
             rb = c;
         }
     }
+    // grouped launches (MoE experts): two row blocks per workgroup share one
+    // operand copy; measured on MI355X for the config-5 layer 56.6 -> 53.0 us
+    // (3: 54.8 us).  CMF_GEMV_GRB overrides.
+    static const int grb_env = env_int("CMF_GEMV_GRB", 2);
+    if (gridy > 1 && grb_env > 1 && pick(grb_env)) {
+        GemvKernel kc = pick(grb_env);
+        const int oc = resident_per_cu(kc, threads, lds);
+        if (oc >= 1) {
+            k = kc;
+            occ = oc;
+            rb = grb_env;
+        }
+    }
     // one workgroup per RB row blocks while the CUs hold them all at once;
     // grouped launches always give every job its full set
     const int units = (a.nrb + rb - 1) / rb;

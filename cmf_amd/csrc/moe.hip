@@ -3,13 +3,15 @@
 // expert, the expert FFNs as grouped GEMVs and the weighted combine in the
 // reference's per-token order (moe_ffn_cpu, pipeline.rs:10997-11045).
 //
-//   1. k_moe_route    one workgroup per token: softmax of the router logits
+//   1. routing        one wave per token: softmax of the router logits
 //                     (max-subtracted, sequential sum), top-k by descending
 //                     probability with the lower index first on ties,
 //                     w_i = p_i / wsum, wsum = sum of the kept p (norm_topk)
-//                     or 1, divided by routed_scaling.
-//   2. k_moe_jobs     one job per distinct routed expert, in expert order,
-//                     and the job of every (token, rank) slot.
+//                     or 1, divided by routed_scaling;
+//   2. job numbering  one job per distinct routed expert, in expert order,
+//                     and the job of every (token, rank) slot; 1 and 2 are
+//                     one launch (k_moe_route_jobs), 2 alone for caller-routed
+//                     batches (k_moe_jobs).
 //   3. prep x         prepared operand of the b token rows (shared by all jobs).
 //   4. gate|up        grouped GEMV: job j = W_gu[e_j] x for all b rows (the
 //                     weights are read once per expert; rows of tokens that
@@ -25,66 +27,87 @@
 #include "common.h"
 #include "gemv.h"
 #include "runtime.h"
+#include "wave.h"
 
 namespace cmf {
 
 constexpr int MOE_MAX_EXPERTS = 1024;
 constexpr int MOE_MAX_TOPK = 32;
 
-__global__ __launch_bounds__(256) void k_moe_route(const float* __restrict__ logits, int ne, int k, int norm_topk,
-                                                   float scaling, int* __restrict__ idx, float* __restrict__ w) {
-    __shared__ float p[MOE_MAX_EXPERTS];
-    __shared__ float redm[4];
-    __shared__ float tot;
-    __shared__ int sel[MOE_MAX_TOPK];
-    const int t = blockIdx.x, tid = threadIdx.x;
-    const float* lg = logits + (size_t)t * ne;
+// Routing of token t by wave t (b <= 16 waves, all tokens at once): softmax
+// of the router logits (max-subtracted; the sum sequential in expert order,
+// as the reference adds), then the top k by k rounds of a wave arg-max over
+// the normalised p: the largest p, the lower index among equal p (the
+// reference's order), each pick removed before the next round.  w_i = p_i /
+// wsum with wsum = the sum of the kept p in rank order (norm_topk) or 1,
+// divided by routed_scaling.  The picks also go to sidx (LDS) for the job
+// numbering that follows.
+__device__ __forceinline__ void moe_route_tokens(const float* __restrict__ logits, int b, int ne, int k,
+                                                 int norm_topk, float scaling, int* __restrict__ idx,
+                                                 float* __restrict__ w, int* sidx) {
+    __shared__ float p[MAXB][MOE_MAX_EXPERTS];
+    __shared__ float tot[MAXB];
+    const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
+    const bool on = t < b;
+    const float* lg = logits + (size_t)(on ? t : 0) * ne;
     float mx = -INFINITY;
-    for (int e = tid; e < ne; e += blockDim.x) mx = fmaxf(mx, lg[e]);
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if ((tid & 63) == 0) redm[tid >> 6] = mx;
+    for (int e = lane; e < ne; e += 64) mx = fmaxf(mx, lg[e]);
+    mx = wave_max(mx);
+    for (int e = lane; e < ne; e += 64) p[t][e] = expf(lg[e] - mx);
     __syncthreads();
-    mx = fmaxf(fmaxf(redm[0], redm[1]), fmaxf(redm[2], redm[3]));
-    for (int e = tid; e < ne; e += blockDim.x) p[e] = expf(lg[e] - mx);
-    __syncthreads();
-    if (tid == 0) {  // the reference sums in expert order
-        float s = 0.0f;
-        for (int e = 0; e < ne; e++) s += p[e];
-        tot = s;
-    }
-    __syncthreads();
-    const float s = tot;
-    for (int e = tid; e < ne; e += blockDim.x) p[e] = p[e] / s;
-    __syncthreads();
-    // rank of e = experts ahead of it (higher p, or equal p and lower index)
-    for (int e = tid; e < ne; e += blockDim.x) {
-        const float pe = p[e];
-        int rank = 0;
-        for (int f = 0; f < ne; f++) rank += (p[f] > pe || (p[f] == pe && f < e)) ? 1 : 0;
-        if (rank < k) sel[rank] = e;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float ws;
-        if (norm_topk) {
-            float a = 0.0f;
-            for (int i = 0; i < k; i++) a += p[sel[i]];
-            ws = a / scaling;
-        } else {
-            ws = 1.0f / scaling;
+    if (lane == 0) {
+        float sm = 0.0f;  // in expert order; the reads eight at a time
+        int e = 0;
+        for (; e + 8 <= ne; e += 8) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = p[t][e + j];
+#pragma unroll
+            for (int j = 0; j < 8; j++) sm += v[j];
         }
-        for (int i = 0; i < k; i++) {
-            idx[t * k + i] = sel[i];
-            w[t * k + i] = p[sel[i]] / ws;
-        }
+        for (; e < ne; e++) sm += p[t][e];
+        tot[t] = sm;
     }
+    __syncthreads();
+    const float sm = tot[t];
+    for (int e = lane; e < ne; e += 64) p[t][e] = p[t][e] / sm;
+    float wsum = 0.0f;
+    for (int i = 0; i < k; i++) {
+        // the lane's best (largest p, then lowest index) among its experts;
+        // picked experts hold -1
+        float bv = -1.0f;
+        int bi = ne;
+        for (int e = lane; e < ne; e += 64) {
+            const float pe = p[t][e];
+            if (pe > bv) {
+                bv = pe;
+                bi = e;
+            }
+        }
+        const float v = wave_max(bv);
+        const int e = (int)wave_reduce_f32(bv == v ? (float)bi : INFINITY, INFINITY,
+                                           [](float x, float y) { return fminf(x, y); });
+        const float pv = v;  // p of the pick (every lane)
+        if (lane == (e & 63)) p[t][e] = -1.0f;
+        if (on && lane == 0) {
+            idx[t * k + i] = e;
+            sidx[t * k + i] = e;
+            w[t * k + i] = pv;  // scaled below
+        }
+        wsum += pv;
+    }
+    if (on && lane == 0) {
+        const float ws = norm_topk ? wsum / scaling : 1.0f / scaling;
+        for (int i = 0; i < k; i++) w[t * k + i] = w[t * k + i] / ws;
+    }
+    __syncthreads();
 }
 
 // jobs = [njobs, expert of job 0, ...] (experts in increasing order);
 // slot[t * k + i] = job of token t's rank-i expert.  One workgroup of 256:
 // per-wave ballots and popcounts number the used experts.
-__global__ __launch_bounds__(256) void k_moe_jobs(const int* __restrict__ idx, int b, int k, int ne,
-                                                  int* __restrict__ jobs, int* __restrict__ slot) {
+__device__ __forceinline__ void moe_jobs_body(const int* idx, int b, int k, int ne, int* __restrict__ jobs,
+                                              int* __restrict__ slot) {
     __shared__ int job_of[MOE_MAX_EXPERTS];
     __shared__ int used[MOE_MAX_EXPERTS];
     __shared__ int wave_base[MOE_MAX_EXPERTS / 64 + 1];
@@ -121,6 +144,20 @@ __global__ __launch_bounds__(256) void k_moe_jobs(const int* __restrict__ idx, i
     }
     __syncthreads();
     for (int i = tid; i < b * k; i += blockDim.x) slot[i] = job_of[idx[i]];
+}
+__global__ __launch_bounds__(256) void k_moe_jobs(const int* __restrict__ idx, int b, int k, int ne,
+                                                  int* __restrict__ jobs, int* __restrict__ slot) {
+    moe_jobs_body(idx, b, k, ne, jobs, slot);
+}
+// Routing of the b tokens and their job numbering in one launch (one
+// workgroup, one wave per token slot).
+__global__ __launch_bounds__(1024) void k_moe_route_jobs(const float* __restrict__ logits, int b, int ne, int k,
+                                                        int norm_topk, float scaling, int* __restrict__ idx,
+                                                        float* __restrict__ w, int* __restrict__ jobs,
+                                                        int* __restrict__ slot) {
+    __shared__ int sidx[MAXB * MOE_MAX_TOPK];
+    moe_route_tokens(logits, b, ne, k, norm_topk, scaling, idx, w, sidx);
+    moe_jobs_body(sidx, b, k, ne, jobs, slot);
 }
 
 // out[t][h] = sum over ranks i (in order, from 0) of w[t][i] * yd[job][t][h];
@@ -191,9 +228,9 @@ static int moe_ready(cmf_moe m) {
 
 // Steps 3-7 on the routed batch (idx / w already on the device), k experts
 // per token.
-static int moe_experts(cmf_moe m, const float* d_x, int b, int k, float* d_out, hipStream_t s) {
+static int moe_experts(cmf_moe m, const float* d_x, int b, int k, float* d_out, hipStream_t s, bool numbered) {
     const int H = m->hidden, I = m->inter;
-    hipLaunchKernelGGL(k_moe_jobs, dim3(1), dim3(256), 0, s, m->idx, b, k, m->ne, m->jobs, m->slot);
+    if (!numbered) hipLaunchKernelGGL(k_moe_jobs, dim3(1), dim3(256), 0, s, m->idx, b, k, m->ne, m->jobs, m->slot);
     XSrc rows{};
     rows.mode = XS_ROWS;
     rows.x = d_x;
@@ -344,9 +381,9 @@ int cmf_moe_ffn_dev(cmf_moe m, const float* d_x, const float* d_logits, int b, f
     if (b < 1 || b > MAXB) return fail("moe: batch must be 1..16");
     if (!d_x || !d_logits || !d_out) return fail("moe: null pointer");
     hipStream_t s = stream();
-    hipLaunchKernelGGL(k_moe_route, dim3(b), dim3(256), 0, s, d_logits, m->ne, m->top_k, m->norm_topk, m->scaling,
-                       m->idx, m->w);
-    const int rc = moe_experts(m, d_x, b, m->top_k, d_out, s);
+    hipLaunchKernelGGL(k_moe_route_jobs, dim3(1), dim3(64 * MAXB), 0, s, d_logits, b, m->ne, m->top_k, m->norm_topk,
+                       m->scaling, m->idx, m->w, m->jobs, m->slot);
+    const int rc = moe_experts(m, d_x, b, m->top_k, d_out, s, true);
     if (rc != CMF_OK) return rc;
     CMF_HIP(hipGetLastError());
     return CMF_OK;
@@ -402,7 +439,7 @@ int cmf_moe_block(cmf_moe m, const float* x, const int32_t* experts, const float
     CMF_HIP(hipMemcpyAsync(m->x, x, sizeof(float) * m->hidden, hipMemcpyHostToDevice, s));
     CMF_HIP(hipMemcpyAsync(m->idx, experts, sizeof(int) * njobs, hipMemcpyHostToDevice, s));
     CMF_HIP(hipMemcpyAsync(m->w, weights, sizeof(float) * njobs, hipMemcpyHostToDevice, s));
-    const int rc = moe_experts(m, m->x, 1, njobs, m->out, s);
+    const int rc = moe_experts(m, m->x, 1, njobs, m->out, s, false);
     if (rc != CMF_OK) return rc;
     CMF_HIP(hipMemcpyAsync(out, m->out, sizeof(float) * m->hidden, hipMemcpyDeviceToHost, s));
     CMF_HIP(hipStreamSynchronize(s));
