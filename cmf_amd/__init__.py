@@ -81,6 +81,7 @@ SIGNATURES = {
     "cmf_weight_device_bytes": (_S, [_P]),
     "cmf_q8_matvec_range": (_I, [_P, _I, _P, _I, _I, _P]),
     "cmf_q8_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
+    "cmf_matmat_a8w8": (_I, [_P, _P, _I, _P]),
     "cmf_q4t_matvec": (_I, [_P, _P, _I, _I, _P]),
     "cmf_q4t_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
     "cmf_q4tp_matvec": (_I, [_P, _P, _I, _I, _P]),
@@ -245,6 +246,16 @@ def matmul(w, xs):
     fn = {DT_Q8ROW: q8_matmat, DT_Q4T: q4t_matmat, DT_Q4TP: q4tp_matmat}[w.dtype]
     if not fn(w, xs, b, w.rows, w.cols, out):
         raise CmfError("declined")
+    return out
+
+
+def matmul_a8w8(w, xs):
+    """w * xs under the a8w8 contract (split_act operand, integer tile dots,
+    exact outliers): xs [b][cols] (any b), returns [b][rows]."""
+    xs = np.ascontiguousarray(np.atleast_2d(xs), dtype=np.float32)
+    b = xs.shape[0]
+    out = np.empty((b, w.rows), dtype=np.float32)
+    check(lib().cmf_matmat_a8w8(w.h, _ptr(xs), b, _ptr(out)))
     return out
 
 

@@ -45,6 +45,15 @@ struct GemvDesc {
     const float2* rowp;
 };
 
+// split_act outliers of the a8w8 operand: cnt[b] of them for batch row b at
+// idx/val[b * cap ..] (index order).
+struct A8Out {
+    int* cnt;
+    int* idx;
+    float* val;
+    int cap;
+};
+
 struct GemvArgs {
     const void* w;
     const void* scale;
@@ -108,6 +117,14 @@ int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const in
                             size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st);
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
                 hipStream_t st);
+// The a8w8 operand (split_act) of m rows of x: planes / xs as launch_prep,
+// plus the outlier lists in o (cap >= w.cols).
+int launch_prep_a8(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs, const A8Out& o,
+                   hipStream_t st);
+// y = W x under the a8w8 contract from launch_prep_a8's operand (the GEMV,
+// then the outlier terms).
+int gemv_a8(const DevWeight& w, const uint8_t* planes, const float* xs, const A8Out& o, float* y, int ldy, int m,
+            hipStream_t st);
 // y[b*ldy + (r - row_lo)] for rows [row_lo, row_hi) and b < m.
 int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
                 int m, int row_lo, int row_hi, hipStream_t st, int ks_override = 0);

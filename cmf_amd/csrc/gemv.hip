@@ -107,6 +107,139 @@ __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk
     else prep16_row(vals, K, am, nk, b, ms, planes, xs, tid, nt, mstride ? mstride : 16);
 }
 
+// The a8w8 operand (split_act, qtensor.rs:9237-9281) of row b of x: rms =
+// sqrt(sum(x*x) / n) (f32 products, f64 sum), outliers |x| > 8 rms listed
+// exactly in index order (idx/val, count), sx = max|x| of the rest / 127
+// (1 if 0), xq = clamp(round half away(x / sx), +-127) and 0 at outliers.
+// xq (small integers) is written as the prepared planes: q8 plane 0 = xq,
+// planes 1, 2 = 0; q4 hi = xq * 2^8 exactly, lo = 0.  xs[b] = sx (q8) or
+// sx * 2^-8 (q4), so the GEMVs' integer tile dots and scales reproduce the
+// contract; the outliers are added in their epilogue.  grid (m), 512.
+__global__ __launch_bounds__(512) void k_prep_a8(const float* __restrict__ x, int ldx, int K, int fmt, int nk,
+                                                 uint8_t* __restrict__ planes, float* __restrict__ xs,
+                                                 int* __restrict__ ocnt, int* __restrict__ oidx,
+                                                 float* __restrict__ oval, int ocap) {
+    extern __shared__ float vals[];  // K
+    __shared__ double red[8];
+    __shared__ float redm[8];
+    __shared__ int wcnt[8], cnt_thr[512];
+    const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
+    const int nw = nt >> 6;
+    const float* row = x + (size_t)b * ldx;
+    double ss = 0.0;
+    for (int i = tid; i < K; i += nt) {
+        const float v = row[i];
+        vals[i] = v;
+        ss += (double)(v * v);
+    }
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    double t = 0.0;
+    for (int q = 0; q < nw; q++) t += red[q];
+    const float thr = 8.0f * (float)sqrt(t / (double)(K > 1 ? K : 1));
+    // thread tid owns the contiguous columns [c0, c1): outliers keep index order
+    const int per = (K + nt - 1) / nt, c0 = min(K, tid * per), c1 = min(K, c0 + per);
+    int n_out = 0;
+    float am = 0.f;
+    for (int i = c0; i < c1; i++) {
+        const float a = fabsf(vals[i]);
+        if (a > thr) n_out++;
+        else am = fmaxf(am, a);
+    }
+    cnt_thr[tid] = n_out;
+    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
+    if (lane == 0) redm[wave] = am;
+    __syncthreads();
+    if (tid == 0) {  // exclusive scan of the per-thread counts
+        int acc = 0;
+        for (int q = 0; q < nt; q++) {
+            const int c = cnt_thr[q];
+            cnt_thr[q] = acc;
+            acc += c;
+        }
+        ocnt[b] = acc;
+        wcnt[0] = acc;
+    }
+    __syncthreads();
+    am = 0.f;
+    for (int q = 0; q < nw; q++) am = fmaxf(am, redm[q]);
+    const float sx = am > 0.f ? am / 127.0f : 1.0f;
+    const float inv = 1.0f / sx;
+    const bool any = wcnt[0] > 0;
+    int o = cnt_thr[tid];
+    for (int i = c0; i < c1; i++) {
+        const float v = vals[i];
+        float q;
+        if (any && fabsf(v) > thr) {
+            oidx[(size_t)b * ocap + o] = i;
+            oval[(size_t)b * ocap + o] = v;
+            o++;
+            q = 0.f;
+        } else {
+            q = fminf(127.f, fmaxf(-127.f, roundf(v * inv)));
+        }
+        vals[i] = q;
+    }
+    __syncthreads();
+    if (fmt == DT_Q8ROW) prep8_row(vals, K, 127.0f, nk, b, gridDim.x, planes, xs, tid, nt);
+    else prep16_row(vals, K, 127.0f, nk, b, gridDim.x, planes, xs, tid, nt);
+    __syncthreads();
+    if (tid == 0) xs[b] = fmt == DT_Q8ROW ? sx : ldexpf(sx, -8);
+}
+
+// The split_act outlier terms of the a8w8 contract, after the GEMV (grid
+// (rows / 256, m)): q4t / q4tp y += ((nib - 8) * tile scale) * x per outlier
+// in index order, as q4t_outlier / q4tp_outlier add them after the tile sum
+// (qtensor.rs:4405-4413, 4666-4671); q8 y += (sum of w * x) * row scale (the
+// reference adds w * x before its row-scale multiply, qtensor.rs:9094-9101:
+// one rounding apart).  The weight is read from the device layout (row block
+// row / 16, lane 16 s + row % 16).
+__global__ __launch_bounds__(256) void k_a8_outliers(const void* __restrict__ wv, const void* __restrict__ scale,
+                                                     const float2* __restrict__ rowp, int fmt, int rows, int nk,
+                                                     A8Out o, float* __restrict__ y, int ldy) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x, b = blockIdx.y;
+    if (row >= rows) return;
+    const int n = o.cnt[b];
+    if (n == 0) return;
+    const int rb = row >> 4, r = row & 15;
+    float* yp = y + (size_t)b * ldy + row;
+    if (fmt == DT_Q8ROW) {
+        const int8_t* wq = (const int8_t*)wv;
+        float acc = 0.f;
+        for (int i = 0; i < n; i++) {
+            const int j = o.idx[(size_t)b * o.cap + i];
+            const int c = j >> 6, sl = (j >> 4) & 3, jj = j & 15;
+            acc += (float)wq[(((size_t)rb * nk + c) * 64 + 16 * sl + r) * 16 + jj] * o.val[(size_t)b * o.cap + i];
+        }
+        *yp += acc * ((const float*)scale)[row];
+        return;
+    }
+    const uint8_t* wb = (const uint8_t*)wv;
+    float acc = *yp;
+    for (int i = 0; i < n; i++) {
+        const int j = o.idx[(size_t)b * o.cap + i];
+        const int g = j >> 7, t = (j >> 5) & 3, sl = (j >> 3) & 3, q = j & 7;  // column 128 g + 32 t + 8 sl + q
+        const size_t step = (size_t)rb * nk + g;
+        const uint8_t by = wb[(step * 64 + 16 * sl + r) * 16 + 4 * t + (q >> 1)];
+        const int nib = (by >> (4 * (q & 1))) & 15;
+        float sc;
+        if (fmt == DT_Q4T) {
+            const uint16_t h = ((const uint16_t*)scale)[(step * 16 + r) * 4 + t];
+            sc = (float)__builtin_bit_cast(_Float16, h);
+        } else {
+            const uint32_t cw = ((const uint32_t*)scale)[step * 16 + r];
+            const int code = (cw >> (5 * t)) & 31;
+            const float2 pr = rowp[row];
+            float tv = pr.x;  // the ladder t[c] = t[c-1] * ratio
+            for (int c = 1; c <= code; c++) tv = tv * pr.y;
+            sc = tv;
+        }
+        acc += ((float)(nib - 8) * sc) * o.val[(size_t)b * o.cap + i];
+    }
+    *yp = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------
@@ -152,6 +285,15 @@ size_t prep_bytes(const DevWeight& w) {
     // at most 16 batch rows: q8 3 planes of nk*64*16 B ; q4 2 planes of ntiles*64*16 B
     // (+ q4 tile biases [tile][16] f32)
     return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 1024 * 3 : (size_t)w.kchunks * 4 * (1024 * 2 + 64);
+}
+
+int launch_prep_a8(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs, const A8Out& o,
+                   hipStream_t st) {
+    if (m < 1 || m > MAXB || o.cap < w.cols) return fail("prep_a8: batch 1..16 and an outlier capacity of cols");
+    const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
+    hipLaunchKernelGGL(k_prep_a8, dim3(m), dim3(512), (size_t)w.cols * sizeof(float), st, x, ldx, w.cols, w.dtype,
+                       nk, planes, xs, o.cnt, o.idx, o.val, o.cap);
+    return CMF_OK;
 }
 
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
@@ -373,6 +515,20 @@ int gemv_grouped(const DevWeight& proto, const GemvDesc* desc, const int* jobs, 
     return launch_args(proto, a, 0, 0, max_jobs, st);
 }
 
+
+int gemv_a8(const DevWeight& w, const uint8_t* planes, const float* xs, const A8Out& o, float* y, int ldy, int m,
+            hipStream_t st) {
+    if (m < 1 || m > MAXB) return fail("gemv: batch must be 1..16");
+    XSrc src{};
+    src.mode = XS_GLOBAL;
+    src.planes = planes;
+    src.xs = xs;
+    GemvArgs a = base_args(w, src, y, ldy, m, 0, w.rows, false);
+    if (launch_args(w, a, 0, 0, 1, st) != CMF_OK) return CMF_ERR;
+    hipLaunchKernelGGL(k_a8_outliers, dim3((w.rows + 255) / 256, m), dim3(256), 0, st, w.w, w.scale, w.rowp,
+                       w.dtype, w.rows, w.kchunks, o, y, ldy);
+    return CMF_OK;
+}
 
 int launch_gemv(const DevWeight& w, const uint8_t* planes, const float* xs, float* y, int ldy,
                 int m, int row_lo, int row_hi, hipStream_t st, int ks_override) {

@@ -200,6 +200,10 @@ struct SeamScratch {
     size_t x_cap = 0;
     float* y = nullptr;
     size_t y_cap = 0;
+    int* a8cnt = nullptr;  // split_act outliers of the a8w8 ops: [MAXB], [MAXB][cols]
+    int* a8idx = nullptr;
+    float* a8val = nullptr;
+    size_t a8_cap = 0;
 };
 static SeamScratch g_ss;
 
@@ -365,12 +369,53 @@ int cmf_weight_free(cmf_weight w) {
 
 size_t cmf_weight_device_bytes(cmf_weight w) { return w ? w->w.bytes : 0; }
 
+// y[b][rows] = W x[b] under the a8w8 contract (split_act operand, integer
+// tile dots, outliers exact), batches of 16.
+static int seam_matmat_a8(const DevWeight& w, const float* xs, int b, float* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    const int rows = w.rows, cols = w.cols;
+    if (grow((void**)&g_ss.planes, &g_ss.planes_cap, prep_bytes(w)) != CMF_OK) return CMF_ERR;
+    if (!g_ss.xs) CMF_HIP(hipMalloc(&g_ss.xs, 64 * sizeof(float)));
+    if (grow((void**)&g_ss.x, &g_ss.x_cap, (size_t)MAXB * cols * sizeof(float)) != CMF_OK) return CMF_ERR;
+    if (grow((void**)&g_ss.y, &g_ss.y_cap, (size_t)MAXB * rows * sizeof(float)) != CMF_OK) return CMF_ERR;
+    if (!g_ss.a8cnt) CMF_HIP(hipMalloc(&g_ss.a8cnt, MAXB * sizeof(int)));
+    if ((size_t)cols > g_ss.a8_cap) {
+        if (g_ss.a8idx) (void)hipFree(g_ss.a8idx);
+        if (g_ss.a8val) (void)hipFree(g_ss.a8val);
+        g_ss.a8idx = nullptr;
+        g_ss.a8val = nullptr;
+        g_ss.a8_cap = 0;
+        CMF_HIP(hipMalloc(&g_ss.a8idx, (size_t)MAXB * cols * sizeof(int)));
+        CMF_HIP(hipMalloc(&g_ss.a8val, (size_t)MAXB * cols * sizeof(float)));
+        g_ss.a8_cap = cols;
+    }
+    const A8Out o{g_ss.a8cnt, g_ss.a8idx, g_ss.a8val, (int)g_ss.a8_cap};
+    hipStream_t st = stream();
+    for (int b0 = 0; b0 < b; b0 += MAXB) {
+        const int m = std::min(MAXB, b - b0);
+        CMF_HIP(hipMemcpyAsync(g_ss.x, xs + (size_t)b0 * cols, (size_t)m * cols * sizeof(float), hipMemcpyHostToDevice,
+                               st));
+        if (launch_prep_a8(w, g_ss.x, cols, m, g_ss.planes, g_ss.xs, o, st) != CMF_OK) return CMF_ERR;
+        if (gemv_a8(w, g_ss.planes, g_ss.xs, o, g_ss.y, rows, m, st) != CMF_OK) return CMF_ERR;
+        CMF_HIP(hipMemcpyAsync(out + (size_t)b0 * rows, g_ss.y, (size_t)m * rows * sizeof(float),
+                               hipMemcpyDeviceToHost, st));
+    }
+    CMF_HIP(hipStreamSynchronize(st));
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
 static int seam(cmf_weight w, int dt, int row0, const float* xs, int b, int rows, int cols,
                 float* out) {
     if (!w || !xs || !out) return fail("null argument");
     if (w->w.dtype != dt) return CMF_DECLINED;  // not this codec: caller's CPU path
     if (cols != w->w.cols) return fail("cols mismatch");
     return seam_matmat(w->w, row0, xs, b, rows, out);
+}
+
+int cmf_matmat_a8w8(cmf_weight w, const float* xs, int b, float* out) {
+    if (!w || !xs || !out || b < 1) return fail("null argument or empty batch");
+    return seam_matmat_a8(w->w, xs, b, out);
 }
 
 int cmf_q8_matvec_range(cmf_weight w, int row0, const float* xs, int rows, int cols, float* out) {

@@ -66,6 +66,12 @@ int cmf_q4t_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, flo
 /* gpu.rs:2400 / 2358 */
 int cmf_q4tp_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out);
 int cmf_q4tp_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out);
+/* The a8w8 contract of qmatvec / q4t_matvec / q4tp_matvec / their matmats
+ * on x86 with VNNI (qtensor.rs:9980-10047, 5683-5717, 4674-4716): each row
+ * of xs goes through split_act (qtensor.rs:9237-9281; per-vector int8 scale,
+ * |x| > 8 rms kept exactly), integer tile dots, then the outliers; out
+ * [b][rows] for any q8 / q4t / q4tp weight, batches of 16 per launch. */
+int cmf_matmat_a8w8(cmf_weight w, const float* xs, int b, float* out);
 /* gpu.rs:1773 / 1794 q4t_ffn / q4tp_ffn: out = w2 * (silu(w1 x) * (w3 x)),
  * xs [b][hidden], out [b][hidden]. */
 int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b, int hidden,
