@@ -68,6 +68,20 @@ class GenStats(C.Structure):
                 ("device_ms", C.c_double)]
 
 
+class FileSections(C.Structure):
+    """cmf_file_sections: the envelope of an open .cmf file."""
+    _fields_ = [("required_features", C.c_uint32), ("off", C.c_uint64 * 6), ("len", C.c_uint64 * 6),
+                ("header_hash", C.c_uint64), ("dir_hash", C.c_uint64), ("base", C.c_void_p),
+                ("file_len", C.c_uint64)]
+
+
+class FileTensor(C.Structure):
+    """cmf_file_tensor: one tensor directory record."""
+    _fields_ = [("name", C.c_void_p), ("name_len", C.c_int), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_uint64 * 6), ("off", C.c_uint64), ("nbytes", C.c_uint64), ("hash", C.c_uint64),
+                ("shard", C.c_int), ("data", C.c_void_p)]
+
+
 # every symbol include/cmf_hip.h declares, with its ctypes signature
 _P, _I, _F, _S, _U64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_uint64
 SIGNATURES = {
@@ -120,6 +134,17 @@ SIGNATURES = {
     "cmf_kv_truncate": (_I, [_P, _I]),
     "cmf_state_get": (_I, [_P, C.POINTER(_I), _P]),
     "cmf_kv_export": (_I, [_P, _I, _I, _P, _P]),
+    "cmf_model_set_embed": (_I, [_P, C.POINTER(Tensor)]),
+    # .cmf container (csrc/container.cpp)
+    "cmf_hash64": (_U64, [_P, _S]),
+    "cmf_file_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "cmf_file_close": (_I, [_P]),
+    "cmf_file_info": (_I, [_P, C.POINTER(FileSections)]),
+    "cmf_file_count": (_I, [_P]),
+    "cmf_file_entry": (_I, [_P, _I, C.POINTER(FileTensor)]),
+    "cmf_file_find": (_I, [_P, C.c_char_p, _S]),
+    "cmf_file_attach_shard": (_I, [_P, _P]),
+    "cmf_file_verify": (_I, [_P, _P, C.c_char_p, _S, C.POINTER(_I)]),
     # host-only synthetic data generators (csrc/synth.cpp)
     "cmf_synth_normal": (None, [_U64, C.c_int64, _F, _P]),
     "cmf_synth_q8_uniform": (None, [_U64, _I, _I, _P, _P]),

@@ -37,6 +37,7 @@ struct cmf_model_s {
     std::vector<LayerDev> L;
     bool has_head = false, has_mtp = false;
     DevWeight lm;
+    DevWeight emb;  // untied embedding table (q8); empty: lm doubles as the table
     float* final_norm = nullptr;
     float *enorm = nullptr, *hnorm = nullptr, *mtp_norm = nullptr;
     DevWeight eh;
@@ -198,7 +199,8 @@ void free_layer(LayerDev& l) {
 }
 
 EmbedSrc embed_src(cmf_model_s* m) {
-    return EmbedSrc{(const int8_t*)m->lm.w, (const float*)m->lm.scale, m->lm.rows, m->lm.kchunks};
+    const DevWeight& e = m->emb.w ? m->emb : m->lm;
+    return EmbedSrc{(const int8_t*)e.w, (const float*)e.scale, e.rows, e.kchunks};
 }
 
 XSrc src_norm(const float* x, int ldx, const float* w, double eps) {
@@ -506,6 +508,7 @@ int cmf_model_free(cmf_model m) {
     for (auto& l : m->L) free_layer(l);
     free_layer(m->mtp);
     free_weight(m->lm);
+    free_weight(m->emb);
     free_weight(m->eh);
     for (void* p : m->allocs) (void)hipFree(p);
     delete m;
@@ -531,6 +534,15 @@ int cmf_model_set_head(cmf_model m, const cmf_tensor* lm, const float* final_nor
     if (ensure_logits(m)) return CMF_ERR;
     m->has_head = true;
     return CMF_OK;
+}
+
+int cmf_model_set_embed(cmf_model m, const cmf_tensor* e) {
+    if (m) drop_graph(m);
+    if (!m || !e) return fail("set_embed: null argument");
+    if (e->dtype != DT_Q8ROW) return fail("set_embed: the embedding table must be q8");
+    if (check_tensor(*e, m->c.vocab, m->c.hidden, "embed_tokens")) return CMF_ERR;
+    free_weight(m->emb);
+    return build_cat(m->emb, {e});
 }
 
 int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh,

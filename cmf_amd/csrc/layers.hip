@@ -143,7 +143,7 @@ __device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[
 // chunk at p0, one wave per row: appended to the cache and, when Kn is given,
 // kept in LDS (Kn[b], V[pos - p0]) for the chunk's own attention.
 __device__ __forceinline__ void append_rows(const AttnArgs& a, int g, int p0, int pos0, int wave, int lane,
-                                            float (*Kn)[128], float (*V)[128 + 4]) {
+                                            float (*Kn)[128 + 4], float (*V)[128 + 4]) {
     constexpr int HD = 128, C = ATT_C;
     const int b_lo = max(0, p0 - pos0), b_hi = min(a.nb, p0 + C - pos0);
     const int nw = blockDim.x >> 6;
@@ -245,10 +245,10 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const int stored = pos0 + a.nb;
     const int p0 = c * C;
     constexpr int QR = 4 * NQW < 16 ? 16 : 4 * NQW;  // Q rows: whole MFMA query blocks
-    __shared__ __align__(16) float Q[QR][HD];
+    __shared__ __align__(16) float Q[QR][HD + 4];  // rows padded: the MFMA A reads take 16 rows at once
     __shared__ __align__(16) float V[C][HD + 4];
     __shared__ __align__(16) float S[4 * NQW][C];
-    __shared__ __align__(16) float Kn[MAXB][HD];
+    __shared__ __align__(16) float Kn[MAXB][HD + 4];
     if (!a.attend) {  // KV append only (MTP warm-up)
         if (p0 < stored) append_rows(a, g, p0, pos0, wave, lane, nullptr, nullptr);
         return;

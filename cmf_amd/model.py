@@ -51,12 +51,21 @@ class Model:
         keep = []
         check(lib().cmf_model_set_head(self.h, C.byref(_tensor(sm["lm_head"], keep)),
                                        _f32(sm["final_norm"], keep)))
+        if "embed" in sm:  # untied embedding table
+            keep = []
+            check(lib().cmf_model_set_embed(self.h, C.byref(_tensor(sm["embed"], keep))))
         self.has_mtp = "mtp" in sm
         if self.has_mtp:
             mt, keep = sm["mtp"], []
             check(lib().cmf_model_set_mtp(self.h, _f32(mt["enorm"], keep), _f32(mt["hnorm"], keep),
                                           C.byref(_tensor(mt["eh_proj"], keep)),
                                           C.byref(_layer(mt["layer"], keep)), _f32(mt["norm"], keep)))
+
+    @classmethod
+    def from_cmf(cls, path, max_seq=None):
+        """A model loaded from a .cmf file (or shard 1 of a sharded one)."""
+        from .loader import load
+        return cls(load(path, max_seq=max_seq))
 
     def prefill(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

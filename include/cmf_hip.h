@@ -233,6 +233,82 @@ int cmf_kv_export(cmf_model m, int li, int n, float* k, float* v);
  * a measurement helper. */
 int cmf_time_attention(cmf_model m, int nb, int pos0, int merge, int iters, float* avg_ms);
 
+
+/* ---- .cmf v2 container (cortiq-core/src/format.rs) ------------------- */
+/* Error kinds of the container calls (CmfError, format.rs; the message of
+ * cmf_last_error() carries the details). */
+#define CMF_E_NOTFOUND (-2) /* FileNotFound */
+#define CMF_E_MAGIC (-3)    /* InvalidMagic */
+#define CMF_E_VERSION (-4)  /* UnsupportedVersion */
+#define CMF_E_FEATURE (-5)  /* UnsupportedFeature */
+#define CMF_E_BOUNDS (-6)   /* Bounds */
+#define CMF_E_PARSE (-7)    /* Parse */
+#define CMF_E_DTYPE (-8)    /* UnknownDtype */
+#define CMF_E_IO (-9)       /* Io */
+#define CMF_E_MISSING (-10) /* MissingTensor */
+
+typedef struct CmfFileS* cmf_file;
+
+/* Envelope of an open file: sections header, dir, data, masks, vocab,
+ * index (offset, length; length 0 = absent), the stored header / directory
+ * hashes (0 = absent) and the mapping's base address and length. */
+typedef struct {
+    uint32_t required_features;
+    uint64_t off[6], len[6];
+    uint64_t header_hash, dir_hash;
+    const uint8_t* base;
+    uint64_t file_len;
+} cmf_file_sections;
+
+/* One tensor directory record (TensorEntry, format.rs:255-269).  name is
+ * not NUL-terminated; data points into the read-only mapping of the owning
+ * shard (entry_bytes, format.rs:924-933) and lives until cmf_file_close. */
+typedef struct {
+    const char* name;
+    int name_len;
+    int dtype;
+    int ndim;
+    uint64_t shape[6];
+    uint64_t off, nbytes, hash;
+    int shard;
+    const uint8_t* data;
+} cmf_file_tensor;
+
+/* hash64 (cortiq-core/src/hash.rs:18-35): murmur3 fmix64 over 64-bit LE
+ * words with positional salt, XOR fold, length mix. */
+uint64_t cmf_hash64(const void* data, size_t n);
+/* CmfModel::open (format.rs:390-584): maps the file read-only and validates
+ * the envelope (magic, version 2, required feature bits, section bounds,
+ * 4096-aligned data), the header's JSON syntax, the directory (56-byte
+ * records, name pool, UTF-8 names, known dtype ids, ndim <= 6) and every
+ * tensor (64-aligned offset, inside the data section, shape product,
+ * expected_nbytes of fixed-size dtypes, no duplicate names).  The header's
+ * fields are read by the caller from the header section. */
+int cmf_file_open(const char* path, cmf_file* out);
+int cmf_file_close(cmf_file f);
+int cmf_file_info(cmf_file f, cmf_file_sections* s);
+int cmf_file_count(cmf_file f);
+int cmf_file_entry(cmf_file f, int i, cmf_file_tensor* e);
+/* tensor_index (format.rs:809-821): directory index of a tensor by name, or
+ * CMF_E_MISSING. */
+int cmf_file_find(cmf_file f, const char* name, size_t name_len);
+/* The directory-merge step of open_sharded (format.rs:589-650): appends the
+ * tensors of an opened sibling shard to f (entry.shard = 1, 2, ... in call
+ * order) and takes over its mapping; shard is consumed on success.  A name
+ * already present is CMF_E_PARSE and leaves both files unchanged.  The
+ * caller checks the shard coordinates of the sibling's header. */
+int cmf_file_attach_shard(cmf_file f, cmf_file shard);
+/* verify (format.rs:1063-1110): the envelope's header and directory hashes,
+ * the optional sections' hashes stored[0..2] = masks, vocab, index (0 or a
+ * NULL array: not checked; they are read from the header's section_hashes
+ * by the caller) and every tensor's hash.  *nproblems = count; the messages,
+ * one per line, go to buf (truncated to cap). */
+int cmf_file_verify(cmf_file f, const uint64_t* stored, char* buf, size_t cap, int* nproblems);
+/* A model whose embedding table is not tied to lm_head (loader.rs:714-724):
+ * q8 [vocab][hidden], read row by row by the embedding lookups.  Without
+ * this call the lm_head doubles as the embedding table. */
+int cmf_model_set_embed(cmf_model m, const cmf_tensor* embed);
+
 #ifdef __cplusplus
 }
 #endif

@@ -76,14 +76,16 @@ static float dot_f32(const float* a, const float* b, int n) {
 }
 
 void or_embed(const or_model* m, uint32_t id, float* out) {
-    /* pipeline.rs:5568-5575: row_f32 of the (tied, q8) embedding table */
+    /* pipeline.rs:5568-5575: row_f32 of the q8 embedding table (the tied
+     * lm_head unless the model carries its own) */
     int H = m->cfg.hidden;
-    if ((int)id >= m->lm_head.rows) {
+    const or_qt* e = m->embed.q ? &m->embed : &m->lm_head;
+    if ((int)id >= e->rows) {
         memset(out, 0, sizeof(float) * (size_t)H);
         return;
     }
-    const int8_t* q = m->lm_head.q + (size_t)id * H;
-    float rs = m->lm_head.row_scale[id];
+    const int8_t* q = e->q + (size_t)id * H;
+    float rs = e->row_scale[id];
     for (int i = 0; i < H; i++) out[i] = (float)q[i] * rs;
 }
 

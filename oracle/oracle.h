@@ -136,6 +136,7 @@ typedef struct {
     or_qt eh_proj;          /* [hidden, 2*hidden] */
     or_layer mtp;
     int threads;
+    or_qt embed;            /* untied q8 embedding table (loader.rs:714-724); q == NULL: lm_head */
 } or_model;
 
 /* KV: per layer k[n_kv][max_seq][head_dim], same for v; len = stored rows.

@@ -40,7 +40,7 @@ class Layer(C.Structure):
 class Model(C.Structure):
     _fields_ = [("cfg", Cfg), ("layers", C.c_void_p), ("lm_head", QT), ("final_norm", C.c_void_p),
                 ("has_mtp", C.c_int), ("enorm", C.c_void_p), ("hnorm", C.c_void_p), ("mtp_norm", C.c_void_p),
-                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int)]
+                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int), ("embed", QT)]
 
 
 class KV(C.Structure):
@@ -173,6 +173,8 @@ class OracleModel:
                     c["max_seq"], c["rope_theta"], c["eps"])
         m.layers = C.cast(layers, C.c_void_p)
         m.lm_head = qt(sm["lm_head"], self.keep)
+        if "embed" in sm:  # untied embedding table
+            m.embed = qt(sm["embed"], self.keep)
         m.final_norm = _f32(sm["final_norm"], self.keep)
         m.threads = threads
         if "mtp" in sm:

@@ -38,7 +38,7 @@ def _np_forward(sm, toks):
     """f64 forward of every position; returns the final hidden rows (before the final norm)"""
     c = sm["cfg"]
     H, nh, nkv, hd, eps = c["hidden"], c["n_heads"], c["n_kv"], c["head_dim"], c["eps"]
-    E = _dq(sm["lm_head"])
+    E = _dq(sm.get("embed", sm["lm_head"]))
     hs = np.stack([E[t] for t in toks])
     for l in sm["layers"]:
         Wq, Wk, Wv, Wo = _dq(l["wq"]), _dq(l["wk"]), _dq(l["wv"]), _dq(l["wo"])
@@ -78,6 +78,23 @@ def test_forward_matches_f64_numpy(tiny):
     lg = o.logits(got[-1])
     E = _dq(tiny["lm_head"])
     ref_lg = E @ _rms(ref[-1], tiny["final_norm"], TINY["eps"])
+    assert np.linalg.norm(lg - ref_lg) / np.linalg.norm(ref_lg) < 1e-5
+
+
+def test_untied_embedding_matches_f64_numpy(tiny):
+    """an embedding table of its own (loader.rs:714-724): rows come from it,
+    logits from lm_head"""
+    from cmf_amd import synth
+    sm = dict(tiny, embed=synth.q8_normal(91, TINY["vocab"], TINY["hidden"], 0.05))
+    toks = synth.ids(5, 4, TINY["vocab"])
+    o = orc.OracleModel(sm, threads=2)
+    got = np.stack([o.forward(int(t), i) for i, t in enumerate(toks)])
+    ref = _np_forward(sm, toks)
+    assert (np.linalg.norm(got - ref, axis=1) / np.linalg.norm(ref, axis=1)).max() < 1e-5
+    tied = np.stack([orc.OracleModel(tiny, threads=2).forward(int(toks[0]), 0)])
+    assert np.linalg.norm(tied[0] - got[0]) > 1e-3 * np.linalg.norm(got[0])  # the table matters
+    lg = o.logits(got[-1])
+    ref_lg = _dq(tiny["lm_head"]) @ _rms(ref[-1], tiny["final_norm"], TINY["eps"])
     assert np.linalg.norm(lg - ref_lg) / np.linalg.norm(ref_lg) < 1e-5
 
 
