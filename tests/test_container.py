@@ -399,3 +399,34 @@ def test_loader_refuses_what_the_engine_cannot_run(tmp_path):
     W.write(p, W.header_of(W.arch_of(TINY, mtp=False, tie=False)), t)
     with pytest.raises(CmfError, match="lm_head"):
         loader.load(str(p))
+
+
+def test_corrupted_files_fail_cleanly(tmp_path):
+    """Random byte damage (biased to the envelope and directory) either opens
+    or raises a CmfFileError; an opened file's views and verify() stay usable."""
+    K = _mod()
+    p = tmp_path / "seed.cmf"
+    _write_tiny(p)
+    seed = open(p, "rb").read()
+    rng = np.random.default_rng(11)
+    q = tmp_path / "fz.cmf"
+    opened = 0
+    for it in range(400):
+        b = bytearray(seed)
+        for _ in range(int(rng.integers(1, 8))):
+            lim = [128, 2176, len(b)][int(rng.integers(0, 3))]
+            pos = int(rng.integers(0, min(lim, len(b))))
+            b[pos] = int(rng.integers(0, 256))
+        if rng.integers(0, 10) == 0:
+            b = b[: int(rng.integers(0, len(b) + 1))]
+        q.write_bytes(bytes(b))
+        try:
+            f = K.CmfFile.open(q)
+        except K.CmfFileError:
+            continue
+        opened += 1
+        for e in f.tensors:
+            assert len(f.entry_bytes(e)) == e.nbytes
+        assert isinstance(f.verify(), list)
+        f.close()
+    assert opened > 0
