@@ -428,44 +428,62 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x
             bi = i;
         }
     }
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o) {
-            const float v2 = sv[threadIdx.x + o];
-            const int i2 = si[threadIdx.x + o];
-            if (v2 > sv[threadIdx.x] || (v2 == sv[threadIdx.x] && i2 > si[threadIdx.x])) {
-                sv[threadIdx.x] = v2;
-                si[threadIdx.x] = i2;
-            }
+    // the same lexicographic (value, index) maximum: butterfly in each wave,
+    // then the four waves' winners
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(bv, o);
+        const int i2 = __shfl_xor(bi, o);
+        if (v2 > bv || (v2 == bv && i2 > bi)) {
+            bv = v2;
+            bi = i2;
         }
-        __syncthreads();
     }
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        sv[w] = bv;
+        si[w] = bi;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        pv[(size_t)r * gridDim.x + s] = sv[0];
-        pi[(size_t)r * gridDim.x + s] = si[0];
+        for (int q = 1; q < 4; q++)
+            if (sv[q] > bv || (sv[q] == bv && si[q] > bi)) {
+                bv = sv[q];
+                bi = si[q];
+            }
+        pv[(size_t)r * gridDim.x + s] = bv;
+        pi[(size_t)r * gridDim.x + s] = bi;
     }
 }
 
-// Pass 2: one thread per row.
-__global__ void k_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi, int ns,
-                               int nrows, int* __restrict__ out) {
-    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+// Pass 2: one wave per row.  The winner is the lexicographic maximum of
+// (value, index) over the partials and the start (-inf, 0), the order the
+// sequential scan of argmax (sampler.rs:1130-1154) keeps: a larger value wins,
+// an equal value with a higher index wins, NaN never wins.  A maximum is
+// order-free, so the lanes' strided scans and the butterfly give the same
+// index as one scan over all partials.
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i > bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+__global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                     int ns, int nrows, int* __restrict__ out) {
+    const int r = blockIdx.x, lane = threadIdx.x;
     if (r >= nrows) return;
     float bv = -INFINITY;
     int bi = 0;
-    for (int s = 0; s < ns; s++) {
-        const float v = pv[(size_t)r * ns + s];
-        const int i = pi[(size_t)r * ns + s];
-        if (v > bv || (v == bv && i > bi)) {
-            bv = v;
-            bi = i;
-        }
+    for (int s = lane; s < ns; s += 64) argmax_take(bv, bi, pv[(size_t)r * ns + s], pi[(size_t)r * ns + s]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(bv, o);
+        const int i2 = __shfl_xor(bi, o);
+        argmax_take(bv, bi, v2, i2);
     }
-    out[r] = bi;
+    if (lane == 0) out[r] = bi;
 }
 
 // ---------------------------------------------------------------------------
@@ -500,7 +518,7 @@ void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi,
                    hipStream_t st) {
     const int slice = 4096, ns = (n + slice - 1) / slice;
     hipLaunchKernelGGL(k_argmax_part, dim3(ns, nrows), dim3(256), 0, st, x, ld, n, slice, pv, pi);
-    hipLaunchKernelGGL(k_argmax_final, dim3((nrows + 63) / 64), dim3(64), 0, st, pv, pi, ns, nrows,
+    hipLaunchKernelGGL(k_argmax_final, dim3(nrows), dim3(64), 0, st, pv, pi, ns, nrows,
                        out);
 }
 
