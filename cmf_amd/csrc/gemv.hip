@@ -314,13 +314,22 @@ static size_t lds_bytes(const DevWeight& w, int m) {
 // path does not apply (other producers, the f16 operand of m > 8 rows,
 // unaligned rows, more than the LDS budget).
 size_t fused_lds_bytes(const DevWeight& w, const XSrc& src, int m) {
-    if (src.mode != XS_NORM && src.mode != XS_ROWS) return 0;
+    if (src.mode != XS_NORM && src.mode != XS_ROWS && src.mode != XS_CAT) return 0;
     if (w.dtype != DT_Q8ROW && m > 8) return 0;
     const int K = src.K ? src.K : w.cols;
     if (K != w.cols || K % 4 || src.ldx % 4 || (uintptr_t)src.x % 16) return 0;
     if (src.mode == XS_NORM && (!src.w || (uintptr_t)src.w % 16)) return 0;
     const size_t planes = (lds_bytes(w, m) + 1023) & ~(size_t)1023;
-    const size_t raw = ((size_t)(m + (src.mode == XS_NORM ? 1 : 0)) * K * 4 + 1023) & ~(size_t)1023;
+    size_t raw = ((size_t)(m + (src.mode == XS_NORM ? 1 : 0)) * K * 4 + 1023) & ~(size_t)1023;
+    if (src.mode == XS_CAT) {
+        const int H = src.H;
+        if (2 * H != K || H % 256 || !src.toks || !src.emb.w || !src.emb.rs || !src.w || !src.w2 ||
+            (uintptr_t)src.w % 16 || (uintptr_t)src.w2 % 16)
+            return 0;
+        // rows x, w, w2 (f32), the int8 embedding rows (1 KiB each), their scales
+        const size_t eh = ((size_t)H + 1023) & ~(size_t)1023;
+        raw += ((size_t)(m + 2) * H * 4 + (size_t)m * eh + 4 * (size_t)m + 1023) & ~(size_t)1023;
+    }
     return planes + raw <= (size_t)LDSX_MAX ? planes + raw : 0;
 }
 

@@ -107,7 +107,56 @@ __device__ __forceinline__ void x_dma(const XSrc& s, int n, uint8_t* lx) {
 // evaluates the producer in every workgroup while its weights are in flight.
 // raw[] sits after the planes at a 1 KiB boundary and its allocation is
 // rounded up to 1 KiB, so the clamped tail of the last wave load stays in it.
+// XS_CAT (the MTP operand [rms_norm(embed(tok)) * w ; rms_norm(x) * w2], H
+// columns each, pipeline.rs:3085-3094): after the m output rows raw[m][K]
+// (1 KiB aligned) sit the rows x [m][H], w [H], w2 [H] (f32), the tokens'
+// int8 embedding rows [m][cat_row_bytes(H)] and their row scales [m] (0 for
+// a token outside the table).  The host admits it for H % 256 == 0, so the
+// f32 part is a whole number of wave loads and needs no clamped tail.
+__device__ __forceinline__ int cat_row_bytes(int H) { return (H + 1023) & ~1023; }
+__device__ __forceinline__ float* cat_area(float* raw, int m, int K) {
+    return raw + ((((size_t)m * K * 4) + 1023) & ~(size_t)1023) / 4;
+}
+
+__device__ __forceinline__ void x_dma_cat(const XSrc& s, int m, float* raw) {
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    const int H = s.H, c16 = H >> 2;
+    float* area = cat_area(raw, m, 2 * H);
+    const int n = (m + 2) * c16;  // a multiple of 64
+    for (int c = wave * 64; c < n; c += nw * 64) {
+        const int idx = c + lane;
+        const int b = idx / c16, j = idx - b * c16;
+        const float* g = b < m ? s.x + (size_t)b * s.ldx + 4 * j : (b == m ? s.w : s.w2) + 4 * j;
+        __builtin_amdgcn_global_load_lds((const void*)g, (__attribute__((address_space(3))) void*)(area + 4 * c), 16,
+                                         0, 0);
+    }
+    // embedding row of token t: the 16-byte chunk j (columns 16j..16j+15) of
+    // the q8 device layout sits at ((t/16 * nkc + j/4) * 64 + 16 (j%4) + t%16) * 16
+    uint8_t* eq = (uint8_t*)(area + (size_t)(m + 2) * H);
+    const int EH = cat_row_bytes(H), e16 = H >> 4;
+    float* crs = (float*)(eq + (size_t)m * EH);
+    for (int b = wave; b < m; b += nw) {
+        const int tok = s.toks[b];
+        const bool tv = tok >= 0 && tok < s.emb.rows;
+        const int t = tv ? tok : 0;
+        const int8_t* rowbase = s.emb.w + ((size_t)(t >> 4) * s.emb.nkc * 64 + (t & 15)) * 16;
+        for (int j0 = 0; j0 < e16; j0 += 64) {
+            const int j = min(j0 + lane, e16 - 1);  // the tail stays inside the row's EH bytes
+            __builtin_amdgcn_global_load_lds((const void*)(rowbase + ((size_t)(j >> 2) * 64 + 16 * (j & 3)) * 16),
+                                             (__attribute__((address_space(3))) void*)(eq + (size_t)b * EH + 16 * j0),
+                                             16, 0, 0);
+        }
+        const float rs = ldg(s.emb.rs + t);
+        if (lane == 0) crs[b] = tv ? rs : 0.f;
+    }
+}
+
 __device__ __forceinline__ void x_dma_rows(const XSrc& s, int m, int K, float* raw) {
+    if (s.mode == XS_CAT) {
+        x_dma_cat(s, m, raw);
+        return;
+    }
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nw = blockDim.x >> 6;
     const int c16 = K >> 2;  // 16-byte chunks per row
@@ -128,8 +177,10 @@ __device__ __forceinline__ void x_dma_rows(const XSrc& s, int m, int K, float* r
 // max|y| reduce inside the wave, so the rows proceed in parallel with no
 // workgroup barrier between them.  Ends with a barrier; the caller has made
 // raw[] visible (barrier after the loads).
-__device__ __forceinline__ void stage_fused(int mode, double eps, int m, int K, int fmt, int nk, float* raw,
+__device__ __forceinline__ void stage_fused(const XSrc& src, int m, int K, int fmt, int nk, float* raw,
                                             uint8_t* planes, float* xs) {
+    const int mode = src.mode;
+    const double eps = src.eps;
     __shared__ float amv[MAXB];
     const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nt >> 6;
@@ -138,7 +189,52 @@ __device__ __forceinline__ void stage_fused(int mode, double eps, int m, int K, 
     // float4 LDS reads, four in flight per lane (K % 4 == 0, rows 16 B
     // aligned): each pass costs about one LDS round trip per 1024 columns
     const int K4 = K >> 2;
-    for (int b = wave; b < m; b += nw) {
+    if (mode == XS_CAT) {
+        // the two halves: the token's embedding row (int8 * row scale, as
+        // k_prep_src) and the hidden row, each rms-normed with its weight
+        const int H = K >> 1, H4 = H >> 2;
+        const float* area = cat_area(raw, m, K);
+        const float4* w1 = (const float4*)(area + (size_t)m * H);
+        const float4* w2 = w1 + H4;
+        const uint8_t* eq = (const uint8_t*)(area + (size_t)(m + 2) * H);
+        const int EH = cat_row_bytes(H);
+        const float* crs = (const float*)(eq + (size_t)m * EH);
+        for (int b = wave; b < m; b += nw) {
+            float4* xr = (float4*)(raw + (size_t)b * K);
+            const float4* hr = (const float4*)(area + (size_t)b * H);
+            const uint32_t* er = (const uint32_t*)(eq + (size_t)b * EH);
+            const float rs = crs[b];
+            double a1 = 0.0, a2 = 0.0;
+#pragma unroll 4
+            for (int i = lane; i < H4; i += 64) {
+                const uint32_t q = er[i];
+                const float4 e = make_float4((float)(int8_t)(q & 0xFF) * rs, (float)(int8_t)((q >> 8) & 0xFF) * rs,
+                                             (float)(int8_t)((q >> 16) & 0xFF) * rs, (float)(int8_t)(q >> 24) * rs);
+                xr[i] = e;
+                a1 += (double)e.x * (double)e.x + (double)e.y * (double)e.y + (double)e.z * (double)e.z +
+                      (double)e.w * (double)e.w;
+                const float4 h = hr[i];
+                a2 += (double)h.x * (double)h.x + (double)h.y * (double)h.y + (double)h.z * (double)h.z +
+                      (double)h.w * (double)h.w;
+            }
+            const float inv1 = 1.0f / (float)sqrt(wave_sum(a1) / (double)H + eps);
+            const float inv2 = 1.0f / (float)sqrt(wave_sum(a2) / (double)H + eps);
+            float am = 0.f;
+#pragma unroll 4
+            for (int i = lane; i < H4; i += 64) {
+                const float4 e = xr[i], we = w1[i], h = hr[i], wh = w2[i];
+                const float4 y1 = make_float4(e.x * inv1 * we.x, e.y * inv1 * we.y, e.z * inv1 * we.z, e.w * inv1 * we.w);
+                const float4 y2 = make_float4(h.x * inv2 * wh.x, h.y * inv2 * wh.y, h.z * inv2 * wh.z, h.w * inv2 * wh.w);
+                xr[i] = y1;
+                xr[H4 + i] = y2;
+                am = fmaxf(am, fmaxf(fmaxf(fabsf(y1.x), fabsf(y1.y)), fmaxf(fabsf(y1.z), fabsf(y1.w))));
+                am = fmaxf(am, fmaxf(fmaxf(fabsf(y2.x), fabsf(y2.y)), fmaxf(fabsf(y2.z), fabsf(y2.w))));
+            }
+            am = wave_max(am);
+            if (lane == 0) amv[b] = am;
+        }
+    }
+    for (int b = wave; mode != XS_CAT && b < m; b += nw) {
         float4* xr = (float4*)(raw + (size_t)b * K);
         const float4* w4 = (const float4*)wn;
         float inv = 1.f;
@@ -322,7 +418,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     } else if constexpr (XM == XM_FUSED) {
         wait_vmcnt<NL>();  // raw rows are in
         __syncthreads();
-        stage_fused(a.src.mode, a.src.eps, M, a.src.K, FMT, ntg * 4, raw, smem, lxs);
+        stage_fused(a.src, M, a.src.K, FMT, ntg * 4, raw, smem, lxs);
     } else if (threadIdx.x < 16) {
         lxs[threadIdx.x] = a.src.xs[threadIdx.x];
     }
@@ -539,7 +635,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     } else if constexpr (XM == XM_FUSED) {
         wait_vmcnt<SP>();  // raw rows are in
         __syncthreads();
-        stage_fused(a.src.mode, a.src.eps, M, a.src.K, DT_Q8ROW, nkc, raw, smem, lxs);
+        stage_fused(a.src, M, a.src.K, DT_Q8ROW, nkc, raw, smem, lxs);
     } else if (threadIdx.x < 16) {
         lxs[threadIdx.x] = a.src.xs[threadIdx.x];
     }
