@@ -232,33 +232,64 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
 
 // The planes of rows b < m at raw + b*K (prep8_row / prep16_row layout, M =
 // m) by the whole workgroup at once, the work of all rows spread over its
-// threads (q8: 4 columns per unit; q4: one item of 8 columns); amv[b] =
+// threads (q8: one item of 16 columns per thread; q4: a pair of 8-column
+// items, 16 columns, per thread); amv[b] =
 // max|x| of row b.
 __device__ inline void prep8_rows(const float* raw, int K, const float* amv, int nk, int m,
                                   uint8_t* planes, float* xs, int tid, int nthr) {
-    const int units = nk * 16;
+    const int items = nk * 4;
     uint8_t* p0 = planes;
     uint8_t* p1 = planes + (size_t)nk * 64 * m;
     uint8_t* p2 = planes + (size_t)nk * 128 * m;
-    for (int j = tid; j < m * units; j += nthr) {
-        const int b = j / units, u = j - b * units;
+    if (m * items * 4 < 3 * nthr) {
+        // few columns per thread: one thread per 4 columns (one byte lane of
+        // a word in each plane), more threads busy
+        const int units = items * 4;
+        for (int j = tid; j < m * units; j += nthr) {
+            const int b = j / units, u = j - b * units;
+            const float amax = amv[b];
+            const float sx = amax > 0.f ? amax / 127.0f : 1.0f;
+            const float inv = 1.0f / sx;
+            if (u == 0) xs[b] = sx;
+            const int idx = u >> 2, q4 = u & 3;
+            const int c0 = (idx >> 2) * 64 + 16 * (idx & 3) + 4 * q4;
+            // K % 4 == 0: a unit is all inside or all past the row
+            const float4 xv = c0 < K ? *(const float4*)(raw + (size_t)b * K + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+            uint32_t a = 0, bb = 0, c = 0;
+            q8_split(xv.x * inv, 0, a, bb, c);
+            q8_split(xv.y * inv, 1, a, bb, c);
+            q8_split(xv.z * inv, 2, a, bb, c);
+            q8_split(xv.w * inv, 3, a, bb, c);
+            const size_t off = ((size_t)idx * m + b) * 16 + 4 * q4;
+            *(uint32_t*)(p0 + off) = a;
+            *(uint32_t*)(p1 + off) = bb;
+            *(uint32_t*)(p2 + off) = c;
+        }
+        return;
+    }
+    // one thread per item (16 columns): the row's scale and reciprocal once
+    // for its four 4-column units
+    for (int j = tid; j < m * items; j += nthr) {
+        const int b = j / items, idx = j - b * items;
         const float amax = amv[b];
         const float sx = amax > 0.f ? amax / 127.0f : 1.0f;
         const float inv = 1.0f / sx;
-        if (u == 0) xs[b] = sx;
-        const int idx = u >> 2, q4 = u & 3;
-        const int c0 = (idx >> 2) * 64 + 16 * (idx & 3) + 4 * q4;
-        // K % 4 == 0: a unit is all inside or all past the row
-        const float4 xv = c0 < K ? *(const float4*)(raw + (size_t)b * K + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
-        uint32_t a = 0, bb = 0, c = 0;
-        q8_split(xv.x * inv, 0, a, bb, c);
-        q8_split(xv.y * inv, 1, a, bb, c);
-        q8_split(xv.z * inv, 2, a, bb, c);
-        q8_split(xv.w * inv, 3, a, bb, c);
-        const size_t off = ((size_t)idx * m + b) * 16 + 4 * q4;
-        *(uint32_t*)(p0 + off) = a;
-        *(uint32_t*)(p1 + off) = bb;
-        *(uint32_t*)(p2 + off) = c;
+        if (idx == 0) xs[b] = sx;
+        const int c0 = (idx >> 2) * 64 + 16 * (idx & 3);
+        const size_t off = ((size_t)idx * m + b) * 16;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const int c = c0 + 4 * q4;
+            const float4 xv = c < K ? *(const float4*)(raw + (size_t)b * K + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            uint32_t a = 0, bb = 0, cc = 0;
+            q8_split(xv.x * inv, 0, a, bb, cc);
+            q8_split(xv.y * inv, 1, a, bb, cc);
+            q8_split(xv.z * inv, 2, a, bb, cc);
+            q8_split(xv.w * inv, 3, a, bb, cc);
+            *(uint32_t*)(p0 + off + 4 * q4) = a;
+            *(uint32_t*)(p1 + off + 4 * q4) = bb;
+            *(uint32_t*)(p2 + off + 4 * q4) = cc;
+        }
     }
 }
 __device__ inline void prep16_rows(const float* raw, int K, const float* amv, int ntiles, int m,
@@ -267,9 +298,11 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
     uint8_t* ph = planes;
     uint8_t* pl = planes + (size_t)ntiles * 64 * m;
     float* bias = (float*)(planes + (size_t)ntiles * 128 * m);
-    const int per = ntiles * 4;  // items per row (a multiple of 4: tiles never straddle rows)
-    for (int i0 = 0; i0 < m * per; i0 += nthr) {  // uniform trip count (shuffles below)
-        const int jx = i0 + tid;
+    if (m * ntiles * 4 <= nthr) {
+        // one pass with one item (8 columns) per thread: the tile's four
+        // items are the lanes of one quad
+        const int per = ntiles * 4;
+        const int jx = tid;
         const bool on = jx < m * per;
         const int b = on ? jx / per : 0, idx = jx - b * per;
         const float amax = amv[b];
@@ -278,11 +311,11 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
         const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
         if (on && idx == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
-        // K % 4 == 0: each half of the item is all inside or all past the row
-        const float* x = raw + (size_t)b * K + c0;
+        const bool in = on && c0 < K;
+        const float* x = raw + (size_t)b * K + min(c0, K - 8);
+        const float4 xa0 = *(const float4*)x, xb0 = *(const float4*)(x + 4);
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 xa = on && c0 < K ? *(const float4*)x : z4;
-        const float4 xb = on && c0 + 4 < K ? *(const float4*)(x + 4) : z4;
+        const float4 xa = in ? xa0 : z4, xb = in ? xb0 : z4;
         const float xv[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};  // columns {0,4,2,6,1,5,3,7}
         uint16_t hv[8], lv[8];
         float part = 0.f;
@@ -295,16 +328,81 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
             lv[j] = __builtin_bit_cast(uint16_t, l);
             part += (float)h + (float)l;
         }
-        // the four items of a tile are lanes 4t'..4t'+3 of one quad
         part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0xb1, 0xf, 0xf, false));
         part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0x4e, 0xf, 0xf, false));
-        if (!on) continue;
+        if (!on) return;
         const size_t off = ((size_t)idx * m + b) * 16;
         *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
                                          lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
         if (s == 0) {
+            bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
+            if (b == 0)
+                for (int r = m; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
+        }
+        return;
+    }
+    // otherwise one thread per pair of items (s = 2p, 2p + 1) of a tile: 16
+    // columns, half the passes; the tile's two pairs sit in lanes 2k, 2k + 1
+    // (per2 is even)
+    const int per2 = ntiles * 2;
+    for (int i0 = 0; i0 < m * per2; i0 += nthr) {  // uniform trip count (shuffles below)
+        const int jx = i0 + tid;
+        const bool on = jx < m * per2;
+        const int b = on ? jx / per2 : 0, ip = jx - b * per2;
+        const float amax = amv[b];
+        int ex = 0;
+        if (amax > 0.f) frexpf(amax, &ex);
+        const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
+        if (on && ip == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+        const int t = ip >> 1, s0 = (ip & 1) * 2, c0 = t * 32 + 8 * s0;
+        // K % 32 == 0 (q4 rows are whole tiles) and c0 % 16 == 0: the pair
+        // is all inside or all past the row.  Unconditional 16-byte reads at
+        // a clamped address, the values selected.
+        const bool in = on && c0 < K;
+        const float* x = raw + (size_t)b * K + min(c0, K - 16);
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 q[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 r = *(const float4*)(x + 4 * k);
+            q[k] = in ? r : z4;
+        }
+        uint4 hq[2], lq[2];
+        float pp[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const float4 xa = q[2 * u], xb = q[2 * u + 1];
+            const float xv[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};  // columns {0,4,2,6,1,5,3,7}
+            uint16_t hv[8], lv[8];
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float v = xv[j] * scale;
+                const _Float16 h = (_Float16)v;
+                const _Float16 l = (_Float16)(v - (float)h);
+                hv[j] = __builtin_bit_cast(uint16_t, h);
+                lv[j] = __builtin_bit_cast(uint16_t, l);
+                part += (float)h + (float)l;
+            }
+            pp[u] = part;
+            hq[u] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                               hv[6] | (hv[7] << 16));
+            lq[u] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
+                               lv[6] | (lv[7] << 16));
+        }
+        // tile sum (p0 + p1) + (p2 + p3), the pairs' partners one lane apart
+        float part = pp[0] + pp[1];
+        part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0xb1, 0xf, 0xf, false));
+        if (!on) continue;
+        const int idx = 4 * t + s0;
+        const size_t off = ((size_t)idx * m + b) * 16;
+        *(uint4*)(ph + off) = hq[0];
+        *(uint4*)(pl + off) = lq[0];
+        *(uint4*)(ph + off + (size_t)m * 16) = hq[1];
+        *(uint4*)(pl + off + (size_t)m * 16) = lq[1];
+        if (s0 == 0) {
             bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
             if (b == 0)
                 for (int r = m; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
