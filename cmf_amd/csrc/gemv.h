@@ -177,6 +177,19 @@ __device__ inline void prep8_row(const float* x, int K, float amax, int nk, int 
     }
 }
 
+// hi + lo of one split value as f32 (exact: 22 significant bits), by one
+// mixed-precision FMA lo * 1.0 + hi on the f16 registers instead of two
+// conversions and an add.
+__device__ __forceinline__ float f16_pair_sum(_Float16 hi, _Float16 lo) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    float r;
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,1]" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
+#else
+    return (float)hi + (float)lo;
+#endif
+}
+
 // Writes batch row b (of M) of the q4 activation operand: f16 hi/lo of
 // x*2^e with max|x*2^e| < 2^15, xs[b] = 2^-e, planes [item = 4*tile + s][b]
 // x 8 halves of columns 32*tile + 8*s + {0,4,2,6,1,5,3,7} (hi plane, then lo
@@ -212,7 +225,7 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
             const _Float16 l = (_Float16)(v - (float)h);
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
-            part += (float)h + (float)l;
+            part += f16_pair_sum(h, l);
         }
         part += __shfl_xor(part, 1);
         part += __shfl_xor(part, 2);
@@ -326,7 +339,7 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
             const _Float16 l = (_Float16)(v - (float)h);
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
-            part += (float)h + (float)l;
+            part += f16_pair_sum(h, l);
         }
         part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0xb1, 0xf, 0xf, false));
         part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0x4e, 0xf, 0xf, false));
@@ -384,7 +397,7 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
                 const _Float16 l = (_Float16)(v - (float)h);
                 hv[j] = __builtin_bit_cast(uint16_t, h);
                 lv[j] = __builtin_bit_cast(uint16_t, l);
-                part += (float)h + (float)l;
+                part += f16_pair_sum(h, l);
             }
             pp[u] = part;
             hq[u] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
