@@ -139,6 +139,53 @@ __device__ __forceinline__ void attn_values(float (*S)[ATT_C], const float (*V)[
     }
 }
 
+// Chunk softmax (as attn_values) and then the values of all nq queries of
+// the kv head, 16 at a time, by fp32 MFMA (16x16x4): D[q][d] = sum_p E[q][p] V[p][d],
+// A = the weights E (query q = lane % 16, position 4k + lane / 16, rows of S
+// past nq are never stored), B = V (position x dim), wave w producing dims
+// 32w .. 32w+31 (two 16-column blocks).  S rows are SC floats apart and V rows
+// VC floats (both padded so that the 16 A rows and the 4 B rows of one MFMA
+// fall in distinct LDS banks).
+template <int SC, int VC>
+__device__ __forceinline__ void attn_values_mfma(float (*S)[SC], const float (*V)[VC], int w, int lane, int nq,
+                                                 int hpk, int nh, int g, int c, int nch, float* pm, float* pl,
+                                                 float* po) {
+    constexpr int C = ATT_C, HD = 128;
+    for (int qi = w; qi < nq; qi += 4) {
+        const float mx = wave_max(S[qi][lane]);
+        const float e = mx == -INFINITY ? 0.f : expf(S[qi][lane] - mx);
+        S[qi][lane] = e;
+        const float l = wave_sum(e);
+        if (lane == 0) {
+            const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
+            pm[row * nch + c] = mx;
+            pl[row * nch + c] = l;
+        }
+    }
+    __syncthreads();
+    const int d0 = 32 * w, q = lane & 15, kq = lane >> 4;
+    for (int qb = 0; qb < nq; qb += 16) {  // blocks of 16 queries
+        float4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+#pragma unroll 4
+        for (int k = 0; k < C / 4; k++) {
+            const int p = 4 * k + kq;
+            const float a = S[qb + q][p];
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, V[p][d0 + q], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, V[p][d0 + 16 + q], acc1, 0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int qi = qb + 4 * kq + e;
+            if (qi < nq) {
+                const size_t row = (size_t)(qi / hpk) * nh + g * hpk + qi % hpk;
+                float* o = po + (row * nch + c) * HD + d0 + q;
+                o[0] = acc0[e];
+                o[16] = acc1[e];
+            }
+        }
+    }
+}
+
 // K (k-norm + RoPE) and V rows of the new positions pos0 + b that fall in the
 // chunk at p0, one wave per row: appended to the cache and, when Kn is given,
 // kept in LDS (Kn[b], V[pos - p0]) for the chunk's own attention.
@@ -246,8 +293,11 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     const int p0 = c * C;
     constexpr int QR = 4 * NQW < 16 ? 16 : 4 * NQW;  // Q rows: whole MFMA query blocks
     __shared__ __align__(16) float Q[QR][HD + 4];  // rows padded: the MFMA A reads take 16 rows at once
-    __shared__ __align__(16) float V[C][HD + 4];
-    __shared__ __align__(16) float S[4 * NQW][C];
+    // VM: values by MFMA (at least 9 queries); padded rows for its bank pattern
+    constexpr bool VM = NQW >= 3;
+    constexpr int VC = VM ? HD + 16 : HD + 4, SC = VM ? C + 4 : C, SR = VM ? (4 * NQW + 15) / 16 * 16 : 4 * NQW;
+    __shared__ __align__(16) float V[C][VC];
+    __shared__ __align__(16) float S[SR][SC];
     __shared__ __align__(16) float Kn[MAXB][HD + 4];
     if (!a.attend) {  // KV append only (MTP warm-up)
         if (p0 < stored) append_rows(a, g, p0, pos0, wave, lane, nullptr, nullptr);
@@ -401,7 +451,11 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     }
     __syncthreads();
     const int nqw = (nq - wave + 3) >> 2;  // queries of this wave
-    if (nqw > 0) attn_values<NQW>(S, V, wave, lane, hpk, nh, g, c, a.nch, nqw, a.pm, a.pl, a.po);
+    if constexpr (VM) {
+        attn_values_mfma<SC, VC>(S, V, wave, lane, nq, hpk, nh, g, c, a.nch, a.pm, a.pl, a.po);
+    } else if (nqw > 0) {
+        attn_values<NQW>(S, V, wave, lane, hpk, nh, g, c, a.nch, nqw, a.pm, a.pl, a.po);
+    }
 }
 
 // Argmax per row, ties to the highest index.  Pass 1: grid (nslices, nrows).
