@@ -423,7 +423,7 @@ __global__ void k_build_vtok(DState* st, int k) {
 
 // greedy acceptance (pipeline.rs:3989-3999): a = longest prefix with
 // argmax(row i) == d_i; emits [t_next, d_0..d_{a-1}]; next token argmax(row a)
-__global__ void k_accept_greedy(DState* st, int k, int* out) {
+__device__ __forceinline__ void accept_greedy(DState* st, int k, int* out) {
     int a = 0;
     while (a < k && st->argmax[a] == st->drafts[a]) a++;
     const int n = st->n_out;
@@ -433,6 +433,32 @@ __global__ void k_accept_greedy(DState* st, int k, int* out) {
     st->a = a;
     st->t_new = st->argmax[a];
     st->accepted += a;
+}
+
+// The verify rows' argmax (second pass, wave r reduces row r's partials)
+// followed by the greedy acceptance in the same launch: one workgroup of
+// 64 (k + 1) threads, k <= 8.
+__global__ __launch_bounds__(1024) void k_argmax_accept(const float* __restrict__ pv,
+                                                                   const int* __restrict__ pi, int ns, DState* st,
+                                                                   int k, int* out) {
+    const int r = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float bv = -INFINITY;
+    int bi = 0;
+    for (int s = lane; s < ns; s += 64) argmax_take(bv, bi, pv[(size_t)r * ns + s], pi[(size_t)r * ns + s]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(bv, o);
+        const int i2 = __shfl_xor(bi, o);
+        argmax_take(bv, bi, v2, i2);
+    }
+    __shared__ int win[MAXB + 1];
+    if (lane == 0) win[r] = bi;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        // one thread writes the rows' picks and then reads them back
+        for (int j = 0; j <= k; j++) st->argmax[j] = win[j];
+        accept_greedy(st, k, out);
+    }
 }
 
 // commit: h_tip = hidden row a, next_pos += a + 1, t_next = t_new
@@ -632,8 +658,9 @@ static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_conf
     if (sampling) {
         sample_rows(m->sb, m->logits, V, k + 1, sc, m->st, SampleMode::Accept, k, m->out, s);
     } else {
-        launch_argmax(m->logits, V, V, k + 1, m->am_v, m->am_i, m->st->argmax, s);
-        hipLaunchKernelGGL(k_accept_greedy, dim3(1), dim3(1), 0, s, m->st, k, m->out);
+        const int ns = launch_argmax_part(m->logits, V, V, k + 1, m->am_v, m->am_i, s);
+        hipLaunchKernelGGL(k_argmax_accept, dim3(1), dim3(64 * (k + 1)), 0, s, m->am_v, m->am_i, ns, m->st, k,
+                           m->out);
     }
     mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, graph_len ? graph_len : np + k + 1, s);
     hipLaunchKernelGGL(k_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H);

@@ -33,6 +33,17 @@ struct AttnArgs {
 };
 // k_attention (chunk partials) then, with merge, k_attn_merge (rows of a.out).
 void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge = true);
+// The lexicographic (value, index) maximum step of argmax (sampler.rs:1130-1154
+// keeps the higher index on equal values; NaN never wins).
+__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
+    if (v > bv || (v == bv && i > bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+// The first pass of launch_argmax alone: per-slice partials of nrows rows
+// into pv/pi [nrows][ns]; returns ns.
+int launch_argmax_part(const float* x, int ld, int n, int nrows, float* pv, int* pi, hipStream_t st);
 void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
                    hipStream_t st);
 

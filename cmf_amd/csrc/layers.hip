@@ -518,12 +518,6 @@ __global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x
 // an equal value with a higher index wins, NaN never wins.  A maximum is
 // order-free, so the lanes' strided scans and the butterfly give the same
 // index as one scan over all partials.
-__device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i > bi)) {
-        bv = v;
-        bi = i;
-    }
-}
 __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ pv, const int* __restrict__ pi,
                                                      int ns, int nrows, int* __restrict__ out) {
     const int r = blockIdx.x, lane = threadIdx.x;
@@ -568,10 +562,14 @@ void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge
     hipLaunchKernelGGL(k_attn_merge, dim3(a.nb * a.nh), dim3(64), 0, st, a);
 }
 
-void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
-                   hipStream_t st) {
+int launch_argmax_part(const float* x, int ld, int n, int nrows, float* pv, int* pi, hipStream_t st) {
     const int slice = 4096, ns = (n + slice - 1) / slice;
     hipLaunchKernelGGL(k_argmax_part, dim3(ns, nrows), dim3(256), 0, st, x, ld, n, slice, pv, pi);
+    return ns;
+}
+void launch_argmax(const float* x, int ld, int n, int nrows, float* pv, int* pi, int* out,
+                   hipStream_t st) {
+    const int ns = launch_argmax_part(x, ld, n, nrows, pv, pi, st);
     hipLaunchKernelGGL(k_argmax_final, dim3(nrows), dim3(64), 0, st, pv, pi, ns, nrows,
                        out);
 }
