@@ -132,6 +132,9 @@ SIGNATURES = {
     "cmf_decode_tokens": (_I, [_P, _P, _I]),
     "cmf_forward_batch": (_I, [_P, _P, _I, _I, _P, _P]),
     "cmf_kv_truncate": (_I, [_P, _I]),
+    "cmf_verify_step": (_I, [_P, _P, _I, _I, C.POINTER(SamplerConfig), _P, _P, _P, _P, _P, _P, C.POINTER(_I),
+                             C.POINTER(_I)]),
+    "cmf_sparse_distribution": (_I, [_P, _P, C.POINTER(SamplerConfig), _P, _P]),
     "cmf_state_get": (_I, [_P, C.POINTER(_I), _P]),
     "cmf_kv_export": (_I, [_P, _I, _I, _P, _P]),
     "cmf_model_set_embed": (_I, [_P, C.POINTER(Tensor)]),

@@ -69,6 +69,7 @@ struct cmf_model_s {
     bool decoding = false;
     int rounds = 0;
     int emitted_host = 0;
+    int accepted_host = 0;
     cmf_sampler_config sc{};
 };
 
@@ -710,6 +711,7 @@ int cmf_decode_begin(cmf_model m, const cmf_sampler_config* sc, uint64_t seed) {
     m->decoding = true;
     m->rounds = 0;
     m->emitted_host = 0;
+    m->accepted_host = 0;
     return CMF_OK;
 }
 
@@ -780,13 +782,14 @@ int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats)
     m->next_pos_host = hs.next_pos;
     m->emitted_host = hs.n_out;
     m->rounds += spec ? n : 0;
-    if (stats) {
+    if (stats) {  // this call's rounds
         stats->generated = hs.n_out;
-        stats->drafted = m->rounds * k;
-        stats->accepted = hs.accepted;
-        stats->rounds = m->rounds;
+        stats->drafted = spec ? n * k : 0;
+        stats->accepted = hs.accepted - m->accepted_host;
+        stats->rounds = spec ? n : 0;
         stats->device_ms = ms;
     }
+    m->accepted_host = hs.accepted;
     return CMF_OK;
 }
 
@@ -807,7 +810,7 @@ int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64
     if (rc != CMF_OK) return rc;
     hipStream_t s = stream();
     double ms = 0.0;
-    cmf_gen_stats st{};
+    cmf_gen_stats st{}, tot{};
     int generated = 0;
     while (true) {
         if (generated + 1 >= max_tokens) {
@@ -821,15 +824,18 @@ int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64
         rc = cmf_decode_rounds(m, 1, sp ? 1 : 0, k, &st);
         if (rc != CMF_OK) return rc;
         ms += st.device_ms;
+        tot.drafted += st.drafted;
+        tot.accepted += st.accepted;
+        tot.rounds += st.rounds;
         generated = m->emitted_host;
     }
     const int n = cmf_decode_tokens(m, out, m->emitted_host);
     if (n < 0) return CMF_ERR;
     if (stats) {
         stats->generated = n;
-        stats->drafted = m->rounds * k;
-        stats->accepted = st.accepted;
-        stats->rounds = m->rounds;
+        stats->drafted = tot.drafted;
+        stats->accepted = tot.accepted;
+        stats->rounds = tot.rounds;
         stats->device_ms = ms;
     }
     m->decoding = false;
@@ -847,6 +853,7 @@ int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float
     hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, pos0);
     launch_embed(m->toks, embed_src(m), H, m->hv, H, b, s);
     trunk_forward(m, b, pb, 0, pos0 + b, logits != nullptr, s);
+    CMF_HIP(hipMemcpyAsync(m->h_tip, m->hv + (size_t)(b - 1) * H, H * sizeof(float), hipMemcpyDeviceToDevice, s));
     if (hidden) CMF_HIP(hipMemcpyAsync(hidden, m->hv, (size_t)b * H * sizeof(float), hipMemcpyDeviceToHost, s));
     if (logits)
         CMF_HIP(hipMemcpyAsync(logits, m->logits, (size_t)b * m->c.vocab * sizeof(float), hipMemcpyDeviceToHost, s));
@@ -855,6 +862,93 @@ int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float
     CMF_HIP(hipGetLastError());
     m->next_pos_host = pos0 + b;
     return CMF_OK;
+}
+
+int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const cmf_sampler_config* sc,
+                    const int32_t* q_ids, const float* q_probs, const int32_t* q_n, const float* uniforms,
+                    int32_t* argmax_out, float* logits_out, int32_t* accepted, int32_t* next_token) {
+    if (ready(m)) return CMF_ERR;
+    const int k = b - 1;
+    if (!tokens || k < 1 || k > 8 || pos0 < 1 || pos0 + b + 1 > m->c.max_seq)
+        return fail("verify_step: 2 <= b <= 9 tokens, 1 <= pos0, pos0 + b < max_seq");
+    const int V = m->c.vocab, H = m->c.hidden;
+    for (int i = 0; i < b; i++)
+        if (tokens[i] < 0 || tokens[i] >= V) return fail("verify_step: token id out of range");
+    const bool sampling = sc && sc->temperature >= 1e-6f;
+    if (sampling) {
+        const int rc = check_sampler(m, sc);
+        if (rc != CMF_OK) return rc;
+        if (!q_ids || !q_probs || !q_n || !uniforms) return fail("verify_step: sampling needs q and uniforms");
+        for (int j = 0; j < k; j++)
+            if (q_n[j] < 1 || q_n[j] > SPARSE_K_MAX) return fail("verify_step: q_n[j] must be 1..64");
+    }
+    if (ensure_out(m, m->c.max_seq + 32)) return CMF_ERR;
+    hipStream_t s = stream();
+    DState init{};
+    init.next_pos = pos0;
+    init.t_next = tokens[0];
+    init.forced = -1;
+    for (int j = 0; j < k; j++) init.drafts[j] = tokens[1 + j];
+    CMF_HIP(hipMemcpyAsync(m->st, &init, sizeof(DState), hipMemcpyHostToDevice, s));
+    if (sampling) {
+        CMF_HIP(hipMemcpyAsync(m->sb.qid, q_ids, (size_t)k * SPARSE_K_MAX * 4, hipMemcpyHostToDevice, s));
+        CMF_HIP(hipMemcpyAsync(m->sb.qp, q_probs, (size_t)k * SPARSE_K_MAX * 4, hipMemcpyHostToDevice, s));
+        CMF_HIP(hipMemcpyAsync(m->sb.qn, q_n, (size_t)k * 4, hipMemcpyHostToDevice, s));
+        CMF_HIP(hipMemcpyAsync(m->sb.uni, uniforms, (size_t)b * 4, hipMemcpyHostToDevice, s));
+    }
+    int* pb = &m->st->next_pos;
+    // the MTP row of the first draft, (tip hidden, t_next) at pos0 - 1: what
+    // the device draft chain writes before a round
+    if (m->has_mtp) mtp_warm(m, &m->st->t_next, m->h_tip, 1, pb, -1, pos0, s);
+    hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
+    launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, b, s);
+    trunk_forward(m, b, pb, 0, pos0 + b, true, s);
+    if (sampling) {
+        sample_rows(m->sb, m->logits, V, b, *sc, m->st, SampleMode::Accept, k, m->out, s, b);
+        if (argmax_out) launch_argmax(m->logits, V, V, b, m->am_v, m->am_i, m->st->argmax, s);
+    } else {
+        const int ns = launch_argmax_part(m->logits, V, V, b, m->am_v, m->am_i, s);
+        hipLaunchKernelGGL(k_argmax_accept, dim3(1), dim3(64 * b), 0, s, m->am_v, m->am_i, ns, m->st, k, m->out);
+    }
+    if (logits_out)
+        CMF_HIP(hipMemcpyAsync(logits_out, m->logits, (size_t)b * V * sizeof(float), hipMemcpyDeviceToHost, s));
+    if (m->has_mtp) mtp_warm(m, m->st->drafts, m->hv, k, pb, 0, pos0 + b, s);
+    hipLaunchKernelGGL(k_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H);
+    DState hs{};
+    CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
+    CMF_HIP(hipStreamSynchronize(s));
+    CMF_HIP(hipGetLastError());
+    m->next_pos_host = hs.next_pos;
+    m->prefilled = true;
+    m->decoding = false;
+    if (accepted) *accepted = hs.a;
+    if (next_token) *next_token = hs.t_next;
+    if (argmax_out)
+        for (int i = 0; i < b; i++) argmax_out[i] = hs.argmax[i];
+    return CMF_OK;
+}
+
+int cmf_sparse_distribution(cmf_model m, const float* logits, const cmf_sampler_config* sc, int32_t* ids,
+                            float* probs) {
+    if (ready(m)) return CMF_ERR;
+    if (!logits || !sc || !ids || !probs) return fail("sparse_distribution: null argument");
+    if (sc->temperature < 1e-6f) return fail("sparse_distribution: temperature must be > 0");
+    const int rc = check_sampler(m, sc);
+    if (rc != CMF_OK) return rc;
+    hipStream_t s = stream();
+    const int V = m->c.vocab;
+    int* d_n = m->toks;  // scratch
+    CMF_HIP(hipMemcpyAsync(m->logits, logits, (size_t)V * sizeof(float), hipMemcpyHostToDevice, s));
+    sample_distribution(m->sb, m->logits, V, *sc, m->sb.rid + MAXB * SPARSE_K_MAX,
+                        m->sb.rv + MAXB * SPARSE_K_MAX, d_n, s);
+    int n = 0;
+    CMF_HIP(hipMemcpyAsync(&n, d_n, sizeof(int), hipMemcpyDeviceToHost, s));
+    CMF_HIP(hipStreamSynchronize(s));
+    if (n < 1 || n > SPARSE_K_MAX) return fail("sparse_distribution: bad count");
+    CMF_HIP(hipMemcpy(ids, m->sb.rid + MAXB * SPARSE_K_MAX, n * 4, hipMemcpyDeviceToHost));
+    CMF_HIP(hipMemcpy(probs, m->sb.rv + MAXB * SPARSE_K_MAX, n * 4, hipMemcpyDeviceToHost));
+    CMF_HIP(hipGetLastError());
+    return n;
 }
 
 int cmf_kv_truncate(cmf_model m, int n) {

@@ -44,6 +44,7 @@ struct SampleBufs {
     int* qid = nullptr;     // draft distributions [8][K_MAX]
     float* qp = nullptr;
     int* qn = nullptr;      // [8]
+    float* uni = nullptr;   // caller uniforms of a verify step [MAXB + 1]
 };
 
 int sample_alloc(SampleBufs& b, int V, const std::function<int(void**, size_t)>& alloc);
@@ -53,7 +54,15 @@ int sample_alloc(SampleBufs& b, int V, const std::function<int(void**, size_t)>&
 //   Plain : p from row 0, draw -> st->t_new
 //   Accept: rows 0..k against q_0..q_{k-1}; emits [t_next, accepted drafts]
 //           into out, sets a, forced, t_new (correction or draw from row a)
+// nuni > 0: the chain's uniforms are b.uni[0..nuni) in order (the caller's
+// shared uniforms), then the SplitMix64 stream.
 void sample_rows(SampleBufs& b, const float* logits, int V, int rows, const cmf_sampler_config& sc,
-                 DState* st, SampleMode mode, int j_or_k, int* out, hipStream_t s);
+                 DState* st, SampleMode mode, int j_or_k, int* out, hipStream_t s, int nuni = 0);
+
+// The sparse distribution of logits row 0 (sparse_distribution_into with the
+// argmax fallback of a fully filtered row): ids ascending into ids[0..n),
+// probabilities into probs, n into *n (all device pointers).
+void sample_distribution(SampleBufs& b, const float* logits, int V, const cmf_sampler_config& sc, int* ids,
+                         float* probs, int* n, hipStream_t s);
 
 }  // namespace cmf

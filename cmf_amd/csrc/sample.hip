@@ -307,8 +307,17 @@ __device__ int row_argmax(const int* rid, const float* rv, int k) {
     return best;
 }
 
-__device__ int draw_sparse(const int* id, const float* p, int n, unsigned long long* rng) {
-    const float r = next_f32(rng);
+// The chain's uniform source: the caller's uniforms first (a verify step
+// under shared uniforms), then the SplitMix64 stream.
+struct Uni {
+    unsigned long long rng;
+    const float* u;
+    int n, used;
+    __device__ float next() { return used < n ? u[used++] : next_f32(&rng); }
+};
+
+__device__ int draw_sparse(const int* id, const float* p, int n, Uni* rng) {
+    const float r = rng->next();
     float cum = 0.f;
     for (int i = 0; i < n; i++) {
         cum += p[i];
@@ -329,12 +338,12 @@ __global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restri
                                 const float* __restrict__ rv, const float* __restrict__ lmax,
                                 const float* __restrict__ sum, int* __restrict__ qid,
                                 float* __restrict__ qp, int* __restrict__ qn, DState* st,
-                                int* __restrict__ out) {
+                                int* __restrict__ out, const float* __restrict__ uni, int nuni) {
     // the O(k) chain runs in one thread; its working lists live in LDS
     __shared__ int pid[SPARSE_K_MAX], rsid[SPARSE_K_MAX];
     __shared__ float pp[SPARSE_K_MAX], rsp[SPARSE_K_MAX];
     if (threadIdx.x != 0) return;
-    unsigned long long rng = st->rng;
+    Uni rng{st->rng, uni, nuni, 0};
     if (mode == 0 || mode == 1) {  // Draft / Plain: distribution of row 0, one draw
         int n = sparse_dist(rid, rv, lmax[0], sum[0], c, pid, pp);
         if (n == 0) {
@@ -353,7 +362,7 @@ __global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restri
         } else {
             st->t_new = tok;
         }
-        st->rng = rng;
+        st->rng = rng.rng;
         return;
     }
     // Accept (pipeline.rs:3894-3934 + the loop-top sample of row a)
@@ -373,7 +382,7 @@ __global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restri
         const float* q_p = qp + a * SPARSE_K_MAX;
         const int nq = qn[a];
         const float pd = sparse_get(pid, pp, np, d), qd = sparse_get(q_id, q_p, nq, d);
-        const float r = next_f32(&rng);
+        const float r = rng.next();
         if (qd > 0.f && r * qd < pd) {
             a++;
             continue;
@@ -413,7 +422,26 @@ __global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restri
     st->forced = forced;
     st->t_new = tnew;
     st->accepted += a;
-    st->rng = rng;
+    st->rng = rng.rng;
+}
+
+__global__ void k_sample_dist(SampCfg c, const int* __restrict__ rid, const float* __restrict__ rv,
+                              const float* __restrict__ lmax, const float* __restrict__ sum, int* __restrict__ ids,
+                              float* __restrict__ probs, int* __restrict__ n_out) {
+    __shared__ int pid[SPARSE_K_MAX];
+    __shared__ float pp[SPARSE_K_MAX];
+    if (threadIdx.x != 0) return;
+    int n = sparse_dist(rid, rv, lmax[0], sum[0], c, pid, pp);
+    if (n == 0) {
+        pid[0] = row_argmax(rid, rv, c.k);
+        pp[0] = 1.f;
+        n = 1;
+    }
+    for (int i = 0; i < n; i++) {
+        ids[i] = pid[i];
+        probs[i] = pp[i];
+    }
+    *n_out = n;
 }
 
 int sample_alloc(SampleBufs& b, int V, const std::function<int(void**, size_t)>& alloc) {
@@ -426,25 +454,40 @@ int sample_alloc(SampleBufs& b, int V, const std::function<int(void**, size_t)>&
         alloc((void**)&b.rid, (size_t)R * SPARSE_K_MAX * 4) || alloc((void**)&b.rv, (size_t)R * SPARSE_K_MAX * 4) ||
         alloc((void**)&b.lmax, R * 4) || alloc((void**)&b.sum, R * 4) ||
         alloc((void**)&b.qid, 8 * SPARSE_K_MAX * 4) || alloc((void**)&b.qp, 8 * SPARSE_K_MAX * 4) ||
-        alloc((void**)&b.qn, 8 * 4))
+        alloc((void**)&b.qn, 8 * 4) || alloc((void**)&b.uni, (MAXB + 1) * 4))
         return CMF_ERR;
     return CMF_OK;
 }
 
-void sample_rows(SampleBufs& b, const float* logits, int V, int rows, const cmf_sampler_config& sc,
-                 DState* st, SampleMode mode, int jk, int* out, hipStream_t s) {
+static SampCfg samp_cfg(const cmf_sampler_config& sc, int V) {
     SampCfg c;
     c.t = sc.temperature > 0.f ? sc.temperature : 1.0f;
     c.top_p = sc.top_p;
     c.min_p = sc.min_p;
     c.k = (int)sc.top_k < V ? (int)sc.top_k : V;
+    return c;
+}
+
+void sample_distribution(SampleBufs& b, const float* logits, int V, const cmf_sampler_config& sc, int* ids,
+                         float* probs, int* n, hipStream_t s) {
+    const SampCfg c = samp_cfg(sc, V);
+    hipLaunchKernelGGL(k_topk_slice, dim3(b.nslices, 1), dim3(256), 0, s, logits, V, c, b.nslices, b.cid, b.cv,
+                       b.smax, b.ssum);
+    hipLaunchKernelGGL(k_topk_merge, dim3(1), dim3(256), 0, s, V, c, b.nslices, b.cid, b.cv, b.smax, b.ssum,
+                       b.rid, b.rv, b.lmax, b.sum);
+    hipLaunchKernelGGL(k_sample_dist, dim3(1), dim3(64), 0, s, c, b.rid, b.rv, b.lmax, b.sum, ids, probs, n);
+}
+
+void sample_rows(SampleBufs& b, const float* logits, int V, int rows, const cmf_sampler_config& sc,
+                 DState* st, SampleMode mode, int jk, int* out, hipStream_t s, int nuni) {
+    const SampCfg c = samp_cfg(sc, V);
     hipLaunchKernelGGL(k_topk_slice, dim3(b.nslices, rows), dim3(256), 0, s, logits, V, c, b.nslices, b.cid,
                        b.cv, b.smax, b.ssum);
     hipLaunchKernelGGL(k_topk_merge, dim3(rows), dim3(256), 0, s, V, c, b.nslices, b.cid, b.cv, b.smax,
                        b.ssum, b.rid, b.rv, b.lmax, b.sum);
     const int m = mode == SampleMode::Draft ? 0 : (mode == SampleMode::Plain ? 1 : 2);
     hipLaunchKernelGGL(k_sample_finish, dim3(1), dim3(64), 0, s, c, m, jk, b.rid, b.rv, b.lmax, b.sum, b.qid,
-                       b.qp, b.qn, st, out);
+                       b.qp, b.qn, st, out, b.uni, nuni);
 }
 
 }  // namespace cmf

@@ -107,6 +107,42 @@ class Model:
         check(lib().cmf_forward_batch(self.h, _ptr(tokens), b, pos0, _ptr(hid), _ptr(lg)))
         return hid, lg
 
+    def verify_step(self, tokens, pos0, sampler=None, q=None, uniforms=None, want_logits=False):
+        """cmf_verify_step: returns (accepted, next_token, argmax [b], logits
+        [b][vocab] or None).  q = (ids [b-1][64], probs [b-1][64], n [b-1])
+        and uniforms [b] for a sampled verify."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        b = len(tokens)
+        keep = []
+        qi = qp = qn = u = None
+        if q is not None:
+            qi = np.ascontiguousarray(q[0], dtype=np.int32)
+            qp = np.ascontiguousarray(q[1], dtype=np.float32)
+            qn = np.ascontiguousarray(q[2], dtype=np.int32)
+            assert qi.shape == (b - 1, 64) and qp.shape == (b - 1, 64)
+        if uniforms is not None:
+            u = np.zeros(b, np.float32)
+            u[: len(uniforms)] = uniforms
+        am = np.empty(b, np.int32)
+        lg = np.empty((b, self.cfg["vocab"]), np.float32) if want_logits else None
+        a, nxt = C.c_int(), C.c_int()
+        rc = check(lib().cmf_verify_step(self.h, _ptr(tokens), b, pos0, C.byref(sampler) if sampler else None,
+                                         _ptr(qi), _ptr(qp), _ptr(qn), _ptr(u), _ptr(am), _ptr(lg),
+                                         C.byref(a), C.byref(nxt)))
+        if not rc:
+            raise CmfError("verify declined (sampler config beyond the device sampler)")
+        return a.value, nxt.value, am, lg
+
+    def sparse_distribution(self, logits, sampler):
+        logits = np.ascontiguousarray(logits, dtype=np.float32)
+        ids = np.empty(64, np.int32)
+        pr = np.empty(64, np.float32)
+        n = lib().cmf_sparse_distribution(self.h, _ptr(logits), C.byref(sampler), _ptr(ids), _ptr(pr))
+        if n <= 0:
+            check(n)
+            raise CmfError("sparse_distribution declined")
+        return ids[:n].copy(), pr[:n].copy()
+
     def kv_truncate(self, n):
         check(lib().cmf_kv_truncate(self.h, n))
 

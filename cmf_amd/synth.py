@@ -160,3 +160,36 @@ def synth_model(cfg=None, seed=1, attn_dtype=DT_Q8ROW, ffn_dtype=DT_Q4T, mtp=Tru
             "norm": _norm(seed * 7 + 9, H, norm_noise),
         }
     return m
+
+
+def accept_model(cfg, seed=5, sigma=0.05, norm_noise=0.1, eh_noise=10.0, logit_scale=8.0):
+    """A synthetic model whose MTP head drafts tokens the trunk accepts.
+
+    Random-init trunks with a tied embedding fall into runs of one token
+    (the tied lm_head favours the input's own row); this head repeats its
+    input token: eh_proj = [I | noise] acts as the identity on the
+    normalised embedding half, plus int8 noise of std `eh_noise` (/127) on
+    every entry, which lets the hidden half and the MTP block move the
+    draft (at eh_noise 30 no draft survives).  logit_scale multiplies the
+    final and MTP norms, so temperature-0.8 distributions are peaked
+    enough to accept draws.  Used to put the speculative accept, commit
+    and re-warm paths under test (rounds with 0 < a < K)."""
+    sm = synth_model(cfg, seed=seed, sigma=sigma, norm_noise=norm_noise)
+    H = sm["cfg"]["hidden"]
+    noise = normal(seed * 7 + 11, H * 2 * H, eh_noise).reshape(H, 2 * H)
+    q = np.clip(np.round(noise), -127, 127).astype(np.int8)
+    q[np.arange(H), np.arange(H)] = 127
+    sm["mtp"]["eh_proj"] = tensor(DT_Q8ROW, H, 2 * H, q=q, row_scale=np.full(H, 1.0 / 127.0, np.float32))
+    sm["final_norm"] = (sm["final_norm"] * logit_scale).astype(np.float32)
+    sm["mtp"]["norm"] = (sm["mtp"]["norm"] * logit_scale).astype(np.float32)
+    return sm
+
+
+def constant_head_model(cfg, seed=5, sigma=0.05):
+    """The reference's speculative_accepts_constant_oracle model
+    (pipeline.rs:11567-11587): every lm_head row equal, so every logit ties
+    and both the trunk and the draft head pick the highest id."""
+    sm = synth_model(cfg, seed=seed, sigma=sigma)
+    V, H = sm["cfg"]["vocab"], sm["cfg"]["hidden"]
+    sm["lm_head"] = tensor(DT_Q8ROW, V, H, q=np.full((V, H), 1, np.int8), row_scale=np.full(V, 0.01, np.float32))
+    return sm

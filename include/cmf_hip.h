@@ -188,6 +188,8 @@ typedef struct {
     float repetition_penalty, min_p, presence_penalty;
 } cmf_sampler_config;
 
+/* generated: tokens emitted since cmf_decode_begin; drafted, accepted,
+ * rounds and device_ms: of this call. */
 typedef struct {
     int generated, drafted, accepted, rounds;
     double device_ms;
@@ -215,6 +217,39 @@ int cmf_decode_tokens(cmf_model m, int32_t* out, int cap);
  * [b][hidden] and logits [b][vocab] (either may be NULL). */
 int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden,
                       float* logits);
+/* Largest sparse distribution the device sampler holds (its top_k bound). */
+#define CMF_SPARSE_K_MAX 64
+
+/* One verify step of graph_spec_step with the caller's drafts: the
+ * forward_batch_graph + SpecTail verify (gpu.rs:1455-1497) and the
+ * acceptance, commit and rollback that follow it (pipeline.rs:3885-4176,
+ * kv_cache.rs:883).  tokens [b] = [t_next, d_0 .. d_{b-2}] (2 <= b <= 9) at
+ * positions pos0 .. (pos0 >= 1; the decode state's tip hidden is the trunk
+ * output at pos0 - 1: after cmf_prefill, cmf_forward_batch, a decode round
+ * or a previous verify step).
+ *   greedy (sc NULL or temperature < 1e-6): a = the longest prefix with
+ *     argmax(row i) == d_i (ties to the highest id); *next_token =
+ *     argmax(row a);
+ *   sampled: spec_accept_or_correct_sparse (sampler.rs:683-711) of each
+ *     draft against the caller's draft distributions q_ids / q_probs
+ *     [b-1][CMF_SPARSE_K_MAX] (ids ascending, q_n[j] entries) and the
+ *     row's sparse distribution p; the uniforms [b] are consumed in the
+ *     reference's order (one per tested draft, one for the correction or
+ *     for the draw from row a); *next_token = the correction or that draw.
+ * Commit: trunk KV holds positions [0, pos0 + a + 1), the tip hidden is row
+ * a, and with an MTP head its cache holds the pairs (tip, t_next) at
+ * pos0 - 1 and (row j, d_j) at pos0 + j for j < a (rows past that are
+ * scratch for the next round).  argmax_out [b] (picks of every row) and
+ * logits_out [b][vocab] may be NULL. */
+int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const cmf_sampler_config* sc,
+                    const int32_t* q_ids, const float* q_probs, const int32_t* q_n, const float* uniforms,
+                    int32_t* argmax_out, float* logits_out, int32_t* accepted, int32_t* next_token);
+/* sparse_distribution_into (sampler.rs:440-514) of one logits row [vocab]
+ * (host) on the device sampler: ids ascending and their probabilities
+ * (capacity CMF_SPARSE_K_MAX); returns the count (>= 1: a fully filtered
+ * row gives its argmax with probability 1, as the decode loop does). */
+int cmf_sparse_distribution(cmf_model m, const float* logits, const cmf_sampler_config* sc, int32_t* ids,
+                            float* probs);
 /* KV rollback (kv_cache.rs:883 truncate_last / gpu.rs:1514 graph_kv_reset):
  * the decode position moves back by n. */
 int cmf_kv_truncate(cmf_model m, int n);

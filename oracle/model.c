@@ -255,6 +255,59 @@ static uint32_t choose(const float* lg, int V, const or_sampler_cfg* c, const ui
 
 static void truncate_kv(or_kv* kv, int n) { kv->len -= n < kv->len ? n : kv->len; }
 
+/* The verify half of graph_spec_step (pipeline.rs:3768-4176) given the
+ * drafts: the b = K + 1 rows [t_next, d_0 .. d_{K-1}] at next_pos .. as
+ * ordinary per-position forwards (vlog / hid: [b][V] / [b][H]), acceptance
+ * (pipeline.rs:3887-4001), the trunk rows past the accepted prefix dropped
+ * (truncate_last, kv_cache.rs:883) and the accepted pairs warmed into the
+ * MTP cache (pipeline.rs:4120-4176).  qs: the draft distributions
+ * (sampling only); all/nall: the committed stream the sampler reads.
+ * Returns a; *forced = the correction token or -1. */
+static int verify_core(const or_model* m, or_state* s, int next_pos, uint32_t t_next, const uint32_t* drafts,
+                       int K, const or_sampler_cfg* sc, const sparse_t* qs, or_rng* rng, uint32_t* all,
+                       int nall, float* vlog, float* hid, int* forced) {
+    const or_cfg* c = &m->cfg;
+    int H = c->hidden, V = c->vocab, b = K + 1;
+    sparse_t* ps = (sparse_t*)malloc(sizeof(sparse_t));
+    for (int i = 0; i < b; i++) {
+        uint32_t t = i == 0 ? t_next : drafts[i - 1];
+        float* h = hid + (size_t)i * H;
+        or_embed(m, t, h);
+        or_forward(m, s, h, next_pos + i);
+        or_logits(m, h, vlog + (size_t)i * V);
+    }
+    int a = 0;
+    *forced = -1;
+    if (is_sampling(sc)) {
+        int base = nall;
+        while (a < K) {
+            const float* row = vlog + (size_t)a * V;
+            ps->n = or_sparse_distribution(row, V, sc, all, nall, ps->ids, ps->p);
+            if (ps->n == 0) {
+                ps->ids[0] = or_argmax(row, V);
+                ps->p[0] = 1.0f;
+                ps->n = 1;
+            }
+            int64_t r = or_spec_accept_sparse(ps->ids, ps->p, ps->n, qs[a].ids, qs[a].p, qs[a].n, drafts[a], rng);
+            if (r < 0) {
+                all[nall++] = drafts[a];
+                a++;
+            } else {
+                *forced = (int)r;
+                break;
+            }
+        }
+        nall = base;
+    } else {
+        while (a < K && or_argmax(vlog + (size_t)a * V, V) == drafts[a]) a++;
+    }
+    for (int li = 0; li < c->n_layers; li++) truncate_kv(&s->trunk[li], K - a);
+    if (m->has_mtp)
+        for (int j = 0; j < a; j++) or_mtp_step(m, s, hid + (size_t)j * H, drafts[j], next_pos + j, NULL, NULL);
+    free(ps);
+    return a;
+}
+
 int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const uint32_t* ids0,
               int nids, int max_tokens, const or_gen_cfg* g, uint64_t* rng_state, uint32_t* out,
               or_gen_stats* st) {
@@ -270,7 +323,6 @@ int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const
     float* hx = (float*)malloc(sizeof(float) * (size_t)H);
     float* hj = (float*)malloc(sizeof(float) * (size_t)H);
     sparse_t* qs = (sparse_t*)malloc(sizeof(sparse_t) * (size_t)(K > 0 ? K : 1));
-    sparse_t ps;
     int have_logits = 0, forced = -1;
     memset(st, 0, sizeof(*st));
     while (generated < max_tokens) {
@@ -287,7 +339,7 @@ int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const
         out[generated++] = t_next;
         if (generated >= max_tokens) break;
         if (g->spec && m->has_mtp && generated + 1 < max_tokens && next_pos > 0) {
-            /* ---- graph_spec_step ---- */
+            /* ---- graph_spec_step: the draft chain ---- */
             st->rounds++;
             uint32_t drafts[16];
             int base = nall;
@@ -302,46 +354,11 @@ int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const
             }
             nall = base;
             st->drafted += K;
-            /* verify: rows [t_next, d_0 .. d_{K-1}] at next_pos .. */
-            int b = K + 1;
-            for (int i = 0; i < b; i++) {
-                uint32_t t = i == 0 ? t_next : drafts[i - 1];
-                float* h = hid + (size_t)i * H;
-                or_embed(m, t, h);
-                or_forward(m, s, h, next_pos + i);
-                or_logits(m, h, vlog + (size_t)i * V);
-            }
-            /* acceptance, pipeline.rs:3887-4001 */
-            int a = 0;
-            if (is_sampling(&g->sc)) {
-                while (a < K) {
-                    const float* row = vlog + (size_t)a * V;
-                    ps.n = or_sparse_distribution(row, V, &g->sc, all, nall, ps.ids, ps.p);
-                    if (ps.n == 0) {
-                        ps.ids[0] = or_argmax(row, V);
-                        ps.p[0] = 1.0f;
-                        ps.n = 1;
-                    }
-                    int64_t r = or_spec_accept_sparse(ps.ids, ps.p, ps.n, qs[a].ids, qs[a].p, qs[a].n,
-                                                      drafts[a], &rng);
-                    if (r < 0) {
-                        all[nall++] = drafts[a];
-                        a++;
-                    } else {
-                        forced = (int)r;
-                        break;
-                    }
-                }
-                nall = base;
-            } else {
-                while (a < K && or_argmax(vlog + (size_t)a * V, V) == drafts[a]) a++;
-            }
-            st->accepted += a;
-            /* commit: trunk rows past a are dropped */
-            for (int li = 0; li < c->n_layers; li++) truncate_kv(&s->trunk[li], K - a);
-            /* MTP: keep the first draft row, re-warm the accepted pairs */
+            /* MTP cache: keep the first draft row (its inputs were real) */
             truncate_kv(&s->mtp, K - 1);
-            for (int j = 0; j < a; j++) or_mtp_step(m, s, hid + (size_t)j * H, drafts[j], next_pos + j, NULL, NULL);
+            int a = verify_core(m, s, next_pos, t_next, drafts, K, &g->sc, qs, &rng, all, nall, vlog, hid, &forced);
+            st->accepted += a;
+            st->hist[a]++;
             if (forced < 0) {
                 memcpy(logits, vlog + (size_t)a * V, sizeof(float) * (size_t)V);
                 have_logits = 1;
@@ -368,6 +385,48 @@ int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const
     free(hj);
     free(qs);
     return generated;
+}
+
+int or_verify_step(const or_model* m, or_state* s, float* hidden, int pos0, const uint32_t* tokens, int b,
+                   const or_sampler_cfg* sc, const uint32_t* q_ids, const float* q_p, const int* q_n,
+                   int q_stride, or_rng* rng, const uint32_t* past, int npast, int warm_tip, float* logits,
+                   uint32_t* argmax, uint32_t* next) {
+    const or_cfg* c = &m->cfg;
+    int H = c->hidden, V = c->vocab, K = b - 1;
+    float* vlog = (float*)malloc(sizeof(float) * (size_t)V * (size_t)b);
+    float* hid = (float*)malloc(sizeof(float) * (size_t)H * (size_t)b);
+    sparse_t* qs = (sparse_t*)calloc((size_t)(K > 0 ? K : 1), sizeof(sparse_t));
+    uint32_t* all = (uint32_t*)malloc(sizeof(uint32_t) * (size_t)(npast + b + 1));
+    if (npast > 0) memcpy(all, past, sizeof(uint32_t) * (size_t)npast);
+    if (is_sampling(sc))
+        for (int j = 0; j < K; j++) {
+            qs[j].n = q_n[j];
+            for (int i = 0; i < q_n[j]; i++) {
+                qs[j].ids[i] = q_ids[(size_t)j * q_stride + i];
+                qs[j].p[i] = q_p[(size_t)j * q_stride + i];
+            }
+        }
+    /* the MTP row of the first draft: (tip hidden, t_next) at pos0 - 1 */
+    if (warm_tip && m->has_mtp && pos0 > 0) or_mtp_step(m, s, hidden, tokens[0], pos0 - 1, NULL, NULL);
+    int forced = -1;
+    int a = verify_core(m, s, pos0, tokens[0], tokens + 1, K, sc, qs, rng, all, npast, vlog, hid, &forced);
+    if (argmax)
+        for (int i = 0; i < b; i++) argmax[i] = or_argmax(vlog + (size_t)i * V, V);
+    if (logits) memcpy(logits, vlog, sizeof(float) * (size_t)V * (size_t)b);
+    if (forced >= 0) {
+        *next = (uint32_t)forced;
+    } else {
+        /* the loop top picks from row a over the stream with the accepted drafts */
+        int n = npast;
+        for (int j = 0; j < a; j++) all[n++] = tokens[1 + j];
+        *next = or_sample(vlog + (size_t)a * V, V, sc, all, n, rng);
+    }
+    memcpy(hidden, hid + (size_t)a * H, sizeof(float) * (size_t)H);
+    free(vlog);
+    free(hid);
+    free(qs);
+    free(all);
+    return a;
 }
 
 int or_generate(const or_model* m, or_state* s, const uint32_t* prompt, int np, int max_tokens,

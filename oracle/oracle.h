@@ -88,7 +88,14 @@ void or_rms_norm(const float* x, const float* w, int n, double eps, float* out);
 void or_rope_inv_freq(int head_dim, float theta, float* out);
 
 /* ---- sampler.rs ------------------------------------------------------- */
-typedef struct { uint64_t state; } or_rng;
+/* SplitMix64 state.  seq != NULL replaces the stream's uniforms: next_f32
+ * returns seq[used++] (the caller's shared uniforms of a verify step) and
+ * falls back to the generator once nseq are used. */
+typedef struct {
+    uint64_t state;
+    const float* seq;
+    int nseq, used;
+} or_rng;
 uint64_t or_rng_next_u64(or_rng* r);
 float or_rng_next_f32(or_rng* r);
 uint32_t or_argmax(const float* v, int n);
@@ -172,6 +179,7 @@ typedef struct {
 
 typedef struct {
     int drafted, accepted, rounds;
+    int hist[17]; /* rounds by accepted count a = 0..16 */
 } or_gen_stats;
 
 /* generate_from_ids restated (pipeline.rs:1913-2980 with the decode loop at
@@ -187,6 +195,23 @@ int or_generate(const or_model* m, or_state* s, const uint32_t* prompt, int np, 
 int or_decode(const or_model* m, or_state* s, float* hidden, int next_pos, const uint32_t* ids,
               int nids, int max_tokens, const or_gen_cfg* g, uint64_t* rng_state, uint32_t* out,
               or_gen_stats* st);
+
+/* One verify step of graph_spec_step with caller drafts (pipeline.rs:
+ * 3768-4176): rows tokens[0..b) = [t_next, d_0 .. d_{b-2}] at positions
+ * pos0.. through the trunk (KV appended), acceptance (greedy argmax
+ * equality, or spec_accept_or_correct_sparse against the caller's draft
+ * distributions q_ids/q_p/q_n [b-1][q_stride] with rng's uniforms), the
+ * trunk KV cut to pos0 + a + 1 and, with an MTP head, the MTP rows
+ * (hidden, t_next) at pos0 - 1 (warm_tip = 1: the caller drafted
+ * elsewhere; 0: the draft chain wrote it) and the accepted pairs.
+ * hidden: in = trunk output at pos0 - 1, out = row a.  past/npast: the
+ * committed stream (t_next included).  logits (b*vocab) and argmax (b)
+ * may be NULL.  *next = the token after the accepted ones (correction,
+ * or the pick of row a).  Returns a. */
+int or_verify_step(const or_model* m, or_state* s, float* hidden, int pos0, const uint32_t* tokens, int b,
+                   const or_sampler_cfg* sc, const uint32_t* q_ids, const float* q_p, const int* q_n,
+                   int q_stride, or_rng* rng, const uint32_t* past, int npast, int warm_tip, float* logits,
+                   uint32_t* argmax, uint32_t* next);
 
 /* MoE routing + expert FFN for one token (pipeline.rs:10780-10841,
  * 10868-11045). experts: 3*ne tensors (gate, up, down per expert). */

@@ -60,8 +60,13 @@ class GenCfg(C.Structure):
     _fields_ = [("spec", C.c_int), ("k", C.c_int), ("sc", SamplerCfg), ("seed", C.c_uint64)]
 
 
+class Rng(C.Structure):
+    """or_rng: SplitMix64 state; seq/nseq replace its uniforms in order."""
+    _fields_ = [("state", C.c_uint64), ("seq", C.c_void_p), ("nseq", C.c_int), ("used", C.c_int)]
+
+
 class GenStats(C.Structure):
-    _fields_ = [("drafted", C.c_int), ("accepted", C.c_int), ("rounds", C.c_int)]
+    _fields_ = [("drafted", C.c_int), ("accepted", C.c_int), ("rounds", C.c_int), ("hist", C.c_int * 17)]
 
 
 _lib = None
@@ -106,6 +111,9 @@ def lib():
                                       C.POINTER(GenCfg), P, C.POINTER(GenStats)]),
             "or_decode": (C.c_int, [C.POINTER(Model), C.POINTER(State), P, C.c_int, P, C.c_int, C.c_int,
                                     C.POINTER(GenCfg), P, P, C.POINTER(GenStats)]),
+            "or_verify_step": (C.c_int, [C.POINTER(Model), C.POINTER(State), P, C.c_int, P, C.c_int,
+                                         C.POINTER(SamplerCfg), P, P, P, C.c_int, C.POINTER(Rng), P, C.c_int,
+                                         C.c_int, P, P, P]),
             "or_moe_route": (C.c_int, [P, C.c_int, C.c_int, C.c_int, C.c_float, P, P]),
             "or_moe_ffn": (None, [P, C.c_int, C.c_int, C.c_int, C.c_float, P, P, C.c_int, P, C.c_int]),
         }
@@ -165,6 +173,7 @@ class OracleModel:
     def __init__(self, sm, threads=8):
         c = sm["cfg"]
         self.c = c
+        self.sm = sm
         self.keep = []
         layers = (Layer * c["n_layers"])(*[_layer(l, self.keep) for l in sm["layers"]])
         self.keep.append(layers)
@@ -230,6 +239,51 @@ class OracleModel:
         n = lib().or_decode(C.byref(self.m), C.byref(self.st), _p(hidden), next_pos, _p(ids), len(ids), max_tokens,
                             C.byref(g), C.byref(rs), _p(out), C.byref(st))
         return out[:n].astype(np.int32), st
+
+    def verify_step(self, hidden, pos0, tokens, sampler=None, q=None, uniforms=None, seed=0, past=None,
+                    warm_tip=True):
+        """or_verify_step: returns (a, next, hidden row a, argmax [b], logits
+        [b][vocab]).  q = (ids [b-1][S], probs [b-1][S], n [b-1]) for
+        sampling; uniforms replace the seeded stream's draws in order."""
+        V = self.c["vocab"]
+        tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+        b = len(tokens)
+        hidden = np.ascontiguousarray(hidden, dtype=np.float32).copy()
+        sc = sampler or SamplerCfg(0.0, 0.9, 40, 1.0, 0.05, 0.0)
+        keep = []
+        qi = qp = qn = None
+        stride = 0
+        if q is not None:
+            qi = np.ascontiguousarray(q[0], dtype=np.uint32)
+            qp = np.ascontiguousarray(q[1], dtype=np.float32)
+            qn = np.ascontiguousarray(q[2], dtype=np.int32)
+            stride = qi.shape[1]
+        u = None if uniforms is None else np.ascontiguousarray(uniforms, dtype=np.float32)
+        rng = Rng(seed, _p(u), 0 if u is None else len(u), 0)
+        past = np.ascontiguousarray(tokens[:1] if past is None else past, dtype=np.uint32)
+        am = np.empty(b, np.uint32)
+        lg = np.empty((b, V), np.float32)
+        nxt = C.c_uint32(0)
+        a = lib().or_verify_step(C.byref(self.m), C.byref(self.st), _p(hidden), pos0, _p(tokens), b, C.byref(sc),
+                                 _p(qi), _p(qp), _p(qn), stride, C.byref(rng), _p(past), len(past),
+                                 1 if warm_tip else 0, _p(lg), _p(am), C.byref(nxt))
+        self.rng_used = rng.used
+        return a, int(nxt.value), hidden, am.astype(np.int32), lg
+
+    def kv(self, li):
+        """(k, v) rows [0, len) of layer li (-1: the MTP block), [n_kv][len][hd]."""
+        i = li if li >= 0 else self.c["n_layers"]
+        n = self.kvs[li].len if li >= 0 else self.st.mtp.len
+        return self.kk[i][:, :n].copy(), self.vv[i][:, :n].copy()
+
+    def prefill(self, prompt):
+        """prompt positions through the trunk + MTP warm pairs; returns the tip hidden"""
+        h = None
+        for p, t in enumerate(prompt):
+            h = self.forward(int(t), p)
+            if "mtp" in self.sm and p + 1 < len(prompt):
+                lib().or_mtp_step(C.byref(self.m), C.byref(self.st), _p(h), int(prompt[p + 1]), p, None, None)
+        return h
 
     def forward(self, tok, pos):
         h = np.empty(self.c["hidden"], np.float32)

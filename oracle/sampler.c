@@ -18,7 +18,10 @@ uint64_t or_rng_next_u64(or_rng* r) {
     return z ^ (z >> 31);
 }
 
-float or_rng_next_f32(or_rng* r) { return (float)(or_rng_next_u64(r) >> 40) / (float)(1u << 24); }
+float or_rng_next_f32(or_rng* r) {
+    if (r->seq && r->used < r->nseq) return r->seq[r->used++];
+    return (float)(or_rng_next_u64(r) >> 40) / (float)(1u << 24);
+}
 
 /* sampler.rs:832-867 — four running maxima, ties to the highest index. */
 uint32_t or_argmax(const float* v, int n) {

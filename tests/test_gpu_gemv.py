@@ -51,6 +51,13 @@ def test_q4t_config2(gpu, shape, m):
     _check(gpu, t, _x(32 + m, m, shape[1]))
 
 
+def test_q8_config5_projection(gpu):
+    """BASELINE config 5's q8 4096x2048 attention projection at M=5"""
+    from cmf_amd import synth
+    t = synth.q8_uniform(5003, 4096, 2048)
+    _check(gpu, t, _x(5004, 5, 2048))
+
+
 @pytest.mark.parametrize("shape", [(12288, 4096), (4096, 12288)])
 def test_q4tp_config3(gpu, shape):
     from cmf_amd import synth

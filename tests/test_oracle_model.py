@@ -2,6 +2,8 @@
 forward of the same Qwen3-arch block (dequantized weights, plain softmax
 attention), and greedy speculative decode == vanilla greedy
 (pipeline.rs:11543-11564)."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -114,3 +116,193 @@ def test_spec_sampling_is_seed_deterministic(tiny):
     a, sa = orc.OracleModel(tiny, threads=2).generate(prompt, 16, spec=True, k=3, sampler=sc, seed=7)
     b, sb = orc.OracleModel(tiny, threads=4).generate(prompt, 16, spec=True, k=3, sampler=sc, seed=7)
     assert a.tolist() == b.tolist() and sa.accepted == sb.accepted
+
+
+# ---------------------------------------------------------------------------
+# The accept / commit / re-warm branch of graph_spec_step, pinned on models
+# whose drafts get accepted.
+# ---------------------------------------------------------------------------
+ACC_PROMPT_SEED = 23  # greedy K=4 rounds accept 0, 1, 3 and 4 drafts on TINY / SMALL
+
+
+@pytest.fixture(scope="module")
+def acc():
+    from cmf_amd import synth
+    return synth.accept_model(TINY)
+
+
+def _reference_state(sm, toks):
+    """trunk KV of positions [0, n) and MTP KV rows [0, n-1) built by plain
+    forwards and (h_p, t_{p+1}) warms — what every committed round must
+    leave (pipeline.rs:2275-2318 prefill warm, 4120-4176 re-warm)"""
+    o = orc.OracleModel(sm, threads=2)
+    o.prefill(np.asarray(toks))
+    return o
+
+
+def _assert_state_equal(o, ref, n_layers):
+    for li in list(range(n_layers)) + [-1]:
+        k, v = o.kv(li)
+        rk, rv = ref.kv(li)
+        if li < 0:  # plain steps after the last round do not warm the head
+            assert k.shape[1] <= rk.shape[1]
+            rk, rv = rk[:, :k.shape[1]], rv[:, :k.shape[1]]
+        assert k.shape == rk.shape, (li, k.shape, rk.shape)
+        assert np.array_equal(k, rk) and np.array_equal(v, rv), li
+
+
+def test_spec_accepts_constant_oracle():
+    """pipeline.rs:11567-11587: constant lm_head -> every logit ties -> the
+    trunk and the draft head both pick the highest id: 100% acceptance and
+    one repeated token"""
+    from cmf_amd import synth
+    sm = synth.constant_head_model(TINY)
+    prompt = synth.ids(4, 4, TINY["vocab"])
+    toks, st = orc.OracleModel(sm, threads=2).generate(prompt, 10, spec=True, k=4)
+    assert st.drafted > 0
+    assert st.accepted == st.drafted
+    assert st.hist[4] == st.rounds
+    assert set(toks.tolist()) == {TINY["vocab"] - 1}
+
+
+@pytest.mark.parametrize("k", [1, 4])
+def test_spec_greedy_equals_vanilla_with_acceptance(acc, k):
+    """speculative_equals_vanilla_greedy (pipeline.rs:11543-11564) with the
+    evidence the reference's test asks for: drafts are accepted, and for
+    K = 4 rounds end at 0 < a < K (partial commits)"""
+    from cmf_amd import synth
+    prompt = synth.ids(ACC_PROMPT_SEED, 20, TINY["vocab"])
+    o = orc.OracleModel(acc, threads=2)
+    a, st = o.generate(prompt, 40, spec=True, k=k)
+    b, _ = orc.OracleModel(acc, threads=2).generate(prompt, 40, spec=False)
+    assert a[:40].tolist() == b[:40].tolist()
+    assert st.accepted > 0
+    if k == 4:
+        assert sum(st.hist[1:4]) > 0, list(st.hist)
+        assert st.hist[0] > 0 and st.hist[4] > 0
+    # committed state == plain forwards + (h_p, t_{p+1}) warms
+    n = o.kvs[0].len
+    assert n - 1 - k <= o.st.mtp.len <= n - 1
+    ref = _reference_state(acc, np.concatenate([prompt, a])[:n])
+    _assert_state_equal(o, ref, TINY["n_layers"])
+
+
+def test_spec_sampling_accepts_and_commits(acc):
+    """temperature 0.8: drafts are accepted (some rounds partially), the run
+    is seed-deterministic and the committed state is the plain-forward one"""
+    from cmf_amd import synth
+    prompt = synth.ids(19, 20, TINY["vocab"])
+    sc = orc.SamplerCfg(0.8, 0.9, 40, 1.0, 0.05, 0.0)
+    o = orc.OracleModel(acc, threads=2)
+    a, st = o.generate(prompt, 40, spec=True, k=4, sampler=sc, seed=1234)
+    b, st2 = orc.OracleModel(acc, threads=4).generate(prompt, 40, spec=True, k=4, sampler=sc, seed=1234)
+    assert a.tolist() == b.tolist() and st.accepted == st2.accepted
+    assert st.accepted > 0 and sum(st.hist[1:4]) > 0, list(st.hist)
+    n = o.kvs[0].len
+    ref = _reference_state(acc, np.concatenate([prompt, a])[:n])
+    _assert_state_equal(o, ref, TINY["n_layers"])
+
+
+def test_spec_accept_hand_computed_toy():
+    """spec_accept_or_correct_sparse (sampler.rs:683-711) on a 3-token toy,
+    by hand, over SplitMix64 seed 0's published uniforms 0.8833108,
+    0.43152797, 0.026433766:
+      p = {0: .5, 1: .3, 2: .2}, q = {0: .2, 1: .8}
+      d = 0: r = .8833; r*q_d = .1767 < p_d = .5       -> accept
+      d = 1: r = .4315; r*q_d = .3452 >= p_d = .3      -> reject;
+             residual max(0, p - q) = {0: .3, 2: .2} -> {0: .6, 2: .4};
+             r = .0264 < .6                            -> correction 0
+    and with caller uniforms [.9, .7]: d = 1 rejected, .7 >= .6 -> 2"""
+    L = orc.lib()
+    pid, pp = np.array([0, 1, 2], np.uint32), np.array([0.5, 0.3, 0.2], np.float32)
+    qid, qp = np.array([0, 1], np.uint32), np.array([0.2, 0.8], np.float32)
+    P = lambda a: a.ctypes.data_as(C.c_void_p)
+    r = orc.Rng(0)
+    assert L.or_spec_accept_sparse(P(pid), P(pp), 3, P(qid), P(qp), 2, 0, C.byref(r)) == -1
+    assert L.or_spec_accept_sparse(P(pid), P(pp), 3, P(qid), P(qp), 2, 1, C.byref(r)) == 0
+    u = np.array([0.9, 0.7], np.float32)
+    r = orc.Rng(0, P(u), 2, 0)
+    assert L.or_spec_accept_sparse(P(pid), P(pp), 3, P(qid), P(qp), 2, 1, C.byref(r)) == 2
+    assert r.used == 2
+    # three uniforms of seed 0 consumed by the first two calls
+    r = orc.Rng(0)
+    L.or_spec_accept_sparse(P(pid), P(pp), 3, P(qid), P(qp), 2, 0, C.byref(r))
+    L.or_spec_accept_sparse(P(pid), P(pp), 3, P(qid), P(qp), 2, 1, C.byref(r))
+    r0 = orc.Rng(0)
+    for _ in range(3):
+        L.or_rng_next_u64(C.byref(r0))
+    assert r.state == r0.state
+
+
+def _vanilla(sm, prompt, n):
+    toks, _ = orc.OracleModel(sm, threads=2).generate(prompt, n, spec=False)
+    return toks
+
+
+@pytest.mark.parametrize("a_want", [0, 1, 2, 3, 4])
+def test_verify_step_greedy_chosen_drafts(acc, a_want):
+    """or_verify_step with drafts = the next a_want vanilla tokens and then a
+    wrong one: a == a_want, the next token and the row picks are the vanilla
+    ones, and the committed trunk / MTP caches equal plain forwards"""
+    from cmf_amd import synth
+    K = 4
+    prompt = synth.ids(7, 12, TINY["vocab"])
+    s = _vanilla(acc, prompt, K + 2)  # s[0] = t_next
+    toks = [int(t) for t in s[:a_want + 1]]
+    while len(toks) < K + 1:
+        toks.append((int(s[len(toks)]) + 1) % TINY["vocab"])
+    o = orc.OracleModel(acc, threads=2)
+    tip = o.prefill(prompt)
+    a, nxt, h, am, lg = o.verify_step(tip, len(prompt), toks, past=np.concatenate([prompt, s[:1]]))
+    assert a == a_want
+    assert nxt == int(s[a + 1])
+    assert am[:a + 1].tolist() == [int(t) for t in s[1:a + 2]]
+    assert o.kvs[0].len == len(prompt) + a + 1 and o.st.mtp.len == len(prompt) + a
+    ref = _reference_state(acc, np.concatenate([prompt, s[:a + 1]]))
+    _assert_state_equal(o, ref, TINY["n_layers"])
+    # the hidden row a is the plain forward's tip
+    ref2 = orc.OracleModel(acc, threads=2)
+    hp = ref2.prefill(np.concatenate([prompt, s[:a + 1]]))
+    assert np.array_equal(h, hp)
+
+
+def test_verify_step_sampled_shared_uniforms(acc):
+    """the sampled verify under caller uniforms: draft i = the vanilla
+    argmax token with q = {d: 1}; uniforms 0 accept every draft inside
+    supp(p); a draft outside the top-k is rejected (p_d = 0) and the
+    correction is p's inverse CDF at the next uniform"""
+    from cmf_amd import synth
+    K = 4
+    V = TINY["vocab"]
+    prompt = synth.ids(7, 12, V)
+    s = _vanilla(acc, prompt, K + 2)
+    sc = orc.SamplerCfg(0.8, 0.9, 40, 1.0, 0.05, 0.0)
+    o0 = orc.OracleModel(acc, threads=2)
+    tip0 = o0.prefill(prompt)
+    _, _, _, _, lg = o0.verify_step(tip0, len(prompt), s[:K + 1], past=np.concatenate([prompt, s[:1]]))
+    # a token outside every row's top-40
+    far = int(np.argmin(lg[2]))
+    toks = [int(s[0]), int(s[1]), int(s[2]), far, int(s[4])]
+    qi = np.zeros((K, 64), np.uint32)
+    qp = np.zeros((K, 64), np.float32)
+    qi[:, 0] = toks[1:]
+    qp[:, 0] = 1.0
+    qn = np.ones(K, np.int32)
+    u_c = 0.37
+    o = orc.OracleModel(acc, threads=2)
+    tip = o.prefill(prompt)
+    a, nxt, h, am, lg2 = o.verify_step(tip, len(prompt), toks, sampler=sc, q=(qi, qp, qn),
+                                       uniforms=[0.0, 0.0, 0.0, u_c], past=np.concatenate([prompt, s[:1]]))
+    assert a == 2 and o.rng_used == 4
+    # p of row 2 (the stream holds the accepted drafts) at u_c
+    ids = np.empty(4 * 256 + 64, np.uint32)
+    pr = np.empty(4 * 256 + 64, np.float32)
+    past = np.concatenate([prompt, s[:3]]).astype(np.uint32)
+    P = lambda x: x.ctypes.data_as(C.c_void_p)
+    m = orc.lib().or_sparse_distribution(P(np.ascontiguousarray(lg2[2])), V, C.byref(sc), P(past), len(past),
+                                         P(ids), P(pr))
+    assert far not in ids[:m].tolist()
+    cdf = np.cumsum(pr[:m].astype(np.float32), dtype=np.float32)
+    assert nxt == int(ids[int(np.argmax(u_c < cdf))])
+    ref = _reference_state(acc, np.concatenate([prompt, s[:3]]))
+    _assert_state_equal(o, ref, TINY["n_layers"])

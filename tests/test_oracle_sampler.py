@@ -14,8 +14,7 @@ def _p(a):
     return a.ctypes.data_as(C.c_void_p)
 
 
-class Rng(C.Structure):
-    _fields_ = [("state", C.c_uint64)]
+Rng = orc.Rng
 
 
 def test_splitmix64_published_outputs():
