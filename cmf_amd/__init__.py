@@ -108,6 +108,7 @@ SIGNATURES = {
     "cmf_prep_bytes": (_S, [_P]),
     "cmf_prep_dev": (_I, [_P, _P, _I, _I, _P, _P]),
     "cmf_gemv_prepared": (_I, [_P, _P, _P, _I, _P, _I, _I]),
+    "cmf_gemv_dev_noalloc": (_I, [_P, _P, _I, _I, _P, _I]),
     "cmf_time_gemv": (_I, [C.POINTER(_P), _I, _P, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_copy": (_I, [_S, _I, _I, C.POINTER(_F)]),
     "cmf_time_attention": (_I, [_P, _I, _I, _I, _I, C.POINTER(_F)]),

@@ -22,6 +22,19 @@ int fail(const std::string& m) {
     return CMF_ERR;
 }
 
+// Workspace of cmf_gemv_dev_noalloc: the prepared operand planes of one
+// GEMV (prep_bytes of a weight with cols <= 16384: q4 128 KiB-tile groups
+// 1 081 344 B, q8 786 432 B) followed by the 16 per-row operand scales.
+// Each device the library initialises holds its own copy until the process
+// ends; calls on one device share it (the last call's contents stay).
+constexpr size_t NOALLOC_PLANES_MAX = 1310720;
+constexpr size_t NOALLOC_BYTES = NOALLOC_PLANES_MAX + 256;
+constexpr int NOALLOC_MAX_DEV = 64;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_BYTES];
+// device address of `scratch` per device (the host-side name is a stand-in,
+// never a device address)
+static uint8_t* g_scratch_ptr[NOALLOC_MAX_DEV] = {};
+
 static std::mutex g_mu;
 static bool g_init = false;
 static int g_dev = 0;
@@ -284,6 +297,14 @@ int cmf_init(int dev) {
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return fail(std::string("libcmfhip is built for gfx950, device is ") + p.gcnArchName);
     CMF_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
+    if (dev < NOALLOC_MAX_DEV) {
+        // this device's copy of the no-allocation workspace (device current)
+        const hipError_t e = hipGetSymbolAddress((void**)&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            g_scratch_ptr[dev] = nullptr;
+            return fail(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        }
+    }
     g_dev = dev;
     g_init = true;
     return CMF_OK;
@@ -512,6 +533,28 @@ int cmf_prep_dev(cmf_weight w, const float* d_x, int ldx, int b, void* d_planes,
     if (ensure_init() != CMF_OK) return CMF_ERR;
     if (!w || b < 1 || b > MAXB) return fail("prep_dev: bad arguments");
     launch_prep(w->w, d_x, ldx, b, (uint8_t*)d_planes, d_xs, stream());
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
+}
+
+int cmf_gemv_dev_noalloc(cmf_weight w, const float* d_x, int ldx, int b, float* d_y, int ldy) {
+    if (!g_init) return fail("gemv_dev_noalloc: call cmf_init first");
+    if (!w || !d_x || !d_y) return fail("gemv_dev_noalloc: null argument");
+    if (b < 1 || b > MAXB) return fail("gemv_dev_noalloc: batch must be 1..16");
+    if (ldx < w->w.cols || ldy < w->w.rows) return fail("gemv_dev_noalloc: ldx < cols or ldy < rows");
+    const size_t need = prep_bytes(w->w);
+    if (need > NOALLOC_PLANES_MAX)
+        return fail("gemv_dev_noalloc: the operand of this weight needs " + std::to_string(need) +
+                    " B of workspace, more than the " + std::to_string(NOALLOC_PLANES_MAX) +
+                    " B the library holds (cols <= 16384)");
+    uint8_t* base = g_dev < NOALLOC_MAX_DEV ? g_scratch_ptr[g_dev] : nullptr;
+    if (!base) return fail("gemv_dev_noalloc: no workspace on this device");
+    float* xs = (float*)(base + NOALLOC_PLANES_MAX);
+    hipStream_t st = stream();
+    int rc = launch_prep(w->w, d_x, ldx, b, base, xs, st);
+    if (rc != CMF_OK) return rc;
+    rc = launch_gemv(w->w, base, xs, d_y, ldy, b, 0, w->w.rows, st);
+    if (rc != CMF_OK) return rc;
     CMF_HIP(hipGetLastError());
     return CMF_OK;
 }

@@ -90,6 +90,16 @@ int cmf_prep_dev(cmf_weight w, const float* d_x, int ldx, int b, void* d_planes,
  * ks = waves per workgroup splitting K (0 = heuristic). */
 int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int b, float* d_y,
                       int ldy, int ks);
+/* y[b][ldy] = w * x[b][ldx] on device pointers with no allocation: the
+ * operand is prepared into a workspace the library holds in a static device
+ * array (1 310 976 B per device, set up by cmf_init), then the GEMV of
+ * cmf_gemv_prepared runs on it; the same kernels and results as
+ * cmf_prep_dev + cmf_gemv_prepared with a caller workspace.  Weights whose
+ * operand needs more (cols > 16384) are rejected with an error.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops).  Requires
+ * cmf_init; calls that overlap on one device race on the workspace. */
+int cmf_gemv_dev_noalloc(cmf_weight w, const float* d_x, int ldx, int b, float* d_y, int ldy);
 /* Average device time (ms) of `iters` back-to-back launches of the GEMV
  * on ws[i % nw] (rotating copies defeat the 256 MB last-level cache),
  * measured with HIP events on the library stream. */
