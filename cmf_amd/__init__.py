@@ -63,6 +63,21 @@ class SamplerConfig(C.Structure):
         super().__init__(temperature, top_p, top_k, repetition_penalty, min_p, presence_penalty)
 
 
+class MoeJob(C.Structure):
+    """cmf_moe_job: one caller-routed expert trio (MoeJob, gpu.rs:814-841)."""
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p),
+                ("gate_row_scale", C.c_void_p), ("up_row_scale", C.c_void_p), ("down_row_scale", C.c_void_p),
+                ("xs_gate", C.c_void_p), ("xs_up", C.c_void_p), ("down_col", C.c_void_p), ("w", C.c_float),
+                ("q1", C.c_int), ("q4t", C.c_int), ("q4tp", C.c_int), ("gu_q2", C.c_int),
+                ("swiglu_limit", C.c_float)]
+
+
+class BatchJob(C.Structure):
+    """cmf_batch_job: one independent matvec (BatchJob, gpu.rs:843-864)."""
+    _fields_ = [("w", C.c_void_p), ("rows", C.c_int), ("cols", C.c_int), ("row_scale", C.c_void_p),
+                ("xs", C.c_void_p), ("layout", C.c_int)]
+
+
 class GenStats(C.Structure):
     _fields_ = [("generated", C.c_int), ("drafted", C.c_int), ("accepted", C.c_int), ("rounds", C.c_int),
                 ("device_ms", C.c_double)]
@@ -93,8 +108,10 @@ SIGNATURES = {
     "cmf_weight_upload_q8": (_I, [_P, _P, _I, _I, C.POINTER(_P)]),
     "cmf_weight_free": (_I, [_P]),
     "cmf_weight_device_bytes": (_S, [_P]),
-    "cmf_q8_matvec_range": (_I, [_P, _I, _P, _I, _I, _P]),
-    "cmf_q8_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
+    "cmf_q8_matvec_range": (_I, [_P, _I, _P, _P, _I, _I, _P]),
+    "cmf_q8_matmat": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "cmf_moe_block_jobs": (_I, [C.POINTER(MoeJob), _I, _P]),
+    "cmf_matvec_batch": (_I, [C.POINTER(BatchJob), _I, C.POINTER(_P)]),
     "cmf_matmat_a8w8": (_I, [_P, _P, _I, _P]),
     "cmf_q4t_matvec": (_I, [_P, _P, _I, _I, _P]),
     "cmf_q4t_matmat": (_I, [_P, _P, _I, _I, _I, _P]),
@@ -225,16 +242,61 @@ def _seam_out(rows, b=1):
     return np.empty((b, rows), dtype=np.float32)
 
 
-def q8_matvec_range(w, row0, xs, rows, cols, out):
-    """gpu.rs:1104 — rows [row0, row0+rows) of q8 w times xs into out."""
+def _f32_or_none(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def q8_matvec_range(w, row0, xs, rows, cols, out, row_scale=None):
+    """gpu.rs:1104 — rows [row0, row0+rows) of q8 w times xs into out, with
+    the caller's row scales [rows] (None: the upload-time ones)."""
     xs = np.ascontiguousarray(xs, dtype=np.float32)
-    return check(lib().cmf_q8_matvec_range(w.h, row0, _ptr(xs), rows, cols, _ptr(out)))
+    rs = _f32_or_none(row_scale)
+    return check(lib().cmf_q8_matvec_range(w.h, row0, _ptr(rs), _ptr(xs), rows, cols, _ptr(out)))
 
 
-def q8_matmat(w, xs, b, rows, cols, out):
+def q8_matmat(w, xs, b, rows, cols, out, row_scale=None):
     """gpu.rs:1155 — out[b*rows + r]."""
     xs = np.ascontiguousarray(xs, dtype=np.float32)
-    return check(lib().cmf_q8_matmat(w.h, _ptr(xs), b, rows, cols, _ptr(out)))
+    rs = _f32_or_none(row_scale)
+    return check(lib().cmf_q8_matmat(w.h, _ptr(rs), _ptr(xs), b, rows, cols, _ptr(out)))
+
+
+def moe_block_jobs(jobs, hidden):
+    """moe_block (gpu.rs:2482) over caller-routed jobs: each a dict with
+    gate/up/down (Weight), xs_gate, xs_up, w and optionally *_row_scale,
+    q1, q4t, q4tp, gu_q2, swiglu_limit, down_col.  Returns the [hidden]
+    output, or None when declined."""
+    keep = []
+
+    def arr(a):
+        if a is None:
+            return None
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        keep.append(a)
+        return _ptr(a)
+    cj = (MoeJob * len(jobs))()
+    for i, j in enumerate(jobs):
+        cj[i] = MoeJob(j["gate"].h, j["up"].h, j["down"].h, arr(j.get("gate_row_scale")),
+                       arr(j.get("up_row_scale")), arr(j.get("down_row_scale")), arr(j["xs_gate"]),
+                       arr(j["xs_up"]), arr(j.get("down_col")), j["w"], int(j.get("q1", 0)), int(j.get("q4t", 0)),
+                       int(j.get("q4tp", 0)), int(j.get("gu_q2", 0)), j.get("swiglu_limit", 0.0))
+    out = np.zeros(hidden, np.float32)
+    return out if check(lib().cmf_moe_block_jobs(cj, len(jobs), _ptr(out))) else None
+
+
+def matvec_batch(jobs):
+    """matvec_batch (gpu.rs:2494): jobs = [(Weight, xs, row_scale or None,
+    layout)], returns the outputs, or None when declined."""
+    keep = []
+    cj = (BatchJob * len(jobs))()
+    outs = [np.zeros(w.rows, np.float32) for w, _, _, _ in jobs]
+    for i, (w, xs, rs, layout) in enumerate(jobs):
+        xs = np.ascontiguousarray(xs, dtype=np.float32)
+        rs = _f32_or_none(rs)
+        keep += [xs, rs]
+        cj[i] = BatchJob(w.h, w.rows, w.cols, _ptr(rs), _ptr(xs), layout)
+    po = (C.c_void_p * len(jobs))(*[_ptr(o) for o in outs])
+    return outs if check(lib().cmf_matvec_batch(cj, len(jobs), po)) else None
 
 
 def q4t_matvec(w, xs, rows, cols, out):

@@ -213,6 +213,8 @@ struct SeamScratch {
     size_t x_cap = 0;
     float* y = nullptr;
     size_t y_cap = 0;
+    float* rs = nullptr;   // caller q8 row scales [rows_pad]
+    size_t rs_cap = 0;
     int* a8cnt = nullptr;  // split_act outliers of the a8w8 ops: [MAXB], [MAXB][cols]
     int* a8idx = nullptr;
     float* a8val = nullptr;
@@ -229,10 +231,22 @@ static int grow(void** p, size_t* cap, size_t need) {
     return CMF_OK;
 }
 
-// y (host) = w rows [row0, row0+rows) * x (host), x [b][cols].
-int seam_matmat(const DevWeight& w, int row0, const float* xs, int b, int rows, float* out) {
+// y (host) = w rows [row0, row0+rows) * x (host), x [b][cols].  q8 only:
+// row_scale (host, rows entries for rows row0..; NULL = the upload-time
+// scales) replaces the stored per-row scales, as the reference seam passes
+// them with every call (gpu.rs:1104, 1155).
+int seam_matmat(const DevWeight& w_in, int row0, const float* xs, int b, int rows, float* out,
+                const float* row_scale) {
     if (ensure_init() != CMF_OK) return CMF_ERR;
-    if (row0 < 0 || rows < 1 || row0 + rows > w.rows) return fail("row range outside the tensor");
+    if (row0 < 0 || rows < 1 || row0 + rows > w_in.rows) return fail("row range outside the tensor");
+    DevWeight w = w_in;
+    if (row_scale) {
+        if (w.dtype != DT_Q8ROW) return fail("row_scale applies to q8 weights only");
+        if (grow((void**)&g_ss.rs, &g_ss.rs_cap, (size_t)w.rows_pad * sizeof(float)) != CMF_OK) return CMF_ERR;
+        CMF_HIP(hipMemcpyAsync(g_ss.rs + row0, row_scale, (size_t)rows * sizeof(float), hipMemcpyHostToDevice,
+                               stream()));
+        w.scale = g_ss.rs;
+    }
     if (grow((void**)&g_ss.planes, &g_ss.planes_cap, prep_bytes(w)) != CMF_OK) return CMF_ERR;
     if (!g_ss.xs) CMF_HIP(hipMalloc(&g_ss.xs, 64 * sizeof(float)));
     const size_t xb = (size_t)std::min(b, MAXB) * w.cols * sizeof(float);
@@ -427,11 +441,11 @@ static int seam_matmat_a8(const DevWeight& w, const float* xs, int b, float* out
 }
 
 static int seam(cmf_weight w, int dt, int row0, const float* xs, int b, int rows, int cols,
-                float* out) {
+                float* out, const float* row_scale = nullptr) {
     if (!w || !xs || !out) return fail("null argument");
     if (w->w.dtype != dt) return CMF_DECLINED;  // not this codec: caller's CPU path
     if (cols != w->w.cols) return fail("cols mismatch");
-    return seam_matmat(w->w, row0, xs, b, rows, out);
+    return seam_matmat(w->w, row0, xs, b, rows, out, row_scale);
 }
 
 int cmf_matmat_a8w8(cmf_weight w, const float* xs, int b, float* out) {
@@ -439,11 +453,12 @@ int cmf_matmat_a8w8(cmf_weight w, const float* xs, int b, float* out) {
     return seam_matmat_a8(w->w, xs, b, out);
 }
 
-int cmf_q8_matvec_range(cmf_weight w, int row0, const float* xs, int rows, int cols, float* out) {
-    return seam(w, DT_Q8ROW, row0, xs, 1, rows, cols, out);
+int cmf_q8_matvec_range(cmf_weight w, int row0, const float* row_scale, const float* xs, int rows, int cols,
+                        float* out) {
+    return seam(w, DT_Q8ROW, row0, xs, 1, rows, cols, out, row_scale);
 }
-int cmf_q8_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out) {
-    return seam(w, DT_Q8ROW, 0, xs, b, rows, cols, out);
+int cmf_q8_matmat(cmf_weight w, const float* row_scale, const float* xs, int b, int rows, int cols, float* out) {
+    return seam(w, DT_Q8ROW, 0, xs, b, rows, cols, out, row_scale);
 }
 int cmf_q4t_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out) {
     return seam(w, DT_Q4T, 0, xs, 1, rows, cols, out);
@@ -503,6 +518,158 @@ int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b,
     (void)hipFree(pl);
     if (rc == CMF_OK) CMF_HIP(hipGetLastError());
     return rc;
+}
+
+}  // extern "C"
+
+namespace cmf {
+// y[i] = sum_j w_j d_j[i] over the jobs in order, from 0, one rounded
+// multiply and one rounded add per term (acc += w * d of moe_ffn_cpu,
+// pipeline.rs:11017-11030, and of the device block's y += w * d).
+__global__ void k_combine_jobs(const float* __restrict__ d, const float* __restrict__ w, int njobs, int n,
+                               float* __restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float acc = 0.f;
+    for (int j = 0; j < njobs; j++) acc = __fadd_rn(acc, __fmul_rn(w[j], d[(size_t)j * n + i]));
+    y[i] = acc;
+}
+
+// q8 weights with caller scales: a view whose scale array holds them (rows
+// [0, rows) of a [rows_pad] buffer).
+static int with_scales(DevWeight& v, const float* row_scale, float* dbuf, hipStream_t st) {
+    if (!row_scale) return CMF_OK;
+    if (v.dtype != DT_Q8ROW) return fail("row_scale applies to q8 weights only");
+    CMF_HIP(hipMemcpyAsync(dbuf, row_scale, (size_t)v.rows * sizeof(float), hipMemcpyHostToDevice, st));
+    v.scale = dbuf;
+    return CMF_OK;
+}
+}  // namespace cmf
+
+extern "C" {
+
+int cmf_moe_block_jobs(const cmf_moe_job* jobs, int njobs, float* out) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!jobs || !out || njobs < 1) return fail("moe_block_jobs: null argument or no jobs");
+    // refusals of gpu.rs:814-841 / gpu_wgpu.rs moe_block: the whole block
+    // goes back to the caller's CPU path, nothing written
+    const int kind = jobs[0].q4tp ? 2 : (jobs[0].q4t ? 1 : 0);
+    for (int j = 0; j < njobs; j++) {
+        const cmf_moe_job& J = jobs[j];
+        if (J.q1 || J.gu_q2 || J.swiglu_limit != 0.0f || J.down_col) return CMF_DECLINED;
+        if (J.q4t && J.q4tp) return CMF_DECLINED;
+        if ((J.q4tp ? 2 : (J.q4t ? 1 : 0)) != kind) return CMF_DECLINED;
+        if (!J.gate || !J.up || !J.down || !J.xs_gate || !J.xs_up) return fail("moe_block_jobs: null job field");
+        const int want = kind == 2 ? DT_Q4TP : (kind == 1 ? DT_Q4T : DT_Q8ROW);
+        if (J.gate->w.dtype != want || J.up->w.dtype != want || J.down->w.dtype != want) return CMF_DECLINED;
+    }
+    const int inter = jobs[0].gate->w.rows, hidden = jobs[0].down->w.rows, cols = jobs[0].gate->w.cols;
+    for (int j = 0; j < njobs; j++) {
+        const cmf_moe_job& J = jobs[j];
+        if (J.gate->w.rows != inter || J.up->w.rows != inter || J.gate->w.cols != cols || J.up->w.cols != cols ||
+            J.down->w.cols != inter || J.down->w.rows != hidden)
+            return fail("moe_block_jobs: every trio must share gate/up [inter x cols] and down [hidden x inter]");
+    }
+    hipStream_t st = stream();
+    // device staging: xs [2 njobs][cols], gate|up [2 inter], d [njobs][hidden],
+    // weights, y, caller scales (3 x rows_pad), planes, xs scales
+    const size_t pb = std::max(prep_bytes(jobs[0].gate->w), prep_bytes(jobs[0].down->w));
+    const size_t rsn = (size_t)std::max(jobs[0].gate->w.rows_pad, jobs[0].down->w.rows_pad);
+    float *dx = nullptr, *dgu = nullptr, *dd = nullptr, *dw = nullptr, *dy = nullptr, *drs = nullptr, *dxs = nullptr;
+    uint8_t* pl = nullptr;
+    int rc = CMF_OK;
+    auto al = [&](void** p, size_t n) {
+        if (rc == CMF_OK && hipMalloc(p, n) != hipSuccess) rc = fail("moe_block_jobs: hipMalloc failed");
+    };
+    al((void**)&dx, (size_t)2 * njobs * cols * 4);
+    al((void**)&dgu, (size_t)2 * inter * 4);
+    al((void**)&dd, (size_t)njobs * hidden * 4);
+    al((void**)&dw, (size_t)njobs * 4);
+    al((void**)&dy, (size_t)hidden * 4);
+    al((void**)&drs, 3 * rsn * 4);
+    al((void**)&dxs, 64 * 4);
+    al((void**)&pl, pb);
+    std::vector<float> ws(njobs);
+    for (int j = 0; j < njobs && rc == CMF_OK; j++) {
+        const cmf_moe_job& J = jobs[j];
+        ws[j] = J.w;
+        if (hipMemcpyAsync(dx + (size_t)(2 * j) * cols, J.xs_gate, (size_t)cols * 4, hipMemcpyHostToDevice, st) ||
+            hipMemcpyAsync(dx + (size_t)(2 * j + 1) * cols, J.xs_up, (size_t)cols * 4, hipMemcpyHostToDevice, st))
+            rc = fail("moe_block_jobs: upload failed");
+        DevWeight g = J.gate->w, u = J.up->w, d = J.down->w;
+        if (rc == CMF_OK) rc = with_scales(g, J.gate_row_scale, drs, st);
+        if (rc == CMF_OK) rc = with_scales(u, J.up_row_scale, drs + rsn, st);
+        if (rc == CMF_OK) rc = with_scales(d, J.down_row_scale, drs + 2 * rsn, st);
+        if (rc != CMF_OK) break;
+        // g = W_g xs_gate, u = W_u xs_up, a = silu(g) * u, d_j = W_d a
+        launch_prep(g, dx + (size_t)(2 * j) * cols, cols, 1, pl, dxs, st);
+        rc = launch_gemv(g, pl, dxs, dgu, inter, 1, 0, inter, st);
+        if (rc != CMF_OK) break;
+        launch_prep(u, dx + (size_t)(2 * j + 1) * cols, cols, 1, pl, dxs, st);
+        rc = launch_gemv(u, pl, dxs, dgu + inter, inter, 1, 0, inter, st);
+        if (rc != CMF_OK) break;
+        XSrc sg{};
+        sg.mode = XS_SILU;
+        sg.x = dgu;
+        sg.ldx = 2 * inter;
+        sg.K = inter;
+        rc = launch_prep_src(d, sg, 1, pl, dxs, st);
+        if (rc == CMF_OK) rc = launch_gemv(d, pl, dxs, dd + (size_t)j * hidden, hidden, 1, 0, hidden, st);
+        // the scale staging is reused by the next job: wait for this one
+        if (rc == CMF_OK && (J.gate_row_scale || J.up_row_scale || J.down_row_scale) &&
+            hipStreamSynchronize(st) != hipSuccess)
+            rc = fail("moe_block_jobs: stream error");
+    }
+    if (rc == CMF_OK) {
+        if (hipMemcpyAsync(dw, ws.data(), (size_t)njobs * 4, hipMemcpyHostToDevice, st) != hipSuccess)
+            rc = fail("moe_block_jobs: upload failed");
+        hipLaunchKernelGGL(k_combine_jobs, dim3((hidden + 255) / 256), dim3(256), 0, st, dd, dw, njobs, hidden, dy);
+        if (rc == CMF_OK &&
+            hipMemcpyAsync(out, dy, (size_t)hidden * 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+            rc = fail("moe_block_jobs: download failed");
+    }
+    (void)hipStreamSynchronize(st);
+    for (void* p : {(void*)dx, (void*)dgu, (void*)dd, (void*)dw, (void*)dy, (void*)drs, (void*)dxs, (void*)pl})
+        if (p) (void)hipFree(p);
+    if (rc == CMF_OK) CMF_HIP(hipGetLastError());
+    return rc;
+}
+
+int cmf_matvec_batch(const cmf_batch_job* jobs, int njobs, float* const* outs) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (!jobs || !outs || njobs < 1) return fail("matvec_batch: null argument or no jobs");
+    // validate every job first: a refusal writes nothing (gpu.rs:1-12)
+    size_t pb = 0, ymax = 0, xmax = 0;
+    for (int j = 0; j < njobs; j++) {
+        const cmf_batch_job& J = jobs[j];
+        if (!J.w || !J.xs || !outs[j]) return fail("matvec_batch: null job field");
+        if (J.layout != DT_Q8ROW && J.layout != DT_Q4T && J.layout != DT_Q4TP) return CMF_DECLINED;  // Q1
+        if (J.w->w.dtype != J.layout) return CMF_DECLINED;
+        if (J.rows != J.w->w.rows || J.cols != J.w->w.cols) return fail("matvec_batch: job shape != weight shape");
+        if (J.row_scale && J.layout != DT_Q8ROW) return fail("matvec_batch: row_scale applies to q8 jobs only");
+        pb = std::max(pb, prep_bytes(J.w->w));
+        ymax = std::max(ymax, (size_t)J.w->w.rows_pad);
+        xmax = std::max(xmax, (size_t)J.cols);
+    }
+    hipStream_t st = stream();
+    if (grow((void**)&g_ss.planes, &g_ss.planes_cap, pb) != CMF_OK) return CMF_ERR;
+    if (!g_ss.xs) CMF_HIP(hipMalloc(&g_ss.xs, 64 * sizeof(float)));
+    if (grow((void**)&g_ss.x, &g_ss.x_cap, xmax * 4) != CMF_OK) return CMF_ERR;
+    if (grow((void**)&g_ss.y, &g_ss.y_cap, ymax * 4) != CMF_OK) return CMF_ERR;
+    if (grow((void**)&g_ss.rs, &g_ss.rs_cap, ymax * 4) != CMF_OK) return CMF_ERR;
+    for (int j = 0; j < njobs; j++) {
+        const cmf_batch_job& J = jobs[j];
+        DevWeight w = J.w->w;
+        if (with_scales(w, J.row_scale, g_ss.rs, st) != CMF_OK) return CMF_ERR;
+        CMF_HIP(hipMemcpyAsync(g_ss.x, J.xs, (size_t)J.cols * 4, hipMemcpyHostToDevice, st));
+        launch_prep(w, g_ss.x, J.cols, 1, g_ss.planes, g_ss.xs, st);
+        const int rc = launch_gemv(w, g_ss.planes, g_ss.xs, g_ss.y, J.rows, 1, 0, J.rows, st);
+        if (rc != CMF_OK) return rc;
+        CMF_HIP(hipMemcpyAsync(outs[j], g_ss.y, (size_t)J.rows * 4, hipMemcpyDeviceToHost, st));
+        CMF_HIP(hipStreamSynchronize(st));  // the staging is reused by the next job
+    }
+    CMF_HIP(hipGetLastError());
+    return CMF_OK;
 }
 
 void* cmf_dev_alloc(size_t bytes) {

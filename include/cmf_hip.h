@@ -55,11 +55,15 @@ int cmf_weight_free(cmf_weight w);
 size_t cmf_weight_device_bytes(cmf_weight w);
 
 /* ---- seam ops on host slices (gpu.rs) -------------------------------- */
-/* gpu.rs:1104 q8_matvec_range: rows [row0, row0+rows) of w times x. */
-int cmf_q8_matvec_range(cmf_weight w, int row0, const float* xs, int rows, int cols, float* out);
-/* gpu.rs:1155 q8_matmat: out[b*rows + r], b <= 16 per launch (larger b is
- * split into launches of 16). */
-int cmf_q8_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out);
+/* gpu.rs:1104 q8_matvec_range: rows [row0, row0+rows) of w times x, each
+ * row r scaled by row_scale[r - row0] (the caller's f32 row scales, as the
+ * reference passes them with every call; NULL: the scales given at upload). */
+int cmf_q8_matvec_range(cmf_weight w, int row0, const float* row_scale, const float* xs, int rows, int cols,
+                        float* out);
+/* gpu.rs:1155 q8_matmat: out[b*rows + r] with row_scale [rows] (NULL: the
+ * upload-time scales), b <= 16 per launch (larger b is split into launches
+ * of 16). */
+int cmf_q8_matmat(cmf_weight w, const float* row_scale, const float* xs, int b, int rows, int cols, float* out);
 /* gpu.rs:2423 / 2439 */
 int cmf_q4t_matvec(cmf_weight w, const float* xs, int rows, int cols, float* out);
 int cmf_q4t_matmat(cmf_weight w, const float* xs, int b, int rows, int cols, float* out);
@@ -76,6 +80,42 @@ int cmf_matmat_a8w8(cmf_weight w, const float* xs, int b, float* out);
  * xs [b][hidden], out [b][hidden]. */
 int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b, int hidden,
             int inter, float* out);
+
+/* MoeJob (gpu.rs:814-841): one expert trio of a caller-routed MoE FFN.
+ * gate/up [inter x cols], down [hidden x inter], all three of one codec:
+ * q8 (q4t = q4tp = 0; *_row_scale [rows] or NULL = upload-time scales),
+ * q4t (q4t = 1) or q4tp (q4tp = 1).  xs_gate / xs_up [cols]: the gate and
+ * up inputs; w: the blending weight. */
+typedef struct {
+    cmf_weight gate, up, down;
+    const float *gate_row_scale, *up_row_scale, *down_row_scale;
+    const float *xs_gate, *xs_up;
+    const float* down_col; /* q8_2f column field of down: no device kernel, must be NULL */
+    float w;
+    int q1, q4t, q4tp, gu_q2;
+    float swiglu_limit;
+} cmf_moe_job;
+/* moe_block (gpu.rs:2482, wgpu arm gpu_wgpu.rs:28964): out [hidden] =
+ * sum over jobs in order of w * down(silu(gate xs_gate) * (up xs_up)).
+ * Declined (>0, nothing written) as the reference backends refuse: any q1,
+ * gu_q2 (2-bit gate/up), swiglu_limit != 0 or down_col job, jobs of mixed
+ * kinds, or a trio whose codec does not match its flags. */
+int cmf_moe_block_jobs(const cmf_moe_job* jobs, int njobs, float* out);
+
+/* BatchJob (gpu.rs:843-864): one independent matvec; layout is the
+ * BatchLayout as a dtype id (CMF_DT_Q8ROW, CMF_DT_Q4T, CMF_DT_Q4TP; Q1 and
+ * anything else is declined). */
+typedef struct {
+    cmf_weight w;
+    int rows, cols;
+    const float* row_scale; /* q8: [rows] or NULL (upload-time scales) */
+    const float* xs;        /* [cols] */
+    int layout;
+} cmf_batch_job;
+/* matvec_batch (gpu.rs:2494): outs[j] [rows_j] = job j's weight times its
+ * xs.  Every job is validated before any runs: a declined job declines the
+ * whole batch with nothing written. */
+int cmf_matvec_batch(const cmf_batch_job* jobs, int njobs, float* const* outs);
 
 /* ---- device-resident variants (inputs already in HBM) ----------------- */
 void* cmf_dev_alloc(size_t bytes);

@@ -112,6 +112,84 @@ def test_q8_matvec_range(gpu):
     assert gpu.q8_matvec_range(w, 5, x, 37, 256, out)
     ref = orc.matmat(t, x)[:, 5:42]
     assert rel_l2(out, ref) < TOL
+    # the caller's row scales replace the stored ones (gpu.rs:1104 passes
+    # row_scale[row0..] with every call)
+    rs = (t["row_scale"][5:42] * np.linspace(0.5, 2.0, 37)).astype(np.float32)
+    out2 = np.zeros((1, 37), np.float32)
+    assert gpu.q8_matvec_range(w, 5, x, 37, 256, out2, row_scale=rs)
+    t2 = dict(t, row_scale=t["row_scale"].copy())
+    t2["row_scale"][5:42] = rs
+    ref2 = orc.matmat(t2, x)[:, 5:42]
+    print(f"caller scales: rel-L2 {rel_l2(out2, ref2):.2e}", flush=True)
+    assert rel_l2(out2, ref2) < TOL and rel_l2(out2, ref) > 0.1
+    # and the stored ones are untouched
+    out3 = np.zeros((1, 37), np.float32)
+    assert gpu.q8_matvec_range(w, 5, x, 37, 256, out3)
+    assert rel_l2(out3, ref) < TOL
+    out4 = np.zeros((2, 300), np.float32)
+    rs_all = (t["row_scale"] * 1.5).astype(np.float32)
+    x2 = _x(83, 2, 256)
+    assert gpu.q8_matmat(w, x2, 2, 300, 256, out4, row_scale=rs_all)
+    assert rel_l2(out4, orc.matmat(dict(t, row_scale=rs_all), x2)) < TOL
+
+
+def _silu(x):
+    x = x.astype(np.float32)
+    return (x / (np.float32(1) + np.exp(-x))).astype(np.float32)
+
+
+@pytest.mark.parametrize("codec", ["q8", "q4t", "q4tp"])
+def test_moe_block_jobs(gpu, codec):
+    """moe_block (gpu.rs:2482) over MoeJob-shaped jobs with their own inputs
+    and blend weights: out = sum_j w_j down_j(silu(gate_j xg_j) * up_j xu_j)"""
+    from cmf_amd import synth
+    H, I, nj = 256, 128, 3
+    mk = {"q8": lambda s, r, c: synth.q8_normal(s, r, c, 0.05), "q4t": lambda s, r, c: synth.q4t_normal(s, r, c, 0.05),
+          "q4tp": lambda s, r, c: synth.q4tp_uniform(s, r, c, 0.05)}[codec]
+    W = lambda t: gpu.Weight(t["dtype"], t["rows"], t["cols"], payload=t["bytes"], q=t["q"], row_scale=t["row_scale"])
+    trios = [(mk(300 + 3 * j, I, H), mk(301 + 3 * j, I, H), mk(302 + 3 * j, H, I)) for j in range(nj)]
+    ws = [W(t) for tr in trios for t in tr]
+    jobs, ref = [], np.zeros(H, np.float32)
+    for j, (g, u, d) in enumerate(trios):
+        xg, xu = _x(400 + j, 1, H)[0], _x(500 + j, 1, H)[0]
+        bw = np.float32(0.2 + 0.3 * j)
+        job = {"gate": ws[3 * j], "up": ws[3 * j + 1], "down": ws[3 * j + 2], "xs_gate": xg, "xs_up": xu, "w": bw,
+               "q4t": codec == "q4t", "q4tp": codec == "q4tp"}
+        if codec == "q8" and j == 1:  # caller scales on one trio
+            job["gate_row_scale"] = (g["row_scale"] * 0.7).astype(np.float32)
+            g = dict(g, row_scale=job["gate_row_scale"])
+        jobs.append(job)
+        a = (_silu(orc.matmat(g, xg)[0]) * orc.matmat(u, xu)[0]).astype(np.float32)
+        ref = (ref + bw * orc.matmat(d, a)[0]).astype(np.float32)
+    got = gpu.moe_block_jobs(jobs, H)
+    print(f"{codec}: rel-L2 {rel_l2(got, ref):.2e}", flush=True)
+    assert rel_l2(got, ref) < TOL
+    # the refusals of gpu.rs:814-841: the whole block is declined
+    for bad in ({"swiglu_limit": 7.0}, {"q1": 1}, {"gu_q2": 1}, {"down_col": np.ones(I, np.float32)},
+                {"q4t": codec != "q4t", "q4tp": codec == "q4t"}):
+        jb = [dict(jobs[0]), dict(jobs[1], **bad)]
+        assert gpu.moe_block_jobs(jb, H) is None, bad
+    for w in ws:
+        w.free()
+
+
+def test_matvec_batch(gpu):
+    """matvec_batch (gpu.rs:2494): independent matvecs of three codecs in one
+    call; a Q1 job declines the whole batch"""
+    from cmf_amd import synth
+    ts = [synth.q8_normal(601, 96, 128, 0.05), synth.q4t_normal(602, 64, 256, 0.05), synth.q4tp_uniform(603, 32, 512)]
+    ws = [gpu.Weight(t["dtype"], t["rows"], t["cols"], payload=t["bytes"], q=t["q"], row_scale=t["row_scale"])
+          for t in ts]
+    xs = [_x(610 + i, 1, t["cols"])[0] for i, t in enumerate(ts)]
+    rs0 = (ts[0]["row_scale"] * 2).astype(np.float32)
+    outs = gpu.matvec_batch([(ws[0], xs[0], rs0, 3), (ws[1], xs[1], None, 11), (ws[2], xs[2], None, 15)])
+    refs = [orc.matmat(dict(ts[0], row_scale=rs0), xs[0])[0], orc.matmat(ts[1], xs[1])[0], orc.matmat(ts[2], xs[2])[0]]
+    for o, r in zip(outs, refs):
+        assert rel_l2(o, r) < TOL
+    assert gpu.matvec_batch([(ws[1], xs[1], None, 11), (ws[0], xs[0], None, 1)]) is None  # Q1 layout
+    assert gpu.matvec_batch([(ws[1], xs[1], None, 15)]) is None  # layout != weight codec
+    for w in ws:
+        w.free()
 
 
 def test_seam_declines_other_codec(gpu):
