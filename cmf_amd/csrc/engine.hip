@@ -61,6 +61,9 @@ struct cmf_model_s {
     std::vector<void*> allocs;
     int next_pos_host = 0;
     bool prefilled = false;
+    // prefill chunk buffers [PREFILL_CHUNK rows] (allocated by the first prefill)
+    float *pf_h = nullptr, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_gu = nullptr, *pf_hm = nullptr;
+    int* pf_toks = nullptr;
     hipGraphExec_t round_graph = nullptr;
     int graph_k = 0;
     int graph_len = 0;  // attention length bound the captured round was built for
@@ -407,8 +410,62 @@ int ensure_out(cmf_model_s* m, int cap) {
 
 __global__ void k_set_int(int* p, int v) { *p = v; }
 
-// prompt positions per prefill step (the verify batch class of kernels)
-constexpr int PREFILL_CHUNK = 4;
+// prompt positions per prefill chunk: every weight is read once per chunk by
+// the large-batch GEMMs (prefill_batch, pipeline.rs:5100-5108)
+constexpr int PREFILL_CHUNK = 256;
+
+int ensure_prefill_bufs(cmf_model_s* m) {
+    if (m->pf_h) return CMF_OK;
+    const auto& c = m->c;
+    const int H = c.hidden, QKV = (c.n_heads + 2 * c.n_kv) * c.head_dim;
+    const size_t R = PREFILL_CHUNK;
+    if (dalloc_t(m, &m->pf_h, R * H) || dalloc_t(m, &m->pf_qkv, R * QKV) ||
+        dalloc_t(m, &m->pf_ao, R * c.n_heads * c.head_dim) || dalloc_t(m, &m->pf_gu, R * 2 * c.inter) ||
+        dalloc_t(m, &m->pf_hm, R * H) || dalloc_t(m, &m->pf_toks, R))
+        return CMF_ERR;
+    return CMF_OK;
+}
+
+// Causal attention of cnt chunk rows (positions *pb + i) in groups the
+// attention kernel serves (at most 32 queries per kv head); attend = 0 only
+// appends their K/V (the MTP warm).
+void prefill_attention(cmf_model_s* m, LayerDev& l, const float* qkv, float* ao, int cnt, const int* pb, int p0,
+                       bool attend, hipStream_t s) {
+    const auto& c = m->c;
+    const int hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv, QKV = (nh + 2 * nkv) * hd;
+    const int rows_per = std::min(MAXB, std::max(1, 32 / (nh / nkv)));
+    for (int b0 = 0; b0 < cnt; b0 += rows_per) {
+        const int nb = std::min(rows_per, cnt - b0);
+        AttnArgs at{qkv + (size_t)b0 * QKV, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq, nb, nh, nkv,
+                    c.eps, pb, b0, attend ? m->pm : nullptr, attend ? m->pl : nullptr, attend ? m->po : nullptr,
+                    attend ? m->nch_cap : 0, attend ? ao + (size_t)b0 * nh * hd : nullptr, attend ? 1 : 0};
+        launch_attention(at, p0 + b0 + nb, s);
+    }
+}
+
+// One decoder block over a prefill chunk of cnt rows of h (forward_layers_span
+// over a batch, pipeline.rs:5100-5108 / 7981-8700) on the GEMMs: the
+// norm and SwiGLU producers prepare each GEMM's operand, the residual adds
+// are GEMM epilogues.
+int prefill_block(cmf_model_s* m, LayerDev& l, float* h, int cnt, const int* pb, int p0, hipStream_t s) {
+    const auto& c = m->c;
+    const int H = c.hidden, hd = c.head_dim, nh = c.n_heads, QKV = (nh + 2 * c.n_kv) * hd, I = c.inter;
+    int rc = gemm(l.qkv, src_norm(h, H, l.in_norm, c.eps), cnt, m->pf_qkv, QKV, false, s);
+    if (rc != CMF_OK) return rc;
+    prefill_attention(m, l, m->pf_qkv, m->pf_ao, cnt, pb, p0, true, s);
+    XSrc ra{};
+    ra.mode = XS_ROWS;
+    ra.x = m->pf_ao;
+    ra.ldx = nh * hd;
+    if ((rc = gemm(l.wo, ra, cnt, h, H, true, s)) != CMF_OK) return rc;
+    if ((rc = gemm(l.gu, src_norm(h, H, l.post_norm, c.eps), cnt, m->pf_gu, 2 * I, false, s)) != CMF_OK) return rc;
+    XSrc sd{};
+    sd.mode = XS_SILU8;
+    sd.x = m->pf_gu;
+    sd.ldx = 2 * I;
+    sd.K = I;
+    return gemm(l.down, sd, cnt, h, H, true, s);
+}
 
 __global__ void k_copy_rows_i32(int* dst, const int* src, int n) {
     const int i = threadIdx.x;
@@ -599,26 +656,35 @@ static int ready(cmf_model m) {
 int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
     if (ready(m)) return CMF_ERR;
     if (!ids || n < 1 || n + 1 > m->c.max_seq) return fail("prefill: 1 <= n < max_seq");
+    if (ensure_prefill_bufs(m)) return CMF_ERR;
+    for (int i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= m->c.vocab) return fail("prefill: token id out of range");
     hipStream_t s = stream();
-    const int H = m->c.hidden;
+    const auto& c = m->c;
+    const int H = c.hidden, QKV = (c.n_heads + 2 * c.n_kv) * c.head_dim;
     int* pb = &m->st->next_pos;
     for (int p0 = 0; p0 < n; p0 += PREFILL_CHUNK) {
         const int cnt = std::min(PREFILL_CHUNK, n - p0);
-        CMF_HIP(hipMemcpyAsync(m->toks, ids + p0, cnt * sizeof(int), hipMemcpyHostToDevice, s));
+        CMF_HIP(hipMemcpyAsync(m->pf_toks, ids + p0, cnt * sizeof(int), hipMemcpyHostToDevice, s));
         hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, p0);
-        launch_embed(m->toks, embed_src(m), H, m->hv, H, cnt, s);
-        trunk_forward(m, cnt, pb, 0, p0 + cnt, false, s);
+        launch_embed(m->pf_toks, embed_src(m), H, m->pf_h, H, cnt, s);
+        for (int li = 0; li < c.n_layers; li++)
+            if (prefill_block(m, m->L[li], m->pf_h, cnt, pb, p0, s) != CMF_OK) return CMF_ERR;
         if (m->has_mtp) {
+            // MTP warm on the (h_p, id_{p+1}) pairs of the chunk (pipeline.rs:2275-2318)
             const int pairs = (p0 + cnt < n) ? cnt : cnt - 1;
             if (pairs > 0) {
-                CMF_HIP(hipMemcpyAsync(m->toks + MAXB, ids + p0 + 1, pairs * sizeof(int), hipMemcpyHostToDevice, s));
-                mtp_warm(m, m->toks + MAXB, m->hv, pairs, pb, 0, p0 + pairs, s);
+                CMF_HIP(hipMemcpyAsync(m->pf_toks, ids + p0 + 1, pairs * sizeof(int), hipMemcpyHostToDevice, s));
+                if (gemm(m->eh, src_cat(m, m->pf_toks, m->pf_h), pairs, m->pf_hm, H, false, s) ||
+                    gemm(m->mtp.qkv, src_norm(m->pf_hm, H, m->mtp.in_norm, c.eps), pairs, m->pf_qkv, QKV, false, s))
+                    return CMF_ERR;
+                prefill_attention(m, m->mtp, m->pf_qkv, nullptr, pairs, pb, p0, false, s);
             }
         }
         if (p0 + cnt == n)
-            CMF_HIP(hipMemcpyAsync(m->h_tip, m->hv + (size_t)(cnt - 1) * H, H * sizeof(float),
+            CMF_HIP(hipMemcpyAsync(m->h_tip, m->pf_h + (size_t)(cnt - 1) * H, H * sizeof(float),
                                    hipMemcpyDeviceToDevice, s));
-        CMF_HIP(hipStreamSynchronize(s));  // host buffers of this chunk are reused
+        CMF_HIP(hipStreamSynchronize(s));  // the host ids of this chunk are reused
     }
     hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, n);
     CMF_HIP(hipMemsetAsync(&m->st->n_out, 0, sizeof(int), s));

@@ -23,13 +23,13 @@
 namespace cmf {
 
 struct GemmArgs {
-    const void* w;        // [rb][group of 4 tiles][lane][16 B]
-    const void* scale;    // q4t f16 [rb][group][16][4]; q4tp u32 codes
+    const void* w;        // [rb][group of 4 tiles][lane][16 B]   (q8: [rb][64-column chunk][lane][16 B])
+    const void* scale;    // q4t f16 [rb][group][16][4]; q4tp u32 codes; q8 f32 row scales
     const float2* rowp;   // q4tp (2^lo, 2^step) per row
-    const uint8_t* planes;  // hi [item][Mp], lo [item][Mp] (16 B), bias [tile][Mp] f32
-    const float* xs;      // [Mp] 2^-e per batch row
+    const uint8_t* planes;  // hi [item][Mp], lo [item][Mp] (16 B), bias [tile][Mp] f32 (q8: q0 q1 q2 [item][Mp])
+    const float* xs;      // [Mp] 2^-e per batch row (q8: amax / 127)
     float* y;
-    int ldy, M, Mp, N, ntg, nrb;
+    int ldy, M, Mp, N, ntg, nrb, resid;
 };
 
 constexpr int GB = 64;             // batch rows per workgroup
@@ -177,7 +177,131 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int b = GB * by + 16 * mb + 4 * s + v;
-                if (b < a.M) a.y[(size_t)b * a.ldy + n] = acc[q][mb][v] * a.xs[b] * 16777216.0f;
+                if (b < a.M) {
+                    float* yp = a.y + (size_t)b * a.ldy + n;
+                    const float val = acc[q][mb][v] * a.xs[b] * 16777216.0f;
+                    *yp = a.resid ? *yp + val : val;
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// q8 (qmatvec's exact arm in batches, qtensor.rs:9980-10047): int8 weights
+// times the operand carried as three int8 planes x ~= sx (q0 + q1/128 +
+// q2/16384) (prep8_row), on v_mfma_i32_16x16x64_i8.  A workgroup of 4 waves
+// owns 64 batch rows x 64 Q8RB weight rows and walks K in steps of two
+// 64-column chunks: the step's operand (3 planes x 2 chunks x 64 rows x
+// 64 B = 24 KiB) is staged one step ahead through registers into a
+// double-buffered LDS tile, the next step's weights are requested before the
+// current MFMAs.  Each plane keeps its own int32 accumulators over the whole
+// K (exact: |sum| <= 127 * 127 * K < 2^31 for K <= 16384), combined in f32
+// at the end as the GEMV does: ((s0 + s1/128 + s2/16384) * sx) * rs.
+// ---------------------------------------------------------------------------
+constexpr int Q8CH = 24;              // 1 KiB operand chunks per step
+constexpr int Q8J = Q8CH / 4;         // per wave
+template <int Q8RB>
+__global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
+    __shared__ __align__(16) int4v At[2][Q8CH * 64];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4;
+    const int by = blockIdx.y, rbw = (blockIdx.x * 4 + wave) * Q8RB;
+    const int nk = a.ntg, Mp = a.Mp;
+    const int4v* P = (const int4v*)a.planes;  // plane p, item (kc * 4 + s): P[(p * nk * 4 + item) * Mp + row]
+    // operand chunk c of step g: plane c / 8, chunk 2g + (c / 4) % 2, quarter c % 4
+    auto src_a = [&](int j, int g) __attribute__((always_inline)) -> const int4v* {
+        const int c = wave + 4 * j;
+        const int p = c >> 3, kc = min(2 * g + ((c >> 2) & 1), nk - 1), q = c & 3;
+        return P + ((size_t)p * nk * 4 + kc * 4 + q) * Mp + GB * by + lane;
+    };
+    auto load_w = [&](int4v (*wv)[2], int g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < Q8RB; q++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const size_t t = (size_t)min(rbw + q, a.nrb - 1) * nk + min(2 * g + h, nk - 1);
+                wv[q][h] = ld_stream((const int4v*)a.w + t * 64 + lane);
+            }
+    };
+    int4v acc[Q8RB][4][3];
+#pragma unroll
+    for (int q = 0; q < Q8RB; q++)
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+            for (int p = 0; p < 3; p++) acc[q][mb][p] = int4v{0, 0, 0, 0};
+    int4v ra[Q8J], wA[Q8RB][2], wB[Q8RB][2];
+    const int nst = (nk + 1) / 2;
+#pragma unroll
+    for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, 0));
+    load_w(wA, 0);
+#pragma unroll
+    for (int j = 0; j < Q8J; j++) At[0][(wave + 4 * j) * 64 + lane] = ra[j];
+    __syncthreads();
+
+    auto compute = [&](int buf, int4v (*wv)[2], int g) __attribute__((always_inline)) {
+        const int4v* A = At[buf];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            if (2 * g + h >= nk) break;  // uniform: an odd chunk count's last step
+#pragma unroll
+            for (int mb = 0; mb < 4; mb++) {
+                const int4v x0 = A[(0 * 8 + h * 4 + s) * 64 + 16 * mb + r];
+                const int4v x1 = A[(1 * 8 + h * 4 + s) * 64 + 16 * mb + r];
+                const int4v x2 = A[(2 * 8 + h * 4 + s) * 64 + 16 * mb + r];
+#pragma unroll
+                for (int q = 0; q < Q8RB; q++) {
+                    acc[q][mb][0] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, wv[q][h], acc[q][mb][0], 0, 0, 0);
+                    acc[q][mb][1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, wv[q][h], acc[q][mb][1], 0, 0, 0);
+                    acc[q][mb][2] = __builtin_amdgcn_mfma_i32_16x16x64_i8(x2, wv[q][h], acc[q][mb][2], 0, 0, 0);
+                }
+            }
+        }
+    };
+    for (int g = 0; g < nst; g += 2) {
+        {
+            const int gn = min(g + 1, nst - 1);
+#pragma unroll
+            for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gn));
+            load_w(wB, gn);
+            compute(0, wA, g);
+            if (g + 1 < nst) {
+#pragma unroll
+                for (int j = 0; j < Q8J; j++) At[1][(wave + 4 * j) * 64 + lane] = ra[j];
+            }
+        }
+        __syncthreads();
+        if (g + 1 >= nst) break;
+        {
+            const int gn = min(g + 2, nst - 1);
+#pragma unroll
+            for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gn));
+            load_w(wA, gn);
+            compute(1, wB, g + 1);
+            if (g + 2 < nst) {
+#pragma unroll
+                for (int j = 0; j < Q8J; j++) At[0][(wave + 4 * j) * 64 + lane] = ra[j];
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int q = 0; q < Q8RB; q++) {
+        const int n = (rbw + q) * 16 + r;
+        if (rbw + q >= a.nrb || n >= a.N) continue;
+        const float rs = ((const float*)a.scale)[n];
+#pragma unroll
+        for (int mb = 0; mb < 4; mb++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int b = GB * by + 16 * mb + 4 * s + v;
+                if (b < a.M) {
+                    const float tt = (float)acc[q][mb][0][v] + (float)acc[q][mb][1][v] * 0.0078125f +
+                                     (float)acc[q][mb][2][v] * 6.103515625e-05f;
+                    const float val = (tt * a.xs[b]) * rs;
+                    float* yp = a.y + (size_t)b * a.ldy + n;
+                    *yp = a.resid ? *yp + val : val;
+                }
             }
     }
 }
@@ -189,13 +313,15 @@ static float* g_gemm_xs = nullptr;
 static size_t g_gemm_xs_cap = 0;
 
 size_t gemm_planes_bytes(const DevWeight& w, int mp) {
-    // hi + lo: 2 * items * Mp * 16 B; biases: tiles * Mp * 4 B
+    // q8: three planes of nk * 64 * Mp B; q4: hi + lo 2 * items * Mp * 16 B
+    // and the tile biases tiles * Mp * 4 B
+    if (w.dtype == DT_Q8ROW) return (size_t)w.kchunks * 64 * mp * 3;
     return (size_t)w.kchunks * 16 * mp * 32 + (size_t)w.kchunks * 4 * mp * 4;
 }
 
-int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st) {
-    if (w.dtype != DT_Q4T && w.dtype != DT_Q4TP) return fail("gemm: q4t / q4tp weights only");
-    if (m < 1 || m > 65535 * GB) return fail("gemm: bad batch");
+int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool resid, hipStream_t st) {
+    if (w.dtype != DT_Q4T && w.dtype != DT_Q4TP && w.dtype != DT_Q8ROW) return fail("gemm: q8 / q4t / q4tp weights");
+    if (m < 1 || m > 65535) return fail("gemm: batch must be 1..65535");
     const int mp = (m + GB - 1) / GB * GB;
     const size_t pb = gemm_planes_bytes(w, mp);
     if (g_gemm_cap < pb) {
@@ -214,7 +340,7 @@ int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ld
         CMF_HIP(hipMalloc(&g_gemm_xs, (size_t)mp * sizeof(float)));
         g_gemm_xs_cap = mp;
     }
-    int rc = launch_prep_rows_gemm(w, x, ldx, m, mp, g_gemm_planes, g_gemm_xs, st);
+    int rc = launch_prep_src_gemm(w, src, m, mp, g_gemm_planes, g_gemm_xs, st);
     if (rc != CMF_OK) return rc;
     GemmArgs a;
     a.w = w.w;
@@ -229,6 +355,17 @@ int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ld
     a.N = w.rows;
     a.ntg = w.kchunks;
     a.nrb = w.rows_pad / 16;
+    a.resid = resid ? 1 : 0;
+    if (w.dtype == DT_Q8ROW) {
+        // two row blocks per wave once that still leaves ~4 workgroups per CU
+        const bool big = (long)((a.nrb + 7) / 8) * (mp / GB) >= 1024;
+        const int rbwg = big ? 8 : 4;
+        const dim3 grid((a.nrb + rbwg - 1) / rbwg, mp / GB);
+        if (big) hipLaunchKernelGGL((k_gemm_q8<2>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_gemm_q8<1>), grid, dim3(256), 0, st, a);
+        CMF_HIP(hipGetLastError());
+        return CMF_OK;
+    }
     // four row blocks per wave once that still leaves ~4 workgroups per CU
     const bool big = (long)((a.nrb + 15) / 16) * (mp / GB) >= 1024;
     const int rbwg = big ? 16 : 4;
@@ -242,6 +379,14 @@ int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ld
     }
     CMF_HIP(hipGetLastError());
     return CMF_OK;
+}
+
+int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st) {
+    XSrc r{};
+    r.mode = XS_ROWS;
+    r.x = x;
+    r.ldx = ldx;
+    return gemm(w, r, m, y, ldy, false, st);
 }
 
 }  // namespace cmf

@@ -22,7 +22,10 @@ struct EmbedSrc {
 //   XS_ROWS : x = x_row
 //   XS_CAT  : x = [rms_norm(embed(tok), w) ; rms_norm(x_row, w2)]  (H each,
 //             the MTP input, pipeline.rs:3085-3094)
-enum { XS_GLOBAL = 0, XS_NORM = 2, XS_SILU = 3, XS_ROWS = 4, XS_CAT = 5 };
+//   XS_SILU8: x[i] = silu(g) * u of a gate|up row whose 16-column blocks
+//             hold 8 gate then the 8 matching up values (the interleaved
+//             gate|up weight's output): g = row[16 (i/8) + i%8], u = g's + 8
+enum { XS_GLOBAL = 0, XS_NORM = 2, XS_SILU = 3, XS_ROWS = 4, XS_CAT = 5, XS_SILU8 = 6 };
 struct XSrc {
     int mode;
     const float* x;
@@ -103,12 +106,17 @@ size_t prep_bytes(const DevWeight& w);
 // Prepared planes (prep_bytes, the layout of prep8_row / prep16_row) and
 // xs[16] of the operand producer src for m batch rows of w.
 int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes, float* xs, hipStream_t st);
-// Prepared GEMM operand of m rows (q4 weights): planes with row stride
-// mstride (a multiple of 64) and tile biases [tile][mstride].
+// Prepared GEMM operand of m rows of the producer src: planes with row
+// stride mstride (a multiple of 64; q4: and tile biases [tile][mstride]).
+int launch_prep_src_gemm(const DevWeight& w, const XSrc& src, int m, int mstride, uint8_t* planes, float* xs,
+                         hipStream_t st);
 int launch_prep_rows_gemm(const DevWeight& w, const float* x, int ldx, int m, int mstride, uint8_t* planes,
                           float* xs, hipStream_t st);
-// y[b][n] (ldy) = W x[b] for b < m (x device rows, ldx), any m, q4t / q4tp
-// weights: the large-batch MFMA GEMM (gemm.hip).
+// y[b][n] (ldy) (+)= W x[b] for b < m, any m, q8 / q4t / q4tp weights: the
+// large-batch MFMA GEMM (gemm.hip) over the operand of the producer src
+// (XS_ROWS, XS_NORM, XS_SILU8, XS_CAT; resid: y += W x).
+int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool resid, hipStream_t st);
+// the same over plain device rows x [m][ldx]
 int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st);
 // The same for up to max_jobs jobs of a device job list (GemvArgs::jobs):
 // job j reads rows at src.x + j * x_stride and writes planes + j *

@@ -49,6 +49,10 @@ __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk
         if (s.mode == XS_SILU) {
             const float g = row[i], u = row[s.K + i];
             v = (g / (1.0f + expf(-g))) * u;
+        } else if (s.mode == XS_SILU8) {
+            const int o = 16 * (i >> 3) + (i & 7);
+            const float g = row[o], u = row[o + 8];
+            v = (g / (1.0f + expf(-g))) * u;
         } else if (s.mode == XS_CAT) {
             if (i < H) {
                 // int8 of the token's row in the q8 device layout, times its row scale
@@ -254,18 +258,26 @@ int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes,
     return CMF_OK;
 }
 
+int launch_prep_src_gemm(const DevWeight& w, const XSrc& src, int m, int mstride, uint8_t* planes, float* xs,
+                         hipStream_t st) {
+    const int K = src.K ? src.K : w.cols;
+    if (m < 1 || m > mstride || mstride % 64) return fail("prep: GEMM rows must be 1..mstride, mstride % 64 == 0");
+    if (m > 65535) return fail("prep: at most 65535 GEMM rows per launch");
+    if (K < 1 || K > w.cols || K > 16384) return fail("prep: operand length must be 1..min(cols, 16384)");
+    if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
+    const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
+    hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
+                       xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride);
+    return CMF_OK;
+}
+
 int launch_prep_rows_gemm(const DevWeight& w, const float* x, int ldx, int m, int mstride, uint8_t* planes,
                           float* xs, hipStream_t st) {
-    const int K = w.cols;
-    if (m < 1 || m > mstride || mstride % 64) return fail("prep: GEMM rows must be 1..mstride, mstride % 64 == 0");
-    if (w.dtype == DT_Q8ROW) return fail("prep: GEMM operands are q4 only");
     XSrc r{};
     r.mode = XS_ROWS;
     r.x = x;
     r.ldx = ldx;
-    hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, r, K, w.dtype, w.kchunks * 4,
-                       planes, xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride);
-    return CMF_OK;
+    return launch_prep_src_gemm(w, r, m, mstride, planes, xs, st);
 }
 
 int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const int* jobs, int max_jobs,

@@ -254,7 +254,7 @@ int seam_matmat(const DevWeight& w_in, int row0, const float* xs, int b, int row
     if (grow((void**)&g_ss.x, &g_ss.x_cap, xb) != CMF_OK) return CMF_ERR;
     if (grow((void**)&g_ss.y, &g_ss.y_cap, yb) != CMF_OK) return CMF_ERR;
     hipStream_t st = stream();
-    if (b > MAXB && w.dtype != DT_Q8ROW && row0 == 0 && rows == w.rows) {
+    if (b > MAXB && row0 == 0 && rows == w.rows) {
         // large batch: one MFMA GEMM pass over the weights
         const size_t xb_all = (size_t)b * w.cols * sizeof(float), yb_all = (size_t)b * rows * sizeof(float);
         if (grow((void**)&g_ss.x, &g_ss.x_cap, xb_all) != CMF_OK) return CMF_ERR;

@@ -82,16 +82,21 @@ def test_ragged_shapes(gpu):
 
 
 def test_large_batch_split(gpu):
-    """q8 with b > 16 is served as GEMV launches of 16"""
+    """q8 with b > 16: the int8 MFMA GEMM (37 rows: one ragged 64-row tile)"""
     from cmf_amd import synth
     _check(gpu, synth.q8_normal(71, 256, 512), _x(72, 37, 512))
 
 
 @pytest.mark.parametrize("b", [17, 64, 130])
-@pytest.mark.parametrize("fmt", ["q4t", "q4tp"])
+@pytest.mark.parametrize("fmt", ["q4t", "q4tp", "q8"])
 def test_gemm_large_batch(gpu, fmt, b):
-    """q4 with b > 16: the MFMA GEMM (ragged batch tiles and row blocks)"""
+    """b > 16: the MFMA GEMM (ragged batch tiles and row blocks; q8 with an
+    odd count of 64-column chunks: 640 columns = 10, 704 = 11)"""
     from cmf_amd import synth
+    if fmt == "q8":
+        _check(gpu, synth.q8_uniform(73 + b, 272, 704), _x(74 + b, b, 704))
+        _check(gpu, synth.q8_uniform(75 + b, 4096, 1024), _x(76 + b, b, 1024))
+        return
     mk = synth.q4t_uniform if fmt == "q4t" else synth.q4tp_uniform
     _check(gpu, mk(73 + b, 272, 640), _x(74 + b, b, 640))
 
