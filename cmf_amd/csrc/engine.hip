@@ -19,6 +19,7 @@
 #include "layers.h"
 #include "runtime.h"
 #include "sample.h"
+#include "wave.h"
 
 namespace cmf {
 
@@ -26,7 +27,47 @@ struct LayerDev {
     float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
     DevWeight qkv, wo, gu, down;
     float *kc = nullptr, *vc = nullptr;
+    // routed-expert FFN (GraphFfn::Moe, gpu.rs:1248-1361): the router and the
+    // caller's MoE layer (borrowed) instead of gu / down
+    cmf_moe_s* moe = nullptr;
+    DevWeight router;
+    float* router_f32 = nullptr;  // a dense (f32 / f16 / bf16 in the file) router [ne][hidden] as f32
+    int n_experts = 0;
 };
+
+// rms_norm of nb rows (inference.rs:33-50: f64 mean of squares, the inverse
+// cast to f32, x * inv * w), one workgroup per row.
+__global__ __launch_bounds__(256) void k_rms_rows(const float* __restrict__ x, int ldx, const float* __restrict__ w,
+                                                  int H, double eps, float* __restrict__ out) {
+    __shared__ double red[4];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const float* row = x + (size_t)b * ldx;
+    double ss = 0.0;
+    for (int i = t; i < H; i += 256) ss += (double)row[i] * (double)row[i];
+    ss = wave_sum(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    const double tot = red[0] + red[1] + red[2] + red[3];
+    const float inv = 1.0f / (float)sqrt(tot / (double)H + eps);
+    for (int i = t; i < H; i += 256) out[(size_t)b * H + i] = row[i] * inv * w[i];
+}
+
+// Router logits of a dense f32 router (QTensor::F32 matvec, pool.rs:535-548):
+// logits[b][e] = sum_k W[e][k] x[b][k], one wave per expert row, the rows of
+// x from L2.
+__global__ __launch_bounds__(256) void k_router_f32(const float* __restrict__ W, const float* __restrict__ x,
+                                                    int ne, int H, int nb, float* __restrict__ out) {
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (e >= ne) return;  // uniform over the wave
+    const float* wr = W + (size_t)e * H;
+    for (int b = 0; b < nb; b++) {
+        const float* xr = x + (size_t)b * H;
+        float acc = 0.f;
+        for (int k = lane; k < H; k += 64) acc += wr[k] * xr[k];
+        acc = wave_sum(acc);
+        if (lane == 0) out[(size_t)b * ne + e] = acc;
+    }
+}
 
 }  // namespace cmf
 
@@ -55,6 +96,8 @@ struct cmf_model_s {
     int* out = nullptr;
     int out_cap = 0;
     float* h_tip = nullptr;
+    float* rlog = nullptr;  // router logits [MAXB][rlog_cap]
+    int rlog_cap = 0;
     uint8_t* planes = nullptr;  // prepared GEMV operand (largest prep_bytes of the model)
     float* xs = nullptr;        // its per-row scales [16]
     SampleBufs sb;
@@ -255,6 +298,28 @@ int gemv_f(cmf_model_s* m, const DevWeight& w, XSrc src, float* y, int ldy, int 
     return CMF_OK;
 }
 
+// The routed-expert FFN of a block (moe_ffn, pipeline.rs:10868-10915) over
+// nb <= 16 rows of h: router logits of the normed rows (a q8 / q4 router on
+// the GEMV with the norm staged inside, a dense one on k_router_f32 over
+// rows normed by k_rms_rows), then routing + the routed experts, and
+// h += their weighted sum.
+int moe_block_ffn(cmf_model_s* m, LayerDev& l, float* h, int nb, hipStream_t s) {
+    const auto& c = m->c;
+    const int H = c.hidden, ne = l.n_experts;
+    if (l.router_f32) {
+        hipLaunchKernelGGL(k_rms_rows, dim3(nb), dim3(256), 0, s, h, H, l.post_norm, H, c.eps, m->xrows);
+        hipLaunchKernelGGL(k_router_f32, dim3((ne + 3) / 4), dim3(256), 0, s, l.router_f32, m->xrows, ne, H, nb,
+                           m->rlog);
+        XSrc r{};
+        r.mode = XS_ROWS;
+        r.x = m->xrows;
+        r.ldx = H;
+        return moe_ffn_launch(l.moe, r, m->rlog, nb, h, H, true, s);
+    }
+    gemv_f(m, l.router, src_norm(h, H, l.post_norm, c.eps), m->rlog, ne, nb, false, s);
+    return moe_ffn_launch(l.moe, src_norm(h, H, l.post_norm, c.eps), m->rlog, nb, h, H, true, s);
+}
+
 // One decoder block over nb rows of the residual h at positions *pb + padd
 // + i (forward_layers_span, pipeline.rs:7981-8700):
 //   h += Wo attn(qk-norm/RoPE(Wqkv rms_norm(h)))
@@ -285,6 +350,10 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
     ra.x = m->ao;
     ra.ldx = nh * hd;
     gemv_f(m, l.wo, ra, h, H, nb, true, s);
+    if (l.moe) {
+        moe_block_ffn(m, l, h, nb, s);
+        return;
+    }
     // gate|up with the SwiGLU epilogue: gu_out [nb][I] = silu(g) * u
     gemv_f(m, l.gu, src_norm(h, H, l.post_norm, c.eps), m->gu_out, I, nb, false, s, EPI_SWIGLU);
     XSrc sd{};
@@ -458,6 +527,11 @@ int prefill_block(cmf_model_s* m, LayerDev& l, float* h, int cnt, const int* pb,
     ra.x = m->pf_ao;
     ra.ldx = nh * hd;
     if ((rc = gemm(l.wo, ra, cnt, h, H, true, s)) != CMF_OK) return rc;
+    if (l.moe) {  // the routed experts in batches of 16 rows (the verify-batch kernels)
+        for (int b0 = 0; b0 < cnt; b0 += MAXB)
+            if ((rc = moe_block_ffn(m, l, h + (size_t)b0 * H, std::min(MAXB, cnt - b0), s))) return rc;
+        return CMF_OK;
+    }
     if ((rc = gemm(l.gu, src_norm(h, H, l.post_norm, c.eps), cnt, m->pf_gu, 2 * I, false, s)) != CMF_OK) return rc;
     XSrc sd{};
     sd.mode = XS_SILU8;
@@ -589,7 +663,10 @@ int cmf_model_free(cmf_model m) {
     if (!m) return CMF_OK;
     (void)hipStreamSynchronize(stream());
     if (m->round_graph) (void)hipGraphExecDestroy(m->round_graph);
-    for (auto& l : m->L) free_layer(l);
+    for (auto& l : m->L) {
+        free_layer(l);
+        free_weight(l.router);
+    }
     free_layer(m->mtp);
     free_weight(m->lm);
     free_weight(m->emb);
@@ -604,7 +681,69 @@ int cmf_model_set_layer(cmf_model m, int li, const cmf_layer_desc* d) {
     if (!m || !d || li < 0 || li >= m->c.n_layers) return fail("set_layer: bad arguments");
     if (m->c.n_heads / m->c.n_kv * MAXB > 32 && m->c.n_heads / m->c.n_kv > 2)
         return fail("set_layer: the attention kernel serves <= 32 queries per KV head");
+    m->L[li].moe = nullptr;
+    free_weight(m->L[li].router);
     return upload_layer(m, m->L[li], d, true);
+}
+
+int cmf_model_set_layer_moe(cmf_model m, int li, const cmf_layer_desc* d, const cmf_tensor* router,
+                            cmf_moe moe) {
+    if (m) drop_graph(m);
+    if (!m || !d || !router || !moe || li < 0 || li >= m->c.n_layers) return fail("set_layer_moe: bad arguments");
+    const auto& c = m->c;
+    const int H = c.hidden, hd = c.head_dim, Q = c.n_heads * hd, KV = c.n_kv * hd;
+    if (moe_hidden(moe) != H) return fail("set_layer_moe: the MoE layer's hidden differs from the model's");
+    const int ne = moe_experts_count(moe);
+    const bool dense = router->dtype == 0 || router->dtype == 1 || router->dtype == 2;  // F32 / F16 / BF16
+    if (dense) {
+        if (router->rows != ne || router->cols != H || !router->bytes)
+            return fail("set_layer_moe: router must be [n_experts x hidden] with its bytes");
+    } else if (check_tensor(*router, ne, H, "router")) {
+        return CMF_ERR;
+    }
+    if (check_tensor(d->wq, Q, H, "wq") || check_tensor(d->wk, KV, H, "wk") || check_tensor(d->wv, KV, H, "wv") ||
+        check_tensor(d->wo, H, Q, "wo"))
+        return CMF_ERR;
+    LayerDev& l = m->L[li];
+    if (upload_f32(m, &l.in_norm, d->input_norm, H) || upload_f32(m, &l.post_norm, d->post_norm, H) ||
+        upload_f32(m, &l.q_norm, d->q_norm, hd) || upload_f32(m, &l.k_norm, d->k_norm, hd))
+        return CMF_ERR;
+    free_layer(l);
+    free_weight(l.router);
+    l.router_f32 = nullptr;
+    if (build_cat(l.qkv, {&d->wq, &d->wk, &d->wv}) || build_cat(l.wo, {&d->wo})) return CMF_ERR;
+    if (dense) {
+        // f16 / bf16 widen exactly to f32 (dequant_tensor; load_matrix keeps an f32 QTensor)
+        std::vector<float> w((size_t)ne * H);
+        for (size_t i = 0; i < w.size(); i++) {
+            if (router->dtype == 0) {
+                memcpy(&w[i], router->bytes + 4 * i, 4);
+            } else {
+                uint16_t u;
+                memcpy(&u, router->bytes + 2 * i, 2);
+                if (router->dtype == 2) {
+                    const uint32_t bits = (uint32_t)u << 16;
+                    memcpy(&w[i], &bits, 4);
+                } else {
+                    w[i] = (float)__builtin_bit_cast(_Float16, u);
+                }
+            }
+        }
+        if (upload_f32(m, &l.router_f32, w.data(), w.size())) return CMF_ERR;
+    } else if (build_cat(l.router, {router})) {
+        return CMF_ERR;
+    }
+    l.n_experts = ne;
+    if (!l.kc) {
+        const size_t n = (size_t)c.n_kv * c.max_seq * hd;
+        if (dalloc_t(m, &l.kc, n) || dalloc_t(m, &l.vc, n)) return CMF_ERR;
+    }
+    if (m->rlog_cap < ne) {
+        if (dalloc_t(m, &m->rlog, (size_t)MAXB * ne)) return CMF_ERR;
+        m->rlog_cap = ne;
+    }
+    l.moe = moe;
+    return CMF_OK;
 }
 
 int cmf_model_set_head(cmf_model m, const cmf_tensor* lm, const float* final_norm) {
@@ -648,8 +787,10 @@ int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const
 static int ready(cmf_model m) {
     if (!m) return fail("null model");
     if (!m->has_head) return fail("model has no lm_head (cmf_model_set_head)");
-    for (auto& l : m->L)
+    for (auto& l : m->L) {
         if (!l.qkv.w) return fail("model has unset layers (cmf_model_set_layer)");
+        if (l.moe && moe_prepare(l.moe) != CMF_OK) return CMF_ERR;  // before any captured round
+    }
     return CMF_OK;
 }
 

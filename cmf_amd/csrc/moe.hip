@@ -164,7 +164,8 @@ __global__ __launch_bounds__(1024) void k_moe_route_jobs(const float* __restrict
 // grid (hidden / 256, b): the k job rows of a thread are requested together.
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ yd, size_t y_stride, int ldy,
                                                      const int* __restrict__ slot, const float* __restrict__ w,
-                                                     int k, int hidden, float* __restrict__ out) {
+                                                     int k, int hidden, float* __restrict__ out, int ldo,
+                                                     int resid) {
     __shared__ int js[MOE_MAX_TOPK];
     __shared__ float ws[MOE_MAX_TOPK];
     const int t = blockIdx.y, h = blockIdx.x * blockDim.x + threadIdx.x;
@@ -179,7 +180,9 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
     for (int i = 0; i < k; i++) v[i] = yd[js[i] * y_stride + (size_t)t * ldy + h];
     float acc = 0.0f;
     for (int i = 0; i < k; i++) acc += ws[i] * v[i];
-    out[(size_t)t * hidden + h] = acc;
+    // resid: the decoder block's h += moe_ffn(x) (the sum completed first)
+    float* o = out + (size_t)t * ldo + h;
+    *o = resid ? *o + acc : acc;
 }
 
 }  // namespace cmf
@@ -228,14 +231,13 @@ static int moe_ready(cmf_moe m) {
 
 // Steps 3-7 on the routed batch (idx / w already on the device), k experts
 // per token.
-static int moe_experts(cmf_moe m, const float* d_x, int b, int k, float* d_out, hipStream_t s, bool numbered) {
+// x: the operand producer of the token rows (plain rows, or the block's
+// RMSNorm of the residual); out rows [b][ldo], resid: out += the FFN.
+static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int ldo, bool resid, hipStream_t s,
+                       bool numbered) {
     const int H = m->hidden, I = m->inter;
     if (!numbered) hipLaunchKernelGGL(k_moe_jobs, dim3(1), dim3(256), 0, s, m->idx, b, k, m->ne, m->jobs, m->slot);
-    XSrc rows{};
-    rows.mode = XS_ROWS;
-    rows.x = d_x;
-    rows.ldx = H;
-    int rc = launch_prep_src(m->gu[0], rows, b, m->px, m->xsx, s);
+    int rc = launch_prep_src(m->gu[0], x, b, m->px, m->xsx, s);
     const int mj = std::min(m->max_jobs, b * k);
     const size_t ygu_stride = (size_t)MAXB * 2 * I, yd_stride = (size_t)MAXB * H;
     if (rc == CMF_OK)
@@ -251,8 +253,28 @@ static int moe_experts(cmf_moe m, const float* d_x, int b, int k, float* d_out, 
         rc = gemv_grouped(m->down[0], m->d_down, m->jobs, mj, m->ph, m->ph_stride, m->xsh, m->yd, yd_stride, H, b, s);
     if (rc != CMF_OK) return rc;
     hipLaunchKernelGGL(k_moe_combine, dim3((H + 255) / 256, b), dim3(256), 0, s, m->yd, yd_stride, H, m->slot, m->w,
-                       k, H, d_out);
+                       k, H, d_out, ldo, resid ? 1 : 0);
     return CMF_OK;
+}
+
+static XSrc rows_src(const float* d_x, int H) {
+    XSrc r{};
+    r.mode = XS_ROWS;
+    r.x = d_x;
+    r.ldx = H;
+    return r;
+}
+
+int cmf::moe_prepare(cmf_moe m) { return moe_ready(m); }
+int cmf::moe_hidden(cmf_moe m) { return m ? m->hidden : 0; }
+int cmf::moe_experts_count(cmf_moe m) { return m ? m->ne : 0; }
+
+int cmf::moe_ffn_launch(cmf_moe m, const XSrc& x, const float* d_logits, int b, float* d_out, int ldo, bool resid,
+                   hipStream_t s) {
+    if (b < 1 || b > MAXB) return fail("moe: batch must be 1..16");
+    hipLaunchKernelGGL(k_moe_route_jobs, dim3(1), dim3(64 * MAXB), 0, s, d_logits, b, m->ne, m->top_k, m->norm_topk,
+                       m->scaling, m->idx, m->w, m->jobs, m->slot);
+    return moe_experts(m, x, b, m->top_k, d_out, ldo, resid, s, true);
 }
 
 extern "C" {
@@ -380,10 +402,7 @@ int cmf_moe_ffn_dev(cmf_moe m, const float* d_x, const float* d_logits, int b, f
     if (moe_ready(m) != CMF_OK) return CMF_ERR;
     if (b < 1 || b > MAXB) return fail("moe: batch must be 1..16");
     if (!d_x || !d_logits || !d_out) return fail("moe: null pointer");
-    hipStream_t s = stream();
-    hipLaunchKernelGGL(k_moe_route_jobs, dim3(1), dim3(64 * MAXB), 0, s, d_logits, b, m->ne, m->top_k, m->norm_topk,
-                       m->scaling, m->idx, m->w, m->jobs, m->slot);
-    const int rc = moe_experts(m, d_x, b, m->top_k, d_out, s, true);
+    const int rc = moe_ffn_launch(m, rows_src(d_x, m->hidden), d_logits, b, d_out, m->hidden, false, stream());
     if (rc != CMF_OK) return rc;
     CMF_HIP(hipGetLastError());
     return CMF_OK;
@@ -439,7 +458,7 @@ int cmf_moe_block(cmf_moe m, const float* x, const int32_t* experts, const float
     CMF_HIP(hipMemcpyAsync(m->x, x, sizeof(float) * m->hidden, hipMemcpyHostToDevice, s));
     CMF_HIP(hipMemcpyAsync(m->idx, experts, sizeof(int) * njobs, hipMemcpyHostToDevice, s));
     CMF_HIP(hipMemcpyAsync(m->w, weights, sizeof(float) * njobs, hipMemcpyHostToDevice, s));
-    const int rc = moe_experts(m, m->x, 1, njobs, m->out, s, false);
+    const int rc = moe_experts(m, rows_src(m->x, m->hidden), 1, njobs, m->out, m->hidden, false, s, false);
     if (rc != CMF_OK) return rc;
     CMF_HIP(hipMemcpyAsync(out, m->out, sizeof(float) * m->hidden, hipMemcpyDeviceToHost, s));
     CMF_HIP(hipStreamSynchronize(s));

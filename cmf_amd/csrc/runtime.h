@@ -28,3 +28,17 @@ int fill_q4src(Q4Src& s, int dtype, int rows, int cols, const uint8_t* payload, 
 void free_weight(DevWeight& w);
 
 }  // namespace cmf
+
+struct cmf_moe_s;
+namespace cmf {
+struct XSrc;
+// The MoE layer (moe.hip) as the decode engine drives it: descriptors
+// uploaded (before any capture), then routing + experts of b <= 16 rows of
+// the operand producer x on the stream, out [b][ldo] (resid: +=).
+int moe_prepare(cmf_moe_s* m);
+int moe_hidden(cmf_moe_s* m);
+int moe_experts_count(cmf_moe_s* m);
+int moe_ffn_launch(cmf_moe_s* m, const XSrc& x, const float* d_logits, int b, float* d_out, int ldo, bool resid,
+                   hipStream_t s);
+
+}  // namespace cmf

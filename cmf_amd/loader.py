@@ -26,7 +26,7 @@ _DEFAULTS = {
     "sliding_window_pattern": None, "rope_local_base_freq": None, "local_partial_rotary_factor": None,
     "global_head_dim": None, "num_global_kv_heads": None, "global_partial_rotary_factor": None,
     "final_logit_softcapping": None, "mla": None, "activation_situ_beta": None,
-    "activation_situ_linear_beta": None, "attn_logit_softcapping": None, "attn_v_norm": False, "moe": None,
+    "activation_situ_linear_beta": None, "attn_logit_softcapping": None, "attn_v_norm": False,
     "linear_core": None, "head_clusters": None, "rope_freq_factors": None, "logit_multiplier": None,
     "g3n": None, "kda_gate_lower_bound": None, "num_loops": 1, "loop_final_norm": False,
 }
@@ -46,6 +46,17 @@ def check_arch(arch):
     lt = arch["layer_types"]
     if len(lt) != arch["num_layers"] or any(t != "FullAttention" for t in lt):
         raise CmfError("this engine runs full-attention layers only (layer_types)")
+    moe = arch.get("moe")
+    if moe is not None:
+        # MoeConfig (cortiq-core/src/types.rs:251-281): the Qwen3-MoE subset
+        bad = [k for k, d in (("shared_expert_intermediate_size", None), ("router_sigmoid", False),
+                              ("router_resonance", False)) if moe.get(k, d) != d]
+        if bad:
+            raise CmfError("this engine runs softmax-routed experts without a shared expert; unsupported "
+                           "arch.moe fields: " + ", ".join(f"{k}={moe[k]!r}" for k in bad))
+        for k in ("num_experts", "top_k", "moe_intermediate_size"):
+            if k not in moe:
+                raise CmfError(f"header arch.moe: missing field `{k}`")
     return {"n_layers": int(arch["num_layers"]), "hidden": int(arch["hidden_size"]),
             "n_heads": int(arch["num_attention_heads"]), "n_kv": int(arch["num_kv_heads"]),
             "head_dim": int(arch["head_dim"]), "inter": int(arch["intermediate_size"]),
@@ -53,8 +64,10 @@ def check_arch(arch):
             "rope_theta": float(arch.get("rope_theta", 10000.0)), "eps": float(arch["rms_norm_eps"])}
 
 
-def matrix(f, name, shape=None):
-    """One weight matrix in the model-dict form (QTensor::from_model)."""
+def matrix(f, name, shape=None, dense_ok=False):
+    """One weight matrix in the model-dict form (QTensor::from_model);
+    dense_ok: an f32 / f16 / bf16 tensor is kept as stored (MoE routers,
+    which the reference converter writes at f16)."""
     e = f.tensor(name)
     if e is None:
         raise MissingTensor(f"tensor '{name}' not found in CMF directory")
@@ -64,6 +77,8 @@ def matrix(f, name, shape=None):
     if shape is not None and (rows, cols) != tuple(shape):
         raise CmfError(f"tensor '{name}': shape {[rows, cols]}, expected {list(shape)}")
     raw = f.entry_bytes(e)
+    if dense_ok and e.dtype in (0, 1, 2):  # f32 / f16 / bf16 kept as stored (widened to f32 on upload)
+        return {"dtype": e.dtype, "rows": rows, "cols": cols, "q": None, "row_scale": None, "bytes": raw}
     if e.dtype == DT_Q8ROW:
         n = rows * cols
         q = raw[:n].view(np.int8).reshape(rows, cols)
@@ -84,7 +99,7 @@ def vector(f, name, n):
     return dequant_vector(e, f.entry_bytes(e))
 
 
-def _layer(f, p, c):
+def _layer(f, p, c, arch=None):
     H, hd, nh, nkv, I = c["hidden"], c["head_dim"], c["n_heads"], c["n_kv"], c["inter"]
     return {
         "input_norm": vector(f, p + "input_layernorm.weight", H),
@@ -95,10 +110,39 @@ def _layer(f, p, c):
         "wk": matrix(f, p + "self_attn.k_proj.weight", (nkv * hd, H)),
         "wv": matrix(f, p + "self_attn.v_proj.weight", (nkv * hd, H)),
         "wo": matrix(f, p + "self_attn.o_proj.weight", (H, nh * hd)),
-        "gate": matrix(f, p + "mlp.gate_proj.weight", (I, H)),
-        "up": matrix(f, p + "mlp.up_proj.weight", (I, H)),
-        "down": matrix(f, p + "mlp.down_proj.weight", (H, I)),
+        **_ffn(f, p, c, arch),
     }
+
+
+def _ffn(f, p, c, arch):
+    """The block's FFN (build_ffn_at, loader.rs:~200-400): routed experts
+    when `mlp.gate.weight` (the router) is present, else dense SwiGLU."""
+    H, I = c["hidden"], c["inter"]
+    if arch is None or f.tensor(p + "mlp.gate.weight") is None:
+        return {"gate": matrix(f, p + "mlp.gate_proj.weight", (I, H)),
+                "up": matrix(f, p + "mlp.up_proj.weight", (I, H)),
+                "down": matrix(f, p + "mlp.down_proj.weight", (H, I))}
+    mc = arch.get("moe")
+    if mc is None:
+        raise CmfError(f"{p}mlp.gate.weight present but header has no arch.moe block")
+    for extra in ("mlp.shared_expert.gate_proj.weight", "mlp.expert_bias"):
+        if f.tensor(p + extra) is not None:
+            raise CmfError(f"{p}{extra}: shared experts and selection biases are not run by this engine")
+    Ie = int(mc["moe_intermediate_size"])
+    experts = []
+    for e in range(int(mc["num_experts"])):  # by tensor presence up to the header count (loader.rs)
+        q = f"{p}mlp.experts.{e}."
+        if f.tensor(q + "gate_proj.weight") is None:
+            break
+        experts.append({"gate": matrix(f, q + "gate_proj.weight", (Ie, H)),
+                        "up": matrix(f, q + "up_proj.weight", (Ie, H)),
+                        "down": matrix(f, q + "down_proj.weight", (H, Ie))})
+    if not experts:
+        raise CmfError(f"{p}: router present but no expert tensors")
+    router = matrix(f, p + "mlp.gate.weight", (len(experts), H), dense_ok=True)
+    return {"moe": {"router": router, "experts": experts, "top_k": int(mc["top_k"]),
+                    "norm_topk": bool(mc.get("norm_topk_prob", False)),
+                    "routed_scaling": float(mc.get("routed_scaling_factor") or 1.0)}}
 
 
 def load(f, max_seq=None):
@@ -113,7 +157,7 @@ def load(f, max_seq=None):
         c["max_seq"] = min(c["max_seq"], int(max_seq))
     H, V = c["hidden"], c["vocab"]
     m = {"cfg": c, "file": f}
-    m["layers"] = [_layer(f, f"model.layers.{i}.", c) for i in range(c["n_layers"])]
+    m["layers"] = [_layer(f, f"model.layers.{i}.", c, f.arch) for i in range(c["n_layers"])]
     m["final_norm"] = vector(f, "model.norm.weight", H)
     embed = matrix(f, "model.embed_tokens.weight", (V, H))
     if f.tensor("lm_head.weight") is not None:

@@ -30,10 +30,12 @@ def _f32(a, keep):
 
 
 def _layer(l, keep):
+    dense = "moe" not in l
+    empty = Tensor(0, 0, 0, None, None, None)
+    t = lambda n: _tensor(l[n], keep) if dense else empty
     return LayerDesc(_f32(l["input_norm"], keep), _f32(l["post_norm"], keep), _f32(l["q_norm"], keep),
                      _f32(l["k_norm"], keep), _tensor(l["wq"], keep), _tensor(l["wk"], keep),
-                     _tensor(l["wv"], keep), _tensor(l["wo"], keep), _tensor(l["gate"], keep),
-                     _tensor(l["up"], keep), _tensor(l["down"], keep))
+                     _tensor(l["wv"], keep), _tensor(l["wo"], keep), t("gate"), t("up"), t("down"))
 
 
 class Model:
@@ -45,8 +47,19 @@ class Model:
         h = C.c_void_p()
         check(lib().cmf_model_create(C.byref(mc), C.byref(h)))
         self.h = h
+        self.moes = []  # the MoE layers the model borrows (freed after it)
         for li, l in enumerate(sm["layers"]):
             keep = []
+            if "moe" in l:
+                from .moe import MoE
+                mo = l["moe"]
+                ex = mo["experts"]
+                moe = MoE(len(ex), c["hidden"], ex[0]["gate"]["rows"], mo["top_k"], ex,
+                          norm_topk=mo.get("norm_topk", True), routed_scaling=mo.get("routed_scaling", 1.0))
+                self.moes.append(moe)
+                check(lib().cmf_model_set_layer_moe(self.h, li, C.byref(_layer(l, keep)),
+                                                    C.byref(_tensor(mo["router"], keep)), moe.h))
+                continue
             check(lib().cmf_model_set_layer(self.h, li, C.byref(_layer(l, keep))))
         keep = []
         check(lib().cmf_model_set_head(self.h, C.byref(_tensor(sm["lm_head"], keep)),
@@ -163,6 +176,9 @@ class Model:
         if getattr(self, "h", None):
             lib().cmf_model_free(self.h)
             self.h = None
+        for moe in getattr(self, "moes", []):
+            moe.free()
+        self.moes = []
 
     def __del__(self):
         try:

@@ -141,14 +141,40 @@ def _layer(cfg, seed, attn_dt, ffn_dt, sigma, noise):
     }
 
 
+def _moe(cfg, seed, moe, ffn_dtype, sigma):
+    """A routed-expert FFN (Qwen3-MoE: softmax router, no shared expert):
+    router [n_experts x hidden] q8, experts gate/up [inter x hidden] and down
+    [hidden x inter] in ffn_dtype."""
+    H, ne, I = cfg["hidden"], moe["n_experts"], moe["inter"]
+    s = lambda i: (seed * 1000033 + i) & 0xFFFFFFFFFFFFFFFF
+    if moe.get("router_dtype", "q8") == "f16":  # the reference converter keeps routers at f16
+        rv = normal(s(1), ne * H, moe.get("router_sigma", 0.1)).astype(np.float16)
+        router = {"dtype": 1, "rows": ne, "cols": H, "q": None, "row_scale": None, "bytes": rv.view(np.uint8)}
+    else:
+        router = q8_normal(s(1), ne, H, moe.get("router_sigma", 0.1))
+    return {"router": router, "top_k": moe["top_k"],
+            "norm_topk": moe.get("norm_topk", True), "routed_scaling": moe.get("routed_scaling", 1.0),
+            "experts": [{"gate": _w(ffn_dtype, s(10 + 3 * e), I, H, sigma), "up": _w(ffn_dtype, s(11 + 3 * e), I, H, sigma),
+                         "down": _w(ffn_dtype, s(12 + 3 * e), H, I, sigma)} for e in range(ne)]}
+
+
 def synth_model(cfg=None, seed=1, attn_dtype=DT_Q8ROW, ffn_dtype=DT_Q4T, mtp=True, sigma=0.02,
-                norm_noise=0.0):
+                norm_noise=0.0, moe=None):
     """Random-init Qwen3-arch weights: N(0, sigma^2) then quantized (attention
-    q8, FFN q4t; lm_head, tied embedding and eh_proj q8)."""
+    q8, FFN q4t; lm_head, tied embedding and eh_proj q8).  moe = {"n_experts",
+    "top_k", "inter", "layers": [indices], optional "router_dtype": "q8" |
+    "f16"} makes those layers' FFNs routed experts (Qwen3-MoE); the MTP
+    block stays dense."""
     cfg = dict(QWEN3_06B if cfg is None else cfg)
     m = {"cfg": cfg}
     m["layers"] = [_layer(cfg, seed * 131 + li, attn_dtype, ffn_dtype, sigma, norm_noise)
                    for li in range(cfg["n_layers"])]
+    if moe:
+        for li in moe["layers"]:
+            L = m["layers"][li]
+            for n in ("gate", "up", "down"):
+                del L[n]
+            L["moe"] = _moe(cfg, seed * 131 + li, moe, ffn_dtype, sigma)
     m["lm_head"] = q8_normal(seed * 7 + 3, cfg["vocab"], cfg["hidden"], sigma)
     m["final_norm"] = _norm(seed * 7 + 4, cfg["hidden"], norm_noise)
     if mtp:

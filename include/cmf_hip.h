@@ -167,6 +167,7 @@ int cmf_time_copy(size_t bytes, int nbuf, int iters, float* avg_ms);
 
 /* ---- model: Qwen3-arch decoder + MTP head (pipeline.rs) --------------- */
 typedef struct cmf_model_s* cmf_model;
+typedef struct cmf_moe_s* cmf_moe;
 
 typedef struct {
     int n_layers, hidden, n_heads, n_kv, head_dim, inter, vocab, max_seq;
@@ -192,6 +193,16 @@ typedef struct {
 int cmf_model_create(const cmf_model_config* cfg, cmf_model* out);
 int cmf_model_free(cmf_model m);
 int cmf_model_set_layer(cmf_model m, int li, const cmf_layer_desc* d);
+/* A decoder block whose FFN is routed experts (FfnKind::Moe / GraphFfn::Moe,
+ * pipeline.rs:434-470, gpu.rs:1248-1361; Qwen3-MoE): d supplies the norms
+ * and attention weights (its gate/up/down are not read), router [n_experts x
+ * hidden] scores the block's normed rows (q8 / q4t / q4tp, or a dense router
+ * as the reference's converter stores it: dtype 0 f32, 1 f16, 2 bf16 in
+ * bytes, widened to f32 on upload), and moe (created
+ * with cmf_moe_create, experts set; hidden equal to the model's) runs
+ * moe_route + the experts; h += their weighted sum.  The model borrows moe:
+ * free it after the model. */
+int cmf_model_set_layer_moe(cmf_model m, int li, const cmf_layer_desc* d, const cmf_tensor* router, cmf_moe moe);
 /* lm_head (q8) doubles as the tied embedding table; final_norm [hidden]. */
 int cmf_model_set_head(cmf_model m, const cmf_tensor* lm_head, const float* final_norm);
 /* MtpModule (pipeline.rs:600-612). */
@@ -199,7 +210,6 @@ int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const
                       const cmf_layer_desc* layer, const float* norm);
 
 /* ---- MoE FFN (moe_ffn / moe_block) ------------------------------------ */
-typedef struct cmf_moe_s* cmf_moe;
 
 /* A routed-expert FFN layer (MoeFfn, pipeline.rs:10868-11045): n_experts
  * SwiGLU experts gate/up [inter x hidden], down [hidden x inter], softmax

@@ -173,7 +173,16 @@ static void block(const or_model* m, const or_layer* L, or_kv* kv, const float* 
     or_rms_norm(h, L->input_norm, H, m->cfg.eps, n1);
     attention(m, L, kv, inv_freq, n1, pos, a, 1);
     add_rms_norm(h, a, L->post_norm, H, m->cfg.eps, n1);
-    ffn(m, L, n1, f);
+    if (L->n_experts > 0) {
+        /* moe_ffn_forward (pipeline.rs:10868-11045): router logits of the
+         * normed row, routing, the routed experts' weighted sum */
+        float* lg = (float*)malloc(sizeof(float) * (size_t)L->n_experts);
+        or_matvec(&L->router, n1, lg, m->threads);
+        or_moe_ffn(L->experts, L->n_experts, L->top_k, L->norm_topk, L->routed_scaling, lg, n1, H, f, m->threads);
+        free(lg);
+    } else {
+        ffn(m, L, n1, f);
+    }
     for (int i = 0; i < H; i++) h[i] += f[i];
     free(n1);
     free(a);

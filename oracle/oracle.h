@@ -46,7 +46,7 @@ extern "C" {
 #endif
 
 /* TensorDtype ids, cortiq-core/src/types.rs:10-90 */
-enum { OR_Q8ROW = 3, OR_Q4T = 11, OR_Q4TP = 15 };
+enum { OR_F32 = 0, OR_Q8ROW = 3, OR_Q4T = 11, OR_Q4TP = 15 };
 
 /* ---- quant.rs ---------------------------------------------------------- */
 float or_f16_to_f32(uint16_t h);
@@ -67,7 +67,9 @@ typedef struct {
     int rows, cols;
     const int8_t* q;         /* q8: [rows*cols] */
     const float* row_scale;  /* q8: f32 per row (qtensor.rs:196-231) */
-    const uint8_t* bytes;    /* q4t / q4tp payload in the quant.rs layout */
+    const uint8_t* bytes;    /* q4t / q4tp payload in the quant.rs layout; F32: rows*cols floats
+                              * (an f16 / bf16 file tensor converted at load, as load_matrix does,
+                              * loader.rs:~510) */
 } or_qt;
 
 /* exact contract, qtensor.rs:9980-10047 / 5683-5717 / 4674-4716 */
@@ -128,9 +130,18 @@ typedef struct {
     double eps;
 } or_cfg;
 
+/* One decoder block.  n_experts > 0: the FFN is a routed MoE (MoeFfn,
+ * pipeline.rs:434-470; Qwen3-MoE: softmax router, no shared expert):
+ * logits = router * rms_norm(h), moe_route + moe_ffn_cpu
+ * (pipeline.rs:10780-10841, 11017-11030), experts [n_experts][3] =
+ * gate, up, down; gate/up/down of the layer itself are unused. */
 typedef struct {
     const float *input_norm, *post_norm, *q_norm, *k_norm;
     or_qt wq, wk, wv, wo, gate, up, down;
+    int n_experts, top_k, norm_topk;
+    float routed_scaling;
+    or_qt router;
+    const or_qt* experts;
 } or_layer;
 
 typedef struct {

@@ -34,7 +34,8 @@ class Cfg(C.Structure):
 class Layer(C.Structure):
     _fields_ = [("input_norm", C.c_void_p), ("post_norm", C.c_void_p), ("q_norm", C.c_void_p),
                 ("k_norm", C.c_void_p), ("wq", QT), ("wk", QT), ("wv", QT), ("wo", QT), ("gate", QT),
-                ("up", QT), ("down", QT)]
+                ("up", QT), ("down", QT), ("n_experts", C.c_int), ("top_k", C.c_int), ("norm_topk", C.c_int),
+                ("routed_scaling", C.c_float), ("router", QT), ("experts", C.c_void_p)]
 
 
 class Model(C.Structure):
@@ -162,9 +163,30 @@ def _f32(a, keep):
 
 
 def _layer(l, keep):
-    return Layer(_f32(l["input_norm"], keep), _f32(l["post_norm"], keep), _f32(l["q_norm"], keep),
-                 _f32(l["k_norm"], keep), qt(l["wq"], keep), qt(l["wk"], keep), qt(l["wv"], keep),
-                 qt(l["wo"], keep), qt(l["gate"], keep), qt(l["up"], keep), qt(l["down"], keep))
+    dense = "moe" not in l
+    empty = QT(0, 0, 0, None, None, None)
+    L = Layer(_f32(l["input_norm"], keep), _f32(l["post_norm"], keep), _f32(l["q_norm"], keep),
+              _f32(l["k_norm"], keep), qt(l["wq"], keep), qt(l["wk"], keep), qt(l["wv"], keep),
+              qt(l["wo"], keep), qt(l["gate"], keep) if dense else empty, qt(l["up"], keep) if dense else empty,
+              qt(l["down"], keep) if dense else empty)
+    if not dense:
+        mo = l["moe"]
+        ex = (QT * (3 * len(mo["experts"])))(*[qt(e[n], keep) for e in mo["experts"] for n in ("gate", "up", "down")])
+        keep.append(ex)
+        L.n_experts = len(mo["experts"])
+        L.top_k = mo["top_k"]
+        L.norm_topk = 1 if mo.get("norm_topk", True) else 0
+        L.routed_scaling = mo.get("routed_scaling", 1.0)
+        r = mo["router"]
+        if r["dtype"] in (1, 2):  # f16 / bf16 file tensor: widened to f32 at load (load_matrix)
+            raw = np.ascontiguousarray(r["bytes"], dtype=np.uint8).view(np.uint16)
+            f = raw.view(np.float16).astype(np.float32) if r["dtype"] == 1 else \
+                (raw.astype(np.uint32) << 16).view(np.float32)
+            r = {"dtype": 0, "rows": r["rows"], "cols": r["cols"], "q": None, "row_scale": None,
+                 "bytes": np.ascontiguousarray(f).view(np.uint8)}
+        L.router = qt(r, keep)
+        L.experts = C.cast(ex, C.c_void_p)
+    return L
 
 
 class OracleModel:

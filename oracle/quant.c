@@ -227,7 +227,16 @@ void or_matmat(const or_qt* w, const float* xs, int b, float* out, int threads) 
         float* sc = (w->dtype == OR_Q4TP) ? (float*)malloc(sizeof(float) * (gpr ? gpr : 1)) : NULL;
 #pragma omp for schedule(static)
         for (int r = 0; r < rows; r++) {
-            if (w->dtype == OR_Q8ROW) {
+            if (w->dtype == OR_F32) {
+                /* QTensor::F32 -> matvec_rows (pool.rs:535-548): sequential sum */
+                const float* row = (const float*)w->bytes + (size_t)r * cols;
+                for (int bi = 0; bi < b; bi++) {
+                    const float* x = xs + (size_t)bi * cols;
+                    float sum = 0.0f;
+                    for (int j = 0; j < cols; j++) sum += row[j] * x[j];
+                    out[(size_t)bi * rows + r] = sum;
+                }
+            } else if (w->dtype == OR_Q8ROW) {
                 /* qtensor.rs:10033-10046: dot_i8_f32(row, xs) * row_scale */
                 const int8_t* row = w->q + (size_t)r * cols;
                 for (int bi = 0; bi < b; bi++)

@@ -184,7 +184,12 @@ def round_q8_scales(t):
 def f16_model(sm):
     """The synthetic model with every q8 row scale rounded to f16."""
     def layer(l):
-        return {k: round_q8_scales(v) if isinstance(v, dict) else v for k, v in l.items()}
+        out = {k: round_q8_scales(v) if isinstance(v, dict) and k != "moe" else v for k, v in l.items()}
+        if "moe" in l:
+            mo = l["moe"]
+            out["moe"] = dict(mo, router=round_q8_scales(mo["router"]),
+                              experts=[{k: round_q8_scales(v) for k, v in ex.items()} for ex in mo["experts"]])
+        return out
     out = dict(sm, layers=[layer(l) for l in sm["layers"]], lm_head=round_q8_scales(sm["lm_head"]))
     if "embed" in sm:
         out["embed"] = round_q8_scales(sm["embed"])
@@ -221,6 +226,13 @@ def model_tensors(sm, norm_dtype=0):
         vec(p + "self_attn.k_norm.weight", l["k_norm"])
         for k, n in (("wq", "q_proj"), ("wk", "k_proj"), ("wv", "v_proj"), ("wo", "o_proj")):
             mat(p + f"self_attn.{n}.weight", l[k])
+        if "moe" in l:  # router (as stored: q8 or f16) + experts by index
+            mo = l["moe"]
+            mat(p + "mlp.gate.weight", mo["router"])
+            for e, ex in enumerate(mo["experts"]):
+                for k in ("gate", "up", "down"):
+                    mat(p + f"mlp.experts.{e}.{k}_proj.weight", ex[k])
+            return
         for k in ("gate", "up", "down"):
             mat(p + f"mlp.{k}_proj.weight", l[k])
 
@@ -243,5 +255,10 @@ def model_tensors(sm, norm_dtype=0):
 
 
 def write_model(path, sm, norm_dtype=0, **arch_extra):
+    moe = next((l["moe"] for l in sm["layers"] if "moe" in l), None)
+    if moe is not None and "moe" not in arch_extra:
+        arch_extra["moe"] = {"num_experts": len(moe["experts"]), "top_k": moe["top_k"],
+                             "moe_intermediate_size": moe["experts"][0]["gate"]["rows"],
+                             "norm_topk_prob": bool(moe.get("norm_topk", True))}
     arch = arch_of(sm["cfg"], mtp="mtp" in sm, tie="embed" not in sm, **arch_extra)
     return write(path, header_of(arch), model_tensors(sm, norm_dtype))

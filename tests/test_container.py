@@ -326,7 +326,15 @@ def _same_tensor(a, b):
 
 def _same_layer(a, b):
     for k in a:
-        if isinstance(a[k], dict):
+        if k == "moe":
+            ma, mb = a["moe"], b["moe"]
+            assert (ma["top_k"], ma["norm_topk"]) == (mb["top_k"], mb["norm_topk"])
+            _same_tensor(ma["router"], mb["router"])
+            assert len(ma["experts"]) == len(mb["experts"])
+            for ea, eb in zip(ma["experts"], mb["experts"]):
+                for n in ("gate", "up", "down"):
+                    _same_tensor(ea[n], eb[n])
+        elif isinstance(a[k], dict):
             _same_tensor(a[k], b[k])
         else:
             assert np.array_equal(np.asarray(a[k], np.float32), np.asarray(b[k], np.float32)), k
@@ -375,6 +383,33 @@ def test_loader_untied_embedding_and_q4tp(tmp_path):
     _same_tensor(sm["lm_head"], m["lm_head"])
     _same_tensor(sm["layers"][1]["down"], m["layers"][1]["down"])
     assert "mtp" not in m
+
+
+@pytest.mark.parametrize("router", ["f16", "q8"])
+def test_loader_moe_layers(tmp_path, router):
+    from cmf_amd import CmfError
+    """Qwen3-MoE blocks (build_ffn_at's MoE arm, loader.rs:~200-400): the
+    router `mlp.gate.weight` (f16 as the reference converter stores it, or
+    q8) and `mlp.experts.{e}.*` by presence; arch.moe gives top_k and
+    norm_topk_prob; the loaded model runs the oracle forward as the memory one"""
+    from cmf_amd import synth, loader
+    from oracle import oracle as orc
+    moe = dict(n_experts=6, top_k=2, inter=64, layers=[1], router_dtype=router)
+    sm = W.f16_model(synth.synth_model(TINY, seed=6, norm_noise=0.1, moe=moe))
+    p = tmp_path / "moe.cmf"
+    W.write_model(p, sm)
+    m = loader.load(str(p))
+    for a, b in zip(sm["layers"], m["layers"]):
+        _same_layer(a, b)
+    assert "moe" in m["layers"][1] and "moe" not in m["layers"][0]
+    toks = synth.ids(7, 3, TINY["vocab"])
+    a = [orc.OracleModel(sm, threads=2).forward(int(toks[0]), 0)]
+    b = [orc.OracleModel(m, threads=2).forward(int(toks[0]), 0)]
+    assert np.array_equal(a[0], b[0])
+    # what the engine does not run is refused by name
+    W.write_model(p, sm, moe={"num_experts": 6, "top_k": 2, "moe_intermediate_size": 64, "router_sigmoid": True})
+    with pytest.raises(CmfError, match="router_sigmoid"):
+        loader.load(str(p))
 
 
 def test_loader_refuses_what_the_engine_cannot_run(tmp_path):

@@ -64,3 +64,28 @@ def test_file_model_greedy_spec_tokens_equal_oracle(gpu, tmp_path):
     print("gpu", gt[:n].tolist(), "cpu", ot[:n].tolist(), flush=True)
     assert n >= 20 and gt[:n].tolist() == ot[:n].tolist()
     g.free()
+
+
+def test_file_moe_model_equals_memory_model_and_oracle(gpu, tmp_path):
+    """a Qwen3-MoE file (f16 router, q4t experts) through the loader: the
+    same hidden rows as the in-memory model, tokens equal to the oracle's"""
+    from cmf_amd import synth
+    from cmf_amd.model import Model
+    moe = dict(n_experts=8, top_k=2, inter=128, layers=[0], router_dtype="f16")
+    sm = W.f16_model(synth.synth_model(SMALL, seed=15, norm_noise=0.3, sigma=0.08, moe=moe))
+    p = tmp_path / "moe.cmf"
+    W.write_model(p, sm)
+    gf = Model.from_cmf(str(p))
+    gm = Model(sm)
+    ids = synth.ids(18, 8, SMALL["vocab"])
+    hf, _ = gf.forward_batch(ids, 0)
+    hm, _ = gm.forward_batch(ids, 0)
+    assert np.array_equal(hf, hm)
+    prompt = synth.ids(20, 16, SMALL["vocab"])
+    gf.prefill(prompt)
+    gt, _ = gf.decode(12, spec=True, k=4)
+    ot, _ = orc.OracleModel(sm).generate(prompt, 12, spec=True, k=4)
+    print("gpu", gt.tolist(), "cpu", ot.tolist(), flush=True)
+    assert gt.tolist() == ot.tolist()
+    gf.free()
+    gm.free()
