@@ -96,6 +96,8 @@ struct cmf_model_s {
     int* out = nullptr;
     int out_cap = 0;
     float* h_tip = nullptr;
+    uint8_t* plw = nullptr;  // the output projections' q8 operand, written by the attention merge
+    float* plw_cs = nullptr;
     float* rlog = nullptr;  // router logits [MAXB][rlog_cap]
     int rlog_cap = 0;
     uint8_t* planes = nullptr;  // prepared GEMV operand (largest prep_bytes of the model)
@@ -335,21 +337,39 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
     // the attention kernel holds at most 32 query heads per kv head and
     // MAXB new rows
     const int rows_per = std::min(MAXB, std::max(1, 32 / (nh / nkv)));
+    // a q8 output projection takes its operand straight from the merge:
+    // every merge wave writes its head's two 64-column chunks as int8 planes
+    // with their own chunk scales, so the wo GEMV neither stages the rows nor
+    // waits for a producer launch
+    const bool wo_planes = l.wo.dtype == DT_Q8ROW && (nh * hd) % 64 == 0;
     for (int b0 = 0; b0 < nb; b0 += rows_per) {
         AttnArgs at{m->qkv_out + (size_t)b0 * QKV, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq,
                     std::min(rows_per, nb - b0), nh, nkv, c.eps, pb, padd + b0, m->pm, m->pl, m->po, m->nch_cap,
                     m->ao + (size_t)b0 * nh * hd, 1};
+        if (wo_planes) {
+            at.wop = m->plw;
+            at.wop_cs = m->plw_cs;
+            at.wop_M = nb;
+            at.wop_b0 = b0;
+        }
         launch_attention(at, max_len, s);
     }
-    // the merged rows (ao) are the wo operand: prepared inside the wo GEMV
-    // for small batches, by a producer launch otherwise (measured on MI355X
-    // both beat a merge that also writes the prepared operand: its one
-    // workgroup per row serialises the 16 heads' merges)
-    XSrc ra{};
-    ra.mode = XS_ROWS;
-    ra.x = m->ao;
-    ra.ldx = nh * hd;
-    gemv_f(m, l.wo, ra, h, H, nb, true, s);
+    if (wo_planes) {
+        XSrc pw{};
+        pw.mode = XS_GLOBAL;
+        pw.planes = m->plw;
+        pw.cs = m->plw_cs;
+        pw.cs_ld = l.wo.kchunks;
+        (void)gemv(l.wo, pw, h, H, nb, 0, l.wo.rows, true, s);
+    } else {
+        // the merged rows (ao): prepared inside the wo GEMV for small
+        // batches, by a producer launch otherwise
+        XSrc ra{};
+        ra.mode = XS_ROWS;
+        ra.x = m->ao;
+        ra.ldx = nh * hd;
+        gemv_f(m, l.wo, ra, h, H, nb, true, s);
+    }
     if (l.moe) {
         moe_block_ffn(m, l, h, nb, s);
         return;
@@ -430,6 +450,10 @@ int alloc_scratch(cmf_model_s* m) {
         dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H) ||
         dalloc_t(m, &m->xs, 16))
         return CMF_ERR;
+    {
+        const size_t nk = (size_t)c.n_heads * hd / 64;  // 64-column chunks of the output projection's K
+        if (dalloc(m, (void**)&m->plw, nk * 192 * MAXB) || dalloc_t(m, &m->plw_cs, nk * MAXB)) return CMF_ERR;
+    }
     {
         // prepared operand of the widest GEMV: q8 K <= max(2H, nh*hd), q4 K <= max(H, I)
         const size_t k8 = ((size_t)std::max(2 * H, c.n_heads * hd) + 63) / 64;

@@ -39,6 +39,11 @@ struct XSrc {
     double eps;
     const uint8_t* planes;  // XS_GLOBAL
     const float* xs;
+    // XS_GLOBAL, q8 only: chunk-scaled planes (x of batch row b in 64-column
+    // chunk c ~= cs[b * cs_ld + c] (q0 + q1/128 + q2/16384)) instead of one
+    // scale per row (xs); written by a producer that owns whole chunks
+    const float* cs;
+    int cs_ld;
 };
 
 // One weight of a group (an MoE expert): its device blocks.

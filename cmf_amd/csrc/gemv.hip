@@ -425,7 +425,15 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
     if (a.src.mode != XS_GLOBAL && m > 2 && ks_override <= 0) ks = std::max(ks, FUSED_MIN_KS);
     size_t lds = 0;
     int xm = XM_GLOBAL;
-    if (a.src.mode == XS_GLOBAL) {
+    if (a.src.mode == XS_GLOBAL && a.src.cs) {
+        // chunk-scaled q8 planes: the planes (1 KiB aligned) then the chunk
+        // scales, rounded to whole 1 KiB direct-load chunks
+        if (w.dtype != DT_Q8ROW || a.src.cs_ld != w.kchunks || gridy > 1)
+            return fail("gemv: chunk-scaled operands are q8, contiguous, ungrouped");
+        lds = ((lds_bytes(w, m) + 1023) & ~(size_t)1023) + (((size_t)m * w.kchunks * 4 + 1023) & ~(size_t)1023);
+        if (lds > LDSX_MAX) return fail("gemv: chunk-scaled operand too large for LDS");
+        xm = XM_PREPC;
+    } else if (a.src.mode == XS_GLOBAL) {
         lds = lds_bytes(w, m);
         if (lds > LDSX_MAX) lds = 0;  // planes read in place from global memory
         xm = lds ? XM_PREP : XM_GLOBAL;

@@ -93,6 +93,14 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 // the operand is in LDS once at most the weight loads issued after it are
 // outstanding (vmcnt).  Wave w copies 1 KiB chunks w, w + nw, ... (indices
 // clamped to the last item, so the copy never reads past the planes).
+__device__ __forceinline__ void x_dma_ptr(const void* src, int n, uint8_t* lx) {
+    const uint4* g = (const uint4*)src;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    for (int c = wave; c * 64 < n; c += nw)
+        __builtin_amdgcn_global_load_lds((const void*)(g + min(c * 64 + lane, n - 1)),
+                                         (__attribute__((address_space(3))) void*)(lx + c * 1024), 16, 0, 0);
+}
 __device__ __forceinline__ void x_dma(const XSrc& s, int n, uint8_t* lx) {
     const uint4* g = (const uint4*)s.planes;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -315,7 +323,8 @@ __device__ __forceinline__ void prefetch_epilogue(const GemvArgs& a, int rb, int
 // slower per GEMV on MI355X: the per-workgroup staging sits on the critical
 // path of these latency-bound launches.)
 constexpr int SP = 4;  // weight steps per wave and work unit
-enum { XM_PREP = 0, XM_FUSED = 1, XM_GLOBAL = 2 };
+// XM_PREPC (q8): XM_PREP with one scale per (batch row, 64-column chunk)
+enum { XM_PREP = 0, XM_FUSED = 1, XM_GLOBAL = 2, XM_PREPC = 3 };
 
 template <int FMT, int NV, int KS, bool HL, int XM, int RB>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
@@ -616,9 +625,15 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     const int rb_first = rb;
     float rs_first, y_first[4];
     prefetch_epilogue(a, rb, r, s, M, (const float*)a.scale, rs_first, y_first);
+    // XM_PREPC: the chunk scales [M][nkc] (contiguous, cs_ld == nkc) follow
+    // the planes in LDS at a 1 KiB boundary, copied by direct loads like them
+    float* lcs = (float*)(smem + planes_lds_bytes(DT_Q8ROW, nkc, M));
     if constexpr (XM == XM_PREP) {
         x_dma(a.src, nkc * 4 * M * 3, smem);  // three planes
         xsv = ldg(a.src.xs + (threadIdx.x & 15));
+    } else if constexpr (XM == XM_PREPC) {
+        x_dma(a.src, nkc * 4 * M * 3, smem);
+        x_dma_ptr(a.src.cs, (M * nkc + 3) / 4, (uint8_t*)lcs);
     } else if constexpr (XM == XM_FUSED) {
         x_dma_rows(a.src, M, a.src.K, raw);
         // the raw rows arrive before the weight stream is requested: measured
@@ -632,6 +647,9 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     if constexpr (XM == XM_PREP) {
         wait_vmcnt<SP>();  // operand planes and xs are in
         if (threadIdx.x < 16) lxs[threadIdx.x] = xsv;
+    } else if constexpr (XM == XM_PREPC) {
+        wait_vmcnt<SP>();  // operand planes are in
+        if (threadIdx.x < 16) lxs[threadIdx.x] = 1.f;  // the chunk scales carry the operand's scale
     } else if constexpr (XM == XM_FUSED) {
         wait_vmcnt<SP>();  // raw rows are in
         __syncthreads();
@@ -651,6 +669,19 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
     const int4v* LP = L0 + pr * lpl;
     const int xoff = s * M + br, M4 = 4 * M;
     int4v a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0};
+    // XM_PREPC: per-chunk partials in f32, each chunk's int32 sums scaled
+    // by its chunk scale (and, PK, the plane weight of the lane's D rows
+    // 4s + v = p M + b)
+    float4v c0f = {0.f, 0.f, 0.f, 0.f}, c1f = c0f, c2f = c0f;
+    int cb_[4];
+    float cpw_[4];
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const int rr = 4 * s + v;
+        const int p = PK ? min(rr / M, 2) : 0, b = PK ? rr - p * M : rr;
+        cb_[v] = min(b, M - 1);
+        cpw_[v] = p == 0 ? 1.f : (p == 1 ? 0.0078125f : 6.103515625e-05f);
+    }
 
     auto process = [&](const int4v* wv) {
         const int c0 = kp * KS * SP + wave * SP;
@@ -658,7 +689,26 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
         for (int u = 0; u < SP; u++) {
             if (c0 + u < nkc) {
                 const int o = (c0 + u) * M4 + xoff;
-                if constexpr (PK) {
+                if constexpr (XM == XM_PREPC) {
+                    const int cc = c0 + u;
+                    const int4v zi = {0, 0, 0, 0};
+                    if constexpr (PK) {
+                        const int4v d = __builtin_amdgcn_mfma_i32_16x16x64_i8(LP[o], wv[u], zi, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) c0f[v] += (float)d[v] * (lcs[cb_[v] * nkc + cc] * cpw_[v]);
+                    } else {
+                        const int4v d0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(L0[o], wv[u], zi, 0, 0, 0);
+                        const int4v d1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(L0[lpl + o], wv[u], zi, 0, 0, 0);
+                        const int4v d2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(L0[2 * lpl + o], wv[u], zi, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 4; v++) {
+                            const float sc = lcs[cb_[v] * nkc + cc];
+                            c0f[v] += (float)d0[v] * sc;
+                            c1f[v] += (float)d1[v] * sc;
+                            c2f[v] += (float)d2[v] * sc;
+                        }
+                    }
+                } else if constexpr (PK) {
                     const int4v x0 = LP[o];
                     a0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, wv[u], a0, 0, 0, 0);
                 } else {
@@ -675,6 +725,14 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
         float4v f0 = {(float)a0[0], (float)a0[1], (float)a0[2], (float)a0[3]};
         float4v f1 = {(float)a1[0], (float)a1[1], (float)a1[2], (float)a1[3]};
         float4v f2 = {(float)a2[0], (float)a2[1], (float)a2[2], (float)a2[3]};
+        if constexpr (XM == XM_PREPC) {  // already scaled (plane weights included for PK)
+            f0 = c0f;
+            f1 = PK ? c0f * 0.f : c1f * 0.0078125f;
+            f2 = PK ? c0f * 0.f : c2f * 6.103515625e-05f;
+            c0f = float4v{0.f, 0.f, 0.f, 0.f};
+            c1f = c0f;
+            c2f = c0f;
+        }
         a0 = int4v{0, 0, 0, 0};
         a1 = a0;
         a2 = a0;
@@ -723,7 +781,8 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     const int b = 4 * s + v;
-                    const float tt = f0[v] + f1[v] * 0.0078125f + f2[v] * 6.103515625e-05f;
+                    const float tt = XM == XM_PREPC ? f0[v] + f1[v] + f2[v]
+                                                    : f0[v] + f1[v] * 0.0078125f + f2[v] * 6.103515625e-05f;
                     const float val = (tt * lxs[b & 15]) * rs;
                     const float u = __shfl_xor(val, 8);
                     if (r < 8 && b < M)
@@ -735,7 +794,8 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
                 for (int v = 0; v < 4; v++) {
                     const int b = 4 * s + v;
                     if (b < M) {
-                        const float tt = f0[v] + f1[v] * 0.0078125f + f2[v] * 6.103515625e-05f;
+                        const float tt = XM == XM_PREPC ? f0[v] + f1[v] + f2[v]
+                                                        : f0[v] + f1[v] * 0.0078125f + f2[v] * 6.103515625e-05f;
                         float* yp = a.y + (size_t)b * a.ldy + (row - a.row_lo);
                         const float val = (tt * lxs[b]) * rs;
                         *yp = a.resid ? (first ? y_first[v] : *yp) + val : val;
@@ -820,6 +880,7 @@ GemvKernel q8_by_xm(int xm, int ks) {
         case XM_PREP: return q8_by_ks<PK, XM_PREP>(ks);
         case XM_FUSED: return q8_by_ks<PK, XM_FUSED>(ks);
         case XM_GLOBAL: return q8_by_ks<PK, XM_GLOBAL>(ks);
+        case XM_PREPC: return q8_by_ks<PK, XM_PREPC>(ks);
     }
     return nullptr;
 }

@@ -30,6 +30,12 @@ struct AttnArgs {
     int nch;            // chunk capacity of the partial buffers
     float* out;
     int attend;         // 0: only append the rows' K/V (no queries, no output)
+    // optional: the merge also writes the rows as the chunk-scaled q8 operand
+    // of the output projection (planes [3][2 nh][4][wop_M] x 16 B, chunk scales
+    // [wop_M][2 nh]); this launch's rows are rows wop_b0.. of that operand
+    uint8_t* wop = nullptr;
+    float* wop_cs = nullptr;
+    int wop_M = 0, wop_b0 = 0;
 };
 // k_attention (chunk partials) then, with merge, k_attn_merge (rows of a.out).
 void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge = true);

@@ -221,8 +221,8 @@ __device__ __forceinline__ void append_rows(const AttnArgs& a, int g, int p0, in
 // are requested together, so a merge over <= CB chunks costs one memory
 // round trip (chunk indices clamped; chunks past `used` weigh 0).
 template <int CB>
-__device__ __forceinline__ void attn_merge_row(const float* pm, const float* pl, const float* po, int nch,
-                                               size_t row, int used, float* out) {
+__device__ __forceinline__ float2 attn_merge_row(const float* pm, const float* pl, const float* po, int nch,
+                                                 size_t row, int used, float* out) {
     constexpr int HD = 128;
     static_assert(64 % CB == 0, "chunk batch");
     const int lane = threadIdx.x & 63;
@@ -259,14 +259,36 @@ __device__ __forceinline__ void attn_merge_row(const float* pm, const float* pl,
         }
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
-    ((float2*)out)[lane] = make_float2(O.x * inv, O.y * inv);
+    const float2 res = make_float2(O.x * inv, O.y * inv);
+    ((float2*)out)[lane] = res;
+    return res;
 }
 
 // Merge of the chunk partials, one wave per (row, head): grid nb * nh.
+// With a.wop the wave also writes its head's 128 values as two 64-column
+// chunks of the output projection's q8 operand: x ~= cs (q0 + q1/128 +
+// q2/16384), cs = max|x| of the chunk / 127 (the layout and split of
+// prep8_row with one scale per chunk instead of per row).
 __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     const int rh = blockIdx.x, b = rh / a.nh;
     const int used = (*a.pbase + a.padd + b + ATT_C) / ATT_C;
-    attn_merge_row<32>(a.pm, a.pl, a.po, a.nch, (size_t)rh, used, a.out + (size_t)rh * 128);
+    const float2 o = attn_merge_row<32>(a.pm, a.pl, a.po, a.nch, (size_t)rh, used, a.out + (size_t)rh * 128);
+    if (!a.wop) return;
+    const int lane = threadIdx.x & 63, h = rh - b * a.nh, br = a.wop_b0 + b, nk = 2 * a.nh, M = a.wop_M;
+    float am = fmaxf(fabsf(o.x), fabsf(o.y));
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) am = fmaxf(am, __shfl_xor(am, off));  // each 32-lane half: one chunk
+    const float sx = am > 0.f ? am / 127.0f : 1.0f;
+    const float inv = 1.0f / sx;
+    uint32_t p0 = 0, p1 = 0, p2 = 0;
+    q8_split(o.x * inv, 0, p0, p1, p2);
+    q8_split(o.y * inv, 1, p0, p1, p2);
+    const int cc = 2 * h + (lane >> 5), j = (2 * lane) & 63;
+    const size_t off = ((size_t)(4 * cc + (j >> 4)) * M + br) * 16 + (j & 15);
+    *(uint16_t*)(a.wop + off) = (uint16_t)p0;
+    *(uint16_t*)(a.wop + (size_t)nk * 64 * M + off) = (uint16_t)p1;
+    *(uint16_t*)(a.wop + (size_t)nk * 128 * M + off) = (uint16_t)p2;
+    if ((lane & 31) == 0) a.wop_cs[(size_t)br * nk + cc] = sx;
 }
 
 // Decode attention of one layer for the nb rows at positions pos0 .. pos0+nb-1
