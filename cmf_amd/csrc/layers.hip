@@ -75,6 +75,23 @@ __device__ __forceinline__ float2 norm_rope(float x0, float x1, float w0, float 
     const float a = x0 * inv * w0, b = x1 * inv * w1;
     return make_float2(a * cs.x - b * cs.y, a * cs.y + b * cs.x);
 }
+// N head rows at once, as norm_rope with its own weights per row: the f64
+// wave reductions of the N rows interleaved.
+template <int N>
+__device__ __forceinline__ void norm_rope_n(float (&x0)[N], float (&x1)[N], const float2 (&cs)[N], const float (&w0)[N],
+                                            const float (&w1)[N], double eps) {
+    double ss[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) ss[i] = (double)x0[i] * (double)x0[i] + (double)x1[i] * (double)x1[i];
+    wave_sum_n<N>(ss);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const float inv = (float)(1.0 / sqrt(ss[i] / 128.0 + eps));
+        const float a = x0[i] * inv * w0[i], b = x1[i] * inv * w1[i];
+        x0[i] = a * cs[i].x - b * cs[i].y;
+        x1[i] = a * cs[i].y + b * cs[i].x;
+    }
+}
 __device__ __forceinline__ float2 head_norm_rope(float x0, float x1, const float* w, const float2* rope, int pos,
                                                  double eps, int lane) {
     return norm_rope(x0, x1, w[lane], w[lane + 64], rope[(size_t)pos * 64 + lane], eps);
@@ -186,35 +203,6 @@ __device__ __forceinline__ void attn_values_mfma(float (*S)[SC], const float (*V
     }
 }
 
-// K (k-norm + RoPE) and V rows of the new positions pos0 + b that fall in the
-// chunk at p0, one wave per row: appended to the cache and, when Kn is given,
-// kept in LDS (Kn[b], V[pos - p0]) for the chunk's own attention.
-__device__ __forceinline__ void append_rows(const AttnArgs& a, int g, int p0, int pos0, int wave, int lane,
-                                            float (*Kn)[128 + 4], float (*V)[128 + 4]) {
-    constexpr int HD = 128, C = ATT_C;
-    const int b_lo = max(0, p0 - pos0), b_hi = min(a.nb, p0 + C - pos0);
-    const int nw = blockDim.x >> 6;
-    for (int b = b_lo + wave; b < b_hi; b += nw) {
-        const int pos = pos0 + b;
-        const float* xk = a.qkv + (size_t)b * a.ldq + (size_t)(a.nh + g) * HD;
-        const float* xv = a.qkv + (size_t)b * a.ldq + (size_t)(a.nh + a.nkv + g) * HD;
-        const float2 k = head_norm_rope(xk[lane], xk[lane + 64], a.kn, a.rope, pos, a.eps, lane);
-        const float v0 = xv[lane], v1 = xv[lane + 64];
-        if (Kn) {
-            Kn[b][lane] = k.x;
-            Kn[b][lane + 64] = k.y;
-            V[pos - p0][lane] = v0;
-            V[pos - p0][lane + 64] = v1;
-        }
-        float* kd = a.kc + ((size_t)g * a.max_seq + pos) * HD;
-        float* vd = a.vc + ((size_t)g * a.max_seq + pos) * HD;
-        kd[lane] = k.x;
-        kd[lane + 64] = k.y;
-        vd[lane] = v0;
-        vd[lane + 64] = v1;
-    }
-}
-
 // Merge of the chunk partials of one (batch row b, head h) by one wave:
 // out = sum_c w_c o_c / sum_c w_c l_c with w_c = exp(m_c - M), M = max_c m_c.
 // The chunk maxima, sums and the first CB chunks' outputs (lane = dim pair)
@@ -291,6 +279,25 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
     if ((lane & 31) == 0) a.wop_cs[(size_t)br * nk + cc] = sx;
 }
 
+// KV append only (the MTP warm-up, attend = 0): row b of kv head g, one wave
+// per (b, g): k-norm + RoPE of K, V as projected (finish_projection +
+// append, attention.rs:818-890).  grid (nb, nkv), block 64.
+__global__ __launch_bounds__(64) void k_kv_append(AttnArgs a) {
+    constexpr int HD = 128;
+    const int b = blockIdx.x, g = blockIdx.y, lane = threadIdx.x;
+    const int pos = *a.pbase + a.padd + b;
+    const float* xk = a.qkv + (size_t)b * a.ldq + (size_t)(a.nh + g) * HD;
+    const float* xv = a.qkv + (size_t)b * a.ldq + (size_t)(a.nh + a.nkv + g) * HD;
+    const float v0 = xv[lane], v1 = xv[lane + 64];
+    const float2 k = head_norm_rope(xk[lane], xk[lane + 64], a.kn, a.rope, pos, a.eps, lane);
+    float* kd = a.kc + ((size_t)g * a.max_seq + pos) * HD;
+    float* vd = a.vc + ((size_t)g * a.max_seq + pos) * HD;
+    kd[lane] = k.x;
+    kd[lane + 64] = k.y;
+    vd[lane] = v0;
+    vd[lane + 64] = v1;
+}
+
 // Decode attention of one layer for the nb rows at positions pos0 .. pos0+nb-1
 // (pos0 = *pbase + padd), one workgroup per (kv head g, 64-position chunk c),
 // NQW = queries per wave (the hpk * nb queries of g, query qi on wave qi % 4):
@@ -307,7 +314,9 @@ __global__ __launch_bounds__(64) void k_attn_merge(AttnArgs a) {
 template <int NQW>
 __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     constexpr int HD = 128, C = ATT_C, NR = MAXB / 4;  // NR: new rows per wave
-    const int g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+    // the highest chunks (the new positions) first: past 256 workgroups the
+    // last ones share a CU, and the new-row chunk has the longest chain
+    const int g = blockIdx.x, c = gridDim.y - 1 - blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int nh = a.nh, hpk = nh / a.nkv, nq = a.nb * hpk;
     const int pos0 = *a.pbase + a.padd;
@@ -321,10 +330,6 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     __shared__ __align__(16) float V[C][VC];
     __shared__ __align__(16) float S[SR][SC];
     __shared__ __align__(16) float Kn[MAXB][HD + 4];
-    if (!a.attend) {  // KV append only (MTP warm-up)
-        if (p0 < stored) append_rows(a, g, p0, pos0, wave, lane, nullptr, nullptr);
-        return;
-    }
     if (p0 >= stored) return;
     const int np = min(C, stored - p0);
     const int nold = min(np, max(0, pos0 - p0));  // cached positions of this chunk
@@ -379,31 +384,59 @@ __global__ __launch_bounds__(256) void k_attention(AttnArgs a) {
     }
     // every load is issued before any of them is waited for
     __builtin_amdgcn_sched_barrier(0);
-    // queries: q-norm + RoPE
+    // queries: q-norm + RoPE and, in the chunk that holds new positions, the
+    // new rows' k-norm + RoPE, their wave reductions interleaved (x[NQW + j]:
+    // new row b_lo + wave + 4 j)
+    float x0[NQW + NR], x1[NQW + NR], w0[NQW + NR], w1[NQW + NR];
+    float2 cs[NQW + NR];
+#pragma unroll
+    for (int i = 0; i < NQW; i++) {
+        x0[i] = qx0[i];
+        x1[i] = qx1[i];
+        w0[i] = qw0;
+        w1[i] = qw1;
+        cs[i] = qcs[i];
+    }
+#pragma unroll
+    for (int j = 0; j < NR; j++) {
+        x0[NQW + j] = kx0[j];
+        x1[NQW + j] = kx1[j];
+        w0[NQW + j] = kw0;
+        w1[NQW + j] = kw1;
+        cs[NQW + j] = kcs[j];
+    }
+    if (b_lo < b_hi) {
+        norm_rope_n<NQW + NR>(x0, x1, cs, w0, w1, a.eps);
+    } else {
+        float (&y0)[NQW] = *reinterpret_cast<float (*)[NQW]>(x0);
+        float (&y1)[NQW] = *reinterpret_cast<float (*)[NQW]>(x1);
+        const float2 (&c2)[NQW] = *reinterpret_cast<const float2 (*)[NQW]>(cs);
+        const float (&v0)[NQW] = *reinterpret_cast<const float (*)[NQW]>(w0);
+        const float (&v1)[NQW] = *reinterpret_cast<const float (*)[NQW]>(w1);
+        norm_rope_n<NQW>(y0, y1, c2, v0, v1, a.eps);
+    }
 #pragma unroll
     for (int i = 0; i < NQW; i++) {
         const int qi = wave + 4 * i;
-        const float2 o = norm_rope(qx0[i], qx1[i], qw0, qw1, qcs[i], a.eps);
         if (qi < nq) {
-            Q[qi][lane] = o.x;
-            Q[qi][lane + 64] = o.y;
+            Q[qi][lane] = x0[i];
+            Q[qi][lane + 64] = x1[i];
         }
     }
-    // new rows: k-norm + RoPE, appended to the cache, kept in LDS
+    // new rows: appended to the cache, kept in LDS
 #pragma unroll
     for (int j = 0; j < NR; j++) {
         const int b = b_lo + wave + 4 * j;
         if (b < b_hi) {
             const int pos = pos0 + b;
-            const float2 k = norm_rope(kx0[j], kx1[j], kw0, kw1, kcs[j], a.eps);
-            Kn[b][lane] = k.x;
-            Kn[b][lane + 64] = k.y;
+            Kn[b][lane] = x0[NQW + j];
+            Kn[b][lane + 64] = x1[NQW + j];
             V[pos - p0][lane] = vx0[j];
             V[pos - p0][lane + 64] = vx1[j];
             float* kd = a.kc + ((size_t)g * a.max_seq + pos) * HD;
             float* vd = a.vc + ((size_t)g * a.max_seq + pos) * HD;
-            kd[lane] = k.x;
-            kd[lane + 64] = k.y;
+            kd[lane] = x0[NQW + j];
+            kd[lane + 64] = x1[NQW + j];
             vd[lane] = vx0[j];
             vd[lane + 64] = vx1[j];
         }
@@ -565,6 +598,10 @@ void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo
 }
 
 void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge) {
+    if (!a.attend) {  // a one-wave-per-row append: the attention grid's chunks would all idle
+        hipLaunchKernelGGL(k_kv_append, dim3(a.nb, a.nkv), dim3(64), 0, st, a);
+        return;
+    }
     const int nch = (max_len + ATT_C - 1) / ATT_C;
     const int nqw = (a.nb * (a.nh / a.nkv) + 3) / 4;  // queries per wave
     void (*k)(AttnArgs) = nullptr;

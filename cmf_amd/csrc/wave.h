@@ -53,6 +53,38 @@ __device__ __forceinline__ float wave_reduce_f32(float v, float ident, Op op) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// N f64 sums over the wave at once: every DPP step is applied to all N
+// values before the next, so the N chains overlap instead of running one
+// after another; the totals are wave-uniform.
+template <int N>
+__device__ __forceinline__ void wave_sum_n(double (&v)[N]) {
+    auto step = [&](auto ctrl, auto rows) {
+        constexpr int C = decltype(ctrl)::value, R = decltype(rows)::value;
+        uint32_t lo[N], hi[N];
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            const uint64_t u = __builtin_bit_cast(uint64_t, v[i]);
+            lo[i] = dpp_u32<C, R>((uint32_t)u, 0u);
+            hi[i] = dpp_u32<C, R>((uint32_t)(u >> 32), 0u);
+        }
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] += __builtin_bit_cast(double, ((uint64_t)hi[i] << 32) | lo[i]);
+    };
+    step(std::integral_constant<int, 0xb1>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x4e>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xa>{});
+    step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xc>{});
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v[i]);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+        v[i] = __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+    }
+}
+
 // sum over the wave (f64), the same value in every lane
 __device__ __forceinline__ double wave_sum(double v) {
     return wave_reduce_f64(v, 0.0, [](double x, double y) { return x + y; });

@@ -49,6 +49,22 @@ def test_verify_block_is_causal(small):
     assert rel_l2(np.stack(rows), hb) < 1e-5
 
 
+@pytest.mark.parametrize("b", [1, 3, 5])
+def test_small_batches_match_oracle(small, b):
+    """verify-sized batches (1 + K rows) against the oracle, row by row"""
+    sm, g = small
+    from cmf_amd import synth
+    ids = synth.ids(11, b, SMALL["vocab"])
+    hid, lg = g.forward_batch(ids, 0)
+    o = orc.OracleModel(sm)
+    for i, t in enumerate(ids):
+        h = o.forward(int(t), i)
+        e = rel_l2(hid[i], h)
+        print(f"b={b} row {i}: hidden rel {e:.2e}", flush=True)
+        assert e < 1e-4
+        assert rel_l2(lg[i], o.logits(h)) < 1e-4
+
+
 def _gen_pair(sm, g, prompt, n, spec, k, sampler_gpu=None, sampler_or=None, seed=0):
     g.prefill(prompt)
     gt, gst = g.decode(n, sampler=sampler_gpu, seed=seed, spec=spec, k=k)
