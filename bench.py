@@ -137,6 +137,81 @@ def moe_layer(cmf, synth, b=5, ne=128, hidden=2048, inter=768, top_k=8):
             "layer_us": round((ms.value + pms) * 1e3, 2)}
 
 
+def _cpu_rate(fn, min_s=0.5):
+    """Seconds per call of fn on the host (repeated to at least min_s)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s:
+            return dt / n
+
+
+def cpu_baseline(sm, cpu_state, prompt, args):
+    """The reference's CPU path restated (the C oracle) on the host cores:
+    spec decode from the GPU's prefilled state under both matvec contracts of
+    the reference (exact, CMF_SDOT=0; a8w8, split_act + integer dots, its
+    default on hosts with integer dot instructions), and the BASELINE configs'
+    CPU kernels (configs 1-3, 5).  value = the exact-contract decode."""
+    from oracle import oracle as orc
+    from cmf_amd import synth
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    n_cpu = 6
+    legs = {}
+    for contract in ("exact", "a8w8"):
+        o = orc.OracleModel(sm, threads=threads, a8w8=contract == "a8w8")
+        for li, (kk, vv) in enumerate(cpu_state["kv"]):
+            o.import_kv(li, kk, vv)
+        o.import_kv(-1, *cpu_state["mtp"])
+        tc = time.perf_counter()
+        ct, cst = o.decode(cpu_state["hidden"], cpu_state["next_pos"], prompt, n_cpu, spec=True, k=args.k)
+        tcpu = time.perf_counter() - tc
+        legs[contract] = {"tok/s": round(len(ct) / tcpu, 3), "tokens": len(ct), "rounds": cst.rounds,
+                          "s": round(tcpu, 1)}
+        if contract == "exact":
+            toks_exact = ct
+    # BASELINE configs 1-3 and 5 on the CPU path (exact contract; a8w8 at M=1)
+    kern = []
+    t1 = synth.q8_uniform(11, 4096, 4096)
+    x1 = synth.normal(7, 4096).reshape(1, 4096)
+    for a8 in (False, True):
+        sec = _cpu_rate(lambda: orc.matmat(t1, x1, threads=threads, a8w8=a8))
+        kern.append({"config": 1, "kernel": f"q8 4096x4096 M=1 ({'a8w8' if a8 else 'exact'})",
+                     "us": round(sec * 1e6, 1), "GB/s": round((4096 * 4096 + 4096 * 4) / sec / 1e9, 2)})
+    t2 = synth.q4t_uniform(31 + 12288, 12288, 4096)
+    for m, a8 in ((1, False), (1, True), (8, False)):
+        x2 = synth.normal(7, m * 4096).reshape(m, 4096)
+        sec = _cpu_rate(lambda: orc.matmat(t2, x2, threads=threads, a8w8=a8))
+        kern.append({"config": 2, "kernel": f"q4t 12288x4096 M={m} ({'a8w8' if a8 else 'exact'})",
+                     "us": round(sec * 1e6, 1), "GB/s": round(q4_bytes(12288, 4096, m, "q4t") / sec / 1e9, 2)})
+    t3 = synth.q4tp_uniform(41 + 12288, 12288, 4096)
+    x3 = synth.normal(7, 5 * 4096).reshape(5, 4096)
+    sec = _cpu_rate(lambda: orc.matmat(t3, x3, threads=threads))
+    kern.append({"config": 3, "kernel": "q4tp 12288x4096 M=5 (exact)", "us": round(sec * 1e6, 1),
+                 "GB/s": round(q4_bytes(12288, 4096, 5, "q4tp") / sec / 1e9, 2)})
+    ne, hidden, inter, top_k = 128, 2048, 768, 8
+    ex = [{"gate": synth.q4t_uniform(900 + 3 * e, inter, hidden), "up": synth.q4t_uniform(901 + 3 * e, inter, hidden),
+           "down": synth.q4t_uniform(902 + 3 * e, hidden, inter)} for e in range(ne)]
+    xm = synth.normal(5001, 5 * hidden).reshape(5, hidden)
+    lg = synth.normal(5002, 5 * ne).reshape(5, ne)
+    sec = _cpu_rate(lambda: orc.moe_ffn_rows(ex, top_k, lg, xm, threads=threads))
+    t8 = synth.q8_uniform(5003, 4096, 2048)
+    x8 = synth.normal(7, 5 * 2048).reshape(5, 2048)
+    sec8 = _cpu_rate(lambda: orc.matmat(t8, x8, threads=threads))
+    kern.append({"config": 5, "kernel": "MoE FFN M=5 (128 q4t experts, top-8) + q8 4096x2048 M=5 (exact)",
+                 "us": round((sec + sec8) * 1e6, 1)})
+    base = {"value": legs["exact"]["tok/s"], "unit": "tok/s", "cores": threads, "threads": threads,
+            "kind": "port",
+            "sample": f"C oracle (the reference's CPU path restated, OpenMP over {threads} host threads): "
+                      f"{legs['exact']['tokens']} tokens of spec decode (K={args.k}, {legs['exact']['rounds']} "
+                      f"rounds, exact contract) from the GPU's prefilled {args.ctx}-token state in "
+                      f"{legs['exact']['s']} s; the a8w8 contract and the configs' kernels beside it",
+            "contracts": legs, "kernels": kern}
+    return base, toks_exact
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -275,20 +350,7 @@ def main():
 
     # ---------------- CPU baseline: the oracle from the same state ----------------
     if cpu_state is not None:
-        from oracle import oracle as orc
-        threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-        o = orc.OracleModel(sm, threads=threads)
-        for li, (kk, vv) in enumerate(cpu_state["kv"]):
-            o.import_kv(li, kk, vv)
-        o.import_kv(-1, *cpu_state["mtp"])
-        n_cpu = 6
-        tc = time.perf_counter()
-        ct, cst = o.decode(cpu_state["hidden"], cpu_state["next_pos"], prompt, n_cpu, spec=True, k=args.k)
-        tcpu = time.perf_counter() - tc
-        out["cpu_baseline"] = {"value": round(len(ct) / tcpu, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-                               "sample": f"C oracle (exact contract), {len(ct)} tokens of spec decode "
-                                         f"(K={args.k}, {cst.rounds} rounds) from the GPU's prefilled "
-                                         f"{args.ctx}-token state, {tcpu:.1f} s"}
+        out["cpu_baseline"], ct = cpu_baseline(sm, cpu_state, prompt, args)
         n = min(len(ct), len(toks))
         out["cpu_gpu_tokens_equal"] = bool(n > 0 and ct[:n].tolist() == toks[:n].tolist())
     out["setup_s"] = round(time.perf_counter() - t_setup, 1)

@@ -35,6 +35,15 @@ static void add_rms_norm(float* h, const float* d, const float* w, int n, double
 }
 
 /* attention.rs:606-624: qk-norm, inv computed in f64 then cast. */
+/* The model's quantized matvecs under the contract it runs: exact (the
+ * default, CMF_SDOT=0) or a8w8 (split_act + integer dots, qtensor.rs:9237-9281,
+ * the reference's default on hosts with integer dot instructions); f32
+ * weights (a dense router) always take the exact path. */
+static void mv(const or_model* m, const or_qt* w, const float* x, float* out) {
+    if (m->a8w8 && w->dtype != OR_F32) or_matvec_a8w8(w, x, out, m->threads);
+    else or_matvec(w, x, out, m->threads);
+}
+
 static void rmsnorm_head(float* x, const float* w, int n, double eps) {
     double ss = 0.0;
     for (int i = 0; i < n; i++) ss += (double)x[i] * (double)x[i];
@@ -97,9 +106,9 @@ static void attention(const or_model* m, const or_layer* L, or_kv* kv, const flo
     float* q = (float*)malloc(sizeof(float) * (size_t)(nh * hd));
     float* k = (float*)malloc(sizeof(float) * (size_t)(nkv * hd));
     float* v = (float*)malloc(sizeof(float) * (size_t)(nkv * hd));
-    or_matvec(&L->wq, x, q, m->threads);
-    or_matvec(&L->wk, x, k, m->threads);
-    or_matvec(&L->wv, x, v, m->threads);
+    mv(m, &L->wq, x, q);
+    mv(m, &L->wk, x, k);
+    mv(m, &L->wv, x, v);
     /* finish_projection, attention.rs:818-890: qk-norm then RoPE */
     for (int h = 0; h < nh; h++) rmsnorm_head(q + h * hd, L->q_norm, hd, c->eps);
     for (int g = 0; g < nkv; g++) rmsnorm_head(k + g * hd, L->k_norm, hd, c->eps);
@@ -141,7 +150,7 @@ static void attention(const or_model* m, const or_layer* L, or_kv* kv, const flo
                 }
             }
         }
-        or_matvec(&L->wo, ao, out, m->threads);
+        mv(m, &L->wo, ao, out);
         free(ao);
         free(sc);
     }
@@ -155,10 +164,10 @@ static void ffn(const or_model* m, const or_layer* L, const float* x, float* out
     int I = L->gate.rows;
     float* g = (float*)malloc(sizeof(float) * (size_t)I);
     float* u = (float*)malloc(sizeof(float) * (size_t)I);
-    or_matvec(&L->gate, x, g, m->threads);
-    or_matvec(&L->up, x, u, m->threads);
+    mv(m, &L->gate, x, g);
+    mv(m, &L->up, x, u);
     for (int i = 0; i < I; i++) g[i] = or_silu(g[i]) * u[i];
-    or_matvec(&L->down, g, out, m->threads);
+    mv(m, &L->down, g, out);
     free(g);
     free(u);
 }
@@ -198,7 +207,7 @@ void or_logits(const or_model* m, const float* h, float* logits) {
     int H = m->cfg.hidden;
     float* n = (float*)malloc(sizeof(float) * (size_t)H);
     or_rms_norm(h, m->final_norm, H, m->cfg.eps, n);
-    or_matvec(&m->lm_head, n, logits, m->threads);
+    mv(m, &m->lm_head, n, logits);
     free(n);
 }
 
@@ -213,7 +222,7 @@ void or_mtp_step(const or_model* m, or_state* s, const float* hidden, uint32_t t
     or_embed(m, tok, e);
     or_rms_norm(e, m->enorm, H, m->cfg.eps, cat);      /* embedding FIRST */
     or_rms_norm(hidden, m->hnorm, H, m->cfg.eps, cat + H);
-    or_matvec(&m->eh_proj, cat, x, m->threads);
+    mv(m, &m->eh_proj, cat, x);
     if (logits == NULL) {
         float* n1 = (float*)malloc(sizeof(float) * (size_t)H);
         or_rms_norm(x, m->mtp.input_norm, H, m->cfg.eps, n1);
@@ -223,7 +232,7 @@ void or_mtp_step(const or_model* m, or_state* s, const float* hidden, uint32_t t
         block(m, &m->mtp, &s->mtp, s->inv_freq, x, pos);
         float* n = (float*)malloc(sizeof(float) * (size_t)H);
         or_rms_norm(x, m->mtp_norm, H, m->cfg.eps, n);
-        or_matvec(&m->lm_head, n, logits, m->threads);
+        mv(m, &m->lm_head, n, logits);
         free(n);
     }
     if (h_out) memcpy(h_out, x, sizeof(float) * (size_t)H);

@@ -155,6 +155,7 @@ typedef struct {
     or_layer mtp;
     int threads;
     or_qt embed;            /* untied q8 embedding table (loader.rs:714-724); q == NULL: lm_head */
+    int a8w8;               /* 1: the quantized matvecs of the forward under the a8w8 contract */
 } or_model;
 
 /* KV: per layer k[n_kv][max_seq][head_dim], same for v; len = stored rows.

@@ -41,7 +41,7 @@ class Layer(C.Structure):
 class Model(C.Structure):
     _fields_ = [("cfg", Cfg), ("layers", C.c_void_p), ("lm_head", QT), ("final_norm", C.c_void_p),
                 ("has_mtp", C.c_int), ("enorm", C.c_void_p), ("hnorm", C.c_void_p), ("mtp_norm", C.c_void_p),
-                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int), ("embed", QT)]
+                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int), ("embed", QT), ("a8w8", C.c_int)]
 
 
 class KV(C.Structure):
@@ -192,7 +192,7 @@ def _layer(l, keep):
 class OracleModel:
     """The CPU reference model over the same synthetic arrays the GPU uses."""
 
-    def __init__(self, sm, threads=8):
+    def __init__(self, sm, threads=8, a8w8=False):
         c = sm["cfg"]
         self.c = c
         self.sm = sm
@@ -208,6 +208,7 @@ class OracleModel:
             m.embed = qt(sm["embed"], self.keep)
         m.final_norm = _f32(sm["final_norm"], self.keep)
         m.threads = threads
+        m.a8w8 = 1 if a8w8 else 0
         if "mtp" in sm:
             mt = sm["mtp"]
             m.has_mtp = 1
@@ -326,6 +327,19 @@ def moe_route(logits, top_k, norm_topk=True, routed_scaling=1.0):
     w = np.empty(max(top_k, 1), np.float32)
     k = lib().or_moe_route(_p(lg), len(lg), top_k, 1 if norm_topk else 0, routed_scaling, _p(idx), _p(w))
     return idx[:k], w[:k]
+
+
+def moe_ffn_rows(experts, top_k, router_logits, xs, norm_topk=True, routed_scaling=1.0, threads=8):
+    """moe_ffn_cpu for each row of a batch (the experts marshalled once)."""
+    keep = []
+    arr = (QT * (3 * len(experts)))(*[qt(ex[n], keep) for ex in experts for n in ("gate", "up", "down")])
+    lg = np.ascontiguousarray(router_logits, dtype=np.float32)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    out = np.empty((xs.shape[0], experts[0]["down"]["rows"]), np.float32)
+    for i in range(xs.shape[0]):
+        lib().or_moe_ffn(C.cast(arr, C.c_void_p), len(experts), top_k, 1 if norm_topk else 0, routed_scaling,
+                         _p(lg[i]), _p(xs[i]), xs.shape[1], _p(out[i]), threads)
+    return out
 
 
 def moe_ffn(experts, top_k, router_logits, x, norm_topk=True, routed_scaling=1.0, threads=8):

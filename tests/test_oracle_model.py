@@ -355,3 +355,16 @@ def test_verify_step_sampled_shared_uniforms(acc):
     assert nxt == int(ids[int(np.argmax(u_c < cdf))])
     ref = _reference_state(acc, np.concatenate([prompt, s[:3]]))
     _assert_state_equal(o, ref, TINY["n_layers"])
+
+
+def test_a8w8_contract_switch(tiny):
+    """OracleModel(a8w8=True) routes the forward's quantized matvecs through
+    the a8w8 contract (split_act + integer dots, qtensor.rs:9237-9281): the
+    hidden state moves by the contract's activation rounding (~1e-2), and the
+    exact model is untouched by the switch"""
+    he = orc.OracleModel(tiny, threads=2).forward(5, 0)
+    ha = orc.OracleModel(tiny, threads=2, a8w8=True).forward(5, 0)
+    he2 = orc.OracleModel(tiny, threads=2, a8w8=False).forward(5, 0)
+    rel = np.linalg.norm(he - ha) / np.linalg.norm(he)
+    assert 1e-4 < rel < 5e-2
+    assert np.array_equal(he, he2)
