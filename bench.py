@@ -328,6 +328,21 @@ def main():
     out["spec"] = {"k": args.k, "rounds": args.steps, "tokens": produced, "accepted_total": st.accepted,
                    "drafted_total": st.drafted, "device_ms_per_round": round(st.device_ms / max(args.steps, 1), 4),
                    "acceptance": round(st.accepted / max(st.drafted, 1), 4)}
+    # config 4 at T = 0.8 (sampler defaults otherwise, repetition penalty 1.0):
+    # the device sparse chain + sampled acceptance, continuing from this state
+    from cmf_amd import SamplerConfig
+    n_s = max(8, args.steps // 4)
+    model.decode_begin(SamplerConfig(temperature=0.8, repetition_penalty=1.0), seed=7)
+    model.decode_rounds(2, spec=True, k=args.k)
+    cmf.lib().cmf_sync()
+    s0 = len(model.tokens())
+    ts0 = time.perf_counter()
+    sst = model.decode_rounds(n_s, spec=True, k=args.k)
+    cmf.lib().cmf_sync()
+    dts = time.perf_counter() - ts0
+    out["sampled"] = {"temperature": 0.8, "top_k": 40, "top_p": 0.9, "min_p": 0.05, "rounds": n_s,
+                      "tokens": len(model.tokens()) - s0, "tok/s": round((len(model.tokens()) - s0) / dts, 2),
+                      "ms_per_round": round(dts * 1e3 / n_s, 4), "accepted": sst.accepted, "drafted": sst.drafted}
     # HBM bytes a round must stream at ctx ~2048 (weights + KV), for context
     c = sm["cfg"]
     layer_w = sum(len(t["bytes"]) if t["bytes"] is not None else t["q"].nbytes + t["row_scale"].nbytes

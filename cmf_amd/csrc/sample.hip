@@ -2,19 +2,22 @@
 //
 // Selection: every block takes SLICE logits of one row, finds the top-k by
 // (value desc, id asc) with an in-LDS radix select over order-preserving
-// keys, and records the slice max and sum of exp((l - max)/T); a merge block
-// per row selects the row's top-k from the slice lists and combines the
-// sums (sum_all = sum_s ssum_s * exp((smax_s - lmax)/T)).  The O(k) chain of
+// keys (each pass's bucket found by a block-wide scan), and records the slice
+// max and sum of exp((l - max)/T); a merge block per row selects the row's
+// top-k from the slice lists and combines the sums (sum_all = sum_s ssum_s *
+// exp((smax_s - lmax)/T), in slice order).  The O(k) chain of
 // sparse_distribution_into (sampler.rs:440-514), draw_sparse (:661-671) and
-// spec_accept_or_correct_sparse (:683-711) then runs in one thread with the
-// SplitMix64 state (sampler.rs:54-84) kept in HBM, consuming uniforms in the
-// reference's order.  Ties at the k-th value keep the k lowest ids (the
+// spec_accept_or_correct_sparse (:683-711) then runs on one wave (lane =
+// candidate; every order-dependent float sum walks the lanes in the
+// reference's order) with the SplitMix64 state (sampler.rs:54-84) kept in
+// HBM, consuming uniforms in the reference's order.  Ties at the k-th value keep the k lowest ids (the
 // reference also keeps every further tie; continuous logits have none).
 #include <math.h>
 
 #include "../../include/cmf_hip.h"
 #include "common.h"
 #include "sample.h"
+#include "wave.h"
 
 namespace cmf {
 
@@ -32,6 +35,40 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
     return va > vb || (va == vb && ia < ib);
 }
 
+// Bucket selection of one radix pass: with the 256 bucket counts of the keys
+// still in play (hist, 256 threads) and kk of them still needed, the bucket d
+// scanning 255 -> 0 where the count above d is < kk and with d >= kk, and kk
+// less the count above.  A block-wide scan replaces the serial walk over the
+// buckets (a wave-level inclusive scan, then the waves' totals).  With no
+// such bucket the prefix stays and kk is unchanged (d = 0).
+__device__ __forceinline__ void pick_bucket(const int* hist, int shift, uint32_t* s_prefix, uint32_t* s_mask,
+                                            int* s_kk, int* wsum) {
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int kk = *s_kk;
+    const uint32_t pre = *s_prefix, msk = *s_mask;
+    const int h = hist[255 - t];
+    int p = h;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(p, o);
+        if (lane >= o) p += u;
+    }
+    if (lane == 63) wsum[w] = p;
+    __syncthreads();
+    int base = 0;
+    for (int i = 0; i < w; i++) base += wsum[i];
+    p += base;
+    __syncthreads();  // every thread has read kk, the prefix and wsum
+    if (t == 0) {
+        *s_mask = msk | (0xFFu << shift);  // prefix unchanged (d = 0) unless a bucket is picked below
+    }
+    if (p >= kk && p - h < kk) {
+        *s_prefix = pre | ((uint32_t)(255 - t) << shift);
+        *s_kk = kk - (p - h);
+    }
+    __syncthreads();
+}
+
 // Top-k of (vals, ids) in LDS, n entries, 256 threads.  Writes the k winners
 // sorted by (value desc, id asc) into ov/oi.  scratch: hist[256], ties.
 __device__ void select_topk(const float* vals, const int* ids, int n, int k, float* ov, int* oi,
@@ -39,12 +76,12 @@ __device__ void select_topk(const float* vals, const int* ids, int n, int k, flo
     const int t = threadIdx.x;
     __shared__ uint32_t s_prefix, s_mask;
     __shared__ int s_kk;
+    __shared__ int wsum[4];
     if (t == 0) {
         s_prefix = 0;
         s_mask = 0;
         s_kk = k < n ? k : n;
     }
-    __syncthreads();
     const int kk_total = k < n ? k : n;
     for (int shift = 24; shift >= 0; shift -= 8) {
         hist[t] = 0;
@@ -55,21 +92,7 @@ __device__ void select_topk(const float* vals, const int* ids, int n, int k, flo
             if ((key & msk) == pre) atomicAdd(&hist[(key >> shift) & 255], 1);
         }
         __syncthreads();
-        if (t == 0) {
-            int cum = 0, kk = s_kk, sel = 0;
-            for (int d = 255; d >= 0; d--) {
-                if (cum + hist[d] >= kk) {
-                    sel = d;
-                    kk -= cum;
-                    break;
-                }
-                cum += hist[d];
-            }
-            s_prefix = pre | ((uint32_t)sel << shift);
-            s_mask = msk | (0xFFu << shift);
-            s_kk = kk;
-        }
-        __syncthreads();
+        pick_bucket(hist, shift, &s_prefix, &s_mask, &s_kk, wsum);
     }
     const uint32_t kth = s_prefix;
     const int need_eq = s_kk;  // entries equal to kth still needed
@@ -168,23 +191,19 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
             }
         }
     }
-    red[t] = mx;
+    // slice max and sum of exp((l - max) / T): wave reductions, then the
+    // four waves' values in wave order
+    const int w = t >> 6;
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red[w] = mx;
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (t < o) red[t] = fmaxf(red[t], red[t + o]);
-        __syncthreads();
-    }
-    mx = red[0];
-    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float se = 0.f;
     for (int i = t; i < n; i += 256) se += expf((vals[i] - mx) / c.t);
-    red[t] = se;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-        if (t < o) red[t] += red[t + o];
-        __syncthreads();
-    }
-    select_topk(vals, ids, n, c.k, ov, oi, hist, tv, ti, cnt);
+    se = wave_sum(se);
+    __syncthreads();  // red[] reads above are done
+    if ((t & 63) == 0) red[4 + w] = se;
+    select_topk(vals, ids, n, c.k, ov, oi, hist, tv, ti, cnt);  // (its barriers publish red[4..7])
     const size_t base = ((size_t)row * nslices + sl) * SPARSE_K_MAX;
     const int m = min(c.k, n);
     if (t < SPARSE_K_MAX) {
@@ -193,7 +212,7 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
     }
     if (t == 0) {
         smax[(size_t)row * nslices + sl] = mx;
-        ssum[(size_t)row * nslices + sl] = red[0];
+        ssum[(size_t)row * nslices + sl] = (red[4] + red[5]) + (red[6] + red[7]);
     }
 }
 
@@ -240,17 +259,27 @@ __global__ __launch_bounds__(256) void k_topk_merge(int V, SampCfg c, int nslice
         rid[(size_t)row * SPARSE_K_MAX + t] = t < k ? oi[t] : -1;
         rv[(size_t)row * SPARSE_K_MAX + t] = t < k ? ov[t] : -INFINITY;
     }
+    // sum_all = sum over slices (in slice order) of ssum_s exp((smax_s - lmax)/T):
+    // the terms in parallel, the sum by one thread
+    __shared__ float term[256];
+    const float lm = ov[0];
+    for (int s2 = t; s2 < nslices; s2 += 256)
+        term[s2] = ssum[(size_t)row * nslices + s2] * expf((smax[(size_t)row * nslices + s2] - lm) / c.t);
+    __syncthreads();
     if (t == 0) {
-        const float lm = ov[0];
         float tot = 0.f;
-        for (int s = 0; s < nslices; s++)
-            tot += ssum[(size_t)row * nslices + s] * expf((smax[(size_t)row * nslices + s] - lm) / c.t);
+        for (int s2 = 0; s2 < nslices; s2++) tot += term[s2];
         lmax[row] = lm;
         sum[row] = tot;
     }
 }
 
-// ---- the O(k) chain, one thread ----
+// ---- the O(k) chain on one wave ----
+// Lane i holds candidate i of a list; every order-dependent sum (the top-p
+// cumulative, the normalisation, the inverse-CDF draw, the residual total)
+// is taken in the reference's order by a wave-uniform walk over the lanes
+// (readlane), so the floating-point results are those of the sequential
+// chain; sorting by id and membership lookups are lane-parallel.
 __device__ __forceinline__ float next_f32(unsigned long long* s) {
     *s += 0x9E3779B97F4A7C15ull;
     unsigned long long z = *s;
@@ -259,44 +288,82 @@ __device__ __forceinline__ float next_f32(unsigned long long* s) {
     z ^= z >> 31;
     return (float)(z >> 40) / 16777216.0f;
 }
+__device__ __forceinline__ float lanef(float v, int i) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), i));
+}
+__device__ __forceinline__ int lanei(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
 
-// sparse_distribution_into over the merged candidates of one row: ids
-// ascending, probabilities summing to 1.  Returns the count (0 = filtered).
-__device__ int sparse_dist(const int* rid, const float* rv, float lmax, float sum_all, SampCfg c,
-                           int* oid, float* op) {
-    int n = 0;
-    float cum = 0.f;
-    bool cut = false;
-    for (int i = 0; i < c.k && !cut; i++) {
-        const int id = rid[i];
-        if (id < 0) break;
-        const float e = expf((rv[i] - lmax) / c.t);
-        if (c.min_p > 0.f && e < c.min_p) continue;
-        const float pr = e / sum_all;
-        if (pr <= 0.f) continue;
-        oid[n] = id;
-        op[n] = pr;
-        n++;
-        cum += pr;
-        if (c.top_p < 1.f && c.top_p > 0.f && cum >= c.top_p) cut = true;
-    }
-    float s = 0.f;
-    for (int i = 0; i < n; i++) s += op[i];
-    if (!(s > 0.f)) return 0;
-    for (int i = 0; i < n; i++) op[i] /= s;
-    for (int i = 1; i < n; i++) {  // by id
-        const int id = oid[i];
-        const float p = op[i];
-        int j = i - 1;
-        while (j >= 0 && oid[j] > id) {
-            oid[j + 1] = oid[j];
-            op[j + 1] = op[j];
-            j--;
+// A sparse list over the wave: lane i < n holds (id, p), ids ascending.
+struct WList {
+    int id;
+    float p;
+    int n;
+};
+
+// sparse_distribution_into (sampler.rs:440-514) over the merged candidates of
+// one row (value desc, id asc; lane i = candidate i): min-p filter, p = e /
+// sum_all, top-p cut (cumulative in candidate order), renormalised (sum in
+// candidate order), then ids ascending.  n = 0: everything filtered.
+__device__ WList wsparse_dist(const int* rid, const float* rv, float lmax, float sum_all, SampCfg c) {
+    const int lane = threadIdx.x;
+    const int id = lane < c.k ? rid[lane] : -1;
+    const float v = lane < c.k ? rv[lane] : -INFINITY;
+    const float e = expf((v - lmax) / c.t);
+    const float pr = e / sum_all;
+    // kept: in the list, past min-p, p > 0; the list stops at the first id < 0
+    const bool kept = id >= 0 && !(c.min_p > 0.f && e < c.min_p) && pr > 0.f;
+    const int nlist = c.k < 64 ? c.k : 64;
+    int stop = nlist;  // first index with id < 0
+    for (int i = 0; i < nlist; i++)
+        if (lanei(id, i) < 0) {
+            stop = i;
+            break;
         }
-        oid[j + 1] = id;
-        op[j + 1] = p;
+    // top-p: the first kept candidate at which the cumulative reaches top_p
+    // ends the list (inclusive)
+    int last = stop;
+    if (c.top_p < 1.f && c.top_p > 0.f) {
+        float cum = 0.f;
+        for (int i = 0; i < stop; i++) {
+            if (!__builtin_amdgcn_readlane((int)kept, i)) continue;
+            cum += lanef(pr, i);
+            if (cum >= c.top_p) {
+                last = i + 1;
+                break;
+            }
+        }
     }
-    return n;
+    const bool in = kept && lane < last;
+    float s = 0.f;
+    for (int i = 0; i < last; i++)
+        if (__builtin_amdgcn_readlane((int)in, i)) s += lanef(pr, i);
+    WList out;
+    out.n = __builtin_popcountll(__ballot(in));
+    if (!(s > 0.f)) {
+        out.n = 0;
+        out.id = -1;
+        out.p = 0.f;
+        return out;
+    }
+    const float pn = pr / s;
+    // rank by id among the kept (ids are distinct)
+    int rank = 0;
+    for (int i = 0; i < last; i++)
+        if (__builtin_amdgcn_readlane((int)in, i) && lanei(id, i) < id) rank++;
+    __shared__ int sid[64];
+    __shared__ float sp[64];
+    if (in) {
+        sid[rank] = id;
+        sp[rank] = pn;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    out.id = lane < out.n ? sid[lane] : -1;
+    out.p = lane < out.n ? sp[lane] : 0.f;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    return out;
 }
 
 // the greedy fallback of a fully filtered row: argmax, ties to the highest id
@@ -308,7 +375,7 @@ __device__ int row_argmax(const int* rid, const float* rv, int k) {
 }
 
 // The chain's uniform source: the caller's uniforms first (a verify step
-// under shared uniforms), then the SplitMix64 stream.
+// under shared uniforms), then the SplitMix64 stream (wave-uniform).
 struct Uni {
     unsigned long long rng;
     const float* u;
@@ -316,93 +383,114 @@ struct Uni {
     __device__ float next() { return used < n ? u[used++] : next_f32(&rng); }
 };
 
-__device__ int draw_sparse(const int* id, const float* p, int n, Uni* rng) {
+// draw_sparse (sampler.rs:661-671): inverse CDF in list order
+__device__ int wdraw(const WList& l, Uni* rng) {
     const float r = rng->next();
     float cum = 0.f;
-    for (int i = 0; i < n; i++) {
-        cum += p[i];
-        if (r < cum) return id[i];
+    for (int i = 0; i < l.n; i++) {
+        cum += lanef(l.p, i);
+        if (r < cum) return lanei(l.id, i);
     }
-    for (int i = n - 1; i >= 0; i--)
-        if (p[i] > 0.f) return id[i];
+    for (int i = l.n - 1; i >= 0; i--)
+        if (lanef(l.p, i) > 0.f) return lanei(l.id, i);
     return 0;
 }
 
-__device__ float sparse_get(const int* id, const float* p, int n, int q) {
-    for (int i = 0; i < n; i++)
-        if (id[i] == q) return p[i];
-    return 0.f;
+// p in list l of each lane's own id x (0 if absent): lane-parallel lookup
+__device__ float wget_lane(const WList& l, int x) {
+    float r = 0.f;
+    for (int i = 0; i < l.n; i++)
+        if (lanei(l.id, i) == x) r = lanef(l.p, i);
+    return r;
 }
 
-__global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restrict__ rid,
-                                const float* __restrict__ rv, const float* __restrict__ lmax,
-                                const float* __restrict__ sum, int* __restrict__ qid,
-                                float* __restrict__ qp, int* __restrict__ qn, DState* st,
-                                int* __restrict__ out, const float* __restrict__ uni, int nuni) {
-    // the O(k) chain runs in one thread; its working lists live in LDS
-    __shared__ int pid[SPARSE_K_MAX], rsid[SPARSE_K_MAX];
-    __shared__ float pp[SPARSE_K_MAX], rsp[SPARSE_K_MAX];
-    if (threadIdx.x != 0) return;
+// p of id q in the list (0 if absent)
+__device__ float wget(const WList& l, int q) {
+    const unsigned long long m = __ballot(threadIdx.x < l.n && l.id == q);
+    return m ? lanef(l.p, __builtin_ctzll(m)) : 0.f;
+}
+
+__global__ __launch_bounds__(64) void k_sample_finish(SampCfg c, int mode, int jk, const int* __restrict__ rid,
+                                                      const float* __restrict__ rv, const float* __restrict__ lmax,
+                                                      const float* __restrict__ sum, int* __restrict__ qid,
+                                                      float* __restrict__ qp, int* __restrict__ qn, DState* st,
+                                                      int* __restrict__ out, const float* __restrict__ uni,
+                                                      int nuni) {
+    const int lane = threadIdx.x;
     Uni rng{st->rng, uni, nuni, 0};
     if (mode == 0 || mode == 1) {  // Draft / Plain: distribution of row 0, one draw
-        int n = sparse_dist(rid, rv, lmax[0], sum[0], c, pid, pp);
-        if (n == 0) {
-            pid[0] = row_argmax(rid, rv, c.k);
-            pp[0] = 1.f;
-            n = 1;
+        WList l = wsparse_dist(rid, rv, lmax[0], sum[0], c);
+        if (l.n == 0) {
+            l.id = lane == 0 ? row_argmax(rid, rv, c.k) : -1;
+            l.p = lane == 0 ? 1.f : 0.f;
+            l.n = 1;
         }
-        const int tok = draw_sparse(pid, pp, n, &rng);
+        const int tok = wdraw(l, &rng);
         if (mode == 0) {
-            for (int i = 0; i < n; i++) {
-                qid[jk * SPARSE_K_MAX + i] = pid[i];
-                qp[jk * SPARSE_K_MAX + i] = pp[i];
+            if (lane < l.n) {
+                qid[jk * SPARSE_K_MAX + lane] = l.id;
+                qp[jk * SPARSE_K_MAX + lane] = l.p;
             }
-            qn[jk] = n;
-            st->drafts[jk] = tok;
-        } else {
+            if (lane == 0) {
+                qn[jk] = l.n;
+                st->drafts[jk] = tok;
+            }
+        } else if (lane == 0) {
             st->t_new = tok;
         }
-        st->rng = rng.rng;
+        if (lane == 0) st->rng = rng.rng;
         return;
     }
-    // Accept (pipeline.rs:3894-3934 + the loop-top sample of row a)
+    // Accept (spec_accept_or_correct_sparse, sampler.rs:683-711, per verify
+    // row as pipeline.rs:3894-3934, then the loop-top sample of row a)
     const int k = jk;
     int a = 0, forced = -1;
     while (a < k) {
         const int* r_id = rid + (size_t)a * SPARSE_K_MAX;
         const float* r_v = rv + (size_t)a * SPARSE_K_MAX;
-        int np = sparse_dist(r_id, r_v, lmax[a], sum[a], c, pid, pp);
-        if (np == 0) {
-            pid[0] = row_argmax(r_id, r_v, c.k);
-            pp[0] = 1.f;
-            np = 1;
+        WList p = wsparse_dist(r_id, r_v, lmax[a], sum[a], c);
+        if (p.n == 0) {
+            p.id = lane == 0 ? row_argmax(r_id, r_v, c.k) : -1;
+            p.p = lane == 0 ? 1.f : 0.f;
+            p.n = 1;
         }
         const int d = st->drafts[a];
-        const int* q_id = qid + a * SPARSE_K_MAX;
-        const float* q_p = qp + a * SPARSE_K_MAX;
-        const int nq = qn[a];
-        const float pd = sparse_get(pid, pp, np, d), qd = sparse_get(q_id, q_p, nq, d);
+        WList q;
+        q.n = qn[a];
+        q.id = lane < q.n ? qid[a * SPARSE_K_MAX + lane] : -1;
+        q.p = lane < q.n ? qp[a * SPARSE_K_MAX + lane] : 0.f;
+        const float pd = wget(p, d), qd = wget(q, d);
         const float r = rng.next();
         if (qd > 0.f && r * qd < pd) {
             a++;
             continue;
         }
-        int nr = 0;
+        // residual max(0, p - q) over p's support, in p's order
+        const float ri = lane < p.n ? p.p - wget_lane(q, p.id) : 0.f;
+        const bool pos = lane < p.n && ri > 0.f;
         float total = 0.f;
-        for (int i = 0; i < np; i++) {
-            const float ri = pp[i] - sparse_get(q_id, q_p, nq, pid[i]);
-            if (ri > 0.f) {
-                rsid[nr] = pid[i];
-                rsp[nr] = ri;
-                nr++;
-                total += ri;
-            }
-        }
+        for (int i = 0; i < p.n; i++)
+            if (__builtin_amdgcn_readlane((int)pos, i)) total += lanef(ri, i);
         if (total <= 0.f) {
-            forced = draw_sparse(pid, pp, np, &rng);
+            forced = wdraw(p, &rng);
         } else {
-            for (int i = 0; i < nr; i++) rsp[i] /= total;
-            forced = draw_sparse(rsid, rsp, nr, &rng);
+            // the residual list: p's order, entries with ri > 0, ri / total
+            const unsigned long long pm = __ballot(pos);
+            const int slot = __builtin_popcountll(pm & ((1ull << lane) - 1));
+            __shared__ int rsid[64];
+            __shared__ float rsp[64];
+            if (pos) {
+                rsid[slot] = p.id;
+                rsp[slot] = ri / total;
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            WList rs;
+            rs.n = __builtin_popcountll(pm);
+            rs.id = lane < rs.n ? rsid[lane] : -1;
+            rs.p = lane < rs.n ? rsp[lane] : 0.f;
+            forced = wdraw(rs, &rng);
         }
         break;
     }
@@ -410,43 +498,45 @@ __global__ void k_sample_finish(SampCfg c, int mode, int jk, const int* __restri
     if (forced < 0) {  // loop top: sample row a (sample_with_scratch_pool)
         const int* r_id = rid + (size_t)a * SPARSE_K_MAX;
         const float* r_v = rv + (size_t)a * SPARSE_K_MAX;
-        int np = sparse_dist(r_id, r_v, lmax[a], sum[a], c, pid, pp);
-        if (np > 0) tnew = draw_sparse(pid, pp, np, &rng);
+        const WList p = wsparse_dist(r_id, r_v, lmax[a], sum[a], c);
+        if (p.n > 0) tnew = wdraw(p, &rng);
         else tnew = row_argmax(r_id, r_v, c.k);
     }
-    const int n0 = st->n_out;
-    out[n0] = st->t_next;
-    for (int j = 0; j < a; j++) out[n0 + 1 + j] = st->drafts[j];
-    st->n_out = n0 + 1 + a;
-    st->a = a;
-    st->forced = forced;
-    st->t_new = tnew;
-    st->accepted += a;
-    st->rng = rng.rng;
+    if (lane == 0) {
+        const int n0 = st->n_out;
+        out[n0] = st->t_next;
+        for (int j = 0; j < a; j++) out[n0 + 1 + j] = st->drafts[j];
+        st->n_out = n0 + 1 + a;
+        st->a = a;
+        st->forced = forced;
+        st->t_new = tnew;
+        st->accepted += a;
+        st->rng = rng.rng;
+    }
 }
 
-__global__ void k_sample_dist(SampCfg c, const int* __restrict__ rid, const float* __restrict__ rv,
-                              const float* __restrict__ lmax, const float* __restrict__ sum, int* __restrict__ ids,
-                              float* __restrict__ probs, int* __restrict__ n_out) {
-    __shared__ int pid[SPARSE_K_MAX];
-    __shared__ float pp[SPARSE_K_MAX];
-    if (threadIdx.x != 0) return;
-    int n = sparse_dist(rid, rv, lmax[0], sum[0], c, pid, pp);
-    if (n == 0) {
-        pid[0] = row_argmax(rid, rv, c.k);
-        pp[0] = 1.f;
-        n = 1;
+__global__ __launch_bounds__(64) void k_sample_dist(SampCfg c, const int* __restrict__ rid,
+                                                    const float* __restrict__ rv, const float* __restrict__ lmax,
+                                                    const float* __restrict__ sum, int* __restrict__ ids,
+                                                    float* __restrict__ probs, int* __restrict__ n_out) {
+    const int lane = threadIdx.x;
+    WList l = wsparse_dist(rid, rv, lmax[0], sum[0], c);
+    if (l.n == 0) {
+        l.id = lane == 0 ? row_argmax(rid, rv, c.k) : -1;
+        l.p = lane == 0 ? 1.f : 0.f;
+        l.n = 1;
     }
-    for (int i = 0; i < n; i++) {
-        ids[i] = pid[i];
-        probs[i] = pp[i];
+    if (lane < l.n) {
+        ids[lane] = l.id;
+        probs[lane] = l.p;
     }
-    *n_out = n;
+    if (lane == 0) *n_out = l.n;
 }
 
 int sample_alloc(SampleBufs& b, int V, const std::function<int(void**, size_t)>& alloc) {
     b.V = V;
     b.nslices = (V + SLICE - 1) / SLICE;
+    if (b.nslices > 256) return CMF_ERR;  // the merge's per-slice terms (vocab <= 1 048 576)
     const int R = MAXB + 1;
     const size_t nc = (size_t)R * b.nslices * SPARSE_K_MAX;
     if (alloc((void**)&b.cid, nc * 4) || alloc((void**)&b.cv, nc * 4) ||
