@@ -69,14 +69,27 @@ __device__ __forceinline__ void pick_bucket(const int* hist, int shift, uint32_t
     __syncthreads();
 }
 
-// Top-k of (vals, ids) in LDS, n entries, 256 threads.  Writes the k winners
-// sorted by (value desc, id asc) into ov/oi.  scratch: hist[256], ties.
-__device__ void select_topk(const float* vals, const int* ids, int n, int k, float* ov, int* oi,
-                            int* hist, float* tv, int* ti, int* cnt) {
-    const int t = threadIdx.x;
+// Top-k by (value desc, id asc) of n entries held NPT per thread (entry i =
+// thread t's slot u with i = t + 256 u; entries i >= n are not in play),
+// 256 threads.  Writes the k winners sorted into ov/oi.  Radix select over
+// order-preserving keys, 8 bits a pass, each pass's bucket found by a
+// block-wide scan; the keys stay in registers, and the pass counts go to 16
+// copies of the histogram (lane % 16 picks the copy: at most 16 lanes of a
+// wave meet on one address, where same-bucket keys, the common case in the
+// first pass, used to serialize 64 deep; the copies are 257 words apart so
+// that one bucket's copies sit in distinct LDS banks).  scratch: hist[16][257],
+// ties.
+template <int NPT>
+__device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int n, int k, float* ov, int* oi,
+                                int (*hist)[257], float* tv, int* ti, int* cnt) {
+    const int t = threadIdx.x, hc = t & 15;
     __shared__ uint32_t s_prefix, s_mask;
     __shared__ int s_kk;
     __shared__ int wsum[4];
+    __shared__ int htot[256];
+    uint32_t key[NPT];
+#pragma unroll
+    for (int u = 0; u < NPT; u++) key[u] = t + 256 * u < n ? fkey(v[u]) : 0u;  // 0: below every real key
     if (t == 0) {
         s_prefix = 0;
         s_mask = 0;
@@ -84,15 +97,20 @@ __device__ void select_topk(const float* vals, const int* ids, int n, int k, flo
     }
     const int kk_total = k < n ? k : n;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[t] = 0;
+#pragma unroll
+        for (int c = 0; c < 16; c++) hist[c][t] = 0;
         __syncthreads();
         const uint32_t pre = s_prefix, msk = s_mask;
-        for (int i = t; i < n; i += 256) {
-            const uint32_t key = fkey(vals[i]);
-            if ((key & msk) == pre) atomicAdd(&hist[(key >> shift) & 255], 1);
-        }
+#pragma unroll
+        for (int u = 0; u < NPT; u++)
+            if (t + 256 * u < n && (key[u] & msk) == pre) atomicAdd(&hist[hc][(key[u] >> shift) & 255], 1);
         __syncthreads();
-        pick_bucket(hist, shift, &s_prefix, &s_mask, &s_kk, wsum);
+        int s = 0;
+#pragma unroll
+        for (int c = 0; c < 16; c++) s += hist[c][t];
+        htot[t] = s;
+        __syncthreads();
+        pick_bucket(htot, shift, &s_prefix, &s_mask, &s_kk, wsum);
     }
     const uint32_t kth = s_prefix;
     const int need_eq = s_kk;  // entries equal to kth still needed
@@ -102,19 +120,20 @@ __device__ void select_topk(const float* vals, const int* ids, int n, int k, flo
     }
     __syncthreads();
     // strictly greater: all of them; equal: collect (capped) then lowest ids
-    for (int i = t; i < n; i += 256) {
-        const uint32_t key = fkey(vals[i]);
-        if (key > kth) {
+#pragma unroll
+    for (int u = 0; u < NPT; u++) {
+        if (t + 256 * u >= n) continue;
+        if (key[u] > kth) {
             const int p = atomicAdd(&cnt[0], 1);
             if (p < SPARSE_K_MAX) {
-                tv[p] = vals[i];
-                ti[p] = ids[i];
+                tv[p] = v[u];
+                ti[p] = id[u];
             }
-        } else if (key == kth) {
+        } else if (key[u] == kth) {
             const int p = atomicAdd(&cnt[1], 1);
             if (p < 256) {
-                tv[SPARSE_K_MAX + p] = vals[i];
-                ti[SPARSE_K_MAX + p] = ids[i];
+                tv[SPARSE_K_MAX + p] = v[u];
+                ti[SPARSE_K_MAX + p] = id[u];
             }
         }
     }
@@ -162,9 +181,7 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
                                                     float* __restrict__ cv, float* __restrict__ smax,
                                                     float* __restrict__ ssum) {
     const int sl = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
-    __shared__ float vals[SLICE];
-    __shared__ int ids[SLICE];
-    __shared__ int hist[256];
+    __shared__ int hist[16][257];  // copies 257 apart: one bucket's copies fall in distinct banks
     __shared__ float tv[SPARSE_K_MAX + 256];
     __shared__ int ti[SPARSE_K_MAX + 256];
     __shared__ int cnt[4];
@@ -174,23 +191,17 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
     const int lo = sl * SLICE, n = min(SLICE, V - lo);
     const float* src = logits + (size_t)row * V + lo;
     float mx = -INFINITY;
-    {
-        float tmp[SLICE / 256];  // all loads in flight together
+    constexpr int NPT = SLICE / 256;
+    float vals[NPT];  // entry t + 256 u (all loads in flight together)
+    int ids[NPT];
 #pragma unroll
-        for (int u = 0; u < SLICE / 256; u++) {
-            const int i = t + 256 * u;
-            tmp[u] = i < n ? src[i] : -INFINITY;
-        }
-#pragma unroll
-        for (int u = 0; u < SLICE / 256; u++) {
-            const int i = t + 256 * u;
-            if (i < n) {
-                vals[i] = tmp[u];
-                ids[i] = lo + i;
-                mx = fmaxf(mx, tmp[u]);
-            }
-        }
+    for (int u = 0; u < NPT; u++) {
+        const int i = t + 256 * u;
+        vals[u] = i < n ? src[i] : -INFINITY;
+        ids[u] = lo + i;
     }
+#pragma unroll
+    for (int u = 0; u < NPT; u++) mx = fmaxf(mx, vals[u]);
     // slice max and sum of exp((l - max) / T): wave reductions, then the
     // four waves' values in wave order
     const int w = t >> 6;
@@ -199,11 +210,13 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     float se = 0.f;
-    for (int i = t; i < n; i += 256) se += expf((vals[i] - mx) / c.t);
+#pragma unroll
+    for (int u = 0; u < NPT; u++)
+        if (t + 256 * u < n) se += expf((vals[u] - mx) / c.t);
     se = wave_sum(se);
     __syncthreads();  // red[] reads above are done
     if ((t & 63) == 0) red[4 + w] = se;
-    select_topk(vals, ids, n, c.k, ov, oi, hist, tv, ti, cnt);  // (its barriers publish red[4..7])
+    select_topk_reg<NPT>(vals, ids, n, c.k, ov, oi, hist, tv, ti, cnt);  // (its barriers publish red[4..7])
     const size_t base = ((size_t)row * nslices + sl) * SPARSE_K_MAX;
     const int m = min(c.k, n);
     if (t < SPARSE_K_MAX) {
@@ -224,9 +237,7 @@ __global__ __launch_bounds__(256) void k_topk_merge(int V, SampCfg c, int nslice
                                                     float* __restrict__ rv, float* __restrict__ lmax,
                                                     float* __restrict__ sum) {
     const int row = blockIdx.x, t = threadIdx.x;
-    __shared__ float vals[SLICE];
-    __shared__ int ids[SLICE];
-    __shared__ int hist[256];
+    __shared__ int hist[16][257];  // copies 257 apart: one bucket's copies fall in distinct banks
     __shared__ float tv[SPARSE_K_MAX + 256];
     __shared__ int ti[SPARSE_K_MAX + 256];
     __shared__ int cnt[4];
@@ -234,27 +245,19 @@ __global__ __launch_bounds__(256) void k_topk_merge(int V, SampCfg c, int nslice
     __shared__ int oi[SPARSE_K_MAX];
     const int k = min(c.k, V);
     const int n = nslices * k;  // <= SLICE (checked by the host)
-    {
-        int ti_[SLICE / 256];
-        float tv_[SLICE / 256];
+    constexpr int NPT = SLICE / 256;
+    float vals[NPT];  // candidate t + 256 u
+    int ids[NPT];
 #pragma unroll
-        for (int u = 0; u < SLICE / 256; u++) {
-            const int e = t + 256 * u, sl = e / k, i = e - sl * k;
-            const size_t at = ((size_t)row * nslices + sl) * SPARSE_K_MAX + i;
-            ti_[u] = e < n ? cid[at] : -1;
-            tv_[u] = e < n ? cv[at] : -INFINITY;
-        }
-#pragma unroll
-        for (int u = 0; u < SLICE / 256; u++) {
-            const int e = t + 256 * u;
-            if (e < n) {
-                vals[e] = ti_[u] >= 0 ? tv_[u] : -INFINITY;
-                ids[e] = ti_[u] >= 0 ? ti_[u] : 0x7FFFFFFF;
-            }
-        }
+    for (int u = 0; u < NPT; u++) {
+        const int e = t + 256 * u, sl = e / k, i = e - sl * k;
+        const size_t at = ((size_t)row * nslices + sl) * SPARSE_K_MAX + i;
+        const int id = e < n ? cid[at] : -1;
+        const float v = e < n ? cv[at] : -INFINITY;
+        vals[u] = id >= 0 ? v : -INFINITY;
+        ids[u] = id >= 0 ? id : 0x7FFFFFFF;
     }
-    __syncthreads();
-    select_topk(vals, ids, n, k, ov, oi, hist, tv, ti, cnt);
+    select_topk_reg<NPT>(vals, ids, n, k, ov, oi, hist, tv, ti, cnt);
     if (t < SPARSE_K_MAX) {
         rid[(size_t)row * SPARSE_K_MAX + t] = t < k ? oi[t] : -1;
         rv[(size_t)row * SPARSE_K_MAX + t] = t < k ? ov[t] : -INFINITY;
