@@ -571,12 +571,6 @@ __global__ void k_copy_rows_i32(int* dst, const int* src, int n) {
 }
 
 // verify batch tokens [t_next, d_0 .. d_{K-1}]
-__global__ void k_build_vtok(DState* st, int k) {
-    const int i = threadIdx.x;
-    if (i == 0) st->vtok[0] = st->t_next;
-    else if (i <= k) st->vtok[i] = st->drafts[i - 1];
-}
-
 // greedy acceptance (pipeline.rs:3989-3999): a = longest prefix with
 // argmax(row i) == d_i; emits [t_next, d_0..d_{a-1}]; next token argmax(row a)
 __device__ __forceinline__ void accept_greedy(DState* st, int k, int* out) {
@@ -884,8 +878,7 @@ static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_conf
         if (sampling) sample_rows(m->sb, m->logits, V, 1, sc, m->st, SampleMode::Draft, j, nullptr, s);
         else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, &m->st->drafts[j], s);
     }
-    hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
-    launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, k + 1, s);
+    launch_embed(m->st->drafts, embed_src(m), H, m->hv, H, k + 1, s, &m->st->t_next);
     trunk_forward(m, k + 1, pb, 0, graph_len ? graph_len : np + k + 1, true, s);
     if (sampling) {
         sample_rows(m->sb, m->logits, V, k + 1, sc, m->st, SampleMode::Accept, k, m->out, s);
@@ -1131,8 +1124,7 @@ int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const c
     // the MTP row of the first draft, (tip hidden, t_next) at pos0 - 1: what
     // the device draft chain writes before a round
     if (m->has_mtp) mtp_warm(m, &m->st->t_next, m->h_tip, 1, pb, -1, pos0, s);
-    hipLaunchKernelGGL(k_build_vtok, dim3(1), dim3(32), 0, s, m->st, k);
-    launch_embed(m->st->vtok, embed_src(m), H, m->hv, H, b, s);
+    launch_embed(m->st->drafts, embed_src(m), H, m->hv, H, b, s, &m->st->t_next);
     trunk_forward(m, b, pb, 0, pos0 + b, true, s);
     if (sampling) {
         sample_rows(m->sb, m->logits, V, b, *sc, m->st, SampleMode::Accept, k, m->out, s, b);

@@ -8,8 +8,9 @@ namespace cmf {
 
 constexpr int ATT_C = 64;  // key positions per attention workgroup
 
+// tok0: row 0 embeds *tok0, row b > 0 toks[b - 1]
 void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
-                  hipStream_t st);
+                  hipStream_t st, const int* tok0 = nullptr);
 // One layer's decode attention (head_dim 128): q/k-norm + RoPE, KV append,
 // chunked causal attention over the cache and the merge into out
 // [nb][nh * 128].  pm/pl [MAXB * nh][nch], po [MAXB * nh][nch][128] hold the

@@ -47,11 +47,12 @@ __device__ inline float block_max_f(float v, float* red) {
 
 
 // Embedding rows from the (tied) q8 lm_head: out[b] = q8 row * row_scale
-// (pipeline.rs:5568-5575).  grid (nb), block 256.
-__global__ __launch_bounds__(256) void k_embed(const int* __restrict__ toks, EmbedSrc emb, int H,
-                                               float* __restrict__ out, int ldo) {
+// (pipeline.rs:5568-5575).  grid (nb), block 256.  With tok0, row 0 embeds
+// *tok0 and row b > 0 toks[b - 1] (the verify rows [t_next, drafts...]).
+__global__ __launch_bounds__(256) void k_embed(const int* __restrict__ toks, const int* __restrict__ tok0,
+                                               EmbedSrc emb, int H, float* __restrict__ out, int ldo) {
     const int b = blockIdx.x;
-    const int tok = toks[b];
+    const int tok = tok0 ? (b == 0 ? *tok0 : toks[b - 1]) : toks[b];
     const bool ok = tok >= 0 && tok < emb.rows;
     const float rs = ok ? emb.rs[tok] : 0.f;
     const int rb = tok >> 4, r = tok & 15;
@@ -593,8 +594,8 @@ __global__ __launch_bounds__(64) void k_argmax_final(const float* __restrict__ p
 // host launchers
 // ---------------------------------------------------------------------------
 void launch_embed(const int* toks, const EmbedSrc& e, int H, float* out, int ldo, int nb,
-                  hipStream_t st) {
-    hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, e, H, out, ldo);
+                  hipStream_t st, const int* tok0) {
+    hipLaunchKernelGGL(k_embed, dim3(nb), dim3(256), 0, st, toks, tok0, e, H, out, ldo);
 }
 
 void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge) {

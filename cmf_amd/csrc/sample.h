@@ -25,7 +25,6 @@ struct DState {
     int pad;
     unsigned long long rng;  // SplitMix64 state (sampler.rs:54-84)
     int drafts[16];
-    int vtok[17];
     int argmax[17];
 };
 
