@@ -20,6 +20,7 @@
 #include "runtime.h"
 #include "sample.h"
 #include "wave.h"
+#include "xlayer.h"
 
 namespace cmf {
 
@@ -119,6 +120,11 @@ struct cmf_model_s {
     int emitted_host = 0;
     int accepted_host = 0;
     cmf_sampler_config sc{};
+    // XCD-partitioned blocks (xlayer.hip): buffers allocated at create when
+    // the shape and the device take them
+    XlBufs xl;
+    XlShape xls{};
+    bool xl_on = false;
 };
 
 namespace {
@@ -133,6 +139,11 @@ int dalloc(cmf_model_s* m, void** p, size_t bytes) {
 template <class T>
 int dalloc_t(cmf_model_s* m, T** p, size_t n) {
     return dalloc(m, (void**)p, n * sizeof(T));
+}
+
+void* xl_dalloc(void* ctx, size_t n) {
+    void* p = nullptr;
+    return dalloc((cmf_model_s*)ctx, &p, n) == CMF_OK ? p : nullptr;
 }
 
 int upload_f32(cmf_model_s* m, float** d, const float* h, size_t n) {
@@ -385,10 +396,33 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
 
 // Trunk forward of nb rows in m->hv (embeddings in, final hidden rows out,
 // pre-norm as forward_layers returns them); logits when want_logits.
+// Whether block l runs as the two XCD-partitioned launches for nb rows:
+// q8 attention weights, q4t FFN weights, a dense FFN, a shape xlayer.hip
+// is built for.
+bool xl_layer_ok(cmf_model_s* m, const LayerDev& l, int nb, int max_len) {
+    return m->xl_on && !l.moe && l.kc && l.qkv.dtype == DT_Q8ROW && l.wo.dtype == DT_Q8ROW &&
+           l.gu.dtype == DT_Q4T && l.down.dtype == DT_Q4T && xl_shape_ok(m->xls, nb, max_len);
+}
+XlAttnW xl_aw(const LayerDev& l) {
+    return XlAttnW{l.qkv.w, l.qkv.scale, l.wo.w, l.wo.scale, l.qkv.kchunks, l.wo.kchunks,
+                   l.in_norm, l.q_norm, l.k_norm, l.kc, l.vc};
+}
+XlFfnW xl_fw(const LayerDev& l) {
+    return XlFfnW{l.gu.w, l.gu.scale, l.down.w, l.down.scale, l.gu.kchunks, l.down.kchunks, l.post_norm};
+}
+
 void trunk_forward(cmf_model_s* m, int nb, const int* pb, int padd, int max_len, bool want_logits,
                    hipStream_t s) {
     const auto& c = m->c;
-    for (int li = 0; li < c.n_layers; li++) run_block(m, m->L[li], m->hv, nb, pb, padd, max_len, s);
+    bool xl = true;
+    for (int li = 0; li < c.n_layers && xl; li++) xl = xl_layer_ok(m, m->L[li], nb, max_len);
+    if (xl) {
+        for (int li = 0; li < c.n_layers; li++)
+            xl_block(m->xl, m->xls, xl_aw(m->L[li]), xl_fw(m->L[li]), m->hv, nb, pb, padd, m->rope, li, s);
+        xl_finish(m->xl, m->xls, m->hv, nb, s);
+    } else {
+        for (int li = 0; li < c.n_layers; li++) run_block(m, m->L[li], m->hv, nb, pb, padd, max_len, s);
+    }
     if (want_logits)
         gemv_f(m, m->lm, src_norm(m->hv, c.hidden, m->final_norm, c.eps), m->logits, c.vocab, nb, false, s);
 }
@@ -430,7 +464,12 @@ void mtp_step(cmf_model_s* m, const int* tok, const float* hin, float* hout, con
     const auto& c = m->c;
     const int H = c.hidden;
     gemv_f(m, m->eh, src_cat(m, tok, hin), hout, H, 1, false, s);
-    run_block(m, m->mtp, hout, 1, pb, padd, max_len, s);
+    if (xl_layer_ok(m, m->mtp, 1, max_len)) {
+        xl_block(m->xl, m->xls, xl_aw(m->mtp), xl_fw(m->mtp), hout, 1, pb, padd, m->rope, 0, s);
+        xl_finish(m->xl, m->xls, hout, 1, s);
+    } else {
+        run_block(m, m->mtp, hout, 1, pb, padd, max_len, s);
+    }
     gemv_f(m, m->lm, src_norm(hout, H, m->mtp_norm, c.eps), m->logits, c.vocab, 1, false, s);
 }
 
@@ -673,6 +712,15 @@ int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
         cmf_model_free(m);
         return CMF_ERR;
     }
+    m->xls = XlShape{c.hidden, c.inter, c.n_heads, c.n_kv, c.head_dim, c.max_seq, c.eps};
+    const char* xe = getenv("CMF_XL");  // "0": the six-launch blocks only
+    if (!(xe && xe[0] == '0') && xl_shape_ok(m->xls, 1, 16)) {
+        if (xl_alloc(m->xl, m->xls, xl_dalloc, m) != CMF_OK) {
+            cmf_model_free(m);
+            return CMF_ERR;
+        }
+        m->xl_on = true;
+    }
     *out = m;
     return CMF_OK;
 }
@@ -786,6 +834,8 @@ int cmf_model_set_embed(cmf_model m, const cmf_tensor* e) {
     return build_cat(m->emb, {e});
 }
 
+int cmf_model_fused_blocks(cmf_model m) { return m && m->xl_on ? 1 : 0; }
+
 int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh,
                       const cmf_layer_desc* layer, const float* norm) {
     if (m) drop_graph(m);
@@ -800,6 +850,18 @@ int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const
     if (upload_layer(m, m->mtp, layer, true)) return CMF_ERR;
     m->has_mtp = true;
     return CMF_OK;
+}
+
+// An XCD-partitioned block whose exchange wait gave up (or whose attention
+// positions exceeded the host's bound) wrote wrong values: report it once.
+static int xl_check(cmf_model m) {
+    if (!m->xl_on) return CMF_OK;
+    int e = 0;
+    CMF_HIP(hipMemcpy(&e, m->xl.err, sizeof(int), hipMemcpyDeviceToHost));
+    if (e == 0) return CMF_OK;
+    CMF_HIP(hipMemset(m->xl.err, 0, sizeof(int)));
+    return fail(e & 4 ? "XCD-partitioned block: more attention positions than its bound (set CMF_XL=0)"
+                      : "XCD-partitioned block: an exchange wait gave up (set CMF_XL=0)");
 }
 
 static int ready(cmf_model m) {
@@ -1003,6 +1065,7 @@ int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats)
     CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    if (xl_check(m) != CMF_OK) return CMF_ERR;
     m->next_pos_host = hs.next_pos;
     m->emitted_host = hs.n_out;
     m->rounds += spec ? n : 0;
@@ -1084,6 +1147,7 @@ int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float
     hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, pos0 + b);
     CMF_HIP(hipStreamSynchronize(s));
     CMF_HIP(hipGetLastError());
+    if (xl_check(m) != CMF_OK) return CMF_ERR;
     m->next_pos_host = pos0 + b;
     return CMF_OK;
 }
@@ -1141,6 +1205,7 @@ int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const c
     CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
     CMF_HIP(hipStreamSynchronize(s));
     CMF_HIP(hipGetLastError());
+    if (xl_check(m) != CMF_OK) return CMF_ERR;
     m->next_pos_host = hs.next_pos;
     m->prefilled = true;
     m->decoding = false;

@@ -66,16 +66,6 @@ __global__ __launch_bounds__(256) void k_embed(const int* __restrict__ toks, con
     }
 }
 
-// qk-norm + RoPE of one head row x (lane holds dims lane and lane + 64, the
-// rotation pair): x * inv * w with inv = 1/sqrt(mean(x^2) + eps) (f64 sum),
-// then (a, b) -> (a cos - b sin, a sin + b cos); w0/w1 = w[lane], w[lane +
-// 64], cs = the (cos, sin) of the position at lane.
-__device__ __forceinline__ float2 norm_rope(float x0, float x1, float w0, float w1, float2 cs, double eps) {
-    const double ss = wave_sum((double)x0 * (double)x0 + (double)x1 * (double)x1);
-    const float inv = (float)(1.0 / sqrt(ss / 128.0 + eps));
-    const float a = x0 * inv * w0, b = x1 * inv * w1;
-    return make_float2(a * cs.x - b * cs.y, a * cs.y + b * cs.x);
-}
 // N head rows at once, as norm_rope with its own weights per row: the f64
 // wave reductions of the N rows interleaved.
 template <int N>

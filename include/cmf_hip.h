@@ -208,6 +208,13 @@ int cmf_model_set_head(cmf_model m, const cmf_tensor* lm_head, const float* fina
 /* MtpModule (pipeline.rs:600-612). */
 int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const cmf_tensor* eh_proj,
                       const cmf_layer_desc* layer, const float* norm);
+/* 1 when the model's dense decoder blocks run as the XCD-partitioned pair of
+ * launches (MI355X with 256 CUs, hidden 1024, inter 3072, 16 query / 8 KV
+ * heads of 128, q8 attention and q4t FFN weights, batches of up to 16 rows;
+ * environment CMF_XL=0 at model creation turns it off), 0 when they run as
+ * six launches per block.  No counterpart in the reference (a backend
+ * property, not a seam). */
+int cmf_model_fused_blocks(cmf_model m);
 
 /* ---- MoE FFN (moe_ffn / moe_block) ------------------------------------ */
 
