@@ -1100,6 +1100,9 @@ int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64
     cmf_gen_stats st{}, tot{};
     int generated = 0;
     while (true) {
+        // a round that ends at or past max_tokens ends the decode (its next
+        // token is not emitted: pipeline.rs's loop stops at generated >= max)
+        if (generated >= max_tokens) break;
         if (generated + 1 >= max_tokens) {
             hipLaunchKernelGGL(k_emit, dim3(1), dim3(1), 0, s, m->st, m->out);
             CMF_HIP(hipStreamSynchronize(s));
