@@ -140,21 +140,57 @@ __device__ __forceinline__ void q8_digits(float v, int8_t& d0, int8_t& d1, int8_
     d2 = (int8_t)q2;
 }
 
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+// x = hi + lo in f16 (22 significant bits while |x| < 65504: the score
+// operands q and k after their RMS norms, |.| <= sqrt(128) max|norm weight|)
+__device__ __forceinline__ void split16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);
+}
+
 // slot of tile element e (0..7 of a k-slot) in the MFMA operand order
 // {0,4,2,6,1,5,3,7} (the nibble-pair order of dq_nib_word); an involution
 __device__ __forceinline__ int nib_slot(int e) { return ((e & 1) << 2) | (e & 2) | ((e >> 2) & 1); }
 
-__device__ __forceinline__ float sum32(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+// Reductions over a DPP row (16 lanes) or a quad (4 lanes) in registers
+// (no LDS permutes): quad swaps, row_shr 4 and 8 (the row's total in lane
+// 15), row_newbcast 15 hands it to the row's 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v, float ident) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, ident),
+                                                                 __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
-__device__ __forceinline__ float max32(float v) {
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+template <int CTRL>
+__device__ __forceinline__ double dppd(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
-
+__device__ __forceinline__ float quad_sum(float v) {
+    v += dppf<0xb1>(v, 0.f);
+    return v + dppf<0x4e>(v, 0.f);
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v = quad_sum(v);
+    v += dppf<0x114>(v, 0.f);
+    v += dppf<0x118>(v, 0.f);
+    return dppf<0x15F>(v, 0.f);
+}
+__device__ __forceinline__ double row_sum_d(double v) {
+    v += dppd<0xb1>(v);
+    v += dppd<0x4e>(v);
+    v += dppd<0x114>(v);
+    v += dppd<0x118>(v);
+    return dppd<0x15F>(v);
+}
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dppf<0xb1>(v, -INFINITY));
+    v = fmaxf(v, dppf<0x4e>(v, -INFINITY));
+    v = fmaxf(v, dppf<0x114>(v, -INFINITY));
+    v = fmaxf(v, dppf<0x118>(v, -INFINITY));
+    return dppf<0x15F>(v, -INFINITY);
+}
 // f16 exponent scaling of a q4 operand: x * 2^e with max |x * 2^e| < 2^15
 __device__ __forceinline__ void f16_scale(float amax, float& scale, float& xs) {
     int ex = 0;
@@ -243,14 +279,17 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
 
     // LDS: K / V tiles (positions of this workgroup), queries, scores; the
     // step-4 operand and planes overlay the K tiles
-    __shared__ __align__(16) float KT[NPOS][HD + 4];
+    // (K and Q rows as f16 hi / lo planes [row][dim], padded against bank
+    // conflicts; V rows f32; scores, then the softmax weights in place)
+    constexpr int KS = HD + 8;
+    __shared__ __align__(16) _Float16 KHL[2][NPOS][KS];
     __shared__ __align__(16) float VT[NPOS][HD + 4];
-    __shared__ __align__(16) float Q[XL_NQ][HD + 4];
+    __shared__ __align__(16) _Float16 QHL[2][XL_NQ][KS];
     __shared__ __align__(16) float S[XL_NQ][NPOS + 4];
     __shared__ __align__(16) int8_t P8[3 * 4 * 16 * 16];
     __shared__ float sx0[MAXB], sxo[MAXB];
     __shared__ double ssd[MAXB], ssp[MAXB][NKC];
-    static_assert(MAXB * QD * 4 + 3 * QC * 1024 + 12 * 64 * 16 <= NPOS * (HD + 4) * 4, "overlay");
+    static_assert(MAXB * QD * 4 + 3 * QC * 1024 + 12 * 64 * 16 <= 2 * NPOS * (HD + 8) * 2, "overlay");
 
     const int kc = j % NKC, rp = j / NKC;
     const int pos0 = *a.pbase + a.padd;
@@ -271,13 +310,14 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     // output projection's weights and this workgroup's cached K / V
     int4v wq[RBW];
     float rsq[RBW];
-    float hv[4], pv[4][8];
-    float wn = 0.f;
+    float4v hv4 = {0.f, 0.f, 0.f, 0.f}, pv4[8], wn4 = hv4;
     int4v wov[CW];
     float rso = 0.f;
     float4v kq[KVN], vq[KVN];
-    const int col = kc * 64 + lane;
     if (wave < 4) {
+        // the weights first (the long HBM round trip), then the operand:
+        // thread (b = t / 16, four columns) of the chunk, the row of h and
+        // the eight partials as float4
 #pragma unroll
         for (int i = 0; i < RBW; i++) {
             const int l = rp * NRB0 + wave + 4 * i;  // XCD row block
@@ -287,16 +327,14 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             wq[i] = ld_stream(a.wqkv + ((size_t)g * NKC + kc) * 64 + lane);
             rsq[i] = ldg(a.sqkv + g * 16 + r);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        const int b = min(t >> 4, nb - 1), c = kc * 64 + 4 * (t & 15);
+        hv4 = ldg((const float4v*)(a.hb + (size_t)b * H + c));
+        if (a.parts) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int b = min(wave + 4 * i, nb - 1);
-            hv[i] = ldg(a.hb + (size_t)b * H + col);
-            if (a.parts) {
-#pragma unroll
-                for (int xx = 0; xx < 8; xx++) pv[i][xx] = ldg(a.parts + ((size_t)xx * MAXB + b) * H + col);
-            }
+            for (int xx = 0; xx < 8; xx++) pv4[xx] = ldg((const float4v*)(a.parts + ((size_t)xx * MAXB + b) * H + c));
         }
-        wn = ldg(a.nw + col);
+        wn4 = ldg((const float4v*)(a.nw + c));
     } else {
         const int w4 = wave - 4, rbl = w4 % RBO, cs = w4 / RBO, g = j * RBO + rbl;
 #pragma unroll
@@ -317,35 +355,44 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
 
     XL_MARK(1);
     // ---- step 0: this chunk of h_in * w_norm as int8 planes (waves 0-3),
-    // wave w holding batch rows w, w + 4, ...; h_in written by XCD 0
+    // thread (b = t / 16, columns 4 (t % 16) ..): the row's statistics over
+    // its 16 lanes; h_in written by XCD 0
     if (wave < 4) {
+        const int b = t >> 4, c4 = t & 15;
+        float4v h = hv4;
+        if (a.parts) {
+#pragma unroll
+            for (int xx = 0; xx < 8; xx++) h += pv4[xx];
+        }
+        if (b < nb && x == 0 && rp == 0) *(float4v*)(a.hout + (size_t)b * H + kc * 64 + 4 * c4) = h;
+        const double ss = row_sum_d((double)h[0] * (double)h[0] + (double)h[1] * (double)h[1] +
+                                     (double)h[2] * (double)h[2] + (double)h[3] * (double)h[3]);
+        const float4v u = h * wn4;
+        const float am = row_max(fmaxf(fmaxf(fabsf(u[0]), fabsf(u[1])), fmaxf(fabsf(u[2]), fabsf(u[3]))));
+        const float sx = am > 0.f ? am / 127.0f : 1.0f;
+        uint32_t w0 = 0, w1 = 0, w2 = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int b = wave + 4 * i;
-            if (b >= nb) break;
-            float h = hv[i];
-            if (a.parts) {
-#pragma unroll
-                for (int xx = 0; xx < 8; xx++) h += pv[i][xx];
-            }
-            if (x == 0 && rp == 0) a.hout[(size_t)b * H + col] = h;
-            const double ss = wave_sum((double)h * (double)h);
-            const float u = h * wn;
-            const float am = wave_max(fabsf(u));
-            const float sx = am > 0.f ? am / 127.0f : 1.0f;
             int8_t d0, d1, d2;
-            q8_digits(u / sx, d0, d1, d2);
-            const int o = ((lane >> 4) * 16 + b) * 16 + (lane & 15);
-            P8[o] = d0;
-            P8[1024 + o] = d1;
-            P8[2048 + o] = d2;
-            if (lane == 0) {
+            q8_digits(u[i] / sx, d0, d1, d2);
+            w0 |= (uint32_t)(uint8_t)d0 << (8 * i);
+            w1 |= (uint32_t)(uint8_t)d1 << (8 * i);
+            w2 |= (uint32_t)(uint8_t)d2 << (8 * i);
+        }
+        if (b < nb) {
+            const int o = ((c4 >> 2) * 16 + b) * 16 + 4 * (c4 & 3);
+            *(uint32_t*)&P8[o] = w0;
+            *(uint32_t*)&P8[1024 + o] = w1;
+            *(uint32_t*)&P8[2048 + o] = w2;
+            if (c4 == 0) {
                 sx0[b] = sx;
                 ssd[b] = ss;
             }
         }
     }
+    XL_MARK(13);
     lds_barrier();
+    XL_MARK(14);
     uint64_t* e0w = a.e0 + (size_t)(x * XL_WG + j) * MAXB * a.e0s;
     if (wave < 4) {
         const int4v* A = (const int4v*)P8;
@@ -404,14 +451,24 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             xput(a.e1 + ((size_t)x * MAXB + b) * a.e1s + R, acc * inv, tag);
         }
     } else {
-        // waves 4-7: the cached K / V of this workgroup's positions into LDS;
-        // V rows past its positions zeroed (their weights are 0)
+        // waves 4-7: the cached K (as f16 hi / lo) and V of this workgroup's
+        // positions into LDS; V rows past its share zeroed (their weights
+        // are 0)
         const int t4 = t - 256;
 #pragma unroll
         for (int u = 0; u < KVN; u++) {
             const int f = t4 + 256 * u, sl = f >> 5, c4 = f & 31;
             if (sl < nold) {
-                *(float4v*)&KT[sl][4 * c4] = kq[u];
+                half4 kh, kl;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    _Float16 h, l;
+                    split16(kq[u][i], h, l);
+                    kh[i] = h;
+                    kl[i] = l;
+                }
+                *(half4*)&KHL[0][sl][4 * c4] = kh;
+                *(half4*)&KHL[1][sl][4 * c4] = kl;
                 *(float4v*)&VT[sl][4 * c4] = vq[u];
             } else if (sl >= np) {
                 *(float4v*)&VT[sl][4 * c4] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -431,8 +488,8 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
         xget<2>([&](int i) { return e1x + (size_t)b * a.e1s + hh * HD + lane + 64 * i; }, tag, v2, err);
         const float2 o = norm_rope(v2[0], v2[1], a.qn[lane], a.qn[lane + 64], a.rope[(size_t)(pos0 + b) * 64 + lane],
                                    a.eps);
-        Q[qi][lane] = o.x;
-        Q[qi][lane + 64] = o.y;
+        split16(o.x, QHL[0][qi][lane], QHL[1][qi][lane]);
+        split16(o.y, QHL[0][qi][lane + 64], QHL[1][qi][lane + 64]);
     }
     {
         const int blo = max(0, plo - pos0), bhi = min(nb, phi - pos0);
@@ -443,8 +500,8 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             const int pos = pos0 + b, sl = pos - plo;
             const float2 k = norm_rope(v4[0], v4[1], a.kn[lane], a.kn[lane + 64], a.rope[(size_t)pos * 64 + lane],
                                        a.eps);
-            KT[sl][lane] = k.x;
-            KT[sl][lane + 64] = k.y;
+            split16(k.x, KHL[0][sl][lane], KHL[1][sl][lane]);
+            split16(k.y, KHL[0][sl][lane + 64], KHL[1][sl][lane + 64]);
             VT[sl][lane] = v4[2];
             VT[sl][lane + 64] = v4[3];
             float* kd = a.kc + ((size_t)x * a.max_seq + pos) * HD;
@@ -457,24 +514,24 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     }
     XL_MARK(5);
     lds_barrier();
-    // ---- step 2b: scores by fp32 MFMA (16x16x4), one (tile, query block)
-    // per wave: A = 16 queries, B = the tile's 16 positions, the lane's dims
-    // 16 j4 + 4 s + c; causal limit pos0 + b (kv_cache.rs:521-690)
+    // ---- step 2b: scores on the f16 MFMA (16x16x32) from hi / lo planes,
+    // q.k = qh.kh + qh.kl + ql.kh (22 significant bits), one (tile, query
+    // block) per wave: A = 16 queries, B = the tile's 16 positions; causal
+    // limit pos0 + b (kv_cache.rs:521-690)
     const int nqb = (nq + 15) >> 4;
     const float scale = 1.0f / sqrtf((float)HD);
     for (int it = wave; it < ntile * nqb; it += 8) {
         const int tt = it % ntile, qb = it / ntile;
-        const float* qrow = Q[min(qb * 16 + r, XL_NQ - 1)];
-        const float* krow = KT[tt * 16 + r];
+        const int qr = min(qb * 16 + r, XL_NQ - 1);
         float4v d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j4 = 0; j4 < 8; j4++) {
-            const float4v qa = *(const float4v*)&qrow[16 * j4 + 4 * s];
-            const float4v ka = *(const float4v*)&krow[16 * j4 + 4 * s];
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[0], ka[0], d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[1], ka[1], d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[2], ka[2], d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[3], ka[3], d, 0, 0, 0);
+        for (int ks = 0; ks < HD / 32; ks++) {
+            const int o = 32 * ks + 8 * s;
+            const half8 qh = *(const half8*)&QHL[0][qr][o], ql = *(const half8*)&QHL[1][qr][o];
+            const half8 kh = *(const half8*)&KHL[0][tt * 16 + r][o], kl = *(const half8*)&KHL[1][tt * 16 + r][o];
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh, kh, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh, kl, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql, kh, d, 0, 0, 0);
         }
         const int p = plo + tt * 16 + r;
 #pragma unroll
@@ -489,7 +546,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     XL_MARK(6);
     lds_barrier();
     // ---- step 2c: softmax over this workgroup's positions, one wave per
-    // query (m, l to the partial); the weights overwrite the scores
+    // query: m, l to the partial, the weights e = exp(s - m) over the scores
     uint64_t* e2w = a.e2 + (size_t)(x * XL_WG + j) * XL_NQ * XL_E2S;
     const int npr = ntile * 16;
     for (int q = wave; q < nq; q += 8) {
@@ -512,21 +569,23 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     }
     XL_MARK(7);
     lds_barrier();
-    // ---- step 2d: values by fp32 MFMA, wave w dims 16 w .. 16 w + 15:
-    // o[q][d] = sum_p e[q][p] V[p][d] over the positions in order of k steps
+    // ---- step 2d: values by fp32 MFMA (16x16x4), wave w dims 16 w .. 16 w +
+    // 15: o[q][d] = sum_p e[q][p] V[p][d], two accumulators over the k steps
+    // (on the f16 MFMA this pass would need V transposed in LDS: slower)
     if (npr > 0) {
         const int d0 = 16 * wave;
         for (int qb = 0; qb < nqb; qb++) {
             const float* erow = S[min(qb * 16 + r, XL_NQ - 1)];
-            float4v acc = {0.f, 0.f, 0.f, 0.f};
+            float4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
             for (int k = 0; k < npr / 4; k++) {
                 const int p = 4 * k + s;
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(erow[p], VT[p][d0 + r], acc, 0, 0, 0);
+                acc[k & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(erow[p], VT[p][d0 + r], acc[k & 1], 0, 0, 0);
             }
+            const float4v o = acc[0] + acc[1];
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int q = qb * 16 + 4 * s + e;
-                if (q < nq) xput(e2w + (size_t)q * XL_E2S + 2 + d0 + r, acc[e], tag);
+                if (q < nq) xput(e2w + (size_t)q * XL_E2S + 2 + d0 + r, o[e], tag);
             }
         }
     }
@@ -534,21 +593,34 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     // ---- step 3: merge of dims [DJ j, DJ j + DJ) over the 32 shares:
     // out = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - M) (lanes = shares)
     {
+        // thread (share pair js, js + 16; batch row b = t / 16): one DPP row
+        // per batch row reduces the 32 shares in registers
         const int dbase = j * DJ, hh = dbase / HD, dd = dbase % HD;
-        const int js = t & 31, b = t >> 5, bq = min(b, nb - 1), q = bq * HPK + hh;
-        const uint64_t* src = a.e2 + ((size_t)(x * XL_WG + js) * XL_NQ + q) * XL_E2S;
-        float v[DJ + 2];
-        if (b < nb) xget<DJ + 2>([&](int i) { return i < 2 ? src + i : src + 2 + dd + (i - 2); }, tag, v, err);
-        else {
+        const int js = t & 15, b = t >> 4, bq = min(b, nb - 1), q = bq * HPK + hh;
+        const uint64_t* s0 = a.e2 + ((size_t)(x * XL_WG + js) * XL_NQ + q) * XL_E2S;
+        const uint64_t* s1 = s0 + (size_t)16 * XL_NQ * XL_E2S;
+        float v[2 * (DJ + 2)];
+        if (b < nb) {
+            xget<2 * (DJ + 2)>(
+                [&](int i) {
+                    const uint64_t* sp = i < DJ + 2 ? s0 : s1;
+                    const int k = i < DJ + 2 ? i : i - (DJ + 2);
+                    return k < 2 ? sp + k : sp + 2 + dd + (k - 2);
+                },
+                tag, v, err);
+        } else {
 #pragma unroll
-            for (int i = 0; i < DJ + 2; i++) v[i] = 0.f;
+            for (int i = 0; i < 2 * (DJ + 2); i++) v[i] = i == 0 || i == DJ + 2 ? -INFINITY : 0.f;
         }
-        const float M = max32(v[0]);
-        const float w = v[0] == -INFINITY ? 0.f : expf(v[0] - M);
-        const float L = sum32(w * v[1]);
+        const float* v0 = v;
+        const float* v1 = v + DJ + 2;
+        const float M = row_max(fmaxf(v0[0], v1[0]));
+        const float w0 = v0[0] == -INFINITY ? 0.f : expf(v0[0] - M);
+        const float w1 = v1[0] == -INFINITY ? 0.f : expf(v1[0] - M);
+        const float L = row_sum(w0 * v0[1] + w1 * v1[1]);
         float O[DJ];
 #pragma unroll
-        for (int i = 0; i < DJ; i++) O[i] = sum32(w * v[2 + i]);
+        for (int i = 0; i < DJ; i++) O[i] = row_sum(w0 * v0[2 + i] + w1 * v1[2 + i]);
         if (js == 0 && b < nb) {
             const float inv = L > 0.f ? 1.0f / L : 0.f;
 #pragma unroll
@@ -560,7 +632,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     // ---- step 4: output projection rows of this workgroup over the XCD's
     // K slice: the merged rows (all of them) as int8 planes with one scale
     // per row, then the MFMAs of waves 4-7 on the weights requested at start
-    float* Xo = &KT[0][0];
+    float* Xo = (float*)&KHL[0][0][0];
     int8_t* P8o = (int8_t*)(Xo + MAXB * QD);
     int4v* red = (int4v*)(P8o + 3 * QC * 1024);
     {
@@ -640,15 +712,30 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
 // ---------------------------------------------------------------------------
 // FFN launch
 // ---------------------------------------------------------------------------
-// The q4 operand element (batch row b, column e of tile tt) as f16 hi/lo in
-// the MFMA A layout [tile][k-slot][row][8], HL: hi in row b, lo in row 8 + b
-// of one plane; otherwise hi and lo planes (lo at +lo_off halves), row b.
+// Eight operand columns 8 s .. 8 s + 7 of tile tt, batch row b, as f16 hi /
+// lo in the MFMA A layout [tile][k-slot][row][8] (the nibble-pair order
+// {0,4,2,6,1,5,3,7} within the slot); HL: hi in row b, lo in row 8 + b of
+// one plane, otherwise hi and lo planes (lo at +lo_off halves), row b.  The
+// quad sum of (hi + lo) over the tile's four slots comes back (the bias).
 template <bool HL>
-__device__ __forceinline__ void put_hl(_Float16* ap, int lo_off, int tt, int e, int b, _Float16 hi, _Float16 lo) {
-    const int o = ((tt * 4 + (e >> 3)) * 16 + b) * 8 + nib_slot(e & 7);
-    ap[o] = hi;
-    if constexpr (HL) ap[o + 64] = lo;  // row 8 + b
-    else ap[lo_off + o] = lo;
+__device__ __forceinline__ float put8(_Float16* ap, int lo_off, int tt, int s, int b, const float (&v)[8], bool on) {
+    half8 h8, l8;
+    float part = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float x = v[nib_slot(k)];
+        const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+        h8[k] = hi;
+        l8[k] = lo;
+        part += f16_pair_sum(hi, lo);
+    }
+    const int o = ((tt * 4 + s) * 16 + b) * 8;
+    if (on) {
+        *(half8*)(ap + o) = h8;
+        if constexpr (HL) *(half8*)(ap + o + 64) = l8;  // row 8 + b
+        else *(half8*)(ap + lo_off + o) = l8;
+    }
+    return quad_sum(part);
 }
 // One tile's MFMA: A rows of the operand, B the 8 nibbles of the lane's word
 // as f16 denormals, C the tile's bias rows 4 s .. 4 s + 3.
@@ -684,7 +771,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
     constexpr int NPAIR = RBD * G8, PW = (NPAIR + 3) / 4;
     constexpr int NT2 = I8 / 32;            // tiles of the down operand
     constexpr int LO0 = HL ? 0 : 4 * 4 * 16 * 8, LO2 = HL ? 0 : NT2 * 4 * 16 * 8;
-    static_assert(NRB0 % 4 == 0 && RPB * NKG == XL_WG && IW <= 16 && I8 % 128 == 0,
+    static_assert(NRB0 % 4 == 0 && RPB * NKG == XL_WG && IW <= 16 && I8 % 128 == 0 && I8 <= 512,
                   "shape");
 
     // the XCD this workgroup runs on; workgroups i and i + 8 share one, so
@@ -711,31 +798,30 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
     const int w4 = wave - 4;
     uint4 wg[RBW];
     uint64_t sg[RBW];
-    float hv[4][2], pv[4][2][8];
-    float wn0 = 0.f, wn1 = 0.f;
+    // step-0 operand: thread (b = t / 16, columns 8 (t % 16) .. + 7) of the
+    // group, i.e. one DPP row per batch row and one quad per 32-column tile
+    float4v hv4[2], pv4[2][8], wn4[2];
     uint4 wd[PW];
     uint64_t sd[PW];
-    const int c0 = kg * 128 + lane, c1 = c0 + 64;
+    const int cg = kg * 128 + 8 * (t & 15);
     if (wave < 4) {
+        // the weights first (the long HBM round trip), then the operand
 #pragma unroll
         for (int i = 0; i < RBW; i++) {
             const int g = x * NRBX + rp * NRB0 + wave + 4 * i;
             wg[i] = ld_stream(a.wgu + ((size_t)g * a.ntg_gu + kg) * 64 + lane);
             sg[i] = ldg(a.sgu + ((size_t)g * a.ntg_gu + kg) * 16 + r);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        const int b = min(t >> 4, nb - 1);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int b = min(wave + 4 * i, nb - 1);
-            hv[i][0] = ldg(a.hb + (size_t)b * H + c0);
-            hv[i][1] = ldg(a.hb + (size_t)b * H + c1);
+        for (int hf = 0; hf < 2; hf++) {
+            hv4[hf] = ldg((const float4v*)(a.hb + (size_t)b * H + cg + 4 * hf));
 #pragma unroll
-            for (int xx = 0; xx < 8; xx++) {
-                pv[i][0][xx] = ldg(a.parts + ((size_t)xx * MAXB + b) * H + c0);
-                pv[i][1][xx] = ldg(a.parts + ((size_t)xx * MAXB + b) * H + c1);
-            }
+            for (int xx = 0; xx < 8; xx++)
+                pv4[hf][xx] = ldg((const float4v*)(a.parts + ((size_t)xx * MAXB + b) * H + cg + 4 * hf));
+            wn4[hf] = ldg((const float4v*)(a.nw + cg + 4 * hf));
         }
-        wn0 = ldg(a.nw + c0);
-        wn1 = ldg(a.nw + c1);
     } else {
 #pragma unroll
         for (int k = 0; k < PW; k++) {
@@ -753,46 +839,45 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
 
     XL_MARK(17);
     // ---- step 0: this 128-column group of h_mid * w_norm as f16 hi/lo
-    // (waves 0-3, wave w holding batch rows w, w + 4, ...), h_mid written by
-    // XCD 0
+    // (waves 0-3), h_mid written by XCD 0
     if (wave < 4) {
+        const int b = t >> 4, c8 = t & 15;
+        float4v h[2];
+        float u[8];
+        double ss = 0.0;
+        float am = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int b = wave + 4 * i;
-            if (b >= nb) break;
-            float h0 = hv[i][0], h1 = hv[i][1];
+        for (int hf = 0; hf < 2; hf++) {
+            h[hf] = hv4[hf];
 #pragma unroll
-            for (int xx = 0; xx < 8; xx++) {
-                h0 += pv[i][0][xx];
-                h1 += pv[i][1][xx];
+            for (int xx = 0; xx < 8; xx++) h[hf] += pv4[hf][xx];
+            if (b < nb && x == 0 && rp == 0) *(float4v*)(a.hout + (size_t)b * H + cg + 4 * hf) = h[hf];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ss += (double)h[hf][i] * (double)h[hf][i];
+                u[4 * hf + i] = h[hf][i] * wn4[hf][i];
+                am = fmaxf(am, fabsf(u[4 * hf + i]));
             }
-            if (x == 0 && rp == 0) {
-                a.hout[(size_t)b * H + c0] = h0;
-                a.hout[(size_t)b * H + c1] = h1;
-            }
-            const double ss = wave_sum((double)h0 * (double)h0 + (double)h1 * (double)h1);
-            const float u0 = h0 * wn0, u1 = h1 * wn1;
-            const float am = wave_max(fmaxf(fabsf(u0), fabsf(u1)));
-            float sc, xs;
-            f16_scale(am, sc, xs);
-            const float v0 = u0 * sc, v1 = u1 * sc;
-            const _Float16 hi0 = (_Float16)v0, lo0 = (_Float16)(v0 - (float)hi0);
-            const _Float16 hi1 = (_Float16)v1, lo1 = (_Float16)(v1 - (float)hi1);
-            const float ts0 = sum32(f16_pair_sum(hi0, lo0)), ts1 = sum32(f16_pair_sum(hi1, lo1));
-            const int e = lane & 31, tt0 = lane >> 5, tt1 = 2 + (lane >> 5);
-            put_hl<HL>(AP, LO0, tt0, e, b, hi0, lo0);
-            put_hl<HL>(AP, LO0, tt1, e, b, hi1, lo1);
-            if (e == 0) {
-                LB[tt0 * 16 + b] = ts0 * -4.76837158203125e-07f;  // -8 * 2^-24
-                LB[tt1 * 16 + b] = ts1 * -4.76837158203125e-07f;
-            }
-            if (lane == 0) {
+        }
+        ss = row_sum_d(ss);
+        am = row_max(am);
+        float sc, xs;
+        f16_scale(am, sc, xs);
+#pragma unroll
+        for (int i = 0; i < 8; i++) u[i] *= sc;
+        const int tt = c8 >> 2;
+        const float ts = put8<HL>(AP, LO0, tt, c8 & 3, b, u, b < nb);
+        if (b < nb) {
+            if ((c8 & 3) == 0) LB[tt * 16 + b] = ts * -4.76837158203125e-07f;  // -8 * 2^-24
+            if (c8 == 0) {
                 xs0[b] = xs;
                 ssd[b] = ss;
             }
         }
     }
+    XL_MARK(26);
     lds_barrier();
+    XL_MARK(27);
     uint64_t* e0w = a.e0 + (size_t)(x * XL_WG + j) * MAXB * a.e0s;
     if (wave < 4) {
 #pragma unroll
@@ -877,27 +962,22 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
     XL_MARK(22);
     lds_barrier();
     for (int b = wave; b < nb; b += 8) {
-        float vv[I8 / 64];
+        // lane l < I8 / 8: columns 8 l .. 8 l + 7 (tile l / 4, k-slot l % 4)
+        constexpr int NL = I8 / 8;
+        const int l = min(lane, NL - 1);
+        const float4v v0 = *(const float4v*)&Xd[b * I8 + 8 * l], v1 = *(const float4v*)&Xd[b * I8 + 8 * l + 4];
+        float u[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
         float am = 0.f;
 #pragma unroll
-        for (int k = 0; k < I8 / 64; k++) {
-            vv[k] = Xd[b * I8 + 64 * k + lane];
-            am = fmaxf(am, fabsf(vv[k]));
-        }
+        for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(u[i]));
         am = wave_max(am);
         float sc, xs;
         f16_scale(am, sc, xs);
         if (lane == 0) xs2[b] = xs;
-        const int e = lane & 31;
 #pragma unroll
-        for (int k = 0; k < I8 / 64; k++) {
-            const float v = vv[k] * sc;
-            const _Float16 hi = (_Float16)v, lo = (_Float16)(v - (float)hi);
-            const float ts = sum32(f16_pair_sum(hi, lo));
-            const int tt = 2 * k + (lane >> 5);
-            put_hl<HL>(AP2, LO2, tt, e, b, hi, lo);
-            if (e == 0) LB2[tt * 16 + b] = ts * -4.76837158203125e-07f;
-        }
+        for (int i = 0; i < 8; i++) u[i] *= sc;
+        const float ts = put8<HL>(AP2, LO2, l >> 2, l & 3, b, u, lane < NL);
+        if (lane < NL && (lane & 3) == 0) LB2[(l >> 2) * 16 + b] = ts * -4.76837158203125e-07f;
     }
     XL_MARK(23);
     lds_barrier();
