@@ -13,7 +13,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libcmfhip.so")
+# CMF_LIB: another build of the library (A/B timing of two builds on one box)
+LIB_PATH = os.environ.get("CMF_LIB") or os.path.join(_HERE, "libcmfhip.so")
 
 DT_Q8ROW, DT_Q4T, DT_Q4TP = 3, 11, 15
 

@@ -615,7 +615,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
         const int c0 = kpl * KS * SP + wave * SP;
         // unconditional loads (steps past the row clamped to its last one)
 #pragma unroll
-        for (int u = 0; u < SP; u++) wv[u] = ld_stream((const int4v*)a.w + (wbase + min(c0 + u, nkc - 1)) * 64 + lane);
+        for (int u = 0; u < SP; u++) wv[u] = ldg((const int4v*)a.w + (wbase + min(c0 + u, nkc - 1)) * 64 + lane);
     };
     int4v wA[SP];
     float xsv = 0.f;

@@ -59,13 +59,14 @@ constexpr int XL_SPIN = 1 << 16;  // polls before a wait gives up (~50 ms)
 
 // Phase timestamps for tuning builds (XL_STAMPS defined before this file is
 // compiled: lane 0 of waves 0 and 4 of every workgroup records
-// s_memrealtime at the marks into xl_stamps[workgroup][wave / 4][32]).
+// s_memrealtime at the marks into stamps[workgroup][wave / 4][32], the
+// buffer a kernel argument so that a mark waits for no memory operation).
 #ifdef XL_STAMPS
-__device__ unsigned long long* xl_stamps;
-#define XL_MARK(k)                                                                                   \
-    do {                                                                                             \
-        if ((threadIdx.x & 255) == 0 && xl_stamps)                                                   \
-            xl_stamps[(blockIdx.x * 2 + (threadIdx.x >> 8)) * 32 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+unsigned long long* xl_stamp_buf = nullptr;  // host: the buffer the launches pass
+#define XL_MARK(k)                                                                               \
+    do {                                                                                         \
+        if ((threadIdx.x & 255) == 0 && a.stamps)                                                \
+            a.stamps[(blockIdx.x * 2 + (threadIdx.x >> 8)) * 32 + (k)] = __builtin_amdgcn_s_memrealtime(); \
     } while (0)
 #else
 #define XL_MARK(k) \
@@ -222,6 +223,7 @@ struct XlAArgs {
     int* err;
     int nb, H, nh, max_seq;
     double eps;
+    unsigned long long* stamps;  // tuning builds only (XL_STAMPS)
 };
 
 struct XlBArgs {
@@ -243,6 +245,7 @@ struct XlBArgs {
     int* err;
     int nb, H;
     double eps;
+    unsigned long long* stamps;  // tuning builds only (XL_STAMPS)
 };
 
 // ---------------------------------------------------------------------------
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     __shared__ __align__(16) int8_t P8[3 * 4 * 16 * 16];
     __shared__ float sx0[MAXB], sxo[MAXB];
     __shared__ double ssd[MAXB], ssp[MAXB][NKC];
-    static_assert(MAXB * QD * 4 + 3 * QC * 1024 + 12 * 64 * 16 <= 2 * NPOS * (HD + 8) * 2, "overlay");
+    static_assert(3 * QC * 1024 + 12 * 64 * 16 <= 2 * NPOS * (HD + 8) * 2, "overlay");
 
     const int kc = j % NKC, rp = j / NKC;
     const int pos0 = *a.pbase + a.padd;
@@ -348,8 +351,8 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
         for (int u = 0; u < KVN; u++) {
             const int f = t4 + 256 * u, sl = f >> 5, c4 = f & 31;
             const size_t off = (size_t)(sl < nold ? plo + sl : 0) * HD + 4 * c4;
-            kq[u] = ldg((const float4v*)(kb + off));
-            vq[u] = ldg((const float4v*)(vb + off));
+            kq[u] = __builtin_nontemporal_load(gptr((const float4v*)(kb + off)));
+            vq[u] = __builtin_nontemporal_load(gptr((const float4v*)(vb + off)));
         }
     }
 
@@ -394,6 +397,11 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     lds_barrier();
     XL_MARK(14);
     uint64_t* e0w = a.e0 + (size_t)(x * XL_WG + j) * MAXB * a.e0s;
+    // step 1's thread (row, b1): XCD row R1; its partials and share in pv1
+    const bool on1 = t < RW * nb, ss_on = t < NKC * nb;
+    const int b1 = min(t / RW, nb - 1), R1 = j * RW + t % RW;
+    const int rpp = R1 / ROWS0, lrow = R1 % ROWS0;
+    float pv1[NKC + 2];
     if (wave < 4) {
         const int4v* A = (const int4v*)P8;
         const int4v a0 = A[s * 16 + r], a1 = A[64 + s * 16 + r], a2 = A[128 + s * 16 + r];
@@ -421,34 +429,35 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             xput(e0w + (size_t)t * a.e0s + ROWS0 + 1, lo, tag);
         }
         XL_MARK(2);
-        // ---- step 1a: sum(h^2) shares of the NKC chunks (row part 0)
-        if (t < NKC * nb) {
-            const int k = t % NKC, b = t / NKC;
-            const uint64_t* p = a.e0 + ((size_t)(x * XL_WG + k) * MAXB + b) * a.e0s + ROWS0;
-            float v2[2];
-            xget<2>([&](int i) { return p + i; }, tag, v2, err);
-            ssp[b][k] = (double)v2[0] + (double)v2[1];
+        // ---- step 1: rows [RW j, RW j + RW) of the XCD: thread (row, b)
+        // waits for its NKC chunk partials and, at once, for one of the
+        // sum(h^2) shares (chunk t % NKC, row t / NKC; row part 0)
+        const int ks = ss_on ? t % NKC : 0, bs = ss_on ? t / NKC : 0;
+        const uint64_t* pss = a.e0 + ((size_t)(x * XL_WG + ks) * MAXB + bs) * a.e0s + ROWS0;
+        if (on1 || ss_on) {  // (only the threads that own a row or a share poll)
+            xget<NKC + 2>(
+                [&](int k) {
+                    return k < NKC ? a.e0 + ((size_t)(x * XL_WG + rpp * NKC + k) * MAXB + b1) * a.e0s + lrow
+                                   : pss + (k - NKC);
+                },
+                tag, pv1, err);
+            if (ss_on) ssp[bs][ks] = (double)pv1[NKC] + (double)pv1[NKC + 1];
         }
     }
     XL_MARK(3);
     lds_barrier();
     if (wave < 4) {
-        // ---- step 1b: rows [RW j, RW j + RW) of the XCD: chunk partials in
-        // chunk order, times 1 / rms (inference.rs:33-50: f64 mean of squares)
-        for (int id = t; id < RW * nb; id += 256) {
-            const int row = id % RW, b = id / RW, R = j * RW + row;
-            const int rpp = R / ROWS0, lrow = R % ROWS0;
-            float pv16[NKC];
-            xget<NKC>([&](int k) { return a.e0 + ((size_t)(x * XL_WG + rpp * NKC + k) * MAXB + b) * a.e0s + lrow; },
-                      tag, pv16, err);
+        // the partials in chunk order, times 1 / rms (inference.rs:33-50: f64
+        // mean of squares)
+        if (on1) {
             double ss = 0.0;
 #pragma unroll
-            for (int k = 0; k < NKC; k++) ss += ssp[b][k];
+            for (int k = 0; k < NKC; k++) ss += ssp[b1][k];
             const float inv = (float)(1.0 / sqrt(ss / (double)H + a.eps));
             float acc = 0.f;
 #pragma unroll
-            for (int k = 0; k < NKC; k++) acc += pv16[k];
-            xput(a.e1 + ((size_t)x * MAXB + b) * a.e1s + R, acc * inv, tag);
+            for (int k = 0; k < NKC; k++) acc += pv1[k];
+            xput(a.e1 + ((size_t)x * MAXB + b1) * a.e1s + R1, acc * inv, tag);
         }
     } else {
         // waves 4-7: the cached K (as f16 hi / lo) and V of this workgroup's
@@ -707,6 +716,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             }
         }
     }
+    XL_MARK(12);
 }
 
 // ---------------------------------------------------------------------------
@@ -753,7 +763,6 @@ __device__ __forceinline__ uint32_t word_of(const uint4& w, int tt) {
 }
 __device__ __forceinline__ float tile_scale(uint64_t sw, int tt) {
     return f16_bits_to_f32((uint32_t)(sw >> (16 * tt)) & 0xFFFFu);
-    XL_MARK(12);
 }
 
 // NKG = H / 128 (K groups of gate|up), I8 = I / 8 (the XCD's inter slice),
@@ -879,6 +888,20 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
     lds_barrier();
     XL_MARK(27);
     uint64_t* e0w = a.e0 + (size_t)(x * XL_WG + j) * MAXB * a.e0s;
+    // step 1's items t and t + 256: row part, row within it, batch row; the
+    // partials (and a sum(h^2) share) in pg
+    const bool ss_on = t < NKG * nb;
+    int rpi[2], lri[2], bi[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int id = min(t + 256 * u, 2 * IW * nb - 1);
+        const int il = id % IW, gu = (id / IW) & 1;
+        const int i = IW * j + il, R = 16 * (i >> 3) + (i & 7) + 8 * gu;
+        rpi[u] = R / ROWS0;
+        lri[u] = R % ROWS0;
+        bi[u] = id / (2 * IW);
+    }
+    float pg[2 * NKG + 2];
     if (wave < 4) {
 #pragma unroll
         for (int i = 0; i < RBW; i++) {
@@ -906,35 +929,43 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
             xput(e0w + (size_t)t * a.e0s + ROWS0 + 1, lo, tag);
         }
         XL_MARK(18);
-        // ---- step 1a: sum(h^2) shares of the NKG groups (row part 0)
-        if (t < NKG * nb) {
-            const int k = t % NKG, b = t / NKG;
-            const uint64_t* p = a.e0 + ((size_t)(x * XL_WG + k) * MAXB + b) * a.e0s + ROWS0;
-            float v2[2];
-            xget<2>([&](int i) { return p + i; }, tag, v2, err);
-            ssp[b][k] = (double)v2[0] + (double)v2[1];
+        // ---- step 1: thread t waits for the group partials of the gate / up
+        // rows of items t and t + 256 (item = (inter index IW j + il, gate or
+        // up, b)) and, at once, for one sum(h^2) share (group t % NKG, row
+        // t / NKG; row part 0)
+        const int ks = ss_on ? t % NKG : 0, bs = ss_on ? t / NKG : 0;
+        const uint64_t* pss = a.e0 + ((size_t)(x * XL_WG + ks) * MAXB + bs) * a.e0s + ROWS0;
+        if (t < 2 * IW * nb || ss_on) {  // (only the threads that own an item or a share poll)
+            xget<2 * NKG + 2>(
+                [&](int k) {
+                    return k < 2 * NKG
+                               ? a.e0 + ((size_t)(x * XL_WG + rpi[k / NKG] * NKG + k % NKG) * MAXB + bi[k / NKG]) *
+                                            a.e0s +
+                                     lri[k / NKG]
+                               : pss + (k - 2 * NKG);
+                },
+                tag, pg, err);
+            if (ss_on) ssp[bs][ks] = (double)pg[2 * NKG] + (double)pg[2 * NKG + 1];
         }
     }
     XL_MARK(19);
     lds_barrier();
-    // ---- step 1b: gate and up rows of inter indices [IW j, IW j + IW): group
-    // partials in order, times 1 / rms
+    // the partials in group order, times 1 / rms
     if (wave < 4) {
-        for (int id = t; id < 2 * IW * nb; id += 256) {
-            const int il = id % IW, gu = (id / IW) & 1, b = id / (2 * IW);
-            const int i = IW * j + il, R = 16 * (i >> 3) + (i & 7) + 8 * gu;
-            const int rpp = R / ROWS0, lrow = R % ROWS0;
-            float pg[NKG];
-            xget<NKG>([&](int k) { return a.e0 + ((size_t)(x * XL_WG + rpp * NKG + k) * MAXB + b) * a.e0s + lrow; },
-                      tag, pg, err);
-            double ss = 0.0;
 #pragma unroll
-            for (int k = 0; k < NKG; k++) ss += ssp[b][k];
-            const float inv = (float)(1.0 / sqrt(ss / (double)H + a.eps));
-            float acc = 0.f;
+        for (int u = 0; u < 2; u++) {
+            const int id = t + 256 * u;
+            if (id < 2 * IW * nb) {
+                const int il = id % IW, gu = (id / IW) & 1, b = bi[u];
+                double ss = 0.0;
 #pragma unroll
-            for (int k = 0; k < NKG; k++) acc += pg[k];
-            GU[(gu * MAXB + b) * IW + il] = acc * inv;
+                for (int k = 0; k < NKG; k++) ss += ssp[b][k];
+                const float inv = (float)(1.0 / sqrt(ss / (double)H + a.eps));
+                float acc = 0.f;
+#pragma unroll
+                for (int k = 0; k < NKG; k++) acc += pg[u * NKG + k];
+                GU[(gu * MAXB + b) * IW + il] = acc * inv;
+            }
         }
     }
     XL_MARK(20);
@@ -1121,6 +1152,9 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
     A.nh = s.nh;
     A.max_seq = s.max_seq;
     A.eps = s.eps;
+#ifdef XL_STAMPS
+    A.stamps = xl_stamp_buf;
+#endif
     if (li > 127) return fail("xl: too many blocks in one sequence");
     hipLaunchKernelGGL((k_xl_attn<2, 16>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, A);
     XlBArgs B{};
@@ -1145,6 +1179,9 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
     B.nb = nb;
     B.H = s.H;
     B.eps = s.eps;
+#ifdef XL_STAMPS
+    B.stamps = xl_stamp_buf;
+#endif
     if (nb <= 8) hipLaunchKernelGGL((k_xl_ffn<8, 384, true>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, B);
     else hipLaunchKernelGGL((k_xl_ffn<8, 384, false>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, B);
     return CMF_OK;
