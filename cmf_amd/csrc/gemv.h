@@ -85,6 +85,12 @@ struct GemvArgs {
 typedef void (*GemvKernel)(GemvArgs);
 GemvKernel q4t_kernel(int m, int xm, int ks, int rb);
 GemvKernel q4tp_kernel(int m, int xm, int ks, int rb);
+// three groups of 4 waves per workgroup (k_gemv_q4<..., G = 3, SPW = 8>)
+GemvKernel q4t_kernel_g3(int m, int xm);
+GemvKernel q4tp_kernel_g3(int m, int xm);
+// 16 waves x 6 steps (k_gemv_q4<..., KS = 16, HL, ..., SPW = 6>), m <= 8
+GemvKernel q4t_kernel_s6(int m, int xm);
+GemvKernel q4tp_kernel_s6(int m, int xm);
 GemvKernel q8_kernel(int m, int xm, int ks);
 
 enum { EPI_NONE = 0, EPI_SWIGLU = 1 };

@@ -376,7 +376,7 @@ static int resident_per_cu(GemvKernel k, int threads, size_t lds) {
     if (hipFuncGetAttributes(&fa, (const void*)k) == hipSuccess) st = fa.sharedSizeBytes;
     const size_t cap = 160 * 1024 > st ? 160 * 1024 - st : 0;
     (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize,
-                              (int)std::min<size_t>(cap, LDSX_MAX));
+                              (int)cap);
     int occ = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, (const void*)k, threads, lds) != hipSuccess) occ = 0;
     (void)hipGetLastError();
@@ -441,6 +441,52 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
         lds = fused_lds_bytes(w, a.src, m);
         if (!lds || gridy > 1) return fail("gemv: this operand must be prepared (launch_prep_src)");
         xm = XM_FUSED;
+    }
+    // Two more q4 shapes of the prepared-operand GEMV, chosen by what
+    // measured faster on MI355X (GEMV alone, 10 weight copies rotating;
+    // CMF_GEMV_G=0/3 and CMF_GEMV_S6=0/1 force either):
+    //  - three groups of 4 waves x 8 steps per workgroup, one workgroup per
+    //    CU sharing one operand copy, for K <= 4096 and 4 <= m <= 8 (the
+    //    per-workgroup operand, 16 KiB per batch row, was read three times
+    //    per CU): 12288x4096 m=4 10.3 -> 9.4 us, m=8 12.5 -> 10.1 us; q4tp
+    //    m=5 11.0 -> 10.7 us (m=1 8.2 vs 7.5 us, m=2 8.9 vs 8.4: 12 waves per
+    //    CU hide the stream's latency worse than 24);
+    //  - 16 waves x 6 steps for rows of 65..96 steps (K <= 12288), one K part
+    //    instead of two walked one after the other: 4096x12288 m=1 9.0 ->
+    //    8.8 us, m=8 12.9 -> 12.6 us (m=2 9.6 vs 10.0 us: not used there;
+    //    q4tp at m > 1 keeps the 16 x 4 kernel, whose in-place variant
+    //    would spill).
+    static const int g_env = env_int("CMF_GEMV_G", -1), s6_env = env_int("CMF_GEMV_S6", -1);
+    const bool alt_ok = w.dtype != DT_Q8ROW && gridy == 1 && grid_override <= 0 && ks_override <= 0 &&
+                        a.src.mode == XS_GLOBAL && !a.src.cs;
+    const bool g3 = alt_ok && w.kchunks <= 32 && a.nrb >= 3 * num_cus() &&
+                    (g_env == 3 || (g_env < 0 && m >= 4 && m <= 8));
+    if (g3) {
+        const size_t lg = lds_bytes(w, m);  // (K <= 4096, m <= 8: at most 139 KiB)
+        GemvKernel kg = lg <= (size_t)LDSX_MAX_G3 ? (w.dtype == DT_Q4T ? q4t_kernel_g3(m, XM_PREP)
+                                                                    : q4tp_kernel_g3(m, XM_PREP))
+                                                  : nullptr;
+        const int og = kg ? resident_per_cu(kg, 64 * 4 * 3, lg) : 0;
+        if (og >= 1) {
+            a.lds = 1;
+            const int grid = std::min((a.nrb + 2) / 3, og * num_cus());
+            void* args[] = {&a};
+            CMF_HIP(hipLaunchKernel((const void*)kg, dim3(grid), dim3(64 * 4 * 3), args, lg, st));
+            return CMF_OK;
+        }
+    }
+    const bool s6 = alt_ok && w.kchunks > 64 && w.kchunks <= 96 && m <= 8 &&
+                    (s6_env == 1 || (s6_env < 0 && (m == 1 || m >= 5)));
+    if (s6) {
+        GemvKernel k6 = w.dtype == DT_Q4T ? q4t_kernel_s6(m, xm) : q4tp_kernel_s6(m, xm);
+        const int o6 = k6 ? resident_per_cu(k6, 1024, lds) : 0;
+        if (o6 >= 1) {
+            a.lds = lds ? 1 : 0;
+            const int grid = std::min(a.nrb, o6 * num_cus());
+            void* args[] = {&a};
+            CMF_HIP(hipLaunchKernel((const void*)k6, dim3(grid), dim3(1024), args, lds, st));
+            return CMF_OK;
+        }
     }
     a.lds = lds ? 1 : 0;
     const int threads = 64 * ks;

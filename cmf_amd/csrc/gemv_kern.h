@@ -69,6 +69,7 @@ __device__ __forceinline__ uint4 ld_stream(const uint4* p) {
 }
 
 constexpr int LDSX_MAX = 128 * 1024;  // largest LDS-staged activation operand (+ scratch)
+constexpr int LDSX_MAX_G3 = 144 * 1024;  // ... of a grouped (one per CU) workgroup
 
 // Four nibble bytes (8 weights: elements 8s..8s+7 of a tile) to the f16
 // denormals n * 2^-24 (exact, the raw nibble under a zero exponent) in the
@@ -326,8 +327,8 @@ constexpr int SP = 4;  // weight steps per wave and work unit
 // XM_PREPC (q8): XM_PREP with one scale per (batch row, 64-column chunk)
 enum { XM_PREP = 0, XM_FUSED = 1, XM_GLOBAL = 2, XM_PREPC = 3 };
 
-template <int FMT, int NV, int KS, bool HL, int XM, int RB>
-__global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
+template <int FMT, int NV, int KS, bool HL, int XM, int RB, int G = 1, int SPW = SP>
+__global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
     GemvArgs a = args;
     if (a.jobs) {  // grouped launch: this workgroup serves job blockIdx.y
         const int j = blockIdx.y;
@@ -341,53 +342,67 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
         a.y += j * a.y_stride;
     }
     extern __shared__ __align__(16) uint8_t smem[];
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // G groups of KS waves: group grp owns its own row blocks, wave (K
+    // share) within it; the groups share the operand copy
+    const int grp = G > 1 ? wv / KS : 0, wave = G > 1 ? wv % KS : wv;
     const int r = lane & 15, s = lane >> 4;
     const int M = a.m, ntg = a.nk;  // nk = groups of 4 tiles
     constexpr bool TP = FMT == DT_Q4TP;
     constexpr int LD = 16 * 33;  // one row block's ladders
-    __shared__ float lad[TP ? 2 : 1][TP ? RB * LD : 1];  // ladders of the current / next row blocks
-    __shared__ float4v part[KS][RB][64];
+    __shared__ float lad[G][TP ? 2 : 1][TP ? RB * LD : 1];  // ladders of the current / next row blocks
+    __shared__ float4v part[G][KS][RB][64];
     __shared__ float lxs[16];
-    const int P = (ntg + KS * SP - 1) / (KS * SP);  // K parts per row block
-    const int rstep = gridDim.x * RB;
-    int rb = blockIdx.x * RB, kp = 0;  // first of the RB row blocks of the unit
-    if (rb >= a.nrb) return;           // uniform over the workgroup
+    const int P = (ntg + KS * SPW - 1) / (KS * SPW);  // K parts per row block
+    const int rstep = gridDim.x * G * RB;
+    int rb = (blockIdx.x * G + grp) * RB, kp = 0;  // first of the RB row blocks of the unit
+    // groups past the matrix run with clamped loads and store nothing; the
+    // workgroup's first group decides (uniform) when the walk ends
+    if (blockIdx.x * G * RB >= a.nrb) return;
     // weights + tile scales of a unit (q4tp: and the row ladder parameters
     // of its row blocks), all unconditional (steps past the row clamped to
     // its last one, row blocks past the matrix to its last one): a load
     // under a branch makes the compiler wait for it at once.  NL = loads per
     // call.
-    constexpr int NL = RB * (2 * SP + (TP ? 1 : 0));
-    auto load = [&](uint4* wv, uint2* sv, float2* pv, int rbl, int kpl) {
-        const int t0 = kpl * KS * SP + wave * SP;
+    constexpr int NL = RB * (2 * SPW + (TP ? 1 : 0));
+    auto load_steps = [&](uint4* wv, uint2* sv, int rbl, int kpl, int u0, int u1) {
+        const int t0 = kpl * KS * SPW + wave * SPW;
 #pragma unroll
         for (int q = 0; q < RB; q++) {
             const size_t wbase = (size_t)(a.rb0 + min(rbl + q, a.nrb - 1)) * ntg;
 #pragma unroll
-            for (int u = 0; u < SP; u++) {
+            for (int u = u0; u < u1; u++) {
                 const size_t t = wbase + min(t0 + u, ntg - 1);
-                wv[q * SP + u] = ld_stream((const uint4*)a.w + t * 64 + lane);
-                if constexpr (TP) sv[q * SP + u] = make_uint2(ldg((const uint32_t*)a.scale + t * 16 + r), 0u);
+                wv[q * SPW + u] = ld_stream((const uint4*)a.w + t * 64 + lane);
+                if constexpr (TP) sv[q * SPW + u] = make_uint2(ldg((const uint32_t*)a.scale + t * 16 + r), 0u);
                 else {
                     const uint64_t sw = ldg((const uint64_t*)a.scale + t * 16 + r);  // (scalar type: see gptr)
-                    sv[q * SP + u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
+                    sv[q * SPW + u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
                 }
             }
-            if constexpr (TP) pv[q] = ldg_f2(a.rowp + (a.rb0 + min(rbl + q, a.nrb - 1)) * 16 + r);
         }
+    };
+    auto load_rowp = [&](float2* pv, int rbl) {
+        if constexpr (TP) {
+#pragma unroll
+            for (int q = 0; q < RB; q++) pv[q] = ldg_f2(a.rowp + (a.rb0 + min(rbl + q, a.nrb - 1)) * 16 + r);
+        }
+    };
+    auto load = [&](uint4* wv, uint2* sv, float2* pv, int rbl, int kpl) {
+        load_steps(wv, sv, rbl, kpl, 0, SPW);
+        load_rowp(pv, rbl);
     };
     // the 32-rung ladder of each row of the RB row blocks: t[c] = t[c-1] *
     // ratio (quant.rs:399-410), by 16 threads per row block starting at the
     // second wave (the first one reduces meanwhile)
     auto ladder = [&](int buf, const float2* p) {
         if constexpr (TP) {
-            const int lt = (int)threadIdx.x - (KS > 1 ? 64 : 0);
+            const int lt = (int)threadIdx.x - grp * 64 * KS - (KS > 1 ? 64 : 0);
 #pragma unroll
             for (int q = 0; q < RB; q++) {
                 if (lt >= 16 * q && lt < 16 * q + 16) {
                     float tv = p[q].x;
-                    float* lq = &lad[buf][q * LD + (lt - 16 * q) * 33];
+                    float* lq = &lad[grp][buf][q * LD + (lt - 16 * q) * 33];
                     lq[0] = tv;
                     for (int c = 1; c < 32; c++) {
                         tv = tv * p[q].y;
@@ -397,8 +412,8 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
             }
         }
     };
-    uint4 wA[RB * SP];
-    uint2 sA[RB * SP];
+    uint4 wA[RB * SPW];
+    uint2 sA[RB * SPW];
     float2 pA[RB] = {};
     float xsv = 0.f;
     float* raw = (float*)(smem + planes_lds_bytes(FMT, ntg, M));
@@ -451,15 +466,15 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
     // one work unit: rb/kp current, rn the next unit's first row block
     // (rn >= nrb: none); one operand read serves the RB row blocks
     auto process = [&](const uint4* wv, const uint2* sv, const float2* pn, int rn) {
-        const int t0 = kp * KS * SP + wave * SP;
+        const int t0 = kp * KS * SPW + wave * SPW;
 #pragma unroll
-        for (int u = 0; u < SP; u++) {
+        for (int u = 0; u < SPW; u++) {
             if (t0 + u < ntg) {
                 const int tg = t0 + u;
                 float sc[RB][4];
 #pragma unroll
                 for (int q = 0; q < RB; q++) {
-                    const uint2 sq = sv[q * SP + u];
+                    const uint2 sq = sv[q * SPW + u];
                     if constexpr (!TP) {
                         sc[q][0] = f16_bits_to_f32(sq.x & 0xFFFFu);
                         sc[q][1] = f16_bits_to_f32(sq.x >> 16);
@@ -467,7 +482,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
                         sc[q][3] = f16_bits_to_f32(sq.y >> 16);
                     } else {
                         const uint32_t cw = sq.x;
-                        const float* lq = &lad[buf][q * LD + r * 33];
+                        const float* lq = &lad[grp][buf][q * LD + r * 33];
                         sc[q][0] = lq[cw & 31];
                         sc[q][1] = lq[(cw >> 5) & 31];
                         sc[q][2] = lq[(cw >> 10) & 31];
@@ -487,10 +502,10 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
                     }
 #pragma unroll
                     for (int q = 0; q < RB; q++) {
-                        const uint32_t wq = t == 0 ? wv[q * SP + u].x
-                                            : t == 1 ? wv[q * SP + u].y
-                                            : t == 2 ? wv[q * SP + u].z
-                                                     : wv[q * SP + u].w;
+                        const uint32_t wq = t == 0 ? wv[q * SPW + u].x
+                                            : t == 1 ? wv[q * SPW + u].y
+                                            : t == 2 ? wv[q * SPW + u].z
+                                                     : wv[q * SPW + u].w;
                         const half8 bq = dq_nib_word(wq);
                         float4v d;
                         if constexpr (HL) {
@@ -508,7 +523,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
         if (kp < P - 1) return;  // the row blocks continue in the next unit
         if constexpr (KS > 1) {
 #pragma unroll
-            for (int q = 0; q < RB; q++) part[wave][q][lane] = acc[q];
+            for (int q = 0; q < RB; q++) part[grp][wave][q][lane] = acc[q];
             __syncthreads();
         }
         if (wave == 0) {
@@ -517,7 +532,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
                 float4v o4 = acc[q];
 #pragma unroll
                 for (int w = 1; w < KS; w++) {
-                    const float4v o = part[w][q][lane];
+                    const float4v o = part[grp][w][q][lane];
 #pragma unroll
                     for (int v = 0; v < NV; v++) o4[v] += o[v];
                 }
@@ -556,7 +571,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
         for (int q = 0; q < RB; q++) acc[q] = zero;
         if (rn < a.nrb) ladder(buf ^ 1, pn);
         buf ^= 1;
-        if constexpr (KS > 1 || TP) __syncthreads();
+        if constexpr (KS > 1 || TP || G > 1) __syncthreads();
     };
 
     for (;;) {
@@ -572,7 +587,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4(GemvArgs args) {
                 for (int q = 0; q < RB; q++) pn[q] = ldg_f2(a.rowp + (a.rb0 + min(rn + q, a.nrb - 1)) * 16 + r);
             }
         process(wA, sA, pn, rn);
-        if (rn >= a.nrb) break;
+        if (rn - grp * RB >= a.nrb) break;  // the first group's next unit (uniform)
         rb = rn;
         kp = kn;
         load(wA, sA, pA, rb, kp);
@@ -856,6 +871,24 @@ GemvKernel q4_by_xm(int xm, int ks, int rb) {
     } else {
         return rb == 1 ? q4_by_ks<FMT, NV, HL, XM_PREP, 1>(ks) : nullptr;
     }
+}
+// Grouped workgroups (G = 3 groups of 4 waves x 8 steps: three row blocks of
+// K <= 4096 share one operand copy in LDS), m <= 8
+template <int FMT>
+GemvKernel q4_pick_g3(int m, int xm) {
+    if (xm != XM_PREP || m > 8) return nullptr;
+    return m == 1 ? k_gemv_q4<FMT, 1, 4, true, XM_PREP, 1, 3, 8> : k_gemv_q4<FMT, 4, 4, true, XM_PREP, 1, 3, 8>;
+}
+// 16 waves x 6 steps: rows of 65..96 steps (K <= 12288) in one K part
+template <int FMT>
+GemvKernel q4_pick_s6(int m, int xm) {
+    if (m > 8) return nullptr;
+    if (xm == XM_PREP) return m == 1 ? k_gemv_q4<FMT, 1, 16, true, XM_PREP, 1, 1, 6> : k_gemv_q4<FMT, 4, 16, true, XM_PREP, 1, 1, 6>;
+    if (xm != XM_GLOBAL) return nullptr;
+    if (m == 1) return k_gemv_q4<FMT, 1, 16, true, XM_GLOBAL, 1, 1, 6>;
+    // (q4tp's in-place instance for m > 1 needs more than 128 registers)
+    if constexpr (FMT == DT_Q4T) return k_gemv_q4<FMT, 4, 16, true, XM_GLOBAL, 1, 1, 6>;
+    return nullptr;
 }
 template <int FMT>
 GemvKernel q4_pick(int m, int xm, int ks, int rb) {
