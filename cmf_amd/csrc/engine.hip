@@ -9,6 +9,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 
 #include <string>
 #include <vector>
@@ -26,6 +27,7 @@ namespace cmf {
 
 struct LayerDev {
     float *in_norm = nullptr, *post_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    float qk_norm_max = 0.f;  // max |q_norm|, |k_norm| (bounds the normed q / k rows)
     DevWeight qkv, wo, gu, down;
     float *kc = nullptr, *vc = nullptr;
     // routed-expert FFN (GraphFfn::Moe, gpu.rs:1248-1361): the router and the
@@ -237,6 +239,9 @@ int upload_layer(cmf_model_s* m, LayerDev& l, const cmf_layer_desc* d, bool kv) 
     if (upload_f32(m, &l.in_norm, d->input_norm, H) || upload_f32(m, &l.post_norm, d->post_norm, H) ||
         upload_f32(m, &l.q_norm, d->q_norm, hd) || upload_f32(m, &l.k_norm, d->k_norm, hd))
         return CMF_ERR;
+    l.qk_norm_max = 0.f;
+    for (int i = 0; i < hd; i++)
+        l.qk_norm_max = std::max(l.qk_norm_max, std::max(std::fabs(d->q_norm[i]), std::fabs(d->k_norm[i])));
     free_weight(l.qkv);
     free_weight(l.wo);
     free_weight(l.gu);
@@ -399,9 +404,15 @@ void run_block(cmf_model_s* m, LayerDev& l, float* h, int nb, const int* pb, int
 // Whether block l runs as the two XCD-partitioned launches for nb rows:
 // q8 attention weights, q4t FFN weights, a dense FFN, a shape xlayer.hip
 // is built for.
+// The fused blocks score with f16 hi / lo halves of the normed, rotated q
+// and k rows, which needs |q|, |k| < 65504: after the qk-norm an element is at
+// most sqrt(head_dim) * max|norm weight| (|x_i| / rms(x) <= sqrt(n)), after
+// RoPE sqrt(2) times that, so norm weights up to 2048 keep it below 32768.
+constexpr float XL_QK_NORM_MAX = 2048.f;
 bool xl_layer_ok(cmf_model_s* m, const LayerDev& l, int nb, int max_len) {
     return m->xl_on && !l.moe && l.kc && l.qkv.dtype == DT_Q8ROW && l.wo.dtype == DT_Q8ROW &&
-           l.gu.dtype == DT_Q4T && l.down.dtype == DT_Q4T && xl_shape_ok(m->xls, nb, max_len);
+           l.gu.dtype == DT_Q4T && l.down.dtype == DT_Q4T && l.qk_norm_max <= XL_QK_NORM_MAX &&
+           xl_shape_ok(m->xls, nb, max_len);
 }
 XlAttnW xl_aw(const LayerDev& l) {
     return XlAttnW{l.qkv.w, l.qkv.scale, l.wo.w, l.wo.scale, l.qkv.kchunks, l.wo.kchunks,

@@ -28,9 +28,12 @@
 //      1 / rms (rms_norm's row factor moves past the matvec);
 //   2. attention: workgroup j takes an equal share of 16-position tiles of
 //      [0, pos0 + nb); q-norm + RoPE of the queries, k-norm + RoPE and the
-//      cache append of new rows, scores / softmax / values on the fp32 MFMA
-//      (K and V of its cached positions were requested at kernel start by
-//      waves 4-7, so that stream overlaps steps 0-1);
+//      cache append of new rows, scores on the f16 MFMA from hi / lo halves
+//      of q and k (q_h k_h + q_h k_l + q_l k_h, 22-bit operands, f32
+//      accumulation; the host keeps layers whose qk-norm weights could take
+//      |q|, |k| past the f16 range on the six-launch path), softmax, values
+//      on the fp32 MFMA (K and V of its cached positions were requested at
+//      kernel start by waves 4-7, so that stream overlaps steps 0-1);
 //   3. workgroup j merges 8 output dims over the 32 position shares;
 //   4. output projection rows [32 j, 32 j + 32) over the XCD's K slice
 //      (weights requested at kernel start) -> partial pa[x].
