@@ -429,7 +429,7 @@ void trunk_forward(cmf_model_s* m, int nb, const int* pb, int padd, int max_len,
     for (int li = 0; li < c.n_layers && xl; li++) xl = xl_layer_ok(m, m->L[li], nb, max_len);
     if (xl) {
         for (int li = 0; li < c.n_layers; li++)
-            xl_block(m->xl, m->xls, xl_aw(m->L[li]), xl_fw(m->L[li]), m->hv, nb, pb, padd, m->rope, li, s);
+            xl_block(m->xl, m->xls, xl_aw(m->L[li]), xl_fw(m->L[li]), m->hv, nb, pb, padd, max_len, m->rope, li, s);
         xl_finish(m->xl, m->xls, m->hv, nb, s);
     } else {
         for (int li = 0; li < c.n_layers; li++) run_block(m, m->L[li], m->hv, nb, pb, padd, max_len, s);
@@ -476,7 +476,7 @@ void mtp_step(cmf_model_s* m, const int* tok, const float* hin, float* hout, con
     const int H = c.hidden;
     gemv_f(m, m->eh, src_cat(m, tok, hin), hout, H, 1, false, s);
     if (xl_layer_ok(m, m->mtp, 1, max_len)) {
-        xl_block(m->xl, m->xls, xl_aw(m->mtp), xl_fw(m->mtp), hout, 1, pb, padd, m->rope, 0, s);
+        xl_block(m->xl, m->xls, xl_aw(m->mtp), xl_fw(m->mtp), hout, 1, pb, padd, max_len, m->rope, 0, s);
         xl_finish(m->xl, m->xls, hout, 1, s);
     } else {
         run_block(m, m->mtp, hout, 1, pb, padd, max_len, s);

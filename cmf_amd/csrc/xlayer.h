@@ -55,8 +55,9 @@ int xl_alloc(XlBufs& b, const XlShape& s, void* (*alloc)(void*, size_t), void* c
 // rows to ha and leaves its output projection as partials pa; the FFN launch
 // writes h_mid = ha + sum(pa) to hb and leaves the down projection as
 // partials pb, until the next block or xl_finish adds them.
+// max_len bounds the positions after the block's rows (as xl_shape_ok).
 int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW& fw, const float* h0, int nb,
-             const int* pbase, int padd, const float2* rope, int li, hipStream_t st);
+             const int* pbase, int padd, int max_len, const float2* rope, int li, hipStream_t st);
 // hout = hb + sum(pb) (the sequence's output rows); next generation.
 void xl_finish(const XlBufs& b, const XlShape& s, float* hout, int nb, hipStream_t st);
 

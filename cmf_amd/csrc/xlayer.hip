@@ -254,8 +254,11 @@ struct XlBArgs {
 // ---------------------------------------------------------------------------
 // attention launch
 // ---------------------------------------------------------------------------
-// HPK query heads per kv head, NKC = H / 64 (K chunks of the q|k|v rows).
-template <int HPK, int NKC>
+// HPK query heads per kv head, NKC = H / 64 (K chunks of the q|k|v rows),
+// BT = 16-position tiles a workgroup holds (<= XL_BT; the K / V requests
+// cover BT tiles whatever the share, so the host picks the smallest BT the
+// call's position bound needs).
+template <int HPK, int NKC, int BT>
 __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     constexpr int HD = 128, NKV = XL_XCD;
     constexpr int RX = (HPK + 2) * HD;         // q|k|v rows of one XCD
@@ -270,9 +273,9 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     constexpr int WPR = 4 / RBO;               // waves per wo row block (waves 4-7)
     constexpr int CW = QC / WPR;               // wo chunks per wave
     constexpr int DJ = QD / XL_WG;             // merged dims per workgroup
-    constexpr int NPOS = XL_BT * 16;
+    constexpr int NPOS = BT * 16;
     constexpr int KVN = NPOS * 32 / 256;       // float4 of K (and of V) per thread of waves 4-7
-    static_assert(NRB0 % 4 == 0 && RP * NKC == XL_WG && RW <= 16 && WPR * RBO == 4 && DJ >= 1, "shape");
+    static_assert(NRB0 % 4 == 0 && RP * NKC == XL_WG && RW <= 16 && WPR * RBO == 4 && DJ >= 1 && BT <= XL_BT, "shape");
 
     // the XCD this workgroup runs on; workgroups i and i + 8 share one, so
     // blockIdx / 8 numbers the 32 workgroups of each XCD
@@ -302,9 +305,9 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     const int P = pos0 + nb, T = (P + 15) >> 4;
     const int tlo = j * T / XL_WG;
     int thi = (j + 1) * T / XL_WG;
-    if (thi - tlo > XL_BT) {  // more positions than the host's bound admitted
+    if (thi - tlo > BT) {  // more positions than the host's bound admitted
         if (t == 0) atomicOr(err, 4);
-        thi = tlo + XL_BT;
+        thi = tlo + BT;
     }
     const int plo = tlo * 16, phi = min(thi * 16, P);
     const int np = max(0, phi - plo), nold = max(0, min(phi, pos0) - plo);
@@ -1122,7 +1125,7 @@ int xl_alloc(XlBufs& b, const XlShape& s, void* (*alloc)(void*, size_t), void* c
 }
 
 int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW& fw, const float* h0, int nb,
-             const int* pbase, int padd, const float2* rope, int li, hipStream_t st) {
+             const int* pbase, int padd, int max_len, const float2* rope, int li, hipStream_t st) {
     XlAArgs A{};
     A.hb = li == 0 ? h0 : b.hb;
     A.parts = li == 0 ? nullptr : b.pb;
@@ -1159,7 +1162,15 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
     A.stamps = xl_stamp_buf;
 #endif
     if (li > 127) return fail("xl: too many blocks in one sequence");
-    hipLaunchKernelGGL((k_xl_attn<2, 16>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, A);
+    // tiles per workgroup for the bound (measured: 5 instead of 6 tiles at
+    // context 2048 took the K = 4 round 1.133 -> 1.122 ms)
+    const int bt = ((max_len + 15) / 16 + XL_WG - 1) / XL_WG;
+    if (bt <= 4)
+        hipLaunchKernelGGL((k_xl_attn<2, 16, 4>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, A);
+    else if (bt == 5)
+        hipLaunchKernelGGL((k_xl_attn<2, 16, 5>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, A);
+    else
+        hipLaunchKernelGGL((k_xl_attn<2, 16, 6>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, A);
     XlBArgs B{};
     B.hb = b.ha;
     B.parts = b.pa;

@@ -14,7 +14,9 @@ Checked: verify-batch hidden rows (1, 5, 9 and 16 rows: one MFMA for hi and
 lo planes up to 8 rows, two beyond) within 3e-4 relative L2 of the oracle
 and 5e-5 of the six-launch blocks, the same argmax; greedy and sampled
 tokens and accepted counts equal to the oracle's, eager and graph-captured;
-the committed trunk and MTP caches equal to plain forwards."""
+the committed trunk and MTP caches equal to plain forwards; at contexts of
+1000, 2300 and 2900 positions (the attention launch's three tile counts) the
+verify rows and new K / V rows equal the six-launch blocks'."""
 import os
 
 import numpy as np
@@ -155,3 +157,46 @@ def test_sampled_decode_like_oracle(xl):
     print(f"T=0.8: gpu accepted {gst.accepted}/{gst.drafted} oracle {ost.accepted}/{ost.drafted}", flush=True)
     assert gt.tolist() == ot.tolist()
     assert gst.accepted == ost.accepted and gst.accepted > 0
+
+
+XL_LONG = dict(XL, max_seq=3072)
+
+
+@pytest.fixture(scope="module")
+def xl_long(gpu):
+    from cmf_amd import synth
+    sm = synth.accept_model(XL_LONG, sigma=0.02, eh_noise=10.0)
+    g, six = _model(sm), _model(sm, xl=False)
+    assert gpu.lib().cmf_model_fused_blocks(g.h) == 1
+    yield sm, g, six
+    g.free()
+    six.free()
+
+
+@pytest.mark.parametrize("pos0", [1000, 2300, 2900])
+def test_long_context_matches_six_launch(xl_long, pos0):
+    """the attention launch is instantiated for 4, 5 and 6 position tiles
+    per workgroup, picked from the call's position bound (pos0 + b: 63, 145
+    and 182 tiles over 32 workgroups); after the same prefill, the verify
+    rows and the appended K / V rows equal the six-launch blocks' (whose
+    attention the oracle pins at short context)"""
+    sm, g, six = xl_long
+    from cmf_amd import synth
+    prompt = synth.ids(31, pos0, XL["vocab"])
+    ids = synth.ids(37, 5, XL["vocab"])
+    g.prefill(prompt)
+    six.prefill(prompt)
+    h1, l1 = g.forward_batch(ids, pos0)
+    h0, l0 = six.forward_batch(ids, pos0)
+    for i in range(len(ids)):
+        e = rel_l2(h1[i], h0[i])
+        print(f"pos0={pos0} row {i}: hidden rel {e:.2e}", flush=True)
+        assert e < PATH_TOL
+        assert int(np.argmax(l1[i])) == int(np.argmax(l0[i]))
+    n = pos0 + len(ids)
+    for li in range(XL["n_layers"]):
+        k1, v1 = g.kv_export(li, n)
+        k0, v0 = six.kv_export(li, n)
+        ek, ev = rel_l2(k1[:, pos0:], k0[:, pos0:]), rel_l2(v1[:, pos0:], v0[:, pos0:])
+        print(f"  layer {li}: new K rel {ek:.2e} V rel {ev:.2e}", flush=True)
+        assert ek < PATH_TOL and ev < PATH_TOL
