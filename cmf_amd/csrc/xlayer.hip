@@ -303,8 +303,10 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     const int kc = j % NKC, rp = j / NKC;
     const int pos0 = *a.pbase + a.padd;
     const int P = pos0 + nb, T = (P + 15) >> 4;
-    const int tlo = j * T / XL_WG;
-    int thi = (j + 1) * T / XL_WG;
+    // shares rounded up: the extra tiles of T % 32 go to the first
+    // workgroups, not to the last one, which also appends the new rows
+    const int tlo = (j * T + XL_WG - 1) / XL_WG;
+    int thi = ((j + 1) * T + XL_WG - 1) / XL_WG;
     if (thi - tlo > BT) {  // more positions than the host's bound admitted
         if (t == 0) atomicOr(err, 4);
         thi = tlo + BT;
