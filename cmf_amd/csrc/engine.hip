@@ -110,7 +110,7 @@ struct cmf_model_s {
     int next_pos_host = 0;
     bool prefilled = false;
     // prefill chunk buffers [PREFILL_CHUNK rows] (allocated by the first prefill)
-    float *pf_h = nullptr, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_gu = nullptr, *pf_hm = nullptr;
+    float *pf_h = nullptr, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_gu = nullptr, *pf_hm = nullptr, *pf_q = nullptr;
     int* pf_toks = nullptr;
     hipGraphExec_t round_graph = nullptr;
     int graph_k = 0;
@@ -564,7 +564,8 @@ int ensure_prefill_bufs(cmf_model_s* m) {
     const size_t R = PREFILL_CHUNK;
     if (dalloc_t(m, &m->pf_h, R * H) || dalloc_t(m, &m->pf_qkv, R * QKV) ||
         dalloc_t(m, &m->pf_ao, R * c.n_heads * c.head_dim) || dalloc_t(m, &m->pf_gu, R * 2 * c.inter) ||
-        dalloc_t(m, &m->pf_hm, R * H) || dalloc_t(m, &m->pf_toks, R))
+        dalloc_t(m, &m->pf_hm, R * H) || dalloc_t(m, &m->pf_toks, R) ||
+        dalloc_t(m, &m->pf_q, R * c.n_heads * c.head_dim))
         return CMF_ERR;
     return CMF_OK;
 }
@@ -576,6 +577,15 @@ void prefill_attention(cmf_model_s* m, LayerDev& l, const float* qkv, float* ao,
                        bool attend, hipStream_t s) {
     const auto& c = m->c;
     const int hd = c.head_dim, nh = c.n_heads, nkv = c.n_kv, QKV = (nh + 2 * nkv) * hd;
+    static const bool tiled = !(getenv("CMF_PREFILL_ATTN") && getenv("CMF_PREFILL_ATTN")[0] == '0');
+    if (tiled && prefill_attention_fits(nh, nkv, hd)) {
+        // the whole chunk at once: the tiled prefill attention (one launch
+        // for the norms + append, one for the attention)
+        PrefillAttnArgs pa{qkv, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq, cnt, p0, nh, nkv,
+                           c.eps, m->pf_q, attend ? ao : nullptr};
+        launch_prefill_attention(pa, s);
+        return;
+    }
     const int rows_per = std::min(MAXB, std::max(1, 32 / (nh / nkv)));
     for (int b0 = 0; b0 < cnt; b0 += rows_per) {
         const int nb = std::min(rows_per, cnt - b0);

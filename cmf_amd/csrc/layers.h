@@ -52,6 +52,24 @@ struct AttnArgs {
 };
 // k_attention (chunk partials) then, with merge, k_attn_merge (rows of a.out).
 void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge = true);
+
+// Causal attention of a prefill chunk (prefill_attn.hip): cnt rows at
+// positions p0 + i of qkv [cnt][ldq] (q | k | v heads); q/k-norm + RoPE, the
+// rows' K / V appended to the cache, out [cnt][nh * 128] (out == nullptr:
+// only the append).  qbuf: [cnt][nh][128] scratch for the rotated queries.
+struct PrefillAttnArgs {
+    const float* qkv;
+    int ldq;
+    const float *qn, *kn;
+    const float2* rope;
+    float *kc, *vc;
+    int max_seq, cnt, p0, nh, nkv;
+    double eps;
+    float* qbuf;
+    float* out;
+};
+bool prefill_attention_fits(int nh, int nkv, int hd);
+int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);
 // The lexicographic (value, index) maximum step of argmax (sampler.rs:1130-1154
 // keeps the higher index on equal values; NaN never wins).
 __device__ __forceinline__ void argmax_take(float& bv, int& bi, float v, int i) {
