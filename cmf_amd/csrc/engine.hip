@@ -112,6 +112,7 @@ struct cmf_model_s {
     // prefill chunk buffers [PREFILL_CHUNK rows] (allocated by the first prefill)
     float *pf_h = nullptr, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_gu = nullptr, *pf_hm = nullptr, *pf_q = nullptr;
     int* pf_toks = nullptr;
+    _Float16* pf_khl = nullptr;  // the prefill attention's K / V operands (f16 hi / lo keys, then f32 values)
     hipGraphExec_t round_graph = nullptr;
     int graph_k = 0;
     int graph_len = 0;  // attention length bound the captured round was built for
@@ -565,7 +566,8 @@ int ensure_prefill_bufs(cmf_model_s* m) {
     if (dalloc_t(m, &m->pf_h, R * H) || dalloc_t(m, &m->pf_qkv, R * QKV) ||
         dalloc_t(m, &m->pf_ao, R * c.n_heads * c.head_dim) || dalloc_t(m, &m->pf_gu, R * 2 * c.inter) ||
         dalloc_t(m, &m->pf_hm, R * H) || dalloc_t(m, &m->pf_toks, R) ||
-        dalloc_t(m, &m->pf_q, R * c.n_heads * c.head_dim))
+        dalloc_t(m, &m->pf_q, R * c.n_heads * c.head_dim) ||
+        dalloc(m, (void**)&m->pf_khl, (size_t)c.n_kv * ((c.max_seq + 127) / 128 * 128) * c.head_dim * 8))
         return CMF_ERR;
     return CMF_OK;
 }
@@ -582,7 +584,7 @@ void prefill_attention(cmf_model_s* m, LayerDev& l, const float* qkv, float* ao,
         // the whole chunk at once: the tiled prefill attention (one launch
         // for the norms + append, one for the attention)
         PrefillAttnArgs pa{qkv, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq, cnt, p0, nh, nkv,
-                           c.eps, m->pf_q, attend ? ao : nullptr};
+                           c.eps, m->pf_q, attend ? ao : nullptr, m->pf_khl};
         launch_prefill_attention(pa, s);
         return;
     }

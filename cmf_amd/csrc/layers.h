@@ -56,7 +56,9 @@ void launch_attention(const AttnArgs& a, int max_len, hipStream_t st, bool merge
 // Causal attention of a prefill chunk (prefill_attn.hip): cnt rows at
 // positions p0 + i of qkv [cnt][ldq] (q | k | v heads); q/k-norm + RoPE, the
 // rows' K / V appended to the cache, out [cnt][nh * 128] (out == nullptr:
-// only the append).  qbuf: [cnt][nh][128] scratch for the rotated queries.
+// only the append).  qbuf: [cnt][nh][128] scratch for the rotated queries;
+// khl: scratch for the rearranged K / V operands, nkv * npad * 128 * 8 bytes
+// (npad = ceil((p0 + cnt) / 128) * 128).
 struct PrefillAttnArgs {
     const float* qkv;
     int ldq;
@@ -67,6 +69,7 @@ struct PrefillAttnArgs {
     double eps;
     float* qbuf;
     float* out;
+    _Float16* khl;
 };
 bool prefill_attention_fits(int nh, int nkv, int hd);
 int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);

@@ -1,27 +1,26 @@
 // Causal attention of a prefill chunk (head_dim 128) for gfx950.
 //
 // The chunk's rows sit at positions p0 .. p0 + cnt - 1 (p0 known to the
-// host).  k_prefill_qk applies q-norm + RoPE to the queries (into a scratch
-// buffer) and k-norm + RoPE to the new K rows, appending K and V to the
-// cache (attention.rs:606-624, 818-890; kv_cache.rs:366-505), exactly as the
-// decode kernels do.  k_prefill_attn then runs the attention of 16 query rows
-// per workgroup — 16 / HPK positions times the HPK query heads of one kv
-// head, which share its K / V — over 64-position key tiles with a running
-// (online) softmax:
-//   - the tile's K as f16 hi / lo halves and V (f32) in LDS, the next tile's
-//     K / V requested into registers while the current one is used;
-//   - scores on the f16 MFMA (q.k = qh.kh + qh.kl + ql.kh, 22-bit operands,
-//     f32 sums), wave w the tile's keys 16 w .. 16 w + 15, causal limit the
-//     row's position (kv_cache.rs:521-690);
-//   - per row the running maximum m, the sum l and the factor exp(m_old -
-//     m_new) applied to the row's output before the tile's values are added;
-//   - values on the fp32 MFMA (16x16x4), wave w output dims 32 w .. 32 w + 31.
+// host).  Three launches per chunk and layer:
+//   - k_prefill_qk: q-norm + RoPE of the queries (into a scratch buffer),
+//     k-norm + RoPE of the new K rows, K and V appended to the cache
+//     (attention.rs:606-624, 818-890; kv_cache.rs:366-505), as the decode
+//     kernels do it;
+//   - k_prefill_kv: the cache's K / V rows [0, p0 + cnt) rearranged into
+//     the attention's MFMA operand layout (K as f16 hi / lo halves);
+//   - k_prefill_attn: 16 query rows per workgroup — 16 / HPK positions times
+//     the HPK query heads of one kv head, which share its K / V — over
+//     128-key tiles with a running (online) softmax: scores on the f16 MFMA
+//     (q.k = qh.kh + qh.kl + ql.kh, 22-bit operands, f32 sums), causal
+//     limit the row's position (kv_cache.rs:521-690), values on the fp32
+//     MFMA (16x16x4).
 // Rows of a workgroup past the chunk see no keys and write nothing.
 #include <math.h>
 
 #include "common.h"
 #include "layers.h"
 #include "wave.h"
+#include "xlayer.h"
 
 namespace cmf {
 
@@ -30,12 +29,47 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 128;
-constexpr int KT = 64;        // keys per tile
-constexpr int KST = HD + 8;   // f16 row stride of Q / K in LDS
-constexpr int VST = HD + 16;  // f32 row stride of V in LDS (conflict-free value operand reads)
-constexpr int PST = KT + 4;   // f32 row stride of the scores / weights
+constexpr int KT = 64;        // key rows per scratch padding unit
+constexpr int KT2 = 128;      // keys per attention tile (two groups of 64)
+constexpr int PST = KT + 4;   // f32 row stride of the scores / weights (64 keys a group)
+
+// Workgroup barrier over LDS only: __syncthreads also waits for every
+// global load in flight (vmcnt(0)), which would wait for the next tile's
+// K / V requests; uses of those registers get the compiler's own waits.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Four f32 reductions over the wave at once (each DPP step applied to all
+// four before the next, so the chains overlap), with the DPP pattern of
+// wave_reduce_f32; the results are wave-uniform.
+template <typename Op>
+__device__ __forceinline__ void wave_reduce4(float (&v)[4], float ident, Op op) {
+    const uint32_t iu = __builtin_bit_cast(uint32_t, ident);
+    auto step = [&](auto ctrl, auto rows) {
+        constexpr int C = decltype(ctrl)::value, R = decltype(rows)::value;
+        float w[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) w[i] = __builtin_bit_cast(float, dpp_u32<C, R>(__builtin_bit_cast(uint32_t, v[i]), iu));
+#pragma unroll
+        for (int i = 0; i < 4; i++) v[i] = op(v[i], w[i]);
+    };
+    step(std::integral_constant<int, 0xb1>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x4e>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xf>{});
+    step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xa>{});
+    step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xc>{});
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[i]), 63));
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(v));
+    return v;
+}
 
 __device__ __forceinline__ void split16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;
@@ -74,140 +108,236 @@ __global__ __launch_bounds__(64) void k_prefill_qk(const float* __restrict__ qkv
     }
 }
 
-// grid (ceil(cnt / (16 / HPK)), nkv), 256 threads.  Row q (0..15) of block
-// qb: chunk row qb * PPW + q % PPW, query head g * HPK + q / PPW.
-template <int HPK>
-__global__ __launch_bounds__(256) void k_prefill_attn(const float* __restrict__ qbuf, const float* __restrict__ kc,
-                                                      const float* __restrict__ vc, int max_seq, int cnt, int p0,
+// The cached K / V rows [0, n) of every kv head rearranged once per chunk
+// as the attention's MFMA operands, so that each wave load (16 B a lane)
+// reads 1 KiB in register order (rows [n, npad) zero):
+//   kop [nkv][npad / 16][8 chunks][64 lanes] x 16 B: key block kb (keys
+//       16 kb + r), chunk ch = 2 ks + plane (f16 hi / lo), lane 16 s + r:
+//       dims 32 ks + 8 s .. + 7 of key 16 kb + r;
+//   vop [nkv][npad / 64][8 dim blocks][4][64 lanes] x 16 B: key block kb
+//       (keys 64 kb ..), dim block db, step i, lane 16 s + r: keys
+//       64 kb + 16 s + 4 i .. + 3 of dim 16 db + r.
+// grid (npad / 64, nkv), 256 threads: 64 keys through LDS.
+__global__ __launch_bounds__(256) void k_prefill_kv(const float* __restrict__ kc, const float* __restrict__ vc,
+                                                    int max_seq, int n, int npad, int4v* __restrict__ kop,
+                                                    float4v* __restrict__ vop) {
+    const int t = threadIdx.x, kb64 = blockIdx.x, g = blockIdx.y;
+    __shared__ float KS[64][HD + 4], VS[64][HD + 1];
+    for (int e = t; e < 64 * 32; e += 256) {
+        const int k = e >> 5, c4 = 4 * (e & 31), key = 64 * kb64 + k;
+        float4v kv = {0.f, 0.f, 0.f, 0.f}, vv = kv;
+        if (key < n) {
+            kv = *(const float4v*)(kc + ((size_t)g * max_seq + key) * HD + c4);
+            vv = *(const float4v*)(vc + ((size_t)g * max_seq + key) * HD + c4);
+        }
+        *(float4v*)&KS[k][c4] = kv;
+#pragma unroll
+        for (int i = 0; i < 4; i++) VS[k][c4 + i] = vv[i];
+    }
+    __syncthreads();
+    const int nkb = npad / 16, nvb = npad / 64;
+    // K: 4 key blocks x 8 chunks x 64 lanes
+    for (int e = t; e < 4 * 8 * 64; e += 256) {
+        const int l = e & 63, ch = (e >> 6) & 7, kb = e >> 9, r = l & 15, sl = l >> 4;
+        const int ks = ch >> 1, plane = ch & 1, k = 16 * kb + r;
+        half8 h;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            _Float16 hh, ll;
+            split16(KS[k][32 * ks + 8 * sl + j], hh, ll);
+            h[j] = plane ? ll : hh;
+        }
+        kop[(((size_t)g * nkb + 4 * kb64 + kb) * 8 + ch) * 64 + l] = __builtin_bit_cast(int4v, h);
+    }
+    // V: 8 dim blocks x 4 steps x 64 lanes
+    for (int e = t; e < 8 * 4 * 64; e += 256) {
+        const int l = e & 63, i = (e >> 6) & 3, db = e >> 8, r = l & 15, sl = l >> 4;
+        float4v v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = VS[16 * sl + 4 * i + j][16 * db + r];
+        vop[(((size_t)g * nvb + kb64) * 8 + db) * 4 * 64 + i * 64 + l] = v;
+    }
+}
+
+// grid (ceil(cnt / (16 / HPK)), nkv), 512 threads.  Row q (0..15) of block
+// qb: chunk row qb * PPW + q % PPW, query head g * HPK + q / PPW.  XCD (8 kv
+// heads on an MI355X): grid (8 ceil(cnt / PPW)), kv head g = the XCD the
+// workgroup runs on, qb = blockIdx / 8 (the dispatcher deals workgroups to
+// the 8 XCDs in turn), so one head's K / V serves all of its query blocks
+// from that XCD's L2.
+// The 8 waves form two groups: group G takes keys 64 G .. 64 G + 63 of each
+// 128-key tile with a running softmax of its own, wave wl of the group the
+// scores of keys 16 wl .. + 15 and the values of dims 32 wl .. + 31; its K
+// and V operands come from the rearranged scratch straight into registers
+// (the next tile's requested while the current one is used), the queries
+// stay in registers, and LDS holds only the weights and row statistics.
+// The groups' (m, l, o) are merged at the end.
+template <int HPK, bool XCD>
+__global__ __launch_bounds__(512) void k_prefill_attn(const float* __restrict__ qbuf, const int4v* __restrict__ kop,
+                                                      const float4v* __restrict__ vop, int npad, int cnt, int p0,
                                                       int nh, float* __restrict__ out) {
     constexpr int PPW = 16 / HPK;  // positions per workgroup
-    const int qb = blockIdx.x, g = blockIdx.y, t = threadIdx.x, lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    constexpr int GK = KT2 / 2;    // keys per group and tile
+    const int qb = XCD ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+    const int g = XCD ? (int)(xcc_id() & 7) : (int)blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), G = wave >> 2, wl = wave & 3;
     const int r = lane & 15, s = lane >> 4;
-    __shared__ __align__(16) _Float16 QHL[2][16][KST];
-    __shared__ __align__(16) _Float16 KHL[2][KT][KST];
-    __shared__ __align__(16) float VT[KT][VST];
-    __shared__ __align__(16) float P[16][PST];
-    __shared__ float s_m[16], s_l[16], s_al[16];
+    __shared__ __align__(16) float P[2][16][PST];
+    __shared__ __align__(16) float O1[16][HD];
+    __shared__ float s_m[2][16], s_l[2][16], s_al[2][16];
     const int i0 = qb * PPW;
     const int npos = min(PPW, cnt - i0);
-    // the queries as f16 hi / lo (rows past the chunk: zeros)
-    for (int e = t; e < 16 * HD; e += 256) {
-        const int q = e / HD, d = e % HD;
-        const float v = q % PPW < npos ? qbuf[((size_t)(i0 + q % PPW) * nh + g * HPK + q / PPW) * HD + d] : 0.f;
-        split16(v, QHL[0][q][d], QHL[1][q][d]);
+    // the score operand's queries (row r, dims 32 ks + 8 s ..) as f16 hi / lo
+    half8 qh[HD / 32], ql[HD / 32];
+    {
+        const bool qv = r % PPW < npos;
+        const float* qrow = qbuf + ((size_t)(i0 + (qv ? r % PPW : 0)) * nh + g * HPK + r / PPW) * HD;
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++) {
+            const float4v a0 = *(const float4v*)(qrow + 32 * ks + 8 * s);
+            const float4v a1 = *(const float4v*)(qrow + 32 * ks + 8 * s + 4);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                _Float16 hh, ll;
+                split16(qv ? (j < 4 ? a0[j] : a1[j - 4]) : 0.f, hh, ll);
+                qh[ks][j] = hh;
+                ql[ks][j] = ll;
+            }
+        }
     }
-    if (t < 16) {
-        s_m[t] = -INFINITY;
-        s_l[t] = 0.f;
+    if (t < 32) {
+        s_m[t >> 4][t & 15] = -INFINITY;
+        s_l[t >> 4][t & 15] = 0.f;
     }
     const int plast = p0 + i0 + npos - 1;  // the block's last query position
-    const int ntiles = plast / KT + 1;
-    const float* kb = kc + (size_t)g * max_seq * HD;
-    const float* vb = vc + (size_t)g * max_seq * HD;
-    // thread t moves float4 f = t + 256 u of a tile: key f / 32, dims 4 (f % 32)
-    float4v kr[8], vr[8];
-    auto load_tile = [&](int tile) {
+    const int ntiles = plast / KT2 + 1;
+    const int nkb = npad / 16, nvb = npad / 64;
+    const int4v* kw = kop + ((size_t)g * nkb + 4 * G + wl) * 8 * 64 + lane;          // + tile * 8 key blocks
+    const float4v* vw = vop + (((size_t)g * nvb + G) * 8 + 2 * wl) * 4 * 64 + lane;  // + tile * 2 key blocks
+    int4v ka[8], kn[8];
+    float4v va[8], vn[8];
+    auto load = [&](int tile, int4v (&k)[8], float4v (&v)[8]) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int f = t + 256 * u;
-            const int key = min(tile * KT + (f >> 5), plast);  // (keys past the last query: masked)
-            kr[u] = *(const float4v*)(kb + (size_t)key * HD + 4 * (f & 31));
-            vr[u] = *(const float4v*)(vb + (size_t)key * HD + 4 * (f & 31));
-        }
+        for (int ch = 0; ch < 8; ch++) k[ch] = kw[(size_t)tile * 8 * 8 * 64 + ch * 64];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = vw[(size_t)tile * 2 * 8 * 4 * 64 + i * 64];
     };
-    load_tile(0);
-    const float scale = 1.0f / sqrtf((float)HD);
-    float4v o[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    for (int tile = 0; tile < ntiles; tile++) {
-        __syncthreads();  // the previous tile's LDS reads are done (and the queries written)
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int f = t + 256 * u, kl = f >> 5, c = 4 * (f & 31);
-            half4 h4, l4;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                _Float16 hh, ll;
-                split16(kr[u][i], hh, ll);
-                h4[i] = hh;
-                l4[i] = ll;
-            }
-            *(half4*)&KHL[0][kl][c] = h4;
-            *(half4*)&KHL[1][kl][c] = l4;
-            *(float4v*)&VT[kl][c] = vr[u];
-        }
-        __syncthreads();
-        if (tile + 1 < ntiles) load_tile(tile + 1);
-        // scores of keys 16 wave .. + 15 of the tile
+    // scores in log2 units: exp(x - m) = exp2(x log2e - m log2e)
+    const float scale = 1.4426950408889634f / sqrtf((float)HD);
+    float4v o[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    auto step = [&](int tile, const int4v (&k)[8], const float4v (&v)[8]) {
+        // scores of keys GK G + 16 wl .. + 15 of the tile
         {
-            float4v d = {0.f, 0.f, 0.f, 0.f};
+            float4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0, d2 = d0;
 #pragma unroll
             for (int ks = 0; ks < HD / 32; ks++) {
-                const int oo = 32 * ks + 8 * s;
-                const half8 qh = *(const half8*)&QHL[0][r][oo], ql = *(const half8*)&QHL[1][r][oo];
-                const half8 kh = *(const half8*)&KHL[0][16 * wave + r][oo];
-                const half8 kl = *(const half8*)&KHL[1][16 * wave + r][oo];
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh, kh, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh, kl, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql, kh, d, 0, 0, 0);
+                const half8 kh = __builtin_bit_cast(half8, k[2 * ks]), kl = __builtin_bit_cast(half8, k[2 * ks + 1]);
+                d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kh, d0, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kl, d1, 0, 0, 0);
+                d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], kh, d2, 0, 0, 0);
             }
-            const int key = tile * KT + 16 * wave + r;
+            const float4v d = d0 + (d1 + d2);
+            const int key = tile * KT2 + GK * G + 16 * wl + r;
+            lds_barrier();  // the previous tile's weights are read
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int q = 4 * s + e;
                 const bool see = q % PPW < npos && key <= p0 + i0 + q % PPW;
-                P[q][16 * wave + r] = see ? d[e] * scale : -INFINITY;
+                P[G][q][16 * wl + r] = see ? d[e] * scale : -INFINITY;
             }
         }
-        __syncthreads();
-        // running softmax: wave w rows 4 w .. 4 w + 3, lane = key
+        lds_barrier();
+        // running softmax of the group: wave wl rows 4 wl .. 4 wl + 3, lane =
+        // key (the four rows' reductions interleaved)
+        {
+            float sv[4], mo[4], mt[4], p[4];
 #pragma unroll
-        for (int qq = 0; qq < 4; qq++) {
-            const int q = 4 * wave + qq;
-            const float sv = P[q][lane];
-            const float mo = s_m[q];
-            const float mn = fmaxf(mo, wave_max(sv));
-            const float p = mn == -INFINITY ? 0.f : expf(sv - mn);
-            const float lt = wave_sum(p);
-            const float al = mo == -INFINITY ? 0.f : expf(mo - mn);
-            P[q][lane] = p;
-            if (lane == 0) {
-                s_m[q] = mn;
-                s_l[q] = s_l[q] * al + lt;
-                s_al[q] = al;
+            for (int qq = 0; qq < 4; qq++) {
+                sv[qq] = P[G][4 * wl + qq][lane];
+                mo[qq] = s_m[G][4 * wl + qq];
+                mt[qq] = sv[qq];
+            }
+            wave_reduce4(mt, -INFINITY, [](float x, float y) { return fmaxf(x, y); });
+            float mn[4];
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                mn[qq] = fmaxf(mo[qq], mt[qq]);
+                p[qq] = mn[qq] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[qq] - mn[qq]);
+                mt[qq] = p[qq];
+            }
+            wave_reduce4(mt, 0.f, [](float x, float y) { return x + y; });
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+                const int q = 4 * wl + qq;
+                const float al = mo[qq] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo[qq] - mn[qq]);
+                P[G][q][lane] = p[qq];
+                if (lane == 0) {
+                    s_m[G][q] = mn[qq];
+                    s_l[G][q] = s_l[G][q] * al + mt[qq];
+                    s_al[G][q] = al;
+                }
             }
         }
-        __syncthreads();
-        // values: output dims 32 wave + 16 tt + r, rows 4 s + e
+        lds_barrier();
+        // values: output dims 32 wl + 16 tt + r, rows 4 s + e; MFMA step kk
+        // takes key 16 s + kk of the group (lane s), as the operand layout
         {
             float al[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) al[e] = s_al[4 * s + e];
+            for (int e = 0; e < 4; e++) al[e] = s_al[G][4 * s + e];
 #pragma unroll
-            for (int tt = 0; tt < 2; tt++)
+            for (int tt = 0; tt < 4; tt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) o[tt][e] *= al[e];
-            const int d0 = 32 * wave;
+            float4v pa[4];
 #pragma unroll
-            for (int k = 0; k < KT / 4; k++) {
-                const int p = 4 * k + s;
-                const float a = P[r][p];
-                o[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, VT[p][d0 + r], o[0], 0, 0, 0);
-                o[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, VT[p][d0 + 16 + r], o[1], 0, 0, 0);
+            for (int i = 0; i < 4; i++) pa[i] = *(const float4v*)&P[G][r][16 * s + 4 * i];
+#pragma unroll
+            for (int kk = 0; kk < GK / 4; kk++) {
+                const float a = pa[kk >> 2][kk & 3];
+                o[(kk & 1) * 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, v[kk >> 2][kk & 3], o[(kk & 1) * 2], 0, 0, 0);
+                o[(kk & 1) * 2 + 1] =
+                    __builtin_amdgcn_mfma_f32_16x16x4f32(a, v[4 + (kk >> 2)][kk & 3], o[(kk & 1) * 2 + 1], 0, 0, 0);
             }
         }
+    };
+    load(0, ka, va);
+    for (int tile = 0; tile < ntiles; tile += 2) {
+        if (tile + 1 < ntiles) load(tile + 1, kn, vn);
+        step(tile, ka, va);
+        if (tile + 1 >= ntiles) break;
+        if (tile + 2 < ntiles) load(tile + 2, ka, va);
+        step(tile + 1, kn, vn);
     }
-    __syncthreads();
+    lds_barrier();
+    // merge: group 1 leaves its outputs in LDS, group 0 combines
+    // (m = max(m0, m1), w_G = exp2(m_G - m), out = sum_G w_G o_G / sum_G w_G l_G)
+    if (G == 1) {
 #pragma unroll
-    for (int tt = 0; tt < 2; tt++)
+        for (int tt = 0; tt < 2; tt++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) O1[4 * s + e][32 * wl + 16 * tt + r] = o[tt][e] + o[tt + 2][e];
+    }
+    lds_barrier();
+    if (G == 0) {
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int q = 4 * s + e;
-            if (q % PPW < npos) {
-                const int row = i0 + q % PPW, head = g * HPK + q / PPW;
-                out[(size_t)row * nh * HD + (size_t)head * HD + 32 * wave + 16 * tt + r] = o[tt][e] / s_l[q];
+            if (q % PPW >= npos) continue;
+            const float m0 = s_m[0][q], m1 = s_m[1][q], m = fmaxf(m0, m1);
+            const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
+            const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+            const float l = s_l[0][q] * w0 + s_l[1][q] * w1;
+            const int row = i0 + q % PPW, head = g * HPK + q / PPW;
+#pragma unroll
+            for (int tt = 0; tt < 2; tt++) {
+                const int dd = 32 * wl + 16 * tt + r;
+                out[(size_t)row * nh * HD + (size_t)head * HD + dd] =
+                    ((o[tt][e] + o[tt + 2][e]) * w0 + O1[q][dd] * w1) / l;
             }
         }
+    }
 }
 
 }  // namespace
@@ -225,15 +355,24 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(k_prefill_qk, dim3(a.cnt, hq + a.nkv), dim3(64), 0, st, a.qkv, a.ldq, a.qn, a.kn, a.rope,
                        a.kc, a.vc, a.max_seq, a.p0, a.nh, a.nkv, a.eps, a.qbuf, hq);
     if (!a.out) return CMF_OK;
-    const int hpk = a.nh / a.nkv, ppw = 16 / hpk;
-    const dim3 grid((a.cnt + ppw - 1) / ppw, a.nkv);
+    const int hpk = a.nh / a.nkv, ppw = 16 / hpk, nqb = (a.cnt + ppw - 1) / ppw;
+    const bool xcd = a.nkv == 8 && xl_device_fits();
+    const dim3 grid = xcd ? dim3(8 * nqb) : dim3(nqb, a.nkv);
+    typedef void (*Kern)(const float*, const int4v*, const float4v*, int, int, int, int, float*);
+    Kern k;
     switch (hpk) {
-        case 1: hipLaunchKernelGGL(k_prefill_attn<1>, grid, dim3(256), 0, st, a.qbuf, a.kc, a.vc, a.max_seq, a.cnt, a.p0, a.nh, a.out); break;
-        case 2: hipLaunchKernelGGL(k_prefill_attn<2>, grid, dim3(256), 0, st, a.qbuf, a.kc, a.vc, a.max_seq, a.cnt, a.p0, a.nh, a.out); break;
-        case 4: hipLaunchKernelGGL(k_prefill_attn<4>, grid, dim3(256), 0, st, a.qbuf, a.kc, a.vc, a.max_seq, a.cnt, a.p0, a.nh, a.out); break;
-        case 8: hipLaunchKernelGGL(k_prefill_attn<8>, grid, dim3(256), 0, st, a.qbuf, a.kc, a.vc, a.max_seq, a.cnt, a.p0, a.nh, a.out); break;
-        default: hipLaunchKernelGGL(k_prefill_attn<16>, grid, dim3(256), 0, st, a.qbuf, a.kc, a.vc, a.max_seq, a.cnt, a.p0, a.nh, a.out); break;
+        case 1: k = xcd ? k_prefill_attn<1, true> : k_prefill_attn<1, false>; break;
+        case 2: k = xcd ? k_prefill_attn<2, true> : k_prefill_attn<2, false>; break;
+        case 4: k = xcd ? k_prefill_attn<4, true> : k_prefill_attn<4, false>; break;
+        case 8: k = xcd ? k_prefill_attn<8, true> : k_prefill_attn<8, false>; break;
+        default: k = xcd ? k_prefill_attn<16, true> : k_prefill_attn<16, false>; break;
     }
+    const int n = a.p0 + a.cnt, npad = (n + KT2 - 1) / KT2 * KT2;
+    int4v* kop = (int4v*)a.khl;
+    float4v* vop = (float4v*)(a.khl + (size_t)a.nkv * npad * 2 * HD);
+    hipLaunchKernelGGL(k_prefill_kv, dim3(npad / 64, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, kop,
+                       vop);
+    hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a.qbuf, kop, vop, npad, a.cnt, a.p0, a.nh, a.out);
     return CMF_OK;
 }
 

@@ -43,6 +43,9 @@ struct XlFfnW {
     const float* post_norm;
 };
 
+// An MI355X as these launches assume it: gfx950 with 8 XCDs x 32 CUs, a
+// launch's workgroups dispatched round-robin over the XCDs.
+bool xl_device_fits();
 // Whether the shape (and the device) can take the XCD-partitioned blocks for
 // batches of up to nb rows and attention over up to max_len positions.
 bool xl_shape_ok(const XlShape& s, int nb, int max_len);

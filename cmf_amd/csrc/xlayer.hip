@@ -1077,7 +1077,7 @@ __global__ __launch_bounds__(256) void k_xl_finish(const float* __restrict__ hb,
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-static int device_fits() {
+bool xl_device_fits() {
     static int ok = -1;
     if (ok < 0) {
         int dev = 0;
@@ -1089,7 +1089,7 @@ static int device_fits() {
 }
 
 bool xl_shape_ok(const XlShape& s, int nb, int max_len) {
-    if (!device_fits()) return false;
+    if (!xl_device_fits()) return false;
     if (s.H != 1024 || s.I != 3072 || s.nkv != XL_XCD || s.hd != 128 || s.nh != 2 * XL_XCD) return false;
     if (nb < 1 || nb > MAXB || 2 * nb > XL_NQ) return false;
     const int tiles = (max_len + 15) / 16;
