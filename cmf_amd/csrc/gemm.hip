@@ -30,6 +30,11 @@ struct GemmArgs {
     const float* xs;      // [Mp] 2^-e per batch row (q8: amax / 127)
     float* y;
     int ldy, M, Mp, N, ntg, nrb, resid;
+    // split K: workgroup z takes K steps [z gsteps, (z + 1) gsteps) and
+    // writes its partial sums to part [z][M][N] (part == nullptr: one part,
+    // y written directly)
+    int gsteps;
+    float* part;
 };
 
 constexpr int GB = 64;             // batch rows per workgroup
@@ -101,12 +106,13 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
         for (int mb = 0; mb < 4; mb++) acc[q][mb] = float4v{0.f, 0.f, 0.f, 0.f};
 
     static_assert(GJ == 9, "GEMM_RA lists nine chunks");
+    const int gs0 = blockIdx.z * a.gsteps, gs1 = min(ntg, gs0 + a.gsteps);  // this part's K steps
     uint4 ra0, ra1, ra2, ra3, ra4, ra5, ra6, ra7, ra8, wA[GRB], wB[GRB];
     uint2 sA[GRB], sB[GRB];
     {
-        const int g_ = 0, buf_ = 0;
+        const int g_ = gs0, buf_ = 0;
         GEMM_RA(GEMM_LD)
-        load_w(wA, sA, 0);
+        load_w(wA, sA, gs0);
         GEMM_RA(GEMM_ST)
     }
     __syncthreads();
@@ -144,24 +150,24 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
         }
     };
 
-    for (int g = 0; g < ntg; g += 2) {
+    for (int g = gs0; g < gs1; g += 2) {
         // the next step's operand and weights go out before this step's MFMAs
         // (past the last step the loads repeat it and are not stored)
         {
-            const int g_ = min(g + 1, ntg - 1), buf_ = 1;
+            const int g_ = min(g + 1, gs1 - 1), buf_ = 1;
             GEMM_RA(GEMM_LD)
             load_w(wB, sB, g_);
             compute(0, wA, sA);
-            if (g + 1 < ntg) { GEMM_RA(GEMM_ST) }
+            if (g + 1 < gs1) { GEMM_RA(GEMM_ST) }
         }
         __syncthreads();
-        if (g + 1 >= ntg) break;
+        if (g + 1 >= gs1) break;
         {
-            const int g_ = min(g + 2, ntg - 1), buf_ = 0;
+            const int g_ = min(g + 2, gs1 - 1), buf_ = 0;
             GEMM_RA(GEMM_LD)
             load_w(wA, sA, g_);
             compute(1, wB, sB);
-            if (g + 2 < ntg) { GEMM_RA(GEMM_ST) }
+            if (g + 2 < gs1) { GEMM_RA(GEMM_ST) }
         }
         __syncthreads();
     }
@@ -178,9 +184,13 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
             for (int v = 0; v < 4; v++) {
                 const int b = GB * by + 16 * mb + 4 * s + v;
                 if (b < a.M) {
-                    float* yp = a.y + (size_t)b * a.ldy + n;
                     const float val = acc[q][mb][v] * a.xs[b] * 16777216.0f;
-                    *yp = a.resid ? *yp + val : val;
+                    if (a.part) {
+                        a.part[((size_t)blockIdx.z * a.M + b) * a.N + n] = val;
+                    } else {
+                        float* yp = a.y + (size_t)b * a.ldy + n;
+                        *yp = a.resid ? *yp + val : val;
+                    }
                 }
             }
     }
@@ -232,9 +242,10 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
             for (int p = 0; p < 3; p++) acc[q][mb][p] = int4v{0, 0, 0, 0};
     int4v ra[Q8J], wA[Q8RB][2], wB[Q8RB][2];
     const int nst = (nk + 1) / 2;
+    const int gs0 = blockIdx.z * a.gsteps, gs1 = min(nst, gs0 + a.gsteps);  // this part's K steps
 #pragma unroll
-    for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, 0));
-    load_w(wA, 0);
+    for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gs0));
+    load_w(wA, gs0);
 #pragma unroll
     for (int j = 0; j < Q8J; j++) At[0][(wave + 4 * j) * 64 + lane] = ra[j];
     __syncthreads();
@@ -258,27 +269,27 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
             }
         }
     };
-    for (int g = 0; g < nst; g += 2) {
+    for (int g = gs0; g < gs1; g += 2) {
         {
-            const int gn = min(g + 1, nst - 1);
+            const int gn = min(g + 1, gs1 - 1);
 #pragma unroll
             for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gn));
             load_w(wB, gn);
             compute(0, wA, g);
-            if (g + 1 < nst) {
+            if (g + 1 < gs1) {
 #pragma unroll
                 for (int j = 0; j < Q8J; j++) At[1][(wave + 4 * j) * 64 + lane] = ra[j];
             }
         }
         __syncthreads();
-        if (g + 1 >= nst) break;
+        if (g + 1 >= gs1) break;
         {
-            const int gn = min(g + 2, nst - 1);
+            const int gn = min(g + 2, gs1 - 1);
 #pragma unroll
             for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gn));
             load_w(wA, gn);
             compute(1, wB, g + 1);
-            if (g + 2 < nst) {
+            if (g + 2 < gs1) {
 #pragma unroll
                 for (int j = 0; j < Q8J; j++) At[0][(wave + 4 * j) * 64 + lane] = ra[j];
             }
@@ -299,11 +310,27 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
                     const float tt = (float)acc[q][mb][0][v] + (float)acc[q][mb][1][v] * 0.0078125f +
                                      (float)acc[q][mb][2][v] * 6.103515625e-05f;
                     const float val = (tt * a.xs[b]) * rs;
-                    float* yp = a.y + (size_t)b * a.ldy + n;
-                    *yp = a.resid ? *yp + val : val;
+                    if (a.part) {
+                        a.part[((size_t)blockIdx.z * a.M + b) * a.N + n] = val;
+                    } else {
+                        float* yp = a.y + (size_t)b * a.ldy + n;
+                        *yp = a.resid ? *yp + val : val;
+                    }
                 }
             }
     }
+}
+
+// y = (resid ? y : 0) + sum over the parts in part order (split K).
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int nz, int M, int N,
+                                                     float* __restrict__ y, int ldy, int resid) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= M * N) return;
+    const int b = i / N, n = i - b * N;
+    float acc = part[i];
+    for (int z = 1; z < nz; z++) acc += part[(size_t)z * M * N + i];
+    float* yp = y + (size_t)b * ldy + n;
+    *yp = resid ? *yp + acc : acc;
 }
 
 // Operand planes of the GEMM (grown on demand).
@@ -311,6 +338,23 @@ static uint8_t* g_gemm_planes = nullptr;
 static size_t g_gemm_cap = 0;
 static float* g_gemm_xs = nullptr;
 static size_t g_gemm_xs_cap = 0;
+static float* g_gemm_part = nullptr;  // split-K partial sums
+static size_t g_gemm_part_cap = 0;
+
+// K parts for a grid of base workgroups over nsteps K steps: enough parts
+// for ~256 workgroups (one per CU), at least 4 steps each.  Measured on
+// MI355X at m = 256 (prefill chunks): the down projection 1024x3072 (64
+// workgroups unsplit) and wo 1024x2048.
+static int gemm_kparts(long base, int nsteps) {
+    static const int env = [] {
+        const char* e = getenv("CMF_GEMM_SPLITK");
+        return e ? atoi(e) : -1;
+    }();
+    if (env == 0) return 1;
+    int z = 1;
+    while (base * z * 2 <= 256 && nsteps / (z * 2) >= 4) z *= 2;
+    return z;
+}
 
 size_t gemm_planes_bytes(const DevWeight& w, int mp) {
     // q8: three planes of nk * 64 * Mp B; q4: hi + lo 2 * items * Mp * 16 B
@@ -356,20 +400,48 @@ int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool res
     a.ntg = w.kchunks;
     a.nrb = w.rows_pad / 16;
     a.resid = resid ? 1 : 0;
+    a.part = nullptr;
+    // split K (nz parts into the partial buffer, then k_gemm_reduce)
+    auto split = [&](long base, int nsteps) -> int {
+        const int nz = gemm_kparts(base, nsteps);
+        a.gsteps = (nsteps + nz - 1) / nz;
+        if (nz == 1) return 1;
+        const size_t need = (size_t)nz * m * w.rows;
+        if (g_gemm_part_cap < need) {
+            (void)hipStreamSynchronize(st);
+            if (g_gemm_part) (void)hipFree(g_gemm_part);
+            g_gemm_part = nullptr;
+            g_gemm_part_cap = 0;
+            if (hipMalloc(&g_gemm_part, need * sizeof(float)) != hipSuccess) return -1;
+            g_gemm_part_cap = need;
+        }
+        a.part = g_gemm_part;
+        return (nsteps + a.gsteps - 1) / a.gsteps;
+    };
+    auto reduce = [&](int nz) -> int {
+        if (nz > 1)
+            hipLaunchKernelGGL(k_gemm_reduce, dim3((m * w.rows + 255) / 256), dim3(256), 0, st, g_gemm_part, nz, m,
+                               w.rows, y, ldy, a.resid);
+        CMF_HIP(hipGetLastError());
+        return CMF_OK;
+    };
     if (w.dtype == DT_Q8ROW) {
         // two row blocks per wave once that still leaves ~4 workgroups per CU
         const bool big = (long)((a.nrb + 7) / 8) * (mp / GB) >= 1024;
         const int rbwg = big ? 8 : 4;
-        const dim3 grid((a.nrb + rbwg - 1) / rbwg, mp / GB);
+        const int gx = (a.nrb + rbwg - 1) / rbwg, nz = split((long)gx * (mp / GB), (a.ntg + 1) / 2);
+        if (nz < 0) return fail("gemm: split-K buffer");
+        const dim3 grid(gx, mp / GB, nz);
         if (big) hipLaunchKernelGGL((k_gemm_q8<2>), grid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((k_gemm_q8<1>), grid, dim3(256), 0, st, a);
-        CMF_HIP(hipGetLastError());
-        return CMF_OK;
+        return reduce(nz);
     }
     // four row blocks per wave once that still leaves ~4 workgroups per CU
     const bool big = (long)((a.nrb + 15) / 16) * (mp / GB) >= 1024;
     const int rbwg = big ? 16 : 4;
-    const dim3 grid((a.nrb + rbwg - 1) / rbwg, mp / GB);
+    const int gx = (a.nrb + rbwg - 1) / rbwg, nz = split((long)gx * (mp / GB), a.ntg);
+    if (nz < 0) return fail("gemm: split-K buffer");
+    const dim3 grid(gx, mp / GB, nz);
     if (w.dtype == DT_Q4T) {
         if (big) hipLaunchKernelGGL((k_gemm_q4<DT_Q4T, 4>), grid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((k_gemm_q4<DT_Q4T, 1>), grid, dim3(256), 0, st, a);
@@ -377,8 +449,7 @@ int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool res
         if (big) hipLaunchKernelGGL((k_gemm_q4<DT_Q4TP, 4>), grid, dim3(256), 0, st, a);
         else hipLaunchKernelGGL((k_gemm_q4<DT_Q4TP, 1>), grid, dim3(256), 0, st, a);
     }
-    CMF_HIP(hipGetLastError());
-    return CMF_OK;
+    return reduce(nz);
 }
 
 int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st) {
