@@ -341,10 +341,13 @@ static size_t g_gemm_xs_cap = 0;
 static float* g_gemm_part = nullptr;  // split-K partial sums
 static size_t g_gemm_part_cap = 0;
 
-// K parts for a grid of base workgroups over nsteps K steps: enough parts
-// for ~256 workgroups (one per CU), at least 4 steps each.  Measured on
-// MI355X at m = 256 (prefill chunks): the down projection 1024x3072 (64
-// workgroups unsplit) and wo 1024x2048.
+// K parts for a grid of base workgroups over nsteps K steps: doubled while
+// the grid is below one workgroup per CU (256), at least 4 steps a part.
+// Measured on MI355X: at m = 256 (prefill chunks) the down projection
+// 1024x3072 (64 workgroups unsplit) and wo 1024x2048 take 4 parts; q4t
+// 12288x4096 at m = 64 (192 workgroups) 2 parts, 71 -> 56 us; qkv at
+// m = 256 (256 workgroups) split in 2 made the prefill slower (32.9 ->
+// 33.6 ms).
 static int gemm_kparts(long base, int nsteps) {
     static const int env = [] {
         const char* e = getenv("CMF_GEMM_SPLITK");
@@ -352,7 +355,7 @@ static int gemm_kparts(long base, int nsteps) {
     }();
     if (env == 0) return 1;
     int z = 1;
-    while (base * z * 2 <= 256 && nsteps / (z * 2) >= 4) z *= 2;
+    while (base * z < 256 && nsteps / (z * 2) >= 4) z *= 2;
     return z;
 }
 
