@@ -73,11 +73,12 @@ __device__ __forceinline__ void pick_bucket(const int* hist, int shift, uint32_t
 // thread t's slot u with i = t + 256 u; entries i >= n are not in play),
 // 256 threads.  Writes the k winners sorted into ov/oi.  Radix select over
 // order-preserving keys, 8 bits a pass, each pass's bucket found by a
-// block-wide scan; the keys stay in registers, and the pass counts go to 16
-// copies of the histogram (lane % 16 picks the copy: at most 16 lanes of a
-// wave meet on one address, where same-bucket keys, the common case in the
-// first pass, used to serialize 64 deep; the copies are 257 words apart so
-// that one bucket's copies sit in distinct LDS banks).  scratch: hist[16][257],
+// block-wide scan; the keys stay in registers.  The first pass counts into
+// 16 copies of the histogram (lane % 16 picks the copy: at most 16 lanes of
+// a wave meet on one address, where same-bucket keys, the common case
+// there, used to serialize 64 deep; the copies are 257 words apart so that
+// one bucket's copies sit in distinct LDS banks); the later passes count
+// only the keys under the chosen prefix, into one histogram.  scratch: hist[16][257],
 // ties.
 template <int NPT>
 __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int n, int k, float* ov, int* oi,
@@ -97,18 +98,30 @@ __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int
     }
     const int kk_total = k < n ? k : n;
     for (int shift = 24; shift >= 0; shift -= 8) {
+        if (shift == 24) {
+            // first pass: most keys share a few top bytes, so the counts go
+            // to the 16 copies
 #pragma unroll
-        for (int c = 0; c < 16; c++) hist[c][t] = 0;
-        __syncthreads();
-        const uint32_t pre = s_prefix, msk = s_mask;
+            for (int c = 0; c < 16; c++) hist[c][t] = 0;
+            __syncthreads();
 #pragma unroll
-        for (int u = 0; u < NPT; u++)
-            if (t + 256 * u < n && (key[u] & msk) == pre) atomicAdd(&hist[hc][(key[u] >> shift) & 255], 1);
-        __syncthreads();
-        int s = 0;
+            for (int u = 0; u < NPT; u++)
+                if (t + 256 * u < n) atomicAdd(&hist[hc][key[u] >> 24], 1);
+            __syncthreads();
+            int s = 0;
 #pragma unroll
-        for (int c = 0; c < 16; c++) s += hist[c][t];
-        htot[t] = s;
+            for (int c = 0; c < 16; c++) s += hist[c][t];
+            htot[t] = s;
+        } else {
+            // later passes count only the keys under the chosen prefix (few,
+            // spread over the buckets): one histogram
+            htot[t] = 0;
+            __syncthreads();
+            const uint32_t pre = s_prefix, msk = s_mask;
+#pragma unroll
+            for (int u = 0; u < NPT; u++)
+                if (t + 256 * u < n && (key[u] & msk) == pre) atomicAdd(&htot[(key[u] >> shift) & 255], 1);
+        }
         __syncthreads();
         pick_bucket(htot, shift, &s_prefix, &s_mask, &s_kk, wsum);
     }
