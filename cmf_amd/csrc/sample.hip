@@ -176,13 +176,30 @@ __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int
     }
     __syncthreads();
     const int m = cnt[2] < kk_total ? cnt[2] : kk_total;
-    // rank sort
+    // rank sort, the entries padded to a multiple of 16 with ones that rank
+    // last and read four at a time (the reads in flight together rather
+    // than one LDS round trip per entry)
+    const int m16 = (m + 15) & ~15;
+    if (t >= m && t < m16) {
+        tv[t] = -INFINITY;
+        ti[t] = 0x7FFFFFFF;
+    }
+    __syncthreads();
     if (t < m) {
         const float v = tv[t];
         const int id = ti[t];
         int r = 0;
-        for (int j = 0; j < m; j++)
-            if (better(tv[j], ti[j], v, id)) r++;
+        for (int j = 0; j < m16; j += 16) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const float4 a4 = *(const float4*)&tv[j + i];
+                const int4 b4 = *(const int4*)&ti[j + i];
+                r += better(a4.x, b4.x, v, id) ? 1 : 0;
+                r += better(a4.y, b4.y, v, id) ? 1 : 0;
+                r += better(a4.z, b4.z, v, id) ? 1 : 0;
+                r += better(a4.w, b4.w, v, id) ? 1 : 0;
+            }
+        }
         ov[r] = v;
         oi[r] = id;
     }
@@ -195,8 +212,8 @@ __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ lo
                                                     float* __restrict__ ssum) {
     const int sl = blockIdx.x, row = blockIdx.y, t = threadIdx.x;
     __shared__ int hist[16][257];  // copies 257 apart: one bucket's copies fall in distinct banks
-    __shared__ float tv[SPARSE_K_MAX + 256];
-    __shared__ int ti[SPARSE_K_MAX + 256];
+    __shared__ __align__(16) float tv[SPARSE_K_MAX + 256];
+    __shared__ __align__(16) int ti[SPARSE_K_MAX + 256];
     __shared__ int cnt[4];
     __shared__ float ov[SPARSE_K_MAX];
     __shared__ int oi[SPARSE_K_MAX];
@@ -251,8 +268,8 @@ __global__ __launch_bounds__(256) void k_topk_merge(int V, SampCfg c, int nslice
                                                     float* __restrict__ sum) {
     const int row = blockIdx.x, t = threadIdx.x;
     __shared__ int hist[16][257];  // copies 257 apart: one bucket's copies fall in distinct banks
-    __shared__ float tv[SPARSE_K_MAX + 256];
-    __shared__ int ti[SPARSE_K_MAX + 256];
+    __shared__ __align__(16) float tv[SPARSE_K_MAX + 256];
+    __shared__ __align__(16) int ti[SPARSE_K_MAX + 256];
     __shared__ int cnt[4];
     __shared__ float ov[SPARSE_K_MAX];
     __shared__ int oi[SPARSE_K_MAX];
