@@ -326,6 +326,48 @@ __device__ __forceinline__ float lanef(float v, int i) {
 }
 __device__ __forceinline__ int lanei(int v, int i) { return __builtin_amdgcn_readlane(v, i); }
 
+// Orders the wave's LDS accesses before and after (one wave per workgroup).
+__device__ __forceinline__ void wsync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Inclusive prefix sum of x over lanes 0..lane, lanes < n: every lane adds
+// the values one at a time from lane 0 up, the rounding of a serial loop
+// (a lane that does not count passes x = 0, and s + 0 == s for s >= 0).
+__device__ float wseq_prefix(float x, int n) {
+    __shared__ __align__(16) float buf[64];
+    const int lane = threadIdx.x;
+    wsync();
+    buf[lane] = lane < n ? x : 0.f;
+    wsync();
+    float acc = 0.f;
+    for (int i = 0; i < n; i += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&buf[i]);
+        acc = i <= lane ? acc + v.x : acc;
+        acc = i + 1 <= lane ? acc + v.y : acc;
+        acc = i + 2 <= lane ? acc + v.z : acc;
+        acc = i + 3 <= lane ? acc + v.w : acc;
+    }
+    return acc;
+}
+
+// The number of lanes i < n with in_i and key_i < key (each lane its own key).
+__device__ int wcount_less(int key, bool in, int n) {
+    __shared__ __align__(16) int buf[64];
+    const int lane = threadIdx.x;
+    wsync();
+    buf[lane] = in && lane < n ? key : INT_MAX;
+    wsync();
+    int r = 0;
+    for (int i = 0; i < n; i += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(&buf[i]);
+        r += (v.x < key) + (v.y < key) + (v.z < key) + (v.w < key);
+    }
+    return r;
+}
+
 // A sparse list over the wave: lane i < n holds (id, p), ids ascending.
 struct WList {
     int id;
@@ -346,30 +388,20 @@ __device__ WList wsparse_dist(const int* rid, const float* rv, float lmax, float
     // kept: in the list, past min-p, p > 0; the list stops at the first id < 0
     const bool kept = id >= 0 && !(c.min_p > 0.f && e < c.min_p) && pr > 0.f;
     const int nlist = c.k < 64 ? c.k : 64;
-    int stop = nlist;  // first index with id < 0
-    for (int i = 0; i < nlist; i++)
-        if (lanei(id, i) < 0) {
-            stop = i;
-            break;
-        }
+    const unsigned long long neg = __ballot(lane < nlist && id < 0);
+    const int stop = neg ? __builtin_ctzll(neg) : nlist;  // first index with id < 0
+    // cumulative p of the kept candidates, in candidate order
+    const float cum = wseq_prefix(kept ? pr : 0.f, stop);
     // top-p: the first kept candidate at which the cumulative reaches top_p
     // ends the list (inclusive)
     int last = stop;
     if (c.top_p < 1.f && c.top_p > 0.f) {
-        float cum = 0.f;
-        for (int i = 0; i < stop; i++) {
-            if (!__builtin_amdgcn_readlane((int)kept, i)) continue;
-            cum += lanef(pr, i);
-            if (cum >= c.top_p) {
-                last = i + 1;
-                break;
-            }
-        }
+        const unsigned long long hit = __ballot(lane < stop && kept && cum >= c.top_p);
+        if (hit) last = __builtin_ctzll(hit) + 1;
     }
     const bool in = kept && lane < last;
-    float s = 0.f;
-    for (int i = 0; i < last; i++)
-        if (__builtin_amdgcn_readlane((int)in, i)) s += lanef(pr, i);
+    // the kept candidates before last are the list: its sum is the cumulative
+    const float s = last > 0 ? lanef(cum, last - 1) : 0.f;
     WList out;
     out.n = __builtin_popcountll(__ballot(in));
     if (!(s > 0.f)) {
@@ -380,22 +412,18 @@ __device__ WList wsparse_dist(const int* rid, const float* rv, float lmax, float
     }
     const float pn = pr / s;
     // rank by id among the kept (ids are distinct)
-    int rank = 0;
-    for (int i = 0; i < last; i++)
-        if (__builtin_amdgcn_readlane((int)in, i) && lanei(id, i) < id) rank++;
+    const int rank = wcount_less(id, in, last);
     __shared__ int sid[64];
     __shared__ float sp[64];
+    wsync();
     if (in) {
         sid[rank] = id;
         sp[rank] = pn;
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    wsync();
     out.id = lane < out.n ? sid[lane] : -1;
     out.p = lane < out.n ? sp[lane] : 0.f;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
+    wsync();
     return out;
 }
 
@@ -419,21 +447,34 @@ struct Uni {
 // draw_sparse (sampler.rs:661-671): inverse CDF in list order
 __device__ int wdraw(const WList& l, Uni* rng) {
     const float r = rng->next();
-    float cum = 0.f;
-    for (int i = 0; i < l.n; i++) {
-        cum += lanef(l.p, i);
-        if (r < cum) return lanei(l.id, i);
-    }
-    for (int i = l.n - 1; i >= 0; i--)
-        if (lanef(l.p, i) > 0.f) return lanei(l.id, i);
+    const int lane = threadIdx.x;
+    const float cum = wseq_prefix(l.p, l.n);
+    const unsigned long long hit = __ballot(lane < l.n && r < cum);
+    if (hit) return lanei(l.id, __builtin_ctzll(hit));
+    // rounding left the cumulative short of r: the last entry with p > 0
+    const unsigned long long pos = __ballot(lane < l.n && l.p > 0.f);
+    if (pos) return lanei(l.id, 63 - __builtin_clzll(pos));
     return 0;
 }
 
 // p in list l of each lane's own id x (0 if absent): lane-parallel lookup
 __device__ float wget_lane(const WList& l, int x) {
+    __shared__ __align__(16) int bid[64];
+    __shared__ __align__(16) float bp[64];
+    const int lane = threadIdx.x;
+    wsync();
+    bid[lane] = lane < l.n ? l.id : -1;
+    bp[lane] = lane < l.n ? l.p : 0.f;
+    wsync();
     float r = 0.f;
-    for (int i = 0; i < l.n; i++)
-        if (lanei(l.id, i) == x) r = lanef(l.p, i);
+    for (int i = 0; i < l.n; i += 4) {
+        const int4 d = *reinterpret_cast<const int4*>(&bid[i]);
+        const float4 q = *reinterpret_cast<const float4*>(&bp[i]);
+        r = d.x == x ? q.x : r;
+        r = d.y == x ? q.y : r;
+        r = d.z == x ? q.z : r;
+        r = d.w == x ? q.w : r;
+    }
     return r;
 }
 
@@ -501,9 +542,7 @@ __global__ __launch_bounds__(64) void k_sample_finish(SampCfg c, int mode, int j
         // residual max(0, p - q) over p's support, in p's order
         const float ri = lane < p.n ? p.p - wget_lane(q, p.id) : 0.f;
         const bool pos = lane < p.n && ri > 0.f;
-        float total = 0.f;
-        for (int i = 0; i < p.n; i++)
-            if (__builtin_amdgcn_readlane((int)pos, i)) total += lanef(ri, i);
+        const float total = lanef(wseq_prefix(pos ? ri : 0.f, p.n), p.n - 1);
         if (total <= 0.f) {
             forced = wdraw(p, &rng);
         } else {
@@ -512,13 +551,12 @@ __global__ __launch_bounds__(64) void k_sample_finish(SampCfg c, int mode, int j
             const int slot = __builtin_popcountll(pm & ((1ull << lane) - 1));
             __shared__ int rsid[64];
             __shared__ float rsp[64];
+            wsync();
             if (pos) {
                 rsid[slot] = p.id;
                 rsp[slot] = ri / total;
             }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            wsync();
             WList rs;
             rs.n = __builtin_popcountll(pm);
             rs.id = lane < rs.n ? rsid[lane] : -1;
