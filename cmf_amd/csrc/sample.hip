@@ -42,7 +42,7 @@ __device__ __forceinline__ bool better(float va, int ia, float vb, int ib) {
 // buckets (a wave-level inclusive scan, then the waves' totals).  With no
 // such bucket the prefix stays and kk is unchanged (d = 0).
 __device__ __forceinline__ void pick_bucket(const int* hist, int shift, uint32_t* s_prefix, uint32_t* s_mask,
-                                            int* s_kk, int* wsum) {
+                                            int* s_kk, int* wsum, int kk_total, int* s_cand) {
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int kk = *s_kk;
     const uint32_t pre = *s_prefix, msk = *s_mask;
@@ -65,6 +65,43 @@ __device__ __forceinline__ void pick_bucket(const int* hist, int shift, uint32_t
     if (p >= kk && p - h < kk) {
         *s_prefix = pre | ((uint32_t)(255 - t) << shift);
         *s_kk = kk - (p - h);
+        *s_cand = p + (kk_total - kk);  // keys at or above the new prefix
+    }
+    __syncthreads();
+}
+
+// Sorts the m <= 256 entries tv/ti[0, m) by (value desc, id asc) and writes
+// those ranked below k to ov/oi (256 threads).  Each entry counts the
+// entries ahead of it; the list is padded to a multiple of 16 with entries
+// that rank last and read four at a time (the reads in flight together
+// rather than one LDS round trip per entry).  Ids are distinct.
+__device__ void rank_sort_lds(float* tv, int* ti, int m, int k, float* ov, int* oi) {
+    const int t = threadIdx.x;
+    const int m16 = (m + 15) & ~15;
+    if (t >= m && t < m16) {
+        tv[t] = -INFINITY;
+        ti[t] = 0x7FFFFFFF;
+    }
+    __syncthreads();
+    if (t < m) {
+        const float v = tv[t];
+        const int id = ti[t];
+        int r = 0;
+        for (int j = 0; j < m16; j += 16) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const float4 a4 = *(const float4*)&tv[j + i];
+                const int4 b4 = *(const int4*)&ti[j + i];
+                r += better(a4.x, b4.x, v, id) ? 1 : 0;
+                r += better(a4.y, b4.y, v, id) ? 1 : 0;
+                r += better(a4.z, b4.z, v, id) ? 1 : 0;
+                r += better(a4.w, b4.w, v, id) ? 1 : 0;
+            }
+        }
+        if (r < k) {
+            ov[r] = v;
+            oi[r] = id;
+        }
     }
     __syncthreads();
 }
@@ -78,8 +115,10 @@ __device__ __forceinline__ void pick_bucket(const int* hist, int shift, uint32_t
 // a wave meet on one address, where same-bucket keys, the common case
 // there, used to serialize 64 deep; the copies are 257 words apart so that
 // one bucket's copies sit in distinct LDS banks); the later passes count
-// only the keys under the chosen prefix, into one histogram.  scratch: hist[16][257],
-// ties.
+// only the keys under the chosen prefix, into one histogram.  Once at most
+// 256 keys sit at or above the chosen prefix (those above it are in the
+// top-k, those on it compete), the passes stop and a rank sort of those keys
+// decides.  scratch: hist[16][257], ties.
 template <int NPT>
 __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int n, int k, float* ov, int* oi,
                                 int (*hist)[257], float* tv, int* ti, int* cnt) {
@@ -88,6 +127,7 @@ __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int
     __shared__ int s_kk;
     __shared__ int wsum[4];
     __shared__ int htot[256];
+    __shared__ int s_cand;
     uint32_t key[NPT];
 #pragma unroll
     for (int u = 0; u < NPT; u++) key[u] = t + 256 * u < n ? fkey(v[u]) : 0u;  // 0: below every real key
@@ -122,8 +162,28 @@ __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int
             for (int u = 0; u < NPT; u++)
                 if (t + 256 * u < n && (key[u] & msk) == pre) atomicAdd(&htot[(key[u] >> shift) & 255], 1);
         }
+        if (t == 0) s_cand = 0x7FFFFFFF;  // no bucket picked: no early stop
         __syncthreads();
-        pick_bucket(htot, shift, &s_prefix, &s_mask, &s_kk, wsum);
+        pick_bucket(htot, shift, &s_prefix, &s_mask, &s_kk, wsum, kk_total, &s_cand);
+        if (s_cand <= 256) break;
+    }
+    if (s_cand <= 256) {
+        // the keys at or above the prefix: the top-k among them by rank
+        const uint32_t pre = s_prefix, msk = s_mask;
+        if (t == 0) cnt[0] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NPT; u++)
+            if (t + 256 * u < n && (key[u] & msk) >= pre) {
+                const int p = atomicAdd(&cnt[0], 1);
+                if (p < 256) {
+                    tv[p] = v[u];
+                    ti[p] = id[u];
+                }
+            }
+        __syncthreads();
+        rank_sort_lds(tv, ti, cnt[0] < 256 ? cnt[0] : 256, kk_total, ov, oi);
+        return;
     }
     const uint32_t kth = s_prefix;
     const int need_eq = s_kk;  // entries equal to kth still needed
@@ -176,34 +236,7 @@ __device__ void select_topk_reg(const float (&v)[NPT], const int (&id)[NPT], int
     }
     __syncthreads();
     const int m = cnt[2] < kk_total ? cnt[2] : kk_total;
-    // rank sort, the entries padded to a multiple of 16 with ones that rank
-    // last and read four at a time (the reads in flight together rather
-    // than one LDS round trip per entry)
-    const int m16 = (m + 15) & ~15;
-    if (t >= m && t < m16) {
-        tv[t] = -INFINITY;
-        ti[t] = 0x7FFFFFFF;
-    }
-    __syncthreads();
-    if (t < m) {
-        const float v = tv[t];
-        const int id = ti[t];
-        int r = 0;
-        for (int j = 0; j < m16; j += 16) {
-#pragma unroll
-            for (int i = 0; i < 16; i += 4) {
-                const float4 a4 = *(const float4*)&tv[j + i];
-                const int4 b4 = *(const int4*)&ti[j + i];
-                r += better(a4.x, b4.x, v, id) ? 1 : 0;
-                r += better(a4.y, b4.y, v, id) ? 1 : 0;
-                r += better(a4.z, b4.z, v, id) ? 1 : 0;
-                r += better(a4.w, b4.w, v, id) ? 1 : 0;
-            }
-        }
-        ov[r] = v;
-        oi[r] = id;
-    }
-    __syncthreads();
+    rank_sort_lds(tv, ti, m, m, ov, oi);
 }
 
 __global__ __launch_bounds__(256) void k_topk_slice(const float* __restrict__ logits, int V, SampCfg c,
@@ -287,7 +320,34 @@ __global__ __launch_bounds__(256) void k_topk_merge(int V, SampCfg c, int nslice
         vals[u] = id >= 0 ? v : -INFINITY;
         ids[u] = id >= 0 ? id : 0x7FFFFFFF;
     }
-    select_topk_reg<NPT>(vals, ids, n, k, ov, oi, hist, tv, ti, cnt);
+    // tau: the largest k-th value of a full slice list.  That list holds k
+    // entries >= tau, so an entry below tau ranks k or later: the rest
+    // (usually few) go to a rank sort, else to the radix select.
+    __shared__ float red[4];
+    float tau = -INFINITY;
+    for (int s2 = t; s2 < nslices; s2 += 256) {
+        const size_t at = ((size_t)row * nslices + s2) * SPARSE_K_MAX + (k - 1);
+        if (cid[at] >= 0) tau = fmaxf(tau, cv[at]);
+    }
+    tau = wave_max(tau);
+    if ((t & 63) == 0) red[t >> 6] = tau;
+    if (t == 0) cnt[3] = 0;
+    __syncthreads();
+    tau = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+    for (int u = 0; u < NPT; u++)
+        if (t + 256 * u < n && vals[u] >= tau) {
+            const int p = atomicAdd(&cnt[3], 1);
+            if (p < 256) {
+                tv[p] = vals[u];
+                ti[p] = ids[u];
+            }
+        }
+    __syncthreads();
+    const int nc = cnt[3];
+    __syncthreads();  // every thread has read cnt[3]
+    if (nc <= 256) rank_sort_lds(tv, ti, nc, k, ov, oi);
+    else select_topk_reg<NPT>(vals, ids, n, k, ov, oi, hist, tv, ti, cnt);
     if (t < SPARSE_K_MAX) {
         rid[(size_t)row * SPARSE_K_MAX + t] = t < k ? oi[t] : -1;
         rv[(size_t)row * SPARSE_K_MAX + t] = t < k ? ov[t] : -INFINITY;

@@ -87,3 +87,30 @@ def test_sparse_distribution_full_vocab(gpu, seed, scale):
     assert ids.tolist() == oid[:n].astype(np.int32).tolist()
     assert np.allclose(pr, opr[:n], rtol=1e-5, atol=1e-7)
     assert V - 3 in ids.tolist()
+
+
+@pytest.mark.parametrize("levels", [2, 8, 64])
+def test_sparse_distribution_tied_logits(gpu, levels):
+    """logits on a coarse grid over 151936 ids (hundreds of ties at the top
+    of every slice: more keys than a rank sort takes stay in play, and the
+    k-th value is shared): top_k 40, top_p 1, min_p 0, T 1 keeps the 40
+    best by (value desc, id asc); ids equal that, p = softmax over them"""
+    import cmf_amd
+    from cmf_amd import synth
+    from cmf_amd.model import Model
+    V = 151936
+    cfg = dict(n_layers=1, hidden=128, n_heads=1, n_kv=1, head_dim=128, inter=128, vocab=V, max_seq=16,
+               rope_theta=1e6, eps=1e-6)
+    sm = synth.synth_model(cfg, seed=9, mtp=False)
+    g = Model(sm)
+    sg = cmf_amd.SamplerConfig(temperature=1.0, top_k=40, top_p=1.0, min_p=0.0, repetition_penalty=1.0)
+    lg = np.floor(synth.normal(7 + levels, V) * (levels / 8)).astype(np.float32)
+    ids, pr = g.sparse_distribution(lg, sg)
+    g.free()
+    order = np.lexsort((np.arange(V), -lg))[:40]
+    want = np.sort(order)
+    print(f"levels {levels}: top value {lg.max()} x{int((lg == lg.max()).sum())}, "
+          f"k-th value {lg[order[-1]]} x{int((lg == lg[order[-1]]).sum())}", flush=True)
+    assert ids.tolist() == want.tolist()
+    e = np.exp(lg[want].astype(np.float64) - lg.max())
+    assert np.allclose(pr, e / e.sum(), rtol=1e-5, atol=1e-7)
