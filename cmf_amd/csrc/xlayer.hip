@@ -451,22 +451,6 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
                 tag, pv1, err);
             if (ss_on) ssp[bs][ks] = (double)pv1[NKC] + (double)pv1[NKC + 1];
         }
-    }
-    XL_MARK(3);
-    lds_barrier();
-    if (wave < 4) {
-        // the partials in chunk order, times 1 / rms (inference.rs:33-50: f64
-        // mean of squares)
-        if (on1) {
-            double ss = 0.0;
-#pragma unroll
-            for (int k = 0; k < NKC; k++) ss += ssp[b1][k];
-            const float inv = (float)(1.0 / sqrt(ss / (double)H + a.eps));
-            float acc = 0.f;
-#pragma unroll
-            for (int k = 0; k < NKC; k++) acc += pv1[k];
-            xput(a.e1 + ((size_t)x * MAXB + b1) * a.e1s + R1, acc * inv, tag);
-        }
     } else {
         // waves 4-7: the cached K (as f16 hi / lo) and V of this workgroup's
         // positions into LDS; V rows past its share zeroed (their weights
@@ -490,6 +474,22 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             } else if (sl >= np) {
                 *(float4v*)&VT[sl][4 * c4] = float4v{0.f, 0.f, 0.f, 0.f};
             }
+        }
+    }
+    XL_MARK(3);
+    lds_barrier();
+    if (wave < 4) {
+        // the partials in chunk order, times 1 / rms (inference.rs:33-50: f64
+        // mean of squares)
+        if (on1) {
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < NKC; k++) ss += ssp[b1][k];
+            const float inv = (float)(1.0 / sqrt(ss / (double)H + a.eps));
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < NKC; k++) acc += pv1[k];
+            xput(a.e1 + ((size_t)x * MAXB + b1) * a.e1s + R1, acc * inv, tag);
         }
     }
 
