@@ -34,10 +34,7 @@
 //      |q|, |k| past the f16 range on the six-launch path), softmax, values
 //      on the fp32 MFMA (K and V of its cached positions were requested at
 //      kernel start by waves 4-7, so that stream overlaps steps 0-1);
-//   3. workgroup j merges 8 output dims over the 32 position shares and
-//      writes them as three int8 digits against a scale every workgroup
-//      derives alike: max |V| over the shares' positions / 127 (the merged
-//      rows are convex combinations of V rows);
+//   3. workgroup j merges 8 output dims over the 32 position shares;
 //   4. output projection rows [32 j, 32 j + 32) over the XCD's K slice
 //      (weights requested at kernel start) -> partial pa[x].
 // FFN launch (k_xl_ffn), per XCD:
@@ -93,9 +90,6 @@ __device__ __forceinline__ uint32_t xcc_id() {
 // waits for its write-through after every store.
 __device__ __forceinline__ void xput(uint64_t* p, float v, uint32_t tag) {
     *p = ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
-}
-__device__ __forceinline__ void xputu(uint64_t* p, uint32_t v, uint32_t tag) {
-    *p = ((uint64_t)tag << 32) | (uint64_t)v;
 }
 // agent-scope load (sc1): misses the CU's L1, so another CU's store is seen
 // (a plain or sc0 load can keep returning the L1's stale line)
@@ -304,8 +298,6 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     __shared__ __align__(16) int8_t P8[3 * 4 * 16 * 16];
     __shared__ float sx0[MAXB], sxo[MAXB];
     __shared__ double ssd[MAXB], ssp[MAXB][NKC];
-    __shared__ uint32_t s_vmax;  // max |V| over this workgroup's positions (float bits)
-    static_assert(QD < 512, "e3: the row scales follow the XCDs' digits");
     static_assert(3 * QC * 1024 + 12 * 64 * 16 <= 2 * NPOS * (HD + 8) * 2, "overlay");
 
     const int kc = j % NKC, rp = j / NKC;
@@ -322,7 +314,6 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     const int plo = tlo * 16, phi = min(thi * 16, P);
     const int np = max(0, phi - plo), nold = max(0, min(phi, pos0) - plo);
     const int ntile = thi - tlo;
-    if (t == 0) s_vmax = 0u;
     XL_MARK(0);
 
 
@@ -463,9 +454,8 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     } else {
         // waves 4-7: the cached K (as f16 hi / lo) and V of this workgroup's
         // positions into LDS; V rows past its share zeroed (their weights
-        // are 0); the largest |V| (a bound of every merged output)
+        // are 0)
         const int t4 = t - 256;
-        float vm = 0.f;
 #pragma unroll
         for (int u = 0; u < KVN; u++) {
             const int f = t4 + 256 * u, sl = f >> 5, c4 = f & 31;
@@ -481,13 +471,10 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
                 *(half4*)&KHL[0][sl][4 * c4] = kh;
                 *(half4*)&KHL[1][sl][4 * c4] = kl;
                 *(float4v*)&VT[sl][4 * c4] = vq[u];
-                vm = fmaxf(vm, fmaxf(fmaxf(fabsf(vq[u][0]), fabsf(vq[u][1])), fmaxf(fabsf(vq[u][2]), fabsf(vq[u][3]))));
             } else if (sl >= np) {
                 *(float4v*)&VT[sl][4 * c4] = float4v{0.f, 0.f, 0.f, 0.f};
             }
         }
-        vm = wave_max(vm);
-        if (lane == 0) atomicMax(&s_vmax, __float_as_uint(vm));
     }
     XL_MARK(3);
     lds_barrier();
@@ -534,8 +521,6 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
             split16(k.y, KHL[0][sl][lane + 64], KHL[1][sl][lane + 64]);
             VT[sl][lane] = v4[2];
             VT[sl][lane + 64] = v4[3];
-            const float vm = wave_max(fmaxf(fabsf(v4[2]), fabsf(v4[3])));
-            if (lane == 0) atomicMax(&s_vmax, __float_as_uint(vm));
             float* kd = a.kc + ((size_t)x * a.max_seq + pos) * HD;
             float* vd = a.vc + ((size_t)x * a.max_seq + pos) * HD;
             kd[lane] = k.x;
@@ -593,7 +578,6 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
         if (lane == 0) {
             xput(e2w + (size_t)q * XL_E2S, m, tag);
             xput(e2w + (size_t)q * XL_E2S + 1, l, tag);
-            xputu(e2w + (size_t)q * XL_E2S + 130, s_vmax, tag);
         }
         if (npr == 0) {  // no positions: an empty share
             xput(e2w + (size_t)q * XL_E2S + 2 + lane, 0.f, tag);
@@ -632,81 +616,76 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
         const int js = t & 15, b = t >> 4, bq = min(b, nb - 1), q = bq * HPK + hh;
         const uint64_t* s0 = a.e2 + ((size_t)(x * XL_WG + js) * XL_NQ + q) * XL_E2S;
         const uint64_t* s1 = s0 + (size_t)16 * XL_NQ * XL_E2S;
-        // per share: m, l, the share's max |V|, then the DJ dims
-        constexpr int NV = DJ + 3;
-        float v[2 * NV];
+        float v[2 * (DJ + 2)];
         if (b < nb) {
-            xget<2 * NV>(
+            xget<2 * (DJ + 2)>(
                 [&](int i) {
-                    const uint64_t* sp = i < NV ? s0 : s1;
-                    const int k = i < NV ? i : i - NV;
-                    return k < 2 ? sp + k : k == 2 ? sp + 130 : sp + 2 + dd + (k - 3);
+                    const uint64_t* sp = i < DJ + 2 ? s0 : s1;
+                    const int k = i < DJ + 2 ? i : i - (DJ + 2);
+                    return k < 2 ? sp + k : sp + 2 + dd + (k - 2);
                 },
                 tag, v, err);
         } else {
 #pragma unroll
-            for (int i = 0; i < 2 * NV; i++) v[i] = i == 0 || i == NV ? -INFINITY : 0.f;
+            for (int i = 0; i < 2 * (DJ + 2); i++) v[i] = i == 0 || i == DJ + 2 ? -INFINITY : 0.f;
         }
         const float* v0 = v;
-        const float* v1 = v + NV;
+        const float* v1 = v + DJ + 2;
         const float M = row_max(fmaxf(v0[0], v1[0]));
         const float w0 = v0[0] == -INFINITY ? 0.f : expf(v0[0] - M);
         const float w1 = v1[0] == -INFINITY ? 0.f : expf(v1[0] - M);
         const float L = row_sum(w0 * v0[1] + w1 * v1[1]);
         float O[DJ];
 #pragma unroll
-        for (int i = 0; i < DJ; i++) O[i] = row_sum(w0 * v0[3 + i] + w1 * v1[3 + i]);
-        // the output projection's operand scale: the merged row is a convex
-        // combination of V rows, so |out| <= max |V| over the 32 shares
-        // (the same bound, hence the same scale, in every workgroup)
-        const float B = row_max(fmaxf(v0[2], v1[2]));
-        const float sx = B > 0.f ? B / 127.0f : 1.0f;
-        // (the row sums reach all 16 lanes of the row: lane js < DJ takes dim js)
-        if (js < DJ && b < nb) {
+        for (int i = 0; i < DJ; i++) O[i] = row_sum(w0 * v0[2 + i] + w1 * v1[2 + i]);
+        if (js == 0 && b < nb) {
             const float inv = L > 0.f ? 1.0f / L : 0.f;
-            float o = O[0];
 #pragma unroll
-            for (int i = 1; i < DJ; i++) o = js == i ? O[i] : o;
-            int8_t d0, d1, d2;
-            q8_digits(o * inv / sx, d0, d1, d2);
-            xputu(a.e3 + ((size_t)x * MAXB + b) * QD + dbase + js,
-                  (uint32_t)(uint8_t)d0 | (uint32_t)(uint8_t)d1 << 8 | (uint32_t)(uint8_t)d2 << 16, tag);
-            if (j == 0 && js == 0) xput(a.e3 + (size_t)XL_XCD * MAXB * QD + x * MAXB + b, sx, tag);
+            for (int i = 0; i < DJ; i++)
+                xput(a.e3 + ((size_t)x * MAXB + b) * QD + dbase + i, O[i] * inv, tag);
         }
     }
     XL_MARK(9);
     // ---- step 4: output projection rows of this workgroup over the XCD's
-    // K slice: the merged rows (all of them) as the int8 digit planes the
-    // merge owners wrote, one scale per row, then the MFMAs of waves 4-7 on
-    // the weights requested at start
+    // K slice: the merged rows (all of them) as int8 planes with one scale
+    // per row, then the MFMAs of waves 4-7 on the weights requested at start
     float* Xo = (float*)&KHL[0][0][0];
     int8_t* P8o = (int8_t*)(Xo + MAXB * QD);
     int4v* red = (int4v*)(P8o + 3 * QC * 1024);
     {
-        // the nb * QD merged values as int8 digits, 4 per thread (one wait
-        // for each thread's share), into the three planes; the row scales
+        // the nb * QD values, 4 per thread (one wait for each thread's share)
         const int n = nb * QD;
         const uint64_t* e3x = a.e3 + (size_t)x * MAXB * QD;
         for (int i0 = 4 * t; i0 < n; i0 += 4 * XL_T) {
             float ov[4];
             xget<4>([&](int i) { return e3x + i0 + i; }, tag, ov, err);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t dv = __float_as_uint(ov[i]);
-                const int b = (i0 + i) / QD, col = (i0 + i) - b * QD, c = col >> 6, l = col & 63;
-                const int o = ((c * 4 + (l >> 4)) * 16 + b) * 16 + (l & 15);
-                P8o[o] = (int8_t)(dv & 0xFFu);
-                P8o[QC * 1024 + o] = (int8_t)((dv >> 8) & 0xFFu);
-                P8o[2 * QC * 1024 + o] = (int8_t)((dv >> 16) & 0xFFu);
-            }
-        }
-        if (t < nb) {
-            float sv[1];
-            xget<1>([&](int) { return a.e3 + (size_t)XL_XCD * MAXB * QD + x * MAXB + t; }, tag, sv, err);
-            sxo[t] = sv[0];
+            for (int i = 0; i < 4; i++) Xo[i0 + i] = ov[i];
         }
     }
     XL_MARK(10);
+    lds_barrier();
+    for (int b = wave; b < nb; b += 8) {
+        float vv[QC];
+        float am = 0.f;
+#pragma unroll
+        for (int c = 0; c < QC; c++) {
+            vv[c] = Xo[b * QD + 64 * c + lane];
+            am = fmaxf(am, fabsf(vv[c]));
+        }
+        am = wave_max(am);
+        const float sx = am > 0.f ? am / 127.0f : 1.0f;
+        if (lane == 0) sxo[b] = sx;
+#pragma unroll
+        for (int c = 0; c < QC; c++) {
+            int8_t d0, d1, d2;
+            q8_digits(vv[c] / sx, d0, d1, d2);
+            const int o = ((c * 4 + (lane >> 4)) * 16 + b) * 16 + (lane & 15);
+            P8o[o] = d0;
+            P8o[QC * 1024 + o] = d1;
+            P8o[2 * QC * 1024 + o] = d2;
+        }
+    }
     XL_MARK(11);
     lds_barrier();
     const int w4 = wave - 4, rbl = w4 % RBO, cs = w4 / RBO;
