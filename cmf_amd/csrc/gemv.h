@@ -92,6 +92,11 @@ GemvKernel q4tp_kernel_g3(int m, int xm);
 GemvKernel q4t_kernel_s6(int m, int xm);
 GemvKernel q4tp_kernel_s6(int m, int xm);
 GemvKernel q8_kernel(int m, int xm, int ks);
+// M = 1 over a prepared operand, rows of nk 1 KiB steps (k_gemv_q8_m1 /
+// k_gemv_q4t_m1): the instance, its waves per workgroup (*ks) and dynamic
+// LDS bytes (*lds), or nullptr
+GemvKernel q8_kernel_m1(int nk, bool resid, int* ks, size_t* lds);
+GemvKernel q4t_kernel_m1(int nk, bool resid, int* ks, size_t* lds);
 
 enum { EPI_NONE = 0, EPI_SWIGLU = 1 };
 

@@ -442,6 +442,23 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
         if (!lds || gridy > 1) return fail("gemv: this operand must be prepared (launch_prep_src)");
         xm = XM_FUSED;
     }
+    // M = 1 over a prepared operand: the per-wave operand-slice kernels
+    // (k_gemv_q8_m1, k_gemv_q4t_m1), one workgroup per row block
+    // (CMF_GEMV_M1=0 keeps the general kernel)
+    static const int m1_env = env_int("CMF_GEMV_M1", 1);
+    if (m1_env && m == 1 && xm == XM_PREP && gridy == 1 && grid_override <= 0 && ks_override <= 0 &&
+        a.epi == EPI_NONE && (w.dtype == DT_Q8ROW || w.dtype == DT_Q4T)) {
+        int ks1 = 0;
+        size_t l1 = 0;
+        GemvKernel k1 = w.dtype == DT_Q8ROW ? q8_kernel_m1(w.kchunks, a.resid, &ks1, &l1)
+                                            : q4t_kernel_m1(w.kchunks, a.resid, &ks1, &l1);
+        // (resident_per_cu also allows the kernel its dynamic LDS above the default limit)
+        if (k1 && resident_per_cu(k1, 64 * ks1, l1) >= 1) {
+            void* args[] = {&a};
+            CMF_HIP(hipLaunchKernel((const void*)k1, dim3(a.nrb), dim3(64 * ks1), args, l1, st));
+            return CMF_OK;
+        }
+    }
     // Two more q4 shapes of the prepared-operand GEMV, chosen by what
     // measured faster on MI355X (GEMV alone, 10 weight copies rotating;
     // CMF_GEMV_G=0/3 and CMF_GEMV_S6=0/1 force either):

@@ -836,6 +836,209 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8(GemvArgs args) {
 }
 
 // ---------------------------------------------------------------------------
+// M = 1 with a prepared operand (XS_GLOBAL): one workgroup per row block, KS
+// waves each owning SPW consecutive 1 KiB steps of its row.  Every wave
+// copies only its own slice of the operand planes to LDS by direct loads and
+// waits for its own loads alone: no workgroup-wide operand copy and no
+// barrier before the MFMAs (measured on MI355X against the general kernel:
+// q8 4096x4096 5.78 -> 4.65 us, q4t 12288x4096 7.1 -> 6.85 us; the copy of
+// the whole operand by every workgroup, 768 x 24 KiB from L2 for the q4t
+// shape, was the largest cost above a plain read of the weights).  The KS
+// partial sums are reduced in LDS in wave order (deterministic).  The slices
+// live in the dynamic LDS allocation: with a static __shared__ array as the
+// direct-load target the compiler waited for every load of the wave
+// (vmcnt(0)) before the first LDS read instead of for the slice alone.
+// ---------------------------------------------------------------------------
+
+// Row-block epilogue of the M = 1 kernels: wave 0 adds the KS partials in
+// wave order and lanes with s == 0 write row r.
+template <int KS>
+__device__ __forceinline__ float m1_reduce(float (*part)[64], float v, int wave, int lane) {
+    part[wave][lane] = v;
+    __syncthreads();
+    float o = part[0][lane];
+#pragma unroll
+    for (int w = 1; w < KS; w++) o += part[w][lane];
+    return o;
+}
+
+// q8: v_mfma_i32_16x16x64_i8 with A rows 0..2 the three int8 planes of x
+// (the PK layout of k_gemv_q8 at m = 1); exact int32 sums per wave (SPW * 64
+// columns * 127 * 127 < 2^24, so the f32 partial is exact), the planes
+// combined once at the end.
+template <int KS, int SPW, bool RESID>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q8_m1(GemvArgs a) {
+    static_assert(SPW * 64 * 127 * 127 < (1 << 24), "per-wave int32 partial must stay exact in f32");
+    constexpr int NI = SPW * 4 * 3;           // 16-byte operand items of a wave's slice
+    constexpr int NCH = (NI + 63) / 64;       // ... in 1 KiB direct loads
+    __shared__ float part[KS][64];
+    extern __shared__ __align__(16) uint8_t smem[];  // [KS][NCH * 1024]: the waves' operand slices
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4;
+    const int nkc = a.nk, rb = blockIdx.x;
+    const int c0 = wave * SPW;
+    const int row = (a.rb0 + rb) * 16 + r;
+    const int rowc = max(a.row_lo, min(row, a.row_hi - 1));
+    // epilogue reads first (row scale, residual), then the slice, then the weights
+    const float rs = ldg((const float*)a.scale + row);
+    // (every load unconditional: a load under a branch makes the compiler
+    // wait for all loads in flight at the branch; RESID is a template
+    // argument so that a plain GEMV issues no residual read, 0.2 us)
+    const float yold = RESID ? ldg(a.y + (rowc - a.row_lo)) : 0.f;
+    const float xs = ldg(a.src.xs);
+    uint8_t* lx = smem + wave * (NCH * 1024);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        // item i = (u * 4 + s') * 3 + p: plane p of step c0 + u, k-slot s' (clamped to the matrix)
+        const int i = min(c * 64 + lane, NI - 1);
+        const int p = i % 3, us = i / 3, u = us >> 2, sp = us & 3;
+        const int step = min(c0 + u, nkc - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(a.src.planes + ((size_t)p * nkc * 4 + step * 4 + sp) * 16),
+                                         (__attribute__((address_space(3))) void*)(lx + c * 1024), 16, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    int4v wv[SPW];
+    const size_t wbase = (size_t)(a.rb0 + rb) * nkc;
+#pragma unroll
+    for (int u = 0; u < SPW; u++) wv[u] = ldg((const int4v*)a.w + (wbase + min(c0 + u, nkc - 1)) * 64 + lane);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<SPW>();  // this wave's slice is in
+    const int4v* X = (const int4v*)lx;
+    int4v acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        // steps past the row (clamped loads) multiply a zero operand: a
+        // select, not a branch, so that each MFMA waits for its own step only
+        const int4v z = {0, 0, 0, 0};
+        const int4v xv = X[(u * 4 + s) * 3 + min(r, 2)];
+        const int4v xa = (r < 3 && c0 + u < nkc) ? xv : z;
+        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, wv[u], acc, 0, 0, 0);
+    }
+    // lanes s == 0 hold rows 0..2 (the planes) of weight row r
+    const float v = (float)acc[0] + (float)acc[1] * 0.0078125f + (float)acc[2] * 6.103515625e-05f;
+    const float o = m1_reduce<KS>(part, v, wave, lane);
+    if (wave == 0 && s == 0 && row >= a.row_lo && row < a.row_hi && rb < a.nrb) {
+        const float val = (o * xs) * rs;
+        a.y[row - a.row_lo] = RESID ? yold + val : val;
+    }
+}
+
+// q4t: the f16 hi / lo planes of the wave's tiles in LDS, A rows 0..7 the
+// hi plane and 8..15 the lo plane of batch row 0 (HL); each tile's bias
+// -8 * 2^-24 * sum(hi + lo) (the format's -8 offset) comes from the prepared
+// table into the slice too (SPW * 4 <= 64 floats after the planes) and is
+// added to both halves' rows at half weight.  (Scalar loads of the biases
+// made the compiler wait for every load of the wave before the first MFMA.)
+template <int KS, int SPW, bool RESID>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4t_m1(GemvArgs a) {
+    constexpr int NI = SPW * 4 * 4 * 2;  // 16-byte items: step x tile x k-slot x plane
+    constexpr int NCH = (NI + 63) / 64;
+    __shared__ float part[KS][64];
+    static_assert(SPW * 4 <= 64, "one bias per lane");
+    extern __shared__ __align__(16) uint8_t smem[];  // [KS][NCH * 1024 + 256]: the waves' operand slices
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4, p = r < 8 ? 0 : 1;
+    const int ntg = a.nk, rb = blockIdx.x;
+    const int t0 = wave * SPW;
+    const int row = (a.rb0 + rb) * 16 + r;
+    const int rowc = max(a.row_lo, min(row, a.row_hi - 1));
+    const float yold = RESID ? ldg(a.y + (rowc - a.row_lo)) : 0.f;  // (as in k_gemv_q8_m1)
+    const float xs = ldg(a.src.xs);
+    const uint8_t* hi = a.src.planes;
+    const uint8_t* lo = hi + (size_t)ntg * 4 * 4 * 16;
+    const float* btab = (const float*)(lo + (size_t)ntg * 4 * 4 * 16);  // [tile][16]
+    uint8_t* lx = smem + wave * (NCH * 1024 + 256);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        // item i = ((u * 4 + t) * 4 + s') * 2 + plane
+        const int i = min(c * 64 + lane, NI - 1);
+        const int pl = i & 1, q = i >> 1, sp = q & 3, t = (q >> 2) & 3, u = q >> 4;
+        const int tg = min(t0 + u, ntg - 1);
+        __builtin_amdgcn_global_load_lds((const void*)((pl ? lo : hi) + ((size_t)(tg * 4 + t) * 4 + sp) * 16),
+                                         (__attribute__((address_space(3))) void*)(lx + c * 1024), 16, 0, 0);
+    }
+    // the tile biases of the slice (entry [tile][0] of the table), one
+    // 4-byte direct load per lane after the planes
+    {
+        const int tb = min((t0 + (lane >> 2)) * 4 + (lane & 3), ntg * 4 - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(btab + (size_t)tb * 16),
+                                         (__attribute__((address_space(3))) void*)(lx + NCH * 1024), 4, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wv[SPW];
+    uint2 sv[SPW];
+    const size_t wbase = (size_t)(a.rb0 + rb) * ntg;
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const size_t t = wbase + min(t0 + u, ntg - 1);
+        wv[u] = ld_stream((const uint4*)a.w + t * 64 + lane);
+        const uint64_t sw = ldg((const uint64_t*)a.scale + t * 16 + r);
+        sv[u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * SPW>();  // this wave's slice is in
+    const uint4* X = (const uint4*)lx;
+    const float* bias = (const float*)(lx + NCH * 1024);
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        // steps past the row (clamped loads) get a zero scale: a select, not
+        // a branch (see k_gemv_q8_m1)
+        const bool in = t0 + u < ntg;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const half8 xa = __builtin_bit_cast(half8, X[((u * 4 + t) * 4 + s) * 2 + p]);
+            const uint32_t wq = t == 0 ? wv[u].x : t == 1 ? wv[u].y : t == 2 ? wv[u].z : wv[u].w;
+            const float4v z = {0.f, 0.f, 0.f, 0.f};
+            const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, dq_nib_word(wq), z, 0, 0, 0);
+            const uint32_t sw = t < 2 ? sv[u].x : sv[u].y;
+            const float sc = in ? f16_bits_to_f32((t & 1) ? sw >> 16 : sw & 0xFFFFu) : 0.f;
+            acc += __builtin_fmaf(bias[u * 4 + t], 0.5f, d[0]) * sc;
+        }
+    }
+    float o = m1_reduce<KS>(part, acc, wave, lane);
+    o += __shfl_xor(o, 32);  // hi rows (lanes s = 0, 1) + lo rows (s = 2, 3)
+    if (wave == 0 && s == 0 && row >= a.row_lo && row < a.row_hi && rb < a.nrb) {
+        const float val = o * xs * 16777216.0f;  // 2^24: denormal nibbles
+        a.y[row - a.row_lo] = RESID ? yold + val : val;
+    }
+}
+
+// Instance of the M = 1 kernels for rows of nk 1 KiB steps (nullptr: none);
+// *ks = its waves per workgroup, *lds = its dynamic LDS bytes.
+template <int KS, int SPW>
+inline GemvKernel q8_m1_inst(bool resid, int* ks, size_t* lds) {
+    *ks = KS;
+    *lds = (size_t)KS * ((SPW * 12 + 63) / 64) * 1024;
+    return resid ? k_gemv_q8_m1<KS, SPW, true> : k_gemv_q8_m1<KS, SPW, false>;
+}
+template <int KS, int SPW>
+inline GemvKernel q4t_m1_inst(bool resid, int* ks, size_t* lds) {
+    *ks = KS;
+    *lds = (size_t)KS * (((SPW * 32 + 63) / 64) * 1024 + 256);
+    return resid ? k_gemv_q4t_m1<KS, SPW, true> : k_gemv_q4t_m1<KS, SPW, false>;
+}
+inline GemvKernel q8_m1_pick(int nk, bool resid, int* ks, size_t* lds) {
+    if (nk <= 8) return q8_m1_inst<1, 8>(resid, ks, lds);
+    if (nk <= 16) return q8_m1_inst<2, 8>(resid, ks, lds);
+    if (nk <= 32) return q8_m1_inst<4, 8>(resid, ks, lds);
+    if (nk <= 64) return q8_m1_inst<8, 8>(resid, ks, lds);
+    if (nk <= 128) return q8_m1_inst<16, 8>(resid, ks, lds);
+    if (nk <= 192) return q8_m1_inst<16, 12>(resid, ks, lds);
+    return nullptr;
+}
+inline GemvKernel q4t_m1_pick(int nk, bool resid, int* ks, size_t* lds) {
+    if (nk <= 4) return q4t_m1_inst<1, 4>(resid, ks, lds);
+    if (nk <= 8) return q4t_m1_inst<2, 4>(resid, ks, lds);
+    if (nk <= 16) return q4t_m1_inst<4, 4>(resid, ks, lds);
+    if (nk <= 32) return q4t_m1_inst<8, 4>(resid, ks, lds);
+    if (nk <= 64) return q4t_m1_inst<8, 8>(resid, ks, lds);
+    if (nk <= 96) return q4t_m1_inst<16, 6>(resid, ks, lds);
+    if (nk <= 128) return q4t_m1_inst<16, 8>(resid, ks, lds);
+    return nullptr;
+}
+
+// ---------------------------------------------------------------------------
 // Kernel instance tables (one translation unit per weight codec).
 // ---------------------------------------------------------------------------
 template <int FMT, int NV, bool HL, int XM, int RB>

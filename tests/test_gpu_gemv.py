@@ -81,6 +81,17 @@ def test_ragged_shapes(gpu):
     _check(gpu, synth.q4t_uniform(67, 1, 32), _x(68, 1, 32))
 
 
+@pytest.mark.parametrize("cols", [64, 448, 1024, 2048, 4160, 8192, 12288, 16384])
+def test_m1_kernel_instances(gpu, cols):
+    """M = 1 over a prepared operand runs the per-wave operand-slice kernels
+    (k_gemv_q8_m1 / k_gemv_q4t_m1); every instance size (q8: 1..192 K steps
+    of 64 columns, q4t: 1..128 steps of 128 columns), ragged steps (4160 =
+    65 q8 chunks, 32.5 q4t groups) and ragged rows"""
+    from cmf_amd import synth
+    _check(gpu, synth.q8_normal(81 + cols, 77, cols), _x(82 + cols, 1, cols))
+    _check(gpu, synth.q4t_uniform(83 + cols, 93, cols), _x(84 + cols, 1, cols))
+
+
 def test_large_batch_split(gpu):
     """q8 with b > 16: the int8 MFMA GEMM (37 rows: one ragged 64-row tile)"""
     from cmf_amd import synth
