@@ -33,18 +33,24 @@ COPY_BYTES = 64 << 20  # counter-calibration copy (read + write of this many byt
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4t_gemv_12288x4096_m1_traffic.txt")
 
 
+ROOF_KERNEL = "k_gemv_q4t_m1<8, 4, false>"  # the kernel the dispatch runs for the roofline GEMV
+
+
 def measured_traffic():
     """HBM bytes per launch of the roofline GEMV from the committed rocprofv3
     counter summary (FETCH_SIZE + WRITE_SIZE, calibrated on a plain copy), or
-    None when no summary is present."""
+    None when no summary is present or it was measured on another kernel."""
+    kern, val = None, None
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
+                if line.startswith("kernel:"):
+                    kern = line.split(":", 1)[1].strip()
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(float(line.split(":", 1)[1]))
+                    val = int(float(line.split(":", 1)[1]))
     except OSError:
         return None
-    return None
+    return val if kern == ROOF_KERNEL else None
 METRIC = "spec-verify decode tok/s + q4t GEMV HBM GB/s (% of peak), 1 MI355X"
 
 
@@ -75,6 +81,29 @@ def time_gemv(cmf, t, m, copies, iters=200, warmup=20, seed=7):
     cmf.check(cmf.lib().cmf_time_gemv(arr, copies, pl.p, xs.p, m, dy.p, t["rows"], 0, warmup, iters, C.byref(ms)))
     for w in ws:
         w.free()
+    return ms.value
+
+
+def time_gemv_from_x(cmf, t, m, copies, fused, iters=200, warmup=20, seed=7):
+    """Average ms per call of the GEMV from f32 rows x resident in HBM:
+    fused=0 the operand producer launch + the GEMV, fused=1 one launch whose
+    workgroups stage the operand themselves."""
+    import ctypes as C
+    from cmf_amd import synth
+    ws = [cmf.Weight(t["dtype"], t["rows"], t["cols"], payload=t["bytes"], q=t["q"], row_scale=t["row_scale"])
+          for _ in range(copies)]
+    x = synth.normal(seed, m * t["cols"]).reshape(m, t["cols"])
+    dx = cmf.DevBuf(x.nbytes)
+    dx.upload(x)
+    dy = cmf.DevBuf(m * t["rows"] * 4)
+    arr = (C.c_void_p * copies)(*[w.h for w in ws])
+    ms = C.c_float()
+    cmf.check(cmf.lib().cmf_time_gemv_rows(arr, copies, dx.p, t["cols"], None, m, dy.p, t["rows"], fused, warmup,
+                                           iters, C.byref(ms)))
+    for w in ws:
+        w.free()
+    dx.free()
+    dy.free()
     return ms.value
 
 
@@ -268,10 +297,23 @@ def main():
                      "frac": b / ms / 1e6 / PEAK_HBM}
                 kernels.append(e)
                 if shape == (12288, 4096) and m == 1:
+                    import ctypes as C
+                    # the same weight bytes read by a plain kernel of the GEMV's launch
+                    # shape (the ceiling for one launch), and the call from f32 x
+                    pr = C.c_float()
+                    wbytes = 12288 * 4096 // 32 * 18
+                    cmf.check(cmf.lib().cmf_time_read(wbytes, 10, 200, C.byref(pr)))
+                    fx0 = time_gemv_from_x(cmf, t2, 1, 10, 0)
+                    fx1 = time_gemv_from_x(cmf, t2, 1, 10, 1)
                     roof = {"bound": "hbm", "achieved": round(e["GB/s"], 1), "peak": PEAK_HBM, "unit": "GB/s",
                             "frac": round(e["frac"], 4), "traffic": measured_traffic(),
-                            "kernel": "k_gemv_q4<q4t> gate/up 12288x4096 M=1",
-                            "bytes_per_launch": b, "avg_launch_us": round(ms * 1e3, 3)}
+                            "kernel": f"{ROOF_KERNEL} (q4t gate/up 12288x4096, M=1, prepared operand)",
+                            "bytes_per_launch": b, "avg_launch_us": round(ms * 1e3, 3),
+                            "plain_read_us": round(pr.value * 1e3, 3),
+                            "plain_read_GB/s": round(wbytes / pr.value / 1e6, 1),
+                            "gemv_vs_plain_read": round(pr.value / ms, 4),
+                            "from_f32_x_us": {"producer launch + GEMV": round(fx0 * 1e3, 3),
+                                              "operand staged in the GEMV": round(fx1 * 1e3, 3)}}
             t3 = synth.q4tp_uniform(41 + shape[0], shape[0], shape[1])
             ms = time_gemv(cmf, t3, 5, copies=10)
             b = q4_bytes(shape[0], shape[1], 5, "q4tp")
@@ -343,6 +385,30 @@ def main():
     out["sampled"] = {"temperature": 0.8, "top_k": 40, "top_p": 0.9, "min_p": 0.05, "rounds": n_s,
                       "tokens": len(model.tokens()) - s0, "tok/s": round((len(model.tokens()) - s0) / dts, 2),
                       "ms_per_round": round(dts * 1e3 / n_s, 4), "accepted": sst.accepted, "drafted": sst.drafted}
+    # plain decode (spec=False, forward_token_graph's counterpart): greedy
+    # tokens, each one trunk forward + lm_head + argmax, replayed from a
+    # captured step
+    model.decode_begin(seed=0)
+    model.decode_rounds(4, spec=False)
+    cmf.lib().cmf_sync()
+    tp0 = time.perf_counter()
+    model.decode_rounds(args.steps, spec=False)
+    cmf.lib().cmf_sync()
+    dtp = time.perf_counter() - tp0
+    out["plain"] = {"tokens": args.steps, "ms_per_token": round(dtp * 1e3 / args.steps, 4),
+                    "tok/s": round(args.steps / dtp, 2)}
+    # the reference's decode loop with the speculation monitor (SpecMon,
+    # pipeline.rs:661-694): five timed rounds, eight timed plain tokens, then
+    # the faster arm (host-paced rounds, as the reference's)
+    n_mon = 64
+    tm0 = time.perf_counter()
+    mt, mst = model.decode(n_mon, spec="auto", k=args.k)
+    dtm = time.perf_counter() - tm0
+    mon = model.monitor()
+    out["spec_monitor"] = {"tokens": int(len(mt)), "s": round(dtm, 4), "decision": mon.phase_name,
+                           "round_ms": round(mon.round_ms, 4), "tokens_per_round": round(mon.tokens, 3),
+                           "plain_ms": round(mon.plain_ms, 4), "spec_rounds": mon.spec_rounds,
+                           "plain_steps": mon.plain_steps, "accepted": mst.accepted, "drafted": mst.drafted}
     # HBM bytes a round must stream at ctx ~2048 (weights + KV), for context
     c = sm["cfg"]
     layer_w = sum(len(t["bytes"]) if t["bytes"] is not None else t["q"].nbytes + t["row_scale"].nbytes

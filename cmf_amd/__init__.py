@@ -84,6 +84,20 @@ class GenStats(C.Structure):
                 ("device_ms", C.c_double)]
 
 
+class SpecState(C.Structure):
+    """cmf_spec_state: the speculation monitor of a model's last decode
+    (SpecMon and its trial, pipeline.rs:642-694)."""
+    _fields_ = [("round_ms", C.c_double), ("tokens", C.c_double), ("plain_ms", C.c_double), ("n", C.c_int),
+                ("fails", C.c_int), ("phase", C.c_int), ("trial_rounds", C.c_int), ("gen0", C.c_int),
+                ("recheck_at", C.c_int), ("t0_ms", C.c_double), ("spec_rounds", C.c_int), ("plain_steps", C.c_int)]
+
+    PHASES = ("trial", "plain trial", "speculating", "plain")
+
+    @property
+    def phase_name(self):
+        return self.PHASES[self.phase]
+
+
 class FileSections(C.Structure):
     """cmf_file_sections: the envelope of an open .cmf file."""
     _fields_ = [("required_features", C.c_uint32), ("off", C.c_uint64 * 6), ("len", C.c_uint64 * 6),
@@ -129,6 +143,7 @@ SIGNATURES = {
     "cmf_gemv_dev_noalloc": (_I, [_P, _P, _I, _I, _P, _I]),
     "cmf_time_gemv": (_I, [C.POINTER(_P), _I, _P, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_copy": (_I, [_S, _I, _I, C.POINTER(_F)]),
+    "cmf_time_read": (_I, [_S, _I, _I, C.POINTER(_F)]),
     "cmf_time_attention": (_I, [_P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_gemv_rows": (_I, [C.POINTER(_P), _I, _P, _I, _P, _I, _P, _I, _I, _I, _I, C.POINTER(_F)]),
     "cmf_time_gemm": (_I, [_P, _P, _I, _P, _I, _I, C.POINTER(_F)]),
@@ -149,6 +164,7 @@ SIGNATURES = {
     "cmf_prefill": (_I, [_P, _P, _I]),
     "cmf_decode": (_I, [_P, _I, C.POINTER(SamplerConfig), _U64, _I, _I, _P, C.POINTER(GenStats)]),
     "cmf_decode_begin": (_I, [_P, C.POINTER(SamplerConfig), _U64]),
+    "cmf_spec_monitor": (_I, [_P, C.POINTER(SpecState)]),
     "cmf_decode_rounds": (_I, [_P, _I, _I, _I, C.POINTER(GenStats)]),
     "cmf_decode_tokens": (_I, [_P, _P, _I]),
     "cmf_forward_batch": (_I, [_P, _P, _I, _I, _P, _P]),

@@ -4,6 +4,8 @@
 // (graph_spec_step, pipeline.rs:3582-4213) run device-side: drafted tokens,
 // acceptance and the commit never leave HBM; the host reads back one small
 // state record per round.
+#include <chrono>
+#include <climits>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -117,6 +119,10 @@ struct cmf_model_s {
     int graph_k = 0;
     int graph_len = 0;  // attention length bound the captured round was built for
     int graph_sampling = -1;
+    hipGraphExec_t plain_graph = nullptr;  // one captured plain step
+    int plain_len = 0;
+    int plain_sampling = -1;
+    cmf_spec_state mon{};  // the speculation monitor of the last cmf_decode (spec = 2)
     bool use_graph = true;
     bool decoding = false;
     int rounds = 0;
@@ -542,6 +548,8 @@ int ensure_logits(cmf_model_s* m) {
 void drop_graph(cmf_model_s* m) {
     if (m->round_graph) (void)hipGraphExecDestroy(m->round_graph);
     m->round_graph = nullptr;
+    if (m->plain_graph) (void)hipGraphExecDestroy(m->plain_graph);
+    m->plain_graph = nullptr;
 }
 
 int ensure_out(cmf_model_s* m, int cap) {
@@ -751,7 +759,7 @@ int cmf_model_create(const cmf_model_config* cfg, cmf_model* out) {
 int cmf_model_free(cmf_model m) {
     if (!m) return CMF_OK;
     (void)hipStreamSynchronize(stream());
-    if (m->round_graph) (void)hipGraphExecDestroy(m->round_graph);
+    drop_graph(m);
     for (auto& l : m->L) {
         free_layer(l);
         free_weight(l.router);
@@ -977,11 +985,14 @@ static void spec_round(cmf_model m, int k, bool sampling, const cmf_sampler_conf
 }
 
 // One plain decode step: forward t_next at next_pos, emit it, pick the next.
-static void plain_step(cmf_model m, bool sampling, const cmf_sampler_config& sc, int np, hipStream_t s) {
+// graph_len > 0: the attention length bound of a captured step (every
+// position-dependent value is read from the device state).
+static void plain_step(cmf_model m, bool sampling, const cmf_sampler_config& sc, int np, hipStream_t s,
+                       int graph_len = 0) {
     const int H = m->c.hidden, V = m->c.vocab;
     int* pb = &m->st->next_pos;
     launch_embed(&m->st->t_next, embed_src(m), H, m->hv, H, 1, s);
-    trunk_forward(m, 1, pb, 0, np + 1, true, s);
+    trunk_forward(m, 1, pb, 0, graph_len ? graph_len : np + 1, true, s);
     if (sampling) sample_rows(m->sb, m->logits, V, 1, sc, m->st, SampleMode::Plain, 0, nullptr, s);
     else launch_argmax(m->logits, V, V, 1, m->am_v, m->am_i, m->st->argmax, s);
     hipLaunchKernelGGL(k_plain_commit, dim3(1), dim3(256), 0, s, m->st, m->hv, m->h_tip, H, m->out,
@@ -1069,6 +1080,31 @@ int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats)
         for (int r = r0; r < n; r++) CMF_HIP(hipGraphLaunch(m->round_graph, s));
         r0 = n;
     }
+    if (!spec && m->use_graph && n > 1) {
+        // plain steps the same way: one eager step, then one captured step
+        // replayed (the forward_token_graph counterpart, gpu.rs:1368)
+        const int need = std::min(m->c.max_seq, ((np + n + 2 + 511) / 512) * 512);
+        if (!m->plain_graph || m->plain_sampling != (int)sampling || m->plain_len < need) {
+            plain_step(m, sampling, m->sc, np, s);
+            np += 1;
+            r0 = 1;
+            if (m->plain_graph) {
+                (void)hipGraphExecDestroy(m->plain_graph);
+                m->plain_graph = nullptr;
+            }
+            hipGraph_t g;
+            CMF_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            plain_step(m, sampling, m->sc, np, s, need);
+            CMF_HIP(hipStreamEndCapture(s, &g));
+            const hipError_t ie = hipGraphInstantiate(&m->plain_graph, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            CMF_HIP(ie);
+            m->plain_sampling = (int)sampling;
+            m->plain_len = need;
+        }
+        for (int r = r0; r < n; r++) CMF_HIP(hipGraphLaunch(m->plain_graph, s));
+        r0 = n;
+    }
     for (int r = r0; r < n; r++) {
         if (spec) {
             spec_round(m, k, sampling, m->sc, np, s);
@@ -1110,18 +1146,90 @@ int cmf_decode_tokens(cmf_model m, int32_t* out, int cap) {
     return n;
 }
 
+// The speculation monitor (SpecMon, pipeline.rs:661-694): exponential
+// averages of a speculative round's wall time and of the tokens it produced,
+// and the plain token's wall time.  A round pays when tokens * plain_ms >
+// round_ms * 1.03; round 1 after a (re)start is not counted (it pays the
+// one-off set-up).
+namespace {
+void mon_round(cmf_spec_state& s, double dt_ms, int produced) {
+    s.n += 1;
+    if (s.n == 1) return;
+    const double a = s.n == 2 ? 1.0 : 0.3;
+    s.round_ms += a * (dt_ms - s.round_ms);
+    s.tokens += a * ((double)produced - s.tokens);
+}
+bool mon_pays(const cmf_spec_state& s) { return s.plain_ms > 0.0 && s.tokens * s.plain_ms > s.round_ms * 1.03; }
+
+// The trial's step after one speculative round (spec_trial_round,
+// pipeline.rs:3181-3230): five rounds of a trial, then the plain phase (or,
+// with a known plain rate, the decision at once); a decided speculation
+// re-checks the rule every round and stops after four losing rounds in a
+// row, to be retried 128 tokens later.
+void mon_after_round(cmf_spec_state& s, int generated, double now_ms) {
+    if (s.phase == CMF_SPEC_TRIAL) {
+        s.trial_rounds += 1;
+        if (s.trial_rounds >= 5) {
+            if (s.plain_ms > 0.0) {
+                const bool keep = mon_pays(s);
+                s.fails = 0;
+                s.phase = keep ? CMF_SPEC_ON : CMF_SPEC_OFF;
+                s.recheck_at = keep ? INT_MAX : generated + 128;
+            } else {
+                s.phase = CMF_SPEC_PLAIN_TRIAL;
+                s.t0_ms = now_ms;
+                s.gen0 = generated;
+            }
+        }
+    } else if (s.phase == CMF_SPEC_ON) {
+        if (mon_pays(s)) {
+            s.fails = 0;
+        } else if (++s.fails >= 4) {
+            s.phase = CMF_SPEC_OFF;
+            s.recheck_at = generated + 128;
+        }
+    }
+}
+// The per-token part of the trial (pipeline.rs:2655-2689): the plain phase
+// ends after 8 tokens with the decision; a decided arm is re-checked at
+// recheck_at by a new trial.
+void mon_token(cmf_spec_state& s, int generated, double now_ms) {
+    if (s.phase == CMF_SPEC_PLAIN_TRIAL && generated >= s.gen0 + 8) {
+        s.plain_ms = (now_ms - s.t0_ms) / (double)(generated - s.gen0);
+        const bool keep = mon_pays(s);
+        s.fails = 0;
+        s.phase = keep ? CMF_SPEC_ON : CMF_SPEC_OFF;
+        s.recheck_at = keep ? INT_MAX : generated + 128;
+    } else if ((s.phase == CMF_SPEC_ON || s.phase == CMF_SPEC_OFF) && generated >= s.recheck_at) {
+        s.n = 0;
+        s.phase = CMF_SPEC_TRIAL;
+        s.trial_rounds = 0;
+        s.gen0 = generated;
+    }
+}
+double wall_ms() {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+}  // namespace
+
 // The reference decode loop (pipeline.rs:2546-2980) over the device rounds:
 // emit t_next; a speculative round while generated + 1 < max_tokens, else a
-// plain step; the last token is emitted without a forward.
+// plain step; the last token is emitted without a forward.  spec = 2 puts
+// the rounds under the speculation monitor (SpecMon and its trial,
+// pipeline.rs:661-694, 2537, 2655-2760, 3181-3230): speculation stops when
+// the measured rounds do not pay and is retried 128 tokens later.
 int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
                int k, int32_t* out, cmf_gen_stats* stats) {
-    if (!out || max_tokens < 1) return fail("decode: bad arguments");
+    if (!out || max_tokens < 1 || spec < 0 || spec > 2) return fail("decode: bad arguments");
     int rc = cmf_decode_begin(m, sc, seed);
     if (rc != CMF_OK) return rc;
     hipStream_t s = stream();
     double ms = 0.0;
     cmf_gen_stats st{}, tot{};
     int generated = 0;
+    cmf_spec_state& mon = m->mon;
+    mon = cmf_spec_state{};
+    mon.phase = CMF_SPEC_TRIAL;
     while (true) {
         // a round that ends at or past max_tokens ends the decode (its next
         // token is not emitted: pipeline.rs's loop stops at generated >= max)
@@ -1133,14 +1241,28 @@ int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64
             generated += 1;
             break;
         }
-        const bool sp = spec && generated + 2 < max_tokens;
+        if (spec == 2) mon_token(mon, generated, wall_ms());
+        const bool off = spec == 2 && (mon.phase == CMF_SPEC_PLAIN_TRIAL || mon.phase == CMF_SPEC_OFF);
+        const bool sp = spec && !off && generated + 2 < max_tokens;
+        const double t0 = wall_ms();
         rc = cmf_decode_rounds(m, 1, sp ? 1 : 0, k, &st);
         if (rc != CMF_OK) return rc;
         ms += st.device_ms;
         tot.drafted += st.drafted;
         tot.accepted += st.accepted;
         tot.rounds += st.rounds;
+        const int produced = m->emitted_host - generated;
         generated = m->emitted_host;
+        if (sp) {
+            mon.spec_rounds += 1;
+            if (spec == 2) {
+                const double now = wall_ms();
+                mon_round(mon, now - t0, produced);
+                mon_after_round(mon, generated, now);
+            }
+        } else {
+            mon.plain_steps += 1;
+        }
     }
     const int n = cmf_decode_tokens(m, out, m->emitted_host);
     if (n < 0) return CMF_ERR;
@@ -1152,6 +1274,12 @@ int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64
         stats->device_ms = ms;
     }
     m->decoding = false;
+    return CMF_OK;
+}
+
+int cmf_spec_monitor(cmf_model m, cmf_spec_state* out) {
+    if (!m || !out) return fail("spec_monitor: null argument");
+    *out = m->mon;
     return CMF_OK;
 }
 

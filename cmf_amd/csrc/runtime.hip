@@ -739,6 +739,7 @@ int cmf_gemv_prepared(cmf_weight w, const void* d_planes, const float* d_xs, int
 }  // extern "C"
 
 namespace cmf {
+typedef int int4v_rt __attribute__((ext_vector_type(4)));
 // Busy-wait ~`ticks` of the constant-rate wall clock (bounded: also exits
 // after `max_iter` polls), so that launches enqueued behind it leave the
 // device queue full and back-to-back timing sees no host gaps.
@@ -755,9 +756,61 @@ __global__ __launch_bounds__(256) void k_copy16(const uint4* __restrict__ src, u
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
+// Plain read with the M = 1 GEMV's structure: workgroups of 8 waves, each
+// wave requesting 4 KiB (four 1 KiB steps, 16 bytes per lane) at once; the
+// words are folded so that the loads cannot be dropped.
+__global__ __launch_bounds__(512) void k_read32k(const int4v_rt* __restrict__ src, uint32_t* __restrict__ sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t base = ((size_t)blockIdx.x * 8 + wave) * 4 * 64 + lane;
+    int4v_rt v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = __builtin_nontemporal_load(src + base + u * 64);
+    uint32_t x = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) x ^= (uint32_t)(v[u].x ^ v[u].y ^ v[u].z ^ v[u].w);
+    if (x == 0x9E3779B9u) sink[0] = x;  // (practically never: keeps the loads)
+}
 }  // namespace cmf
 
 extern "C" {
+
+int cmf_time_read(size_t bytes, int nbuf, int iters, float* avg_ms) {
+    if (ensure_init() != CMF_OK) return CMF_ERR;
+    if (bytes < 32768 || bytes % 32768 || nbuf < 1 || nbuf > 64 || iters < 1 || !avg_ms)
+        return fail("time_read: bytes must be a positive multiple of 32768, 1 <= nbuf <= 64, iters >= 1");
+    hipStream_t st = stream();
+    std::vector<void*> src(nbuf, nullptr);
+    uint32_t* sink = nullptr;
+    int rc = CMF_OK;
+    for (auto& p : src)
+        if (hipMalloc(&p, bytes) != hipSuccess || hipMemsetAsync(p, 1, bytes, st) != hipSuccess) rc = fail("time_read: allocation failed");
+    if (rc == CMF_OK && hipMalloc(&sink, 64) != hipSuccess) rc = fail("time_read: allocation failed");
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (rc == CMF_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)) rc = fail("time_read: event");
+    if (rc == CMF_OK) {
+        const int grid = (int)(bytes / 32768);
+        for (int i = 0; i < 20; i++)
+            hipLaunchKernelGGL(k_read32k, dim3(grid), dim3(512), 0, st, (const int4v_rt*)src[i % nbuf], sink);
+        int rate_khz = 100000;
+        (void)hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, g_dev);
+        hipLaunchKernelGGL(k_spin, dim3(1), dim3(64), 0, st, (unsigned long long)rate_khz * 5, 1 << 22);
+        (void)hipEventRecord(e0, st);
+        for (int i = 0; i < iters; i++)
+            hipLaunchKernelGGL(k_read32k, dim3(grid), dim3(512), 0, st, (const int4v_rt*)src[i % nbuf], sink);
+        (void)hipEventRecord(e1, st);
+        float ms = 0.f;
+        if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) rc = fail("time_read: timing");
+        *avg_ms = ms / iters;
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    (void)hipStreamSynchronize(st);
+    for (auto p : src)
+        if (p) (void)hipFree(p);
+    if (sink) (void)hipFree(sink);
+    if (rc == CMF_OK) CMF_HIP(hipGetLastError());
+    return rc;
+}
 
 int cmf_time_copy(size_t bytes, int nbuf, int iters, float* avg_ms) {
     if (ensure_init() != CMF_OK) return CMF_ERR;

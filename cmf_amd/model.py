@@ -8,7 +8,7 @@ import ctypes as C
 
 import numpy as np
 
-from . import (CmfError, GenStats, LayerDesc, ModelConfig, SamplerConfig, Tensor, _ptr, check, lib)
+from . import (CmfError, GenStats, LayerDesc, ModelConfig, SamplerConfig, SpecState, Tensor, _ptr, check, lib)
 
 
 def _tensor(t, keep):
@@ -85,15 +85,24 @@ class Model:
         check(lib().cmf_prefill(self.h, _ptr(ids), len(ids)))
 
     def decode(self, max_tokens, sampler=None, seed=0, spec=True, k=4):
-        """Returns (tokens, stats).  sampler=None is greedy."""
+        """Returns (tokens, stats).  sampler=None is greedy.  spec: False
+        (plain steps), True (speculative rounds throughout) or "auto" (the
+        reference's speculation monitor decides, pipeline.rs:661-694;
+        `monitor()` then reports its state)."""
         sc = sampler if sampler is not None else SamplerConfig(temperature=0.0, repetition_penalty=1.0)
         out = np.zeros(max_tokens + k + 2, dtype=np.int32)
         st = GenStats()
-        ok = check(lib().cmf_decode(self.h, max_tokens, C.byref(sc), seed, 1 if spec else 0, k, _ptr(out),
-                                    C.byref(st)))
+        mode = 2 if spec == "auto" else (1 if spec else 0)
+        ok = check(lib().cmf_decode(self.h, max_tokens, C.byref(sc), seed, mode, k, _ptr(out), C.byref(st)))
         if not ok:
             raise CmfError("decode declined (penalised sampler config or top_k beyond the device sampler)")
         return out[: st.generated].copy(), st
+
+    def monitor(self):
+        """The speculation monitor of the last decode (cmf_spec_state)."""
+        ms = SpecState()
+        check(lib().cmf_spec_monitor(self.h, C.byref(ms)))
+        return ms
 
     def decode_begin(self, sampler=None, seed=0):
         sc = sampler if sampler is not None else SamplerConfig(temperature=0.0, repetition_penalty=1.0)

@@ -164,6 +164,10 @@ int cmf_time_gemm(cmf_weight w, const float* d_x, int m, float* d_y, int warmup,
  * measurement helper, the known-size kernel against which HBM traffic
  * counters (FETCH_SIZE / WRITE_SIZE) are calibrated. */
 int cmf_time_copy(size_t bytes, int nbuf, int iters, float* avg_ms);
+/* Diagnostic: average time of a plain read of `bytes` (a multiple of 32 KiB)
+ * in the M = 1 GEMV's launch shape (workgroups of 8 waves x 4 KiB), nbuf
+ * buffers rotated: the ceiling a GEMV streaming that many bytes can reach. */
+int cmf_time_read(size_t bytes, int nbuf, int iters, float* avg_ms);
 
 /* ---- model: Qwen3-arch decoder + MTP head (pipeline.rs) --------------- */
 typedef struct cmf_model_s* cmf_model;
@@ -271,6 +275,23 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n);
  * are produced.  out: capacity max_tokens + k + 1.  Returns via stats. */
 int cmf_decode(cmf_model m, int max_tokens, const cmf_sampler_config* sc, uint64_t seed, int spec,
                int k, int32_t* out, cmf_gen_stats* st);
+/* spec = 2: the rounds run under the speculation monitor (SpecMon,
+ * pipeline.rs:661-694, and its trial, :2537, :2655-2760, :3181-3230): five
+ * timed speculative rounds, eight timed plain tokens, then the faster arm;
+ * a speculating decode re-checks tokens_per_round * plain_ms > round_ms *
+ * 1.03 every round and stops after four losing rounds, and a stopped one is
+ * retried 128 tokens later.  Times are host wall times, as the reference's.
+ * cmf_spec_monitor reads the monitor of the model's last cmf_decode. */
+enum { CMF_SPEC_TRIAL = 0, CMF_SPEC_PLAIN_TRIAL = 1, CMF_SPEC_ON = 2, CMF_SPEC_OFF = 3 };
+typedef struct {
+    double round_ms, tokens, plain_ms; /* SpecMon's averages (pipeline.rs:672-677) */
+    int n, fails;                      /* rounds counted since the trial began; losing rounds in a row */
+    int phase;                         /* CMF_SPEC_*: the SpecTrial phase (pipeline.rs:642-660) */
+    int trial_rounds, gen0, recheck_at;
+    double t0_ms;                      /* start of the plain phase (host wall clock) */
+    int spec_rounds, plain_steps;      /* what the decode ran */
+} cmf_spec_state;
+int cmf_spec_monitor(cmf_model m, cmf_spec_state* out);
 /* The same loop in pieces, for callers that pace it themselves:
  * begin (reset the emitted stream, sample the first token from the tip),
  * exactly n speculative rounds (spec=1) or plain steps (spec=0) with no
