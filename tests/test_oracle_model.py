@@ -368,3 +368,81 @@ def test_a8w8_contract_switch(tiny):
     rel = np.linalg.norm(he - ha) / np.linalg.norm(he)
     assert 1e-4 < rel < 5e-2
     assert np.array_equal(he, he2)
+
+
+def _np_block(l, xs, c):
+    """f64 dense decoder block over rows xs at positions 0..n-1 (its own
+    causal KV): the per-layer body of _np_forward"""
+    H, nh, nkv, hd, eps = c["hidden"], c["n_heads"], c["n_kv"], c["head_dim"], c["eps"]
+    Wq, Wk, Wv, Wo = _dq(l["wq"]), _dq(l["wk"]), _dq(l["wv"]), _dq(l["wo"])
+    Wg, Wu, Wd = _dq(l["gate"]), _dq(l["up"]), _dq(l["down"])
+    hs = np.array(xs, np.float64)
+    n = len(hs)
+    x = np.stack([_rms(h, l["input_norm"], eps) for h in hs])
+    q = (x @ Wq.T).reshape(n, nh, hd)
+    k = (x @ Wk.T).reshape(n, nkv, hd)
+    v = (x @ Wv.T).reshape(n, nkv, hd)
+    q = np.stack([[_rope(_rms(q[p, h], l["q_norm"], eps), p, c["rope_theta"]) for h in range(nh)] for p in range(n)])
+    k = np.stack([[_rope(_rms(k[p, g], l["k_norm"], eps), p, c["rope_theta"]) for g in range(nkv)] for p in range(n)])
+    att = np.zeros((n, nh, hd))
+    for p in range(n):
+        for h in range(nh):
+            g = h // (nh // nkv)
+            s = k[: p + 1, g] @ q[p, h] / np.sqrt(hd)
+            w = np.exp(s - s.max())
+            att[p, h] = (w / w.sum()) @ v[: p + 1, g]
+    hs = hs + att.reshape(n, nh * hd) @ Wo.T
+    x2 = np.stack([_rms(h, l["post_norm"], eps) for h in hs])
+    gg, uu = x2 @ Wg.T, x2 @ Wu.T
+    return hs + (gg / (1 + np.exp(-gg)) * uu) @ Wd.T
+
+
+def test_mtp_step_matches_f64_numpy(tiny):
+    """or_mtp_step (mtp_step_hl, pipeline.rs:3051-3160) with a random,
+    non-zero hidden half of eh_proj: x = eh_proj [rms(embed(t_{p+1}), enorm);
+    rms(h_p, hnorm)] with h_p the trunk output BEFORE the final norm (the
+    decode loop's `hidden`, pipeline.rs:2563-2571), one block over the MTP's
+    own KV at positions 0..p, logits = lm_head rms(block(x), mtp norm).  The
+    f64 restatement pins the block output and the logits at every position;
+    the plausible mistakes (no hnorm, the post-final-norm hidden fed, the
+    halves swapped) each land far outside the tolerance."""
+    from cmf_amd import synth
+    c = TINY
+    H, eps = c["hidden"], c["eps"]
+    mtp = tiny["mtp"]
+    Weh = _dq(mtp["eh_proj"])
+    assert np.abs(Weh[:, H:]).max() > 0.0  # the hidden half takes part
+    E = _dq(tiny["lm_head"])
+    toks = synth.ids(12, 7, c["vocab"])
+    hs = _np_forward(tiny, toks)  # pre-final-norm trunk rows (f64)
+    o = orc.OracleModel(tiny, threads=2)
+    hid = [o.forward(int(t), i) for i, t in enumerate(toks)]
+    got_lg, got_h = [], []
+    for p in range(len(toks) - 1):
+        lg = np.empty(c["vocab"], np.float32)
+        ho = np.empty(H, np.float32)
+        orc.lib().or_mtp_step(C.byref(o.m), C.byref(o.st), orc._p(hid[p]), int(toks[p + 1]), p, orc._p(lg), orc._p(ho))
+        got_lg.append(lg)
+        got_h.append(ho)
+
+    def ref(variant):
+        xs = []
+        for p in range(len(toks) - 1):
+            e = _rms(E[toks[p + 1]], mtp["enorm"], eps)
+            h = hs[p]
+            if variant == "post_norm":
+                h = _rms(h, tiny["final_norm"], eps)
+            hh = h if variant == "no_hnorm" else _rms(h, mtp["hnorm"], eps)
+            xs.append(Weh @ (np.concatenate([hh, e]) if variant == "swapped" else np.concatenate([e, hh])))
+        outs = _np_block(mtp["layer"], xs, c)
+        return outs, [E @ _rms(x, mtp["norm"], eps) for x in outs]
+
+    rh, rl = ref("exact")
+    for p in range(len(got_h)):
+        eh = np.linalg.norm(got_h[p] - rh[p]) / np.linalg.norm(rh[p])
+        el = np.linalg.norm(got_lg[p] - rl[p]) / np.linalg.norm(rl[p])
+        assert eh < 1e-5 and el < 1e-5, (p, eh, el)
+    for variant in ("no_hnorm", "post_norm", "swapped"):
+        wh, _ = ref(variant)
+        d = max(np.linalg.norm(got_h[p] - wh[p]) / np.linalg.norm(wh[p]) for p in range(len(got_h)))
+        assert d > 1e-2, (variant, d)
