@@ -515,7 +515,7 @@ int alloc_scratch(cmf_model_s* m) {
         // prepared operand of the widest GEMV: q8 K <= max(2H, nh*hd), q4 K <= max(H, I)
         const size_t k8 = ((size_t)std::max(2 * H, c.n_heads * hd) + 63) / 64;
         const size_t k4 = ((size_t)std::max(H, c.inter) + 127) / 128;
-        const size_t pb = std::max(k8 * 1024 * 3, k4 * 4 * (1024 * 2 + 64));
+        const size_t pb = std::max(k8 * 1024 * 3, k4 * 4 * (1024 * 2 + 128));
         if (dalloc(m, (void**)&m->planes, pb)) return CMF_ERR;
     }
     // rope table (cos, sin) per (position, freq) with the host libm, as

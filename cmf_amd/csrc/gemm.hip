@@ -7,16 +7,17 @@
 // x 64 GRB weight rows (wave w holds GRB row blocks in registers), and walks
 // K in steps of 128 columns (4 tiles):
 //   - the operand step (hi / lo f16 planes of 64 rows x 4 tiles and their
-//     tile biases, 33 KiB) is loaded into registers one step ahead and
+//     two tables of tile biases, 34 KiB) is loaded into registers one step ahead and
 //     written to the other half of a double-buffered LDS tile after the
 //     current step's MFMAs (one barrier per step);
 //   - the weights of the next step (4 row blocks x 1 KiB + scales per wave)
 //     are requested before the current step is computed;
 //   - per tile and row block: the nibbles become f16 denormals n * 2^-24
-//     (one mask per pair), the MFMA accumulator starts at the tile bias
-//     -8 * 2^-24 * sum(x) (so D = 2^-24 * sum((n - 8) x) exactly), the hi and
-//     lo planes take one MFMA each, and the tile scale multiplies D in f32
-//     as q4t_row_exact does (qtensor.rs:4418-4432).
+//     (one mask per pair); the hi and lo planes (fixed point, prep16_row)
+//     take one MFMA each, each started at its plane's tile bias
+//     -8 * 2^-24 * sum (so D = 2^-24 * sum((n - 8) x) / xs exactly), and the
+//     tile scale multiplies D in f32 as q4t_row_exact does
+//     (qtensor.rs:4418-4432).
 #include "gemv_kern.h"
 #include "runtime.h"
 
@@ -26,7 +27,7 @@ struct GemmArgs {
     const void* w;        // [rb][group of 4 tiles][lane][16 B]   (q8: [rb][64-column chunk][lane][16 B])
     const void* scale;    // q4t f16 [rb][group][16][4]; q4tp u32 codes; q8 f32 row scales
     const float2* rowp;   // q4tp (2^lo, 2^step) per row
-    const uint8_t* planes;  // hi [item][Mp], lo [item][Mp] (16 B), bias [tile][Mp] f32 (q8: q0 q1 q2 [item][Mp])
+    const uint8_t* planes;  // hi [item][Mp], lo [item][Mp] (16 B), biases hi / lo [tile][Mp] f32 (q8: q0 q1 q2 [item][Mp])
     const float* xs;      // [Mp] 2^-e per batch row (q8: amax / 127)
     float* y;
     int ldy, M, Mp, N, ntg, nrb, resid;
@@ -38,7 +39,7 @@ struct GemmArgs {
 };
 
 constexpr int GB = 64;             // batch rows per workgroup
-constexpr int GCH = 33;            // 1 KiB operand chunks per K step (16 hi + 16 lo items, 1 bias)
+constexpr int GCH = 34;            // 1 KiB operand chunks per K step (16 hi + 16 lo items, hi and lo biases)
 constexpr int GJ = (GCH + 3) / 4;  // chunks per wave (clamped)
 
 // GRB: row blocks per wave (4 for large batches; 1 gives small batches 4x
@@ -56,19 +57,21 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
     const uint4* PH = (const uint4*)a.planes;
     const uint4* PL = PH + items * Mp;
     const float* PB = (const float*)(PL + items * Mp);
+    const float* PB2 = PB + (size_t)ntg * 4 * Mp;  // the lo plane's biases
 
     // operand chunk c of step g for this lane: 16 hi items, 16 lo items, the
-    // biases.  One unconditional load per chunk, the source picked by selects
-    // (a load under a branch makes the compiler wait for it at once); chunk
-    // j of this wave is held in its own register quad (RA).
+    // hi biases, the lo biases.  One unconditional load per chunk, the source
+    // picked by selects (a load under a branch makes the compiler wait for it
+    // at once); chunk j of this wave is held in its own register quad (RA).
     auto src_a = [&](int j, int g) __attribute__((always_inline)) -> const uint4* {
         const int c = min(wave + 4 * j, GCH - 1);
         const uint4* ph = PH + (size_t)(16 * g + c) * Mp + GB * by + lane;
         const uint4* pl = PL + (size_t)(16 * g + c - 16) * Mp + GB * by + lane;
-        const uint4* pb = (const uint4*)(PB + (size_t)(4 * g + (lane >> 4)) * Mp + GB * by + 4 * (lane & 15));
+        const size_t bo = (size_t)(4 * g + (lane >> 4)) * Mp + GB * by + 4 * (lane & 15);
+        const uint4* pb = (const uint4*)((c == 32 ? PB : PB2) + bo);
         return c < 16 ? ph : c < 32 ? pl : pb;
     };
-    // the clamped chunk (the biases) is written by every wave with the same data
+    // the clamped chunk (the lo biases) is written by every wave with the same data
     auto dst_a = [&](int j, int buf) __attribute__((always_inline)) -> uint4* {
         return &At[buf][min(wave + 4 * j, GCH - 1) * 64 + lane];
     };
@@ -119,7 +122,8 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
 
     auto compute = [&](int buf, const uint4* wv, const uint2* sv) __attribute__((always_inline)) {
         const uint4* A = At[buf];
-        const float4v* Bias = (const float4v*)(A + 32 * 64);  // [tile][64 rows] f32
+        const float4v* Bias = (const float4v*)(A + 32 * 64);   // hi plane's [tile][64 rows] f32
+        const float4v* BiasL = (const float4v*)(A + 33 * 64);  // lo plane's
 #pragma unroll 1
         for (int t = 0; t < 4; t++) {
             half8 bq[GRB];
@@ -140,10 +144,13 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
                 const half8 xh = __builtin_bit_cast(half8, A[(4 * t + s) * 64 + 16 * mb + r]);
                 const half8 xl = __builtin_bit_cast(half8, A[(16 + 4 * t + s) * 64 + 16 * mb + r]);
                 const float4v cb = Bias[t * 16 + 4 * mb + s];  // rows 16 mb + 4 s .. + 3
+                const float4v cbl = BiasL[t * 16 + 4 * mb + s];
 #pragma unroll
                 for (int q = 0; q < GRB; q++) {
+                    // hi and lo in accumulators of their own: each tile sum is
+                    // exact only within one plane
                     float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq[q], cb, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq[q], d, 0, 0, 0);
+                    d += __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq[q], cbl, 0, 0, 0);
                     acc[q][mb] += d * sc[q];
                 }
             }
@@ -361,9 +368,9 @@ static int gemm_kparts(long base, int nsteps) {
 
 size_t gemm_planes_bytes(const DevWeight& w, int mp) {
     // q8: three planes of nk * 64 * Mp B; q4: hi + lo 2 * items * Mp * 16 B
-    // and the tile biases tiles * Mp * 4 B
+    // and the two tables of tile biases 2 * tiles * Mp * 4 B
     if (w.dtype == DT_Q8ROW) return (size_t)w.kchunks * 64 * mp * 3;
-    return (size_t)w.kchunks * 16 * mp * 32 + (size_t)w.kchunks * 4 * mp * 4;
+    return (size_t)w.kchunks * 16 * mp * 32 + (size_t)w.kchunks * 4 * mp * 8;
 }
 
 int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool resid, hipStream_t st) {

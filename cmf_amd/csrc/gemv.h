@@ -214,23 +214,65 @@ __device__ __forceinline__ float f16_pair_sum(_Float16 hi, _Float16 lo) {
 #endif
 }
 
-// Writes batch row b (of M) of the q4 activation operand: f16 hi/lo of
-// x*2^e with max|x*2^e| < 2^15, xs[b] = 2^-e, planes [item = 4*tile + s][b]
-// x 8 halves of columns 32*tile + 8*s + {0,4,2,6,1,5,3,7} (hi plane, then lo
-// plane), then the tile biases [tile][bstride] f32: -8 * 2^-24 * sum(hi + lo)
-// of the tile at [tile][b], zero for rows in [M, bstride) (the workgroup of
-// row 0 writes those zeros).  M is the planes' row stride (the batch of a
-// GEMV; the padded row count of a GEMM, with bstride = M).  The q4 kernels multiply x by the nibbles as f16 denormals
-// n * 2^-24 and start each tile's accumulator at this bias, so that
-// D = 2^-24 * sum((n - 8) * x).  nthr must
-// be a multiple of 64: the four items of a tile sit in lanes 4t..4t+3 of one
-// wave, which add their partial sums for the bias.
-__device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b, int M,
-                                  uint8_t* planes, float* xs, int tid, int nthr, int bstride = 16) {
+// The q4 activation operand in fixed point: x ~= xs * (a + k / 2048) with
+// xs = 2^(e - 11) for max|x| in [2^(e-1), 2^e), a = rint(x / xs) (|a| <=
+// 2048) and k = rint((x / xs - a) * 2048) (|k| <= 1024): hi = a and lo =
+// k * 2^-11 are exact f16 values (error <= max|x| * 2^-23).  Against the
+// nibbles as f16 denormals n * 2^-24, every product of a tile's MFMA is then
+// a multiple of 2^-24 (hi) or 2^-35 (lo), and a tile's sum, bias included,
+// stays below 2^-3: the MFMA adds exactly.  (With x * 2^e split into
+// floating f16 hi + lo the MFMA's internal sums are not exact: measured on
+// MI355X, 1e-6 relative per tile, biased, so that a q4t matvec drifted
+// 2e-5..5e-5 from an exact product where the reference's f32 loop stays at
+// 1e-7.)  The tiles' products are then scaled and summed in f32.
+constexpr float Q4_LO_UNIT = 0.00048828125f;  // 2^-11
+__device__ __forceinline__ void q4_fix_scale(float amax, float& inv_xs, float& xs) {
     int ex = 0;
     if (amax > 0.f) frexpf(amax, &ex);
-    const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-    if (tid == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+    inv_xs = amax > 0.f ? ldexpf(1.0f, 11 - ex) : 1.0f;
+    xs = amax > 0.f ? ldexpf(1.0f, ex - 11) : 1.0f;
+}
+// hi / lo of v = x / xs (|v| < 2048)
+__device__ __forceinline__ void q4_fix_split(float v, _Float16& hi, _Float16& lo) {
+    const float a = rintf(v);
+    hi = (_Float16)a;
+    lo = (_Float16)(rintf((v - a) * 2048.0f) * Q4_LO_UNIT);
+}
+constexpr float Q4_BIAS = -4.76837158203125e-07f;  // -8 * 2^-24: the format's nibble offset
+
+// Writes batch row b (of M) of the q4 activation operand: the fixed-point
+// hi / lo planes of x (q4_fix_split), xs[b] = 2^(e - 11), planes [item =
+// 4*tile + s][b] x 8 halves of columns 32*tile + 8*s + {0,4,2,6,1,5,3,7} (hi
+// plane, then lo plane), then two tables of tile biases [tile][bstride] f32:
+// T1[t][b] = -8 * 2^-24 * sum(hi) and T2[t][b] = -8 * 2^-24 * sum(lo) of the
+// tile (T2 right after T1), zero for rows in [M, bstride).  With bstride ==
+// 16 and M <= 8 (the GEMVs whose A rows 8 + b carry the lo plane of batch
+// row b) T1[t][8 + b] holds the lo bias as well.  M is the planes' row
+// stride (the batch of a GEMV; the padded row count of a GEMM, with bstride
+// = M).  The q4 kernels multiply by the nibbles as f16 denormals n * 2^-24
+// and start each tile's accumulator at the bias of its plane, so that
+// D = 2^-24 * sum((n - 8) * x) / xs exactly.  nthr must be a multiple of 64:
+// the four items of a tile sit in lanes 4t..4t+3 of one wave, which add
+// their partial sums for the biases.
+__device__ __forceinline__ void q4_put_bias(float* bias, int ntiles, int bstride, int M, int t, int b, float sh,
+                                            float sl) {
+    float* t1 = bias + (size_t)t * bstride;
+    float* t2 = bias + (size_t)ntiles * bstride + (size_t)t * bstride;
+    const bool hl = bstride == 16 && M <= 8;
+    t1[b] = sh * Q4_BIAS;
+    t2[b] = sl * Q4_BIAS;
+    if (hl) t1[8 + b] = sl * Q4_BIAS;
+    if (b == 0)
+        for (int r = M; r < bstride; r++) {
+            if (!(hl && r >= 8 && r - 8 < M)) t1[r] = 0.f;
+            t2[r] = 0.f;
+        }
+}
+__device__ inline void prep16_row(const float* x, int K, float amax, int ntiles, int b, int M,
+                                  uint8_t* planes, float* xs, int tid, int nthr, int bstride = 16) {
+    float scale, xsv;
+    q4_fix_scale(amax, scale, xsv);
+    if (tid == 0) xs[b] = xsv;
     uint8_t* ph = planes;
     uint8_t* pl = planes + (size_t)ntiles * 64 * M;
     float* bias = (float*)(planes + (size_t)ntiles * 128 * M);
@@ -240,30 +282,29 @@ __device__ inline void prep16_row(const float* x, int K, float amax, int ntiles,
         const bool on = idx < ntiles * 4;
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
         uint16_t hv[8], lv[8];
-        float part = 0.f;
+        float sh = 0.f, sl = 0.f;  // (exact: integers and multiples of 2^-11)
 #pragma unroll
         for (int j = 0; j < 8; j++) {
             const int col = c0 + ord[j];
             const float v = on && col < K ? x[col] * scale : 0.f;
-            const _Float16 h = (_Float16)v;
-            const _Float16 l = (_Float16)(v - (float)h);
+            _Float16 h, l;
+            q4_fix_split(v, h, l);
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
-            part += f16_pair_sum(h, l);
+            sh += (float)h;
+            sl += (float)l;
         }
-        part += __shfl_xor(part, 1);
-        part += __shfl_xor(part, 2);
+        sh += __shfl_xor(sh, 1);
+        sh += __shfl_xor(sh, 2);
+        sl += __shfl_xor(sl, 1);
+        sl += __shfl_xor(sl, 2);
         if (!on) continue;
         const size_t off = ((size_t)idx * M + b) * 16;
         *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
                                          lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
-        if (s == 0) {
-            bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
-            if (b == 0)
-                for (int r = M; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
-        }
+        if (s == 0) q4_put_bias(bias, ntiles, bstride, M, t, b, sh, sl);
     }
 }
 
@@ -344,11 +385,9 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
         const int jx = tid;
         const bool on = jx < m * per;
         const int b = on ? jx / per : 0, idx = jx - b * per;
-        const float amax = amv[b];
-        int ex = 0;
-        if (amax > 0.f) frexpf(amax, &ex);
-        const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-        if (on && idx == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+        float scale, xsv;
+        q4_fix_scale(amv[b], scale, xsv);
+        if (on && idx == 0) xs[b] = xsv;
         const int t = idx >> 2, s = idx & 3, c0 = t * 32 + 8 * s;
         const bool in = on && c0 < K;
         const float* x = raw + (size_t)b * K + min(c0, K - 8);
@@ -357,29 +396,27 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
         const float4 xa = in ? xa0 : z4, xb = in ? xb0 : z4;
         const float xv[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};  // columns {0,4,2,6,1,5,3,7}
         uint16_t hv[8], lv[8];
-        float part = 0.f;
+        float sh = 0.f, sl = 0.f;  // (exact: integers and multiples of 2^-11)
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            const float v = xv[j] * scale;
-            const _Float16 h = (_Float16)v;
-            const _Float16 l = (_Float16)(v - (float)h);
+            _Float16 h, l;
+            q4_fix_split(xv[j] * scale, h, l);
             hv[j] = __builtin_bit_cast(uint16_t, h);
             lv[j] = __builtin_bit_cast(uint16_t, l);
-            part += f16_pair_sum(h, l);
+            sh += (float)h;
+            sl += (float)l;
         }
-        part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0xb1, 0xf, 0xf, false));
-        part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0x4e, 0xf, 0xf, false));
+        sh += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sh), 0xb1, 0xf, 0xf, false));
+        sh += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sh), 0x4e, 0xf, 0xf, false));
+        sl += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sl), 0xb1, 0xf, 0xf, false));
+        sl += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sl), 0x4e, 0xf, 0xf, false));
         if (!on) return;
         const size_t off = ((size_t)idx * m + b) * 16;
         *(uint4*)(ph + off) = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16),
                                          hv[4] | (hv[5] << 16), hv[6] | (hv[7] << 16));
         *(uint4*)(pl + off) = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16),
                                          lv[4] | (lv[5] << 16), lv[6] | (lv[7] << 16));
-        if (s == 0) {
-            bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
-            if (b == 0)
-                for (int r = m; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
-        }
+        if (s == 0) q4_put_bias(bias, ntiles, bstride, m, t, b, sh, sl);
         return;
     }
     // otherwise one thread per pair of items (s = 2p, 2p + 1) of a tile: 16
@@ -390,11 +427,9 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
         const int jx = i0 + tid;
         const bool on = jx < m * per2;
         const int b = on ? jx / per2 : 0, ip = jx - b * per2;
-        const float amax = amv[b];
-        int ex = 0;
-        if (amax > 0.f) frexpf(amax, &ex);
-        const float scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-        if (on && ip == 0) xs[b] = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
+        float scale, xsv;
+        q4_fix_scale(amv[b], scale, xsv);
+        if (on && ip == 0) xs[b] = xsv;
         const int t = ip >> 1, s0 = (ip & 1) * 2, c0 = t * 32 + 8 * s0;
         // K % 32 == 0 (q4 rows are whole tiles) and c0 % 16 == 0: the pair
         // is all inside or all past the row.  Unconditional 16-byte reads at
@@ -409,31 +444,33 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
             q[k] = in ? r : z4;
         }
         uint4 hq[2], lq[2];
-        float pp[2];
+        float ph_[2], pl_[2];
 #pragma unroll
         for (int u = 0; u < 2; u++) {
             const float4 xa = q[2 * u], xb = q[2 * u + 1];
             const float xv[8] = {xa.x, xb.x, xa.z, xb.z, xa.y, xb.y, xa.w, xb.w};  // columns {0,4,2,6,1,5,3,7}
             uint16_t hv[8], lv[8];
-            float part = 0.f;
+            float sh = 0.f, sl = 0.f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float v = xv[j] * scale;
-                const _Float16 h = (_Float16)v;
-                const _Float16 l = (_Float16)(v - (float)h);
+                _Float16 h, l;
+                q4_fix_split(xv[j] * scale, h, l);
                 hv[j] = __builtin_bit_cast(uint16_t, h);
                 lv[j] = __builtin_bit_cast(uint16_t, l);
-                part += f16_pair_sum(h, l);
+                sh += (float)h;
+                sl += (float)l;
             }
-            pp[u] = part;
+            ph_[u] = sh;
+            pl_[u] = sl;
             hq[u] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
                                hv[6] | (hv[7] << 16));
             lq[u] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
                                lv[6] | (lv[7] << 16));
         }
-        // tile sum (p0 + p1) + (p2 + p3), the pairs' partners one lane apart
-        float part = pp[0] + pp[1];
-        part += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, part), 0xb1, 0xf, 0xf, false));
+        // tile sums (p0 + p1) + (p2 + p3), the pairs' partners one lane apart
+        float sh = ph_[0] + ph_[1], sl = pl_[0] + pl_[1];
+        sh += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sh), 0xb1, 0xf, 0xf, false));
+        sl += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sl), 0xb1, 0xf, 0xf, false));
         if (!on) continue;
         const int idx = 4 * t + s0;
         const size_t off = ((size_t)idx * m + b) * 16;
@@ -441,11 +478,7 @@ __device__ inline void prep16_rows(const float* raw, int K, const float* amv, in
         *(uint4*)(pl + off) = lq[0];
         *(uint4*)(ph + off + (size_t)m * 16) = hq[1];
         *(uint4*)(pl + off + (size_t)m * 16) = lq[1];
-        if (s0 == 0) {
-            bias[(size_t)t * bstride + b] = part * -4.76837158203125e-07f;  // -8 * 2^-24
-            if (b == 0)
-                for (int r = m; r < bstride; r++) bias[(size_t)t * bstride + r] = 0.f;
-        }
+        if (s0 == 0) q4_put_bias(bias, ntiles, bstride, m, t, b, sh, sl);
     }
 }
 

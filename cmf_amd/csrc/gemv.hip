@@ -116,9 +116,10 @@ __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk
 // exactly in index order (idx/val, count), sx = max|x| of the rest / 127
 // (1 if 0), xq = clamp(round half away(x / sx), +-127) and 0 at outliers.
 // xq (small integers) is written as the prepared planes: q8 plane 0 = xq,
-// planes 1, 2 = 0; q4 hi = xq * 2^8 exactly, lo = 0.  xs[b] = sx (q8) or
-// sx * 2^-8 (q4), so the GEMVs' integer tile dots and scales reproduce the
-// contract; the outliers are added in their epilogue.  grid (m), 512.
+// planes 1, 2 = 0; q4 hi = xq * 2^4 exactly (the fixed-point operand of
+// max|x| = 127), lo = 0.  xs[b] = sx (q8) or sx * 2^-4 (q4), so the GEMVs'
+// integer tile dots and scales reproduce the contract; the outliers are
+// added in their epilogue.  grid (m), 512.
 __global__ __launch_bounds__(512) void k_prep_a8(const float* __restrict__ x, int ldx, int K, int fmt, int nk,
                                                  uint8_t* __restrict__ planes, float* __restrict__ xs,
                                                  int* __restrict__ ocnt, int* __restrict__ oidx,
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(512) void k_prep_a8(const float* __restrict__ x, in
     if (fmt == DT_Q8ROW) prep8_row(vals, K, 127.0f, nk, b, gridDim.x, planes, xs, tid, nt);
     else prep16_row(vals, K, 127.0f, nk, b, gridDim.x, planes, xs, tid, nt);
     __syncthreads();
-    if (tid == 0) xs[b] = fmt == DT_Q8ROW ? sx : ldexpf(sx, -8);
+    if (tid == 0) xs[b] = fmt == DT_Q8ROW ? sx : ldexpf(sx, -4);  // (127 < 2^7: the operand unit 2^(7 - 11))
 }
 
 // The split_act outlier terms of the a8w8 contract, after the GEMV (grid
@@ -295,8 +296,8 @@ int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const in
 
 size_t prep_bytes(const DevWeight& w) {
     // at most 16 batch rows: q8 3 planes of nk*64*16 B ; q4 2 planes of ntiles*64*16 B
-    // (+ q4 tile biases [tile][16] f32)
-    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 1024 * 3 : (size_t)w.kchunks * 4 * (1024 * 2 + 64);
+    // (+ the q4 hi and lo tile-bias tables [tile][16] f32)
+    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 1024 * 3 : (size_t)w.kchunks * 4 * (1024 * 2 + 128);
 }
 
 int launch_prep_a8(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs, const A8Out& o,
@@ -318,8 +319,9 @@ int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* pla
 }
 
 static size_t lds_bytes(const DevWeight& w, int m) {
-    // q4: hi + lo planes and the tile biases [tile][16] f32
-    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m : (size_t)w.kchunks * 4 * (128 * m + 64);
+    // q4: hi + lo planes and the tile biases [tile][16] f32 (m > 8: both tables)
+    return w.dtype == DT_Q8ROW ? (size_t)w.kchunks * 64 * 3 * m
+                               : (size_t)w.kchunks * 4 * (128 * m + (m > 8 ? 128 : 64));
 }
 // LDS of a GEMV that evaluates the producer of src itself (XM_FUSED): the
 // planes (1 KiB aligned), then the raw rows and the norm weight; 0 when that

@@ -279,7 +279,8 @@ __device__ __forceinline__ void stage_fused(const XSrc& src, int m, int K, int f
 // bytes of the prepared planes a GEMV workgroup holds in LDS (1 KiB aligned:
 // the raw rows of XM_FUSED follow)
 __device__ __forceinline__ int planes_lds_bytes(int fmt, int nk, int m) {
-    const int b = fmt == DT_Q8ROW ? nk * 192 * m : nk * 16 * (32 * m + 16);
+    // (q4, m > 8: the lo-plane bias table T2 too)
+    const int b = fmt == DT_Q8ROW ? nk * 192 * m : nk * 16 * (32 * m + (m > 8 ? 32 : 16));
     return (b + 1023) & ~1023;
 }
 
@@ -424,7 +425,7 @@ __global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
 #pragma unroll
     for (int q = 0; q < RB; q++) prefetch_epilogue(a, rb + q, r, s, M, nullptr, rs_unused, y_first[q]);
     if constexpr (XM == XM_PREP) {
-        x_dma(a.src, ntg * (32 * M + 16), smem);  // hi + lo planes + tile biases
+        x_dma(a.src, ntg * (32 * M + (HL ? 16 : 32)), smem);  // hi + lo planes + tile biases (!HL: both tables)
         xsv = ldg(a.src.xs + (threadIdx.x & 15));
     } else if constexpr (XM == XM_FUSED) {
         x_dma_rows(a.src, M, a.src.K, raw);
@@ -451,7 +452,8 @@ __global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
     // operand planes [item][b] x 16 B, hi then lo: in LDS, or read in place
     const uint4* LH = XM != XM_GLOBAL ? (const uint4*)smem : (const uint4*)a.src.planes;
     const uint4* LL = LH + ntg * 4 * 4 * M;
-    const float4v* LB = (const float4v*)(LL + ntg * 4 * 4 * M);  // tile biases [tile][16]
+    const float4v* LB = (const float4v*)(LL + ntg * 4 * 4 * M);  // tile biases [tile][16] (T1)
+    const float4v* LB2 = LB + ntg * 16;                           // the lo plane's (T2), !HL
     // lanes whose A row is past the batch read batch row 0: their D rows are
     // never stored, and every lane loads unconditionally
     const uint4* LX = HL ? (r < 8 ? LH : LL) : LH;
@@ -493,6 +495,8 @@ __global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
                 for (int t = 0; t < 4; t++) {
                     const int item = (tg * 4 + t) * M4 + xoff;
                     const float4v cb = LB[(tg * 4 + t) * 4 + s];  // rows 4s..4s+3
+                    float4v cbl = {0.f, 0.f, 0.f, 0.f};
+                    if constexpr (!HL) cbl = LB2[(tg * 4 + t) * 4 + s];
                     half8 xa, xh, xl;
                     if constexpr (HL) {
                         xa = __builtin_bit_cast(half8, LX[item]);
@@ -511,8 +515,10 @@ __global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
                         if constexpr (HL) {
                             d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, bq, cb, 0, 0, 0);
                         } else {
+                            // hi and lo in accumulators of their own: each
+                            // tile sum is exact only within one plane
                             d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, bq, cb, 0, 0, 0);
-                            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq, d, 0, 0, 0);
+                            d += __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, bq, cbl, 0, 0, 0);
                         }
 #pragma unroll
                         for (int v = 0; v < NV; v++) acc[q][v] += d[v] * sc[q][t];
@@ -924,17 +930,18 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q8_m1(GemvArgs a) {
 }
 
 // q4t: the f16 hi / lo planes of the wave's tiles in LDS, A rows 0..7 the
-// hi plane and 8..15 the lo plane of batch row 0 (HL); each tile's bias
-// -8 * 2^-24 * sum(hi + lo) (the format's -8 offset) comes from the prepared
-// table into the slice too (SPW * 4 <= 64 floats after the planes) and is
-// added to both halves' rows at half weight.  (Scalar loads of the biases
-// made the compiler wait for every load of the wave before the first MFMA.)
+// hi plane and 8..15 the lo plane of batch row 0 (HL); each tile's biases
+// -8 * 2^-24 * sum(hi) and -8 * 2^-24 * sum(lo) (the format's -8 offset per
+// plane) come from the prepared table into the slice too (SPW * 8 <= 64
+// floats after the planes) and are added to the hi and lo rows after the
+// MFMA.  (Scalar loads of the biases made the compiler wait for every load
+// of the wave before the first MFMA.)
 template <int KS, int SPW, bool RESID>
 __global__ __launch_bounds__(64 * KS) void k_gemv_q4t_m1(GemvArgs a) {
     constexpr int NI = SPW * 4 * 4 * 2;  // 16-byte items: step x tile x k-slot x plane
     constexpr int NCH = (NI + 63) / 64;
     __shared__ float part[KS][64];
-    static_assert(SPW * 4 <= 64, "one bias per lane");
+    static_assert(SPW * 8 <= 64, "one bias per lane");
     extern __shared__ __align__(16) uint8_t smem[];  // [KS][NCH * 1024 + 256]: the waves' operand slices
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4, p = r < 8 ? 0 : 1;
@@ -957,11 +964,12 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4t_m1(GemvArgs a) {
         __builtin_amdgcn_global_load_lds((const void*)((pl ? lo : hi) + ((size_t)(tg * 4 + t) * 4 + sp) * 16),
                                          (__attribute__((address_space(3))) void*)(lx + c * 1024), 16, 0, 0);
     }
-    // the tile biases of the slice (entry [tile][0] of the table), one
-    // 4-byte direct load per lane after the planes
+    // the tile biases of the slice (entries [tile][0], hi plane, and
+    // [tile][8], lo plane, of the table), one 4-byte direct load per lane
+    // after the planes
     {
-        const int tb = min((t0 + (lane >> 2)) * 4 + (lane & 3), ntg * 4 - 1);
-        __builtin_amdgcn_global_load_lds((const void*)(btab + (size_t)tb * 16),
+        const int tb = min((t0 + (lane >> 3)) * 4 + ((lane >> 1) & 3), ntg * 4 - 1);
+        __builtin_amdgcn_global_load_lds((const void*)(btab + (size_t)tb * 16 + 8 * (lane & 1)),
                                          (__attribute__((address_space(3))) void*)(lx + NCH * 1024), 4, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -993,7 +1001,7 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4t_m1(GemvArgs a) {
             const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, dq_nib_word(wq), z, 0, 0, 0);
             const uint32_t sw = t < 2 ? sv[u].x : sv[u].y;
             const float sc = in ? f16_bits_to_f32((t & 1) ? sw >> 16 : sw & 0xFFFFu) : 0.f;
-            acc += __builtin_fmaf(bias[u * 4 + t], 0.5f, d[0]) * sc;
+            acc += (d[0] + bias[(u * 4 + t) * 2 + (s >> 1)]) * sc;  // s >= 2: the lo rows
         }
     }
     float o = m1_reduce<KS>(part, acc, wave, lane);

@@ -301,9 +301,9 @@ int cmf_moe_create(int n_experts, int hidden, int inter, int top_k, int norm_top
     m->down.resize(n_experts);
     m->set.assign(n_experts, 0);
     const int H = hidden, I = inter, mj = m->max_jobs;
-    // prepared operand sizes of the widest codec (q8 3 B / q4 4 B per element + q4 tile biases)
-    const size_t px = std::max(((size_t)H + 63) / 64 * 1024 * 3, ((size_t)H + 127) / 128 * 4 * (2048 + 64));
-    m->ph_stride = std::max(((size_t)I + 63) / 64 * 1024 * 3, ((size_t)I + 127) / 128 * 4 * (2048 + 64));
+    // prepared operand sizes of the widest codec (q8 3 B / q4 4 B per element + the q4 tile-bias tables)
+    const size_t px = std::max(((size_t)H + 63) / 64 * 1024 * 3, ((size_t)H + 127) / 128 * 4 * (2048 + 128));
+    m->ph_stride = std::max(((size_t)I + 63) / 64 * 1024 * 3, ((size_t)I + 127) / 128 * 4 * (2048 + 128));
     if (moe_alloc(m, (void**)&m->d_gu, sizeof(GemvDesc) * n_experts) ||
         moe_alloc(m, (void**)&m->d_down, sizeof(GemvDesc) * n_experts) ||
         moe_alloc(m, (void**)&m->x, sizeof(float) * MAXB * H) ||

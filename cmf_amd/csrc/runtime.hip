@@ -24,7 +24,7 @@ int fail(const std::string& m) {
 
 // Workspace of cmf_gemv_dev_noalloc: the prepared operand planes of one
 // GEMV (prep_bytes of a weight with cols <= 16384: q4 128 KiB-tile groups
-// 1 081 344 B, q8 786 432 B) followed by the 16 per-row operand scales.
+// 1 114 112 B, q8 786 432 B) followed by the 16 per-row operand scales.
 // Each device the library initialises holds its own copy until the process
 // ends; calls on one device share it (the last call's contents stay).
 constexpr size_t NOALLOC_PLANES_MAX = 1310720;

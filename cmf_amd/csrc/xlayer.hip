@@ -195,13 +195,6 @@ __device__ __forceinline__ float row_max(float v) {
     v = fmaxf(v, dppf<0x118>(v, -INFINITY));
     return dppf<0x15F>(v, -INFINITY);
 }
-// f16 exponent scaling of a q4 operand: x * 2^e with max |x * 2^e| < 2^15
-__device__ __forceinline__ void f16_scale(float amax, float& scale, float& xs) {
-    int ex = 0;
-    if (amax > 0.f) frexpf(amax, &ex);
-    scale = amax > 0.f ? ldexpf(1.0f, 15 - ex) : 1.0f;
-    xs = amax > 0.f ? ldexpf(1.0f, ex - 15) : 1.0f;
-}
 
 struct XlAArgs {
     const float* hb;     // input rows [nb][H]
@@ -730,22 +723,25 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
 // ---------------------------------------------------------------------------
 // FFN launch
 // ---------------------------------------------------------------------------
-// Eight operand columns 8 s .. 8 s + 7 of tile tt, batch row b, as f16 hi /
-// lo in the MFMA A layout [tile][k-slot][row][8] (the nibble-pair order
-// {0,4,2,6,1,5,3,7} within the slot); HL: hi in row b, lo in row 8 + b of
-// one plane, otherwise hi and lo planes (lo at +lo_off halves), row b.  The
-// quad sum of (hi + lo) over the tile's four slots comes back (the bias).
+// Eight operand columns 8 s .. 8 s + 7 of tile tt, batch row b (already
+// divided by the row's operand unit xs), as the fixed-point f16 hi / lo of
+// q4_fix_split in the MFMA A layout [tile][k-slot][row][8] (the nibble-pair
+// order {0,4,2,6,1,5,3,7} within the slot); HL: hi in row b, lo in row 8 + b
+// of one plane, otherwise hi and lo planes (lo at +lo_off halves), row b.
+// The quad sums of hi and of lo over the tile's four slots come back (the
+// two tile biases; exact).
 template <bool HL>
-__device__ __forceinline__ float put8(_Float16* ap, int lo_off, int tt, int s, int b, const float (&v)[8], bool on) {
+__device__ __forceinline__ float2 put8(_Float16* ap, int lo_off, int tt, int s, int b, const float (&v)[8], bool on) {
     half8 h8, l8;
-    float part = 0.f;
+    float sh = 0.f, sl = 0.f;
 #pragma unroll
     for (int k = 0; k < 8; k++) {
-        const float x = v[nib_slot(k)];
-        const _Float16 hi = (_Float16)x, lo = (_Float16)(x - (float)hi);
+        _Float16 hi, lo;
+        q4_fix_split(v[nib_slot(k)], hi, lo);
         h8[k] = hi;
         l8[k] = lo;
-        part += f16_pair_sum(hi, lo);
+        sh += (float)hi;
+        sl += (float)lo;
     }
     const int o = ((tt * 4 + s) * 16 + b) * 8;
     if (on) {
@@ -753,17 +749,19 @@ __device__ __forceinline__ float put8(_Float16* ap, int lo_off, int tt, int s, i
         if constexpr (HL) *(half8*)(ap + o + 64) = l8;  // row 8 + b
         else *(half8*)(ap + lo_off + o) = l8;
     }
-    return quad_sum(part);
+    return make_float2(quad_sum(sh), quad_sum(sl));
 }
 // One tile's MFMA: A rows of the operand, B the 8 nibbles of the lane's word
-// as f16 denormals, C the tile's bias rows 4 s .. 4 s + 3.
+// as f16 denormals, C the tile's bias rows 4 s .. 4 s + 3 (HL: the hi rows'
+// and the lo rows' biases); !HL: the lo plane in an MFMA of its own started
+// at its biases cl (a tile's sum is exact within one plane).
 template <bool HL>
 __device__ __forceinline__ float4v tile_mfma(const _Float16* ap, int lo_off, int tt, int s, int r, uint32_t word,
-                                             float4v c) {
+                                             float4v c, float4v cl) {
     const half8 bq = dq_nib_word(word);
     const int o = ((tt * 4 + s) * 16 + r) * 8;
     float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8*)(ap + o), bq, c, 0, 0, 0);
-    if constexpr (!HL) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8*)(ap + lo_off + o), bq, d, 0, 0, 0);
+    if constexpr (!HL) d += __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8*)(ap + lo_off + o), bq, cl, 0, 0, 0);
     return d;
 }
 __device__ __forceinline__ uint32_t word_of(const uint4& w, int tt) {
@@ -801,9 +799,13 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
     int* err = a.err;
 
     __shared__ __align__(16) _Float16 AP[(HL ? 1 : 2) * 4 * 4 * 16 * 8];
+    // tile biases [tile][16 rows]: HL rows b the hi plane's, rows 8 + b the
+    // lo plane's; !HL the lo plane's in LBL / LB2L
     __shared__ __align__(16) float LB[4 * 16];
+    __shared__ __align__(16) float LBL[HL ? 1 : 4 * 16];
     __shared__ __align__(16) _Float16 AP2[(HL ? 1 : 2) * NT2 * 4 * 16 * 8];
     __shared__ __align__(16) float LB2[NT2 * 16];
+    __shared__ __align__(16) float LB2L[HL ? 1 : NT2 * 16];
     __shared__ __align__(16) float Xd[MAXB * I8];
     __shared__ __align__(16) float4v red2[NPAIR * 64];
     __shared__ float GU[2 * MAXB * IW];
@@ -847,11 +849,18 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
             wd[k] = ld_stream(a.wdn + u * 64 + lane);
             sd[k] = ldg(a.sdn + u * 16 + r);
         }
-        // bias rows nobody writes (batch rows past nb, the lo rows of HL)
+        // bias rows nobody writes (batch rows past nb; HL: rows r and 8 + r)
         const int t4 = t - 256;
-        if (t4 < 64 && (t4 & 15) >= nb) LB[t4] = 0.f;
+        auto dead = [&](int i) { return HL ? (i & 7) >= nb : (i & 15) >= nb; };
+        if (t4 < 64 && dead(t4)) {
+            LB[t4] = 0.f;
+            if constexpr (!HL) LBL[t4] = 0.f;
+        }
         for (int i = t4; i < NT2 * 16; i += 256)
-            if ((i & 15) >= nb) LB2[i] = 0.f;
+            if (dead(i)) {
+                LB2[i] = 0.f;
+                if constexpr (!HL) LB2L[i] = 0.f;
+            }
     }
 
     XL_MARK(17);
@@ -879,13 +888,17 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
         ss = row_sum_d(ss);
         am = row_max(am);
         float sc, xs;
-        f16_scale(am, sc, xs);
+        q4_fix_scale(am, sc, xs);
 #pragma unroll
         for (int i = 0; i < 8; i++) u[i] *= sc;
         const int tt = c8 >> 2;
-        const float ts = put8<HL>(AP, LO0, tt, c8 & 3, b, u, b < nb);
+        const float2 ts = put8<HL>(AP, LO0, tt, c8 & 3, b, u, b < nb);
         if (b < nb) {
-            if ((c8 & 3) == 0) LB[tt * 16 + b] = ts * -4.76837158203125e-07f;  // -8 * 2^-24
+            if ((c8 & 3) == 0) {
+                LB[tt * 16 + b] = ts.x * Q4_BIAS;
+                if constexpr (HL) LB[tt * 16 + 8 + b] = ts.y * Q4_BIAS;
+                else LBL[tt * 16 + b] = ts.y * Q4_BIAS;
+            }
             if (c8 == 0) {
                 xs0[b] = xs;
                 ssd[b] = ss;
@@ -916,7 +929,8 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
             float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int tt = 0; tt < 4; tt++) {
-                const float4v d = tile_mfma<HL>(AP, LO0, tt, s, r, word_of(wg[i], tt), *(const float4v*)&LB[tt * 16 + 4 * s]);
+                const float4v d = tile_mfma<HL>(AP, LO0, tt, s, r, word_of(wg[i], tt), *(const float4v*)&LB[tt * 16 + 4 * s],
+                                                *(const float4v*)&LBL[HL ? 0 : tt * 16 + 4 * s]);
                 acc += d * tile_scale(sg[i], tt);
             }
             if constexpr (HL) {
@@ -1011,12 +1025,16 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
         for (int i = 0; i < 8; i++) am = fmaxf(am, fabsf(u[i]));
         am = wave_max(am);
         float sc, xs;
-        f16_scale(am, sc, xs);
+        q4_fix_scale(am, sc, xs);
         if (lane == 0) xs2[b] = xs;
 #pragma unroll
         for (int i = 0; i < 8; i++) u[i] *= sc;
-        const float ts = put8<HL>(AP2, LO2, l >> 2, l & 3, b, u, lane < NL);
-        if (lane < NL && (lane & 3) == 0) LB2[(l >> 2) * 16 + b] = ts * -4.76837158203125e-07f;
+        const float2 ts = put8<HL>(AP2, LO2, l >> 2, l & 3, b, u, lane < NL);
+        if (lane < NL && (lane & 3) == 0) {
+            LB2[(l >> 2) * 16 + b] = ts.x * Q4_BIAS;
+            if constexpr (HL) LB2[(l >> 2) * 16 + 8 + b] = ts.y * Q4_BIAS;
+            else LB2L[(l >> 2) * 16 + b] = ts.y * Q4_BIAS;
+        }
     }
     XL_MARK(23);
     lds_barrier();
@@ -1031,7 +1049,8 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
                 for (int tt = 0; tt < 4; tt++) {
                     const int tile = 4 * gl + tt;
                     const float4v d = tile_mfma<HL>(AP2, LO2, tile, s, r, word_of(wd[k], tt),
-                                                    *(const float4v*)&LB2[tile * 16 + 4 * s]);
+                                                    *(const float4v*)&LB2[tile * 16 + 4 * s],
+                                                    *(const float4v*)&LB2L[HL ? 0 : tile * 16 + 4 * s]);
                     acc += d * tile_scale(sd[k], tt);
                 }
                 if constexpr (HL) {

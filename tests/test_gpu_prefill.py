@@ -48,3 +48,62 @@ def test_prefill_chunks_equal_oracle(gpu):
     ot, _ = o.decode(otip, 600, prompt, 6, spec=True, k=4)
     assert gt.tolist() == ot.tolist()
     g.free()
+
+
+CFG4 = dict(n_layers=2, hidden=1024, n_heads=16, n_kv=8, head_dim=128, inter=3072, vocab=4096,
+            max_seq=2304, rope_theta=1e6, eps=1e-6)
+
+
+def test_prefill_config4_block_shape_equals_oracle(gpu):
+    """BASELINE config 4's block shape (hidden 1024, 16 query / 8 KV heads of
+    128, FFN 3072) at its 2048-position context: 8 chunks of 256 on the
+    GEMMs and the tiled prefill attention with one KV head per XCD, the
+    same kernels config 4 runs.  The KV of both layers, the MTP KV of the
+    warm pairs and the tip equal the oracle's per-position forwards; every
+    chunk's rows and every KV head are checked on their own, and greedy
+    K = 4 rounds continue from the prefilled state (the XCD-partitioned
+    decode blocks) with the oracle's tokens.  The tip is also measured
+    against an f64 numpy forward of the 2048 positions: the GPU must be as
+    close to it as the f32 oracle is (both sum 2048-long attention rows in
+    f32, in different orders)."""
+    import time
+    from cmf_amd import synth
+    from cmf_amd.model import Model
+    from test_oracle_model import _np_forward
+    sm = synth.synth_model(CFG4, seed=24, norm_noise=0.1, sigma=0.02)
+    g = Model(sm)
+    n = 2048
+    prompt = synth.ids(25, n, CFG4["vocab"])
+    g.prefill(prompt)
+    pos, tip = g.state()
+    assert pos == n
+    t1 = time.perf_counter()
+    o = orc.OracleModel(sm, threads=16)
+    otip = o.prefill(prompt)
+    t2 = time.perf_counter()
+    ftip = _np_forward(sm, prompt)[-1]
+    print(f"oracle {t2 - t1:.1f} s, f64 {time.perf_counter() - t2:.1f} s; tip: gpu-oracle {rel_l2(tip, otip):.2e}, "
+          f"gpu-f64 {rel_l2(tip, ftip):.2e}, oracle-f64 {rel_l2(otip, ftip):.2e}", flush=True)
+    errs = []
+    for li in list(range(CFG4["n_layers"])) + [-1]:
+        rows = n if li >= 0 else n - 1
+        k, v = g.kv_export(li, rows)
+        rk, rv = o.kv(li)
+        ek, ev = rel_l2(k, rk), rel_l2(v, rv)
+        worst = 0.0
+        for c0 in range(0, rows, 256):
+            c1 = min(rows, c0 + 256)
+            worst = max(worst, rel_l2(k[:, c0:c1], rk[:, c0:c1]), rel_l2(v[:, c0:c1], rv[:, c0:c1]))
+        # each KV head on its own (one per XCD in the prefill attention)
+        heads = max(max(rel_l2(k[h], rk[h]), rel_l2(v[h], rv[h])) for h in range(CFG4["n_kv"]))
+        print(f"layer {li}: K rel {ek:.2e} V rel {ev:.2e}; worst chunk {worst:.2e}, worst head {heads:.2e}",
+              flush=True)
+        errs.append(max(ek, ev, worst, heads))
+    assert max(errs) < 1e-4
+    assert rel_l2(tip, ftip) < 2.0 * rel_l2(otip, ftip) + 1e-5
+    assert rel_l2(tip, otip) < 3e-4
+    assert gpu.lib().cmf_model_fused_blocks(g.h) == 1  # the config-4 decode blocks
+    gt, _ = g.decode(10, spec=True, k=4)
+    ot, _ = o.decode(otip, n, prompt, 10, spec=True, k=4)
+    assert gt.tolist() == ot.tolist()
+    g.free()
