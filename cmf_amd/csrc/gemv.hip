@@ -523,9 +523,17 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
     if (!k) return fail("gemv: no kernel instance for this shape");
     int occ = resident_per_cu(k, threads, lds);
     if (occ < 1) return fail("gemv: kernel does not fit a CU (LDS or registers)");
+    // m > 8 with the operand read in place (XM_GLOBAL): RB row blocks share
+    // each operand read while the grid still covers every CU (the operand,
+    // 2 x 16 rows of f16 planes, is read by every workgroup: q4t
+    // 12288x4096 m = 16 20.0 -> 13.0 us at RB = 3; 4096x12288, 256 row
+    // blocks, 19.8 -> 25.9 us, so not there)
+    const bool share_rb = xm == XM_GLOBAL && m > 8;
     if (gridy == 1 && grid_override <= 0 && pick(2)) {
         for (int c = 2; c <= 3; c++) {
-            const bool want = rb_env > 0 ? c == rb_env : (a.nrb + rb - 1) / rb > occ * num_cus();
+            const bool want = rb_env > 0 ? c == rb_env
+                              : share_rb ? a.nrb >= c * num_cus()
+                                         : (a.nrb + rb - 1) / rb > occ * num_cus();
             if (!want) continue;
             GemvKernel kc = pick(c);
             const int oc = kc ? resident_per_cu(kc, threads, lds) : 0;

@@ -1068,7 +1068,15 @@ GemvKernel q4_by_ks(int ks) {
 // RB > 1 only for the LDS-staged one-MFMA-per-tile kernels (m <= 8)
 template <int FMT, int NV, bool HL>
 GemvKernel q4_by_xm(int xm, int ks, int rb) {
-    if (xm == XM_GLOBAL) return rb == 1 ? q4_by_ks<FMT, NV, HL, XM_GLOBAL, 1>(ks) : nullptr;
+    if (xm == XM_GLOBAL) {
+        if (rb == 1) return q4_by_ks<FMT, NV, HL, XM_GLOBAL, 1>(ks);
+        // m > 8 reads the operand in place: RB row blocks share each read
+        if constexpr (!HL) {
+            if (rb == 2) return q4_by_ks<FMT, NV, HL, XM_GLOBAL, 2>(ks);
+            if (rb == 3) return q4_by_ks<FMT, NV, HL, XM_GLOBAL, 3>(ks);
+        }
+        return nullptr;
+    }
     if constexpr (HL)
         if (xm == XM_FUSED) return rb == 1 ? q4_by_ks<FMT, NV, HL, XM_FUSED, 1>(ks) : nullptr;
     if (xm != XM_PREP) return nullptr;
