@@ -161,6 +161,8 @@ SIGNATURES = {
     "cmf_model_set_layer_moe": (_I, [_P, _I, C.POINTER(LayerDesc), C.POINTER(Tensor), _P]),
     "cmf_model_set_mtp": (_I, [_P, _P, _P, C.POINTER(Tensor), C.POINTER(LayerDesc), _P]),
     "cmf_model_fused_blocks": (_I, [_P]),
+    "cmf_model_prefill_xcd": (_I, [_P]),
+    "cmf_model_xl_fallbacks": (_I, [_P]),
     "cmf_prefill": (_I, [_P, _P, _I]),
     "cmf_decode": (_I, [_P, _I, C.POINTER(SamplerConfig), _U64, _I, _I, _P, C.POINTER(GenStats)]),
     "cmf_decode_begin": (_I, [_P, C.POINTER(SamplerConfig), _U64]),

@@ -115,6 +115,10 @@ struct cmf_model_s {
     float *pf_h = nullptr, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_gu = nullptr, *pf_hm = nullptr, *pf_q = nullptr;
     int* pf_toks = nullptr;
     _Float16* pf_khl = nullptr;  // the prefill attention's K / V operands (f16 hi / lo keys, then f32 values)
+    unsigned long long* pf_cells = nullptr;  // placement check of the XCD prefill attention
+    int* pf_err = nullptr;
+    unsigned long long pf_tag = 0;
+    bool pf_xcd_off = false;  // a placement check failed: the grid-indexed variant from then on
     hipGraphExec_t round_graph = nullptr;
     int graph_k = 0;
     int graph_len = 0;  // attention length bound the captured round was built for
@@ -134,6 +138,8 @@ struct cmf_model_s {
     XlBufs xl;
     XlShape xls{};
     bool xl_on = false;
+    int xl_fallbacks = 0;   // calls re-run on the six-launch blocks after a failed check
+    float* h_save = nullptr;  // the tip hidden before such a call
 };
 
 namespace {
@@ -504,7 +510,7 @@ int alloc_scratch(cmf_model_s* m) {
         dalloc_t(m, &m->pm, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->pl, (size_t)MAXB * c.n_heads * m->nch_cap) ||
         dalloc_t(m, &m->po, (size_t)MAXB * c.n_heads * m->nch_cap * hd) ||
-        dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H) ||
+        dalloc_t(m, &m->toks, 4 * MAXB) || dalloc_t(m, &m->st, 1) || dalloc_t(m, &m->h_tip, H) || dalloc_t(m, &m->h_save, H) ||
         dalloc_t(m, &m->xs, 16))
         return CMF_ERR;
     {
@@ -575,8 +581,12 @@ int ensure_prefill_bufs(cmf_model_s* m) {
         dalloc_t(m, &m->pf_ao, R * c.n_heads * c.head_dim) || dalloc_t(m, &m->pf_gu, R * 2 * c.inter) ||
         dalloc_t(m, &m->pf_hm, R * H) || dalloc_t(m, &m->pf_toks, R) ||
         dalloc_t(m, &m->pf_q, R * c.n_heads * c.head_dim) ||
-        dalloc(m, (void**)&m->pf_khl, (size_t)c.n_kv * ((c.max_seq + 127) / 128 * 128) * c.head_dim * 8))
+        dalloc(m, (void**)&m->pf_khl, (size_t)c.n_kv * ((c.max_seq + 127) / 128 * 128) * c.head_dim * 8) ||
+        dalloc_t(m, &m->pf_cells, PREFILL_XCD_CELLS) || dalloc_t(m, &m->pf_err, 1))
         return CMF_ERR;
+    // (tags start at 1, so the zeroed cells hold none)
+    CMF_HIP(hipMemset(m->pf_cells, 0, PREFILL_XCD_CELLS * sizeof(unsigned long long)));
+    CMF_HIP(hipMemset(m->pf_err, 0, sizeof(int)));
     return CMF_OK;
 }
 
@@ -592,7 +602,8 @@ void prefill_attention(cmf_model_s* m, LayerDev& l, const float* qkv, float* ao,
         // the whole chunk at once: the tiled prefill attention (one launch
         // for the norms + append, one for the attention)
         PrefillAttnArgs pa{qkv, QKV, l.q_norm, l.k_norm, m->rope, l.kc, l.vc, c.max_seq, cnt, p0, nh, nkv,
-                           c.eps, m->pf_q, attend ? ao : nullptr, m->pf_khl};
+                           c.eps, m->pf_q, attend ? ao : nullptr, m->pf_khl, m->pf_cells, m->pf_err, ++m->pf_tag,
+                           !m->pf_xcd_off};
         launch_prefill_attention(pa, s);
         return;
     }
@@ -883,16 +894,55 @@ int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const
     return CMF_OK;
 }
 
-// An XCD-partitioned block whose exchange wait gave up (or whose attention
-// positions exceeded the host's bound) wrote wrong values: report it once.
+// After a call that ran XCD-partitioned blocks (stream idle): an exchange
+// wait that gave up, more attention positions than a launch's bound or two
+// workgroups on one (XCD, index) slot (xlayer.h, err bits 1, 4, 8) mean the
+// call wrote wrong values.  The model then switches to the six-launch
+// blocks for good and XL_RETRY asks the caller to restore its state and run
+// the call again.  The generation is reset before the exchange tags could
+// repeat.  (CMF_XL_FORCE_FAIL=1 reports one failure, to test the fallback.)
+constexpr int XL_RETRY = 2;
 static int xl_check(cmf_model m) {
     if (!m->xl_on) return CMF_OK;
-    int e = 0;
-    CMF_HIP(hipMemcpy(&e, m->xl.err, sizeof(int), hipMemcpyDeviceToHost));
-    if (e == 0) return CMF_OK;
-    CMF_HIP(hipMemset(m->xl.err, 0, sizeof(int)));
-    return fail(e & 4 ? "XCD-partitioned block: more attention positions than its bound (set CMF_XL=0)"
-                      : "XCD-partitioned block: an exchange wait gave up (set CMF_XL=0)");
+    uint32_t w[17] = {};  // gen at 0, err at 16
+    CMF_HIP(hipMemcpy(w, m->xl.gen, sizeof(w), hipMemcpyDeviceToHost));
+    int e = (int)w[16];
+    static bool force = getenv("CMF_XL_FORCE_FAIL") && getenv("CMF_XL_FORCE_FAIL")[0] == '1';
+    if (force) {
+        force = false;
+        e |= 1;
+    }
+    if (e != 0) {
+        CMF_HIP(hipMemset(m->xl.err, 0, sizeof(int)));
+        m->xl_on = false;
+        m->xl_fallbacks += 1;
+        drop_graph(m);
+        return XL_RETRY;
+    }
+    if (w[0] >= XL_GEN_RESET) {
+        xl_reset(m->xl, stream());
+        CMF_HIP(hipStreamSynchronize(stream()));
+    }
+    return CMF_OK;
+}
+// The decode state and tip hidden before a call that may have to run again.
+struct XlSnap {
+    DState st;
+};
+static int xl_save(cmf_model m, XlSnap& sn) {
+    if (!m->xl_on) return CMF_OK;
+    hipStream_t s = stream();
+    CMF_HIP(hipMemcpyAsync(&sn.st, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
+    CMF_HIP(hipMemcpyAsync(m->h_save, m->h_tip, (size_t)m->c.hidden * sizeof(float), hipMemcpyDeviceToDevice, s));
+    CMF_HIP(hipStreamSynchronize(s));
+    return CMF_OK;
+}
+static int xl_restore(cmf_model m, const XlSnap& sn) {
+    hipStream_t s = stream();
+    CMF_HIP(hipMemcpyAsync(m->st, &sn.st, sizeof(DState), hipMemcpyHostToDevice, s));
+    CMF_HIP(hipMemcpyAsync(m->h_tip, m->h_save, (size_t)m->c.hidden * sizeof(float), hipMemcpyDeviceToDevice, s));
+    CMF_HIP(hipStreamSynchronize(s));
+    return CMF_OK;
 }
 
 static int ready(cmf_model m) {
@@ -942,10 +992,26 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
     CMF_HIP(hipMemsetAsync(&m->st->n_out, 0, sizeof(int), s));
     CMF_HIP(hipStreamSynchronize(s));
     CMF_HIP(hipGetLastError());
+    // the XCD prefill attention's placement check: a collision means some
+    // (query block, kv head) went unserved; the prefill runs again on the
+    // grid-indexed variant, which the model keeps from then on
+    // (CMF_PREFILL_PLACEMENT_FAIL=1 reports a collision once, to test this path)
+    int perr = 0;
+    CMF_HIP(hipMemcpy(&perr, m->pf_err, sizeof(int), hipMemcpyDeviceToHost));
+    static const bool force_fail = getenv("CMF_PREFILL_PLACEMENT_FAIL") && getenv("CMF_PREFILL_PLACEMENT_FAIL")[0] == '1';
+    if (force_fail && !m->pf_xcd_off && prefill_attention_fits(c.n_heads, c.n_kv, c.head_dim) && c.n_kv == 8)
+        perr = 1;
+    if (perr && !m->pf_xcd_off) {
+        m->pf_xcd_off = true;
+        CMF_HIP(hipMemset(m->pf_err, 0, sizeof(int)));
+        return cmf_prefill(m, ids, n);
+    }
     m->next_pos_host = n;
     m->prefilled = true;
     return CMF_OK;
 }
+
+int cmf_model_prefill_xcd(cmf_model m) { return m ? (m->pf_xcd_off ? 0 : 1) : CMF_ERR; }
 
 // logits of the tip hidden -> next token (greedy argmax or device sampler)
 static void pick_from_tip(cmf_model m, bool sampling, const cmf_sampler_config* sc, hipStream_t s) {
@@ -1035,7 +1101,7 @@ int cmf_decode_begin(cmf_model m, const cmf_sampler_config* sc, uint64_t seed) {
     return CMF_OK;
 }
 
-int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats) {
+static int decode_rounds_impl(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats) {
     if (ready(m)) return CMF_ERR;
     if (!m->decoding) return fail("decode_rounds: call cmf_decode_begin first");
     if (spec && !m->has_mtp) return fail("decode: speculation needs the MTP head (cmf_model_set_mtp)");
@@ -1124,7 +1190,8 @@ int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats)
     CMF_HIP(hipEventElapsedTime(&ms, e0, e1));
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    if (xl_check(m) != CMF_OK) return CMF_ERR;
+    const int xc = xl_check(m);
+    if (xc != CMF_OK) return xc;
     m->next_pos_host = hs.next_pos;
     m->emitted_host = hs.n_out;
     m->rounds += spec ? n : 0;
@@ -1138,6 +1205,39 @@ int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats)
     m->accepted_host = hs.accepted;
     return CMF_OK;
 }
+
+// Rounds in pieces of at most 2^16 (a piece's generations stay far below
+// the tag reset point, xl_check running between pieces); a piece whose
+// XCD-partitioned blocks failed their check runs again from the state
+// before it on the six-launch blocks.
+int cmf_decode_rounds(cmf_model m, int n, int spec, int k, cmf_gen_stats* stats) {
+    if (!m) return fail("null model");
+    if (n < 0) return fail("decode_rounds: n < 0");
+    cmf_gen_stats tot{};
+    int done = 0;
+    do {
+        const int piece = std::min(n - done, 1 << 16);
+        XlSnap sn{};
+        if (xl_save(m, sn) != CMF_OK) return CMF_ERR;
+        cmf_gen_stats st{};
+        int rc = decode_rounds_impl(m, piece, spec, k, &st);
+        if (rc == XL_RETRY) {
+            if (xl_restore(m, sn) != CMF_OK) return CMF_ERR;
+            rc = decode_rounds_impl(m, piece, spec, k, &st);
+        }
+        if (rc != CMF_OK) return rc == XL_RETRY ? fail("decode: XCD-partitioned blocks failed twice") : rc;
+        tot.generated = st.generated;
+        tot.drafted += st.drafted;
+        tot.accepted += st.accepted;
+        tot.rounds += st.rounds;
+        tot.device_ms += st.device_ms;
+        done += piece;
+    } while (done < n);
+    if (stats) *stats = tot;
+    return CMF_OK;
+}
+
+int cmf_model_xl_fallbacks(cmf_model m) { return m ? m->xl_fallbacks : CMF_ERR; }
 
 int cmf_decode_tokens(cmf_model m, int32_t* out, int cap) {
     if (!m || !out) return fail("decode_tokens: null argument");
@@ -1283,7 +1383,7 @@ int cmf_spec_monitor(cmf_model m, cmf_spec_state* out) {
     return CMF_OK;
 }
 
-int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden, float* logits) {
+static int forward_batch_impl(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden, float* logits) {
     if (ready(m)) return CMF_ERR;
     if (!tokens || b < 1 || b > MAXB || pos0 < 0 || pos0 + b > m->c.max_seq)
         return fail("forward_batch: 1 <= b <= 16 and pos0 + b <= max_seq");
@@ -1301,18 +1401,31 @@ int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float
     hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, pos0 + b);
     CMF_HIP(hipStreamSynchronize(s));
     CMF_HIP(hipGetLastError());
-    if (xl_check(m) != CMF_OK) return CMF_ERR;
+    const int xc = xl_check(m);
+    if (xc != CMF_OK) return xc;
     m->next_pos_host = pos0 + b;
     return CMF_OK;
 }
+// (a call whose XCD-partitioned blocks failed their check runs again on the
+// six-launch blocks: its inputs come from the host)
+int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden, float* logits) {
+    const int rc = forward_batch_impl(m, tokens, b, pos0, hidden, logits);
+    return rc == XL_RETRY ? forward_batch_impl(m, tokens, b, pos0, hidden, logits) : rc;
+}
 
-int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const cmf_sampler_config* sc,
-                    const int32_t* q_ids, const float* q_probs, const int32_t* q_n, const float* uniforms,
-                    int32_t* argmax_out, float* logits_out, int32_t* accepted, int32_t* next_token) {
+static int verify_step_impl(cmf_model m, const int32_t* tokens, int b, int pos0, const cmf_sampler_config* sc,
+                            const int32_t* q_ids, const float* q_probs, const int32_t* q_n, const float* uniforms,
+                            int32_t* argmax_out, float* logits_out, int32_t* accepted, int32_t* next_token) {
     if (ready(m)) return CMF_ERR;
     const int k = b - 1;
     if (!tokens || k < 1 || k > 8 || pos0 < 1 || pos0 + b + 1 > m->c.max_seq)
         return fail("verify_step: 2 <= b <= 9 tokens, 1 <= pos0, pos0 + b < max_seq");
+    // the tip hidden is the trunk output at the committed position - 1: the
+    // verify runs at that position (positions past it would attend over
+    // unwritten KV rows, earlier ones over a stale tip)
+    if (!m->prefilled || pos0 != m->next_pos_host)
+        return fail("verify_step: pos0 must be the committed position (" + std::to_string(m->next_pos_host) +
+                    ", after cmf_prefill / cmf_forward_batch / a decode or verify step)");
     const int V = m->c.vocab, H = m->c.hidden;
     for (int i = 0; i < b; i++)
         if (tokens[i] < 0 || tokens[i] >= V) return fail("verify_step: token id out of range");
@@ -1359,7 +1472,8 @@ int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const c
     CMF_HIP(hipMemcpyAsync(&hs, m->st, sizeof(DState), hipMemcpyDeviceToHost, s));
     CMF_HIP(hipStreamSynchronize(s));
     CMF_HIP(hipGetLastError());
-    if (xl_check(m) != CMF_OK) return CMF_ERR;
+    const int xc = xl_check(m);
+    if (xc != CMF_OK) return xc;
     m->next_pos_host = hs.next_pos;
     m->prefilled = true;
     m->decoding = false;
@@ -1368,6 +1482,24 @@ int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const c
     if (argmax_out)
         for (int i = 0; i < b; i++) argmax_out[i] = hs.argmax[i];
     return CMF_OK;
+}
+
+// (a call whose XCD-partitioned blocks failed their check runs again on the
+// six-launch blocks from the decode state and tip hidden before it)
+int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const cmf_sampler_config* sc,
+                    const int32_t* q_ids, const float* q_probs, const int32_t* q_n, const float* uniforms,
+                    int32_t* argmax_out, float* logits_out, int32_t* accepted, int32_t* next_token) {
+    if (!m) return fail("null model");
+    XlSnap sn{};
+    if (xl_save(m, sn) != CMF_OK) return CMF_ERR;
+    int rc = verify_step_impl(m, tokens, b, pos0, sc, q_ids, q_probs, q_n, uniforms, argmax_out, logits_out, accepted,
+                              next_token);
+    if (rc == XL_RETRY) {
+        if (xl_restore(m, sn) != CMF_OK) return CMF_ERR;
+        rc = verify_step_impl(m, tokens, b, pos0, sc, q_ids, q_probs, q_n, uniforms, argmax_out, logits_out, accepted,
+                              next_token);
+    }
+    return rc == XL_RETRY ? fail("verify_step: XCD-partitioned blocks failed twice") : rc;
 }
 
 int cmf_sparse_distribution(cmf_model m, const float* logits, const cmf_sampler_config* sc, int32_t* ids,

@@ -70,7 +70,15 @@ struct PrefillAttnArgs {
     float* qbuf;
     float* out;
     _Float16* khl;
+    // placement check of the XCD variant (kv head from the XCD a workgroup
+    // runs on): cells [query block][8] take the launch's tag, a collision
+    // sets *perr; cells == nullptr or !allow_xcd: the grid-indexed variant
+    unsigned long long* cells;
+    int* perr;
+    unsigned long long tag;
+    bool allow_xcd;
 };
+constexpr int PREFILL_XCD_CELLS = 8 * 256;  // query blocks of a 256-row chunk x 8 kv heads
 bool prefill_attention_fits(int nh, int nkv, int hd);
 int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);
 // The lexicographic (value, index) maximum step of argmax (sampler.rs:1130-1154

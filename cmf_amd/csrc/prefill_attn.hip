@@ -164,7 +164,11 @@ __global__ __launch_bounds__(256) void k_prefill_kv(const float* __restrict__ kc
 // heads on an MI355X): grid (8 ceil(cnt / PPW)), kv head g = the XCD the
 // workgroup runs on, qb = blockIdx / 8 (the dispatcher deals workgroups to
 // the 8 XCDs in turn), so one head's K / V serves all of its query blocks
-// from that XCD's L2.
+// from that XCD's L2.  That covers each (query block, head) once only while
+// the workgroups go to the XCDs strictly in turn; each workgroup therefore
+// swaps the launch's tag into its cell [qb][g] first, and finding the tag
+// already there (two workgroups on one cell, so some other cell has none)
+// sets *perr: the host then re-runs the prefill on the grid-indexed variant.
 // The 8 waves form two groups: group G takes keys 64 G .. 64 G + 63 of each
 // 128-key tile with a running softmax of its own, wave wl of the group the
 // scores of keys 16 wl .. + 15 and the values of dims 32 wl .. + 31; its K
@@ -175,12 +179,16 @@ __global__ __launch_bounds__(256) void k_prefill_kv(const float* __restrict__ kc
 template <int HPK, bool XCD>
 __global__ __launch_bounds__(512) void k_prefill_attn(const float* __restrict__ qbuf, const int4v* __restrict__ kop,
                                                       const float4v* __restrict__ vop, int npad, int cnt, int p0,
-                                                      int nh, float* __restrict__ out) {
+                                                      int nh, float* __restrict__ out, unsigned long long* cells,
+                                                      int* perr, unsigned long long tag) {
     constexpr int PPW = 16 / HPK;  // positions per workgroup
     constexpr int GK = KT2 / 2;    // keys per group and tile
     const int qb = XCD ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
     const int g = XCD ? (int)(xcc_id() & 7) : (int)blockIdx.y;
     const int t = threadIdx.x, lane = t & 63;
+    if constexpr (XCD) {
+        if (t == 0 && atomicExch(cells + qb * 8 + g, tag) == tag) atomicOr(perr, 1);
+    }
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), G = wave >> 2, wl = wave & 3;
     const int r = lane & 15, s = lane >> 4;
     __shared__ __align__(16) float P[2][16][PST];
@@ -356,9 +364,11 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
                        a.kc, a.vc, a.max_seq, a.p0, a.nh, a.nkv, a.eps, a.qbuf, hq);
     if (!a.out) return CMF_OK;
     const int hpk = a.nh / a.nkv, ppw = 16 / hpk, nqb = (a.cnt + ppw - 1) / ppw;
-    const bool xcd = a.nkv == 8 && xl_device_fits();
+    const bool xcd = a.nkv == 8 && xl_device_fits() && a.allow_xcd && a.cells && a.perr &&
+                     8 * nqb <= PREFILL_XCD_CELLS;
     const dim3 grid = xcd ? dim3(8 * nqb) : dim3(nqb, a.nkv);
-    typedef void (*Kern)(const float*, const int4v*, const float4v*, int, int, int, int, float*);
+    typedef void (*Kern)(const float*, const int4v*, const float4v*, int, int, int, int, float*, unsigned long long*,
+                         int*, unsigned long long);
     Kern k;
     switch (hpk) {
         case 1: k = xcd ? k_prefill_attn<1, true> : k_prefill_attn<1, false>; break;
@@ -372,7 +382,8 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
     float4v* vop = (float4v*)(a.khl + (size_t)a.nkv * npad * 2 * HD);
     hipLaunchKernelGGL(k_prefill_kv, dim3(npad / 64, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, kop,
                        vop);
-    hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a.qbuf, kop, vop, npad, a.cnt, a.p0, a.nh, a.out);
+    hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a.qbuf, kop, vop, npad, a.cnt, a.p0, a.nh, a.out, a.cells, a.perr,
+                       a.tag);
     return CMF_OK;
 }
 

@@ -20,7 +20,11 @@ struct XlBufs {
     float *pa = nullptr, *pb = nullptr;  // per-XCD residual partials [8][MAXB][H] (attention, FFN)
     float *ha = nullptr, *hb = nullptr;  // residual rows [MAXB][H] (ping-pong)
     uint32_t* gen = nullptr;             // sequence generation (tags), bumped by xl_finish
-    int* err = nullptr;                  // nonzero: an exchange wait gave up or a workgroup ran off its XCD
+    // nonzero: bit 1 an exchange wait gave up, bit 4 more attention positions
+    // than the launch's bound, bit 8 two workgroups of a launch claimed one
+    // (XCD, index) slot (a workgroup ran off its XCD)
+    int* err = nullptr;
+    uint32_t* claim = nullptr;           // [8][32] launch tag per (XCD, index) slot
     int e0s = 0, e1s = 0;                // row strides (pairs) of e0 / e1
 };
 
@@ -63,5 +67,9 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
              const int* pbase, int padd, int max_len, const float2* rope, int li, hipStream_t st);
 // hout = hb + sum(pb) (the sequence's output rows); next generation.
 void xl_finish(const XlBufs& b, const XlShape& s, float* hout, int nb, hipStream_t st);
+// Exchange areas and claim slots zeroed, generation 1 (stream-ordered): run
+// before the 32-bit tags (generation * 256 + call) could repeat.
+void xl_reset(const XlBufs& b, hipStream_t st);
+constexpr uint32_t XL_GEN_RESET = 1u << 22;  // generations after which the host resets
 
 }  // namespace cmf

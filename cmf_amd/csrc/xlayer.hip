@@ -44,7 +44,12 @@
 //   2. down projection rows [32 j, 32 j + 32) over the slice -> pb[x].
 // Every wait is bounded: a wait that gives up sets err and the launch still
 // completes (wrong values, reported by the host).  The launch needs all 256
-// workgroups resident at once (one per CU, the host checks 256 CUs).
+// workgroups resident at once (one per CU, the host checks 256 CUs) and
+// dealt to the XCDs in turn: each workgroup first swaps the launch's tag
+// into the claim slot of its (XCD, index); finding the tag there already
+// (two workgroups on one slot, so another slot has none) sets err bit 8,
+// which also ends every wait of the launch early.  The host then switches
+// the model to the six-launch blocks and runs the call again.
 #include <math.h>
 
 #include "common.h"
@@ -112,6 +117,9 @@ __device__ __forceinline__ void xget(F addr, uint32_t tag, float (&out)[N], int*
             atomicOr(err, 1);
             break;
         }
+        // a misplaced launch (err bit 8, set at kernel start) never delivers
+        // some of the values: give up at once instead of after XL_SPIN polls
+        if ((it & 255) == 255 && (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 8)) break;
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
         for (int i = 0; i < N; i++)
@@ -217,6 +225,7 @@ struct XlAArgs {
     const uint32_t* gen;
     int call;
     int* err;
+    uint32_t* claim;  // [8][32] the launch tag of each (XCD, index) slot
     int nb, H, nh, max_seq;
     double eps;
     unsigned long long* stamps;  // tuning builds only (XL_STAMPS)
@@ -239,6 +248,7 @@ struct XlBArgs {
     const uint32_t* gen;
     int call;
     int* err;
+    uint32_t* claim;  // [8][32] the launch tag of each (XCD, index) slot
     int nb, H;
     double eps;
     unsigned long long* stamps;  // tuning builds only (XL_STAMPS)
@@ -278,6 +288,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_attn(XlAArgs a) {
     const int nb = a.nb, H = a.H;
     const uint32_t tag = *a.gen * 256u + (uint32_t)a.call;
     int* err = a.err;
+    if (t == 0 && atomicExch(a.claim + x * XL_WG + j, tag) == tag) atomicOr(err, 8);
 
     // LDS: K / V tiles (positions of this workgroup), queries, scores; the
     // step-4 operand and planes overlay the K tiles
@@ -797,6 +808,7 @@ __global__ __launch_bounds__(XL_T) void k_xl_ffn(XlBArgs a) {
     const int nb = a.nb, H = a.H;
     const uint32_t tag = *a.gen * 256u + (uint32_t)a.call;
     int* err = a.err;
+    if (t == 0 && atomicExch(a.claim + x * XL_WG + j, tag) == tag) atomicOr(err, 8);
 
     __shared__ __align__(16) _Float16 AP[(HL ? 1 : 2) * 4 * 4 * 16 * 8];
     // tile biases [tile][16 rows]: HL rows b the hi plane's, rows 8 + b the
@@ -1138,7 +1150,9 @@ int xl_alloc(XlBufs& b, const XlShape& s, void* (*alloc)(void*, size_t), void* c
     b.hb = (float*)get((size_t)MAXB * s.H * 4);
     b.gen = (uint32_t*)get(256);
     b.err = (int*)(b.gen + 16);
-    if (!b.e0 || !b.e1 || !b.e2 || !b.e3 || !b.pa || !b.pb || !b.ha || !b.hb || !b.gen) return fail("xl: allocation");
+    b.claim = (uint32_t*)get((size_t)XL_XCD * XL_WG * 4);
+    if (!b.e0 || !b.e1 || !b.e2 || !b.e3 || !b.pa || !b.pb || !b.ha || !b.hb || !b.gen || !b.claim)
+        return fail("xl: allocation");
     // tags start at generation 1 (memory starts zeroed)
     const uint32_t one = 1;
     CMF_HIP(hipMemcpy(b.gen, &one, 4, hipMemcpyHostToDevice));
@@ -1174,6 +1188,7 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
     A.gen = b.gen;
     A.call = 2 * li;
     A.err = b.err;
+    A.claim = b.claim;
     A.nb = nb;
     A.H = s.H;
     A.nh = s.nh;
@@ -1211,6 +1226,7 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
     B.gen = b.gen;
     B.call = 2 * li + 1;
     B.err = b.err;
+    B.claim = b.claim;
     B.nb = nb;
     B.H = s.H;
     B.eps = s.eps;
@@ -1220,6 +1236,25 @@ int xl_block(const XlBufs& b, const XlShape& s, const XlAttnW& aw, const XlFfnW&
     if (nb <= 8) hipLaunchKernelGGL((k_xl_ffn<8, 384, true>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, B);
     else hipLaunchKernelGGL((k_xl_ffn<8, 384, false>), dim3(XL_XCD * XL_WG), dim3(XL_T), 0, st, B);
     return CMF_OK;
+}
+
+// Zeroes the exchange areas and the claim slots and sets the generation back
+// to 1 (stream-ordered; the tags of later launches start over).
+__global__ void k_xl_zero(uint64_t* p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0;
+}
+__global__ void k_xl_regen(uint32_t* claim, int nclaim, uint32_t* gen) {
+    for (int i = threadIdx.x; i < nclaim; i += blockDim.x) claim[i] = 0;
+    if (threadIdx.x == 0) *gen = 1u;
+}
+void xl_reset(const XlBufs& b, hipStream_t st) {
+    const size_t n0 = (size_t)XL_XCD * XL_WG * MAXB * b.e0s, n1 = (size_t)XL_XCD * MAXB * b.e1s,
+                 n2 = (size_t)XL_XCD * XL_WG * XL_NQ * XL_E2S, n3 = (size_t)XL_XCD * MAXB * 2 * 128 * 2;
+    hipLaunchKernelGGL(k_xl_zero, dim3(1024), dim3(256), 0, st, b.e0, n0);
+    hipLaunchKernelGGL(k_xl_zero, dim3(256), dim3(256), 0, st, b.e1, n1);
+    hipLaunchKernelGGL(k_xl_zero, dim3(1024), dim3(256), 0, st, b.e2, n2);
+    hipLaunchKernelGGL(k_xl_zero, dim3(256), dim3(256), 0, st, b.e3, n3);
+    hipLaunchKernelGGL(k_xl_regen, dim3(1), dim3(256), 0, st, b.claim, XL_XCD * XL_WG, b.gen);
 }
 
 void xl_finish(const XlBufs& b, const XlShape& s, float* hout, int nb, hipStream_t st) {

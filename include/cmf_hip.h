@@ -219,6 +219,17 @@ int cmf_model_set_mtp(cmf_model m, const float* enorm, const float* hnorm, const
  * six launches per block.  No counterpart in the reference (a backend
  * property, not a seam). */
 int cmf_model_fused_blocks(cmf_model m);
+/* No reference counterpart: 1 while the model's prefill attention may run
+ * the XCD-placed variant (one kv head per XCD, MI355X with 8 kv heads), 0
+ * after its placement check failed once (the prefill was then re-run on the
+ * grid-indexed variant, which the model keeps). */
+int cmf_model_prefill_xcd(cmf_model m);
+/* No reference counterpart: how many calls of the model were run again on
+ * the six-launch blocks because its XCD-partitioned blocks failed their
+ * check (an exchange wait gave up, a position bound was exceeded, or two
+ * workgroups of a launch ran on one XCD slot); after the first, the model
+ * keeps the six-launch blocks (cmf_model_fused_blocks then reports 0). */
+int cmf_model_xl_fallbacks(cmf_model m);
 
 /* ---- MoE FFN (moe_ffn / moe_block) ------------------------------------ */
 
@@ -312,9 +323,10 @@ int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float
  * forward_batch_graph + SpecTail verify (gpu.rs:1455-1497) and the
  * acceptance, commit and rollback that follow it (pipeline.rs:3885-4176,
  * kv_cache.rs:883).  tokens [b] = [t_next, d_0 .. d_{b-2}] (2 <= b <= 9) at
- * positions pos0 .. (pos0 >= 1; the decode state's tip hidden is the trunk
- * output at pos0 - 1: after cmf_prefill, cmf_forward_batch, a decode round
- * or a previous verify step).
+ * positions pos0 .. where pos0 is the committed position (the decode state's
+ * tip hidden is the trunk output at pos0 - 1: after cmf_prefill,
+ * cmf_forward_batch, a decode round or a previous verify step); another
+ * pos0 is an error.
  *   greedy (sc NULL or temperature < 1e-6): a = the longest prefix with
  *     argmax(row i) == d_i (ties to the highest id); *next_token =
  *     argmax(row a);

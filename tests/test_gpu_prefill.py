@@ -107,3 +107,50 @@ def test_prefill_config4_block_shape_equals_oracle(gpu):
     ot, _ = o.decode(otip, n, prompt, 10, spec=True, k=4)
     assert gt.tolist() == ot.tolist()
     g.free()
+
+
+_PLACEMENT_CHILD = r"""
+import sys, json
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import cmf_amd
+from cmf_amd import synth
+from cmf_amd.model import Model
+from oracle import oracle as orc
+cmf_amd.init(0)
+cfg = dict(n_layers=1, hidden=256, n_heads=16, n_kv=8, head_dim=128, inter=512, vocab=2048, max_seq=320,
+           rope_theta=1e6, eps=1e-6)
+sm = synth.synth_model(cfg, seed=27, norm_noise=0.1, sigma=0.05)
+g = Model(sm)
+prompt = synth.ids(28, 300, cfg["vocab"])
+g.prefill(prompt)
+o = orc.OracleModel(sm, threads=8)
+otip = o.prefill(prompt)
+_, tip = g.state()
+k, v = g.kv_export(0, 300)
+rk, rv = o.kv(0)
+rel = lambda a, b: float(np.linalg.norm(a - b) / np.linalg.norm(b))
+print(json.dumps({"xcd": cmf_amd.lib().cmf_model_prefill_xcd(g.h), "tip": rel(tip, otip), "k": rel(k, rk),
+                  "v": rel(v, rv)}))
+"""
+
+
+@pytest.mark.parametrize("forced", [False, True])
+def test_prefill_placement_check_falls_back(gpu, forced):
+    """The XCD-placed prefill attention (8 kv heads) checks that every
+    (query block, kv head) was served once; a failed check (forced from the
+    host here: CMF_PREFILL_PLACEMENT_FAIL=1) re-runs the prefill on the
+    grid-indexed variant, whose results equal the oracle's as well"""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, CMF_PREFILL_PLACEMENT_FAIL="1" if forced else "0")
+    r = subprocess.run([sys.executable, "-c", _PLACEMENT_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["xcd"] == (0 if forced else 1)
+    assert res["tip"] < 1e-4 and res["k"] < 1e-4 and res["v"] < 1e-4

@@ -200,3 +200,50 @@ def test_long_context_matches_six_launch(xl_long, pos0):
         ek, ev = rel_l2(k1[:, pos0:], k0[:, pos0:]), rel_l2(v1[:, pos0:], v0[:, pos0:])
         print(f"  layer {li}: new K rel {ek:.2e} V rel {ev:.2e}", flush=True)
         assert ek < PATH_TOL and ev < PATH_TOL
+
+
+_FALLBACK_CHILD = r"""
+import sys, json
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import cmf_amd
+from cmf_amd import synth
+from cmf_amd.model import Model
+from oracle import oracle as orc
+cmf_amd.init(0)
+XL = dict(n_layers=2, hidden=1024, n_heads=16, n_kv=8, head_dim=128, inter=3072, vocab=4096, max_seq=512,
+          rope_theta=1e6, eps=1e-6)
+sm = synth.accept_model(XL, sigma=0.02, eh_noise=10.0)
+g = Model(sm)
+fused0 = cmf_amd.lib().cmf_model_fused_blocks(g.h)
+prompt = synth.ids(23, 40, XL["vocab"])
+g.prefill(prompt)
+g.decode_begin(seed=0)
+st = g.decode_rounds(4, spec=True, k=4)
+got = g.tokens()
+ot, _ = orc.OracleModel(sm).generate(prompt, len(got) + 6, spec=True, k=4)
+print(json.dumps({"fused0": fused0, "fused1": cmf_amd.lib().cmf_model_fused_blocks(g.h),
+                  "fallbacks": cmf_amd.lib().cmf_model_xl_fallbacks(g.h), "accepted": st.accepted,
+                  "gpu": got.tolist(), "cpu": ot[:len(got)].tolist()}))
+"""
+
+
+def test_failed_check_falls_back_to_six_launch_blocks(gpu):
+    """A call whose XCD-partitioned blocks fail their check (forced from the
+    host here: CMF_XL_FORCE_FAIL=1 reports one failure after the first
+    call) switches the model to the six-launch blocks and runs again from
+    the decode state before it: the tokens (greedy K = 4 rounds with drafts
+    accepted, replayed from a captured graph) still equal the oracle's"""
+    import json
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, CMF_XL_FORCE_FAIL="1")
+    r = subprocess.run([sys.executable, "-c", _FALLBACK_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res["fused0"] == 1 and res["fused1"] == 0 and res["fallbacks"] == 1
+    assert res["accepted"] > 0
+    assert res["gpu"] == res["cpu"]
