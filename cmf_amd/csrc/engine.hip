@@ -1435,7 +1435,7 @@ static int verify_step_impl(cmf_model m, const int32_t* tokens, int b, int pos0,
         if (rc != CMF_OK) return rc;
         if (!q_ids || !q_probs || !q_n || !uniforms) return fail("verify_step: sampling needs q and uniforms");
         for (int j = 0; j < k; j++)
-            if (q_n[j] < 1 || q_n[j] > SPARSE_K_MAX) return fail("verify_step: q_n[j] must be 1..64");
+            if (q_n[j] < 1 || q_n[j] > SPARSE_CAP) return fail("verify_step: q_n[j] must be 1..CMF_SPARSE_CAP");
     }
     if (ensure_out(m, m->c.max_seq + 32)) return CMF_ERR;
     hipStream_t s = stream();
@@ -1446,8 +1446,8 @@ static int verify_step_impl(cmf_model m, const int32_t* tokens, int b, int pos0,
     for (int j = 0; j < k; j++) init.drafts[j] = tokens[1 + j];
     CMF_HIP(hipMemcpyAsync(m->st, &init, sizeof(DState), hipMemcpyHostToDevice, s));
     if (sampling) {
-        CMF_HIP(hipMemcpyAsync(m->sb.qid, q_ids, (size_t)k * SPARSE_K_MAX * 4, hipMemcpyHostToDevice, s));
-        CMF_HIP(hipMemcpyAsync(m->sb.qp, q_probs, (size_t)k * SPARSE_K_MAX * 4, hipMemcpyHostToDevice, s));
+        CMF_HIP(hipMemcpyAsync(m->sb.qid, q_ids, (size_t)k * SPARSE_CAP * 4, hipMemcpyHostToDevice, s));
+        CMF_HIP(hipMemcpyAsync(m->sb.qp, q_probs, (size_t)k * SPARSE_CAP * 4, hipMemcpyHostToDevice, s));
         CMF_HIP(hipMemcpyAsync(m->sb.qn, q_n, (size_t)k * 4, hipMemcpyHostToDevice, s));
         CMF_HIP(hipMemcpyAsync(m->sb.uni, uniforms, (size_t)b * 4, hipMemcpyHostToDevice, s));
     }
@@ -1513,14 +1513,14 @@ int cmf_sparse_distribution(cmf_model m, const float* logits, const cmf_sampler_
     const int V = m->c.vocab;
     int* d_n = m->toks;  // scratch
     CMF_HIP(hipMemcpyAsync(m->logits, logits, (size_t)V * sizeof(float), hipMemcpyHostToDevice, s));
-    sample_distribution(m->sb, m->logits, V, *sc, m->sb.rid + MAXB * SPARSE_K_MAX,
-                        m->sb.rv + MAXB * SPARSE_K_MAX, d_n, s);
+    sample_distribution(m->sb, m->logits, V, *sc, m->sb.rid + MAXB * SPARSE_CAP, m->sb.rv + MAXB * SPARSE_CAP, d_n,
+                        s);
     int n = 0;
     CMF_HIP(hipMemcpyAsync(&n, d_n, sizeof(int), hipMemcpyDeviceToHost, s));
     CMF_HIP(hipStreamSynchronize(s));
-    if (n < 1 || n > SPARSE_K_MAX) return fail("sparse_distribution: bad count");
-    CMF_HIP(hipMemcpy(ids, m->sb.rid + MAXB * SPARSE_K_MAX, n * 4, hipMemcpyDeviceToHost));
-    CMF_HIP(hipMemcpy(probs, m->sb.rv + MAXB * SPARSE_K_MAX, n * 4, hipMemcpyDeviceToHost));
+    if (n < 1 || n > SPARSE_CAP) return fail("sparse_distribution: bad count");
+    CMF_HIP(hipMemcpy(ids, m->sb.rid + MAXB * SPARSE_CAP, n * 4, hipMemcpyDeviceToHost));
+    CMF_HIP(hipMemcpy(probs, m->sb.rv + MAXB * SPARSE_CAP, n * 4, hipMemcpyDeviceToHost));
     CMF_HIP(hipGetLastError());
     return n;
 }

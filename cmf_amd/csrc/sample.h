@@ -10,6 +10,10 @@
 namespace cmf {
 
 constexpr int SPARSE_K_MAX = 64;  // largest top_k the device sampler serves
+// par_topk keeps the top-k and every entry tied with the k-th value, at most
+// 4 k + 64 of them (sampler.rs:515-600): the candidate lists hold that many
+constexpr int SPARSE_CAP = 4 * SPARSE_K_MAX + 64;
+static_assert(SPARSE_CAP % 64 == 0, "candidate lists are whole waves");
 constexpr int SLICE = 4096;       // logits per selection block
 
 // Decode state kept in HBM; kernels read positions from it so a round needs
@@ -32,15 +36,18 @@ enum class SampleMode { Draft, Plain, Accept };
 
 struct SampleBufs {
     int V = 0, nslices = 0;
-    int* cid = nullptr;     // [rows][nslices][K_MAX]
+    int* cid = nullptr;     // [rows][nslices][K_MAX] the slices' top-k, value desc / id asc
     float* cv = nullptr;
+    int* ocnt = nullptr;    // [rows][nslices] ties at the slice's k-th value past its list
+    int* oid = nullptr;     // [rows][nslices][SPARSE_CAP] their ids, index order
     float* smax = nullptr;  // [rows][nslices]
     float* ssum = nullptr;
-    int* rid = nullptr;     // [rows][K_MAX] merged, value desc / id asc
+    int* rid = nullptr;     // [rows][SPARSE_CAP] merged candidates, value desc / id asc
     float* rv = nullptr;
+    int* rn = nullptr;      // [rows] their count
     float* lmax = nullptr;  // [rows]
     float* sum = nullptr;   // [rows]
-    int* qid = nullptr;     // draft distributions [8][K_MAX]
+    int* qid = nullptr;     // draft distributions [8][SPARSE_CAP]
     float* qp = nullptr;
     int* qn = nullptr;      // [8]
     float* uni = nullptr;   // caller uniforms of a verify step [MAXB + 1]
@@ -60,7 +67,8 @@ void sample_rows(SampleBufs& b, const float* logits, int V, int rows, const cmf_
 
 // The sparse distribution of logits row 0 (sparse_distribution_into with the
 // argmax fallback of a fully filtered row): ids ascending into ids[0..n),
-// probabilities into probs, n into *n (all device pointers).
+// probabilities into probs (capacity SPARSE_CAP), n into *n (all device
+// pointers).
 void sample_distribution(SampleBufs& b, const float* logits, int V, const cmf_sampler_config& sc, int* ids,
                          float* probs, int* n, hipStream_t s);
 

@@ -10,6 +10,8 @@ import numpy as np
 
 from . import (CmfError, GenStats, LayerDesc, ModelConfig, SamplerConfig, SpecState, Tensor, _ptr, check, lib)
 
+SPARSE_CAP = 4 * 64 + 64  # CMF_SPARSE_CAP: entries of a sparse distribution list
+
 
 def _tensor(t, keep):
     q = rs = b = None
@@ -138,10 +140,14 @@ class Model:
         keep = []
         qi = qp = qn = u = None
         if q is not None:
-            qi = np.ascontiguousarray(q[0], dtype=np.int32)
-            qp = np.ascontiguousarray(q[1], dtype=np.float32)
+            # rows of CMF_SPARSE_CAP entries (narrower rows are padded)
+            qi = np.zeros((b - 1, SPARSE_CAP), np.int32)
+            qp = np.zeros((b - 1, SPARSE_CAP), np.float32)
+            w = np.asarray(q[0]).shape[1]
+            assert w <= SPARSE_CAP and np.asarray(q[1]).shape == (b - 1, w)
+            qi[:, :w] = q[0]
+            qp[:, :w] = q[1]
             qn = np.ascontiguousarray(q[2], dtype=np.int32)
-            assert qi.shape == (b - 1, 64) and qp.shape == (b - 1, 64)
         if uniforms is not None:
             u = np.zeros(b, np.float32)
             u[: len(uniforms)] = uniforms
@@ -157,8 +163,8 @@ class Model:
 
     def sparse_distribution(self, logits, sampler):
         logits = np.ascontiguousarray(logits, dtype=np.float32)
-        ids = np.empty(64, np.int32)
-        pr = np.empty(64, np.float32)
+        ids = np.empty(SPARSE_CAP, np.int32)
+        pr = np.empty(SPARSE_CAP, np.float32)
         n = lib().cmf_sparse_distribution(self.h, _ptr(logits), C.byref(sampler), _ptr(ids), _ptr(pr))
         if n <= 0:
             check(n)

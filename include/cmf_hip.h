@@ -316,8 +316,11 @@ int cmf_decode_tokens(cmf_model m, int32_t* out, int cap);
  * [b][hidden] and logits [b][vocab] (either may be NULL). */
 int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float* hidden,
                       float* logits);
-/* Largest sparse distribution the device sampler holds (its top_k bound). */
+/* Largest top_k the device sampler serves. */
 #define CMF_SPARSE_K_MAX 64
+/* Capacity of a sparse distribution list: par_topk keeps the top k and every
+ * entry tied with the k-th value, at most 4 k + 64 (sampler.rs:515-600). */
+#define CMF_SPARSE_CAP (4 * CMF_SPARSE_K_MAX + 64)
 
 /* One verify step of graph_spec_step with the caller's drafts: the
  * forward_batch_graph + SpecTail verify (gpu.rs:1455-1497) and the
@@ -332,7 +335,7 @@ int cmf_forward_batch(cmf_model m, const int32_t* tokens, int b, int pos0, float
  *     argmax(row a);
  *   sampled: spec_accept_or_correct_sparse (sampler.rs:683-711) of each
  *     draft against the caller's draft distributions q_ids / q_probs
- *     [b-1][CMF_SPARSE_K_MAX] (ids ascending, q_n[j] entries) and the
+ *     [b-1][CMF_SPARSE_CAP] (ids ascending, q_n[j] entries) and the
  *     row's sparse distribution p; the uniforms [b] are consumed in the
  *     reference's order (one per tested draft, one for the correction or
  *     for the draw from row a); *next_token = the correction or that draw.
@@ -346,7 +349,7 @@ int cmf_verify_step(cmf_model m, const int32_t* tokens, int b, int pos0, const c
                     int32_t* argmax_out, float* logits_out, int32_t* accepted, int32_t* next_token);
 /* sparse_distribution_into (sampler.rs:440-514) of one logits row [vocab]
  * (host) on the device sampler: ids ascending and their probabilities
- * (capacity CMF_SPARSE_K_MAX); returns the count (>= 1: a fully filtered
+ * (capacity CMF_SPARSE_CAP); returns the count (>= 1: a fully filtered
  * row gives its argmax with probability 1, as the decode loop does). */
 int cmf_sparse_distribution(cmf_model m, const float* logits, const cmf_sampler_config* sc, int32_t* ids,
                             float* probs);

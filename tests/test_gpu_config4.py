@@ -89,12 +89,15 @@ def test_sparse_distribution_full_vocab(gpu, seed, scale):
     assert V - 3 in ids.tolist()
 
 
-@pytest.mark.parametrize("levels", [2, 8, 64])
-def test_sparse_distribution_tied_logits(gpu, levels):
-    """logits on a coarse grid over 151936 ids (hundreds of ties at the top
-    of every slice: more keys than a rank sort takes stay in play, and the
-    k-th value is shared): top_k 40, top_p 1, min_p 0, T 1 keeps the 40
-    best by (value desc, id asc); ids equal that, p = softmax over them"""
+@pytest.mark.parametrize("levels,k,tp", [(2, 40, 1.0), (8, 40, 1.0), (8, 40, 0.9), (64, 40, 1.0), (8, 64, 0.9)])
+def test_sparse_distribution_tied_logits(gpu, levels, k, tp):
+    """logits on a coarse grid over 151936 ids, ties at the k-th value:
+    levels 8 (about 200 ids share the top value), 64 (a few share the k-th),
+    2 (tens of thousands tied: the 4 k + 64 cap, first in index order).
+    par_topk keeps every entry tied with the k-th (sampler.rs:515-600), so
+    the ids equal the oracle's or_sparse_distribution and the
+    probabilities agree within 1e-5"""
+    import ctypes as C
     import cmf_amd
     from cmf_amd import synth
     from cmf_amd.model import Model
@@ -103,14 +106,18 @@ def test_sparse_distribution_tied_logits(gpu, levels):
                rope_theta=1e6, eps=1e-6)
     sm = synth.synth_model(cfg, seed=9, mtp=False)
     g = Model(sm)
-    sg = cmf_amd.SamplerConfig(temperature=1.0, top_k=40, top_p=1.0, min_p=0.0, repetition_penalty=1.0)
+    sg = cmf_amd.SamplerConfig(temperature=1.0, top_k=k, top_p=tp, min_p=0.0, repetition_penalty=1.0)
+    so = orc.SamplerCfg(1.0, tp, k, 1.0, 0.0, 0.0)
     lg = np.floor(synth.normal(7 + levels, V) * (levels / 8)).astype(np.float32)
     ids, pr = g.sparse_distribution(lg, sg)
     g.free()
-    order = np.lexsort((np.arange(V), -lg))[:40]
-    want = np.sort(order)
-    print(f"levels {levels}: top value {lg.max()} x{int((lg == lg.max()).sum())}, "
-          f"k-th value {lg[order[-1]]} x{int((lg == lg[order[-1]]).sum())}", flush=True)
-    assert ids.tolist() == want.tolist()
-    e = np.exp(lg[want].astype(np.float64) - lg.max())
-    assert np.allclose(pr, e / e.sum(), rtol=1e-5, atol=1e-7)
+    oid = np.empty(4 * 256 + 64, np.uint32)
+    opr = np.empty(4 * 256 + 64, np.float32)
+    P = lambda a: a.ctypes.data_as(C.c_void_p)
+    n = orc.lib().or_sparse_distribution(P(lg), V, C.byref(so), None, 0, P(oid), P(opr))
+    kth = np.sort(lg)[::-1][k - 1]
+    print(f"levels {levels} k {k} top_p {tp}: k-th value {kth}, {int((lg >= kth).sum())} ids >= it; "
+          f"device n={len(ids)} oracle n={n}", flush=True)
+    assert (lg >= kth).sum() > k
+    assert ids.tolist() == oid[:n].astype(np.int32).tolist()
+    assert np.allclose(pr, opr[:n], rtol=1e-5, atol=1e-7)

@@ -126,3 +126,45 @@ def test_spec_accept_dense_target_distribution():
         cnt[d if res < 0 else res] += 1
     assert cnt[2] == 0
     assert np.abs(cnt / trials - p).sum() < 0.012
+
+
+def _ties_chain(logits, t, top_k, top_p, min_p):
+    """brute force of par_topk's tie rule (sampler.rs:515-600): every entry
+    >= the k-th largest value, the first 4 k + 64 of them in index order,
+    then the chain of sparse_distribution_into (sampler.rs:440-514) in f64"""
+    z = logits.astype(np.float64)
+    kth = np.sort(z)[::-1][top_k - 1]
+    cand = [i for i in range(len(z)) if z[i] >= kth][: 4 * top_k + 64]
+    cand.sort(key=lambda i: (-z[i], i))
+    e = np.exp((z - z.max()) / t)
+    keep, cum = [], 0.0
+    for i in cand:
+        if min_p > 0 and e[i] < min_p:
+            continue
+        keep.append(i)
+        cum += e[i] / e.sum()
+        if 0 < top_p < 1 and cum >= top_p:
+            break
+    keep = np.array(sorted(keep))
+    q = e[keep] / e[keep].sum()
+    return keep, q
+
+
+@pytest.mark.parametrize("levels,k,tp", [(8, 40, 1.0), (8, 40, 0.9), (64, 20, 1.0), (2, 10, 1.0), (2, 64, 0.5)])
+def test_sparse_chain_keeps_ties_at_the_kth_value(levels, k, tp):
+    """logits on a coarse grid: every entry tied with the k-th value stays a
+    candidate (levels 8, 64: tens to hundreds of ties), at most 4 k + 64 of
+    them in index order (levels 2: thousands tied at the top)"""
+    L = orc.lib()
+    rng = np.random.default_rng(100 + levels)
+    n = 20000
+    logits = np.floor(rng.standard_normal(n) * (levels / 8)).astype(np.float32)
+    cfg = orc.SamplerCfg(1.0, tp, k, 1.0, 0.0, 0.0)
+    ids = np.empty(4 * 256 + 64, dtype=np.uint32)
+    pr = np.empty(4 * 256 + 64, dtype=np.float32)
+    m = L.or_sparse_distribution(_p(logits), n, C.byref(cfg), None, 0, _p(ids), _p(pr))
+    want_ids, want_p = _ties_chain(logits, 1.0, k, tp, 0.0)
+    kth = np.sort(logits)[::-1][k - 1]
+    assert (logits >= kth).sum() > k  # ties past the k-th place exist
+    assert ids[:m].tolist() == want_ids.tolist()
+    assert np.allclose(pr[:m], want_p, rtol=2e-5, atol=1e-7)
