@@ -341,12 +341,15 @@ __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ p
 }
 
 // Operand planes of the GEMM (grown on demand).
-static uint8_t* g_gemm_planes = nullptr;
-static size_t g_gemm_cap = 0;
-static float* g_gemm_xs = nullptr;
-static size_t g_gemm_xs_cap = 0;
-static float* g_gemm_part = nullptr;  // split-K partial sums
-static size_t g_gemm_part_cap = 0;
+// operand planes, row scales and split-K partial sums, grown on demand, per
+// host thread (each thread runs on its own stream); a GEMM is never part of
+// a captured graph (the decode rounds' batches are <= 16 rows)
+static thread_local uint8_t* g_gemm_planes = nullptr;
+static thread_local size_t g_gemm_cap = 0;
+static thread_local float* g_gemm_xs = nullptr;
+static thread_local size_t g_gemm_xs_cap = 0;
+static thread_local float* g_gemm_part = nullptr;  // split-K partial sums
+static thread_local size_t g_gemm_part_cap = 0;
 
 // K parts for a grid of base workgroups over nsteps K steps: doubled while
 // the grid is below one workgroup per CU (256), at least 4 steps a part.

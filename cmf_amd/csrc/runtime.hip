@@ -38,14 +38,28 @@ static uint8_t* g_scratch_ptr[NOALLOC_MAX_DEV] = {};
 static std::mutex g_mu;
 static bool g_init = false;
 static int g_dev = 0;
-static hipStream_t g_stream = nullptr;
 
-hipStream_t stream() { return g_stream; }
+// One HIP stream per host thread (the reference's GPU gate is thread-local,
+// gpu.rs:18-46, 978-1000): a thread's first call makes the library's device
+// current on it and creates its stream (default priority); calls of
+// different threads run on their own streams with their own seam and GEMM
+// scratch, and the calls on one model handle are the caller's to serialise
+// (as the reference FFI's per handle).  A thread's stream and scratch stay
+// until the process ends.
+static thread_local hipStream_t t_stream = nullptr;
+hipStream_t stream() {
+    if (!t_stream && g_init) {
+        if (hipSetDevice(g_dev) != hipSuccess || hipStreamCreateWithFlags(&t_stream, hipStreamNonBlocking) != hipSuccess)
+            t_stream = nullptr;
+    }
+    return t_stream;
+}
 int device() { return g_dev; }
 
 int ensure_init() {
-    if (g_init) return CMF_OK;
-    return cmf_init(0);
+    if (!g_init && cmf_init(0) != CMF_OK) return CMF_ERR;
+    if (!stream()) return fail("no HIP stream for this thread");
+    return CMF_OK;
 }
 
 static float f16_to_f32_host(uint16_t h) {
@@ -219,8 +233,14 @@ struct SeamScratch {
     int* a8idx = nullptr;
     float* a8val = nullptr;
     size_t a8_cap = 0;
+    float* gu = nullptr;   // cmf_ffn / cmf_moe_block_jobs: gate | up rows
+    size_t gu_cap = 0;
+    float* d = nullptr;    // cmf_moe_block_jobs: the jobs' down outputs
+    size_t d_cap = 0;
+    float* w = nullptr;    // ... their blend weights
+    size_t w_cap = 0;
 };
-static SeamScratch g_ss;
+static thread_local SeamScratch g_ss;  // (per host thread, as the stream)
 
 static int grow(void** p, size_t* cap, size_t need) {
     if (*cap >= need) return CMF_OK;
@@ -310,7 +330,6 @@ int cmf_init(int dev) {
     CMF_HIP(hipGetDeviceProperties(&p, dev));
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return fail(std::string("libcmfhip is built for gfx950, device is ") + p.gcnArchName);
-    CMF_HIP(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
     if (dev < NOALLOC_MAX_DEV) {
         // this device's copy of the no-allocation workspace (device current)
         const hipError_t e = hipGetSymbolAddress((void**)&g_scratch_ptr[dev], HIP_SYMBOL(scratch));
@@ -321,12 +340,13 @@ int cmf_init(int dev) {
     }
     g_dev = dev;
     g_init = true;
+    if (!stream()) return fail("cmf_init: stream creation failed");
     return CMF_OK;
 }
 
 int cmf_sync(void) {
     if (!g_init) return fail("cmf_init not called");
-    CMF_HIP(hipStreamSynchronize(g_stream));
+    CMF_HIP(hipStreamSynchronize(stream()));
     return CMF_OK;
 }
 
@@ -482,15 +502,17 @@ int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b,
         return fail("ffn: shape mismatch");
     if (w1->w.dtype != w3->w.dtype) return CMF_DECLINED;
     hipStream_t st = stream();
-    // device buffers: x [m][hidden], g/u [m][2*inter], planes, out [m][hidden]
-    float *dx = nullptr, *dgu = nullptr, *dy = nullptr, *dxs = nullptr;
-    uint8_t* pl = nullptr;
+    // device buffers (the thread's grow-only seam scratch): x [m][hidden],
+    // g/u [m][2*inter], planes, out [m][hidden]
     const size_t pb = std::max(prep_bytes(w1->w), prep_bytes(w2->w));
-    CMF_HIP(hipMalloc(&dx, (size_t)MAXB * hidden * sizeof(float)));
-    CMF_HIP(hipMalloc(&dgu, (size_t)MAXB * 2 * inter * sizeof(float)));
-    CMF_HIP(hipMalloc(&dy, (size_t)MAXB * hidden * sizeof(float)));
-    CMF_HIP(hipMalloc(&dxs, 64 * sizeof(float)));
-    CMF_HIP(hipMalloc(&pl, pb));
+    if (grow((void**)&g_ss.x, &g_ss.x_cap, (size_t)MAXB * hidden * sizeof(float)) != CMF_OK ||
+        grow((void**)&g_ss.gu, &g_ss.gu_cap, (size_t)MAXB * 2 * inter * sizeof(float)) != CMF_OK ||
+        grow((void**)&g_ss.y, &g_ss.y_cap, (size_t)MAXB * hidden * sizeof(float)) != CMF_OK ||
+        grow((void**)&g_ss.planes, &g_ss.planes_cap, pb) != CMF_OK)
+        return CMF_ERR;
+    if (!g_ss.xs) CMF_HIP(hipMalloc(&g_ss.xs, 64 * sizeof(float)));
+    float *dx = g_ss.x, *dgu = g_ss.gu, *dy = g_ss.y, *dxs = g_ss.xs;
+    uint8_t* pl = g_ss.planes;
     int rc = CMF_OK;
     for (int b0 = 0; b0 < b && rc == CMF_OK; b0 += MAXB) {
         const int m = std::min(MAXB, b - b0);
@@ -511,11 +533,6 @@ int cmf_ffn(cmf_weight w1, cmf_weight w3, cmf_weight w2, const float* xs, int b,
         CMF_HIP(hipMemcpyAsync(out + (size_t)b0 * hidden, dy, (size_t)m * hidden * 4, hipMemcpyDeviceToHost, st));
     }
     CMF_HIP(hipStreamSynchronize(st));
-    (void)hipFree(dx);
-    (void)hipFree(dgu);
-    (void)hipFree(dy);
-    (void)hipFree(dxs);
-    (void)hipFree(pl);
     if (rc == CMF_OK) CMF_HIP(hipGetLastError());
     return rc;
 }
@@ -575,20 +592,19 @@ int cmf_moe_block_jobs(const cmf_moe_job* jobs, int njobs, float* out) {
     // weights, y, caller scales (3 x rows_pad), planes, xs scales
     const size_t pb = std::max(prep_bytes(jobs[0].gate->w), prep_bytes(jobs[0].down->w));
     const size_t rsn = (size_t)std::max(jobs[0].gate->w.rows_pad, jobs[0].down->w.rows_pad);
-    float *dx = nullptr, *dgu = nullptr, *dd = nullptr, *dw = nullptr, *dy = nullptr, *drs = nullptr, *dxs = nullptr;
-    uint8_t* pl = nullptr;
+    // (the thread's grow-only seam scratch)
+    if (grow((void**)&g_ss.x, &g_ss.x_cap, (size_t)2 * njobs * cols * 4) != CMF_OK ||
+        grow((void**)&g_ss.gu, &g_ss.gu_cap, (size_t)2 * inter * 4) != CMF_OK ||
+        grow((void**)&g_ss.d, &g_ss.d_cap, (size_t)njobs * hidden * 4) != CMF_OK ||
+        grow((void**)&g_ss.w, &g_ss.w_cap, (size_t)njobs * 4) != CMF_OK ||
+        grow((void**)&g_ss.y, &g_ss.y_cap, (size_t)hidden * 4) != CMF_OK ||
+        grow((void**)&g_ss.rs, &g_ss.rs_cap, 3 * rsn * 4) != CMF_OK ||
+        grow((void**)&g_ss.planes, &g_ss.planes_cap, pb) != CMF_OK)
+        return CMF_ERR;
+    if (!g_ss.xs) CMF_HIP(hipMalloc(&g_ss.xs, 64 * sizeof(float)));
+    float *dx = g_ss.x, *dgu = g_ss.gu, *dd = g_ss.d, *dw = g_ss.w, *dy = g_ss.y, *drs = g_ss.rs, *dxs = g_ss.xs;
+    uint8_t* pl = g_ss.planes;
     int rc = CMF_OK;
-    auto al = [&](void** p, size_t n) {
-        if (rc == CMF_OK && hipMalloc(p, n) != hipSuccess) rc = fail("moe_block_jobs: hipMalloc failed");
-    };
-    al((void**)&dx, (size_t)2 * njobs * cols * 4);
-    al((void**)&dgu, (size_t)2 * inter * 4);
-    al((void**)&dd, (size_t)njobs * hidden * 4);
-    al((void**)&dw, (size_t)njobs * 4);
-    al((void**)&dy, (size_t)hidden * 4);
-    al((void**)&drs, 3 * rsn * 4);
-    al((void**)&dxs, 64 * 4);
-    al((void**)&pl, pb);
     std::vector<float> ws(njobs);
     for (int j = 0; j < njobs && rc == CMF_OK; j++) {
         const cmf_moe_job& J = jobs[j];
@@ -629,8 +645,6 @@ int cmf_moe_block_jobs(const cmf_moe_job* jobs, int njobs, float* out) {
             rc = fail("moe_block_jobs: download failed");
     }
     (void)hipStreamSynchronize(st);
-    for (void* p : {(void*)dx, (void*)dgu, (void*)dd, (void*)dw, (void*)dy, (void*)drs, (void*)dxs, (void*)pl})
-        if (p) (void)hipFree(p);
     if (rc == CMF_OK) CMF_HIP(hipGetLastError());
     return rc;
 }
