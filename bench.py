@@ -178,19 +178,45 @@ def _cpu_rate(fn, min_s=0.5):
             return dt / n
 
 
+def host_cpus():
+    """(threads this process may use, physical cores behind them, logical
+    CPUs of the host).  The pool is capped at OMP_NUM_THREADS when set (the
+    GPU box sets it to the box's CPU share)."""
+    aff = sorted(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    use = aff[:cap] if cap > 0 else aff
+    cores = set()
+    for cpu in use:
+        try:
+            base = f"/sys/devices/system/cpu/cpu{cpu}/topology/"
+            with open(base + "physical_package_id") as f:
+                pkg = f.read().strip()
+            with open(base + "core_id") as f:
+                cores.add((pkg, f.read().strip()))
+        except OSError:
+            cores.add(("?", str(cpu)))
+    return len(use), len(cores), os.cpu_count() or len(aff)
+
+
 def cpu_baseline(sm, cpu_state, prompt, args):
     """The reference's CPU path restated (the C oracle) on the host cores:
-    spec decode from the GPU's prefilled state under both matvec contracts of
-    the reference (exact, CMF_SDOT=0; a8w8, split_act + integer dots, its
-    default on hosts with integer dot instructions), and the BASELINE configs'
-    CPU kernels (configs 1-3, 5).  value = the exact-contract decode."""
+    spec decode from the GPU's prefilled state with the verify rows batched
+    (pipeline.rs:4275-4505) under both matvec contracts of the reference:
+    a8w8 (split_act + integer dots) through the AVX-512 VNNI timing arm --
+    the reference's default on an x86 host with VNNI, and `value` -- and the
+    exact contract (CMF_SDOT=0), whose tokens the GPU's must equal.  Beside
+    them the BASELINE configs' CPU kernels (configs 1-3, 5) under both."""
     from oracle import oracle as orc
     from cmf_amd import synth
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
-    n_cpu = 6
+    threads, phys, logical = host_cpus()
+    fast = orc.fast_supported()
     legs = {}
-    for contract in ("exact", "a8w8"):
-        o = orc.OracleModel(sm, threads=threads, a8w8=contract == "a8w8")
+    toks_exact = None
+    for contract, n_cpu in (("a8w8", 24), ("exact", 6)):
+        if contract == "a8w8" and not fast:
+            continue
+        o = orc.OracleModel(sm, threads=threads, a8w8=contract == "a8w8", fast=contract == "a8w8",
+                            batch_verify=True)
         for li, (kk, vv) in enumerate(cpu_state["kv"]):
             o.import_kv(li, kk, vv)
         o.import_kv(-1, *cpu_state["mtp"])
@@ -201,42 +227,44 @@ def cpu_baseline(sm, cpu_state, prompt, args):
                           "s": round(tcpu, 1)}
         if contract == "exact":
             toks_exact = ct
-    # BASELINE configs 1-3 and 5 on the CPU path (exact contract; a8w8 at M=1)
+    # BASELINE configs 1-3 and 5 on the CPU path, exact and a8w8 (VNNI arm)
     kern = []
+
+    def both(config, name, t, x, nbytes):
+        for a8 in ((False, True) if fast else (False,)):
+            sec = _cpu_rate(lambda: orc.matmat(t, x, threads=threads, fast=a8))
+            e = {"config": config, "kernel": f"{name} ({'a8w8 VNNI' if a8 else 'exact'})", "us": round(sec * 1e6, 1)}
+            if nbytes:
+                e["GB/s"] = round(nbytes / sec / 1e9, 2)
+            kern.append(e)
+
     t1 = synth.q8_uniform(11, 4096, 4096)
-    x1 = synth.normal(7, 4096).reshape(1, 4096)
-    for a8 in (False, True):
-        sec = _cpu_rate(lambda: orc.matmat(t1, x1, threads=threads, a8w8=a8))
-        kern.append({"config": 1, "kernel": f"q8 4096x4096 M=1 ({'a8w8' if a8 else 'exact'})",
-                     "us": round(sec * 1e6, 1), "GB/s": round((4096 * 4096 + 4096 * 4) / sec / 1e9, 2)})
+    both(1, "q8 4096x4096 M=1", t1, synth.normal(7, 4096).reshape(1, 4096), 4096 * 4096 + 4096 * 4)
     t2 = synth.q4t_uniform(31 + 12288, 12288, 4096)
-    for m, a8 in ((1, False), (1, True), (8, False)):
-        x2 = synth.normal(7, m * 4096).reshape(m, 4096)
-        sec = _cpu_rate(lambda: orc.matmat(t2, x2, threads=threads, a8w8=a8))
-        kern.append({"config": 2, "kernel": f"q4t 12288x4096 M={m} ({'a8w8' if a8 else 'exact'})",
-                     "us": round(sec * 1e6, 1), "GB/s": round(q4_bytes(12288, 4096, m, "q4t") / sec / 1e9, 2)})
+    for m in (1, 8):
+        both(2, f"q4t 12288x4096 M={m}", t2, synth.normal(7, m * 4096).reshape(m, 4096),
+             q4_bytes(12288, 4096, m, "q4t"))
     t3 = synth.q4tp_uniform(41 + 12288, 12288, 4096)
-    x3 = synth.normal(7, 5 * 4096).reshape(5, 4096)
-    sec = _cpu_rate(lambda: orc.matmat(t3, x3, threads=threads))
-    kern.append({"config": 3, "kernel": "q4tp 12288x4096 M=5 (exact)", "us": round(sec * 1e6, 1),
-                 "GB/s": round(q4_bytes(12288, 4096, 5, "q4tp") / sec / 1e9, 2)})
+    both(3, "q4tp 12288x4096 M=5", t3, synth.normal(7, 5 * 4096).reshape(5, 4096), q4_bytes(12288, 4096, 5, "q4tp"))
     ne, hidden, inter, top_k = 128, 2048, 768, 8
     ex = [{"gate": synth.q4t_uniform(900 + 3 * e, inter, hidden), "up": synth.q4t_uniform(901 + 3 * e, inter, hidden),
            "down": synth.q4t_uniform(902 + 3 * e, hidden, inter)} for e in range(ne)]
     xm = synth.normal(5001, 5 * hidden).reshape(5, hidden)
     lg = synth.normal(5002, 5 * ne).reshape(5, ne)
     sec = _cpu_rate(lambda: orc.moe_ffn_rows(ex, top_k, lg, xm, threads=threads))
-    t8 = synth.q8_uniform(5003, 4096, 2048)
-    x8 = synth.normal(7, 5 * 2048).reshape(5, 2048)
-    sec8 = _cpu_rate(lambda: orc.matmat(t8, x8, threads=threads))
-    kern.append({"config": 5, "kernel": "MoE FFN M=5 (128 q4t experts, top-8) + q8 4096x2048 M=5 (exact)",
-                 "us": round((sec + sec8) * 1e6, 1)})
-    base = {"value": legs["exact"]["tok/s"], "unit": "tok/s", "cores": threads, "threads": threads,
-            "kind": "port",
-            "sample": f"C oracle (the reference's CPU path restated, OpenMP over {threads} host threads): "
-                      f"{legs['exact']['tokens']} tokens of spec decode (K={args.k}, {legs['exact']['rounds']} "
-                      f"rounds, exact contract) from the GPU's prefilled {args.ctx}-token state in "
-                      f"{legs['exact']['s']} s; the a8w8 contract and the configs' kernels beside it",
+    kern.append({"config": 5, "kernel": "MoE FFN M=5 (128 q4t experts, top-8; exact)", "us": round(sec * 1e6, 1)})
+    both(5, "q8 4096x2048 M=5 projection", synth.q8_uniform(5003, 4096, 2048),
+         synth.normal(7, 5 * 2048).reshape(5, 2048), 4096 * 2048)
+    lead = "a8w8" if "a8w8" in legs else "exact"
+    L = legs[lead]
+    base = {"value": L["tok/s"], "unit": "tok/s", "cores": threads, "threads": threads,
+            "host_physical_cores": phys, "host_logical_cpus": logical, "kind": "port",
+            "sample": f"C oracle (the reference's CPU path restated; OpenMP over {threads} threads on {phys} "
+                      f"physical cores of a {logical}-CPU host): {L['tokens']} tokens of spec decode (K={args.k}, "
+                      f"{L['rounds']} rounds, verify rows batched, "
+                      f"{'a8w8 contract on the AVX-512 VNNI kernels' if lead == 'a8w8' else 'exact contract'}) "
+                      f"from the GPU's prefilled {args.ctx}-token state in {L['s']} s; the exact contract and "
+                      f"the configs' kernels beside it",
             "contracts": legs, "kernels": kern}
     return base, toks_exact
 

@@ -35,14 +35,22 @@ static void add_rms_norm(float* h, const float* d, const float* w, int n, double
 }
 
 /* attention.rs:606-624: qk-norm, inv computed in f64 then cast. */
-/* The model's quantized matvecs under the contract it runs: exact (the
+/* The model's quantized matmuls under the contract it runs: exact (the
  * default, CMF_SDOT=0) or a8w8 (split_act + integer dots, qtensor.rs:9237-9281,
  * the reference's default on hosts with integer dot instructions); f32
- * weights (a dense router) always take the exact path. */
-static void mv(const or_model* m, const or_qt* w, const float* x, float* out) {
-    if (m->a8w8 && w->dtype != OR_F32) or_matvec_a8w8(w, x, out, m->threads);
-    else or_matvec(w, x, out, m->threads);
+ * weights (a dense router) always take the exact path.  m->fast routes the
+ * a8w8 matmuls through the AVX-512 VNNI timing arm (fast.c), which returns
+ * the scalar arm's values bit for bit.  xs / out: [b][cols] / [b][rows]. */
+static void mm(const or_model* m, const or_qt* w, const float* xs, int b, float* out) {
+    if (m->a8w8 && w->dtype != OR_F32) {
+        if (!(m->fast && or_fast_matmat_a8w8(w, xs, b, out, m->threads) == 0))
+            or_matmat_a8w8(w, xs, b, out, m->threads);
+    } else {
+        or_matmat(w, xs, b, out, m->threads);
+    }
 }
+
+static void mv(const or_model* m, const or_qt* w, const float* x, float* out) { mm(m, w, x, 1, out); }
 
 static void rmsnorm_head(float* x, const float* w, int n, double eps) {
     double ss = 0.0;
@@ -67,8 +75,10 @@ static void rope(float* x, int pos, const float* inv_freq, int half) {
     }
 }
 
-/* attention.rs:150-182 dot_f32_avx2 */
-static float dot_f32(const float* a, const float* b, int n) {
+/* attention.rs:150-182 dot_f32_avx2.  The clones only let the compiler use
+ * hardware fma and wider registers; the operations and their order are the
+ * same in every clone (no contraction, no reassociation). */
+CLONES static float dot_f32(const float* a, const float* b, int n) {
     float s0[8] = {0}, s1[8] = {0};
     int j = 0;
     for (; j + 16 <= n; j += 16)
@@ -98,109 +108,159 @@ void or_embed(const or_model* m, uint32_t id, float* out) {
     for (int i = 0; i < H; i++) out[i] = (float)q[i] * rs;
 }
 
-/* qwen_attention (attention.rs:1005-1027) for one position over one KV. */
-static void attention(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq,
-                      const float* x, int pos, float* out, int compute_out) {
+/* finish_projection (attention.rs:818-890: qk-norm then RoPE), the KV
+ * append (kv_cache.rs:366-411) and, when ao != NULL, attend_group
+ * (kv_cache.rs:521-690) over the stored rows into ao [n_heads * head_dim].
+ * q / k / v: this position's projections (q and k are changed in place).
+ * Heads are independent, so they are spread over the model's threads. */
+/* o[d] = fma(w, v[d], o[d]) (attend_group's value accumulation) */
+CLONES static void axpy(float w, const float* v, float* o, int n) {
+    for (int d = 0; d < n; d++) o[d] = fmaf(w, v[d], o[d]);
+}
+
+static void attend_row(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq, float* q,
+                       float* k, const float* v, int pos, float* ao) {
     const or_cfg* c = &m->cfg;
     int nh = c->n_heads, nkv = c->n_kv, hd = c->head_dim, S = c->max_seq;
-    float* q = (float*)malloc(sizeof(float) * (size_t)(nh * hd));
-    float* k = (float*)malloc(sizeof(float) * (size_t)(nkv * hd));
-    float* v = (float*)malloc(sizeof(float) * (size_t)(nkv * hd));
-    mv(m, &L->wq, x, q);
-    mv(m, &L->wk, x, k);
-    mv(m, &L->wv, x, v);
-    /* finish_projection, attention.rs:818-890: qk-norm then RoPE */
     for (int h = 0; h < nh; h++) rmsnorm_head(q + h * hd, L->q_norm, hd, c->eps);
     for (int g = 0; g < nkv; g++) rmsnorm_head(k + g * hd, L->k_norm, hd, c->eps);
     for (int h = 0; h < nh; h++) rope(q + h * hd, pos, inv_freq, hd / 2);
     for (int g = 0; g < nkv; g++) rope(k + g * hd, pos, inv_freq, hd / 2);
-    /* kv_cache.rs:366-411 append */
     int p0 = kv->len;
     for (int g = 0; g < nkv; g++) {
         memcpy(kv->k + ((size_t)g * S + p0) * hd, k + g * hd, sizeof(float) * (size_t)hd);
         memcpy(kv->v + ((size_t)g * S + p0) * hd, v + g * hd, sizeof(float) * (size_t)hd);
     }
     kv->len = p0 + 1;
-    if (compute_out) {
-        int stored = kv->len, hpk = nh / nkv;
-        float scale = 1.0f / sqrtf((float)hd);
-        float* ao = (float*)calloc((size_t)(nh * hd), sizeof(float));
+    if (!ao) return;
+    int stored = kv->len, hpk = nh / nkv;
+    float scale = 1.0f / sqrtf((float)hd);
+    memset(ao, 0, sizeof(float) * (size_t)(nh * hd));
+    int nt = m->threads > 1 ? (m->threads < nh ? m->threads : nh) : 1;
+#pragma omp parallel num_threads(nt)
+    {
         float* sc = (float*)malloc(sizeof(float) * (size_t)stored);
-        /* attend_group, kv_cache.rs:521-690 */
-        for (int g = 0; g < nkv; g++) {
+#pragma omp for schedule(static)
+        for (int h = 0; h < nh; h++) {
+            int g = h / hpk;
             const float* K = kv->k + (size_t)g * S * hd;
             const float* V = kv->v + (size_t)g * S * hd;
-            for (int hh = 0; hh < hpk; hh++) {
-                int h = g * hpk + hh;
-                for (int p = 0; p < stored; p++) sc[p] = dot_f32(q + h * hd, K + (size_t)p * hd, hd) * scale;
-                float mx = -INFINITY, sum = 0.0f;
-                for (int p = 0; p < stored; p++) mx = fmaxf(mx, sc[p]);
-                for (int p = 0; p < stored; p++) {
-                    sc[p] = expf(sc[p] - mx);
-                    sum += sc[p];
-                }
-                if (sum > 0.0f)
-                    for (int p = 0; p < stored; p++) sc[p] /= sum;
-                float* o = ao + h * hd;
-                for (int p = 0; p < stored; p++) {
-                    float w = sc[p];
-                    if (fabsf(w) < 1e-12f) continue;
-                    const float* vr = V + (size_t)p * hd;
-                    for (int d = 0; d < hd; d++) o[d] = fmaf(w, vr[d], o[d]);
-                }
+            for (int p = 0; p < stored; p++) sc[p] = dot_f32(q + h * hd, K + (size_t)p * hd, hd) * scale;
+            float mx = -INFINITY, sum = 0.0f;
+            for (int p = 0; p < stored; p++) mx = fmaxf(mx, sc[p]);
+            for (int p = 0; p < stored; p++) {
+                sc[p] = expf(sc[p] - mx);
+                sum += sc[p];
+            }
+            if (sum > 0.0f)
+                for (int p = 0; p < stored; p++) sc[p] /= sum;
+            float* o = ao + h * hd;
+            for (int p = 0; p < stored; p++) {
+                float w = sc[p];
+                if (fabsf(w) < 1e-12f) continue;
+                const float* vr = V + (size_t)p * hd;
+                axpy(w, vr, o, hd);
             }
         }
-        mv(m, &L->wo, ao, out);
-        free(ao);
         free(sc);
     }
+}
+
+/* qwen_attention (attention.rs:1005-1027) for b consecutive positions
+ * pos0 .. pos0+b-1 over one KV: the projections of all rows at once (the
+ * verify batch's matmat, pipeline.rs:4275-4505), then each row in order
+ * appends its K/V and attends over the rows stored so far, then the output
+ * projection of all rows.  x / out: [b][hidden]; out == NULL: append only. */
+static void attention_rows(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq,
+                           const float* x, int b, int pos0, float* out) {
+    const or_cfg* c = &m->cfg;
+    int qd = c->n_heads * c->head_dim, kd = c->n_kv * c->head_dim;
+    float* q = (float*)malloc(sizeof(float) * (size_t)b * qd);
+    float* k = (float*)malloc(sizeof(float) * (size_t)b * kd);
+    float* v = (float*)malloc(sizeof(float) * (size_t)b * kd);
+    float* ao = out ? (float*)malloc(sizeof(float) * (size_t)b * qd) : NULL;
+    mm(m, &L->wq, x, b, q);
+    mm(m, &L->wk, x, b, k);
+    mm(m, &L->wv, x, b, v);
+    for (int i = 0; i < b; i++)
+        attend_row(m, L, kv, inv_freq, q + (size_t)i * qd, k + (size_t)i * kd, v + (size_t)i * kd, pos0 + i,
+                   ao ? ao + (size_t)i * qd : NULL);
+    if (out) mm(m, &L->wo, ao, b, out);
+    free(ao);
     free(q);
     free(k);
     free(v);
 }
 
-/* dense_ffn_cpu (pipeline.rs:9570-9661), exact arm: silu(g)*u then down */
-static void ffn(const or_model* m, const or_layer* L, const float* x, float* out) {
-    int I = L->gate.rows;
-    float* g = (float*)malloc(sizeof(float) * (size_t)I);
-    float* u = (float*)malloc(sizeof(float) * (size_t)I);
-    mv(m, &L->gate, x, g);
-    mv(m, &L->up, x, u);
-    for (int i = 0; i < I; i++) g[i] = or_silu(g[i]) * u[i];
-    mv(m, &L->down, g, out);
+static void attention(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq,
+                      const float* x, int pos, float* out, int compute_out) {
+    attention_rows(m, L, kv, inv_freq, x, 1, pos, compute_out ? out : NULL);
+}
+
+/* dense_ffn_cpu (pipeline.rs:9570-9661), exact arm: silu(g)*u then down,
+ * for b rows at once (x / out: [b][hidden]) */
+static void ffn_rows(const or_model* m, const or_layer* L, const float* x, int b, float* out) {
+    size_t n = (size_t)b * L->gate.rows;
+    float* g = (float*)malloc(sizeof(float) * n);
+    float* u = (float*)malloc(sizeof(float) * n);
+    mm(m, &L->gate, x, b, g);
+    mm(m, &L->up, x, b, u);
+    for (size_t i = 0; i < n; i++) g[i] = or_silu(g[i]) * u[i];
+    mm(m, &L->down, g, b, out);
     free(g);
     free(u);
 }
 
-/* one transformer block: h += attn(norm(h)); h += ffn(norm(h)) */
-static void block(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq,
-                  float* h, int pos) {
+/* one transformer block over b consecutive positions (h: [b][hidden]):
+ * h += attn(norm(h)); h += ffn(norm(h)) */
+static void block_rows(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq, float* h, int b,
+                       int pos0) {
     int H = m->cfg.hidden;
-    float* n1 = (float*)malloc(sizeof(float) * (size_t)H);
-    float* a = (float*)malloc(sizeof(float) * (size_t)H);
-    float* f = (float*)malloc(sizeof(float) * (size_t)H);
-    or_rms_norm(h, L->input_norm, H, m->cfg.eps, n1);
-    attention(m, L, kv, inv_freq, n1, pos, a, 1);
-    add_rms_norm(h, a, L->post_norm, H, m->cfg.eps, n1);
+    size_t n = (size_t)b * H;
+    float* n1 = (float*)calloc(n, sizeof(float));
+    float* a = (float*)malloc(sizeof(float) * n);
+    float* f = (float*)malloc(sizeof(float) * n);
+    for (int i = 0; i < b; i++) or_rms_norm(h + (size_t)i * H, L->input_norm, H, m->cfg.eps, n1 + (size_t)i * H);
+    attention_rows(m, L, kv, inv_freq, n1, b, pos0, a);
+    for (int i = 0; i < b; i++)
+        add_rms_norm(h + (size_t)i * H, a + (size_t)i * H, L->post_norm, H, m->cfg.eps, n1 + (size_t)i * H);
     if (L->n_experts > 0) {
         /* moe_ffn_forward (pipeline.rs:10868-11045): router logits of the
          * normed row, routing, the routed experts' weighted sum */
         float* lg = (float*)malloc(sizeof(float) * (size_t)L->n_experts);
-        or_matvec(&L->router, n1, lg, m->threads);
-        or_moe_ffn(L->experts, L->n_experts, L->top_k, L->norm_topk, L->routed_scaling, lg, n1, H, f, m->threads);
+        for (int i = 0; i < b; i++) {
+            or_matvec(&L->router, n1 + (size_t)i * H, lg, m->threads);
+            or_moe_ffn(L->experts, L->n_experts, L->top_k, L->norm_topk, L->routed_scaling, lg, n1 + (size_t)i * H,
+                       H, f + (size_t)i * H, m->threads);
+        }
         free(lg);
     } else {
-        ffn(m, L, n1, f);
+        ffn_rows(m, L, n1, b, f);
     }
-    for (int i = 0; i < H; i++) h[i] += f[i];
+    for (size_t i = 0; i < n; i++) h[i] += f[i];
     free(n1);
     free(a);
     free(f);
 }
 
+static void block(const or_model* m, const or_layer* L, or_kv* kv, const float* inv_freq, float* h, int pos) {
+    block_rows(m, L, kv, inv_freq, h, 1, pos);
+}
+
 /* forward_layers_span (pipeline.rs:7981-8700) */
 void or_forward(const or_model* m, or_state* s, float* h, int pos) {
     for (int li = 0; li < m->cfg.n_layers; li++) block(m, &m->layers[li], &s->trunk[li], s->inv_freq, h, pos);
+}
+
+/* forward_batch over b consecutive positions (pipeline.rs:4275-4505, the
+ * verify rows as one batch): every layer's matmuls take all rows at once,
+ * attention runs row by row in position order.  Under the exact contract the
+ * rows equal b per-position forwards bit for bit; under a8w8 the q4t
+ * matmuls take the four-input blocked order for rows 0..3 (qtensor.rs:
+ * 5908-5928). */
+void or_forward_rows(const or_model* m, or_state* s, float* h, int b, int pos0) {
+    for (int li = 0; li < m->cfg.n_layers; li++)
+        block_rows(m, &m->layers[li], &s->trunk[li], s->inv_freq, h, b, pos0);
 }
 
 void or_logits(const or_model* m, const float* h, float* logits) {
@@ -243,7 +303,8 @@ void or_mtp_step(const or_model* m, or_state* s, const float* hidden, uint32_t t
 
 /* ---------------------------------------------------------------------------
  * The decode loop with graph_spec_step (pipeline.rs:2546-2980, 3582-4213).
- * The verify rows are ordinary per-position forwards; the trunk KV rows past
+ * The verify rows are per-position forwards, or one batch (or_forward_rows)
+ * when the model asks for it; the trunk KV rows past
  * the accepted prefix are dropped (truncate_last, kv_cache.rs:883).  The
  * reference's timing-based speculation monitor (SpecMon, pipeline.rs:662)
  * is not restated: speculation is on for every round.
@@ -287,12 +348,21 @@ static int verify_core(const or_model* m, or_state* s, int next_pos, uint32_t t_
     const or_cfg* c = &m->cfg;
     int H = c->hidden, V = c->vocab, b = K + 1;
     sparse_t* ps = (sparse_t*)malloc(sizeof(sparse_t));
-    for (int i = 0; i < b; i++) {
-        uint32_t t = i == 0 ? t_next : drafts[i - 1];
-        float* h = hid + (size_t)i * H;
-        or_embed(m, t, h);
-        or_forward(m, s, h, next_pos + i);
-        or_logits(m, h, vlog + (size_t)i * V);
+    if (m->batch_verify) {
+        for (int i = 0; i < b; i++) or_embed(m, i == 0 ? t_next : drafts[i - 1], hid + (size_t)i * H);
+        or_forward_rows(m, s, hid, b, next_pos);
+        float* n = (float*)malloc(sizeof(float) * (size_t)b * H);
+        for (int i = 0; i < b; i++) or_rms_norm(hid + (size_t)i * H, m->final_norm, H, c->eps, n + (size_t)i * H);
+        mm(m, &m->lm_head, n, b, vlog);
+        free(n);
+    } else {
+        for (int i = 0; i < b; i++) {
+            uint32_t t = i == 0 ? t_next : drafts[i - 1];
+            float* h = hid + (size_t)i * H;
+            or_embed(m, t, h);
+            or_forward(m, s, h, next_pos + i);
+            or_logits(m, h, vlog + (size_t)i * V);
+        }
     }
     int a = 0;
     *forced = -1;

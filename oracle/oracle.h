@@ -41,6 +41,15 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* Hot oracle loops are built twice: for hosts with FMA/AVX2 and for any
+ * x86-64 host, picked at load time.  Both clones perform the same float
+ * operations in the same order (-ffp-contract=off, no fast-math). */
+#if defined(__x86_64__) && defined(__GNUC__) && !defined(__clang__)
+#define CLONES __attribute__((target_clones("fma", "default")))
+#else
+#define CLONES
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -79,6 +88,12 @@ void or_matmat(const or_qt* w, const float* xs, int b, float* out, int threads);
 /* a8w8 contract (split_act + integer tile dots), qtensor.rs:9237-9281,
  * 4106-4130, 4405-4413, 4517-4544, 4666-4671, 8921-8933 */
 void or_matvec_a8w8(const or_qt* w, const float* x, float* out, int threads);
+/* a8w8 batch (qmatmat / q4t_matmat / q4tp_matmat x86 VNNI arms): out[b*rows + r] */
+void or_matmat_a8w8(const or_qt* w, const float* xs, int b, float* out, int threads);
+/* fast.c, the timing arm: the same values as or_matmat_a8w8 by AVX-512 VNNI
+ * intrinsics; -1 on a host without AVX-512 VNNI */
+int or_fast_supported(void);
+int or_fast_matmat_a8w8(const or_qt* w, const float* xs, int b, float* out, int threads);
 /* split_act as a plain function (qtensor.rs:9237-9281).  xq: [n];
  * outl_idx/outl_val: capacity n.  Returns the outlier count. */
 int or_split_act(const float* x, int n, int8_t* xq, float* sx, int* outl_idx, float* outl_val,
@@ -156,6 +171,8 @@ typedef struct {
     int threads;
     or_qt embed;            /* untied q8 embedding table (loader.rs:714-724); q == NULL: lm_head */
     int a8w8;               /* 1: the quantized matvecs of the forward under the a8w8 contract */
+    int fast;               /* 1: a8w8 matmuls through the AVX-512 VNNI timing arm (same values) */
+    int batch_verify;       /* 1: the verify rows of a spec round as one batch (or_forward_rows) */
 } or_model;
 
 /* KV: per layer k[n_kv][max_seq][head_dim], same for v; len = stored rows.
@@ -175,6 +192,8 @@ typedef struct {
 void or_embed(const or_model* m, uint32_t id, float* out);
 /* forward_layers (pipeline.rs:5851, 7981-8700): h in/out */
 void or_forward(const or_model* m, or_state* s, float* h, int pos);
+/* forward_batch over positions pos0 .. pos0+b-1, h: [b][hidden] in/out */
+void or_forward_rows(const or_model* m, or_state* s, float* h, int b, int pos0);
 /* final norm + lm_head (pipeline.rs:5919, 8771) */
 void or_logits(const or_model* m, const float* h, float* logits);
 /* mtp_step_hl (pipeline.rs:3051-3160): logits (may be NULL -> warm only,

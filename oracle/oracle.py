@@ -41,7 +41,8 @@ class Layer(C.Structure):
 class Model(C.Structure):
     _fields_ = [("cfg", Cfg), ("layers", C.c_void_p), ("lm_head", QT), ("final_norm", C.c_void_p),
                 ("has_mtp", C.c_int), ("enorm", C.c_void_p), ("hnorm", C.c_void_p), ("mtp_norm", C.c_void_p),
-                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int), ("embed", QT), ("a8w8", C.c_int)]
+                ("eh_proj", QT), ("mtp", Layer), ("threads", C.c_int), ("embed", QT), ("a8w8", C.c_int),
+                ("fast", C.c_int), ("batch_verify", C.c_int)]
 
 
 class KV(C.Structure):
@@ -92,6 +93,9 @@ def lib():
             "or_matvec": (None, [C.POINTER(QT), P, P, C.c_int]),
             "or_matmat": (None, [C.POINTER(QT), P, C.c_int, P, C.c_int]),
             "or_matvec_a8w8": (None, [C.POINTER(QT), P, P, C.c_int]),
+            "or_matmat_a8w8": (None, [C.POINTER(QT), P, C.c_int, P, C.c_int]),
+            "or_fast_supported": (C.c_int, []),
+            "or_fast_matmat_a8w8": (C.c_int, [C.POINTER(QT), P, C.c_int, P, C.c_int]),
             "or_split_act": (C.c_int, [P, C.c_int, P, P, P, P, P]),
             "or_rng_next_u64": (C.c_uint64, [P]),
             "or_rng_next_f32": (C.c_float, [P]),
@@ -141,16 +145,25 @@ def qt(t, keep):
     return QT(t["dtype"], t["rows"], t["cols"], _p(q), _p(rs), _p(b))
 
 
-def matmat(t, xs, threads=8, a8w8=False):
-    """Exact-contract (or a8w8 for b == 1) reference matmul: [b][rows]."""
+def fast_supported():
+    """True when the host has AVX-512 VNNI (the timing arm can run)."""
+    return bool(lib().or_fast_supported())
+
+
+def matmat(t, xs, threads=8, a8w8=False, fast=False):
+    """Reference matmul [b][rows]: the exact contract, or a8w8 (the batch
+    order of the reference's x86 VNNI arms); fast=True runs a8w8 through the
+    AVX-512 VNNI timing arm, which must give the same values."""
     keep = []
     w = qt(t, keep)
     xs = np.ascontiguousarray(np.atleast_2d(xs), dtype=np.float32)
     b = xs.shape[0]
     out = np.empty((b, t["rows"]), dtype=np.float32)
-    if a8w8:
-        for i in range(b):
-            lib().or_matvec_a8w8(C.byref(w), _p(xs[i]), _p(out[i]), threads)
+    if fast:
+        if lib().or_fast_matmat_a8w8(C.byref(w), _p(xs), b, _p(out), threads) != 0:
+            raise RuntimeError("the VNNI timing arm needs AVX-512 VNNI and a quantized tensor")
+    elif a8w8:
+        lib().or_matmat_a8w8(C.byref(w), _p(xs), b, _p(out), threads)
     else:
         lib().or_matmat(C.byref(w), _p(xs), b, _p(out), threads)
     return out
@@ -192,7 +205,7 @@ def _layer(l, keep):
 class OracleModel:
     """The CPU reference model over the same synthetic arrays the GPU uses."""
 
-    def __init__(self, sm, threads=8, a8w8=False):
+    def __init__(self, sm, threads=8, a8w8=False, fast=False, batch_verify=False):
         c = sm["cfg"]
         self.c = c
         self.sm = sm
@@ -209,6 +222,8 @@ class OracleModel:
         m.final_norm = _f32(sm["final_norm"], self.keep)
         m.threads = threads
         m.a8w8 = 1 if a8w8 else 0
+        m.fast = 1 if fast else 0
+        m.batch_verify = 1 if batch_verify else 0
         if "mtp" in sm:
             mt = sm["mtp"]
             m.has_mtp = 1

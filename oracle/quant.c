@@ -151,7 +151,7 @@ void or_dequant_q4tp(const uint8_t* bytes, int rows, int cols, float* dst) {
 /* qtensor.rs:8687-8718 (dot_i8_f32_avx2): two 8-lane FMA accumulators over
  * 16-element steps, then the 8->4->2->1 horizontal reduction, then the
  * scalar tail.  This is the exact-contract q8 row dot on this x86 host. */
-static float dot_i8_f32(const int8_t* w, const float* x, int n) {
+CLONES static float dot_i8_f32(const int8_t* w, const float* x, int n) {
     float a0[8] = {0}, a1[8] = {0};
     int j = 0;
     for (; j + 16 <= n; j += 16)
@@ -170,7 +170,7 @@ static float dot_i8_f32(const int8_t* w, const float* x, int n) {
 
 /* qtensor.rs:4418-4432 — q4t_row_exact: per tile pairwise (lo, hi) terms,
  * then acc += ga * s, tiles in order. */
-static float q4t_row_exact(const uint8_t* bytes, size_t r, size_t gpr, const float* x) {
+CLONES static float q4t_row_exact(const uint8_t* bytes, size_t r, size_t gpr, const float* x) {
     float acc = 0.0f;
     for (size_t g = 0; g < gpr; g++) {
         const uint8_t* t = bytes + (r * gpr + g) * Q4_TILE;
@@ -199,7 +199,7 @@ static void q4tp_scales(const uint8_t* bytes, size_t rows, size_t cols, size_t r
 }
 
 /* qtensor.rs:4647-4661 — q4tp_row_exact. */
-static float q4tp_row_exact(const uint8_t* nib, size_t r, size_t gpr, const float* x,
+CLONES static float q4tp_row_exact(const uint8_t* nib, size_t r, size_t gpr, const float* x,
                             const float* sc) {
     float acc = 0.0f;
     for (size_t g = 0; g < gpr; g++) {
@@ -305,80 +305,132 @@ int or_split_act(const float* x, int n, int8_t* xq, float* sx_out, int* oi, floa
     return no;
 }
 
-void or_matvec_a8w8(const or_qt* w, const float* x, float* out, int threads) {
+/* The integer tile dot of one q4 tile (32 codes, element 2k = low nibble of
+ * byte k) against 32 int8 activations. */
+static int32_t q4_tile_dot(const uint8_t* nib, const int8_t* xq) {
+    int32_t d = 0;
+    for (int k = 0; k < 16; k++)
+        d += ((int)(nib[k] & 0x0F) - 8) * xq[2 * k] + ((int)((nib[k] >> 4) & 0x0F) - 8) * xq[2 * k + 1];
+    return d;
+}
+
+/* The exact outlier corrections of one output (q8: qtensor.rs:8921-8933;
+ * q4t_outlier qtensor.rs:4405-4413: (w * s) * xv; q4tp 4690-4700). */
+static float a8w8_outliers(const or_qt* w, size_t r, size_t gpr, const float* sc, const int* oi,
+                           const float* ov, int no, float acc) {
+    for (int o = 0; o < no; o++) {
+        int j = oi[o], k = j % GROUP;
+        if (w->dtype == OR_Q8ROW) {
+            acc += (float)w->q[r * (size_t)w->cols + j] * ov[o];
+        } else if (w->dtype == OR_Q4T) {
+            const uint8_t* t = w->bytes + (r * gpr + j / GROUP) * Q4_TILE;
+            uint8_t byte = t[2 + k / 2];
+            int nib = (k & 1) ? (byte >> 4) : (byte & 0x0F);
+            acc += (float)(nib - 8) * rd_f16(t) * ov[o];
+        } else {
+            uint8_t byte = w->bytes[(r * gpr + j / GROUP) * Q4TP_NIB + k / 2];
+            int nib = (k & 1) ? (byte >> 4) : (byte & 0x0F);
+            acc += (float)(nib - 8) * sc[j / GROUP] * ov[o];
+        }
+    }
+    return acc;
+}
+
+/* dot_q4t_row_1x4 (qtensor.rs:4315-4361, the x86 VNNI arm of q4t_matmat's
+ * blocked path, 5908-5928): per tile, lane l of 8 holds the integer dot of
+ * elements 4l..4l+3, converted to f32 and fused-multiply-added with the tile
+ * scale into that lane's accumulator; the row result is the 8->4->2->1
+ * horizontal sum (hsum256_ps, qtensor.rs:4300-4310). */
+static float q4t_row_1x4_order(const uint8_t* bytes, size_t r, size_t gpr, const int8_t* xq) {
+    float f[8] = {0};
+    for (size_t g = 0; g < gpr; g++) {
+        const uint8_t* t = bytes + (r * gpr + g) * Q4_TILE;
+        float s = rd_f16(t);
+        for (int l = 0; l < 8; l++) {
+            int32_t p = 0;
+            for (int e = 4 * l; e < 4 * l + 4; e++) {
+                uint8_t byte = t[2 + e / 2];
+                int nib = (e & 1) ? (byte >> 4) : (byte & 0x0F);
+                p += (nib - 8) * xq[g * GROUP + e];
+            }
+            f[l] = fmaf((float)p, s, f[l]);
+        }
+    }
+    float h[4];
+    for (int l = 0; l < 4; l++) h[l] = f[l] + f[4 + l];
+    float a = h[0] + h[2], b = h[1] + h[3];
+    return a + b;
+}
+
+/* One batch under the a8w8 contract on an x86 host with AVX-512 VNNI (the
+ * reference's default there): split_act per input row, then per weight row
+ *   q8   (qmatmat x86 arm, qtensor.rs:3456-3470 with row_dot_avx2 8921-8933):
+ *        integer dot * sx + outliers, * row_scale, every input alone;
+ *   q4t  (q4t_matmat, qtensor.rs:5866-5948): inputs in blocks of four by the
+ *        1x4 order above, the rest by dot_q4t_row_i8 (4106-4130: per tile
+ *        acc += d * s), * sx, + outliers;
+ *   q4tp (dot_q4tp_row_i8 order, 4517-4544), every input alone.
+ * Rows are split into contiguous ranges (pool.rs:320 run_rows); each output
+ * is computed by one thread in a fixed order, so threads do not change it. */
+void or_matmat_a8w8(const or_qt* w, const float* xs, int b, float* out, int threads) {
     const int rows = w->rows, cols = w->cols;
     const size_t gpr = (size_t)cols / GROUP;
-    int8_t* xq = (int8_t*)malloc((size_t)cols);
-    int* oi = (int*)malloc(sizeof(int) * (size_t)cols);
-    float* ov = (float*)malloc(sizeof(float) * (size_t)cols);
-    float sx;
-    int32_t xsum;
-    int no = or_split_act(x, cols, xq, &sx, oi, ov, &xsum);
+    int8_t* xq = (int8_t*)malloc((size_t)b * cols);
+    int* oi = (int*)malloc(sizeof(int) * (size_t)b * cols);
+    float* ov = (float*)malloc(sizeof(float) * (size_t)b * cols);
+    float* sx = (float*)malloc(sizeof(float) * (size_t)b);
+    int* no = (int*)malloc(sizeof(int) * (size_t)b);
+    for (int i = 0; i < b; i++) {
+        int32_t xsum;
+        no[i] = or_split_act(xs + (size_t)i * cols, cols, xq + (size_t)i * cols, &sx[i], oi + (size_t)i * cols,
+                             ov + (size_t)i * cols, &xsum);
+    }
     if (threads < 1) threads = 1;
 #pragma omp parallel num_threads(threads)
     {
         float* sc = (w->dtype == OR_Q4TP) ? (float*)malloc(sizeof(float) * (gpr ? gpr : 1)) : NULL;
 #pragma omp for schedule(static)
         for (int r = 0; r < rows; r++) {
-            float acc;
-            if (w->dtype == OR_Q8ROW) {
-                /* qtensor.rs:8921-8933 row_dot_avx2, then * row_scale (:9094) */
-                const int8_t* row = w->q + (size_t)r * cols;
-                int64_t d = 0;
-                for (int j = 0; j < cols; j++) d += (int64_t)row[j] * xq[j];
-                acc = (float)(int32_t)d * sx;
-                for (int o = 0; o < no; o++) acc += (float)row[oi[o]] * ov[o];
-                acc *= w->row_scale[r];
-            } else if (w->dtype == OR_Q4T) {
-                /* qtensor.rs:4106-4130 then 5695-5700 */
-                float a = 0.0f;
-                for (size_t g = 0; g < gpr; g++) {
-                    const uint8_t* t = w->bytes + ((size_t)r * gpr + g) * Q4_TILE;
-                    float s = rd_f16(t);
-                    int32_t d = 0;
-                    for (int k = 0; k < 16; k++) {
-                        uint8_t b = t[2 + k];
-                        d += ((int)(b & 0x0F) - 8) * xq[g * GROUP + 2 * k] +
-                             ((int)((b >> 4) & 0x0F) - 8) * xq[g * GROUP + 2 * k + 1];
+            if (sc) q4tp_scales(w->bytes, rows, cols, r, sc);
+            for (int i = 0; i < b; i++) {
+                const int8_t* x = xq + (size_t)i * cols;
+                float acc;
+                if (w->dtype == OR_Q8ROW) {
+                    const int8_t* row = w->q + (size_t)r * cols;
+                    int64_t d = 0;
+                    for (int j = 0; j < cols; j++) d += (int64_t)row[j] * x[j];
+                    acc = (float)(int32_t)d * sx[i];
+                } else if (w->dtype == OR_Q4T) {
+                    if (i < (b & ~3)) {
+                        acc = q4t_row_1x4_order(w->bytes, r, gpr, x);
+                    } else {
+                        acc = 0.0f;
+                        for (size_t g = 0; g < gpr; g++) {
+                            const uint8_t* t = w->bytes + ((size_t)r * gpr + g) * Q4_TILE;
+                            acc += (float)q4_tile_dot(t + 2, x + g * GROUP) * rd_f16(t);
+                        }
                     }
-                    a += (float)d * s;
+                    acc *= sx[i];
+                } else {
+                    acc = 0.0f;
+                    for (size_t g = 0; g < gpr; g++)
+                        acc += (float)q4_tile_dot(w->bytes + ((size_t)r * gpr + g) * Q4TP_NIB, x + g * GROUP) * sc[g];
+                    acc *= sx[i];
                 }
-                acc = a * sx;
-                for (int o = 0; o < no; o++) {
-                    /* q4t_outlier, qtensor.rs:4405-4413: (w * s) * xv */
-                    int j = oi[o];
-                    const uint8_t* t = w->bytes + ((size_t)r * gpr + j / GROUP) * Q4_TILE;
-                    float s = rd_f16(t);
-                    int k = j % GROUP;
-                    uint8_t byte = t[2 + k / 2];
-                    int nib = (k & 1) ? (byte >> 4) : (byte & 0x0F);
-                    acc += (float)(nib - 8) * s * ov[o];
-                }
-            } else {
-                /* qtensor.rs:4517-4544 with the ladder scales, 4690-4700 */
-                q4tp_scales(w->bytes, rows, cols, r, sc);
-                float a = 0.0f;
-                for (size_t g = 0; g < gpr; g++) {
-                    const uint8_t* t = w->bytes + ((size_t)r * gpr + g) * Q4TP_NIB;
-                    int32_t d = 0;
-                    for (int k = 0; k < 16; k++)
-                        d += ((int)(t[k] & 0x0F) - 8) * xq[g * GROUP + 2 * k] +
-                             ((int)((t[k] >> 4) & 0x0F) - 8) * xq[g * GROUP + 2 * k + 1];
-                    a += (float)d * sc[g];
-                }
-                acc = a * sx;
-                for (int o = 0; o < no; o++) {
-                    int j = oi[o], k = j % GROUP;
-                    uint8_t byte = w->bytes[((size_t)r * gpr + j / GROUP) * Q4TP_NIB + k / 2];
-                    int nib = (k & 1) ? (byte >> 4) : (byte & 0x0F);
-                    acc += (float)(nib - 8) * sc[j / GROUP] * ov[o];
-                }
+                acc = a8w8_outliers(w, r, gpr, sc, oi + (size_t)i * cols, ov + (size_t)i * cols, no[i], acc);
+                if (w->dtype == OR_Q8ROW) acc *= w->row_scale[r];
+                out[(size_t)i * rows + r] = acc;
             }
-            out[r] = acc;
         }
         free(sc);
     }
     free(xq);
     free(oi);
     free(ov);
+    free(sx);
+    free(no);
+}
+
+void or_matvec_a8w8(const or_qt* w, const float* x, float* out, int threads) {
+    or_matmat_a8w8(w, x, 1, out, threads);
 }
