@@ -9,8 +9,11 @@
  *    >0  declined, nothing written (the caller runs its CPU path)
  *    <0  error; cmf_last_error() says why (thread-local, like
  *        cortiq_last_error in crates/cortiq-ffi/include/cortiq.h:6-24)
- * Calls on one handle are serialised by the caller (cortiq.h:3-5); every
- * handle runs on one HIP stream.
+ * Calls on one handle are serialised by the caller (cortiq.h:3-5).  Each
+ * host thread that calls the library gets its own HIP stream and its own
+ * seam scratch (created on its first call), so seam ops from several
+ * threads run concurrently; a model handle's work runs on the stream of the
+ * thread that calls it.
  */
 #ifndef CMF_HIP_H
 #define CMF_HIP_H
@@ -30,11 +33,11 @@ extern "C" {
 /* ---- library -------------------------------------------------------- */
 /* Thread-local message of the last failing call (cortiq.h:6-24). */
 const char* cmf_last_error(void);
-/* Select the device and create the library stream.  Replaces the backend
- * selection of gpu.rs:866-936.  Idempotent. */
+/* Select the device and create the calling thread's stream.  Replaces the
+ * backend selection of gpu.rs:866-936.  Idempotent. */
 int cmf_init(int device);
 int cmf_device_count(void);
-/* Wait for all work on the library stream. */
+/* Wait for all work on the calling thread's stream. */
 int cmf_sync(void);
 
 /* ---- weights (residency: gpu.rs:507 weight_is_resident) -------------- */
