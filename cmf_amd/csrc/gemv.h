@@ -97,6 +97,8 @@ GemvKernel q8_kernel(int m, int xm, int ks);
 // LDS bytes (*lds), or nullptr
 GemvKernel q8_kernel_m1(int nk, bool resid, int* ks, size_t* lds);
 GemvKernel q4t_kernel_m1(int nk, bool resid, int* ks, size_t* lds);
+// q4t, M = 1, the operand staged from its f32 row inside the kernel (XS_ROWS)
+GemvKernel q4t_kernel_m1x(int nk, bool resid, int* ks);
 
 enum { EPI_NONE = 0, EPI_SWIGLU = 1 };
 

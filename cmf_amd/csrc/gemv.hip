@@ -461,6 +461,19 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
             return CMF_OK;
         }
     }
+    // q4t M = 1 from the f32 row (XS_ROWS): the kernel that stages its own
+    // operand slices (CMF_GEMV_M1X=0 keeps the general fused kernel)
+    static const int m1x_env = env_int("CMF_GEMV_M1X", 1);
+    if (m1x_env && m == 1 && xm == XM_FUSED && a.src.mode == XS_ROWS && w.dtype == DT_Q4T && gridy == 1 &&
+        grid_override <= 0 && ks_override <= 0 && a.epi == EPI_NONE && a.src.K % 8 == 0) {
+        int ks1 = 0;
+        GemvKernel k1 = q4t_kernel_m1x(w.kchunks, a.resid, &ks1);
+        if (k1 && resident_per_cu(k1, 64 * ks1, 0) >= 1) {
+            void* args[] = {&a};
+            CMF_HIP(hipLaunchKernel((const void*)k1, dim3(a.nrb), dim3(64 * ks1), args, 0, st));
+            return CMF_OK;
+        }
+    }
     // Two more q4 shapes of the prepared-operand GEMV, chosen by what
     // measured faster on MI355X (GEMV alone, 10 weight copies rotating;
     // CMF_GEMV_G=0/3 and CMF_GEMV_S6=0/1 force either):

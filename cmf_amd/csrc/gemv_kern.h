@@ -1012,6 +1012,133 @@ __global__ __launch_bounds__(64 * KS) void k_gemv_q4t_m1(GemvArgs a) {
     }
 }
 
+// q4t, M = 1, from the f32 operand row itself (XS_ROWS): the workgroup
+// needs no producer launch.  Wave w reads the SPW * 128 columns of its own
+// steps, one 8-column k-slot item per lane and step group, then the
+// workgroup agrees on the row's max |x| (one LDS exchange: the fixed-point
+// unit 2^(e - 11) of q4_fix_scale needs the whole row), and each wave writes
+// its slice's hi / lo planes and tile biases (exactly what the producer
+// would have written) into its own LDS region and runs the MFMA loop of
+// k_gemv_q4t_m1.  Columns past the row (steps past ntg, tiles past K) are
+// zero: their planes and biases vanish.
+template <int KS, int SPW, bool RESID>
+__global__ __launch_bounds__(64 * KS) void k_gemv_q4t_m1x(GemvArgs a) {
+    constexpr int NIT = SPW / 4;           // 8-column items per lane (16 SPW items per wave)
+    static_assert(SPW % 4 == 0 && SPW * 8 <= 64, "items per lane");
+    __shared__ float part[KS][64];
+    __shared__ float wmax[KS];
+    __shared__ __align__(16) uint4 slice[KS][SPW * 32];  // [item][plane] 16 B, item = (u * 4 + t) * 4 + s'
+    __shared__ float sbias[KS][SPW * 8];                 // [(u * 4 + t) * 2 + plane]
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4, p = r < 8 ? 0 : 1;
+    const int ntg = a.nk, rb = blockIdx.x, K = a.src.K;
+    const int t0 = wave * SPW;
+    const int row = (a.rb0 + rb) * 16 + r;
+    const int rowc = max(a.row_lo, min(row, a.row_hi - 1));
+    const float yold = RESID ? ldg(a.y + (rowc - a.row_lo)) : 0.f;
+    // this lane's items: item q = lane + 64 i = (u * 4 + t) * 4 + s', columns
+    // 32 ((t0 + u) * 4 + t) + 8 s' .. + 7 (clamped loads, zero by select)
+    float4v xv[NIT][2];
+    bool on[NIT];
+#pragma unroll
+    for (int i = 0; i < NIT; i++) {
+        const int q = lane + 64 * i, u = q >> 4, t = (q >> 2) & 3, sp = q & 3;
+        const int c0 = ((t0 + u) * 4 + t) * 32 + 8 * sp;
+        on[i] = t0 + u < ntg && c0 + 8 <= K;
+        const float* src = a.src.x + (on[i] ? c0 : 0);
+        xv[i][0] = ldg((const float4v*)src);
+        xv[i][1] = ldg((const float4v*)(src + 4));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wv[SPW];
+    uint2 sv[SPW];
+    const size_t wbase = (size_t)(a.rb0 + rb) * ntg;
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const size_t t = wbase + min(t0 + u, ntg - 1);
+        wv[u] = ld_stream((const uint4*)a.w + t * 64 + lane);
+        const uint64_t sw = ldg((const uint64_t*)a.scale + t * 16 + r);
+        sv[u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * SPW>();  // this wave's operand columns are in
+    float am = 0.f;
+#pragma unroll
+    for (int i = 0; i < NIT; i++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) am = fmaxf(am, on[i] ? fabsf(xv[i][h][k]) : 0.f);
+    am = wave_max(am);
+    if (lane == 0) wmax[wave] = am;
+    // LDS-only barrier: the weights stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    am = wmax[0];
+#pragma unroll
+    for (int w = 1; w < KS; w++) am = fmaxf(am, wmax[w]);
+    float scale, xs;
+    q4_fix_scale(am, scale, xs);
+    const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+#pragma unroll
+    for (int i = 0; i < NIT; i++) {
+        const int q = lane + 64 * i;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = on[i] ? xv[i][k >> 2][k & 3] : 0.f;
+        uint16_t hv[8], lv[8];
+        float sh = 0.f, sl = 0.f;  // (exact: integers and multiples of 2^-11)
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            _Float16 h, l;
+            q4_fix_split(v[ord[j]] * scale, h, l);
+            hv[j] = __builtin_bit_cast(uint16_t, h);
+            lv[j] = __builtin_bit_cast(uint16_t, l);
+            sh += (float)h;
+            sl += (float)l;
+        }
+        sh += __shfl_xor(sh, 1);
+        sh += __shfl_xor(sh, 2);
+        sl += __shfl_xor(sl, 1);
+        sl += __shfl_xor(sl, 2);
+        slice[wave][q * 2] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                                        hv[6] | (hv[7] << 16));
+        slice[wave][q * 2 + 1] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
+                                            lv[6] | (lv[7] << 16));
+        if ((q & 3) == 0) {
+            sbias[wave][(q >> 2) * 2] = sh * Q4_BIAS;
+            sbias[wave][(q >> 2) * 2 + 1] = sl * Q4_BIAS;
+        }
+    }
+    // the wave reads back what its own lanes wrote (LDS operations of a
+    // wave complete in order; the barrier keeps the compiler from moving
+    // the reads up)
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const uint4* X = slice[wave];
+    const float* bias = sbias[wave];
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const bool in = t0 + u < ntg;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const half8 xa = __builtin_bit_cast(half8, X[((u * 4 + t) * 4 + s) * 2 + p]);
+            const uint32_t wq = t == 0 ? wv[u].x : t == 1 ? wv[u].y : t == 2 ? wv[u].z : wv[u].w;
+            const float4v z = {0.f, 0.f, 0.f, 0.f};
+            const float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, dq_nib_word(wq), z, 0, 0, 0);
+            const uint32_t sw = t < 2 ? sv[u].x : sv[u].y;
+            const float sc = in ? f16_bits_to_f32((t & 1) ? sw >> 16 : sw & 0xFFFFu) : 0.f;
+            acc += (d[0] + bias[(u * 4 + t) * 2 + (s >> 1)]) * sc;  // s >= 2: the lo rows
+        }
+    }
+    float o = m1_reduce<KS>(part, acc, wave, lane);
+    o += __shfl_xor(o, 32);  // hi rows (lanes s = 0, 1) + lo rows (s = 2, 3)
+    if (wave == 0 && s == 0 && row >= a.row_lo && row < a.row_hi && rb < a.nrb) {
+        const float val = o * xs * 16777216.0f;  // 2^24: denormal nibbles
+        a.y[row - a.row_lo] = RESID ? yold + val : val;
+    }
+}
+
 // Instance of the M = 1 kernels for rows of nk 1 KiB steps (nullptr: none);
 // *ks = its waves per workgroup, *lds = its dynamic LDS bytes.
 template <int KS, int SPW>
@@ -1034,6 +1161,20 @@ inline GemvKernel q8_m1_pick(int nk, bool resid, int* ks, size_t* lds) {
     if (nk <= 128) return q8_m1_inst<16, 8>(resid, ks, lds);
     if (nk <= 192) return q8_m1_inst<16, 12>(resid, ks, lds);
     return nullptr;
+}
+template <int KS, int SPW>
+inline GemvKernel q4t_m1x_inst(bool resid, int* ks) {
+    *ks = KS;
+    return resid ? k_gemv_q4t_m1x<KS, SPW, true> : k_gemv_q4t_m1x<KS, SPW, false>;
+}
+// the staged-from-rows kernel: SPW a multiple of 4 (whole items per lane)
+inline GemvKernel q4t_m1x_pick(int nk, bool resid, int* ks) {
+    if (nk <= 4) return q4t_m1x_inst<1, 4>(resid, ks);
+    if (nk <= 8) return q4t_m1x_inst<2, 4>(resid, ks);
+    if (nk <= 16) return q4t_m1x_inst<4, 4>(resid, ks);
+    if (nk <= 32) return q4t_m1x_inst<8, 4>(resid, ks);
+    if (nk <= 64) return q4t_m1x_inst<8, 8>(resid, ks);
+    return nullptr;  // (16 waves x 8 steps of slices would pass the 64 KiB of static LDS)
 }
 inline GemvKernel q4t_m1_pick(int nk, bool resid, int* ks, size_t* lds) {
     if (nk <= 4) return q4t_m1_inst<1, 4>(resid, ks, lds);

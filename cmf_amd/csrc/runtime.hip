@@ -290,9 +290,19 @@ int seam_matmat(const DevWeight& w_in, int row0, const float* xs, int b, int row
         const int m = std::min(MAXB, b - b0);
         CMF_HIP(hipMemcpyAsync(g_ss.x, xs + (size_t)b0 * w.cols, (size_t)m * w.cols * sizeof(float),
                                hipMemcpyHostToDevice, st));
-        launch_prep(w, g_ss.x, w.cols, m, g_ss.planes, g_ss.xs, st);
-        if (launch_gemv(w, g_ss.planes, g_ss.xs, g_ss.y, rows, m, row0, row0 + rows, st) != CMF_OK)
-            return CMF_ERR;
+        int ks1 = 0;
+        if (m == 1 && w.dtype == DT_Q4T && q4t_kernel_m1x(w.kchunks, false, &ks1)) {
+            // one launch: the kernel stages its operand from the f32 row
+            XSrc src{};
+            src.mode = XS_ROWS;
+            src.x = g_ss.x;
+            src.ldx = w.cols;
+            if (gemv(w, src, g_ss.y, rows, 1, row0, row0 + rows, false, st) != CMF_OK) return CMF_ERR;
+        } else {
+            launch_prep(w, g_ss.x, w.cols, m, g_ss.planes, g_ss.xs, st);
+            if (launch_gemv(w, g_ss.planes, g_ss.xs, g_ss.y, rows, m, row0, row0 + rows, st) != CMF_OK)
+                return CMF_ERR;
+        }
         CMF_HIP(hipMemcpyAsync(out + (size_t)b0 * rows, g_ss.y, (size_t)m * rows * sizeof(float),
                                hipMemcpyDeviceToHost, st));
     }

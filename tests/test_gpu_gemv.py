@@ -83,13 +83,55 @@ def test_ragged_shapes(gpu):
 
 @pytest.mark.parametrize("cols", [64, 448, 1024, 2048, 4160, 8192, 12288, 16384])
 def test_m1_kernel_instances(gpu, cols):
-    """M = 1 over a prepared operand runs the per-wave operand-slice kernels
-    (k_gemv_q8_m1 / k_gemv_q4t_m1); every instance size (q8: 1..192 K steps
+    """M = 1 runs the per-wave operand-slice kernels (k_gemv_q8_m1 over a
+    prepared operand; q4t through the seam: k_gemv_q4t_m1x staging its own
+    operand up to 64 steps, k_gemv_q4t_m1 beyond); every instance size (q8: 1..192 K steps
     of 64 columns, q4t: 1..128 steps of 128 columns), ragged steps (4160 =
     65 q8 chunks, 32.5 q4t groups) and ragged rows"""
     from cmf_amd import synth
     _check(gpu, synth.q8_normal(81 + cols, 77, cols), _x(82 + cols, 1, cols))
     _check(gpu, synth.q4t_uniform(83 + cols, 93, cols), _x(84 + cols, 1, cols))
+
+
+def _gemv_rows(gpu, w, x, rows, fused):
+    """y = W x from the f32 row x on the device: fused=1 the kernel stages its
+    operand itself, fused=0 the producer launch + the prepared-operand GEMV"""
+    import ctypes as C
+    dx, dy = gpu.DevBuf(x.nbytes), gpu.DevBuf(rows * 4)
+    dx.upload(x)
+    arr = (C.c_void_p * 1)(w.h)
+    ms = C.c_float()
+    gpu.check(gpu.lib().cmf_time_gemv_rows(arr, 1, dx.p, x.shape[-1], None, 1, dy.p, rows, fused, 0, 1,
+                                            C.byref(ms)))
+    y = dy.download((1, rows))
+    dx.free()
+    dy.free()
+    return y
+
+
+@pytest.mark.parametrize("cols", [64, 448, 1024, 2048, 4160, 8192])
+def test_m1_staged_from_rows(gpu, cols):
+    """q4t M = 1 from an f32 row: the kernel that stages its own operand
+    slices (k_gemv_q4t_m1x, K <= 8192) writes the producer's planes and
+    biases, so its result equals the prepared-operand kernel's bit for bit
+    (both use the same waves x steps instance),
+    and the oracle's within the bar; also with a row max in the last step
+    (the workgroup-wide max must see every wave's columns)"""
+    from cmf_amd import synth
+    t = synth.q4t_uniform(91 + cols, 93, cols)
+    w = gpu.Weight(t["dtype"], 93, cols, payload=t["bytes"])
+    for seed in (0, 1):
+        x = _x(92 + cols + seed, 1, cols)
+        if seed:
+            x[0, cols - 3] = 40.0  # the row max in the last columns
+        fused = _gemv_rows(gpu, w, x, 93, 1)
+        prep = _gemv_rows(gpu, w, x, 93, 0)
+        ref = orc.matmat(t, x, threads=16)
+        err = rel_l2(fused, ref)
+        print(f"q4t 93x{cols} staged-from-rows: rel-L2 {err:.3e}", flush=True)
+        assert err < TOL
+        assert np.array_equal(fused.view(np.uint32), prep.view(np.uint32))
+    w.free()
 
 
 def test_large_batch_split(gpu):
