@@ -18,6 +18,9 @@
 //     -8 * 2^-24 * sum (so D = 2^-24 * sum((n - 8) x) / xs exactly), and the
 //     tile scale multiplies D in f32 as q4t_row_exact does
 //     (qtensor.rs:4418-4432).
+#include <mutex>
+#include <set>
+
 #include "gemv_kern.h"
 #include "runtime.h"
 
@@ -41,13 +44,22 @@ struct GemmArgs {
 constexpr int GB = 64;             // batch rows per workgroup
 constexpr int GCH = 34;            // 1 KiB operand chunks per K step (16 hi + 16 lo items, hi and lo biases)
 constexpr int GJ = (GCH + 3) / 4;  // chunks per wave (clamped)
+constexpr size_t GEMM_AT_BYTES = (size_t)2 * GCH * 64 * 16;  // k_gemm_q4's dynamic LDS
+
+// s_waitcnt lgkmcnt(0) + s_barrier: an LDS-only workgroup barrier (the
+// weight loads in flight are not waited for, as __syncthreads would)
+__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // GRB: row blocks per wave (4 for large batches; 1 gives small batches 4x
 // the workgroups).
 template <int FMT, int GRB>
-__global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
+__global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
     constexpr bool TP = FMT == DT_Q4TP;
-    __shared__ __align__(16) uint4 At[2][GCH * 64];
+    // the double-buffered operand tile [2][GCH chunks][64 lanes] x 16 B,
+    // filled by direct global -> LDS loads (dynamic LDS: with a static array
+    // as the load target the compiler waits for every load in flight before
+    // each LDS read)
+    extern __shared__ __align__(16) uint4 gemm_at[];
     __shared__ float lad[TP ? 4 : 1][TP ? GRB * 16 * 33 : 1];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4;
@@ -71,13 +83,14 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
         const uint4* pb = (const uint4*)((c == 32 ? PB : PB2) + bo);
         return c < 16 ? ph : c < 32 ? pl : pb;
     };
-    // the clamped chunk (the lo biases) is written by every wave with the same data
-    auto dst_a = [&](int j, int buf) __attribute__((always_inline)) -> uint4* {
-        return &At[buf][min(wave + 4 * j, GCH - 1) * 64 + lane];
+    // chunk j of this wave in buffer buf: the wave-uniform 1 KiB it fills
+    // (lane l's 16 bytes land at + 16 l); the clamped chunk (the lo biases)
+    // is written by every wave with the same data
+    auto dma_a = [&](int j, int g, int buf) __attribute__((always_inline)) {
+        uint4* dst = gemm_at + ((size_t)buf * GCH + min(wave + 4 * j, GCH - 1)) * 64;
+        __builtin_amdgcn_global_load_lds((const void*)src_a(j, g), (__attribute__((address_space(3))) void*)dst, 16,
+                                         0, 0);
     };
-#define GEMM_RA(X) X(0) X(1) X(2) X(3) X(4) X(5) X(6) X(7) X(8)
-#define GEMM_LD(J) ra##J = *src_a(J, g_);
-#define GEMM_ST(J) *dst_a(J, buf_) = ra##J;
     // weights of step g for the wave's row blocks (clamped to the last block)
     auto load_w = [&](uint4* wv, uint2* sv, int g) __attribute__((always_inline)) {
 #pragma unroll
@@ -108,20 +121,17 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
 #pragma unroll
         for (int mb = 0; mb < 4; mb++) acc[q][mb] = float4v{0.f, 0.f, 0.f, 0.f};
 
-    static_assert(GJ == 9, "GEMM_RA lists nine chunks");
     const int gs0 = blockIdx.z * a.gsteps, gs1 = min(ntg, gs0 + a.gsteps);  // this part's K steps
-    uint4 ra0, ra1, ra2, ra3, ra4, ra5, ra6, ra7, ra8, wA[GRB], wB[GRB];
+    uint4 wA[GRB], wB[GRB];
     uint2 sA[GRB], sB[GRB];
-    {
-        const int g_ = gs0, buf_ = 0;
-        GEMM_RA(GEMM_LD)
-        load_w(wA, sA, gs0);
-        GEMM_RA(GEMM_ST)
-    }
+#pragma unroll
+    for (int j = 0; j < GJ; j++) dma_a(j, gs0, 0);
+    load_w(wA, sA, gs0);
+    wait_vmcnt<0>();
     __syncthreads();
 
     auto compute = [&](int buf, const uint4* wv, const uint2* sv) __attribute__((always_inline)) {
-        const uint4* A = At[buf];
+        const uint4* A = gemm_at + (size_t)buf * GCH * 64;
         const float4v* Bias = (const float4v*)(A + 32 * 64);   // hi plane's [tile][64 rows] f32
         const float4v* BiasL = (const float4v*)(A + 33 * 64);  // lo plane's
 #pragma unroll 1
@@ -157,30 +167,33 @@ __global__ __launch_bounds__(256) void k_gemm_q4(GemmArgs a) {
         }
     };
 
+    // The next step's operand (into the other buffer, directly) and weights
+    // go out before this step's MFMAs; the wait covers the operand loads only
+    // (the 2 GRB weight loads after them stay in flight), and the barrier
+    // lets every wave's chunks land before they are read and keeps the
+    // buffer being read from being refilled.  Past the last step the loads
+    // repeat it into the buffer no one reads.
     for (int g = gs0; g < gs1; g += 2) {
-        // the next step's operand and weights go out before this step's MFMAs
-        // (past the last step the loads repeat it and are not stored)
         {
-            const int g_ = min(g + 1, gs1 - 1), buf_ = 1;
-            GEMM_RA(GEMM_LD)
+            const int g_ = min(g + 1, gs1 - 1);
+#pragma unroll
+            for (int j = 0; j < GJ; j++) dma_a(j, g_, 1);
             load_w(wB, sB, g_);
             compute(0, wA, sA);
-            if (g + 1 < gs1) { GEMM_RA(GEMM_ST) }
+            wait_vmcnt<2 * GRB>();
         }
-        __syncthreads();
+        lds_sync();
         if (g + 1 >= gs1) break;
         {
-            const int g_ = min(g + 2, gs1 - 1), buf_ = 0;
-            GEMM_RA(GEMM_LD)
+            const int g_ = min(g + 2, gs1 - 1);
+#pragma unroll
+            for (int j = 0; j < GJ; j++) dma_a(j, g_, 0);
             load_w(wA, sA, g_);
             compute(1, wB, sB);
-            if (g + 2 < gs1) { GEMM_RA(GEMM_ST) }
+            wait_vmcnt<2 * GRB>();
         }
-        __syncthreads();
+        lds_sync();
     }
-#undef GEMM_RA
-#undef GEMM_LD
-#undef GEMM_ST
 #pragma unroll
     for (int q = 0; q < GRB; q++) {
         const int n = (rbw + q) * 16 + r;
@@ -455,13 +468,18 @@ int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool res
     const int gx = (a.nrb + rbwg - 1) / rbwg, nz = split((long)gx * (mp / GB), a.ntg);
     if (nz < 0) return fail("gemm: split-K buffer");
     const dim3 grid(gx, mp / GB, nz);
-    if (w.dtype == DT_Q4T) {
-        if (big) hipLaunchKernelGGL((k_gemm_q4<DT_Q4T, 4>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm_q4<DT_Q4T, 1>), grid, dim3(256), 0, st, a);
-    } else {
-        if (big) hipLaunchKernelGGL((k_gemm_q4<DT_Q4TP, 4>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm_q4<DT_Q4TP, 1>), grid, dim3(256), 0, st, a);
+    const void* kf = w.dtype == DT_Q4T ? (big ? (const void*)k_gemm_q4<DT_Q4T, 4> : (const void*)k_gemm_q4<DT_Q4T, 1>)
+                                       : (big ? (const void*)k_gemm_q4<DT_Q4TP, 4> : (const void*)k_gemm_q4<DT_Q4TP, 1>);
+    {
+        // the operand tile's dynamic LDS is above the default 64 KiB limit
+        static std::mutex mu;
+        static std::set<const void*> done;
+        std::lock_guard<std::mutex> g(mu);
+        if (done.insert(kf).second)
+            CMF_HIP(hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)GEMM_AT_BYTES));
     }
+    void* args[] = {&a};
+    CMF_HIP(hipLaunchKernel(kf, grid, dim3(256), args, GEMM_AT_BYTES, st));
     return reduce(nz);
 }
 
