@@ -449,7 +449,7 @@ def main():
     round_bytes = layer_w + lm_w + kv * c["n_layers"] + args.k * (mtp_w + eh_w + lm_w + kv)
     out["prefill"] = {"positions": args.ctx, "ms": round(prefill_s * 1e3, 1),
                       "tok/s": round(args.ctx / prefill_s, 1),
-                      "path": "256-position chunks on the q8 / q4t MFMA GEMMs, tiled causal attention"}
+                      "path": "2048-position chunks on the q8 / q4t MFMA GEMMs, tiled causal attention"}
     out["spec"]["round_hbm_bytes"] = int(round_bytes)
     out["spec"]["round_hbm_GB/s"] = round(round_bytes / (dt / max(args.steps, 1)) / 1e9, 1)
     out["config"] = {"workload": f"spec-verify decode (MTP K={args.k}, greedy) on the synthetic Qwen3-0.6B-arch "

@@ -111,7 +111,7 @@ struct cmf_model_s {
     std::vector<void*> allocs;
     int next_pos_host = 0;
     bool prefilled = false;
-    // prefill chunk buffers [PREFILL_CHUNK rows] (allocated by the first prefill)
+    // prefill chunk buffers [prefill_chunk() rows] (allocated by the first prefill)
     float *pf_h = nullptr, *pf_qkv = nullptr, *pf_ao = nullptr, *pf_gu = nullptr, *pf_hm = nullptr, *pf_q = nullptr;
     int* pf_toks = nullptr;
     _Float16* pf_khl = nullptr;  // the prefill attention's K / V operands (f16 hi / lo keys, then f32 values)
@@ -569,14 +569,24 @@ int ensure_out(cmf_model_s* m, int cap) {
 __global__ void k_set_int(int* p, int v) { *p = v; }
 
 // prompt positions per prefill chunk: every weight is read once per chunk by
-// the large-batch GEMMs (prefill_batch, pipeline.rs:5100-5108)
-constexpr int PREFILL_CHUNK = 256;
+// the large-batch GEMMs (prefill_batch, pipeline.rs:5100-5108), which run
+// far better at m = 2048 than at 256 (2048-position prefill of config 4:
+// 33.9 ms in chunks of 256, 24.9 of 512, 21.7 of 1024, 18.5 of 2048); the
+// CMF_PREFILL_CHUNK environment variable (read once) overrides it
+static int prefill_chunk() {
+    static const int v = [] {
+        const char* e = getenv("CMF_PREFILL_CHUNK");
+        const int c = e ? atoi(e) : 2048;
+        return c >= 16 && c <= 4096 ? c : 2048;
+    }();
+    return v;
+}
 
 int ensure_prefill_bufs(cmf_model_s* m) {
     if (m->pf_h) return CMF_OK;
     const auto& c = m->c;
     const int H = c.hidden, QKV = (c.n_heads + 2 * c.n_kv) * c.head_dim;
-    const size_t R = PREFILL_CHUNK;
+    const size_t R = std::min(prefill_chunk(), c.max_seq);
     if (dalloc_t(m, &m->pf_h, R * H) || dalloc_t(m, &m->pf_qkv, R * QKV) ||
         dalloc_t(m, &m->pf_ao, R * c.n_heads * c.head_dim) || dalloc_t(m, &m->pf_gu, R * 2 * c.inter) ||
         dalloc_t(m, &m->pf_hm, R * H) || dalloc_t(m, &m->pf_toks, R) ||
@@ -965,8 +975,9 @@ int cmf_prefill(cmf_model m, const int32_t* ids, int n) {
     const auto& c = m->c;
     const int H = c.hidden, QKV = (c.n_heads + 2 * c.n_kv) * c.head_dim;
     int* pb = &m->st->next_pos;
-    for (int p0 = 0; p0 < n; p0 += PREFILL_CHUNK) {
-        const int cnt = std::min(PREFILL_CHUNK, n - p0);
+    const int chunk = prefill_chunk();
+    for (int p0 = 0; p0 < n; p0 += chunk) {
+        const int cnt = std::min(chunk, n - p0);
         CMF_HIP(hipMemcpyAsync(m->pf_toks, ids + p0, cnt * sizeof(int), hipMemcpyHostToDevice, s));
         hipLaunchKernelGGL(k_set_int, dim3(1), dim3(1), 0, s, pb, p0);
         launch_embed(m->pf_toks, embed_src(m), H, m->pf_h, H, cnt, s);

@@ -230,9 +230,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
 // ---------------------------------------------------------------------------
 constexpr int Q8CH = 24;              // 1 KiB operand chunks per step
 constexpr int Q8J = Q8CH / 4;         // per wave
+constexpr size_t GEMM_Q8_AT_BYTES = (size_t)2 * Q8CH * 64 * 16;  // k_gemm_q8's dynamic LDS
 template <int Q8RB>
 __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
-    __shared__ __align__(16) int4v At[2][Q8CH * 64];
+    // double-buffered operand tile [2][Q8CH chunks][64 lanes] x 16 B, filled
+    // by direct global -> LDS loads (as k_gemm_q4)
+    extern __shared__ __align__(16) int4v gemm_at8[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, s = lane >> 4;
     const int by = blockIdx.y, rbw = (blockIdx.x * 4 + wave) * Q8RB;
@@ -260,18 +263,24 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
         for (int mb = 0; mb < 4; mb++)
 #pragma unroll
             for (int p = 0; p < 3; p++) acc[q][mb][p] = int4v{0, 0, 0, 0};
-    int4v ra[Q8J], wA[Q8RB][2], wB[Q8RB][2];
+    int4v wA[Q8RB][2], wB[Q8RB][2];
     const int nst = (nk + 1) / 2;
     const int gs0 = blockIdx.z * a.gsteps, gs1 = min(nst, gs0 + a.gsteps);  // this part's K steps
+    auto dma_a = [&](int g, int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gs0));
+        for (int j = 0; j < Q8J; j++) {
+            int4v* dst = gemm_at8 + ((size_t)buf * Q8CH + wave + 4 * j) * 64;
+            __builtin_amdgcn_global_load_lds((const void*)src_a(j, g), (__attribute__((address_space(3))) void*)dst,
+                                             16, 0, 0);
+        }
+    };
+    dma_a(gs0, 0);
     load_w(wA, gs0);
-#pragma unroll
-    for (int j = 0; j < Q8J; j++) At[0][(wave + 4 * j) * 64 + lane] = ra[j];
+    wait_vmcnt<0>();
     __syncthreads();
 
     auto compute = [&](int buf, int4v (*wv)[2], int g) __attribute__((always_inline)) {
-        const int4v* A = At[buf];
+        const int4v* A = gemm_at8 + (size_t)buf * Q8CH * 64;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             if (2 * g + h >= nk) break;  // uniform: an odd chunk count's last step
@@ -289,32 +298,26 @@ __global__ __launch_bounds__(256) void k_gemm_q8(GemmArgs a) {
             }
         }
     };
+    // as k_gemm_q4: the next step's operand straight into the other buffer,
+    // a wait for those loads only, an LDS-only barrier
     for (int g = gs0; g < gs1; g += 2) {
         {
             const int gn = min(g + 1, gs1 - 1);
-#pragma unroll
-            for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gn));
+            dma_a(gn, 1);
             load_w(wB, gn);
             compute(0, wA, g);
-            if (g + 1 < gs1) {
-#pragma unroll
-                for (int j = 0; j < Q8J; j++) At[1][(wave + 4 * j) * 64 + lane] = ra[j];
-            }
+            wait_vmcnt<2 * Q8RB>();
         }
-        __syncthreads();
+        lds_sync();
         if (g + 1 >= gs1) break;
         {
             const int gn = min(g + 2, gs1 - 1);
-#pragma unroll
-            for (int j = 0; j < Q8J; j++) ra[j] = ldg(src_a(j, gn));
+            dma_a(gn, 0);
             load_w(wA, gn);
             compute(1, wB, g + 1);
-            if (g + 2 < gs1) {
-#pragma unroll
-                for (int j = 0; j < Q8J; j++) At[0][(wave + 4 * j) * 64 + lane] = ra[j];
-            }
+            wait_vmcnt<2 * Q8RB>();
         }
-        __syncthreads();
+        lds_sync();
     }
 #pragma unroll
     for (int q = 0; q < Q8RB; q++) {
@@ -458,18 +461,25 @@ int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool res
         const int gx = (a.nrb + rbwg - 1) / rbwg, nz = split((long)gx * (mp / GB), (a.ntg + 1) / 2);
         if (nz < 0) return fail("gemm: split-K buffer");
         const dim3 grid(gx, mp / GB, nz);
-        if (big) hipLaunchKernelGGL((k_gemm_q8<2>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_gemm_q8<1>), grid, dim3(256), 0, st, a);
+        if (big) hipLaunchKernelGGL((k_gemm_q8<2>), grid, dim3(256), GEMM_Q8_AT_BYTES, st, a);
+        else hipLaunchKernelGGL((k_gemm_q8<1>), grid, dim3(256), GEMM_Q8_AT_BYTES, st, a);
         return reduce(nz);
     }
     // four row blocks per wave once that still leaves ~4 workgroups per CU
     const bool big = (long)((a.nrb + 15) / 16) * (mp / GB) >= 1024;
-    const int rbwg = big ? 16 : 4;
+    // two row blocks per wave (half the operand re-reads) while that still
+    // gives >= 384 workgroups: measured 12288x4096 m=256 160 -> 126 us, but
+    // 6144x1024 m=256 (192 workgroups) 30.7 -> 38.8 us
+    const int grb_small = !big && (long)((a.nrb + 7) / 8) * (mp / GB) >= 384 ? 2 : 1;
+    const int rbwg = big ? 16 : 4 * grb_small;
     const int gx = (a.nrb + rbwg - 1) / rbwg, nz = split((long)gx * (mp / GB), a.ntg);
     if (nz < 0) return fail("gemm: split-K buffer");
     const dim3 grid(gx, mp / GB, nz);
-    const void* kf = w.dtype == DT_Q4T ? (big ? (const void*)k_gemm_q4<DT_Q4T, 4> : (const void*)k_gemm_q4<DT_Q4T, 1>)
-                                       : (big ? (const void*)k_gemm_q4<DT_Q4TP, 4> : (const void*)k_gemm_q4<DT_Q4TP, 1>);
+    const void* kf = w.dtype == DT_Q4T
+                         ? (big ? (const void*)k_gemm_q4<DT_Q4T, 4>
+                                : (grb_small == 2 ? (const void*)k_gemm_q4<DT_Q4T, 2> : (const void*)k_gemm_q4<DT_Q4T, 1>))
+                         : (big ? (const void*)k_gemm_q4<DT_Q4TP, 4>
+                                : (grb_small == 2 ? (const void*)k_gemm_q4<DT_Q4TP, 2> : (const void*)k_gemm_q4<DT_Q4TP, 1>));
     {
         // the operand tile's dynamic LDS is above the default 64 KiB limit
         static std::mutex mu;

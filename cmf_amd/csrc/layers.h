@@ -78,7 +78,7 @@ struct PrefillAttnArgs {
     unsigned long long tag;
     bool allow_xcd;
 };
-constexpr int PREFILL_XCD_CELLS = 8 * 256;  // query blocks of a 256-row chunk x 8 kv heads
+constexpr int PREFILL_XCD_CELLS = 8 * 1024;  // query blocks of a chunk x 8 kv heads (2048 rows at 2 per block)
 bool prefill_attention_fits(int nh, int nkv, int hd);
 int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st);
 // The lexicographic (value, index) maximum step of argmax (sampler.rs:1130-1154

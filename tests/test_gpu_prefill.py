@@ -1,10 +1,11 @@
 """Prefill on the large-batch MFMA GEMMs (prefill_batch, pipeline.rs:5100-5108):
-256-position chunks, each weight read once per chunk by the q8 (attention,
-eh_proj) and q4t (FFN) GEMMs with the RMSNorm / SwiGLU / MTP-concat operand
-producers, residual adds in the GEMM epilogue.  The trunk KV of every layer,
-the MTP KV of the (h_p, id_{p+1}) warm pairs and the tip hidden equal the
-oracle's per-position forwards within relative L2 1e-4, over three chunks
-(256 + 256 + 88 rows)."""
+chunks of up to 2048 positions (CMF_PREFILL_CHUNK), each weight read once per
+chunk by the q8 (attention, eh_proj) and q4t (FFN) GEMMs with the RMSNorm /
+SwiGLU / MTP-concat operand producers, residual adds in the GEMM epilogue.
+The trunk KV of every layer, the MTP KV of the (h_p, id_{p+1}) warm pairs and
+the tip hidden equal the oracle's per-position forwards within relative L2
+1e-4, in one chunk and (child processes with smaller chunks) over two and
+three chunks (256 + 256 + 88 rows)."""
 import numpy as np
 import pytest
 
@@ -56,7 +57,7 @@ CFG4 = dict(n_layers=2, hidden=1024, n_heads=16, n_kv=8, head_dim=128, inter=307
 
 def test_prefill_config4_block_shape_equals_oracle(gpu):
     """BASELINE config 4's block shape (hidden 1024, 16 query / 8 KV heads of
-    128, FFN 3072) at its 2048-position context: 8 chunks of 256 on the
+    128, FFN 3072) at its 2048-position context: one 2048-row chunk on the
     GEMMs and the tiled prefill attention with one KV head per XCD, the
     same kernels config 4 runs.  The KV of both layers, the MTP KV of the
     warm pairs and the tip equal the oracle's per-position forwards; every
@@ -154,3 +155,57 @@ def test_prefill_placement_check_falls_back(gpu, forced):
     res = json.loads(r.stdout.strip().splitlines()[-1])
     assert res["xcd"] == (0 if forced else 1)
     assert res["tip"] < 1e-4 and res["k"] < 1e-4 and res["v"] < 1e-4
+
+
+_CHUNK_CHILD = r"""
+import sys, json
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import cmf_amd
+from cmf_amd import synth
+from cmf_amd.model import Model
+from oracle import oracle as orc
+cmf_amd.init(0)
+cfg = dict(n_layers=2, hidden=256, n_heads=4, n_kv=2, head_dim=128, inter=512, vocab=4096, max_seq=640,
+           rope_theta=1e6, eps=1e-6)
+sm = synth.synth_model(cfg, seed=21, norm_noise=0.1, sigma=0.05)
+g = Model(sm)
+prompt = synth.ids(22, 600, cfg["vocab"])
+g.prefill(prompt)
+o = orc.OracleModel(sm, threads=8)
+otip = o.prefill(prompt)
+_, tip = g.state()
+rel = lambda a, b: float(np.linalg.norm(a - b) / np.linalg.norm(b))
+out = {"tip": rel(tip, otip)}
+for li in (0, 1, -1):
+    k, v = g.kv_export(li, 600 if li >= 0 else 599)
+    rk, rv = o.kv(li)
+    out[f"k{li}"], out[f"v{li}"] = rel(k, rk), rel(v, rv)
+    out[f"klast{li}"] = rel(k[:, 512:], rk[:, 512:])
+gt, _ = g.decode(6, spec=True, k=4)
+ot, _ = o.decode(otip, 600, prompt, 6, spec=True, k=4)
+out["tokens_equal"] = gt.tolist() == ot.tolist()
+print(json.dumps(out))
+"""
+
+
+@pytest.mark.parametrize("chunk", [256, 512])
+def test_prefill_multi_chunk(gpu, chunk):
+    """The 600-position prefill in chunks of 256 (three: 256 + 256 + 88) and
+    512 (two): the chunk boundaries (positions, the causal attention over the
+    cached rows, the MTP warm pair across a boundary) give the oracle's KV,
+    tip and decode tokens (a child process: the chunk size is read once per
+    process)"""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, CMF_PREFILL_CHUNK=str(chunk))
+    r = subprocess.run([sys.executable, "-c", _CHUNK_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    assert res.pop("tokens_equal")
+    assert max(res.values()) < 1e-4, res
