@@ -3,6 +3,7 @@
 #include <mutex>
 
 #include "gemv_kern.h"
+#include "prep_src.h"
 
 namespace cmf {
 
@@ -26,89 +27,7 @@ __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk
         planes += j * planes_stride;
         xs += 16 * j;
     }
-    __shared__ double red1[8], red2[8];
-    __shared__ float redm[8];
-    const int b = blockIdx.x, tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6;
-    const int nw = nt >> 6;
-    const bool nrm = s.mode == XS_NORM || s.mode == XS_CAT;
-    const int H = s.mode == XS_CAT ? s.H : K;
-    const float* row = s.x + (size_t)b * s.ldx;
-    int tok = 0, rb = 0, r = 0;
-    float rs = 0.f;
-    bool tv = false;
-    if (s.mode == XS_CAT) {
-        tok = s.toks[b];
-        tv = tok >= 0 && tok < s.emb.rows;
-        rb = tok >> 4;
-        r = tok & 15;
-        rs = tv ? s.emb.rs[tok] : 0.f;
-    }
-    double s1 = 0.0, s2 = 0.0;
-    for (int i = tid; i < K; i += nt) {
-        float v;
-        if (s.mode == XS_SILU) {
-            const float g = row[i], u = row[s.K + i];
-            v = (g / (1.0f + expf(-g))) * u;
-        } else if (s.mode == XS_SILU8) {
-            const int o = 16 * (i >> 3) + (i & 7);
-            const float g = row[o], u = row[o + 8];
-            v = (g / (1.0f + expf(-g))) * u;
-        } else if (s.mode == XS_CAT) {
-            if (i < H) {
-                // int8 of the token's row in the q8 device layout, times its row scale
-                const int kc = i >> 6, sl = (i >> 4) & 3, jj = i & 15;
-                const int8_t q = tv ? s.emb.w[(((size_t)rb * s.emb.nkc + kc) * 64 + 16 * sl + r) * 16 + jj] : 0;
-                v = (float)q * rs;
-            } else {
-                v = row[i - H];
-            }
-        } else {
-            v = row[i];
-        }
-        vals[i] = v;
-        if (nrm) {
-            if (i < H) s1 += (double)v * (double)v;
-            else s2 += (double)v * (double)v;
-        }
-    }
-    if (nrm) {
-        for (int o = 32; o > 0; o >>= 1) {
-            s1 += __shfl_xor(s1, o);
-            s2 += __shfl_xor(s2, o);
-        }
-        if (lane == 0) {
-            red1[wave] = s1;
-            red2[wave] = s2;
-        }
-    }
-    __syncthreads();
-    float am = 0.f;
-    if (nrm) {
-        double t1 = 0.0, t2 = 0.0;
-        for (int q = 0; q < nw; q++) {
-            t1 += red1[q];
-            t2 += red2[q];
-        }
-        const float inv1 = 1.0f / (float)sqrt(t1 / (double)H + s.eps);
-        const float inv2 = s.mode == XS_CAT ? 1.0f / (float)sqrt(t2 / (double)(K - H) + s.eps) : 1.f;
-        for (int i = tid; i < K; i += nt) {
-            const float y = i < H ? vals[i] * inv1 * s.w[i] : vals[i] * inv2 * s.w2[i - H];
-            vals[i] = y;
-            am = fmaxf(am, fabsf(y));
-        }
-    } else {
-        for (int i = tid; i < K; i += nt) am = fmaxf(am, fabsf(vals[i]));
-    }
-    for (int o = 32; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o));
-    if (lane == 0) redm[wave] = am;
-    __syncthreads();
-    am = 0.f;
-    for (int q = 0; q < nw; q++) am = fmaxf(am, redm[q]);
-    // row stride of the planes: the batch (GEMV operands) or a padded row
-    // count (GEMM operands, whose tile biases share that stride)
-    const int ms = mstride ? mstride : gridDim.x;
-    if (fmt == DT_Q8ROW) prep8_row(vals, K, am, nk, b, ms, planes, xs, tid, nt);
-    else prep16_row(vals, K, am, nk, b, ms, planes, xs, tid, nt, mstride ? mstride : 16);
+    prep_src_row(s, K, fmt, nk, planes, xs, mstride, blockIdx.x, gridDim.x, vals);
 }
 
 // The a8w8 operand (split_act, qtensor.rs:9237-9281) of row b of x: rms =

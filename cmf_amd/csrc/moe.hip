@@ -26,6 +26,7 @@
 #include "../../include/cmf_hip.h"
 #include "common.h"
 #include "gemv.h"
+#include "prep_src.h"
 #include "runtime.h"
 #include "wave.h"
 
@@ -160,6 +161,25 @@ __global__ __launch_bounds__(1024) void k_moe_route_jobs(const float* __restrict
     moe_jobs_body(sidx, b, k, ne, jobs, slot);
 }
 
+// Routing + job numbering (workgroup b) and the gate|up operand of the b
+// token rows (workgroups 0 .. b-1, the producer src) in one launch: the two
+// are independent, and each was a launch of its own in the chain before the
+// expert GEMVs.  1024 threads (one wave per token slot for the routing).
+__global__ __launch_bounds__(1024) void k_moe_route_prep(const float* __restrict__ logits, int b, int ne, int k,
+                                                        int norm_topk, float scaling, int* __restrict__ idx,
+                                                        float* __restrict__ w, int* __restrict__ jobs,
+                                                        int* __restrict__ slot, XSrc src, int K, int fmt, int nk,
+                                                        uint8_t* __restrict__ planes, float* __restrict__ xs) {
+    extern __shared__ float vals[];  // K (the operand workgroups)
+    __shared__ int sidx[MAXB * MOE_MAX_TOPK];
+    if ((int)blockIdx.x < b) {
+        prep_src_row(src, K, fmt, nk, planes, xs, 0, blockIdx.x, b, vals);
+        return;
+    }
+    moe_route_tokens(logits, b, ne, k, norm_topk, scaling, idx, w, sidx);
+    moe_jobs_body(sidx, b, k, ne, jobs, slot);
+}
+
 // out[t][h] = sum over ranks i (in order, from 0) of w[t][i] * yd[job][t][h];
 // grid (hidden / 256, b): the k job rows of a thread are requested together.
 __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ yd, size_t y_stride, int ldy,
@@ -234,10 +254,10 @@ static int moe_ready(cmf_moe m) {
 // x: the operand producer of the token rows (plain rows, or the block's
 // RMSNorm of the residual); out rows [b][ldo], resid: out += the FFN.
 static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int ldo, bool resid, hipStream_t s,
-                       bool numbered) {
+                       bool numbered, bool prepared = false) {
     const int H = m->hidden, I = m->inter;
     if (!numbered) hipLaunchKernelGGL(k_moe_jobs, dim3(1), dim3(256), 0, s, m->idx, b, k, m->ne, m->jobs, m->slot);
-    int rc = launch_prep_src(m->gu[0], x, b, m->px, m->xsx, s);
+    int rc = prepared ? CMF_OK : launch_prep_src(m->gu[0], x, b, m->px, m->xsx, s);
     const int mj = std::min(m->max_jobs, b * k);
     const size_t ygu_stride = (size_t)MAXB * 2 * I, yd_stride = (size_t)MAXB * H;
     if (rc == CMF_OK)
@@ -272,9 +292,23 @@ int cmf::moe_experts_count(cmf_moe m) { return m ? m->ne : 0; }
 int cmf::moe_ffn_launch(cmf_moe m, const XSrc& x, const float* d_logits, int b, float* d_out, int ldo, bool resid,
                    hipStream_t s) {
     if (b < 1 || b > MAXB) return fail("moe: batch must be 1..16");
-    hipLaunchKernelGGL(k_moe_route_jobs, dim3(1), dim3(64 * MAXB), 0, s, d_logits, b, m->ne, m->top_k, m->norm_topk,
-                       m->scaling, m->idx, m->w, m->jobs, m->slot);
-    return moe_experts(m, x, b, m->top_k, d_out, ldo, resid, s, true);
+    const DevWeight& g = m->gu[0];
+    const int K = x.K ? x.K : g.cols;
+    if (K < 1 || K > g.cols || K > 16384 || (x.mode == XS_CAT && (x.H < 1 || x.H >= K)))
+        return fail("moe: bad operand producer");
+    const int nk = g.dtype == DT_Q8ROW ? g.kchunks : g.kchunks * 4;
+    static const bool attr = [] {
+        // the routing arrays' static LDS plus the operand row's K floats
+        hipFuncAttributes fa{};
+        const size_t st = hipFuncGetAttributes(&fa, (const void*)k_moe_route_prep) == hipSuccess ? fa.sharedSizeBytes : 0;
+        return hipFuncSetAttribute((const void*)k_moe_route_prep, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)(160 * 1024 - st)) == hipSuccess;
+    }();
+    (void)attr;
+    hipLaunchKernelGGL(k_moe_route_prep, dim3(b + 1), dim3(64 * MAXB), (size_t)K * sizeof(float), s, d_logits, b,
+                       m->ne, m->top_k, m->norm_topk, m->scaling, m->idx, m->w, m->jobs, m->slot, x, K, g.dtype, nk,
+                       m->px, m->xsx);
+    return moe_experts(m, x, b, m->top_k, d_out, ldo, resid, s, true, true);
 }
 
 extern "C" {
