@@ -44,7 +44,9 @@ struct GemmArgs {
 constexpr int GB = 64;             // batch rows per workgroup
 constexpr int GCH = 34;            // 1 KiB operand chunks per K step (16 hi + 16 lo items, hi and lo biases)
 constexpr int GJ = (GCH + 3) / 4;  // chunks per wave (clamped)
-constexpr size_t GEMM_AT_BYTES = (size_t)2 * GCH * 64 * 16;  // k_gemm_q4's dynamic LDS
+// k_gemm_q4's dynamic LDS: the operand tile [2][GCH][64] x 16 B, then the
+// weight rows' tile scales [2][4 waves] x 1 KiB
+constexpr size_t GEMM_AT_BYTES = (size_t)2 * GCH * 64 * 16 + (size_t)2 * 4 * 1024;
 
 // s_waitcnt lgkmcnt(0) + s_barrier: an LDS-only workgroup barrier (the
 // weight loads in flight are not waited for, as __syncthreads would)
@@ -92,13 +94,31 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
                                          0, 0);
     };
     // weights of step g for the wave's row blocks (clamped to the last block)
-    auto load_w = [&](uint4* wv, uint2* sv, int g) __attribute__((always_inline)) {
+    auto load_w = [&](uint4* wv, int g) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < GRB; q++) {
             const size_t t = (size_t)min(rbw + q, a.nrb - 1) * ntg + g;
             wv[q] = ((const uint4*)a.w)[t * 64 + lane];
-            if constexpr (TP) sv[q] = make_uint2(((const uint32_t*)a.scale)[t * 16 + r], 0u);
-            else sv[q] = ((const uint2*)a.scale)[t * 16 + r];
+        }
+    };
+    // the tile scales of step g for the wave's rows into its 1 KiB of the
+    // scale area (buffer buf) by one direct load: q4t 16 B per lane = two
+    // rows' four f16 scales, lane l -> row block l / 8, rows 2 (l % 8) ..;
+    // q4tp 4 B per lane = one row's four rung codes, lane l -> row block
+    // l / 16, row l % 16 (lanes past the wave's rows repeat the last block)
+    uint8_t* sarea = (uint8_t*)(gemm_at + (size_t)2 * GCH * 64);
+    auto dma_s = [&](int g, int buf) __attribute__((always_inline)) {
+        uint8_t* dst = sarea + (size_t)(buf * 4 + wave) * 1024;
+        if constexpr (TP) {
+            const int q = min(lane >> 4, GRB - 1);
+            const size_t t = (size_t)min(rbw + q, a.nrb - 1) * ntg + g;
+            __builtin_amdgcn_global_load_lds((const void*)((const uint32_t*)a.scale + t * 16 + (lane & 15)),
+                                             (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+        } else {
+            const int q = min(lane >> 3, GRB - 1);
+            const size_t t = (size_t)min(rbw + q, a.nrb - 1) * ntg + g;
+            __builtin_amdgcn_global_load_lds((const void*)((const uint2*)a.scale + t * 16 + 2 * (lane & 7)),
+                                             (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
         }
     };
     if constexpr (TP) {  // 32-rung ladders of the wave's rows (quant.rs:399-410)
@@ -123,15 +143,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
 
     const int gs0 = blockIdx.z * a.gsteps, gs1 = min(ntg, gs0 + a.gsteps);  // this part's K steps
     uint4 wA[GRB], wB[GRB];
-    uint2 sA[GRB], sB[GRB];
 #pragma unroll
     for (int j = 0; j < GJ; j++) dma_a(j, gs0, 0);
-    load_w(wA, sA, gs0);
+    dma_s(gs0, 0);
+    load_w(wA, gs0);
     wait_vmcnt<0>();
     __syncthreads();
 
-    auto compute = [&](int buf, const uint4* wv, const uint2* sv) __attribute__((always_inline)) {
+    auto compute = [&](int buf, const uint4* wv) __attribute__((always_inline)) {
         const uint4* A = gemm_at + (size_t)buf * GCH * 64;
+        // this step's scale words of the lane's rows in LDS (q4t: [q][r] four
+        // f16; q4tp: [q][r] u32 of four 5-bit codes), read per tile
+        const uint8_t* sb = sarea + (size_t)(buf * 4 + wave) * 1024;
         const float4v* Bias = (const float4v*)(A + 32 * 64);   // hi plane's [tile][64 rows] f32
         const float4v* BiasL = (const float4v*)(A + 33 * 64);  // lo plane's
 #pragma unroll 1
@@ -143,10 +166,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
                 const uint32_t wd = t == 0 ? wv[q].x : t == 1 ? wv[q].y : t == 2 ? wv[q].z : wv[q].w;
                 bq[q] = dq_nib_word(wd);
                 if constexpr (TP) {
-                    sc[q] = lad[wave][(q * 16 + r) * 33 + ((sv[q].x >> (5 * t)) & 31)];
+                    const uint32_t code = ((const uint32_t*)sb)[q * 16 + r];
+                    sc[q] = lad[wave][(q * 16 + r) * 33 + ((code >> (5 * t)) & 31)];
                 } else {
-                    const uint32_t h = t < 2 ? sv[q].x : sv[q].y;
-                    sc[q] = f16_bits_to_f32((t & 1) ? h >> 16 : h & 0xFFFFu);
+                    sc[q] = f16_bits_to_f32(((const uint16_t*)sb)[(q * 16 + r) * 4 + t]);
                 }
             }
 #pragma unroll
@@ -167,9 +190,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
         }
     };
 
-    // The next step's operand (into the other buffer, directly) and weights
-    // go out before this step's MFMAs; the wait covers the operand loads only
-    // (the 2 GRB weight loads after them stay in flight), and the barrier
+    // The next step's operand and tile scales (into the other buffer,
+    // directly) and weights go out before this step's MFMAs; the wait covers
+    // the direct loads only (the GRB weight loads after them stay in flight), and the barrier
     // lets every wave's chunks land before they are read and keeps the
     // buffer being read from being refilled.  Past the last step the loads
     // repeat it into the buffer no one reads.
@@ -178,9 +201,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
             const int g_ = min(g + 1, gs1 - 1);
 #pragma unroll
             for (int j = 0; j < GJ; j++) dma_a(j, g_, 1);
-            load_w(wB, sB, g_);
-            compute(0, wA, sA);
-            wait_vmcnt<2 * GRB>();
+            dma_s(g_, 1);
+            load_w(wB, g_);
+            compute(0, wA);
+            wait_vmcnt<GRB>();
         }
         lds_sync();
         if (g + 1 >= gs1) break;
@@ -188,9 +212,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q4(GemmArgs a) {
             const int g_ = min(g + 2, gs1 - 1);
 #pragma unroll
             for (int j = 0; j < GJ; j++) dma_a(j, g_, 0);
-            load_w(wA, sA, g_);
-            compute(1, wB, sB);
-            wait_vmcnt<2 * GRB>();
+            dma_s(g_, 0);
+            load_w(wA, g_);
+            compute(1, wB);
+            wait_vmcnt<GRB>();
         }
         lds_sync();
     }
