@@ -114,9 +114,10 @@ __global__ __launch_bounds__(64) void k_prefill_qk(const float* __restrict__ qkv
 //   kop [nkv][npad / 16][8 chunks][64 lanes] x 16 B: key block kb (keys
 //       16 kb + r), chunk ch = 2 ks + plane (f16 hi / lo), lane 16 s + r:
 //       dims 32 ks + 8 s .. + 7 of key 16 kb + r;
-//   vop [nkv][npad / 64][8 dim blocks][4][64 lanes] x 16 B: key block kb
-//       (keys 64 kb ..), dim block db, step i, lane 16 s + r: keys
-//       64 kb + 16 s + 4 i .. + 3 of dim 16 db + r.
+//   vop [nkv][npad / 64][8 dim blocks][2 k-steps][2 planes][64 lanes] x
+//       16 B: key block kb (keys 64 kb ..), dim block db, k-step ks, plane
+//       (f16 hi / lo), lane 16 s + r: keys 64 kb + 32 ks + 8 s .. + 7 of
+//       dim 16 db + r (the B operand of the values' f16 MFMA).
 // grid (npad / 64, nkv), 256 threads: 64 keys through LDS.
 __global__ __launch_bounds__(256) void k_prefill_kv(const float* __restrict__ kc, const float* __restrict__ vc,
                                                     int max_seq, int n, int npad, int4v* __restrict__ kop,
@@ -149,13 +150,18 @@ __global__ __launch_bounds__(256) void k_prefill_kv(const float* __restrict__ kc
         }
         kop[(((size_t)g * nkb + 4 * kb64 + kb) * 8 + ch) * 64 + l] = __builtin_bit_cast(int4v, h);
     }
-    // V: 8 dim blocks x 4 steps x 64 lanes
+    // V: 8 dim blocks x (2 k-steps x 2 planes) x 64 lanes
     for (int e = t; e < 8 * 4 * 64; e += 256) {
         const int l = e & 63, i = (e >> 6) & 3, db = e >> 8, r = l & 15, sl = l >> 4;
-        float4v v;
+        const int ks = i >> 1, plane = i & 1;
+        half8 h;
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = VS[16 * sl + 4 * i + j][16 * db + r];
-        vop[(((size_t)g * nvb + kb64) * 8 + db) * 4 * 64 + i * 64 + l] = v;
+        for (int j = 0; j < 8; j++) {
+            _Float16 hh, ll;
+            split16(VS[32 * ks + 8 * sl + j][16 * db + r], hh, ll);
+            h[j] = plane ? ll : hh;
+        }
+        vop[(((size_t)g * nvb + kb64) * 8 + db) * 4 * 64 + i * 64 + l] = __builtin_bit_cast(float4v, h);
     }
 }
 
@@ -288,8 +294,11 @@ __global__ __launch_bounds__(512) void k_prefill_attn(const float* __restrict__ 
             }
         }
         lds_barrier();
-        // values: output dims 32 wl + 16 tt + r, rows 4 s + e; MFMA step kk
-        // takes key 16 s + kk of the group (lane s), as the operand layout
+        // values: output dims 32 wl + 16 tt + r, rows 4 s + e, on the f16
+        // MFMA (16x16x32) in two k-steps of 32 keys: the weights p of row r,
+        // keys 32 ks + 8 s .., and V split into f16 hi / lo halves, three
+        // products ph vh + ph vl + pl vh (22-bit operands, f32 sums) into
+        // o[tt + 2 ks] (v[tt * 4 + ks * 2 + plane], the operand layout)
         {
             float al[4];
 #pragma unroll
@@ -298,15 +307,27 @@ __global__ __launch_bounds__(512) void k_prefill_attn(const float* __restrict__ 
             for (int tt = 0; tt < 4; tt++)
 #pragma unroll
                 for (int e = 0; e < 4; e++) o[tt][e] *= al[e];
-            float4v pa[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) pa[i] = *(const float4v*)&P[G][r][16 * s + 4 * i];
+            for (int ks = 0; ks < GK / 32; ks++) {
+                const float4v p0 = *(const float4v*)&P[G][r][32 * ks + 8 * s];
+                const float4v p1 = *(const float4v*)&P[G][r][32 * ks + 8 * s + 4];
+                half8 ph, pl;
 #pragma unroll
-            for (int kk = 0; kk < GK / 4; kk++) {
-                const float a = pa[kk >> 2][kk & 3];
-                o[(kk & 1) * 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, v[kk >> 2][kk & 3], o[(kk & 1) * 2], 0, 0, 0);
-                o[(kk & 1) * 2 + 1] =
-                    __builtin_amdgcn_mfma_f32_16x16x4f32(a, v[4 + (kk >> 2)][kk & 3], o[(kk & 1) * 2 + 1], 0, 0, 0);
+                for (int j = 0; j < 8; j++) {
+                    _Float16 hh, ll;
+                    split16(j < 4 ? p0[j] : p1[j - 4], hh, ll);
+                    ph[j] = hh;
+                    pl[j] = ll;
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    const half8 vh = __builtin_bit_cast(half8, v[tt * 4 + ks * 2]);
+                    const half8 vl = __builtin_bit_cast(half8, v[tt * 4 + ks * 2 + 1]);
+                    float4v& acc = o[tt + 2 * ks];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vh, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vl, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vh, acc, 0, 0, 0);
+                }
             }
         }
     };
