@@ -1154,10 +1154,15 @@ inline GemvKernel q4t_m1_inst(bool resid, int* ks, size_t* lds) {
     return resid ? k_gemv_q4t_m1<KS, SPW, true> : k_gemv_q4t_m1<KS, SPW, false>;
 }
 inline GemvKernel q8_m1_pick(int nk, bool resid, int* ks, size_t* lds) {
+    // (measured on MI355X, 10 weight copies rotating: more waves with fewer
+    // steps each pay up to 64 steps: 4096x1024 (16 steps) 2.71 -> 2.44 us
+    // at 8 x 2, the 151936x1024 lm_head 25.7 -> 24.9 us, 1024x2048 2.46 ->
+    // 2.16 us at 8 x 4, 4096x4096 4.72 -> 4.42 us at 16 x 4; for q4t the
+    // table below was already the fastest of the shapes tried)
     if (nk <= 8) return q8_m1_inst<1, 8>(resid, ks, lds);
-    if (nk <= 16) return q8_m1_inst<2, 8>(resid, ks, lds);
-    if (nk <= 32) return q8_m1_inst<4, 8>(resid, ks, lds);
-    if (nk <= 64) return q8_m1_inst<8, 8>(resid, ks, lds);
+    if (nk <= 16) return q8_m1_inst<8, 2>(resid, ks, lds);
+    if (nk <= 32) return q8_m1_inst<8, 4>(resid, ks, lds);
+    if (nk <= 64) return q8_m1_inst<16, 4>(resid, ks, lds);
     if (nk <= 128) return q8_m1_inst<16, 8>(resid, ks, lds);
     if (nk <= 192) return q8_m1_inst<16, 12>(resid, ks, lds);
     return nullptr;

@@ -81,7 +81,7 @@ def test_ragged_shapes(gpu):
     _check(gpu, synth.q4t_uniform(67, 1, 32), _x(68, 1, 32))
 
 
-@pytest.mark.parametrize("cols", [64, 448, 1024, 2048, 4160, 8192, 12288, 16384])
+@pytest.mark.parametrize("cols", [64, 448, 1024, 2048, 2112, 4096, 4160, 8192, 12288, 16384])
 def test_m1_kernel_instances(gpu, cols):
     """M = 1 runs the per-wave operand-slice kernels (k_gemv_q8_m1 over a
     prepared operand; q4t through the seam: k_gemv_q4t_m1x staging its own
