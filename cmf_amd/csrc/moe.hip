@@ -21,11 +21,14 @@
 //   6. down           grouped GEMV: job j = W_down[e_j] h_j.
 //   7. k_moe_combine  out[t] = sum over ranks i of w[t][i] * down[job(t, i)][t],
 //                     accumulated from 0 in rank order, as the reference does.
+#include <map>
+#include <mutex>
 #include <vector>
 
 #include "../../include/cmf_hip.h"
 #include "common.h"
 #include "gemv.h"
+#include "gemv_kern.h"
 #include "prep_src.h"
 #include "runtime.h"
 #include "wave.h"
@@ -34,6 +37,7 @@ namespace cmf {
 
 constexpr int MOE_MAX_EXPERTS = 1024;
 constexpr int MOE_MAX_TOPK = 32;
+constexpr int MOE_JT = 1 + MAXB;  // job token list: count, then the tokens
 
 // Routing of token t by wave t (b <= 16 waves, all tokens at once): softmax
 // of the router logits (max-subtracted; the sum sequential in expert order,
@@ -108,20 +112,20 @@ __device__ __forceinline__ void moe_route_tokens(const float* __restrict__ logit
 // slot[t * k + i] = job of token t's rank-i expert.  One workgroup of 256:
 // per-wave ballots and popcounts number the used experts.
 __device__ __forceinline__ void moe_jobs_body(const int* idx, int b, int k, int ne, int* __restrict__ jobs,
-                                              int* __restrict__ slot) {
+                                              int* __restrict__ slot, int* __restrict__ jt) {
     __shared__ int job_of[MOE_MAX_EXPERTS];
-    __shared__ int used[MOE_MAX_EXPERTS];
+    __shared__ unsigned used[MOE_MAX_EXPERTS];  // bit t: token t picked the expert
     __shared__ int wave_base[MOE_MAX_EXPERTS / 64 + 1];
     const int tid = threadIdx.x, lane = tid & 63;
-    for (int e = tid; e < ne; e += blockDim.x) used[e] = 0;
+    for (int e = tid; e < ne; e += blockDim.x) used[e] = 0u;
     __syncthreads();
-    for (int i = tid; i < b * k; i += blockDim.x) used[idx[i]] = 1;  // benign same-value races
+    for (int i = tid; i < b * k; i += blockDim.x) atomicOr(&used[idx[i]], 1u << (i / k));
     __syncthreads();
     // expert e sits in chunk e / 64, lane e % 64; chunk c is counted by wave c % 4
     const int nch = (ne + 63) / 64;
     for (int c = tid >> 6; c < nch; c += blockDim.x >> 6) {
         const int e = c * 64 + lane;
-        const bool u = e < ne && used[e];
+        const bool u = e < ne && used[e] != 0u;
         const unsigned long long bal = __ballot(u);
         if (lane == 0) wave_base[c] = __popcll(bal);
         if (e < ne) job_of[e] = u ? (int)__popcll(bal & ((1ull << lane) - 1ull)) : -1;
@@ -141,24 +145,22 @@ __device__ __forceinline__ void moe_jobs_body(const int* idx, int b, int k, int 
         if (job_of[e] >= 0) {
             job_of[e] += wave_base[e >> 6];
             jobs[1 + job_of[e]] = e;
+            // the job's tokens in increasing order
+            int* l = jt + (size_t)job_of[e] * MOE_JT;
+            unsigned msk = used[e];
+            l[0] = __popc(msk);
+            for (int n = 1; msk; n++) {
+                l[n] = __ffs(msk) - 1;
+                msk &= msk - 1u;
+            }
         }
     }
     __syncthreads();
     for (int i = tid; i < b * k; i += blockDim.x) slot[i] = job_of[idx[i]];
 }
 __global__ __launch_bounds__(256) void k_moe_jobs(const int* __restrict__ idx, int b, int k, int ne,
-                                                  int* __restrict__ jobs, int* __restrict__ slot) {
-    moe_jobs_body(idx, b, k, ne, jobs, slot);
-}
-// Routing of the b tokens and their job numbering in one launch (one
-// workgroup, one wave per token slot).
-__global__ __launch_bounds__(1024) void k_moe_route_jobs(const float* __restrict__ logits, int b, int ne, int k,
-                                                        int norm_topk, float scaling, int* __restrict__ idx,
-                                                        float* __restrict__ w, int* __restrict__ jobs,
-                                                        int* __restrict__ slot) {
-    __shared__ int sidx[MAXB * MOE_MAX_TOPK];
-    moe_route_tokens(logits, b, ne, k, norm_topk, scaling, idx, w, sidx);
-    moe_jobs_body(sidx, b, k, ne, jobs, slot);
+                                                  int* __restrict__ jobs, int* __restrict__ slot, int* __restrict__ jt) {
+    moe_jobs_body(idx, b, k, ne, jobs, slot, jt);
 }
 
 // Routing + job numbering (workgroup b) and the gate|up operand of the b
@@ -168,8 +170,9 @@ __global__ __launch_bounds__(1024) void k_moe_route_jobs(const float* __restrict
 __global__ __launch_bounds__(1024) void k_moe_route_prep(const float* __restrict__ logits, int b, int ne, int k,
                                                         int norm_topk, float scaling, int* __restrict__ idx,
                                                         float* __restrict__ w, int* __restrict__ jobs,
-                                                        int* __restrict__ slot, XSrc src, int K, int fmt, int nk,
-                                                        uint8_t* __restrict__ planes, float* __restrict__ xs) {
+                                                        int* __restrict__ slot, int* __restrict__ jt, XSrc src, int K,
+                                                        int fmt, int nk, uint8_t* __restrict__ planes,
+                                                        float* __restrict__ xs) {
     extern __shared__ float vals[];  // K (the operand workgroups)
     __shared__ int sidx[MAXB * MOE_MAX_TOPK];
     if ((int)blockIdx.x < b) {
@@ -177,7 +180,7 @@ __global__ __launch_bounds__(1024) void k_moe_route_prep(const float* __restrict
         return;
     }
     moe_route_tokens(logits, b, ne, k, norm_topk, scaling, idx, w, sidx);
-    moe_jobs_body(sidx, b, k, ne, jobs, slot);
+    moe_jobs_body(sidx, b, k, ne, jobs, slot, jt);
 }
 
 // out[t][h] = sum over ranks i (in order, from 0) of w[t][i] * yd[job][t][h];
@@ -205,6 +208,287 @@ __global__ __launch_bounds__(256) void k_moe_combine(const float* __restrict__ y
     *o = resid ? *o + acc : acc;
 }
 
+// ---------------------------------------------------------------------------
+// q4t expert GEMVs over the job's own tokens.  Job j (grid.y) multiplies
+// expert desc[jobs[1 + j]] with the n <= 8 token rows of its list jt[j]
+// only: the other tokens of the batch cost no operand traffic and no LDS.
+// A workgroup holds RBW row blocks x KP parts of the row (wave = K part x
+// RBW + row block, SPW 1 KiB steps each; the parts' partial sums meet in
+// LDS in part order).  Its waves share one copy of the job's operand rows
+// in LDS ([slot][item][plane], 16-byte items of the fixed-point hi / lo
+// f16 planes) and of their tile biases ([tile][16]: A rows 0..7 the hi
+// plane of slots 0..7, 8..15 the lo plane).  A rows of slots past n repeat
+// slot n - 1 and are never stored.
+//   GU: the operand is the prepared planes of all M batch rows (one for
+//       all jobs), copied by direct loads; the weight's row blocks hold 8
+//       gate rows then the matching 8 up rows (build_swiglu), and
+//       y[t][8 rb + r] = silu(g) * u (inference.rs:14-16);
+//   else the operand is made from the job's f32 rows hx[t] in the
+//       workgroup, exactly as the producer would prepare them, and
+//       y[t][16 rb + r] = the row's dot product.
+// ---------------------------------------------------------------------------
+struct MoeGx {
+    const GemvDesc* desc;
+    const int* jobs;
+    const int* jt;
+    const uint8_t* planes;  // GU
+    const float* xs;        // GU: xs[t] of the operand
+    float* y;         // + j * y_stride, token t's row at t * ldy
+    size_t y_stride;
+    int ldy, M, nk, nrb, rows, ns;  // ns: token slots of the LDS copy (>= any job's count)
+    // !GU: the operand rows themselves, f32: token t of job j at hx + j * hx_stride + t * ldh, K columns
+    const float* hx;
+    size_t hx_stride;
+    int ldh, K;
+};
+
+template <int RBW, int KP, int SPW, bool GU>
+__global__ __launch_bounds__(64 * RBW * KP) void k_moe_q4t(MoeGx a) {
+    constexpr int NW = RBW * KP;
+    extern __shared__ __align__(16) uint8_t smem[];
+    __shared__ float4v part[KP > 1 ? KP - 1 : 1][RBW][64];
+    const int j = blockIdx.y;
+    if (j >= a.jobs[0]) return;  // uniform
+    const GemvDesc d = a.desc[a.jobs[1 + j]];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4, p = r < 8 ? 0 : 1;
+    // wave: row block rbi of the workgroup's RBW, K part kp (steps SPW kp ..)
+    const int rbi = wave % RBW, kp = wave / RBW, g0 = kp * SPW;
+    const int ntg = a.nk, M = a.M, rb = blockIdx.x * RBW + rbi;
+    // GU: xs of every batch row (lane t % 16), independent of the token list
+    const float xsv = GU ? ldg(a.xs + (lane & 15)) : 0.f;
+    // the token list by scalar loads (uniform, in flight with the
+    // descriptor's); lane k (mod 8) holds the token of slot min(k, n - 1)
+    const int* jl = a.jt + (size_t)j * MOE_JT;
+    const int n = min(jl[0], 8);
+    int tk[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) tk[k] = jl[1 + k];
+    const int ls = min(lane & 7, n - 1);
+    int tokv = tk[0];
+#pragma unroll
+    for (int k = 1; k < 8; k++) tokv = ls == k ? tk[k] : tokv;
+    const int QI = ntg * 32;  // items of one slot: (step, tile, k-slot) x plane
+    float* lb = (float*)(smem + (size_t)a.ns * QI * 16);
+    uint4 wv[SPW];
+    uint2 sv[SPW];
+    // the weights + tile scales of the wave's row block (clamped: every load unconditional)
+    auto load_weights = [&]() {
+        const size_t wbase = (size_t)min(rb, a.nrb - 1) * ntg;
+#pragma unroll
+        for (int u = 0; u < SPW; u++) {
+            const size_t t = wbase + min(g0 + u, ntg - 1);
+            wv[u] = ld_stream((const uint4*)d.w + t * 64 + lane);
+            const uint64_t sw = ldg((const uint64_t*)d.scale + t * 16 + r);
+            sv[u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
+        }
+    };
+    __shared__ unsigned smax[8];  // !GU: max |x| of each slot's row (f32 bits)
+    __shared__ float sxs[8];      // !GU: the slot's operand unit xs
+    if constexpr (GU) {
+        // the prepared operand: this wave's share of the copy of the job's
+        // rows first, then its weights (the MFMAs wait for the copy, then
+        // for each step's weights in turn)
+        const uint8_t* hi = a.planes;
+        const uint8_t* lo = hi + (size_t)ntg * 4 * 64 * M;
+        const float* T1 = (const float*)(hi + (size_t)ntg * 4 * 128 * M);  // tile biases [tile][16]
+        const float* T2 = T1 + (size_t)ntg * 4 * 16;
+        const int NI = n * QI;
+        constexpr int CMAX = (8 * SPW * KP * 32 / 64 + NW - 1) / NW;  // chunks per wave of 8 slots
+#pragma unroll
+        for (int kc = 0; kc < CMAX; kc++) {
+            const int c = wave + NW * kc;
+            if (c * 64 >= NI) break;
+            const int i = min(c * 64 + lane, NI - 1);
+            const int slot = i / QI, rest = i - slot * QI, pl = rest & 1, q = rest >> 1;
+            int tok = tk[0];
+#pragma unroll
+            for (int k = 1; k < 8; k++) tok = slot == k ? tk[k] : tok;
+            __builtin_amdgcn_global_load_lds((const void*)((pl ? lo : hi) + ((size_t)q * M + tok) * 16),
+                                             (__attribute__((address_space(3))) void*)(smem + c * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int kc = 0; kc < (SPW * KP + NW - 1) / NW; kc++) {
+            const int c = wave + NW * kc;
+            if (c >= ntg) break;
+            const int i = c * 64 + lane, tile = i >> 4, k = i & 15;
+            __builtin_amdgcn_global_load_lds((const void*)((k < 8 ? T1 : T2) + (size_t)tile * 16 + tokv),
+                                             (__attribute__((address_space(3))) void*)(lb + c * 64), 4, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_weights();
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vmcnt<2 * SPW>();                   // this wave's share of the copy
+        asm volatile("s_barrier" ::: "memory");  // ... and every other wave's
+    } else {
+        // the operand from the f32 rows: the workgroup's threads take the
+        // 8-column items (slot, 4 tile + k-slot) in turn, request them before
+        // the weights, agree on each slot's max |x| (LDS atomics), then write
+        // the fixed-point hi / lo planes and tile biases that the producer
+        // (prep16_row) would write, into the LDS layout of the copy above
+        constexpr int NT = 64 * NW;
+        constexpr int IPT = (8 * SPW * KP * 16 + NT - 1) / NT;  // items per thread for 8 slots
+        const int tid = threadIdx.x, IPS = ntg * 16, NIT = n * IPS;
+        const float* hx = a.hx + (size_t)j * a.hx_stride;
+        float4v xv[IPT][2] = {};
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            if (NT * k >= NIT) break;  // (uniform)
+            if (tid + NT * k >= NIT) continue;
+            const int it = tid + NT * k, slot = it / IPS, item = it - slot * IPS;
+            const int c0 = 8 * item;  // 32 tile + 8 k-slot
+            int tok = tk[0];
+#pragma unroll
+            for (int q = 1; q < 8; q++) tok = slot == q ? tk[q] : tok;
+            const float* src = hx + (size_t)tok * a.ldh + min(c0, a.K - 8);
+            xv[k][0] = ldg((const float4v*)src);
+            xv[k][1] = ldg((const float4v*)(src + 4));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_weights();
+        __builtin_amdgcn_sched_barrier(0);
+        if (tid < 8) smax[tid] = 0u;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        wait_vmcnt<2 * SPW>();  // the rows' items (requested before the weights)
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            if (NT * k >= NIT) break;  // (uniform)
+            const int it = tid + NT * k, slot = it / IPS, c0 = 8 * (it - slot * IPS);
+            float am = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float x = xv[k][e >> 2][e & 3];
+                am = fmaxf(am, c0 + e < a.K ? fabsf(x) : 0.f);
+            }
+            if (it < NIT) atomicMax(&smax[slot], __float_as_uint(am));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+#pragma unroll
+        for (int k = 0; k < IPT; k++) {
+            if (NT * k >= NIT) break;  // (uniform: the shuffles below need whole waves)
+            const int it = tid + NT * k, on = it < NIT;
+            const int itc = min(it, NIT - 1), slot = itc / IPS, item = itc - slot * IPS, c0 = 8 * item;
+            float scale, xsl;
+            q4_fix_scale(__uint_as_float(smax[slot]), scale, xsl);
+            uint16_t hv[8], lv[8];
+            float sh = 0.f, sl = 0.f;  // (exact: integers and multiples of 2^-11)
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const int col = ord[e];
+                const float x = xv[k][col >> 2][col & 3];
+                _Float16 h, l;
+                q4_fix_split(c0 + col < a.K ? x * scale : 0.f, h, l);
+                hv[e] = __builtin_bit_cast(uint16_t, h);
+                lv[e] = __builtin_bit_cast(uint16_t, l);
+                sh += (float)h;
+                sl += (float)l;
+            }
+            sh += __shfl_xor(sh, 1);
+            sh += __shfl_xor(sh, 2);
+            sl += __shfl_xor(sl, 1);
+            sl += __shfl_xor(sl, 2);
+            if (on) {
+                uint4* dst = (uint4*)smem + slot * QI + item * 2;
+                dst[0] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                                    hv[6] | (hv[7] << 16));
+                dst[1] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
+                                    lv[6] | (lv[7] << 16));
+                if ((item & 3) == 0) {
+                    lb[(item >> 2) * 16 + slot] = sh * Q4_BIAS;
+                    lb[(item >> 2) * 16 + 8 + slot] = sl * Q4_BIAS;
+                }
+                if (item == 0) sxs[slot] = xsl;
+            }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    const uint4* X = (const uint4*)smem + ls * QI + p;
+    const float4v* LB = (const float4v*)lb;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const bool in = g0 + u < ntg;  // (steps past the row: zero scale, a select)
+        const int uc = min(g0 + u, ntg - 1);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int q = (uc * 4 + t) * 4 + s;
+            const half8 xa = __builtin_bit_cast(half8, X[q * 2]);
+            const float4v cb = LB[(uc * 4 + t) * 4 + s];  // A rows 4s..4s+3
+            const uint32_t wq = t == 0 ? wv[u].x : t == 1 ? wv[u].y : t == 2 ? wv[u].z : wv[u].w;
+            const float4v dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, dq_nib_word(wq), cb, 0, 0, 0);
+            const uint32_t sw = t < 2 ? sv[u].x : sv[u].y;
+            const float sc = in ? f16_bits_to_f32((t & 1) ? sw >> 16 : sw & 0xFFFFu) : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] += dd[v] * sc;
+        }
+    }
+    if constexpr (KP > 1) {  // the other K parts' partials through LDS, added in part order
+        if (kp > 0) part[kp - 1][rbi][lane] = acc;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kp > 0) return;
+#pragma unroll
+        for (int k = 0; k < KP - 1; k++) {
+            const float4v o = part[k][rbi][lane];
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] += o[v];
+        }
+    }
+    float* y = a.y + (size_t)j * a.y_stride;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        acc[v] += __shfl_xor(acc[v], 32);  // hi rows (lanes s = 0, 1) + lo rows (s = 2, 3)
+        const int slot = 4 * (s & 1) + v;
+        const int tok = __shfl(tokv, slot);
+        const float xsl = GU ? __shfl(xsv, tok) : sxs[min(slot, n - 1)];
+        const float val = acc[v] * xsl * 16777216.0f;  // 2^24: denormal nibbles
+        if constexpr (GU) {
+            const float u = __shfl_xor(val, 8);  // the matching up row
+            const int row = 8 * rb + r;
+            if (s < 2 && slot < n && r < 8 && rb < a.nrb && row < a.rows / 2)
+                y[(size_t)tok * a.ldy + row] = (val / (1.0f + expf(-val))) * u;
+        } else {
+            const int row = 16 * rb + r;
+            if (s < 2 && slot < n && rb < a.nrb && row < a.rows) y[(size_t)tok * a.ldy + row] = val;
+        }
+    }
+}
+
+typedef void (*MoeKernel)(MoeGx);
+constexpr int MOE_RBW = 4;  // row blocks per workgroup
+template <int KP, int SPW>
+MoeKernel moe_q4t_inst(bool gu, int* nw) {
+    *nw = MOE_RBW * KP;
+    return gu ? k_moe_q4t<MOE_RBW, KP, SPW, true> : k_moe_q4t<MOE_RBW, KP, SPW, false>;
+}
+// Whether k may take lds bytes of dynamic LDS (allowed once per kernel up
+// to what the CU's 160 KiB leave beside its static LDS).
+bool moe_lds_ok(MoeKernel k, size_t lds) {
+    static std::mutex mu;
+    static std::map<const void*, size_t> cap;
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cap.find((const void*)k);
+    if (it == cap.end()) {
+        hipFuncAttributes fa{};
+        size_t st = 0;
+        if (hipFuncGetAttributes(&fa, (const void*)k) == hipSuccess) st = fa.sharedSizeBytes;
+        size_t c = 160 * 1024 > st ? 160 * 1024 - st : 0;
+        if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)c) != hipSuccess) c = 0;
+        (void)hipGetLastError();
+        it = cap.emplace((const void*)k, c).first;
+    }
+    return lds <= it->second;
+}
+// the instance for rows of nk 1 KiB steps (nullptr: none); *nw = its waves
+MoeKernel moe_q4t_pick(int nk, bool gu, int* nw) {
+    if (nk <= 2) return moe_q4t_inst<1, 2>(gu, nw);
+    if (nk <= 4) return moe_q4t_inst<1, 4>(gu, nw);
+    if (nk <= 6) return moe_q4t_inst<1, 6>(gu, nw);
+    if (nk <= 8) return moe_q4t_inst<1, 8>(gu, nw);
+    if (nk <= 12) return moe_q4t_inst<2, 6>(gu, nw);
+    if (nk <= 16) return moe_q4t_inst<2, 8>(gu, nw);
+    return nullptr;
+}
 }  // namespace cmf
 
 using namespace cmf;
@@ -219,7 +503,7 @@ struct cmf_moe_s {
     bool desc_ok = false;
     // device scratch
     float *x = nullptr, *logits = nullptr, *w = nullptr, *out = nullptr;
-    int *idx = nullptr, *jobs = nullptr, *slot = nullptr;
+    int *idx = nullptr, *jobs = nullptr, *slot = nullptr, *jt = nullptr;
     uint8_t *px = nullptr, *ph = nullptr;
     float *xsx = nullptr, *xsh = nullptr, *ygu = nullptr, *yd = nullptr;
     size_t ph_stride = 0;
@@ -256,22 +540,73 @@ static int moe_ready(cmf_moe m) {
 static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int ldo, bool resid, hipStream_t s,
                        bool numbered, bool prepared = false) {
     const int H = m->hidden, I = m->inter;
-    if (!numbered) hipLaunchKernelGGL(k_moe_jobs, dim3(1), dim3(256), 0, s, m->idx, b, k, m->ne, m->jobs, m->slot);
+    if (!numbered)
+        hipLaunchKernelGGL(k_moe_jobs, dim3(1), dim3(256), 0, s, m->idx, b, k, m->ne, m->jobs, m->slot, m->jt);
     int rc = prepared ? CMF_OK : launch_prep_src(m->gu[0], x, b, m->px, m->xsx, s);
     const int mj = std::min(m->max_jobs, b * k);
     const size_t ygu_stride = (size_t)MAXB * 2 * I, yd_stride = (size_t)MAXB * H;
-    if (rc == CMF_OK)
-        rc = gemv_grouped(m->gu[0], m->d_gu, m->jobs, mj, m->px, 0, m->xsx, m->ygu, ygu_stride, 2 * I, b, s);
     if (rc != CMF_OK) return rc;
-    XSrc sg{};
-    sg.mode = XS_SILU;
-    sg.x = m->ygu;
-    sg.ldx = 2 * I;
-    sg.K = I;
-    rc = launch_prep_src_grouped(m->down[0], sg, b, m->jobs, mj, ygu_stride, m->ph, m->ph_stride, m->xsh, s);
-    if (rc == CMF_OK)
-        rc = gemv_grouped(m->down[0], m->d_down, m->jobs, mj, m->ph, m->ph_stride, m->xsh, m->yd, yd_stride, H, b, s);
-    if (rc != CMF_OK) return rc;
+    // q4t experts and at most 8 tokens: the GEMVs over each job's own tokens
+    // (CMF_MOE_GATHER=0 keeps the all-rows grouped GEMVs)
+    static const bool gather_env = [] {
+        const char* v = getenv("CMF_MOE_GATHER");
+        return !(v && *v == '0');
+    }();
+    int sp1 = 0, sp2 = 0;  // waves per workgroup
+    const DevWeight &gw = m->gu[0], &dw = m->down[0];
+    MoeKernel kg = nullptr, kd = nullptr;
+    if (gather_env && b <= 8 && gw.dtype == DT_Q4T && dw.dtype == DT_Q4T) {
+        kg = moe_q4t_pick(gw.kchunks, true, &sp1);
+        kd = moe_q4t_pick(dw.kchunks, false, &sp2);
+    }
+    // LDS: the operand rows of up to b tokens + the tile biases
+    const size_t lg = (size_t)gw.kchunks * (b * 512 + 256), ld = (size_t)dw.kchunks * (b * 512 + 256);
+    if (kg && kd && moe_lds_ok(kg, lg) && moe_lds_ok(kd, ld)) {
+        // gate|up -> h = silu(g) * u [job][t][I] (in the ygu area), then
+        // down over the listed h rows -> yd [job][t][H]
+        MoeGx g{};
+        g.desc = m->d_gu;
+        g.jobs = m->jobs;
+        g.jt = m->jt;
+        g.planes = m->px;
+        g.xs = m->xsx;
+        g.y = m->ygu;
+        g.y_stride = (size_t)MAXB * I;
+        g.ldy = I;
+        g.M = b;
+        g.nk = gw.kchunks;
+        g.rows = gw.rows;
+        g.ns = b;
+        g.nrb = gw.rows_pad / 16;
+        hipLaunchKernelGGL(kg, dim3((g.nrb + MOE_RBW - 1) / MOE_RBW, mj), dim3(64 * sp1), lg, s, g);
+        MoeGx d = g;
+        d.desc = m->d_down;
+        d.planes = nullptr;  // (the operand from the h rows themselves)
+        d.xs = nullptr;
+        d.hx = m->ygu;
+        d.hx_stride = (size_t)MAXB * I;
+        d.ldh = I;
+        d.K = I;
+        d.y = m->yd;
+        d.y_stride = yd_stride;
+        d.ldy = H;
+        d.nk = dw.kchunks;
+        d.rows = dw.rows;
+        d.nrb = dw.rows_pad / 16;
+        hipLaunchKernelGGL(kd, dim3((d.nrb + MOE_RBW - 1) / MOE_RBW, mj), dim3(64 * sp2), ld, s, d);
+    } else {
+        rc = gemv_grouped(gw, m->d_gu, m->jobs, mj, m->px, 0, m->xsx, m->ygu, ygu_stride, 2 * I, b, s);
+        if (rc != CMF_OK) return rc;
+        XSrc sg{};
+        sg.mode = XS_SILU8;  // (gate|up rows interleaved 8 / 8)
+        sg.x = m->ygu;
+        sg.ldx = 2 * I;
+        sg.K = I;
+        rc = launch_prep_src_grouped(dw, sg, b, m->jobs, mj, ygu_stride, m->ph, m->ph_stride, m->xsh, s);
+        if (rc == CMF_OK)
+            rc = gemv_grouped(dw, m->d_down, m->jobs, mj, m->ph, m->ph_stride, m->xsh, m->yd, yd_stride, H, b, s);
+        if (rc != CMF_OK) return rc;
+    }
     hipLaunchKernelGGL(k_moe_combine, dim3((H + 255) / 256, b), dim3(256), 0, s, m->yd, yd_stride, H, m->slot, m->w,
                        k, H, d_out, ldo, resid ? 1 : 0);
     return CMF_OK;
@@ -306,8 +641,8 @@ int cmf::moe_ffn_launch(cmf_moe m, const XSrc& x, const float* d_logits, int b, 
     }();
     (void)attr;
     hipLaunchKernelGGL(k_moe_route_prep, dim3(b + 1), dim3(64 * MAXB), (size_t)K * sizeof(float), s, d_logits, b,
-                       m->ne, m->top_k, m->norm_topk, m->scaling, m->idx, m->w, m->jobs, m->slot, x, K, g.dtype, nk,
-                       m->px, m->xsx);
+                       m->ne, m->top_k, m->norm_topk, m->scaling, m->idx, m->w, m->jobs, m->slot, m->jt, x, K,
+                       g.dtype, nk, m->px, m->xsx);
     return moe_experts(m, x, b, m->top_k, d_out, ldo, resid, s, true, true);
 }
 
@@ -347,6 +682,7 @@ int cmf_moe_create(int n_experts, int hidden, int inter, int top_k, int norm_top
         moe_alloc(m, (void**)&m->idx, sizeof(int) * MAXB * top_k) ||
         moe_alloc(m, (void**)&m->jobs, sizeof(int) * (1 + MAXB * top_k)) ||
         moe_alloc(m, (void**)&m->slot, sizeof(int) * MAXB * top_k) ||
+        moe_alloc(m, (void**)&m->jt, sizeof(int) * MOE_JT * mj) ||
         moe_alloc(m, (void**)&m->px, px) || moe_alloc(m, (void**)&m->xsx, sizeof(float) * 16) ||
         moe_alloc(m, (void**)&m->ph, m->ph_stride * mj) || moe_alloc(m, (void**)&m->xsh, sizeof(float) * 16 * mj) ||
         moe_alloc(m, (void**)&m->ygu, sizeof(float) * MAXB * 2 * I * mj) ||
@@ -390,21 +726,8 @@ int cmf_moe_set_expert(cmf_moe m, int e, const cmf_tensor* gate, const cmf_tenso
         if (m->set[f] && f != e && (m->gu[f].dtype != gate->dtype || m->down[f].dtype != down->dtype))
             return fail("moe: every expert must use the same codecs");
     DevWeight gu, dn;
-    if (gate->dtype == DT_Q8ROW) {
-        std::vector<const int8_t*> rp;
-        std::vector<float> rs;
-        for (const cmf_tensor* t : {gate, up})
-            for (int r = 0; r < t->rows; r++) {
-                rp.push_back(t->q + (size_t)r * H);
-                rs.push_back(t->row_scale[r]);
-            }
-        if (build_q8(gu, 2 * I, H, rp.data(), rs.data()) != CMF_OK) return CMF_ERR;
-    } else {
-        Q4Src s;
-        fill_q4src(s, gate->dtype, I, H, gate->bytes, 0);
-        fill_q4src(s, up->dtype, I, H, up->bytes, 0);
-        if (build_q4(gu, s) != CMF_OK) return CMF_ERR;
-    }
+    // gate and up interleaved 8 / 8 per row block (the SwiGLU pairs in one block)
+    if (build_swiglu(gu, gate, up) != CMF_OK) return CMF_ERR;
     int rc;
     if (down->dtype == DT_Q8ROW) {
         std::vector<const int8_t*> rp;

@@ -3,6 +3,7 @@
 
 #include <vector>
 
+#include "../../include/cmf_hip.h"
 #include "common.h"
 
 namespace cmf {
@@ -25,6 +26,9 @@ struct Q4Src {
 int build_q8(DevWeight& w, int rows, int cols, const int8_t* const* rowptr, const float* rs);
 int build_q4(DevWeight& w, const Q4Src& src);
 int fill_q4src(Q4Src& s, int dtype, int rows, int cols, const uint8_t* payload, int row_offset);
+// gate and up [I x cols] (same dtype) as one weight of 2I rows whose row
+// blocks hold 8 gate rows then the 8 matching up rows (I % 8 == 0)
+int build_swiglu(DevWeight& w, const cmf_tensor* g, const cmf_tensor* u);
 void free_weight(DevWeight& w);
 
 }  // namespace cmf

@@ -209,6 +209,43 @@ int fill_q4src(Q4Src& s, int dtype, int rows, int cols, const uint8_t* payload, 
     return CMF_OK;
 }
 
+// gate and up as one weight whose row blocks hold 8 gate rows then the 8
+// matching up rows, so that the GEMV's SwiGLU epilogue sees g and u of the
+// same index in one row block.
+int build_swiglu(DevWeight& w, const cmf_tensor* g, const cmf_tensor* u) {
+    const int dt = g->dtype, cols = g->cols, I = g->rows;
+    if (u->dtype != dt || u->cols != cols || u->rows != I) return fail("gate/up must share dtype and shape");
+    if (I % 8) return fail("gate/up rows must be a multiple of 8");
+    if (dt == DT_Q8ROW) {
+        std::vector<const int8_t*> rp;
+        std::vector<float> rs;
+        for (int r0 = 0; r0 < I; r0 += 8)
+            for (const cmf_tensor* t : {g, u})
+                for (int r = r0; r < r0 + 8; r++) {
+                    rp.push_back(t->q + (size_t)r * cols);
+                    rs.push_back(t->row_scale[r]);
+                }
+        return build_q8(w, 2 * I, cols, rp.data(), rs.data());
+    }
+    Q4Src sg, su, s;
+    fill_q4src(sg, dt, I, cols, g->bytes, 0);
+    fill_q4src(su, dt, I, cols, u->bytes, 0);
+    s.dtype = dt;
+    s.cols = cols;
+    s.code_stride = sg.code_stride;
+    for (int r0 = 0; r0 < I; r0 += 8)
+        for (const Q4Src* t : {&sg, &su})
+            for (int r = r0; r < r0 + 8; r++) {
+                s.rowbase.push_back(t->rowbase[r]);
+                if (dt == DT_Q4TP) {
+                    s.codes.push_back(t->codes[r]);
+                    s.params.push_back(t->params[r]);
+                }
+            }
+    s.rows = 2 * I;
+    return build_q4(w, s);
+}
+
 void free_weight(DevWeight& w) {
     if (w.w) (void)hipFree(w.w);
     if (w.scale) (void)hipFree(w.scale);
