@@ -138,11 +138,9 @@ int gemm(const DevWeight& w, const XSrc& src, int m, float* y, int ldy, bool res
 int gemm_q4(const DevWeight& w, const float* x, int ldx, int m, float* y, int ldy, hipStream_t st);
 // The same for up to max_jobs jobs of a device job list (GemvArgs::jobs):
 // job j reads rows at src.x + j * x_stride and writes planes + j *
-// planes_stride, xs + 16 j; with jt ([job][1 + MAXB]: count, then batch
-// rows) only the rows a job lists are written.
+// planes_stride, xs + 16 j.
 int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const int* jobs, int max_jobs,
-                            size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st,
-                            const int* jt = nullptr);
+                            size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st);
 int launch_prep(const DevWeight& w, const float* x, int ldx, int m, uint8_t* planes, float* xs,
                 hipStream_t st);
 // The a8w8 operand (split_act) of m rows of x: planes / xs as launch_prep,

@@ -18,18 +18,11 @@ namespace cmf {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk, uint8_t* __restrict__ planes,
                                                   float* __restrict__ xs, const int* __restrict__ jobs,
-                                                  size_t x_stride, size_t planes_stride, int mstride,
-                                                  const int* __restrict__ jt) {
+                                                  size_t x_stride, size_t planes_stride, int mstride) {
     extern __shared__ float vals[];  // K
     if (jobs) {  // grouped: blockIdx.y = job
         const int j = blockIdx.y;
         if (j >= jobs[0]) return;
-        if (jt) {  // only the rows of the job's token list [count, tokens...]
-            const int* l = jt + (size_t)j * (1 + MAXB);
-            bool listed = false;
-            for (int i = 0; i < l[0]; i++) listed |= l[1 + i] == (int)blockIdx.x;
-            if (!listed) return;
-        }
         s.x += j * x_stride;
         planes += j * planes_stride;
         xs += 16 * j;
@@ -181,7 +174,7 @@ int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes,
     if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
-                       xs, (const int*)nullptr, (size_t)0, (size_t)0, 0, (const int*)nullptr);
+                       xs, (const int*)nullptr, (size_t)0, (size_t)0, 0);
     return CMF_OK;
 }
 
@@ -194,7 +187,7 @@ int launch_prep_src_gemm(const DevWeight& w, const XSrc& src, int m, int mstride
     if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
-                       xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride, (const int*)nullptr);
+                       xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride);
     return CMF_OK;
 }
 
@@ -208,8 +201,7 @@ int launch_prep_rows_gemm(const DevWeight& w, const float* x, int ldx, int m, in
 }
 
 int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const int* jobs, int max_jobs,
-                            size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st,
-                            const int* jt) {
+                            size_t x_stride, uint8_t* planes, size_t planes_stride, float* xs, hipStream_t st) {
     const int K = src.K ? src.K : w.cols;
     if (m < 1 || m > MAXB) return fail("prep: batch must be 1..16");
     if (K < 1 || K > w.cols || K > 16384) return fail("prep: operand length must be 1..min(cols, 16384)");
@@ -217,7 +209,7 @@ int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const in
     if (max_jobs < 1 || max_jobs > 65535 || !jobs) return fail("prep: bad job list");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m, max_jobs), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk,
-                       planes, xs, jobs, x_stride, planes_stride, 0, jt);
+                       planes, xs, jobs, x_stride, planes_stride, 0);
     return CMF_OK;
 }
 

@@ -9,17 +9,18 @@
 //                     w_i = p_i / wsum, wsum = sum of the kept p (norm_topk)
 //                     or 1, divided by routed_scaling;
 //   2. job numbering  one job per distinct routed expert, in expert order,
-//                     and the job of every (token, rank) slot; 1 and 2 are
-//                     one launch (k_moe_route_jobs), 2 alone for caller-routed
-//                     batches (k_moe_jobs).
-//   3. prep x         prepared operand of the b token rows (shared by all jobs).
-//   4. gate|up        grouped GEMV: job j = W_gu[e_j] x for all b rows (the
-//                     weights are read once per expert; rows of tokens that
-//                     did not pick the expert are computed and ignored: they
-//                     cost MFMA rows, not bandwidth).
-//   5. prep h         grouped: h = silu(g) * u per job.
-//   6. down           grouped GEMV: job j = W_down[e_j] h_j.
-//   7. k_moe_combine  out[t] = sum over ranks i of w[t][i] * down[job(t, i)][t],
+//                     the job of every (token, rank) slot and each job's
+//                     token list; 1 and 2 are one launch with the prepared
+//                     operand of the b token rows (k_moe_route_prep), 2 alone
+//                     for caller-routed batches (k_moe_jobs).
+//   q4t experts, b <= 8 (k_moe_q4t, over each job's own tokens only):
+//   3. gate|up        job j: h = silu(g) * u of W_gu[e_j] x for its tokens;
+//   4. down           job j: W_down[e_j] h, the operand made from the h rows
+//                     in the workgroup;
+//   other codecs or larger batches (grouped GEMVs over all b rows; rows of
+//   tokens that did not pick the expert are computed and ignored):
+//   3. gate|up, 3b. the per-job operand h = silu(g) * u, 4. down;
+//   5. k_moe_combine  out[t] = sum over ranks i of w[t][i] * down[job(t, i)][t],
 //                     accumulated from 0 in rank order, as the reference does.
 #include <map>
 #include <mutex>

@@ -21,12 +21,14 @@ def _experts(ne, hidden, inter, dt_gu, dt_down, seed):
              "down": mk[dt_down](seed + 3 * e + 2, hidden, inter)} for e in range(ne)]
 
 
-def _run(gpu, ne, H, I, k, b, dt_gu=DT_Q4T, dt_down=DT_Q4T, seed=7, norm=True, scaling=1.0):
+def _run(gpu, ne, H, I, k, b, dt_gu=DT_Q4T, dt_down=DT_Q4T, seed=7, norm=True, scaling=1.0, bias=None):
     from cmf_amd import synth
     from cmf_amd.moe import MoE
     ex = _experts(ne, H, I, dt_gu, dt_down, seed)
     x = synth.normal(seed + 1000, b * H).reshape(b, H)
     lg = synth.normal(seed + 2000, b * ne).reshape(b, ne)
+    if bias is not None:
+        lg = (lg + np.asarray(bias, np.float32)).astype(np.float32)
     moe = MoE(ne, H, I, k, ex, norm_topk=norm, routed_scaling=scaling)
     out, idx, w = moe.ffn(x, lg)
     for t in range(b):
@@ -79,3 +81,39 @@ def test_moe_block_caller_routed(gpu):
         one[e] = 0.0  # route to e alone with weight 1
         ref += wi * orc.moe_ffn(ex, 1, one, x[0])
     assert rel_l2(got, ref) < TOL
+
+
+def test_moe_every_token_same_experts(gpu):
+    """b = 8 tokens that all pick experts 3 and 5 (router bias): each job
+    lists all eight tokens, the most the per-job-token kernels hold."""
+    bias = np.zeros(8, np.float32)
+    bias[[3, 5]] = 50.0
+    _run(gpu, 8, 256, 128, 2, 8, seed=31, bias=bias)
+
+
+_GROUPED_CHILD = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import cmf_amd as cmf
+cmf.init(0)
+import test_gpu_moe as t
+t._run(None, 8, 256, 128, 2, 5)
+t._run(None, 128, 2048, 768, 8, 5, seed=5)
+print("ok")
+"""
+
+
+def test_moe_grouped_path(gpu):
+    """CMF_MOE_GATHER=0 (child process): q4t experts at b <= 8 through the
+    grouped GEMVs over all rows, the path of the other codecs and of larger
+    batches, on the interleaved gate|up rows."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, CMF_MOE_GATHER="0")
+    r = subprocess.run([sys.executable, "-c", _GROUPED_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().splitlines()[-1] == "ok"
