@@ -456,11 +456,11 @@ __global__ __launch_bounds__(64 * RBW * KP) void k_moe_q4t(MoeGx a) {
 }
 
 typedef void (*MoeKernel)(MoeGx);
-constexpr int MOE_RBW = 4;  // row blocks per workgroup
-template <int KP, int SPW>
-MoeKernel moe_q4t_inst(bool gu, int* nw) {
-    *nw = MOE_RBW * KP;
-    return gu ? k_moe_q4t<MOE_RBW, KP, SPW, true> : k_moe_q4t<MOE_RBW, KP, SPW, false>;
+template <int RBW, int KP, int SPW>
+MoeKernel moe_q4t_inst(bool gu, int* nw, int* rbw) {
+    *nw = RBW * KP;
+    *rbw = RBW;
+    return gu ? k_moe_q4t<RBW, KP, SPW, true> : k_moe_q4t<RBW, KP, SPW, false>;
 }
 // Whether k may take lds bytes of dynamic LDS (allowed once per kernel up
 // to what the CU's 160 KiB leave beside its static LDS).
@@ -481,13 +481,17 @@ bool moe_lds_ok(MoeKernel k, size_t lds) {
     return lds <= it->second;
 }
 // the instance for rows of nk 1 KiB steps (nullptr: none); *nw = its waves
-MoeKernel moe_q4t_pick(int nk, bool gu, int* nw) {
-    if (nk <= 2) return moe_q4t_inst<1, 2>(gu, nw);
-    if (nk <= 4) return moe_q4t_inst<1, 4>(gu, nw);
-    if (nk <= 6) return moe_q4t_inst<1, 6>(gu, nw);
-    if (nk <= 8) return moe_q4t_inst<1, 8>(gu, nw);
-    if (nk <= 12) return moe_q4t_inst<2, 6>(gu, nw);
-    if (nk <= 16) return moe_q4t_inst<2, 8>(gu, nw);
+// (measured on MI355X, config 5: four row blocks per workgroup, gate|up
+// in two K halves of 8 steps: 16.7 us; 8 x 2: 19.2, 2 x 2: 18.2, 4 x 4
+// halves of 4: 16.7, 8 row blocks of whole rows: 30.6; down 4 x 1 x 6
+// steps: 10.7 us; 8 x 1: 10.9, 4 x 2 x 3: 10.8, 2 x 1: 11.6)
+MoeKernel moe_q4t_pick(int nk, bool gu, int* nw, int* rbw) {
+    if (nk <= 2) return moe_q4t_inst<4, 1, 2>(gu, nw, rbw);
+    if (nk <= 4) return moe_q4t_inst<4, 1, 4>(gu, nw, rbw);
+    if (nk <= 6) return moe_q4t_inst<4, 1, 6>(gu, nw, rbw);
+    if (nk <= 8) return moe_q4t_inst<4, 1, 8>(gu, nw, rbw);
+    if (nk <= 12) return moe_q4t_inst<4, 2, 6>(gu, nw, rbw);
+    if (nk <= 16) return moe_q4t_inst<4, 2, 8>(gu, nw, rbw);
     return nullptr;
 }
 }  // namespace cmf
@@ -553,12 +557,12 @@ static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int
         const char* v = getenv("CMF_MOE_GATHER");
         return !(v && *v == '0');
     }();
-    int sp1 = 0, sp2 = 0;  // waves per workgroup
+    int sp1 = 0, sp2 = 0, rw1 = 1, rw2 = 1;  // waves, row blocks per workgroup
     const DevWeight &gw = m->gu[0], &dw = m->down[0];
     MoeKernel kg = nullptr, kd = nullptr;
     if (gather_env && b <= 8 && gw.dtype == DT_Q4T && dw.dtype == DT_Q4T) {
-        kg = moe_q4t_pick(gw.kchunks, true, &sp1);
-        kd = moe_q4t_pick(dw.kchunks, false, &sp2);
+        kg = moe_q4t_pick(gw.kchunks, true, &sp1, &rw1);
+        kd = moe_q4t_pick(dw.kchunks, false, &sp2, &rw2);
     }
     // LDS: the operand rows of up to b tokens + the tile biases
     const size_t lg = (size_t)gw.kchunks * (b * 512 + 256), ld = (size_t)dw.kchunks * (b * 512 + 256);
@@ -579,7 +583,7 @@ static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int
         g.rows = gw.rows;
         g.ns = b;
         g.nrb = gw.rows_pad / 16;
-        hipLaunchKernelGGL(kg, dim3((g.nrb + MOE_RBW - 1) / MOE_RBW, mj), dim3(64 * sp1), lg, s, g);
+        hipLaunchKernelGGL(kg, dim3((g.nrb + rw1 - 1) / rw1, mj), dim3(64 * sp1), lg, s, g);
         MoeGx d = g;
         d.desc = m->d_down;
         d.planes = nullptr;  // (the operand from the h rows themselves)
@@ -594,7 +598,7 @@ static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int
         d.nk = dw.kchunks;
         d.rows = dw.rows;
         d.nrb = dw.rows_pad / 16;
-        hipLaunchKernelGGL(kd, dim3((d.nrb + MOE_RBW - 1) / MOE_RBW, mj), dim3(64 * sp2), ld, s, d);
+        hipLaunchKernelGGL(kd, dim3((d.nrb + rw2 - 1) / rw2, mj), dim3(64 * sp2), ld, s, d);
     } else {
         rc = gemv_grouped(gw, m->d_gu, m->jobs, mj, m->px, 0, m->xsx, m->ygu, ygu_stride, 2 * I, b, s);
         if (rc != CMF_OK) return rc;
