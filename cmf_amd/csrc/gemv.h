@@ -86,8 +86,9 @@ typedef void (*GemvKernel)(GemvArgs);
 GemvKernel q4t_kernel(int m, int xm, int ks, int rb);
 GemvKernel q4tp_kernel(int m, int xm, int ks, int rb);
 // three groups of 4 waves per workgroup (k_gemv_q4<..., G = 3, SPW = 8>)
-GemvKernel q4t_kernel_g3(int m, int xm);
-GemvKernel q4tp_kernel_g3(int m, int xm);
+// (one: the single-unit instance, for grids where every workgroup serves one unit)
+GemvKernel q4t_kernel_g3(int m, int xm, bool one = false);
+GemvKernel q4tp_kernel_g3(int m, int xm, bool one = false);
 // 16 waves x 6 steps (k_gemv_q4<..., KS = 16, HL, ..., SPW = 6>), m <= 8
 GemvKernel q4t_kernel_s6(int m, int xm);
 GemvKernel q4tp_kernel_s6(int m, int xm);

@@ -420,7 +420,15 @@ static int launch_args(const DevWeight& w, GemvArgs& a, int ks_override, int gri
         const int og = kg ? resident_per_cu(kg, 64 * 4 * 3, lg) : 0;
         if (og >= 1) {
             a.lds = 1;
-            const int grid = std::min((a.nrb + 2) / 3, og * num_cus());
+            const int units = (a.nrb + 2) / 3;
+            const int grid = std::min(units, og * num_cus());
+            // every workgroup one unit (K <= 4096 is one K part): the loop-free
+            // instance, if the CUs hold as many of it
+            static const int one_env = env_int("CMF_GEMV_ONE", 1);
+            if (one_env && grid == units) {
+                GemvKernel k1 = w.dtype == DT_Q4T ? q4t_kernel_g3(m, XM_PREP, true) : q4tp_kernel_g3(m, XM_PREP, true);
+                if (k1 && resident_per_cu(k1, 64 * 4 * 3, lg) * num_cus() >= grid) kg = k1;
+            }
             void* args[] = {&a};
             CMF_HIP(hipLaunchKernel((const void*)kg, dim3(grid), dim3(64 * 4 * 3), args, lg, st));
             return CMF_OK;

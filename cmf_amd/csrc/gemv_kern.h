@@ -328,7 +328,10 @@ constexpr int SP = 4;  // weight steps per wave and work unit
 // XM_PREPC (q8): XM_PREP with one scale per (batch row, 64-column chunk)
 enum { XM_PREP = 0, XM_FUSED = 1, XM_GLOBAL = 2, XM_PREPC = 3 };
 
-template <int FMT, int NV, int KS, bool HL, int XM, int RB, int G = 1, int SPW = SP>
+// ONE: every workgroup serves exactly one unit (one K part, its row blocks;
+// the host launches it only so): no loop, so the compiler waits for each
+// step's weights in turn instead of for all of them before the first MFMA
+template <int FMT, int NV, int KS, bool HL, int XM, int RB, int G = 1, int SPW = SP, bool ONE = false>
 __global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
     GemvArgs a = args;
     if (a.jobs) {  // grouped launch: this workgroup serves job blockIdx.y
@@ -580,6 +583,11 @@ __global__ __launch_bounds__(64 * KS * G) void k_gemv_q4(GemvArgs args) {
         if constexpr (KS > 1 || TP || G > 1) __syncthreads();
     };
 
+    if constexpr (ONE) {
+        const float2 pn[RB] = {};
+        process(wA, sA, pn, a.nrb);  // (no next unit)
+        return;
+    }
     for (;;) {
         int rn = rb, kn = kp + 1;
         if (kn == P) {
@@ -1269,8 +1277,11 @@ GemvKernel q4_by_xm(int xm, int ks, int rb) {
 // Grouped workgroups (G = 3 groups of 4 waves x 8 steps: three row blocks of
 // K <= 4096 share one operand copy in LDS), m <= 8
 template <int FMT>
-GemvKernel q4_pick_g3(int m, int xm) {
+GemvKernel q4_pick_g3(int m, int xm, bool one) {
     if (xm != XM_PREP || m > 8) return nullptr;
+    if (one)
+        return m == 1 ? k_gemv_q4<FMT, 1, 4, true, XM_PREP, 1, 3, 8, true>
+                      : k_gemv_q4<FMT, 4, 4, true, XM_PREP, 1, 3, 8, true>;
     return m == 1 ? k_gemv_q4<FMT, 1, 4, true, XM_PREP, 1, 3, 8> : k_gemv_q4<FMT, 4, 4, true, XM_PREP, 1, 3, 8>;
 }
 // 16 waves x 6 steps: rows of 65..96 steps (K <= 12288) in one K part
