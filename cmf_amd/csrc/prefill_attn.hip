@@ -452,37 +452,38 @@ __global__ __launch_bounds__(256) void k_prefill_fakv(const float* __restrict__ 
     }
 }
 
-// grid (8 nqb) (XCD: kv head = the workgroup's XCD, local index i =
-// blockIdx / 8) or (nqb, nkv); 256 threads.  Wave w holds 16 query rows:
-// block 4 qb + w of the 16-row blocks of k_prefill_attn (row q: chunk row
-// PPW (4 qb + w) + q % PPW, query head g HPK + q / PPW).  Under XCD the
-// local index i < ceil(nqb / 2) takes query block i and the others nqb - 1
-// - (i - ceil(nqb / 2)), so that the two workgroups a CU holds (i and i +
-// 32 when the XCD's CUs take its workgroups in turn) together see about
-// the same number of keys; the placement check is k_prefill_attn's.
+// grid (8 np) (XCD: kv head = the workgroup's XCD, pair index i =
+// blockIdx / 8) or (np, nkv), np = ceil(nqb / 2); 512 threads.  The
+// workgroup serves two 64-row query blocks that see about as many keys
+// together as any other pair: waves 0-3 block i, waves 4-7 block nqb - 1 -
+// i (none when that is block i again), sharing one fetch of every K / V
+// tile the short block needs.  Wave w of a block holds 16 query rows: the
+// 16-row block 4 qb + (w % 4) of k_prefill_attn (row q: chunk row PPW (4 qb
+// + w % 4) + q % PPW, query head g HPK + q / PPW).  The placement check is
+// k_prefill_attn's, on the pair's cells.
 template <int HPK, bool XCD>
-__global__ __launch_bounds__(256) void k_prefill_fa(const float* __restrict__ qbuf, const int4v* __restrict__ op,
+__global__ __launch_bounds__(512) void k_prefill_fa(const float* __restrict__ qbuf, const int4v* __restrict__ op,
                                                     int npad, int cnt, int p0, int nh, int nqb, float* __restrict__ out,
                                                     unsigned long long* cells, int* perr, unsigned long long tag) {
     constexpr int PPW = 16 / HPK;
     extern __shared__ __align__(16) uint8_t fsm[];  // two tiles (direct-load targets)
-    int qb, g;
+    const int pi = XCD ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+    const int g = XCD ? (int)(xcc_id() & 7) : (int)blockIdx.y;
+    const int qa = pi, qz = nqb - 1 - pi;  // the pair (qz == qa: one block)
     if constexpr (XCD) {
-        const int i = (int)(blockIdx.x >> 3), h = (nqb + 1) >> 1;
-        qb = i < h ? i : nqb - 1 - (i - h);
-        g = (int)(xcc_id() & 7);
-        if (threadIdx.x == 0 && atomicExch(cells + qb * 8 + g, tag) == tag) atomicOr(perr, 1);
-    } else {
-        qb = blockIdx.x;
-        g = blockIdx.y;
+        if (threadIdx.x == 0 && atomicExch(cells + qa * 8 + g, tag) == tag) atomicOr(perr, 1);
+        if (threadIdx.x == 64 && qz != qa && atomicExch(cells + qz * 8 + g, tag) == tag) atomicOr(perr, 1);
     }
     const int t = threadIdx.x, lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int r = lane & 15, s = lane >> 4;
-    const int i0 = (4 * qb + wave) * PPW;               // this wave's first chunk row
-    const int iw = (4 * qb + 3) * PPW;                  // the workgroup's last block's first row
-    const int lastrow = min(iw + PPW, cnt) - 1;         // the workgroup's last chunk row
+    const bool second = wave >= 4;
+    const bool live = !second || qz != qa;                 // (uniform per wave)
+    const int qb = second ? qz : qa;
+    const int i0 = (4 * qb + (wave & 3)) * PPW;           // this wave's first chunk row
+    const int lastrow = min((4 * qb + 4) * PPW, cnt) - 1; // its block's last chunk row
+    const int lastz = min((4 * max(qa, qz) + 4) * PPW, cnt) - 1;  // the pair's
     // the queries of column r (the B operand of S^T), f16 hi / lo
-    const bool qv = i0 + r % PPW < cnt;
+    const bool qv = live && i0 + r % PPW < cnt;
     const int qpos = p0 + i0 + r % PPW;                 // position of query r
     half8 qh[HD / 32], ql[HD / 32];
     {
@@ -500,13 +501,15 @@ __global__ __launch_bounds__(256) void k_prefill_fa(const float* __restrict__ qb
             }
         }
     }
-    const int ntiles = lastrow < 0 ? 0 : (p0 + lastrow) / FT + 1;
+    // tiles of the pair (the fetch loop) and of this wave's block
+    const int ntiles = lastz < 0 ? 0 : (p0 + lastz) / FT + 1;
+    const int mytiles = !live || lastrow < 0 ? 0 : (p0 + lastrow) / FT + 1;
     const uint8_t* src = (const uint8_t*)(op + (size_t)g * (npad / FT) * (FT_BYTES / 16));
-    // tile tt into buffer b: 32 KiB as 32 chunks of 1 KiB, 8 per wave
+    // tile tt into buffer b: 32 KiB as 32 chunks of 1 KiB, 4 per wave
     auto fetch = [&](int tt, int b) {
 #pragma unroll
-        for (int c = 0; c < 8; c++) {
-            const int ch = 8 * wave + c;
+        for (int c = 0; c < 4; c++) {
+            const int ch = 4 * wave + c;
             __builtin_amdgcn_global_load_lds((const void*)(src + (size_t)tt * FT_BYTES + ch * 1024 + lane * 16),
                                              (__attribute__((address_space(3))) void*)(fsm + b * FT_BYTES + ch * 1024),
                                              16, 0, 0);
@@ -523,6 +526,7 @@ __global__ __launch_bounds__(256) void k_prefill_fa(const float* __restrict__ qb
         wait_vmcnt0();
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave's share is in; buffer b ^ 1 is free
         if (tt + 1 < ntiles) fetch(tt + 1, b ^ 1);
+        if (tt >= mytiles) continue;  // (uniform per wave: past this block's keys)
         const int4v* F = (const int4v*)(fsm + b * FT_BYTES) + lane;
         // S^T for the two key blocks: d[kb][e] = key 16 kb + 4 s + e, query r
         float4v d[2];
@@ -582,7 +586,7 @@ __global__ __launch_bounds__(256) void k_prefill_fa(const float* __restrict__ qb
     }
     // out = o / l of query r: dims 16 db + 4 s .. + 3
     const int row = i0 + r % PPW, head = g * HPK + r / PPW;
-    if (row < cnt) {
+    if (live && row < cnt) {
         float* dst = out + (size_t)row * nh * HD + (size_t)head * HD + 4 * s;
 #pragma unroll
         for (int db = 0; db < 8; db++) *(float4v*)(dst + 16 * db) = o[db] / l;
@@ -609,7 +613,8 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
     // (CMF_PREFILL_FA=0: the 16-row blocks of k_prefill_attn)
     static const bool fa = !(getenv("CMF_PREFILL_FA") && getenv("CMF_PREFILL_FA")[0] == '0');
     if (fa) {
-        const int nqb = (a.cnt + 4 * ppw - 1) / (4 * ppw);  // 64-row workgroups
+        const int nqb = (a.cnt + 4 * ppw - 1) / (4 * ppw);  // 64-row query blocks, paired
+        const int np = (nqb + 1) / 2;
         const bool xcd = a.nkv == 8 && xl_device_fits() && a.allow_xcd && a.cells && a.perr &&
                          8 * nqb <= PREFILL_XCD_CELLS;
         typedef void (*KernF)(const float*, const int4v*, int, int, int, int, int, float*, unsigned long long*, int*,
@@ -624,8 +629,8 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
         }
         int4v* op = (int4v*)a.khl;  // nkv x npad x 1 KiB, the same bytes as the K / V operands below
         hipLaunchKernelGGL(k_prefill_fakv, dim3(npad / FT, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, op);
-        const dim3 grid = xcd ? dim3(8 * nqb) : dim3(nqb, a.nkv);
-        hipLaunchKernelGGL(k, grid, dim3(256), 2 * FT_BYTES, st, a.qbuf, op, npad, a.cnt, a.p0, a.nh, nqb, a.out,
+        const dim3 grid = xcd ? dim3(8 * np) : dim3(np, a.nkv);
+        hipLaunchKernelGGL(k, grid, dim3(512), 2 * FT_BYTES, st, a.qbuf, op, npad, a.cnt, a.p0, a.nh, nqb, a.out,
                            a.cells, a.perr, a.tag);
         return CMF_OK;
     }
