@@ -41,6 +41,7 @@ constexpr int PST = KT + 4;   // f32 row stride of the scores / weights (64 keys
 // K / V requests; uses of those registers get the compiler's own waits.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }  // vmcnt(0) only
+__device__ __forceinline__ void wait_vmcnt4() { __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8)); }  // vmcnt(4) only
 
 // Four f32 reductions over the wave at once (each DPP step applied to all
 // four before the next, so the chains overlap), with the DPP pattern of
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(512) void k_prefill_fa(const float* __restrict__ qb
                                                     int npad, int cnt, int p0, int nh, int nqb, float* __restrict__ out,
                                                     unsigned long long* cells, int* perr, unsigned long long tag) {
     constexpr int PPW = 16 / HPK;
-    extern __shared__ __align__(16) uint8_t fsm[];  // two tiles (direct-load targets)
+    extern __shared__ __align__(16) uint8_t fsm[];  // three tiles (direct-load targets)
     const int pi = XCD ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
     const int g = XCD ? (int)(xcc_id() & 7) : (int)blockIdx.y;
     const int qa = pi, qz = nqb - 1 - pi;  // the pair (qz == qa: one block)
@@ -520,12 +521,15 @@ __global__ __launch_bounds__(512) void k_prefill_fa(const float* __restrict__ qb
     float4v o[8];                   // rows 4 s + e, dims 16 db + r
 #pragma unroll
     for (int db = 0; db < 8; db++) o[db] = float4v{0.f, 0.f, 0.f, 0.f};
+    // three buffers: tile tt + 2 is requested while tile tt is used
     if (ntiles > 0) fetch(0, 0);
+    if (ntiles > 1) fetch(1, 1);
     for (int tt = 0; tt < ntiles; tt++) {
-        const int b = tt & 1;
-        wait_vmcnt0();
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave's share is in; buffer b ^ 1 is free
-        if (tt + 1 < ntiles) fetch(tt + 1, b ^ 1);
+        const int b = tt % 3;
+        if (tt + 1 < ntiles) wait_vmcnt4();  // tile tt's share is in (tile tt + 1's may not be)
+        else wait_vmcnt0();
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // every wave's share is in; tile tt - 1's buffer is free
+        if (tt + 2 < ntiles) fetch(tt + 2, (tt + 2) % 3);
         if (tt >= mytiles) continue;  // (uniform per wave: past this block's keys)
         const int4v* F = (const int4v*)(fsm + b * FT_BYTES) + lane;
         // S^T for the two key blocks: d[kb][e] = key 16 kb + 4 s + e, query r
@@ -630,7 +634,17 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
         int4v* op = (int4v*)a.khl;  // nkv x npad x 1 KiB, the same bytes as the K / V operands below
         hipLaunchKernelGGL(k_prefill_fakv, dim3(npad / FT, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, op);
         const dim3 grid = xcd ? dim3(8 * np) : dim3(np, a.nkv);
-        hipLaunchKernelGGL(k, grid, dim3(512), 2 * FT_BYTES, st, a.qbuf, op, npad, a.cnt, a.p0, a.nh, nqb, a.out,
+        static const bool attr = [] {  // (96 KiB: above the default dynamic LDS limit)
+            bool ok = true;
+            for (KernF f : {k_prefill_fa<1, true>, k_prefill_fa<1, false>, k_prefill_fa<2, true>, k_prefill_fa<2, false>,
+                            k_prefill_fa<4, true>, k_prefill_fa<4, false>, k_prefill_fa<8, true>, k_prefill_fa<8, false>,
+                            k_prefill_fa<16, true>, k_prefill_fa<16, false>})
+                ok &= hipFuncSetAttribute((const void*)f, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * FT_BYTES) ==
+                      hipSuccess;
+            return ok;
+        }();
+        if (!attr) return fail("prefill attention: dynamic LDS attribute");
+        hipLaunchKernelGGL(k, grid, dim3(512), 3 * FT_BYTES, st, a.qbuf, op, npad, a.cnt, a.p0, a.nh, nqb, a.out,
                            a.cells, a.perr, a.tag);
         return CMF_OK;
     }
