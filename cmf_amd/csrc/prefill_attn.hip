@@ -6,15 +6,14 @@
 //     k-norm + RoPE of the new K rows, K and V appended to the cache
 //     (attention.rs:606-624, 818-890; kv_cache.rs:366-505), as the decode
 //     kernels do it;
-//   - k_prefill_kv: the cache's K / V rows [0, p0 + cnt) rearranged into
-//     the attention's MFMA operand layout (K as f16 hi / lo halves);
-//   - k_prefill_attn: 16 query rows per workgroup — 16 / HPK positions times
-//     the HPK query heads of one kv head, which share its K / V — over
-//     128-key tiles with a running (online) softmax: scores on the f16 MFMA
-//     (q.k = qh.kh + qh.kl + ql.kh, 22-bit operands, f32 sums), causal
-//     limit the row's position (kv_cache.rs:521-690), values on the fp32
-//     MFMA (16x16x4).
-// Rows of a workgroup past the chunk see no keys and write nothing.
+//   - k_prefill_fakv: the cache's K / V rows [0, p0 + cnt) rearranged into
+//     32-key tiles of the attention's MFMA fragments (f16 hi / lo halves);
+//   - k_prefill_fa: 64 query rows per block of four waves, two blocks per
+//     workgroup sharing each tile through LDS, with a running (online)
+//     softmax: scores on the f16 MFMA (q.k = qh.kh + qh.kl + ql.kh, 22-bit
+//     operands, f32 sums), causal limit the row's position
+//     (kv_cache.rs:521-690), values ph.vh + ph.vl + pl.vh on the f16 MFMA.
+// Rows of a block past the chunk see no keys and write nothing.
 #include <math.h>
 
 #include "common.h"
@@ -32,40 +31,10 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef int int4v __attribute__((ext_vector_type(4)));
 
 constexpr int HD = 128;
-constexpr int KT = 64;        // key rows per scratch padding unit
-constexpr int KT2 = 128;      // keys per attention tile (two groups of 64)
-constexpr int PST = KT + 4;   // f32 row stride of the scores / weights (64 keys a group)
+constexpr int KT2 = 128;      // the K / V scratch's padding unit (keys)
 
-// Workgroup barrier over LDS only: __syncthreads also waits for every
-// global load in flight (vmcnt(0)), which would wait for the next tile's
-// K / V requests; uses of those registers get the compiler's own waits.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 __device__ __forceinline__ void wait_vmcnt0() { __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8)); }  // vmcnt(0) only
 __device__ __forceinline__ void wait_vmcnt4() { __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (15 << 8)); }  // vmcnt(4) only
-
-// Four f32 reductions over the wave at once (each DPP step applied to all
-// four before the next, so the chains overlap), with the DPP pattern of
-// wave_reduce_f32; the results are wave-uniform.
-template <typename Op>
-__device__ __forceinline__ void wave_reduce4(float (&v)[4], float ident, Op op) {
-    const uint32_t iu = __builtin_bit_cast(uint32_t, ident);
-    auto step = [&](auto ctrl, auto rows) {
-        constexpr int C = decltype(ctrl)::value, R = decltype(rows)::value;
-        float w[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) w[i] = __builtin_bit_cast(float, dpp_u32<C, R>(__builtin_bit_cast(uint32_t, v[i]), iu));
-#pragma unroll
-        for (int i = 0; i < 4; i++) v[i] = op(v[i], w[i]);
-    };
-    step(std::integral_constant<int, 0xb1>{}, std::integral_constant<int, 0xf>{});
-    step(std::integral_constant<int, 0x4e>{}, std::integral_constant<int, 0xf>{});
-    step(std::integral_constant<int, 0x114>{}, std::integral_constant<int, 0xf>{});
-    step(std::integral_constant<int, 0x118>{}, std::integral_constant<int, 0xf>{});
-    step(std::integral_constant<int, 0x142>{}, std::integral_constant<int, 0xa>{});
-    step(std::integral_constant<int, 0x143>{}, std::integral_constant<int, 0xc>{});
-#pragma unroll
-    for (int i = 0; i < 4; i++) v[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[i]), 63));
-}
 
 __device__ __forceinline__ uint32_t xcc_id() {
     uint32_t v;
@@ -126,277 +95,15 @@ __global__ __launch_bounds__(64) void k_prefill_qk(const float* __restrict__ qkv
     }
 }
 
-// The cached K / V rows [0, n) of every kv head rearranged once per chunk
-// as the attention's MFMA operands, so that each wave load (16 B a lane)
-// reads 1 KiB in register order (rows [n, npad) zero):
-//   kop [nkv][npad / 16][8 chunks][64 lanes] x 16 B: key block kb (keys
-//       16 kb + r), chunk ch = 2 ks + plane (f16 hi / lo), lane 16 s + r:
-//       dims 32 ks + 8 s .. + 7 of key 16 kb + r;
-//   vop [nkv][npad / 64][8 dim blocks][2 k-steps][2 planes][64 lanes] x
-//       16 B: key block kb (keys 64 kb ..), dim block db, k-step ks, plane
-//       (f16 hi / lo), lane 16 s + r: keys 64 kb + 32 ks + 8 s .. + 7 of
-//       dim 16 db + r (the B operand of the values' f16 MFMA).
-// grid (npad / 64, nkv), 256 threads: 64 keys through LDS.
-__global__ __launch_bounds__(256) void k_prefill_kv(const float* __restrict__ kc, const float* __restrict__ vc,
-                                                    int max_seq, int n, int npad, int4v* __restrict__ kop,
-                                                    float4v* __restrict__ vop) {
-    const int t = threadIdx.x, kb64 = blockIdx.x, g = blockIdx.y;
-    __shared__ float KS[64][HD + 4], VS[64][HD + 1];
-    for (int e = t; e < 64 * 32; e += 256) {
-        const int k = e >> 5, c4 = 4 * (e & 31), key = 64 * kb64 + k;
-        float4v kv = {0.f, 0.f, 0.f, 0.f}, vv = kv;
-        if (key < n) {
-            kv = *(const float4v*)(kc + ((size_t)g * max_seq + key) * HD + c4);
-            vv = *(const float4v*)(vc + ((size_t)g * max_seq + key) * HD + c4);
-        }
-        *(float4v*)&KS[k][c4] = kv;
-#pragma unroll
-        for (int i = 0; i < 4; i++) VS[k][c4 + i] = vv[i];
-    }
-    __syncthreads();
-    const int nkb = npad / 16, nvb = npad / 64;
-    // K: 4 key blocks x 8 chunks x 64 lanes
-    for (int e = t; e < 4 * 8 * 64; e += 256) {
-        const int l = e & 63, ch = (e >> 6) & 7, kb = e >> 9, r = l & 15, sl = l >> 4;
-        const int ks = ch >> 1, plane = ch & 1, k = 16 * kb + r;
-        half8 h;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            _Float16 hh, ll;
-            split16(KS[k][32 * ks + 8 * sl + j], hh, ll);
-            h[j] = plane ? ll : hh;
-        }
-        kop[(((size_t)g * nkb + 4 * kb64 + kb) * 8 + ch) * 64 + l] = __builtin_bit_cast(int4v, h);
-    }
-    // V: 8 dim blocks x (2 k-steps x 2 planes) x 64 lanes
-    for (int e = t; e < 8 * 4 * 64; e += 256) {
-        const int l = e & 63, i = (e >> 6) & 3, db = e >> 8, r = l & 15, sl = l >> 4;
-        const int ks = i >> 1, plane = i & 1;
-        half8 h;
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            _Float16 hh, ll;
-            split16(VS[32 * ks + 8 * sl + j][16 * db + r], hh, ll);
-            h[j] = plane ? ll : hh;
-        }
-        vop[(((size_t)g * nvb + kb64) * 8 + db) * 4 * 64 + i * 64 + l] = __builtin_bit_cast(float4v, h);
-    }
-}
-
-// grid (ceil(cnt / (16 / HPK)), nkv), 512 threads.  Row q (0..15) of block
-// qb: chunk row qb * PPW + q % PPW, query head g * HPK + q / PPW.  XCD (8 kv
-// heads on an MI355X): grid (8 ceil(cnt / PPW)), kv head g = the XCD the
-// workgroup runs on, qb = blockIdx / 8 (the dispatcher deals workgroups to
-// the 8 XCDs in turn), so one head's K / V serves all of its query blocks
-// from that XCD's L2.  That covers each (query block, head) once only while
-// the workgroups go to the XCDs strictly in turn; each workgroup therefore
-// swaps the launch's tag into its cell [qb][g] first, and finding the tag
-// already there (two workgroups on one cell, so some other cell has none)
-// sets *perr: the host then re-runs the prefill on the grid-indexed variant.
-// The 8 waves form two groups: group G takes keys 64 G .. 64 G + 63 of each
-// 128-key tile with a running softmax of its own, wave wl of the group the
-// scores of keys 16 wl .. + 15 and the values of dims 32 wl .. + 31; its K
-// and V operands come from the rearranged scratch straight into registers
-// (the next tile's requested while the current one is used), the queries
-// stay in registers, and LDS holds only the weights and row statistics.
-// The groups' (m, l, o) are merged at the end.
-template <int HPK, bool XCD>
-__global__ __launch_bounds__(512) void k_prefill_attn(const float* __restrict__ qbuf, const int4v* __restrict__ kop,
-                                                      const float4v* __restrict__ vop, int npad, int cnt, int p0,
-                                                      int nh, float* __restrict__ out, unsigned long long* cells,
-                                                      int* perr, unsigned long long tag) {
-    constexpr int PPW = 16 / HPK;  // positions per workgroup
-    constexpr int GK = KT2 / 2;    // keys per group and tile
-    const int qb = XCD ? (int)(blockIdx.x >> 3) : (int)blockIdx.x;
-    const int g = XCD ? (int)(xcc_id() & 7) : (int)blockIdx.y;
-    const int t = threadIdx.x, lane = t & 63;
-    if constexpr (XCD) {
-        if (t == 0 && atomicExch(cells + qb * 8 + g, tag) == tag) atomicOr(perr, 1);
-    }
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), G = wave >> 2, wl = wave & 3;
-    const int r = lane & 15, s = lane >> 4;
-    __shared__ __align__(16) float P[2][16][PST];
-    __shared__ __align__(16) float O1[16][HD];
-    __shared__ float s_m[2][16], s_l[2][16], s_al[2][16];
-    const int i0 = qb * PPW;
-    const int npos = min(PPW, cnt - i0);
-    // the score operand's queries (row r, dims 32 ks + 8 s ..) as f16 hi / lo
-    half8 qh[HD / 32], ql[HD / 32];
-    {
-        const bool qv = r % PPW < npos;
-        const float* qrow = qbuf + ((size_t)(i0 + (qv ? r % PPW : 0)) * nh + g * HPK + r / PPW) * HD;
-#pragma unroll
-        for (int ks = 0; ks < HD / 32; ks++) {
-            const float4v a0 = *(const float4v*)(qrow + 32 * ks + 8 * s);
-            const float4v a1 = *(const float4v*)(qrow + 32 * ks + 8 * s + 4);
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                _Float16 hh, ll;
-                split16(qv ? (j < 4 ? a0[j] : a1[j - 4]) : 0.f, hh, ll);
-                qh[ks][j] = hh;
-                ql[ks][j] = ll;
-            }
-        }
-    }
-    if (t < 32) {
-        s_m[t >> 4][t & 15] = -INFINITY;
-        s_l[t >> 4][t & 15] = 0.f;
-    }
-    const int plast = p0 + i0 + npos - 1;  // the block's last query position
-    const int ntiles = plast / KT2 + 1;
-    const int nkb = npad / 16, nvb = npad / 64;
-    const int4v* kw = kop + ((size_t)g * nkb + 4 * G + wl) * 8 * 64 + lane;          // + tile * 8 key blocks
-    const float4v* vw = vop + (((size_t)g * nvb + G) * 8 + 2 * wl) * 4 * 64 + lane;  // + tile * 2 key blocks
-    int4v ka[8], kn[8];
-    float4v va[8], vn[8];
-    auto load = [&](int tile, int4v (&k)[8], float4v (&v)[8]) {
-#pragma unroll
-        for (int ch = 0; ch < 8; ch++) k[ch] = kw[(size_t)tile * 8 * 8 * 64 + ch * 64];
-#pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = vw[(size_t)tile * 2 * 8 * 4 * 64 + i * 64];
-    };
-    // scores in log2 units: exp(x - m) = exp2(x log2e - m log2e)
-    const float scale = 1.4426950408889634f / sqrtf((float)HD);
-    float4v o[4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    auto step = [&](int tile, const int4v (&k)[8], const float4v (&v)[8]) {
-        // scores of keys GK G + 16 wl .. + 15 of the tile
-        {
-            float4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0, d2 = d0;
-#pragma unroll
-            for (int ks = 0; ks < HD / 32; ks++) {
-                const half8 kh = __builtin_bit_cast(half8, k[2 * ks]), kl = __builtin_bit_cast(half8, k[2 * ks + 1]);
-                d0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kh, d0, 0, 0, 0);
-                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[ks], kl, d1, 0, 0, 0);
-                d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[ks], kh, d2, 0, 0, 0);
-            }
-            const float4v d = d0 + (d1 + d2);
-            const int key = tile * KT2 + GK * G + 16 * wl + r;
-            lds_barrier();  // the previous tile's weights are read
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int q = 4 * s + e;
-                const bool see = q % PPW < npos && key <= p0 + i0 + q % PPW;
-                P[G][q][16 * wl + r] = see ? d[e] * scale : -INFINITY;
-            }
-        }
-        lds_barrier();
-        // running softmax of the group: wave wl rows 4 wl .. 4 wl + 3, lane =
-        // key (the four rows' reductions interleaved)
-        {
-            float sv[4], mo[4], mt[4], p[4];
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                sv[qq] = P[G][4 * wl + qq][lane];
-                mo[qq] = s_m[G][4 * wl + qq];
-                mt[qq] = sv[qq];
-            }
-            wave_reduce4(mt, -INFINITY, [](float x, float y) { return fmaxf(x, y); });
-            float mn[4];
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                mn[qq] = fmaxf(mo[qq], mt[qq]);
-                p[qq] = mn[qq] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(sv[qq] - mn[qq]);
-                mt[qq] = p[qq];
-            }
-            wave_reduce4(mt, 0.f, [](float x, float y) { return x + y; });
-#pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
-                const int q = 4 * wl + qq;
-                const float al = mo[qq] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo[qq] - mn[qq]);
-                P[G][q][lane] = p[qq];
-                if (lane == 0) {
-                    s_m[G][q] = mn[qq];
-                    s_l[G][q] = s_l[G][q] * al + mt[qq];
-                    s_al[G][q] = al;
-                }
-            }
-        }
-        lds_barrier();
-        // values: output dims 32 wl + 16 tt + r, rows 4 s + e, on the f16
-        // MFMA (16x16x32) in two k-steps of 32 keys: the weights p of row r,
-        // keys 32 ks + 8 s .., and V split into f16 hi / lo halves, three
-        // products ph vh + ph vl + pl vh (22-bit operands, f32 sums) into
-        // o[tt + 2 ks] (v[tt * 4 + ks * 2 + plane], the operand layout)
-        {
-            float al[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) al[e] = s_al[G][4 * s + e];
-#pragma unroll
-            for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-                for (int e = 0; e < 4; e++) o[tt][e] *= al[e];
-#pragma unroll
-            for (int ks = 0; ks < GK / 32; ks++) {
-                const float4v p0 = *(const float4v*)&P[G][r][32 * ks + 8 * s];
-                const float4v p1 = *(const float4v*)&P[G][r][32 * ks + 8 * s + 4];
-                half8 ph, pl;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    _Float16 hh, ll;
-                    split16(j < 4 ? p0[j] : p1[j - 4], hh, ll);
-                    ph[j] = hh;
-                    pl[j] = ll;
-                }
-#pragma unroll
-                for (int tt = 0; tt < 2; tt++) {
-                    const half8 vh = __builtin_bit_cast(half8, v[tt * 4 + ks * 2]);
-                    const half8 vl = __builtin_bit_cast(half8, v[tt * 4 + ks * 2 + 1]);
-                    float4v& acc = o[tt + 2 * ks];
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vh, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vl, acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vh, acc, 0, 0, 0);
-                }
-            }
-        }
-    };
-    load(0, ka, va);
-    for (int tile = 0; tile < ntiles; tile += 2) {
-        if (tile + 1 < ntiles) load(tile + 1, kn, vn);
-        step(tile, ka, va);
-        if (tile + 1 >= ntiles) break;
-        if (tile + 2 < ntiles) load(tile + 2, ka, va);
-        step(tile + 1, kn, vn);
-    }
-    lds_barrier();
-    // merge: group 1 leaves its outputs in LDS, group 0 combines
-    // (m = max(m0, m1), w_G = exp2(m_G - m), out = sum_G w_G o_G / sum_G w_G l_G)
-    if (G == 1) {
-#pragma unroll
-        for (int tt = 0; tt < 2; tt++)
-#pragma unroll
-            for (int e = 0; e < 4; e++) O1[4 * s + e][32 * wl + 16 * tt + r] = o[tt][e] + o[tt + 2][e];
-    }
-    lds_barrier();
-    if (G == 0) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int q = 4 * s + e;
-            if (q % PPW >= npos) continue;
-            const float m0 = s_m[0][q], m1 = s_m[1][q], m = fmaxf(m0, m1);
-            const float w0 = m0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m0 - m);
-            const float w1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
-            const float l = s_l[0][q] * w0 + s_l[1][q] * w1;
-            const int row = i0 + q % PPW, head = g * HPK + q / PPW;
-#pragma unroll
-            for (int tt = 0; tt < 2; tt++) {
-                const int dd = 32 * wl + 16 * tt + r;
-                out[(size_t)row * nh * HD + (size_t)head * HD + dd] =
-                    ((o[tt][e] + o[tt + 2][e]) * w0 + O1[q][dd] * w1) / l;
-            }
-        }
-    }
-}
-
 // ---------------------------------------------------------------------------
-// Flash form: 64 query rows per workgroup share each 32-key tile of K / V
-// through LDS (the 16-row blocks above read every tile from L2 once per 16
-// rows).  Scores are computed transposed, S^T = K Q^T, so that each lane
-// (query r, k-slot s) ends up holding the weights of its own query for the
-// keys {4s..4s+3, 16+4s..16+4s+3}: exactly the B operand of O^T = V^T P^T
-// when the V tile's k-slot s holds the same eight keys, so the weights never
-// go through LDS, and the output's lanes hold their own query's dims.  Same arithmetic as k_prefill_attn: q.k = qh.kh +
-// qh.kl + ql.kh (f16 hi / lo halves, f32 sums), exp2 of log2-scaled scores
-// with a running maximum, values ph.vh + ph.vl + pl.vh.
+// 64 query rows per block share each 32-key tile of K / V through LDS.
+// Scores are computed transposed, S^T = K Q^T, so that each lane (query r,
+// k-slot s) ends up holding the weights of its own query for the keys
+// {4s..4s+3, 16+4s..16+4s+3}: exactly the B operand of O^T = V^T P^T when
+// the V tile's k-slot s holds the same eight keys, so the weights never go
+// through LDS, and the output's lanes hold their own query's dims.  q.k =
+// qh.kh + qh.kl + ql.kh (f16 hi / lo halves, f32 sums), exp2 of log2-scaled
+// scores with a running maximum, values ph.vh + ph.vl + pl.vh.
 // ---------------------------------------------------------------------------
 constexpr int FT = 32;                // keys per tile
 constexpr int FT_BYTES = 32 * 1024;   // one tile of one kv head: K then V fragments
@@ -458,10 +165,15 @@ __global__ __launch_bounds__(256) void k_prefill_fakv(const float* __restrict__ 
 // workgroup serves two 64-row query blocks that see about as many keys
 // together as any other pair: waves 0-3 block i, waves 4-7 block nqb - 1 -
 // i (none when that is block i again), sharing one fetch of every K / V
-// tile the short block needs.  Wave w of a block holds 16 query rows: the
-// 16-row block 4 qb + (w % 4) of k_prefill_attn (row q: chunk row PPW (4 qb
-// + w % 4) + q % PPW, query head g HPK + q / PPW).  The placement check is
-// k_prefill_attn's, on the pair's cells.
+// tile the short block needs.  Wave w of a block holds 16 query rows, PPW =
+// 16 / HPK positions times the HPK query heads of kv head g (row q: chunk
+// row PPW (4 qb + w % 4) + q % PPW, query head g HPK + q / PPW).  XCD: the
+// kv head is the XCD the workgroup runs on (its K / V stays in that XCD's
+// L2), which covers each (query block, head) once only while the
+// dispatcher deals workgroups to the 8 XCDs in turn; each workgroup
+// therefore swaps the launch's tag into its blocks' cells [qb][g] first,
+// and finding the tag already there sets *perr: the host then re-runs the
+// prefill on the grid-indexed variant.
 template <int HPK, bool XCD>
 __global__ __launch_bounds__(512) void k_prefill_fa(const float* __restrict__ qbuf, const int4v* __restrict__ op,
                                                     int npad, int cnt, int p0, int nh, int nqb, float* __restrict__ out,
@@ -614,60 +326,35 @@ int launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t st) {
     if (!a.out) return CMF_OK;
     const int hpk = a.nh / a.nkv, ppw = 16 / hpk;
     const int n = a.p0 + a.cnt, npad = (n + KT2 - 1) / KT2 * KT2;
-    // (CMF_PREFILL_FA=0: the 16-row blocks of k_prefill_attn)
-    static const bool fa = !(getenv("CMF_PREFILL_FA") && getenv("CMF_PREFILL_FA")[0] == '0');
-    if (fa) {
-        const int nqb = (a.cnt + 4 * ppw - 1) / (4 * ppw);  // 64-row query blocks, paired
-        const int np = (nqb + 1) / 2;
-        const bool xcd = a.nkv == 8 && xl_device_fits() && a.allow_xcd && a.cells && a.perr &&
-                         8 * nqb <= PREFILL_XCD_CELLS;
-        typedef void (*KernF)(const float*, const int4v*, int, int, int, int, int, float*, unsigned long long*, int*,
-                              unsigned long long);
-        KernF k;
-        switch (hpk) {
-            case 1: k = xcd ? k_prefill_fa<1, true> : k_prefill_fa<1, false>; break;
-            case 2: k = xcd ? k_prefill_fa<2, true> : k_prefill_fa<2, false>; break;
-            case 4: k = xcd ? k_prefill_fa<4, true> : k_prefill_fa<4, false>; break;
-            case 8: k = xcd ? k_prefill_fa<8, true> : k_prefill_fa<8, false>; break;
-            default: k = xcd ? k_prefill_fa<16, true> : k_prefill_fa<16, false>; break;
-        }
-        int4v* op = (int4v*)a.khl;  // nkv x npad x 1 KiB, the same bytes as the K / V operands below
-        hipLaunchKernelGGL(k_prefill_fakv, dim3(npad / FT, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, op);
-        const dim3 grid = xcd ? dim3(8 * np) : dim3(np, a.nkv);
-        static const bool attr = [] {  // (96 KiB: above the default dynamic LDS limit)
-            bool ok = true;
-            for (KernF f : {k_prefill_fa<1, true>, k_prefill_fa<1, false>, k_prefill_fa<2, true>, k_prefill_fa<2, false>,
-                            k_prefill_fa<4, true>, k_prefill_fa<4, false>, k_prefill_fa<8, true>, k_prefill_fa<8, false>,
-                            k_prefill_fa<16, true>, k_prefill_fa<16, false>})
-                ok &= hipFuncSetAttribute((const void*)f, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * FT_BYTES) ==
-                      hipSuccess;
-            return ok;
-        }();
-        if (!attr) return fail("prefill attention: dynamic LDS attribute");
-        hipLaunchKernelGGL(k, grid, dim3(512), 3 * FT_BYTES, st, a.qbuf, op, npad, a.cnt, a.p0, a.nh, nqb, a.out,
-                           a.cells, a.perr, a.tag);
-        return CMF_OK;
-    }
-    const int nqb = (a.cnt + ppw - 1) / ppw;
+    const int nqb = (a.cnt + 4 * ppw - 1) / (4 * ppw);  // 64-row query blocks, paired
+    const int np = (nqb + 1) / 2;
     const bool xcd = a.nkv == 8 && xl_device_fits() && a.allow_xcd && a.cells && a.perr &&
                      8 * nqb <= PREFILL_XCD_CELLS;
-    const dim3 grid = xcd ? dim3(8 * nqb) : dim3(nqb, a.nkv);
-    typedef void (*Kern)(const float*, const int4v*, const float4v*, int, int, int, int, float*, unsigned long long*,
-                         int*, unsigned long long);
-    Kern k;
+    typedef void (*KernF)(const float*, const int4v*, int, int, int, int, int, float*, unsigned long long*, int*,
+                          unsigned long long);
+    KernF k;
     switch (hpk) {
-        case 1: k = xcd ? k_prefill_attn<1, true> : k_prefill_attn<1, false>; break;
-        case 2: k = xcd ? k_prefill_attn<2, true> : k_prefill_attn<2, false>; break;
-        case 4: k = xcd ? k_prefill_attn<4, true> : k_prefill_attn<4, false>; break;
-        case 8: k = xcd ? k_prefill_attn<8, true> : k_prefill_attn<8, false>; break;
-        default: k = xcd ? k_prefill_attn<16, true> : k_prefill_attn<16, false>; break;
+        case 1: k = xcd ? k_prefill_fa<1, true> : k_prefill_fa<1, false>; break;
+        case 2: k = xcd ? k_prefill_fa<2, true> : k_prefill_fa<2, false>; break;
+        case 4: k = xcd ? k_prefill_fa<4, true> : k_prefill_fa<4, false>; break;
+        case 8: k = xcd ? k_prefill_fa<8, true> : k_prefill_fa<8, false>; break;
+        default: k = xcd ? k_prefill_fa<16, true> : k_prefill_fa<16, false>; break;
     }
-    int4v* kop = (int4v*)a.khl;
-    float4v* vop = (float4v*)(a.khl + (size_t)a.nkv * npad * 2 * HD);
-    hipLaunchKernelGGL(k_prefill_kv, dim3(npad / 64, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, kop,
-                       vop);
-    hipLaunchKernelGGL(k, grid, dim3(512), 0, st, a.qbuf, kop, vop, npad, a.cnt, a.p0, a.nh, a.out, a.cells, a.perr,
-                       a.tag);
+    int4v* op = (int4v*)a.khl;  // nkv x npad x 1 KiB
+    hipLaunchKernelGGL(k_prefill_fakv, dim3(npad / FT, a.nkv), dim3(256), 0, st, a.kc, a.vc, a.max_seq, n, npad, op);
+    const dim3 grid = xcd ? dim3(8 * np) : dim3(np, a.nkv);
+    static const bool attr = [] {  // (96 KiB: above the default dynamic LDS limit)
+        bool ok = true;
+        for (KernF f : {k_prefill_fa<1, true>, k_prefill_fa<1, false>, k_prefill_fa<2, true>, k_prefill_fa<2, false>,
+                        k_prefill_fa<4, true>, k_prefill_fa<4, false>, k_prefill_fa<8, true>, k_prefill_fa<8, false>,
+                        k_prefill_fa<16, true>, k_prefill_fa<16, false>})
+            ok &= hipFuncSetAttribute((const void*)f, hipFuncAttributeMaxDynamicSharedMemorySize, 3 * FT_BYTES) ==
+                  hipSuccess;
+        return ok;
+    }();
+    if (!attr) return fail("prefill attention: dynamic LDS attribute");
+    hipLaunchKernelGGL(k, grid, dim3(512), 3 * FT_BYTES, st, a.qbuf, op, npad, a.cnt, a.p0, a.nh, nqb, a.out,
+                       a.cells, a.perr, a.tag);
     return CMF_OK;
 }
 
