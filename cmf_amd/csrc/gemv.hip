@@ -18,7 +18,7 @@ namespace cmf {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk, uint8_t* __restrict__ planes,
                                                   float* __restrict__ xs, const int* __restrict__ jobs,
-                                                  size_t x_stride, size_t planes_stride, int mstride) {
+                                                  size_t x_stride, size_t planes_stride, int mstride, int m) {
     extern __shared__ float vals[];  // K
     if (jobs) {  // grouped: blockIdx.y = job
         const int j = blockIdx.y;
@@ -27,7 +27,19 @@ __global__ __launch_bounds__(512) void k_prep_src(XSrc s, int K, int fmt, int nk
         planes += j * planes_stride;
         xs += 16 * j;
     }
-    prep_src_row(s, K, fmt, nk, planes, xs, mstride, blockIdx.x, gridDim.x, vals);
+    int b = blockIdx.x;
+    if (mstride) {
+        // GEMM operands: row b's 16-byte items sit 16 mstride bytes apart,
+        // so one 128-byte line of a plane holds 8 consecutive rows (and one
+        // of the q4 bias tables 32): rows 32 (x + 8 k) .. + 31 go to the
+        // workgroups of XCD x (the dispatcher deals workgroups to the 8
+        // XCDs in turn), so that each line is written from one XCD's L2
+        // instead of in pieces from several (the grid is padded to 256)
+        const int x = b & 7, j = b >> 3;
+        b = 32 * (x + 8 * (j >> 5)) + (j & 31);
+        if (b >= m) return;
+    }
+    prep_src_row(s, K, fmt, nk, planes, xs, mstride, b, mstride ? m : gridDim.x, vals);
 }
 
 // The a8w8 operand (split_act, qtensor.rs:9237-9281) of row b of x: rms =
@@ -174,7 +186,7 @@ int launch_prep_src(const DevWeight& w, const XSrc& src, int m, uint8_t* planes,
     if (src.mode == XS_CAT && (src.H < 1 || src.H >= K)) return fail("prep: bad concat split");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
-                       xs, (const int*)nullptr, (size_t)0, (size_t)0, 0);
+                       xs, (const int*)nullptr, (size_t)0, (size_t)0, 0, m);
     return CMF_OK;
 }
 
@@ -189,8 +201,8 @@ int launch_prep_src_gemm(const DevWeight& w, const XSrc& src, int m, int mstride
     // (256 threads a row: all of a 2048-row chunk's workgroups resident at
     // once; measured on MI355X, the 2048-position prefill 12.45 -> 12.21 ms
     // against 512, 12.5 ms at 128)
-    hipLaunchKernelGGL(k_prep_src, dim3(m), dim3(256), (size_t)K * sizeof(float), st, src, K, w.dtype, nk, planes,
-                       xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride);
+    hipLaunchKernelGGL(k_prep_src, dim3((m + 255) / 256 * 256), dim3(256), (size_t)K * sizeof(float), st, src, K,
+                       w.dtype, nk, planes, xs, (const int*)nullptr, (size_t)0, (size_t)0, mstride, m);
     return CMF_OK;
 }
 
@@ -212,7 +224,7 @@ int launch_prep_src_grouped(const DevWeight& w, const XSrc& src, int m, const in
     if (max_jobs < 1 || max_jobs > 65535 || !jobs) return fail("prep: bad job list");
     const int nk = w.dtype == DT_Q8ROW ? w.kchunks : w.kchunks * 4;
     hipLaunchKernelGGL(k_prep_src, dim3(m, max_jobs), dim3(512), (size_t)K * sizeof(float), st, src, K, w.dtype, nk,
-                       planes, xs, jobs, x_stride, planes_stride, 0);
+                       planes, xs, jobs, x_stride, planes_stride, 0, m);
     return CMF_OK;
 }
 

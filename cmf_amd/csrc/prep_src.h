@@ -28,32 +28,45 @@ __device__ inline void prep_src_row(XSrc s, int K, int fmt, int nk, uint8_t* __r
         r = tok & 15;
         rs = tv ? s.emb.rs[tok] : 0.f;
     }
-    double s1 = 0.0, s2 = 0.0;
-    for (int i = tid; i < K; i += nt) {
-        float v;
+    auto raw = [&](int i) -> float {
         if (s.mode == XS_SILU) {
             const float g = row[i], u = row[s.K + i];
-            v = (g / (1.0f + expf(-g))) * u;
-        } else if (s.mode == XS_SILU8) {
+            return (g / (1.0f + expf(-g))) * u;
+        }
+        if (s.mode == XS_SILU8) {
             const int o = 16 * (i >> 3) + (i & 7);
             const float g = row[o], u = row[o + 8];
-            v = (g / (1.0f + expf(-g))) * u;
-        } else if (s.mode == XS_CAT) {
+            return (g / (1.0f + expf(-g))) * u;
+        }
+        if (s.mode == XS_CAT) {
             if (i < H) {
                 // int8 of the token's row in the q8 device layout, times its row scale
                 const int kc = i >> 6, sl = (i >> 4) & 3, jj = i & 15;
                 const int8_t q = tv ? s.emb.w[(((size_t)rb * s.emb.nkc + kc) * 64 + 16 * sl + r) * 16 + jj] : 0;
-                v = (float)q * rs;
-            } else {
-                v = row[i - H];
+                return (float)q * rs;
             }
-        } else {
-            v = row[i];
+            return row[i - H];
         }
-        vals[i] = v;
-        if (nrm) {
-            if (i < H) s1 += (double)v * (double)v;
-            else s2 += (double)v * (double)v;
+        return row[i];
+    };
+    // four columns per thread at a time, their loads issued together (one
+    // round trip per four instead of one per column); the sums of squares
+    // still add the thread's columns in increasing order
+    double s1 = 0.0, s2 = 0.0;
+    for (int i0 = tid; i0 < K; i0 += 4 * nt) {
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = raw(min(i0 + u * nt, K - 1));
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = i0 + u * nt;
+            if (i < K) {
+                vals[i] = v[u];
+                if (nrm) {
+                    if (i < H) s1 += (double)v[u] * (double)v[u];
+                    else s2 += (double)v[u] * (double)v[u];
+                }
+            }
         }
     }
     if (nrm) {
@@ -76,10 +89,22 @@ __device__ inline void prep_src_row(XSrc s, int K, int fmt, int nk, uint8_t* __r
         }
         const float inv1 = 1.0f / (float)sqrt(t1 / (double)H + s.eps);
         const float inv2 = s.mode == XS_CAT ? 1.0f / (float)sqrt(t2 / (double)(K - H) + s.eps) : 1.f;
-        for (int i = tid; i < K; i += nt) {
-            const float y = i < H ? vals[i] * inv1 * s.w[i] : vals[i] * inv2 * s.w2[i - H];
-            vals[i] = y;
-            am = fmaxf(am, fabsf(y));
+        for (int i0 = tid; i0 < K; i0 += 4 * nt) {
+            float wv[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = min(i0 + u * nt, K - 1);
+                wv[u] = i < H ? s.w[i] : s.w2[i - H];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = i0 + u * nt;
+                if (i < K) {
+                    const float y = vals[i] * (i < H ? inv1 : inv2) * wv[u];
+                    vals[i] = y;
+                    am = fmaxf(am, fabsf(y));
+                }
+            }
         }
     } else {
         for (int i = tid; i < K; i += nt) am = fmaxf(am, fabsf(vals[i]));
