@@ -33,7 +33,7 @@ COPY_BYTES = 64 << 20  # counter-calibration copy (read + write of this many byt
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "q4t_gemv_12288x4096_m1_traffic.txt")
 
 
-ROOF_KERNEL = "k_gemv_q4t_m1<8, 4, false>"  # the kernel the dispatch runs for the roofline GEMV
+ROOF_KERNEL = "k_gemv_q4t_m1<8, 4, false, 1>"  # the kernel the dispatch runs for the roofline GEMV
 
 
 def measured_traffic():
