@@ -40,73 +40,93 @@ constexpr int MOE_MAX_EXPERTS = 1024;
 constexpr int MOE_MAX_TOPK = 32;
 constexpr int MOE_JT = 1 + MAXB;  // job token list: count, then the tokens
 
-// Routing of token t by wave t (b <= 16 waves, all tokens at once): softmax
-// of the router logits (max-subtracted; the sum sequential in expert order,
-// as the reference adds), then the top k by k rounds of a wave arg-max over
-// the normalised p: the largest p, the lower index among equal p (the
-// reference's order), each pick removed before the next round.  w_i = p_i /
-// wsum with wsum = the sum of the kept p in rank order (norm_topk) or 1,
-// divided by routed_scaling.  The picks also go to sidx (LDS) for the job
-// numbering that follows.
+// Routing of token t by wave t (b <= 16 waves, all tokens at once; no
+// barrier: each wave works on its own token): softmax of the router logits
+// (max-subtracted; the sum sequential in expert order, as the reference
+// adds), then the top k by k rounds of a wave arg-max over the normalised
+// p: the largest p, the lower index among equal p (the reference's order),
+// each pick removed before the next round.  w_i = p_i / wsum with wsum =
+// the sum of the kept p in rank order (norm_topk) or 1, divided by
+// routed_scaling.  Lane l holds experts l + 64 c in registers; the
+// sequential sum reads the exponentials back from LDS, 32 at a time, in
+// every lane (broadcast reads), so the total is wave-uniform.  A round's
+// pick: the wave max v of p, then the lowest expert holding v from one
+// ballot per register column (experts of column c all precede those of
+// c + 1).  The picks also go to sidx (LDS) for the job numbering.
+template <int MOE_NC>  // register columns: ne <= 64 MOE_NC
 __device__ __forceinline__ void moe_route_tokens(const float* __restrict__ logits, int b, int ne, int k,
                                                  int norm_topk, float scaling, int* __restrict__ idx,
-                                                 float* __restrict__ w, int* sidx) {
-    __shared__ float p[MAXB][MOE_MAX_EXPERTS];
-    __shared__ float tot[MAXB];
+                                                 float* __restrict__ w, int* sidx,
+                                                 float (*pe)[MOE_MAX_EXPERTS]) {
     const int lane = threadIdx.x & 63, t = threadIdx.x >> 6;
-    const bool on = t < b;
-    const float* lg = logits + (size_t)(on ? t : 0) * ne;
-    float mx = -INFINITY;
-    for (int e = lane; e < ne; e += 64) mx = fmaxf(mx, lg[e]);
+    if (t >= b) return;  // (uniform per wave; the caller's barrier follows)
+    const int nc = (ne + 63) >> 6;
+    const float* lg = logits + (size_t)t * ne;
+    float p[MOE_NC];
+#pragma unroll
+    for (int c = 0; c < MOE_NC; c++) {
+        const int e = lane + 64 * c;
+        p[c] = (c < nc && e < ne) ? lg[e] : -INFINITY;
+    }
+    float mx = p[0];
+#pragma unroll
+    for (int c = 1; c < MOE_NC; c++) mx = fmaxf(mx, p[c]);
     mx = wave_max(mx);
-    for (int e = lane; e < ne; e += 64) p[t][e] = expf(lg[e] - mx);
-    __syncthreads();
-    if (lane == 0) {
-        float sm = 0.0f;  // in expert order; the reads eight at a time
-        int e = 0;
-        for (; e + 8 <= ne; e += 8) {
-            float v[8];
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = p[t][e + j];
-#pragma unroll
-            for (int j = 0; j < 8; j++) sm += v[j];
+    for (int c = 0; c < MOE_NC; c++) {
+        const int e = lane + 64 * c;
+        if (c < nc) {
+            const float v = e < ne ? expf(p[c] - mx) : 0.f;
+            pe[t][e] = v;
+            p[c] = v;
         }
-        for (; e < ne; e++) sm += p[t][e];
-        tot[t] = sm;
     }
-    __syncthreads();
-    const float sm = tot[t];
-    for (int e = lane; e < ne; e += 64) p[t][e] = p[t][e] / sm;
-    float wsum = 0.0f;
+    // the sum in expert order (the wave's own LDS writes precede its reads)
+    float sm = 0.0f;
+    const float4* row = (const float4*)pe[t];
+    for (int e0 = 0; e0 < ne; e0 += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = row[(e0 >> 2) + q];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            if (e0 + 4 * q + 0 < ne) sm += v[q].x;
+            if (e0 + 4 * q + 1 < ne) sm += v[q].y;
+            if (e0 + 4 * q + 2 < ne) sm += v[q].z;
+            if (e0 + 4 * q + 3 < ne) sm += v[q].w;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < MOE_NC; c++) p[c] = (c < nc && lane + 64 * c < ne) ? p[c] / sm : -1.0f;
+    float wsum = 0.0f, myw = 0.0f;
+    int mye = 0;
     for (int i = 0; i < k; i++) {
-        // the lane's best (largest p, then lowest index) among its experts;
-        // picked experts hold -1
-        float bv = -1.0f;
-        int bi = ne;
-        for (int e = lane; e < ne; e += 64) {
-            const float pe = p[t][e];
-            if (pe > bv) {
-                bv = pe;
-                bi = e;
-            }
-        }
+        float bv = p[0];
+#pragma unroll
+        for (int c = 1; c < MOE_NC; c++) bv = fmaxf(bv, p[c]);
         const float v = wave_max(bv);
-        const int e = (int)wave_reduce_f32(bv == v ? (float)bi : INFINITY, INFINITY,
-                                           [](float x, float y) { return fminf(x, y); });
-        const float pv = v;  // p of the pick (every lane)
-        if (lane == (e & 63)) p[t][e] = -1.0f;
-        if (on && lane == 0) {
-            idx[t * k + i] = e;
-            sidx[t * k + i] = e;
-            w[t * k + i] = pv;  // scaled below
+        int e = ne;
+#pragma unroll
+        for (int c = 0; c < MOE_NC; c++) {
+            const unsigned long long m = __ballot(p[c] == v);
+            if (e == ne && m) e = 64 * c + (int)__ffsll((long long)m) - 1;
         }
-        wsum += pv;
+        e = __builtin_amdgcn_readfirstlane(e);
+#pragma unroll
+        for (int c = 0; c < MOE_NC; c++)
+            if (e == lane + 64 * c) p[c] = -1.0f;
+        if (lane == i) {
+            mye = e;
+            myw = v;  // scaled below
+        }
+        wsum += v;
     }
-    if (on && lane == 0) {
+    if (lane < k) {
         const float ws = norm_topk ? wsum / scaling : 1.0f / scaling;
-        for (int i = 0; i < k; i++) w[t * k + i] = w[t * k + i] / ws;
+        idx[t * k + lane] = mye;
+        sidx[t * k + lane] = mye;
+        w[t * k + lane] = myw / ws;
     }
-    __syncthreads();
 }
 
 // jobs = [njobs, expert of job 0, ...] (experts in increasing order);
@@ -176,11 +196,20 @@ __global__ __launch_bounds__(1024) void k_moe_route_prep(const float* __restrict
                                                         float* __restrict__ xs) {
     extern __shared__ float vals[];  // K (the operand workgroups)
     __shared__ int sidx[MAXB * MOE_MAX_TOPK];
+    __shared__ __align__(16) float pe[MAXB][MOE_MAX_EXPERTS];  // the routing's exponentials
     if ((int)blockIdx.x < b) {
         prep_src_row(src, K, fmt, nk, planes, xs, 0, blockIdx.x, b, vals);
         return;
     }
-    moe_route_tokens(logits, b, ne, k, norm_topk, scaling, idx, w, sidx);
+    if (ne <= 64)
+        moe_route_tokens<1>(logits, b, ne, k, norm_topk, scaling, idx, w, sidx, pe);
+    else if (ne <= 128)
+        moe_route_tokens<2>(logits, b, ne, k, norm_topk, scaling, idx, w, sidx, pe);
+    else if (ne <= 256)
+        moe_route_tokens<4>(logits, b, ne, k, norm_topk, scaling, idx, w, sidx, pe);
+    else
+        moe_route_tokens<MOE_MAX_EXPERTS / 64>(logits, b, ne, k, norm_topk, scaling, idx, w, sidx, pe);
+    __syncthreads();
     moe_jobs_body(sidx, b, k, ne, jobs, slot, jt);
 }
 

@@ -56,6 +56,13 @@ def test_moe_scaling_no_norm(gpu):
     _run(gpu, 16, 128, 64, 4, 4, norm=False, scaling=2.5)
 
 
+@pytest.mark.parametrize("ne", [64, 200, 300])
+def test_moe_expert_counts(gpu, ne):
+    """the routing's register layouts: 64 experts (one column per lane), up
+    to 256 (four), more (sixteen), with ragged last columns"""
+    _run(gpu, ne, 128, 64, 6, 3, seed=41)
+
+
 def test_moe_all_experts_selected(gpu):
     """top_k = n_experts: every job runs, every token uses every expert."""
     _run(gpu, 4, 128, 64, 4, 5)
