@@ -273,7 +273,7 @@ struct MoeGx {
 };
 
 template <int RBW, int KP, int SPW, bool GU>
-__global__ __launch_bounds__(64 * RBW * KP) void k_moe_q4t(MoeGx a) {
+__global__ __launch_bounds__(64 * RBW * KP, GU && KP > 1 ? 6 : 1) void k_moe_q4t(MoeGx a) {
     constexpr int NW = RBW * KP;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ float4v part[KP > 1 ? KP - 1 : 1][RBW][64];
@@ -513,7 +513,12 @@ bool moe_lds_ok(MoeKernel k, size_t lds) {
 // (measured on MI355X, config 5: four row blocks per workgroup, gate|up
 // in two K halves of 8 steps: 16.7 us; 8 x 2: 19.2, 2 x 2: 18.2, 4 x 4
 // halves of 4: 16.7, 8 row blocks of whole rows: 30.6; down 4 x 1 x 6
-// steps: 10.7 us; 8 x 1: 10.9, 4 x 2 x 3: 10.8, 2 x 1: 11.6)
+// steps: 10.7 us; 8 x 1: 10.9, 4 x 2 x 3: 10.8, 2 x 1: 11.6).  The
+// gate|up instances with two K parts are held to 6 waves per SIMD (<= 80
+// VGPRs, no spill): three 8-wave workgroups per CU instead of two, so the
+// config-5 grid of 840 workgroups takes ~1.1 dispatch rounds instead of
+// ~1.6 (gate|up 16.7 -> 16.1 us; the down instances spill at that bound,
+// and 4 x 2 x 3 there at 64 VGPRs was no faster)
 MoeKernel moe_q4t_pick(int nk, bool gu, int* nw, int* rbw) {
     if (nk <= 2) return moe_q4t_inst<4, 1, 2>(gu, nw, rbw);
     if (nk <= 4) return moe_q4t_inst<4, 1, 4>(gu, nw, rbw);
