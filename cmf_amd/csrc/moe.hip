@@ -15,8 +15,12 @@
 //                     for caller-routed batches (k_moe_jobs).
 //   q4t experts, b <= 8 (k_moe_q4t, over each job's own tokens only):
 //   3. gate|up        job j: h = silu(g) * u of W_gu[e_j] x for its tokens;
-//   4. down           job j: W_down[e_j] h, the operand made from the h rows
-//                     in the workgroup;
+//   4. down           routed batches: per (row block, token), one wave per
+//                     rank i: W_down[e_ti] h_ti with the operand made from
+//                     the h row in the wave, and 5 in the same launch
+//                     (k_moe_down_tok); caller-routed jobs: job j:
+//                     W_down[e_j] h, the operand made from the h rows in the
+//                     workgroup;
 //   other codecs or larger batches (grouped GEMVs over all b rows; rows of
 //   tokens that did not pick the expert are computed and ignored):
 //   3. gate|up, 3b. the per-job operand h = silu(g) * u, 4. down;
@@ -484,6 +488,166 @@ __global__ __launch_bounds__(64 * RBW * KP, GU && KP > 1 ? 6 : 1) void k_moe_q4t
     }
 }
 
+// Down projection and combine of routed batches in one launch (q4t, K =
+// inter <= 1024): workgroup (rb, t) computes rows [16 rb, 16 rb + 16) of
+// token t's MoE output; wave i (one per rank, k waves) multiplies expert
+// idx[t][i]'s down rows with token t's h row of that job, staged by the
+// wave itself exactly as the producer would (row max |x| by a wave
+// reduction, the fixed-point hi / lo planes and tile biases into the
+// wave's own LDS slice), and the k results meet in LDS, where
+// out[t][row] = sum over ranks in order of w[t][i] * down_i[row] (as
+// k_moe_combine).  Every routed expert's down rows are read once per token
+// that picked it instead of once per job; no per-job down rows are stored.
+template <int SPW>
+__global__ __launch_bounds__(1024) void k_moe_down_tok(const GemvDesc* __restrict__ desc, const int* __restrict__ idx,
+                                                      const int* __restrict__ slot, const float* __restrict__ w,
+                                                      int k, const float* __restrict__ hx, size_t hx_stride,
+                                                      int ldh, int K, int nrb, int rows, float* __restrict__ out,
+                                                      int ldo, int resid) {
+    extern __shared__ __align__(16) uint8_t smem[];  // per wave: SPW * 32 items x 16 B + SPW * 4 tiles x 16 biases
+    __shared__ float res[16][16];                    // [rank][row] results
+    __shared__ float resw[16];                       // the ranks' routing weights
+    constexpr int QI = SPW * 32, IPW = (SPW * 16 + 63) / 64;  // items of the row; items per lane
+    const int lane = threadIdx.x & 63, i = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, s = lane >> 4, p = r < 8 ? 0 : 1;
+    const int rb = blockIdx.x, t = blockIdx.y, ntg = SPW;
+    const int e = idx[t * k + i], j = slot[t * k + i];
+    const float wi = w[t * k + i];
+    const GemvDesc d = desc[e];
+    // the h row's items first (8 columns per item: 32 tile + 8 k-slot)
+    const float* h = hx + (size_t)j * hx_stride + (size_t)t * ldh;
+    float4v xv[IPW][2];
+#pragma unroll
+    for (int q = 0; q < IPW; q++) {
+        const int c0 = min(8 * (lane + 64 * q), K - 8);
+        xv[q][0] = ldg((const float4v*)(h + c0));
+        xv[q][1] = ldg((const float4v*)(h + c0 + 4));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 wv[SPW];
+    uint2 sv[SPW];
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+        const size_t tt = (size_t)rb * ntg + u;
+        wv[u] = ld_stream((const uint4*)d.w + tt * 64 + lane);
+        const uint64_t sw = ldg((const uint64_t*)d.scale + tt * 16 + r);
+        sv[u] = make_uint2((uint32_t)sw, (uint32_t)(sw >> 32));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<2 * SPW>();  // the row's items
+    float am = 0.f;
+#pragma unroll
+    for (int q = 0; q < IPW; q++) {
+        const int c0 = 8 * (lane + 64 * q);
+#pragma unroll
+        for (int c = 0; c < 8; c++) am = fmaxf(am, c0 + c < K ? fabsf(xv[q][c >> 2][c & 3]) : 0.f);
+    }
+    am = wave_max(am);
+    float scale, xsl;
+    q4_fix_scale(am, scale, xsl);
+    uint8_t* lw = smem + (size_t)i * (QI * 16 + SPW * 4 * 64);
+    float* lb = (float*)(lw + QI * 16);
+    const int ord[8] = {0, 4, 2, 6, 1, 5, 3, 7};
+#pragma unroll
+    for (int q = 0; q < IPW; q++) {
+        const int item = lane + 64 * q, c0 = 8 * item;
+        uint16_t hv[8], lv[8];
+        float sh = 0.f, sl = 0.f;  // (exact: integers and multiples of 2^-11)
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const int col = ord[c];
+            _Float16 hh, ll;
+            q4_fix_split(c0 + col < K ? xv[q][col >> 2][col & 3] * scale : 0.f, hh, ll);
+            hv[c] = __builtin_bit_cast(uint16_t, hh);
+            lv[c] = __builtin_bit_cast(uint16_t, ll);
+            sh += (float)hh;
+            sl += (float)ll;
+        }
+        sh += __shfl_xor(sh, 1);
+        sh += __shfl_xor(sh, 2);
+        sl += __shfl_xor(sl, 1);
+        sl += __shfl_xor(sl, 2);
+        if (item < SPW * 16) {
+            uint4* dst = (uint4*)lw + item * 2;
+            dst[0] = make_uint4(hv[0] | (hv[1] << 16), hv[2] | (hv[3] << 16), hv[4] | (hv[5] << 16),
+                                hv[6] | (hv[7] << 16));
+            dst[1] = make_uint4(lv[0] | (lv[1] << 16), lv[2] | (lv[3] << 16), lv[4] | (lv[5] << 16),
+                                lv[6] | (lv[7] << 16));
+            if ((item & 3) == 0) {  // A rows 0..7: the hi bias, 8..15: the lo bias (every row the same token)
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    lb[(item >> 2) * 16 + c] = sh * Q4_BIAS;
+                    lb[(item >> 2) * 16 + 8 + c] = sl * Q4_BIAS;
+                }
+            }
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // (the wave's own slice: no barrier)
+    const uint4* X = (const uint4*)lw + p;
+    const float4v* LB = (const float4v*)lb;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < SPW; u++) {
+#pragma unroll
+        for (int tq = 0; tq < 4; tq++) {
+            const int q = (u * 4 + tq) * 4 + s;
+            const half8 xa = __builtin_bit_cast(half8, X[q * 2]);
+            const float4v cb = LB[(u * 4 + tq) * 4 + s];
+            const uint32_t wq = tq == 0 ? wv[u].x : tq == 1 ? wv[u].y : tq == 2 ? wv[u].z : wv[u].w;
+            const float4v dd = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, dq_nib_word(wq), cb, 0, 0, 0);
+            const uint32_t sw = tq < 2 ? sv[u].x : sv[u].y;
+            const float sc = f16_bits_to_f32((tq & 1) ? sw >> 16 : sw & 0xFFFFu);
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] += dd[v] * sc;
+        }
+    }
+    // D row 0 (hi, lanes s = 0) + D row 8 (lo, lanes s = 2)
+    const float val = (acc[0] + __shfl_xor(acc[0], 32)) * xsl * 16777216.0f;  // 2^24: denormal nibbles
+    if (s == 0) res[i][r] = val;
+    if (lane == 0) resw[i] = wi;
+    __syncthreads();
+    if (i == 0 && lane < 16) {
+        const int row = 16 * rb + lane;
+        float v[16], ws[16];
+        for (int q = 0; q < k; q++) {
+            v[q] = res[q][lane];
+            ws[q] = resw[q];
+        }
+        float a2 = 0.0f;
+        for (int q = 0; q < k; q++) a2 += ws[q] * v[q];
+        if (row < rows) {
+            float* o = out + (size_t)t * ldo + row;
+            *o = resid ? *o + a2 : a2;
+        }
+    }
+    (void)nrb;
+}
+typedef void (*MoeDownTok)(const GemvDesc*, const int*, const int*, const float*, int, const float*, size_t, int, int,
+                           int, int, float*, int, int);
+// the instance for rows of nk 1 KiB steps (nullptr: none), its dynamic LDS
+// attribute set once
+MoeDownTok moe_down_tok_pick(int nk) {
+    static MoeDownTok tab[9] = {nullptr,
+                                k_moe_down_tok<1>,
+                                k_moe_down_tok<2>,
+                                k_moe_down_tok<3>,
+                                k_moe_down_tok<4>,
+                                k_moe_down_tok<5>,
+                                k_moe_down_tok<6>,
+                                k_moe_down_tok<7>,
+                                k_moe_down_tok<8>};
+    static std::once_flag once;
+    static bool ok = true;
+    std::call_once(once, [] {
+        for (int n = 1; n <= 8; n++)
+            if (hipFuncSetAttribute((const void*)tab[n], hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    16 * (n * 32 * 16 + n * 4 * 64)) != hipSuccess)
+                ok = false;
+        (void)hipGetLastError();
+    });
+    return ok && nk >= 1 && nk <= 8 ? tab[nk] : nullptr;
+}
+
 typedef void (*MoeKernel)(MoeGx);
 template <int RBW, int KP, int SPW>
 MoeKernel moe_q4t_inst(bool gu, int* nw, int* rbw) {
@@ -618,6 +782,20 @@ static int moe_experts(cmf_moe m, const XSrc& x, int b, int k, float* d_out, int
         g.ns = b;
         g.nrb = gw.rows_pad / 16;
         hipLaunchKernelGGL(kg, dim3((g.nrb + rw1 - 1) / rw1, mj), dim3(64 * sp1), lg, s, g);
+        static const bool tok_env = [] {
+            const char* v = getenv("CMF_MOE_DOWN_TOK");
+            return !(v && *v == '0');
+        }();
+        MoeDownTok kt = numbered && tok_env && k <= 16 ? moe_down_tok_pick(dw.kchunks) : nullptr;
+        if (kt) {
+            // routed (no expert twice in a token's picks): down + combine per
+            // (row block, token), one wave per rank
+            const size_t lt = (size_t)k * (dw.kchunks * 32 * 16 + dw.kchunks * 4 * 64);
+            hipLaunchKernelGGL(kt, dim3(dw.rows_pad / 16, b), dim3(64 * k), lt, s, m->d_down, m->idx, m->slot, m->w,
+                               k, m->ygu, (size_t)MAXB * I, I, I, dw.rows_pad / 16, dw.rows, d_out, ldo,
+                               resid ? 1 : 0);
+            return CMF_OK;
+        }
         MoeGx d = g;
         d.desc = m->d_down;
         d.planes = nullptr;  // (the operand from the h rows themselves)

@@ -111,6 +111,34 @@ print("ok")
 """
 
 
+_PERJOB_CHILD = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[1] + "/tests")
+import cmf_amd as cmf
+cmf.init(0)
+import test_gpu_moe as t
+t._run(None, 8, 256, 128, 2, 5)
+t._run(None, 128, 2048, 768, 8, 5, seed=5)
+print("ok")
+"""
+
+
+def test_moe_per_job_down_path(gpu):
+    """CMF_MOE_DOWN_TOK=0 (child process): routed batches through the
+    per-job down kernel and the separate combine (the path of caller-routed
+    jobs) instead of the per-token down + combine launch"""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, CMF_MOE_DOWN_TOK="0")
+    r = subprocess.run([sys.executable, "-c", _PERJOB_CHILD, root], env=env, capture_output=True, text=True,
+                       timeout=240)
+    print(r.stdout[-3000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().splitlines()[-1] == "ok"
+
+
 def test_moe_grouped_path(gpu):
     """CMF_MOE_GATHER=0 (child process): q4t experts at b <= 8 through the
     grouped GEMVs over all rows, the path of the other codecs and of larger
