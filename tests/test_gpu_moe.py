@@ -63,6 +63,20 @@ def test_moe_expert_counts(gpu, ne):
     _run(gpu, ne, 128, 64, 6, 3, seed=41)
 
 
+@pytest.mark.parametrize("k", [1, 16])
+def test_moe_top_k_extremes(gpu, k):
+    """one rank per token, and 16 ranks (the per-token down launch's
+    1024-thread workgroup)"""
+    _run(gpu, 32, 128, 64, k, 3, seed=43)
+
+
+@pytest.mark.parametrize("inter", [1024, 1152])
+def test_moe_inter_sizes(gpu, inter):
+    """FFN 1024: the largest per-token down instance (8 K steps); 1152: past
+    it, the per-job down kernel and the combine"""
+    _run(gpu, 16, 256, inter, 4, 3, seed=47)
+
+
 def test_moe_all_experts_selected(gpu):
     """top_k = n_experts: every job runs, every token uses every expert."""
     _run(gpu, 4, 128, 64, 4, 5)
